@@ -1,0 +1,114 @@
+// Device-side helpers shared by the gfx950 kernels: record layout, INT4 / FP8
+// decode, wave-64 reductions.
+//
+// Cold record layout (splitter.py:23-39, 55-76, 239-246): 6400 bytes =
+//   u16 nid | gate 2048 B | up 2048 B | down 2048 B | 3 x 32 fp16 scales | pad
+// Records sit at 16 + 6400 k past a 4096-aligned section start, so record
+// bases are 16-byte aligned and every payload vector starts 2 bytes past a
+// 16-byte boundary.  gfx950 under amdhsa runs global memory in unaligned
+// mode, so the kernels read payload chunks with plain 16-byte loads at
+// base + 2 + 16 c.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace oi2 {
+
+constexpr int kH = 4096;                 // hidden size the record format is sized for
+constexpr int kGroup = 128;              // INT4 group size
+constexpr int kGroups = kH / kGroup;     // 32 scales per vector
+constexpr int kVecBytes = kH / 2;        // 2048 nibble bytes per vector
+constexpr int kRecBytes = 6400;          // NEURON_RECORD_BYTES
+constexpr int kOffGate = 2;
+constexpr int kOffUp = kOffGate + kVecBytes;        // 2050
+constexpr int kOffDown = kOffUp + kVecBytes;        // 4098
+constexpr int kOffScales = kOffDown + kVecBytes;    // 6146
+constexpr int kWave = 64;
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_a2 __attribute__((ext_vector_type(4), aligned(2)));
+typedef uint32_t u32x2_a2 __attribute__((ext_vector_type(2), aligned(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+
+// 16 payload bytes at a 2-byte aligned address (one global_load_dwordx4).
+__device__ __forceinline__ u32x4 load16_a2(const uint8_t* p) {
+  return *reinterpret_cast<const u32x4_a2*>(p);
+}
+
+__device__ __forceinline__ u32x4 load16(const uint8_t* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+
+__device__ __forceinline__ float half_bits_to_float(uint16_t b) {
+  return (float)__builtin_bit_cast(_Float16, b);
+}
+
+__device__ __forceinline__ uint16_t float_to_half_bits(float f) {
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+
+__device__ __forceinline__ float bf16_bits_to_float(uint16_t b) {
+  return __builtin_bit_cast(float, (uint32_t)b << 16);
+}
+
+// Signed INT4 nibbles of one dword as exact fp16 pairs, splitter.py:111-124:
+// byte b holds element 2k in bits 0-3 and 2k+1 in bits 4-7, two's complement.
+// Bias each nibble by 8 (xor), place it in the mantissa of 1024.0 (0x6400),
+// then subtract 1032: the result is the signed value, exactly.
+// Output pairs: p[0] = (e0, e4), p[1] = (e1, e5), p[2] = (e2, e6), p[3] = (e3, e7).
+__device__ __forceinline__ void int4x8_to_f16x2x4(uint32_t d, f16x2 p[4]) {
+  const uint32_t t = d ^ 0x88888888u;
+  const f16x2 bias = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t m = ((t >> (4 * k)) & 0x000F000Fu) | 0x64006400u;
+    p[k] = __builtin_bit_cast(f16x2, m) + bias;
+  }
+}
+
+// x pairs matching int4x8_to_f16x2x4's output order for 8 consecutive elements.
+__device__ __forceinline__ void pack_x8(const float* x, f16x2 q[4]) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    q[k].x = (_Float16)x[k];
+    q[k].y = (_Float16)x[k + 4];
+  }
+}
+
+__device__ __forceinline__ float dot2(f16x2 a, f16x2 b, float c) {
+  return __builtin_amdgcn_fdot2(a, b, c, false);
+}
+
+// Two fp8 e4m3fn (bytes 0,1 or 2,3 of d) -> fp16 pair, exact (every e4m3 value
+// is an fp16 normal).
+__device__ __forceinline__ f16x2 fp8x2_to_f16x2(uint32_t d, bool hi) {
+  return hi ? __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d, 1.0f, true)
+            : __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(d, 1.0f, false);
+}
+
+__device__ __forceinline__ f32x2 fp8x2_to_f32x2(uint32_t d, bool hi) {
+  return hi ? __builtin_amdgcn_cvt_pk_f32_fp8(d, true) : __builtin_amdgcn_cvt_pk_f32_fp8(d, false);
+}
+
+// Sum over the 64 lanes of a wave; every lane receives the total.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+__device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (kWave - 1)); }
+
+__device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
+
+// engine.py:163-170: act = relu if activation == "relu" else silu;
+// act(g) * act(u) when act_on_both, else act(g) * u.
+__device__ __forceinline__ float gated_act(float g, float u, int relu, int both) {
+  float ag = relu ? fmaxf(g, 0.0f) : silu(g);
+  float au = both ? (relu ? fmaxf(u, 0.0f) : silu(u)) : u;
+  return ag * au;
+}
+
+}  // namespace oi2

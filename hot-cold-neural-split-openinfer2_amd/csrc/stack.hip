@@ -1,0 +1,370 @@
+// FFN-only decode stack: DesdemonaEngine.forward's layer loop (engine.py:421-438)
+// restricted to the FFN sublayers, batch 1, entirely on device.
+//
+// Per token: layer 0's active set is predicted from the input (engine.py:422),
+// then for each layer L two launches:
+//   ffn_up(L)   hot + cold gate/up of layer L, and the down projection of
+//               layer L+1's predictor on RMSNorm_{L+1}(x_L) (the lookahead,
+//               engine.py:432-436)
+//   ffn_down(L) x_{L+1} = x_L + FFN_L, and layer L+1's logits, threshold and
+//               compacted active set
+// so there is no host synchronisation inside a token.  The launch sequence
+// is captured once into a hipGraph per (x_in, x_out, stream) and replayed.
+#include <algorithm>
+#include <vector>
+
+#include "capi_util.h"
+#include "ffn_kernels.h"
+
+namespace oi2 {
+
+struct StackLayer {
+  oi2_layer l;
+  bool has_pred;
+  int32_t* all_slots = nullptr;   // device: every record slot, for layers without a predictor
+  int32_t* all_count = nullptr;   // device: one int
+  int n_all = 0;
+};
+
+}  // namespace oi2
+
+struct oi2_stack {
+  std::vector<oi2::StackLayer> layers;
+  int n_layers = 0, inter = 0, n_chunks = 0, relu = 0, both = 0, max_hot = 0, max_rank = 0;
+  float eps = 0.0f, thr = 0.0f;
+  uint16_t* xbuf = nullptr;      // (n_layers, H): output of each layer
+  float* h_hot = nullptr;
+  float* partials = nullptr;     // (kMaxColdWG, H)
+  float* z = nullptr;
+  int32_t* sel_counts = nullptr; // (n_layers, n_chunks)
+  int32_t* sel_slots = nullptr;  // (n_layers, n_chunks * 256)
+  int32_t* sel_ids = nullptr;
+  int cold_wg = 1;
+  bool use_graph = true;
+  hipGraphExec_t exec = nullptr;
+  const void* g_in = nullptr;
+  void* g_out = nullptr;
+  hipStream_t g_stream = nullptr;
+};
+
+namespace oi2 {
+
+static int stack_launch(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, hipStream_t st,
+                        hipEvent_t* ev = nullptr) {
+  const int n = s->n_layers;
+  const size_t sel_stride = (size_t)s->n_chunks * kSelChunk;
+  // layer 0's active set from the token itself
+  if (s->layers[0].has_pred) {
+    const oi2_layer& l0 = s->layers[0].l;
+    UpArgs ua{};
+    ua.x = x_in;
+    ua.eps = s->eps;
+    ua.pd_w = l0.pred.down_w;
+    ua.pd_rank = l0.pred.rank;
+    ua.pd_bf16 = l0.pred.dtype == OI2_DTYPE_BF16;
+    ua.pd_norm_w = l0.norm_w;
+    ua.pd_z = s->z;
+    ua.wg_pred = (l0.pred.rank + 3) / 4;
+    hipLaunchKernelGGL(k_pred_up, dim3(ua.wg_pred), dim3(kThreads), 0, st, ua);
+    OI2_CHECK_LAUNCH();
+    DownArgs da{};
+    da.pu_w = l0.pred.up_w;
+    da.pu_b = l0.pred.up_b;
+    da.pu_rank = l0.pred.rank;
+    da.pu_bf16 = l0.pred.dtype == OI2_DTYPE_BF16;
+    da.inter = l0.pred.inter;
+    da.pd_z = s->z;
+    da.thr = s->thr;
+    da.lut = l0.lut;
+    da.sel_slots = s->sel_slots;
+    da.sel_ids = s->sel_ids;
+    da.sel_counts = s->sel_counts;
+    da.wg_pred = s->n_chunks;
+    hipLaunchKernelGGL(k_pred_down, dim3(da.wg_pred), dim3(kThreads), 0, st, da);
+    OI2_CHECK_LAUNCH();
+  }
+  for (int L = 0; L < n; ++L) {
+    const StackLayer& SL = s->layers[L];
+    const oi2_layer& l = SL.l;
+    const bool pred_next = (L + 1 < n) && s->layers[L + 1].has_pred;
+    const uint16_t* xl = (L == 0) ? x_in : s->xbuf + (size_t)(L - 1) * kH;
+
+    UpArgs ua{};
+    ua.x = xl;
+    ua.norm_w = l.norm_w;
+    ua.eps = s->eps;
+    ua.relu = s->relu;
+    ua.both = s->both;
+    ua.n_hot = l.hot.n_hot;
+    ua.gate_q = l.hot.gate_q;
+    ua.up_q = l.hot.up_q;
+    ua.gate_s = l.hot.gate_scale;
+    ua.up_s = l.hot.up_scale;
+    ua.hot_gbias = l.hot.gate_bias;
+    ua.h_hot = s->h_hot;
+    const bool has_cold = l.cold.n_records > 0;
+    if (has_cold) {
+      ua.records = l.cold.records;
+      ua.n_records = l.cold.n_records;
+      ua.cold_gbias = l.cold.gate_bias;
+      if (SL.has_pred)
+        ua.act = ActiveList{s->sel_slots + (size_t)L * sel_stride,
+                            s->sel_counts + (size_t)L * s->n_chunks, s->n_chunks, kSelChunk};
+      else
+        ua.act = ActiveList{SL.all_slots, SL.all_count, 1, SL.n_all};
+    }
+    ua.partials = s->partials;
+    ua.wg_cold = has_cold ? s->cold_wg : 0;
+    ua.wg_hot = (l.hot.n_hot + 7) / 8;
+    if (pred_next) {
+      const oi2_layer& ln = s->layers[L + 1].l;
+      ua.pd_w = ln.pred.down_w;
+      ua.pd_rank = ln.pred.rank;
+      ua.pd_bf16 = ln.pred.dtype == OI2_DTYPE_BF16;
+      ua.pd_norm_w = ln.norm_w;
+      ua.pd_z = s->z;
+      ua.wg_pred = (ln.pred.rank + 3) / 4;
+    }
+    const int grid_up = ua.wg_cold + ua.wg_pred + ua.wg_hot;
+    if (ev) OI2_CHECK_HIP(hipEventRecord(ev[3 * L], st));
+    if (grid_up > 0) {
+      hipLaunchKernelGGL(k_ffn_up, dim3(grid_up), dim3(kThreads), 0, st, ua);
+      OI2_CHECK_LAUNCH();
+    }
+    if (ev) OI2_CHECK_HIP(hipEventRecord(ev[3 * L + 1], st));
+
+    DownArgs da{};
+    da.res = xl;
+    da.h_hot = s->h_hot;
+    da.n_hot = l.hot.n_hot;
+    da.down_stride = l.hot.down_stride;
+    da.down_q = l.hot.down_q;
+    da.down_s = l.hot.down_scale;
+    da.partials = s->partials;
+    da.n_partials = ua.wg_cold;
+    da.out = s->xbuf + (size_t)L * kH;
+    da.out2 = (L == n - 1) ? x_out : nullptr;
+    if (pred_next) {
+      const oi2_layer& ln = s->layers[L + 1].l;
+      da.pu_w = ln.pred.up_w;
+      da.pu_b = ln.pred.up_b;
+      da.pu_rank = ln.pred.rank;
+      da.pu_bf16 = ln.pred.dtype == OI2_DTYPE_BF16;
+      da.inter = ln.pred.inter;
+      da.pd_z = s->z;
+      da.thr = s->thr;
+      da.lut = ln.lut;
+      da.sel_slots = s->sel_slots + (size_t)(L + 1) * sel_stride;
+      da.sel_ids = s->sel_ids + (size_t)(L + 1) * sel_stride;
+      da.sel_counts = s->sel_counts + (size_t)(L + 1) * s->n_chunks;
+      da.wg_pred = s->n_chunks;
+    }
+    da.wg_down = kH / kRowsPerDownWG;
+    hipLaunchKernelGGL(k_ffn_down, dim3(da.wg_pred + da.wg_down), dim3(kThreads), 0, st, da);
+    OI2_CHECK_LAUNCH();
+    if (ev) OI2_CHECK_HIP(hipEventRecord(ev[3 * L + 2], st));
+  }
+  return OI2_OK;
+}
+
+static void stack_free(oi2_stack* s) {
+  for (auto& L : s->layers) {
+    if (L.all_slots) (void)hipFree(L.all_slots);
+    if (L.all_count) (void)hipFree(L.all_count);
+  }
+  if (s->exec) (void)hipGraphExecDestroy(s->exec);
+  for (void* p : {(void*)s->xbuf, (void*)s->h_hot, (void*)s->partials, (void*)s->z,
+                  (void*)s->sel_counts, (void*)s->sel_slots, (void*)s->sel_ids})
+    if (p) (void)hipFree(p);
+}
+
+}  // namespace oi2
+
+using namespace oi2;
+
+extern "C" {
+
+int oi2_stack_create(const oi2_layer* layers, int32_t n_layers, int32_t inter, float eps,
+                     int32_t act, int32_t act_on_both, float threshold_logit, oi2_stack** out) {
+  clear_error();
+  OI2_CHECK_ARG(out, "out is null");
+  *out = nullptr;
+  OI2_CHECK_ARG(layers && n_layers > 0, "need at least one layer");
+  OI2_CHECK_ARG(inter > 0 && inter <= 65536, "inter %d out of range", inter);
+  OI2_CHECK_ARG(act == OI2_ACT_SILU || act == OI2_ACT_RELU, "act %d", act);
+  oi2_stack* s = new oi2_stack();
+  s->n_layers = n_layers;
+  s->inter = inter;
+  s->n_chunks = (inter + kSelChunk - 1) / kSelChunk;
+  s->eps = eps;
+  s->relu = act == OI2_ACT_RELU;
+  s->both = act_on_both != 0;
+  s->thr = threshold_logit;
+  int max_records = 0;
+  for (int L = 0; L < n_layers; ++L) {
+    StackLayer SL;
+    SL.l = layers[L];
+    SL.has_pred = layers[L].pred.down_w != nullptr;
+    const oi2_hot& h = SL.l.hot;
+    if (h.n_hot > 0 &&
+        (h.down_stride < h.n_hot || h.down_stride % 16 || h.down_stride > 4096 || !h.gate_q ||
+         !h.up_q || !h.down_q || !h.gate_scale || !h.up_scale || !h.down_scale)) {
+      set_error("layer %d: invalid hot weights", L);
+      stack_free(s);
+      delete s;
+      return OI2_EINVAL;
+    }
+    if (!SL.l.norm_w || (SL.l.cold.n_records > 0 && (!SL.l.cold.records || !SL.l.lut))) {
+      set_error("layer %d: norm weight, cold records and lut are required", L);
+      stack_free(s);
+      delete s;
+      return OI2_EINVAL;
+    }
+    if (SL.has_pred) {
+      const oi2_predictor& p = SL.l.pred;
+      if (!p.up_w || !p.up_b || p.inter != inter || p.rank <= 0 || p.rank > 256 || p.rank % 8 ||
+          (p.dtype != OI2_DTYPE_F32 && p.dtype != OI2_DTYPE_BF16)) {
+        set_error("layer %d: invalid predictor", L);
+        stack_free(s);
+        delete s;
+        return OI2_EINVAL;
+      }
+      s->max_rank = std::max(s->max_rank, p.rank);
+    }
+    s->max_hot = std::max(s->max_hot, h.n_hot);
+    max_records = std::max(max_records, SL.l.cold.n_records);
+    s->layers.push_back(SL);
+  }
+  s->cold_wg = std::max(1, std::min(kMaxColdWG, (max_records + 7) / 8));
+  const size_t sel = (size_t)n_layers * s->n_chunks * kSelChunk;
+  hipError_t e = hipSuccess;
+  auto alloc = [&](void** p, size_t bytes) {
+    if (e == hipSuccess) e = hipMalloc(p, bytes);
+  };
+  alloc((void**)&s->xbuf, (size_t)n_layers * kH * 2);
+  alloc((void**)&s->h_hot, (size_t)(s->max_hot + 64) * 4);
+  alloc((void**)&s->partials, (size_t)kMaxColdWG * kH * 4);
+  alloc((void**)&s->z, (size_t)(s->max_rank + 64) * 4);
+  alloc((void**)&s->sel_counts, (size_t)n_layers * s->n_chunks * 4);
+  alloc((void**)&s->sel_slots, sel * 4);
+  alloc((void**)&s->sel_ids, sel * 4);
+  // layers without a predictor fetch every cold record (engine.py:282-283):
+  // ascending neuron id order, i.e. the lut's non-negative entries in order
+  for (auto& SL : s->layers) {
+    if (e != hipSuccess || SL.has_pred || SL.l.cold.n_records == 0) continue;
+    std::vector<int32_t> lut(inter);
+    e = hipMemcpy(lut.data(), SL.l.lut, (size_t)inter * 4, hipMemcpyDeviceToHost);
+    std::vector<int32_t> all;
+    for (int i = 0; i < inter; ++i)
+      if (lut[i] >= 0 && lut[i] < SL.l.cold.n_records) all.push_back(lut[i]);
+    SL.n_all = std::max<int>(1, (int)all.size());
+    alloc((void**)&SL.all_slots, (size_t)SL.n_all * 4);
+    alloc((void**)&SL.all_count, 4);
+    const int cnt = (int)all.size();
+    if (e == hipSuccess && cnt) e = hipMemcpy(SL.all_slots, all.data(), (size_t)cnt * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(SL.all_count, &cnt, 4, hipMemcpyHostToDevice);
+  }
+  if (e == hipSuccess) e = hipMemset(s->sel_counts, 0, (size_t)n_layers * s->n_chunks * 4);
+  if (e != hipSuccess) {
+    set_error("stack allocation failed: %s", hipGetErrorString(e));
+    stack_free(s);
+    delete s;
+    return OI2_ENOMEM;
+  }
+  *out = s;
+  return OI2_OK;
+}
+
+int oi2_stack_decode(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, void* stream) {
+  clear_error();
+  OI2_CHECK_ARG(s && x_in && x_out, "null argument");
+  OI2_CHECK_ARG(((uintptr_t)x_in | (uintptr_t)x_out) % 16 == 0, "x must be 16-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  if (!s->use_graph || st == nullptr) return stack_launch(s, x_in, x_out, st);
+  if (!s->exec || s->g_in != x_in || s->g_out != x_out || s->g_stream != st) {
+    if (s->exec) {
+      OI2_CHECK_HIP(hipGraphExecDestroy(s->exec));
+      s->exec = nullptr;
+    }
+    hipGraph_t g = nullptr;
+    OI2_CHECK_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+    int rc = stack_launch(s, x_in, x_out, st);
+    hipError_t ec = hipStreamEndCapture(st, &g);
+    if (rc) {
+      if (g) (void)hipGraphDestroy(g);
+      return rc;
+    }
+    OI2_CHECK_HIP(ec);
+    hipError_t ei = hipGraphInstantiate(&s->exec, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    OI2_CHECK_HIP(ei);
+    s->g_in = x_in;
+    s->g_out = x_out;
+    s->g_stream = st;
+  }
+  OI2_CHECK_HIP(hipGraphLaunch(s->exec, st));
+  return OI2_OK;
+}
+
+int oi2_stack_set_graph(oi2_stack* s, int32_t enable) {
+  clear_error();
+  OI2_CHECK_ARG(s, "null stack");
+  s->use_graph = enable != 0;
+  return OI2_OK;
+}
+
+int oi2_stack_profile(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, float* up_ms,
+                      float* down_ms, void* stream) {
+  clear_error();
+  OI2_CHECK_ARG(s && x_in && x_out && up_ms && down_ms, "null argument");
+  hipStream_t st = (hipStream_t)stream;
+  std::vector<hipEvent_t> ev(3 * (size_t)s->n_layers, nullptr);
+  int rc = OI2_OK;
+  for (auto& e : ev) {
+    if (hipEventCreate(&e) != hipSuccess) {
+      set_error("hipEventCreate failed");
+      rc = OI2_EHIP;
+      break;
+    }
+  }
+  if (rc == OI2_OK) rc = stack_launch(s, x_in, x_out, st, ev.data());
+  if (rc == OI2_OK && hipStreamSynchronize(st) != hipSuccess) {
+    set_error("hipStreamSynchronize failed");
+    rc = OI2_EHIP;
+  }
+  for (int L = 0; rc == OI2_OK && L < s->n_layers; ++L) {
+    if (hipEventElapsedTime(&up_ms[L], ev[3 * L], ev[3 * L + 1]) != hipSuccess ||
+        hipEventElapsedTime(&down_ms[L], ev[3 * L + 1], ev[3 * L + 2]) != hipSuccess) {
+      set_error("hipEventElapsedTime failed");
+      rc = OI2_EHIP;
+    }
+  }
+  for (auto& e : ev)
+    if (e) (void)hipEventDestroy(e);
+  return rc;
+}
+
+int oi2_stack_trace(oi2_stack* s, uint16_t* xs, int32_t* counts, int32_t* slots, int32_t* ids,
+                    void* stream) {
+  clear_error();
+  OI2_CHECK_ARG(s, "null stack");
+  hipStream_t st = (hipStream_t)stream;
+  const size_t sel = (size_t)s->n_layers * s->n_chunks * kSelChunk;
+  if (xs) OI2_CHECK_HIP(hipMemcpyAsync(xs, s->xbuf, (size_t)s->n_layers * kH * 2, hipMemcpyDeviceToDevice, st));
+  if (counts)
+    OI2_CHECK_HIP(hipMemcpyAsync(counts, s->sel_counts, (size_t)s->n_layers * s->n_chunks * 4,
+                                 hipMemcpyDeviceToDevice, st));
+  if (slots) OI2_CHECK_HIP(hipMemcpyAsync(slots, s->sel_slots, sel * 4, hipMemcpyDeviceToDevice, st));
+  if (ids) OI2_CHECK_HIP(hipMemcpyAsync(ids, s->sel_ids, sel * 4, hipMemcpyDeviceToDevice, st));
+  return OI2_OK;
+}
+
+int oi2_stack_destroy(oi2_stack* s) {
+  clear_error();
+  if (!s) return OI2_OK;
+  stack_free(s);
+  delete s;
+  return OI2_OK;
+}
+
+}  // extern "C"

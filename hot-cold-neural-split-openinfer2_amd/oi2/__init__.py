@@ -1,0 +1,18 @@
+"""MI355X (gfx950) hot/cold sparse-FFN decode path behind OpenInfer2's
+interfaces: ColdWeightStore (splitter.py), SparseFFNLayer / sparse_ffn
+(engine.py) and PredictorRegistry / NeuronPredictor (predictor.py)."""
+from . import format
+from ._lib import OI2Error, load_library
+from .format import (ALIGN_BYTES, HIDDEN_DIM, NEURON_RECORD_BYTES, PAGE_ALIGN, quantize_int4)
+from .hot import HotWeights
+from .layer import ColdNeurons, SparseFFNLayer, sparse_ffn
+from .predictor import NeuronPredictor, PredictorRegistry
+from .stack import DecodeStack, StackLayer
+from .store import ColdSection, ColdWeightStore
+
+__all__ = [
+    "format", "OI2Error", "load_library", "ALIGN_BYTES", "HIDDEN_DIM", "NEURON_RECORD_BYTES",
+    "PAGE_ALIGN", "quantize_int4", "HotWeights", "ColdNeurons", "SparseFFNLayer", "sparse_ffn",
+    "NeuronPredictor", "PredictorRegistry", "DecodeStack", "StackLayer", "ColdSection",
+    "ColdWeightStore",
+]

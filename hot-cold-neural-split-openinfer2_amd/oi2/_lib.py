@@ -1,0 +1,132 @@
+"""ctypes binding of liboi2.so (the C ABI declared in include/oi2.h).
+
+The library is the only compute path: if it has not been built, or no
+gfx950 device is present, calls raise instead of falling back to anything.
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import os
+from ctypes import POINTER, Structure, c_float, c_int32, c_size_t, c_void_p
+
+import torch
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "liboi2.so")
+
+OI2_OK = 0
+ACT_SILU, ACT_RELU = 0, 1
+DTYPE_F32, DTYPE_BF16 = 0, 1
+HIDDEN = 4096
+SEL_CHUNK = 256
+
+
+class OI2Error(RuntimeError):
+    pass
+
+
+class Hot(Structure):
+    _fields_ = [("n_hot", c_int32), ("down_stride", c_int32), ("gate_q", c_void_p),
+                ("up_q", c_void_p), ("down_q", c_void_p), ("gate_scale", c_void_p),
+                ("up_scale", c_void_p), ("down_scale", c_void_p), ("gate_bias", c_void_p)]
+
+
+class Cold(Structure):
+    _fields_ = [("records", c_void_p), ("n_records", c_int32), ("gate_bias", c_void_p)]
+
+
+class Active(Structure):
+    _fields_ = [("slots", c_void_p), ("counts", c_void_p), ("n_chunks", c_int32),
+                ("chunk", c_int32)]
+
+
+class Predictor(Structure):
+    _fields_ = [("inter", c_int32), ("rank", c_int32), ("dtype", c_int32), ("down_w", c_void_p),
+                ("up_w", c_void_p), ("up_b", c_void_p)]
+
+
+class Layer(Structure):
+    _fields_ = [("hot", Hot), ("cold", Cold), ("lut", c_void_p), ("norm_w", c_void_p),
+                ("pred", Predictor)]
+
+
+_SIGS = {
+    "oi2_last_error": (ctypes.c_char_p, []),
+    "oi2_abi_version": (c_int32, []),
+    "oi2_record_bytes": (c_int32, []),
+    "oi2_dequant_records": (c_int32, [c_void_p, c_int32, c_void_p, c_int32, c_void_p, c_void_p,
+                                      c_void_p, c_void_p]),
+    "oi2_rmsnorm": (c_int32, [c_void_p, c_void_p, c_int32, c_float, c_void_p, c_void_p]),
+    "oi2_ffn_workspace_bytes": (c_size_t, [c_int32, c_int32]),
+    "oi2_ffn_forward": (c_int32, [c_void_p, c_int32, c_void_p, c_float, POINTER(Hot), POINTER(Cold),
+                                  POINTER(Active), c_int32, c_int32, c_int32, c_void_p, c_void_p,
+                                  c_void_p, c_size_t, c_void_p]),
+    "oi2_predict_workspace_bytes": (c_size_t, [POINTER(Predictor)]),
+    "oi2_predict": (c_int32, [c_void_p, c_int32, POINTER(Predictor), c_float, c_void_p, c_void_p,
+                              c_void_p, c_void_p, c_size_t, c_void_p]),
+    "oi2_predict_select": (c_int32, [c_void_p, c_int32, c_void_p, c_float, POINTER(Predictor),
+                                     c_float, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                     c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
+    "oi2_stack_create": (c_int32, [POINTER(Layer), c_int32, c_int32, c_float, c_int32, c_int32,
+                                   c_float, POINTER(c_void_p)]),
+    "oi2_stack_decode": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p]),
+    "oi2_stack_set_graph": (c_int32, [c_void_p, c_int32]),
+    "oi2_stack_profile": (c_int32, [c_void_p, c_void_p, c_void_p, POINTER(c_float),
+                                    POINTER(c_float), c_void_p]),
+    "oi2_stack_trace": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "oi2_stack_destroy": (c_int32, [c_void_p]),
+}
+
+_lib = None
+
+
+def load_library():
+    """Load liboi2.so and declare every exported signature (no GPU needed)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise OI2Error(f"{LIB_PATH} is missing: build it with `python -c 'import "
+                           f"__graft_entry__ as g; g.build()'` (hipcc, gfx950)")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        if lib.oi2_abi_version() != 1:
+            raise OI2Error("liboi2.so ABI version mismatch")
+        _lib = lib
+    return _lib
+
+
+def lib():
+    """The library, for compute calls: also requires a visible GPU."""
+    L = load_library()
+    if not torch.cuda.is_available():
+        raise OI2Error("oi2 kernels need a gfx950 GPU; none is visible")
+    return L
+
+
+def check(rc: int):
+    if rc != OI2_OK:
+        msg = load_library().oi2_last_error().decode(errors="replace")
+        raise OI2Error(f"oi2 call failed ({rc}): {msg}")
+
+
+def ptr(t) -> int | None:
+    if t is None:
+        return None
+    return t.data_ptr()
+
+
+def stream_handle(device=None) -> int | None:
+    s = torch.cuda.current_stream(device).cuda_stream
+    return s or None
+
+
+def logit_threshold(p: float) -> float:
+    """sigmoid(l) >= p  <=>  l >= log(p / (1 - p))."""
+    if p <= 0.0:
+        return -math.inf
+    if p >= 1.0:
+        return math.inf
+    return math.log(p / (1.0 - p))

@@ -1,0 +1,237 @@
+"""Drop-in hot/cold FFN layer: ``sparse_ffn`` and ``SparseFFNLayer`` with the
+reference's call surface (engine.py:163-312), computed by the fused HIP
+kernels.
+
+Differences in representation, not in meaning:
+  * hot weights stay fp8 in HBM (``HotWeights``) instead of being widened to
+    fp16 at load (engine.py:258-260);
+  * the cold "fetch" result is a ``ColdNeurons`` handle - the layer's resident
+    INT4 records plus the active slot list on the device - instead of three
+    dequantised fp32 tensors (engine.py:266-272); the FFN kernel gathers and
+    dequantises the records itself;
+  * the predictor's mask never leaves the device: the active list is
+    compacted on the GPU (engine.py:274-283 does ``nonzero().tolist()`` and a
+    Python filter), so ``submit_cold_fetch`` enqueues work and returns at once.
+"""
+from __future__ import annotations
+
+import ctypes
+from concurrent.futures import Future
+from pathlib import Path
+from typing import Optional
+
+import torch
+
+from . import _lib
+from .hot import HotWeights
+from .store import ColdSection, ColdWeightStore
+
+HIDDEN = _lib.HIDDEN
+
+
+class ColdNeurons:
+    """Active cold neurons of one layer: records + (chunked) slot list."""
+
+    def __init__(self, section: ColdSection | None, slots: torch.Tensor | None,
+                 counts: torch.Tensor | None, n_chunks: int, chunk: int, ids=None,
+                 gate_bias: torch.Tensor | None = None):
+        self.section = section
+        self.slots = slots
+        self.counts = counts
+        self.n_chunks = n_chunks
+        self.chunk = chunk
+        self.ids = ids
+        self.gate_bias = gate_bias
+
+    @classmethod
+    def from_slots(cls, section: ColdSection | None, slots, gate_bias=None) -> "ColdNeurons":
+        """A plain list of record slots (request order)."""
+        if section is None:
+            return cls(None, None, None, 0, 0)
+        dev = section.records.device
+        s = torch.as_tensor(slots, dtype=torch.int32).to(dev).reshape(-1)
+        n = int(s.shape[0])
+        if n == 0:
+            return cls(section, None, None, 0, 0)
+        counts = torch.tensor([n], dtype=torch.int32, device=dev)
+        return cls(section, s, counts, 1, n, gate_bias=gate_bias)
+
+    @classmethod
+    def from_ids(cls, section: ColdSection | None, neuron_ids, gate_bias=None) -> "ColdNeurons":
+        """read_neurons semantics: request order, absent ids skipped."""
+        if section is None:
+            return cls(None, None, None, 0, 0)
+        return cls.from_slots(section, section.slots_for(neuron_ids), gate_bias)
+
+    def empty(self) -> bool:
+        return self.section is None or self.n_chunks == 0
+
+    def structs(self):
+        if self.empty():
+            return None, None
+        return (self.section.struct(self.gate_bias),
+                _lib.Active(self.slots.data_ptr(), self.counts.data_ptr(), self.n_chunks,
+                            self.chunk))
+
+    def count(self) -> int:
+        """Number of active records (synchronises with the device)."""
+        if self.empty():
+            return 0
+        return int(self.counts.clamp(0, self.chunk).sum().item())
+
+
+class _Ready:
+    """Completed future: the fetch is already ordered on the device stream."""
+
+    def __init__(self, value):
+        self._value = value
+
+    def result(self, timeout=None):
+        return self._value
+
+    def done(self):
+        return True
+
+
+def _ffn(x2d, norm_w, eps, hot: HotWeights | None, cold: ColdNeurons | None, activation,
+         act_on_both, add_residual, out_dtype=torch.float16, want_y32=False):
+    dev = x2d.device
+    x2d = x2d.to(torch.float16).contiguous()
+    B = x2d.shape[0]
+    L = _lib.lib()
+    hot_s = hot.struct() if hot is not None and hot.n_hot > 0 else None
+    cold_s, act_s = cold.structs() if cold is not None else (None, None)
+    n_hot = hot.n_hot if hot_s is not None else 0
+    ws_bytes = L.oi2_ffn_workspace_bytes(B, n_hot)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    out = torch.empty_like(x2d)
+    y32 = torch.empty((B, HIDDEN), dtype=torch.float32, device=dev) if want_y32 else None
+    act = _lib.ACT_RELU if activation == "relu" else _lib.ACT_SILU
+    _lib.check(L.oi2_ffn_forward(
+        x2d.data_ptr(), B, _lib.ptr(norm_w), ctypes.c_float(eps),
+        ctypes.byref(hot_s) if hot_s is not None else None,
+        ctypes.byref(cold_s) if cold_s is not None else None,
+        ctypes.byref(act_s) if act_s is not None else None,
+        act, int(bool(act_on_both)), int(bool(add_residual)), out.data_ptr(), _lib.ptr(y32),
+        ws.data_ptr(), ws_bytes, _lib.stream_handle(dev)))
+    return (out, y32) if want_y32 else out
+
+
+def sparse_ffn(x: torch.Tensor, activation: str, act_on_both: bool,
+               gate_hot: Optional[HotWeights], up_hot=None, down_hot=None,
+               gate_cold: Optional[ColdNeurons] = None, up_cold=None, down_cold=None):
+    """engine.py:173-209: hot half + cold half of the gated FFN for x (B, H).
+
+    ``gate_hot`` carries the whole hot half (a HotWeights), ``gate_cold`` the
+    whole cold half (a ColdNeurons); the up/down arguments are accepted for
+    signature compatibility and must be None.  Either half may be None or
+    empty; both empty gives zeros.  Returns x.dtype (fp16)."""
+    if up_hot is not None or down_hot is not None or up_cold is not None or down_cold is not None:
+        raise TypeError("pass the hot half as one HotWeights and the cold half as one ColdNeurons")
+    if gate_hot is not None and not isinstance(gate_hot, HotWeights):
+        raise TypeError(f"gate_hot must be HotWeights, got {type(gate_hot).__name__}")
+    if gate_cold is not None and not isinstance(gate_cold, ColdNeurons):
+        raise TypeError(f"gate_cold must be ColdNeurons, got {type(gate_cold).__name__}")
+    out = _ffn(x.reshape(-1, HIDDEN), None, 0.0, gate_hot, gate_cold, activation, act_on_both,
+               add_residual=False)
+    return out.reshape(x.shape).to(x.dtype)
+
+
+class SparseFFNLayer(torch.nn.Module):
+    """engine.py:212-312 with the same constructor and methods."""
+
+    _EID = 0
+
+    def __init__(self, layer_idx: int, hot_dir: str, cold_store: ColdWeightStore,
+                 predictor, cfg: dict, device, executor=None, ffn_norm_weight=None,
+                 threshold: float = 0.5, hot: HotWeights | None = None):
+        super().__init__()
+        self.layer_idx = layer_idx
+        self.cold_store = cold_store
+        self.predictor = predictor
+        self.device = torch.device(device)
+        self.executor = executor
+        self.activation = cfg.get("hidden_act", "silu")
+        self.act_on_both = cfg.get("act_on_both", False)
+        self.inter_dim = cfg["intermediate_dim"]
+        self.eps = float(cfg["rms_norm_eps"])
+        self.threshold = threshold
+        H = cfg["hidden_dim"]
+        if H != HIDDEN:
+            raise ValueError(f"hidden_dim {H}: the kernels are built for {HIDDEN}")
+        w = ffn_norm_weight if ffn_norm_weight is not None else torch.ones(H)
+        self.norm_weight = w.to(device=self.device, dtype=torch.float16).contiguous()
+        self.hot = hot
+        if self.hot is None:
+            p = Path(hot_dir) / f"layer_{layer_idx:03d}_expert_{self._EID:03d}.pt"
+            if p.exists():
+                self.hot = HotWeights.load(str(p), self.device)
+        self._hot_id_set = set(self.hot.neuron_ids.tolist()) if self.hot is not None else set()
+        self._section = cold_store.section(layer_idx, self._EID) if cold_store is not None else None
+        self._n_chunks = (self.inter_dim + _lib.SEL_CHUNK - 1) // _lib.SEL_CHUNK
+        self._lut = self._section.lut if self._section is not None else None
+
+    # ── cold selection ──
+    def _cold_ids_for(self, x_normed: torch.Tensor) -> list[int]:
+        """engine.py:274-283 as a host list (debug / compatibility helper; the
+        forward path keeps the list on the device)."""
+        sel = self._select(x_normed, normed=True)
+        if sel.empty():
+            return []
+        ids = []
+        counts = sel.counts.cpu().tolist()
+        cpu_ids = sel.ids.cpu()
+        for c, n in enumerate(counts):
+            ids.extend(cpu_ids[c * sel.chunk: c * sel.chunk + n].tolist())
+        return ids
+
+    def _select(self, x: torch.Tensor, normed: bool) -> ColdNeurons:
+        sec = self._section
+        if sec is None:
+            return ColdNeurons(None, None, None, 0, 0)
+        pred = None
+        if self.predictor is not None:
+            pred = (self.predictor.get(self.layer_idx, self._EID)
+                    if hasattr(self.predictor, "get") else self.predictor)
+        if pred is None:
+            # no predictor: every cold neuron, ascending id order
+            slots = sec.all_slots()
+            return ColdNeurons(sec, slots, torch.tensor([slots.shape[0]], dtype=torch.int32,
+                                                        device=self.device),
+                               1, max(1, int(slots.shape[0])))
+        q = x[:, -1, :] if x.dim() == 3 else x.reshape(-1, HIDDEN)
+        q = q.to(torch.float16).contiguous()
+        nc = self._n_chunks
+        dev = self.device
+        slots = torch.empty(nc * _lib.SEL_CHUNK, dtype=torch.int32, device=dev)
+        ids = torch.empty(nc * _lib.SEL_CHUNK, dtype=torch.int32, device=dev)
+        counts = torch.empty(nc, dtype=torch.int32, device=dev)
+        p = pred.struct()
+        L = _lib.lib()
+        ws_bytes = L.oi2_predict_workspace_bytes(ctypes.byref(p))
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+        _lib.check(L.oi2_predict_select(
+            q.data_ptr(), q.shape[0], None if normed else self.norm_weight.data_ptr(),
+            ctypes.c_float(self.eps), ctypes.byref(p), _lib.logit_threshold(self.threshold),
+            sec.lut.data_ptr(), slots.data_ptr(), ids.data_ptr(), counts.data_ptr(), None, None,
+            None, ws.data_ptr(), ws_bytes, _lib.stream_handle(dev)))
+        return ColdNeurons(sec, slots, counts, nc, _lib.SEL_CHUNK, ids=ids)
+
+    def submit_cold_fetch(self, x: torch.Tensor):
+        """engine.py:285-290: predict this layer's cold set from x (normalised
+        with this layer's norm) and return an object with ``.result()``.  With
+        the device-resident store the work is only enqueued on the stream, so
+        the returned future is already complete."""
+        with torch.no_grad():
+            return _Ready(self._select(x, normed=False))
+
+    def forward(self, x: torch.Tensor, prefetch_future=None) -> torch.Tensor:
+        """engine.py:292-312: residual + FFN(RMSNorm(x)) for x (B, T, H)."""
+        B, T, H = x.shape
+        cold = prefetch_future.result() if prefetch_future is not None else \
+            self._select(x, normed=False)
+        if isinstance(cold, Future):
+            cold = cold.result()
+        out = _ffn(x.reshape(B * T, H), self.norm_weight, self.eps, self.hot, cold,
+                   self.activation, self.act_on_both, add_residual=True)
+        return out.reshape(B, T, H).to(x.dtype)

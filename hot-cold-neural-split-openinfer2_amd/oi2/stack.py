@@ -1,0 +1,100 @@
+"""FFN-only decode stack on the device (the layer loop of engine.py:421-438
+without attention), batch 1, one C call per token."""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import _lib
+from .hot import HotWeights
+from .predictor import NeuronPredictor
+
+HIDDEN = _lib.HIDDEN
+
+
+@dataclass
+class StackLayer:
+    hot: Optional[HotWeights]
+    records: Optional[torch.Tensor]       # (n, 6400) uint8 device
+    lut: Optional[torch.Tensor]           # (inter,) int32 device
+    norm_w: torch.Tensor                  # (H,) fp16 device
+    predictor: Optional[NeuronPredictor]
+    cold_gate_bias: Optional[torch.Tensor] = None
+
+
+class DecodeStack:
+    def __init__(self, layers: list[StackLayer], inter: int, eps: float, activation: str = "silu",
+                 act_on_both: bool = False, threshold_logit: float = 0.0, use_graph: bool = True):
+        self.layers = layers
+        self.inter = inter
+        self.n_layers = len(layers)
+        self.n_chunks = (inter + _lib.SEL_CHUNK - 1) // _lib.SEL_CHUNK
+        arr = (_lib.Layer * self.n_layers)()
+        for i, l in enumerate(layers):
+            hot = l.hot.struct() if l.hot is not None else _lib.Hot()
+            n_rec = int(l.records.shape[0]) if l.records is not None else 0
+            cold = _lib.Cold(_lib.ptr(l.records) if n_rec else None, n_rec, _lib.ptr(l.cold_gate_bias))
+            pred = l.predictor.struct() if l.predictor is not None else _lib.Predictor()
+            arr[i] = _lib.Layer(hot, cold, _lib.ptr(l.lut), l.norm_w.data_ptr(), pred)
+        self._arr = arr
+        L = _lib.lib()
+        h = ctypes.c_void_p()
+        act = _lib.ACT_RELU if activation == "relu" else _lib.ACT_SILU
+        _lib.check(L.oi2_stack_create(arr, self.n_layers, inter, ctypes.c_float(eps), act,
+                                      int(bool(act_on_both)), ctypes.c_float(threshold_logit),
+                                      ctypes.byref(h)))
+        self._h = h
+        _lib.check(L.oi2_stack_set_graph(h, int(bool(use_graph))))
+
+    def decode(self, x_in: torch.Tensor, x_out: torch.Tensor, stream=None):
+        """x_out (H) fp16 = the token after every FFN layer."""
+        s = stream.cuda_stream if stream is not None else _lib.stream_handle(x_in.device)
+        _lib.check(_lib.lib().oi2_stack_decode(self._h, x_in.data_ptr(), x_out.data_ptr(), s or None))
+
+    def profile(self, x_in: torch.Tensor, x_out: torch.Tensor, stream=None):
+        """Per-layer (ffn_up ms, ffn_down ms) from hipEvents on the launch stream."""
+        n = self.n_layers
+        up = (ctypes.c_float * n)()
+        down = (ctypes.c_float * n)()
+        s = stream.cuda_stream if stream is not None else _lib.stream_handle(x_in.device)
+        _lib.check(_lib.lib().oi2_stack_profile(self._h, x_in.data_ptr(), x_out.data_ptr(), up, down,
+                                                s or None))
+        return list(up), list(down)
+
+    def trace(self):
+        """(xs (n_layers, H) fp16 layer outputs, counts (n_layers, n_chunks),
+        slots, ids (n_layers, n_chunks*256)) of the last decode."""
+        dev = self.layers[0].norm_w.device
+        n, nc = self.n_layers, self.n_chunks
+        xs = torch.empty((n, HIDDEN), dtype=torch.float16, device=dev)
+        counts = torch.empty((n, nc), dtype=torch.int32, device=dev)
+        slots = torch.empty((n, nc * _lib.SEL_CHUNK), dtype=torch.int32, device=dev)
+        ids = torch.empty((n, nc * _lib.SEL_CHUNK), dtype=torch.int32, device=dev)
+        _lib.check(_lib.lib().oi2_stack_trace(self._h, xs.data_ptr(), counts.data_ptr(),
+                                              slots.data_ptr(), ids.data_ptr(),
+                                              _lib.stream_handle(dev)))
+        return xs, counts, slots, ids
+
+    def active_ids(self, layer: int, counts=None, ids=None) -> list[int]:
+        if counts is None:
+            _, counts, _, ids = self.trace()
+        c = counts[layer].cpu().tolist()
+        row = ids[layer].cpu()
+        out = []
+        for k, n in enumerate(c):
+            out.extend(row[k * _lib.SEL_CHUNK: k * _lib.SEL_CHUNK + n].tolist())
+        return out
+
+    def close(self):
+        if self._h:
+            _lib.lib().oi2_stack_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

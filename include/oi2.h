@@ -1,0 +1,200 @@
+/*
+ * oi2.h - C ABI of the MI355X (gfx950) hot/cold sparse-FFN decode library.
+ *
+ * Every entry point takes raw device pointers, sizes and a HIP stream passed
+ * as void* (hipStream_t; NULL = the default stream), enqueues its work
+ * asynchronously on that stream and returns an int status: OI2_OK (0) or an
+ * error code, with a message available from oi2_last_error() on the calling
+ * thread.  Nothing throws across the ABI.  Entry points that need scratch
+ * memory take a caller-provided workspace (size from the matching *_bytes
+ * query) and allocate nothing; the stack and stager handles allocate once,
+ * at creation.
+ *
+ * Layouts (H = 4096, the hidden size the cold-record format is sized for):
+ *   activations   fp16, row-major (batch, H)
+ *   hot weights   fp8 e4m3fn (OCP) with fp32 per-row scales:
+ *                 gate/up (n_hot, H), down (H, down_stride) row-major, columns
+ *                 n_hot..down_stride-1 zero
+ *   cold records  the split format's 6400-byte records (splitter.py:23-39),
+ *                 consecutive, record 0 at a 16-byte aligned address
+ *   predictor     fp32 or bf16: down (rank, H), up (inter, rank), bias (inter)
+ *
+ * Citations are file:line in the reference (OpenInfer2) checkout.
+ */
+#ifndef OI2_H
+#define OI2_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OI2_ABI_VERSION 1
+
+enum {
+  OI2_OK = 0,
+  OI2_EINVAL = 1,       /* bad argument (shape, pointer, size) */
+  OI2_EHIP = 2,         /* a HIP runtime call failed */
+  OI2_ENOMEM = 3,       /* workspace too small / allocation failed at creation */
+  OI2_EUNSUPPORTED = 4  /* valid request outside what this build implements */
+};
+
+enum { OI2_ACT_SILU = 0, OI2_ACT_RELU = 1 };          /* engine.py:165 */
+enum { OI2_DTYPE_F32 = 0, OI2_DTYPE_BF16 = 1 };
+
+/* Hot FP8 half of one layer: the tensors SparseFFNLayer loads from
+ * hot_weights/layer_XXX_expert_000.pt (engine.py:252-264, written at
+ * splitter.py:221-226), kept at fp8 with per-row scales (1.0 reproduces the
+ * reference's unscaled cast). */
+typedef struct oi2_hot {
+  int32_t n_hot;
+  int32_t down_stride;        /* bytes per down row; >= n_hot, multiple of 16 */
+  const uint8_t* gate_q;      /* (n_hot, H) */
+  const uint8_t* up_q;        /* (n_hot, H) */
+  const uint8_t* down_q;      /* (H, down_stride) */
+  const float* gate_scale;    /* (n_hot) */
+  const float* up_scale;      /* (n_hot) */
+  const float* down_scale;    /* (H) */
+  const float* gate_bias;     /* (n_hot) gate pre-activation shift, or NULL */
+} oi2_hot;
+
+/* One layer's cold section resident in device memory: the records that
+ * ColdWeightStore.read_neurons decodes (splitter.py:354-403). */
+typedef struct oi2_cold {
+  const uint8_t* records;     /* record slot 0 */
+  int32_t n_records;
+  const float* gate_bias;     /* per record slot, or NULL */
+} oi2_cold;
+
+/* The active cold set: record slots grouped in n_chunks chunks of capacity
+ * `chunk`; counts[c] valid entries start at slots[c * chunk].  A plain list of
+ * n slots is one chunk with counts -> {n}.  counts live in device memory, so a
+ * predictor's output feeds the FFN without a host round trip. */
+typedef struct oi2_active {
+  const int32_t* slots;
+  const int32_t* counts;
+  int32_t n_chunks;           /* 1..256 */
+  int32_t chunk;
+} oi2_active;
+
+/* NeuronPredictor weights (predictor.py:55-75): sigmoid(up(down(x))). */
+typedef struct oi2_predictor {
+  int32_t inter;              /* intermediate size I (<= 65536) */
+  int32_t rank;               /* low-rank width (multiple of 4, <= 256) */
+  int32_t dtype;              /* OI2_DTYPE_F32 or OI2_DTYPE_BF16 */
+  const void* down_w;         /* (rank, H), no bias (predictor.py:67) */
+  const void* up_w;           /* (inter, rank) (predictor.py:68) */
+  const void* up_b;           /* (inter) */
+} oi2_predictor;
+
+/* ---- library ---------------------------------------------------------- */
+const char* oi2_last_error(void);
+int oi2_abi_version(void);
+/* NEURON_RECORD_BYTES, splitter.py:75-76 */
+int oi2_record_bytes(void);
+
+/* ---- cold records ------------------------------------------------------- */
+/* Replaces the per-neuron dequant loop of ColdWeightStore.read_neurons
+ * (splitter.py:369-403) and dequantize_int4 (splitter.py:111-124): decodes
+ * records[slots[k]] for k < n into gate (n, H), up (n, H) and down_t (H, n),
+ * fp32, bit-exact.  Slot lookup / absent-id skipping is the caller's. */
+int oi2_dequant_records(const uint8_t* records, int32_t n_records, const int32_t* slots,
+                        int32_t n, float* gate, float* up, float* down_t, void* stream);
+
+/* ---- norm --------------------------------------------------------------- */
+/* nn.RMSNorm as SparseFFNLayer.input_layernorm (engine.py:247-249, :289,
+ * :295): out = x * rsqrt(mean(x^2) + eps) * w over rows of H fp16 values. */
+int oi2_rmsnorm(const uint16_t* x, const uint16_t* w, int32_t rows, float eps,
+                uint16_t* out, void* stream);
+
+/* ---- FFN ---------------------------------------------------------------- */
+/* Workspace bytes for oi2_ffn_forward at this batch / hot size. */
+size_t oi2_ffn_workspace_bytes(int32_t batch, int32_t n_hot);
+
+/* sparse_ffn (engine.py:173-209) and SparseFFNLayer.forward
+ * (engine.py:292-312) for `batch` tokens sharing one active cold set:
+ *   x_n  = norm_w ? RMSNorm(x) : x
+ *   y    = hot(x_n) + cold(x_n)        fp32, hot = fp8 GEMV, cold = fused
+ *                                      INT4 gather/dequant/act/down
+ *   out  = (add_residual ? x : 0) + y  fp16 (may be NULL)
+ *   y32  = y                           fp32 (may be NULL)
+ * hot may be NULL or n_hot 0; cold/active may be NULL or empty (then that
+ * half contributes nothing, engine.py:194-209).  act: OI2_ACT_*. */
+int oi2_ffn_forward(const uint16_t* x, int32_t batch, const uint16_t* norm_w, float eps,
+                    const oi2_hot* hot, const oi2_cold* cold, const oi2_active* active,
+                    int32_t act, int32_t act_on_both, int32_t add_residual, uint16_t* out,
+                    float* y32, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- predictor ---------------------------------------------------------- */
+size_t oi2_predict_workspace_bytes(const oi2_predictor* p);
+
+/* PredictorRegistry.predict (predictor.py:435-456) with NeuronPredictor's
+ * forward / predict_mask (predictor.py:70-79) for `rows` query rows h (fp16,
+ * cast to the predictor dtype as predictor.py:455 does): logits (rows, inter)
+ * fp32, probs = sigmoid(logits) fp32 and/or mask (rows, inter) bytes =
+ * sigmoid(logit) >= threshold, evaluated as logit >= threshold_logit =
+ * log(p / (1 - p)).  Any output may be NULL. */
+int oi2_predict(const uint16_t* h, int32_t rows, const oi2_predictor* p, float threshold_logit,
+                float* logits, float* probs, uint8_t* mask, void* workspace,
+                size_t workspace_bytes, void* stream);
+
+/* SparseFFNLayer._cold_ids_for (engine.py:274-283) on device: query =
+ * mean over the `batch` rows of RMSNorm(x) (norm_w may be NULL for an already
+ * normalised x), predicted-active ids in ascending order, minus ids whose
+ * lut entry is < 0 (hot or absent from the section, which read_neurons skips,
+ * splitter.py:371-372).  Output is chunked (chunk = 256): counts[c] (device
+ * ints, n_chunks = ceil(inter / 256)), slots[c*256 + k] = lut[id] and
+ * ids[c*256 + k] = id.  If total is non-NULL it receives the dense count and
+ * slots/ids are additionally compacted in place into dense ascending order
+ * (dense_slots / dense_ids, length >= inter). */
+int oi2_predict_select(const uint16_t* x, int32_t batch, const uint16_t* norm_w, float eps,
+                       const oi2_predictor* p, float threshold_logit, const int32_t* lut,
+                       int32_t* slots, int32_t* ids, int32_t* counts, int32_t* dense_slots,
+                       int32_t* dense_ids, int32_t* total, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
+/* ---- whole decode step ------------------------------------------------- */
+/* One layer of the FFN-only decode stack: the per-layer state that
+ * DesdemonaEngine passes to SparseFFNLayer (engine.py:391-398). */
+typedef struct oi2_layer {
+  oi2_hot hot;
+  oi2_cold cold;
+  const int32_t* lut;         /* (inter) id -> record slot, -1 for hot / absent */
+  const uint16_t* norm_w;     /* (H) fp16 post_attention_layernorm weight */
+  oi2_predictor pred;         /* pred.down_w == NULL: no predictor, fetch all */
+} oi2_layer;
+
+typedef struct oi2_stack oi2_stack;
+
+/* DesdemonaEngine.forward's layer loop restricted to the FFN sublayers
+ * (engine.py:421-438), batch 1: layer 0's cold set is predicted from the
+ * input, layer L+1's from layer L's input (the one-sublayer lookahead), and
+ * x_{L+1} = x_L + FFN_L(RMSNorm_L(x_L)).  `layers` is copied; the pointed-to
+ * device memory must outlive the stack.  Allocates its workspaces here. */
+int oi2_stack_create(const oi2_layer* layers, int32_t n_layers, int32_t inter, float eps,
+                     int32_t act, int32_t act_on_both, float threshold_logit,
+                     oi2_stack** out);
+/* One token through all layers: x_out (H) fp16 from x_in (H) fp16. */
+int oi2_stack_decode(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, void* stream);
+/* Replay the launch sequence through a captured hipGraph (default 1) or launch
+ * it directly (0).  Graphs are never used on the NULL stream. */
+int oi2_stack_set_graph(oi2_stack* s, int32_t enable);
+/* Per-layer inputs x_L (n_layers, H) fp16 and active sets of the last
+ * decode: counts (n_layers, n_chunks) and slots/ids (n_layers, n_chunks*256),
+ * copied to device buffers supplied by the caller (any may be NULL). */
+/* One token like oi2_stack_decode, launched directly with a hipEvent
+ * recorded around every layer's two launches; waits for the stream and
+ * writes each layer's ffn_up and ffn_down durations (n_layers floats each,
+ * milliseconds). */
+int oi2_stack_profile(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, float* up_ms,
+                      float* down_ms, void* stream);
+int oi2_stack_trace(oi2_stack* s, uint16_t* xs, int32_t* counts, int32_t* slots, int32_t* ids,
+                    void* stream);
+int oi2_stack_destroy(oi2_stack* s);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* OI2_H */
