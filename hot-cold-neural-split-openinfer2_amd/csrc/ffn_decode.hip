@@ -111,6 +111,12 @@ __device__ void cold_role(const UpArgs& a, int wg, float r, float* s_lds, int* s
   chunk_prefix(a.act, s_prefix);
   const int n_chunks = a.act.n_chunks;
   const int total = s_prefix[n_chunks];
+  // workgroups actually used: about kRecordsPerColdWG records each, so the
+  // number of 16 KB partial rows follows the active count, not the capacity
+  int n_eff = (total + kRecordsPerColdWG - 1) / kRecordsPerColdWG;
+  n_eff = n_eff < 1 ? 1 : (n_eff > a.wg_cold ? a.wg_cold : n_eff);
+  if (wg == 0 && threadIdx.x == 0 && a.n_part_out) *a.n_part_out = n_eff;
+  if (wg >= n_eff) return;
 
   // token values for elements [32 lane + 2048 it, +32), in nibble-pair order
   f16x2 xc[2][16];
@@ -133,7 +139,7 @@ __device__ void cold_role(const UpArgs& a, int wg, float r, float* s_lds, int* s
 #pragma unroll
   for (int i = 0; i < 64; ++i) acc[i] = 0.0f;
 
-  const int n_waves = a.wg_cold * 4;
+  const int n_waves = n_eff * 4;
   for (int i = wg * 4 + w; i < total; i += n_waves) {
     int lo = 0, hi = n_chunks;
     while (hi - lo > 1) {
@@ -457,7 +463,8 @@ __device__ void down_role(const DownArgs& a, int wg, float* s_part, float* s_yho
   }
   const int row = t & 15, ps = t >> 4;
   float s = 0.0f;
-  for (int p = ps; p < a.n_partials; p += 16) s += a.partials[(size_t)p * kH + j0 + row];
+  const int n_part = a.n_part_in ? *a.n_part_in : a.n_partials;
+  for (int p = ps; p < n_part; p += 16) s += a.partials[(size_t)p * kH + j0 + row];
   s_part[t] = s;
   __syncthreads();
   if (t < 16) {
@@ -603,7 +610,7 @@ void clear_error() { g_err.clear(); }
 static int n_chunks_for(int inter) { return (inter + kSelChunk - 1) / kSelChunk; }
 
 static int cold_wg_for(int capacity) {
-  int wg = (capacity + 7) / 8;
+  int wg = (capacity + kRecordsPerColdWG - 1) / kRecordsPerColdWG;
   return wg < 1 ? 1 : (wg > kMaxColdWG ? kMaxColdWG : wg);
 }
 
@@ -702,6 +709,7 @@ int oi2_ffn_forward(const uint16_t* x, int32_t batch, const uint16_t* norm_w, fl
                 oi2_ffn_workspace_bytes(batch, n_hot));
   float* h_hot = reinterpret_cast<float*>(workspace);
   float* partials = h_hot + ((n_hot + 64) & ~63);
+  int* n_part = reinterpret_cast<int*>(partials + (size_t)kMaxColdWG * kH);
   const int wg_cold = has_cold ? cold_wg_for(active->n_chunks * active->chunk < cold->n_records
                                                  ? active->n_chunks * active->chunk
                                                  : cold->n_records)
@@ -731,6 +739,7 @@ int oi2_ffn_forward(const uint16_t* x, int32_t batch, const uint16_t* norm_w, fl
       ua.act = ActiveList{active->slots, active->counts, active->n_chunks, active->chunk};
     }
     ua.partials = partials;
+    ua.n_part_out = n_part;
     ua.wg_cold = wg_cold;
     ua.wg_pred = 0;
     ua.wg_hot = (n_hot + 7) / 8;
@@ -749,7 +758,8 @@ int oi2_ffn_forward(const uint16_t* x, int32_t batch, const uint16_t* norm_w, fl
       da.down_s = hot->down_scale;
     }
     da.partials = partials;
-    da.n_partials = wg_cold;
+    da.n_partials = 0;
+    da.n_part_in = wg_cold ? n_part : nullptr;
     da.out = out ? out + (size_t)b * kH : nullptr;
     da.y32 = y32 ? y32 + (size_t)b * kH : nullptr;
     da.wg_pred = 0;

@@ -8,7 +8,8 @@ constexpr int kThreads = 256;
 constexpr int kRowsPerDownWG = 16;
 constexpr int kSelChunk = 256;
 constexpr int kMaxChunks = 256;
-constexpr int kMaxColdWG = 64;
+constexpr int kMaxColdWG = 256;
+constexpr int kRecordsPerColdWG = 8;   // target records per cold workgroup (2 per wave)
 constexpr int kLdsRed = kH + kH / 32;
 
 struct ActiveList {
@@ -37,6 +38,7 @@ struct UpArgs {
   const float* cold_gbias;
   ActiveList act;
   float* partials;          // (wg_cold, H)
+  int* n_part_out;          // cold workgroup 0 publishes how many partial rows it used
   // predictor down projection of the lookahead layer
   const void* pd_w;
   int pd_rank;
@@ -55,7 +57,8 @@ struct DownArgs {
   const uint8_t* down_q;
   const float* down_s;
   const float* partials;
-  int n_partials;
+  int n_partials;           // used when n_part_in is null
+  const int* n_part_in;     // partial rows written by ffn_up's cold workgroups
   uint16_t* out;
   uint16_t* out2;
   float* y32;

@@ -35,16 +35,20 @@ struct oi2_stack {
   uint16_t* xbuf = nullptr;      // (n_layers, H): output of each layer
   float* h_hot = nullptr;
   float* partials = nullptr;     // (kMaxColdWG, H)
+  int* n_part = nullptr;         // partial rows used by the current layer
   float* z = nullptr;
   int32_t* sel_counts = nullptr; // (n_layers, n_chunks)
   int32_t* sel_slots = nullptr;  // (n_layers, n_chunks * 256)
   int32_t* sel_ids = nullptr;
   int cold_wg = 1;
   bool use_graph = true;
-  hipGraphExec_t exec = nullptr;
-  const void* g_in = nullptr;
-  void* g_out = nullptr;
-  hipStream_t g_stream = nullptr;
+  struct GraphEntry {
+    hipGraphExec_t exec;
+    const void* in;
+    void* out;
+    hipStream_t stream;
+  };
+  std::vector<GraphEntry> graphs;   // small cache keyed by (x_in, x_out, stream)
 };
 
 namespace oi2 {
@@ -114,6 +118,7 @@ static int stack_launch(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, hip
         ua.act = ActiveList{SL.all_slots, SL.all_count, 1, SL.n_all};
     }
     ua.partials = s->partials;
+    ua.n_part_out = s->n_part;
     ua.wg_cold = has_cold ? s->cold_wg : 0;
     ua.wg_hot = (l.hot.n_hot + 7) / 8;
     if (pred_next) {
@@ -141,7 +146,8 @@ static int stack_launch(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, hip
     da.down_q = l.hot.down_q;
     da.down_s = l.hot.down_scale;
     da.partials = s->partials;
-    da.n_partials = ua.wg_cold;
+    da.n_partials = 0;
+    da.n_part_in = ua.wg_cold ? s->n_part : nullptr;
     da.out = s->xbuf + (size_t)L * kH;
     da.out2 = (L == n - 1) ? x_out : nullptr;
     if (pred_next) {
@@ -172,8 +178,9 @@ static void stack_free(oi2_stack* s) {
     if (L.all_slots) (void)hipFree(L.all_slots);
     if (L.all_count) (void)hipFree(L.all_count);
   }
-  if (s->exec) (void)hipGraphExecDestroy(s->exec);
-  for (void* p : {(void*)s->xbuf, (void*)s->h_hot, (void*)s->partials, (void*)s->z,
+  for (auto& g : s->graphs) (void)hipGraphExecDestroy(g.exec);
+  s->graphs.clear();
+  for (void* p : {(void*)s->xbuf, (void*)s->h_hot, (void*)s->partials, (void*)s->n_part, (void*)s->z,
                   (void*)s->sel_counts, (void*)s->sel_slots, (void*)s->sel_ids})
     if (p) (void)hipFree(p);
 }
@@ -235,7 +242,7 @@ int oi2_stack_create(const oi2_layer* layers, int32_t n_layers, int32_t inter, f
     max_records = std::max(max_records, SL.l.cold.n_records);
     s->layers.push_back(SL);
   }
-  s->cold_wg = std::max(1, std::min(kMaxColdWG, (max_records + 7) / 8));
+  s->cold_wg = std::max(1, std::min(kMaxColdWG, (max_records + kRecordsPerColdWG - 1) / kRecordsPerColdWG));
   const size_t sel = (size_t)n_layers * s->n_chunks * kSelChunk;
   hipError_t e = hipSuccess;
   auto alloc = [&](void** p, size_t bytes) {
@@ -244,6 +251,7 @@ int oi2_stack_create(const oi2_layer* layers, int32_t n_layers, int32_t inter, f
   alloc((void**)&s->xbuf, (size_t)n_layers * kH * 2);
   alloc((void**)&s->h_hot, (size_t)(s->max_hot + 64) * 4);
   alloc((void**)&s->partials, (size_t)kMaxColdWG * kH * 4);
+  alloc((void**)&s->n_part, 64);
   alloc((void**)&s->z, (size_t)(s->max_rank + 64) * 4);
   alloc((void**)&s->sel_counts, (size_t)n_layers * s->n_chunks * 4);
   alloc((void**)&s->sel_slots, sel * 4);
@@ -281,28 +289,30 @@ int oi2_stack_decode(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, void* 
   OI2_CHECK_ARG(((uintptr_t)x_in | (uintptr_t)x_out) % 16 == 0, "x must be 16-byte aligned");
   hipStream_t st = (hipStream_t)stream;
   if (!s->use_graph || st == nullptr) return stack_launch(s, x_in, x_out, st);
-  if (!s->exec || s->g_in != x_in || s->g_out != x_out || s->g_stream != st) {
-    if (s->exec) {
-      OI2_CHECK_HIP(hipGraphExecDestroy(s->exec));
-      s->exec = nullptr;
+  for (auto& g : s->graphs)
+    if (g.in == x_in && g.out == x_out && g.stream == st) {
+      OI2_CHECK_HIP(hipGraphLaunch(g.exec, st));
+      return OI2_OK;
     }
-    hipGraph_t g = nullptr;
-    OI2_CHECK_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
-    int rc = stack_launch(s, x_in, x_out, st);
-    hipError_t ec = hipStreamEndCapture(st, &g);
-    if (rc) {
-      if (g) (void)hipGraphDestroy(g);
-      return rc;
-    }
-    OI2_CHECK_HIP(ec);
-    hipError_t ei = hipGraphInstantiate(&s->exec, g, nullptr, nullptr, 0);
-    (void)hipGraphDestroy(g);
-    OI2_CHECK_HIP(ei);
-    s->g_in = x_in;
-    s->g_out = x_out;
-    s->g_stream = st;
+  if (s->graphs.size() >= 8) {
+    OI2_CHECK_HIP(hipGraphExecDestroy(s->graphs.front().exec));
+    s->graphs.erase(s->graphs.begin());
   }
-  OI2_CHECK_HIP(hipGraphLaunch(s->exec, st));
+  hipGraph_t g = nullptr;
+  OI2_CHECK_HIP(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal));
+  int rc = stack_launch(s, x_in, x_out, st);
+  hipError_t ec = hipStreamEndCapture(st, &g);
+  if (rc) {
+    if (g) (void)hipGraphDestroy(g);
+    return rc;
+  }
+  OI2_CHECK_HIP(ec);
+  hipGraphExec_t exec = nullptr;
+  hipError_t ei = hipGraphInstantiate(&exec, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  OI2_CHECK_HIP(ei);
+  s->graphs.push_back({exec, x_in, x_out, st});
+  OI2_CHECK_HIP(hipGraphLaunch(exec, st));
   return OI2_OK;
 }
 

@@ -93,6 +93,19 @@ class _Ready:
         return True
 
 
+def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """nn.RMSNorm over the last dim of fp16 x (engine.py:247-249), on the GPU:
+    fp16(x * rsqrt(mean(x^2) + eps) * w) - the same arithmetic the FFN and
+    predictor kernels apply to their input."""
+    shape = x.shape
+    x2 = x.reshape(-1, HIDDEN).to(torch.float16).contiguous()
+    w = weight.to(device=x2.device, dtype=torch.float16).contiguous()
+    out = torch.empty_like(x2)
+    _lib.check(_lib.lib().oi2_rmsnorm(x2.data_ptr(), w.data_ptr(), x2.shape[0], ctypes.c_float(eps),
+                                      out.data_ptr(), _lib.stream_handle(x2.device)))
+    return out.reshape(shape)
+
+
 def _ffn(x2d, norm_w, eps, hot: HotWeights | None, cold: ColdNeurons | None, activation,
          act_on_both, add_residual, out_dtype=torch.float16, want_y32=False):
     dev = x2d.device

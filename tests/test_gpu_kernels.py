@@ -1,0 +1,366 @@
+"""GPU parity of the HIP path against the CPU oracle, through the C ABI.
+
+Bars: bit-exact for dequant, fp8 decode and index sets (outside the 1e-6
+logit band); FFN outputs within max rel err 1e-2 and cosine >= 0.9999 of the
+float64 oracle over the same quantised weights.
+"""
+import math
+import os
+import tempfile
+import hashlib
+import json
+
+import numpy as np
+import pytest
+import torch
+
+import oi2
+from oi2 import _lib
+from oi2.layer import ColdNeurons, _ffn, rmsnorm
+from oi2.store import ColdSection
+from oi2.synth import SyntheticLayer, calibrate_threshold, random_predictor, records_from_rows
+from oracle import oracle as O
+from tests.fixtures import synthetic_cold_file
+from tests.gpu_helpers import (EPS, assert_ffn_close, chunked_ids, cold_dense, hot_dense,
+                               normed_f16, pred_weights, query_for)
+
+pytestmark = pytest.mark.gpu
+H = 4096
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+@pytest.fixture(scope="module")
+def dev():
+    assert torch.cuda.is_available(), "GPU tests need a visible GPU"
+    return torch.device("cuda:0")
+
+
+def _section(lay):
+    return ColdSection(0, lay.cold_ids.cpu().numpy(), lay.records, lay.lut, lay.lut.cpu().numpy(),
+                       lay.inter)
+
+
+# ── FP8 decode through the hot GEMV ──────────────────────────────────────────
+
+def test_fp8_decode_table_exact(dev):
+    """Hot neuron k's gate row holds code k at position 0; x = +-e_0, up = 1,
+    down = identity, relu(g)*u: y_k is the decoded code exactly."""
+    codes = np.arange(256, dtype=np.uint8)
+    codes[[0x7F, 0xFF]] = 0                      # the two NaN codes
+    n = 256
+    gate = torch.zeros((n, H), dtype=torch.uint8)
+    gate[:, 0] = torch.from_numpy(codes)
+    up = torch.zeros((n, H), dtype=torch.uint8)
+    up[:, 0] = 0x38                               # 1.0
+    down = torch.zeros((H, n), dtype=torch.uint8)
+    down[torch.arange(n), torch.arange(n)] = 0x38
+    ones_n = torch.ones(n)
+    hot = oi2.HotWeights(torch.arange(n), gate.to(dev), up.to(dev), down.to(dev), ones_n.to(dev),
+                         ones_n.to(dev), torch.ones(H).to(dev))
+    table = O.FP8_TABLE.copy()
+    table[[0x7F, 0xFF]] = 0.0
+    for sign in (1.0, -1.0):
+        x = torch.zeros((1, H), dtype=torch.float16, device=dev)
+        x[0, 0] = sign
+        _, y = _ffn(x, None, 0.0, hot, None, "relu", False, add_residual=False, want_y32=True)
+        got = y[0, :n].double().cpu().numpy()
+        want = sign * np.maximum(sign * table, 0.0)
+        assert np.array_equal(got, want), np.nonzero(got != want)
+
+
+# ── INT4 record dequant ──────────────────────────────────────────────────────
+
+def test_dequant_records_bit_exact(dev):
+    g = torch.Generator(device=dev).manual_seed(2)
+    n = 300
+    rows = [torch.randn((n, H), generator=g, device=dev) * s for s in (0.02, 1.0, 5.0)]
+    rec = records_from_rows(torch.arange(n), *rows)
+    # one record of raw bytes: every byte value, every scale sign
+    rec[7, 2:6146] = torch.arange(6144, device=dev).to(torch.uint8)
+    rec[7, 6146:6338] = torch.tensor(np.array([0.5, -1.25, 3.0, 2.0 ** -14] * 24, np.float16)
+                                     .view(np.uint8)).to(dev)
+    slots = torch.tensor([7, 0, 299, 7, 150, 3], dtype=torch.int32, device=dev)
+    out = torch.empty((3, 6, H), device=dev)
+    down_t = torch.empty((H, 6), device=dev)
+    L = _lib.lib()
+    _lib.check(L.oi2_dequant_records(rec.data_ptr(), n, slots.data_ptr(), 6, out[0].data_ptr(),
+                                     out[1].data_ptr(), down_t.data_ptr(), None))
+    torch.cuda.synchronize()
+    G, U, D = O.records_to_dense(rec.cpu().numpy(), slots.cpu().numpy())
+    assert np.array_equal(out[0].cpu().numpy().astype(np.float64), G)
+    assert np.array_equal(out[1].cpu().numpy().astype(np.float64), U)
+    assert np.array_equal(down_t.cpu().numpy().astype(np.float64), D)
+
+
+def test_store_read_neurons_matches_reference_truth(dev):
+    """tests/test_cold_store.py:28-91 semantics on the reference fixture's
+    byte image, values hashed against the reference's own dequant output."""
+    golden = json.load(open(os.path.join(GOLDEN, "cold_seed0.json")))
+    with tempfile.TemporaryDirectory() as tmp:
+        cold_bin, cold_idx, config, layers = synthetic_cold_file(tmp, 4, 16, 0)
+        store = oi2.ColdWeightStore(cold_bin, cold_idx, config, device=dev)
+        try:
+            for li in range(4):
+                nids = layers[li][0]
+                for nid in nids:
+                    gate, up, down = store.read_neurons(li, 0, [nid])
+                    assert gate.shape == (1, H) and up.shape == (1, H) and down.shape == (H, 1)
+                    for name, v in (("gate", gate[0]), ("up", up[0]), ("down", down[:, 0])):
+                        h = hashlib.sha256(v.cpu().numpy().astype("<f4").tobytes()).hexdigest()
+                        assert h == golden["truth_sha256"][f"{li}:{nid}:{name}"]
+            ids0 = layers[0][0]
+            out = store.read_neurons(0, 0, sorted(ids0))
+            assert out[0].shape == (16, H) and out[2].shape == (H, 16)
+            first = store.read_neurons(0, 0, [sorted(ids0)[0]])
+            assert torch.equal(out[0][0], first[0][0])
+            absent = max(ids0) + 1000
+            mixed = store.read_neurons(0, 0, [ids0[0], absent, ids0[0]])
+            assert mixed[0].shape[0] == 2 and torch.equal(mixed[0][0], mixed[0][1])
+            assert store.read_neurons(0, 0, [absent, absent + 1]) is None
+            again = store.read_neurons(1, 0, layers[1][0][:4])
+            assert (1, 0) in store._offset_cache
+            for a, b in zip(again, store.read_neurons(1, 0, layers[1][0][:4])):
+                assert torch.equal(a, b)
+        finally:
+            store.close()
+
+
+# ── the fused FFN ────────────────────────────────────────────────────────────
+
+@pytest.fixture(scope="module")
+def layer_swiglu(dev):
+    """Single SwiGLU layer 4096 x 14336, 20 % hot (2867) fp8 with per-row
+    scales, the rest INT4 records."""
+    g = torch.Generator(device=dev).manual_seed(11)
+    lay = SyntheticLayer(g, 14336, 2867, device=dev)
+    return lay, g
+
+
+def test_ffn_swiglu_full_geometry(dev, layer_swiglu):
+    lay, g = layer_swiglu
+    n_cold = lay.records.shape[0]
+    slots = torch.randperm(n_cold, generator=g, device=dev)[: n_cold // 10].int()
+    cold = ColdNeurons.from_slots(_section(lay), slots)
+    x = torch.randn((1, H), generator=g, device=dev).half()
+    out, y32 = _ffn(x, lay.norm_w, EPS, lay.hot, cold, "silu", False, add_residual=True,
+                    want_y32=True)
+    torch.cuda.synchronize()
+    xn = normed_f16(x, lay.norm_w)
+    Gh, Uh, Dh = hot_dense(lay.hot)
+    Gc, Uc, Dc = cold_dense(lay.records, slots)
+    ref = O.sparse_ffn(xn, "silu", False, Gh, Uh, Dh, Gc, Uc, Dc)
+    assert_ffn_close(y32.cpu().numpy(), ref, what="y32")
+    assert_ffn_close(out.float().cpu().numpy(), x.float().cpu().numpy() + ref, tol=2e-3,
+                     cos_min=0.99999, what="residual out")
+    # each half on its own
+    _, yh = _ffn(x, lay.norm_w, EPS, lay.hot, None, "silu", False, False, want_y32=True)
+    _, yc = _ffn(x, lay.norm_w, EPS, None, cold, "silu", False, False, want_y32=True)
+    assert_ffn_close(yh.cpu().numpy(), O.sparse_ffn(xn, "silu", False, Gh, Uh, Dh, None, None, None),
+                     what="hot half")
+    assert_ffn_close(yc.cpu().numpy(), O.sparse_ffn(xn, "silu", False, None, None, None, Gc, Uc, Dc),
+                     what="cold half")
+
+
+def test_ffn_drelu_true_firing_set_equals_dense(dev):
+    """dReLU with a -1.3 sigma gate shift: hot + the truly firing cold
+    neurons equals the FFN over every neuron (non-firing terms are zero)."""
+    g = torch.Generator(device=dev).manual_seed(21)
+    inter = 14336
+    sigma = 0.02 * math.sqrt(H)
+    lay = SyntheticLayer(g, inter, 3584, device=dev, gate_bias_shift=-1.3 * sigma)
+    x = torch.randn((1, H), generator=g, device=dev).half()
+    xn = normed_f16(x, lay.norm_w)
+    Gc_all, Uc_all, Dc_all = cold_dense(lay.records, np.arange(lay.records.shape[0]))
+    bc = lay.cold_gate_bias.cpu().numpy().astype(np.float64)
+    gc = xn @ Gc_all.T + bc
+    uc = xn @ Uc_all.T
+    firing = np.nonzero((np.maximum(gc, 0) * np.maximum(uc, 0)).ravel() != 0)[0]
+    assert 0.01 * inter < firing.size < 0.15 * inter
+    cold = ColdNeurons.from_slots(_section(lay), firing, gate_bias=lay.cold_gate_bias)
+    _, y32 = _ffn(x, lay.norm_w, EPS, lay.hot, cold, "relu", True, False, want_y32=True)
+    Gh, Uh, Dh = hot_dense(lay.hot)
+    bh = lay.hot.gate_bias.cpu().numpy().astype(np.float64)
+    dense = O.sparse_ffn(xn, "relu", True, Gh, Uh, Dh, Gc_all, Uc_all, Dc_all, bh, bc)
+    assert_ffn_close(y32.cpu().numpy(), dense, what="dReLU vs dense")
+
+
+def test_ffn_edge_cases(dev):
+    g = torch.Generator(device=dev).manual_seed(5)
+    lay = SyntheticLayer(g, 1000, 13, device=dev)
+    sec = _section(lay)
+    x = torch.randn((1, H), generator=g, device=dev).half()
+    xn = normed_f16(x, lay.norm_w)
+    Gh, Uh, Dh = hot_dense(lay.hot)
+    # both halves empty -> zeros (engine.py:207-208)
+    _, y = _ffn(x, lay.norm_w, EPS, None, None, "silu", False, False, want_y32=True)
+    assert torch.count_nonzero(y) == 0
+    # duplicates count twice, invalid slots are skipped
+    slots = [5, 5, 900, -1, 10 ** 6, 17]
+    cold = ColdNeurons.from_slots(sec, slots)
+    _, y = _ffn(x, lay.norm_w, EPS, lay.hot, cold, "silu", False, False, want_y32=True)
+    Gc, Uc, Dc = cold_dense(lay.records, [5, 5, 900, 17])
+    assert_ffn_close(y.cpu().numpy(), O.sparse_ffn(xn, "silu", False, Gh, Uh, Dh, Gc, Uc, Dc))
+    # chunked active list with uneven counts, including an empty chunk
+    sl = torch.full((3 * 8,), -7, dtype=torch.int32, device=dev)
+    sl[0:3] = torch.tensor([1, 2, 3])
+    sl[16:21] = torch.tensor([40, 41, 42, 43, 44])
+    counts = torch.tensor([3, 0, 5], dtype=torch.int32, device=dev)
+    chunked = ColdNeurons(sec, sl, counts, 3, 8)
+    _, y = _ffn(x, lay.norm_w, EPS, None, chunked, "silu", False, False, want_y32=True)
+    Gc, Uc, Dc = cold_dense(lay.records, [1, 2, 3, 40, 41, 42, 43, 44])
+    assert_ffn_close(y.cpu().numpy(), O.sparse_ffn(xn, "silu", False, None, None, None, Gc, Uc, Dc))
+    # batch of 3 rows shares the active set
+    xb = torch.randn((3, H), generator=g, device=dev).half()
+    cold = ColdNeurons.from_slots(sec, [0, 9, 33])
+    _, yb = _ffn(xb, lay.norm_w, EPS, lay.hot, cold, "silu", False, False, want_y32=True)
+    Gc, Uc, Dc = cold_dense(lay.records, [0, 9, 33])
+    ref = O.sparse_ffn(normed_f16(xb, lay.norm_w), "silu", False, Gh, Uh, Dh, Gc, Uc, Dc)
+    assert_ffn_close(yb.cpu().numpy(), ref, what="batch 3")
+
+
+def test_rmsnorm_within_one_fp16_ulp(dev):
+    g = torch.Generator(device=dev).manual_seed(3)
+    x = (torch.randn((5, H), generator=g, device=dev) * torch.tensor([1e-2, 1, 30, 300, 3e3],
+                                                                     device=dev)[:, None]).half()
+    w = (1 + 0.3 * torch.randn(H, generator=g, device=dev)).half()
+    got = rmsnorm(x, w, EPS).cpu().numpy()
+    ref = O.rmsnorm(x.float().cpu().numpy(), w.float().cpu().numpy(), EPS)
+    ulp = np.abs(np.spacing(ref.astype(np.float16))).astype(np.float64)
+    assert (np.abs(got.astype(np.float64) - ref) <= ulp).all()
+    assert (got == ref.astype(np.float16)).mean() > 0.99
+
+
+# ── predictor ────────────────────────────────────────────────────────────────
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_predictor_logits_mask_and_selection(dev, dtype):
+    g = torch.Generator(device=dev).manual_seed(31)
+    inter = 14336
+    pred = random_predictor(g, inter, 64, dtype, dev)
+    D, U, b = pred_weights(pred)
+    x = torch.randn((2, H), generator=g, device=dev).half()
+    logits = pred.logits(x)
+    probs = pred(x)
+    mask = pred.predict_mask(x, 0.5)
+    torch.cuda.synchronize()
+    for r in range(2):
+        q = x[r].float().cpu().numpy().astype(np.float64)
+        if dtype == torch.bfloat16:
+            q = O.to_bf16(q.astype(np.float32)).astype(np.float64)
+        ref = O.predictor_logits(q, D, U, b)
+        got = logits[r].double().cpu().numpy()
+        assert np.abs(got - ref).max() < 1e-5
+        amb = O.ambiguous(ref, 0.5)
+        assert np.array_equal(mask[r].cpu().numpy()[~amb], (ref >= 0.0)[~amb])
+        assert np.allclose(probs[r].double().cpu().numpy(), 1 / (1 + np.exp(-ref)), atol=1e-6)
+    # on-device selection: RMSNorm -> query -> threshold -> LUT filter -> ascending
+    norm_w = (1 + 0.05 * torch.randn(H, generator=g, device=dev)).half()
+    hot_ids = torch.randperm(inter, generator=g, device=dev)[:3584]
+    lut = torch.arange(inter, dtype=torch.int32, device=dev) * 3
+    lut[hot_ids] = -1
+    thr_p = 0.52
+    for rows in (1, 3):
+        xq = torch.randn((rows, H), generator=g, device=dev).half()
+        nc = (inter + 255) // 256
+        slots = torch.empty(nc * 256, dtype=torch.int32, device=dev)
+        ids = torch.empty_like(slots)
+        counts = torch.empty(nc, dtype=torch.int32, device=dev)
+        dslots = torch.empty(inter, dtype=torch.int32, device=dev)
+        dids = torch.empty_like(dslots)
+        total = torch.empty(1, dtype=torch.int32, device=dev)
+        p = pred.struct()
+        import ctypes
+        L = _lib.lib()
+        wsb = L.oi2_predict_workspace_bytes(ctypes.byref(p))
+        ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+        _lib.check(L.oi2_predict_select(xq.data_ptr(), rows, norm_w.data_ptr(), ctypes.c_float(EPS),
+                                        ctypes.byref(p), _lib.logit_threshold(thr_p), lut.data_ptr(),
+                                        slots.data_ptr(), ids.data_ptr(), counts.data_ptr(),
+                                        dslots.data_ptr(), dids.data_ptr(), total.data_ptr(),
+                                        ws.data_ptr(), wsb, None))
+        torch.cuda.synchronize()
+        xn = rmsnorm(xq, norm_w, EPS).double().cpu().numpy()   # the kernels' own normalisation
+        q = query_for(xn, dtype)
+        ref = O.predictor_logits(q, D, U, b)
+        amb = O.ambiguous(ref, thr_p)
+        want = O.cold_ids_for(ref >= O.logit_threshold(thr_p), hot_ids.cpu().tolist(), inter)
+        got = chunked_ids(counts, ids)
+        assert got == sorted(got)
+        gs, ws_ = set(got), set(want)
+        diff = gs ^ ws_
+        assert all(amb[i] for i in diff), f"{len(diff)} ids differ outside the 1e-6 band"
+        n = int(total.item())
+        assert n == len(got)
+        assert dids[:n].cpu().tolist() == got
+        assert dslots[:n].cpu().tolist() == [3 * i for i in got]
+
+
+# ── drop-in layer from split files ───────────────────────────────────────────
+
+def test_sparse_ffn_layer_from_split_files(dev):
+    """SparseFFNLayer built exactly as DesdemonaEngine builds it
+    (engine.py:391-398) from a hot .pt in the reference layout (fp8, no
+    scales), a cold file and an fp32 predictor file."""
+    g = torch.Generator(device=dev).manual_seed(41)
+    inter = 14336
+    lay = SyntheticLayer(g, inter, 3584, device=dev, keep_dense=True, per_row_scale=False,
+                         std=0.05)
+    gate, up, down = lay.dense
+    with tempfile.TemporaryDirectory() as tmp:
+        hot_dir = os.path.join(tmp, "hot_weights")
+        os.makedirs(hot_dir)
+        hid = lay.hot_ids
+        torch.save({"neuron_ids": hid.cpu(), "gate": gate[hid].cpu().to(torch.float8_e4m3fn),
+                    "up": up[hid].cpu().to(torch.float8_e4m3fn),
+                    "down": down[:, hid].cpu().to(torch.float8_e4m3fn)},
+                   os.path.join(hot_dir, "layer_002_expert_000.pt"))
+        w = oi2.format.ColdFileWriter(os.path.join(tmp, "cold_weights.bin"), 3)
+        empty = np.zeros((0, 6400), np.uint8)
+        w.add_section(0, empty)
+        w.add_section(1, empty)
+        w.add_section(2, lay.records.cpu().numpy())
+        w.close(os.path.join(tmp, "cold_index.npy"))
+        pdir = os.path.join(tmp, "pred")
+        os.makedirs(pdir)
+        pred = random_predictor(g, inter, 64, torch.float32, dev)
+        pred.save(os.path.join(pdir, "layer_002_expert_000.pt"))
+        cfg = {"hidden_dim": H, "intermediate_dim": inter, "hidden_act": "silu",
+               "act_on_both": False, "rms_norm_eps": EPS, "num_experts": 1}
+        store = oi2.ColdWeightStore(os.path.join(tmp, "cold_weights.bin"),
+                                    os.path.join(tmp, "cold_index.npy"), cfg, device=dev)
+        reg = oi2.PredictorRegistry(pdir, device=dev)
+        layer = oi2.SparseFFNLayer(2, hot_dir, store, reg, cfg, dev, None,
+                                   ffn_norm_weight=lay.norm_w.cpu())
+        x = torch.randn((1, 1, H), generator=g, device=dev).half()
+        y_direct = layer(x)
+        fut = layer.submit_cold_fetch(x)
+        y_pref = layer(x, fut)
+        torch.cuda.synchronize()
+        assert torch.equal(y_direct, y_pref)
+        xn_gpu = rmsnorm(x, lay.norm_w, EPS)
+        ids = layer._cold_ids_for(xn_gpu)
+        xn = normed_f16(x[0], lay.norm_w)
+        D, U, b = pred_weights(pred)
+        ref_logits = O.predictor_logits(xn_gpu[0, 0].double().cpu().numpy(), D, U, b)
+        want = O.cold_ids_for(ref_logits >= 0.0, hid.cpu().tolist(), inter)
+        diff = set(ids) ^ set(want)
+        assert all(O.ambiguous(ref_logits)[i] for i in diff)
+        sec = store.section(2)
+        slots = sec.slots_for(ids)
+        Gh = O.FP8_TABLE[gate[hid].cpu().to(torch.float8_e4m3fn).view(torch.uint8).numpy()]
+        Uh = O.FP8_TABLE[up[hid].cpu().to(torch.float8_e4m3fn).view(torch.uint8).numpy()]
+        Dh = O.FP8_TABLE[down[:, hid].cpu().to(torch.float8_e4m3fn).view(torch.uint8).numpy()]
+        Gc, Uc, Dc = cold_dense(lay.records, slots)
+        ref = O.sparse_ffn(xn, "silu", False, Gh, Uh, Dh, Gc, Uc, Dc)
+        res = y_direct[0].float().cpu().numpy() - x[0].float().cpu().numpy()
+        assert_ffn_close(res, ref, tol=1e-2, cos_min=0.9999, what="layer forward")
+        # a layer with no predictor fetches every cold neuron (engine.py:282-283)
+        layer_np = oi2.SparseFFNLayer(2, hot_dir, store, None, cfg, dev, None,
+                                      ffn_norm_weight=lay.norm_w.cpu())
+        y_all = layer_np(x)
+        Gc, Uc, Dc = cold_dense(lay.records, np.arange(lay.records.shape[0]))
+        ref_all = O.sparse_ffn(xn, "silu", False, Gh, Uh, Dh, Gc, Uc, Dc)
+        assert_ffn_close(y_all[0].float().cpu().numpy() - x[0].float().cpu().numpy(), ref_all,
+                         what="no predictor")
+        # layers with an empty cold section compute the hot half only
+        store.close()

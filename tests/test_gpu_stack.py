@@ -1,0 +1,100 @@
+"""The on-device decode stack (engine.py:421-438's FFN loop) against the
+oracle, layer by layer on the GPU's own hidden states (teacher forcing), plus
+determinism of hipGraph replay."""
+import numpy as np
+import pytest
+import torch
+
+import oi2
+from oi2.layer import rmsnorm
+from oi2.stack import DecodeStack, StackLayer
+from oi2.synth import SyntheticLayer, calibrate_threshold
+from oracle import oracle as O
+from tests.gpu_helpers import (EPS, assert_ffn_close, cold_dense, hot_dense, normed_f16,
+                               pred_weights, query_for)
+
+pytestmark = pytest.mark.gpu
+H = 4096
+
+
+@pytest.fixture(scope="module")
+def stack4():
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(77)
+    inter = 14336
+    layers = [SyntheticLayer(g, inter, 3584, device=dev, with_predictor=True) for _ in range(4)]
+    # layer 2 has no predictor: it fetches every cold neuron
+    layers[2].predictor = None
+    thr = calibrate_threshold(layers, g, 0.05)
+    st = DecodeStack([StackLayer(l.hot, l.records, l.lut, l.norm_w, l.predictor) for l in layers],
+                     inter, EPS, "silu", False, thr)
+    return dev, g, layers, st, thr
+
+
+def _active_ids(counts, ids, L):
+    out = []
+    for c, n in enumerate(counts[L].cpu().tolist()):
+        out.extend(ids[L, c * 256: c * 256 + n].cpu().tolist())
+    return out
+
+
+def test_stack_layers_match_oracle(stack4):
+    dev, g, layers, st, thr = stack4
+    stream = torch.cuda.Stream(device=dev)
+    x_in = torch.randn(H, generator=g, device=dev).half()
+    x_out = torch.empty_like(x_in)
+    with torch.cuda.stream(stream):
+        st.decode(x_in, x_out, stream)
+    stream.synchronize()
+    xs, counts, slots, ids = st.trace()
+    torch.cuda.synchronize()
+    assert torch.equal(xs[-1], x_out)
+    inputs = [x_in] + [xs[i] for i in range(3)]
+    for L, lay in enumerate(layers):
+        x_l = inputs[L]
+        # active set of layer L: predicted from layer L-1's input (lookahead)
+        if lay.predictor is not None:
+            src = inputs[L - 1] if L > 0 else x_in
+            q_rows = rmsnorm(src[None], lay.norm_w, EPS).double().cpu().numpy()
+            q = query_for(q_rows, lay.predictor.dtype)
+            D, U, b = pred_weights(lay.predictor)
+            logits = O.predictor_logits(q, D, U, b)
+            want = O.cold_ids_for(logits >= thr, lay.hot_ids.cpu().tolist(), lay.inter)
+            got = _active_ids(counts, ids, L)
+            assert got == sorted(got)
+            amb = np.abs(logits - thr) <= 1e-6
+            assert all(amb[i] for i in set(got) ^ set(want)), f"layer {L}: index sets differ"
+            assert 0.02 * lay.inter < len(got) < 0.08 * lay.inter
+            active_slots = [int(lay.lut[i]) for i in got]
+        else:
+            active_slots = np.argsort(lay.cold_ids.cpu().numpy(), kind="stable")
+        xn = normed_f16(x_l[None], lay.norm_w)
+        Gh, Uh, Dh = hot_dense(lay.hot)
+        Gc, Uc, Dc = cold_dense(lay.records, active_slots)
+        ref = O.sparse_ffn(xn, "silu", False, Gh, Uh, Dh, Gc, Uc, Dc)[0]
+        y = xs[L].double().cpu().numpy() - x_l.double().cpu().numpy()
+        assert_ffn_close(y, ref, tol=1e-2, cos_min=0.9999, what=f"layer {L}")
+
+
+def test_graph_replay_is_deterministic(stack4):
+    dev, g, layers, st, thr = stack4
+    stream = torch.cuda.Stream(device=dev)
+    x_in = torch.randn(H, generator=g, device=dev).half()
+    outs = []
+    x_out = torch.empty_like(x_in)       # fixed pointers: one captured graph, replayed
+    for k in range(4):
+        with torch.cuda.stream(stream):
+            st.decode(x_in, x_out, stream)
+            _ = (x_out.float() * 2).sum()          # eager work between replays
+        stream.synchronize()
+        outs.append(x_out.clone())
+    direct = DecodeStack(st.layers, st.inter, EPS, "silu", False, thr, use_graph=False)
+    x_d = torch.empty_like(x_in)
+    direct.decode(x_in, x_d, None)
+    torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+    assert torch.equal(outs[0], x_d)
+    up, down = direct.profile(x_in, x_d)
+    assert len(up) == 4 and all(t > 0 for t in up + down)
+    direct.close()
