@@ -49,6 +49,8 @@ def build_stack(seed, dev):
     thr = calibrate_threshold(layers, g, ACTIVE_FRAC)
     st = DecodeStack([StackLayer(l.hot, l.records, l.lut, l.norm_w, l.predictor) for l in layers],
                      INTER, EPS, "silu", False, thr)
+    # size the cold pass for the calibrated active fraction with headroom
+    st.set_expected_active(int(1.3 * ACTIVE_FRAC * (INTER - N_HOT)))
     return layers, st, thr, g
 
 

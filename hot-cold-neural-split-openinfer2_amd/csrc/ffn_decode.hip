@@ -4,21 +4,22 @@
 //
 // Launch shapes: 256 threads (4 wave64s) per workgroup everywhere.
 //
-// ffn_up   : workgroup roles by blockIdx range, cold first so the gather
-//            workgroups are dispatched ahead of the bulk hot stream:
-//   cold   - one wave per active record (round robin): 16-byte loads of the
-//            gate/up/down nibbles + scales, gate/up dots against the
-//            normalised token, activation, then the record's down column
-//            scaled by h into 64 per-lane accumulators; the workgroup sums its
-//            4 waves in LDS and writes one fp32 partial y (16 KB).
+// ffn_up   : workgroup roles by blockIdx range
+//   cold   - one wave per active record: 16-byte loads of its gate/up nibbles
+//            and scales, dots against the normalised token, activation; the
+//            (slot, h) pair goes to a dense list for ffn_down.
 //   pred   - one wave per predictor down row (the lookahead layer's z).
-//   hot    - two neurons per wave: fp8 gate/up rows -> fp16 pairs ->
-//            v_dot2 against the fp16 normalised token, activation, h_hot.
+//   hot    - two neurons per wave: fp8 gate/up rows -> fp16 pairs -> v_dot2.
 // ffn_down : roles
 //   pred   - 256 neurons per workgroup: logits = U z + b, threshold, LUT
 //            filter, ballot/prefix compaction into an ascending chunk.
-//   down   - 16 output rows per workgroup: fp8 down rows x h_hot, plus the
-//            sum of the cold partials, plus the residual.
+//   down   - 16 output rows per workgroup: fp8 down rows x h_hot (h staged in
+//            LDS), plus every active cold record's 16 down nibbles x h, plus
+//            the residual; it also emits x * w_next and the sum-of-squares
+//            partial the next layer's RMSNorm needs.
+//
+// Every workgroup issues its HBM loads before its first barrier (a barrier's
+// release fence waits for all outstanding global loads on gfx950).
 #include "capi_util.h"
 #include "ffn_kernels.h"
 
@@ -37,52 +38,48 @@ __device__ __forceinline__ float round_bf16(float f) {
 
 __device__ __forceinline__ float round_f16(float f) { return (float)(_Float16)f; }
 
-// rsqrt(mean(x^2) + eps) over the H fp16 values of x; every thread of the
-// block must call it.
-__device__ float block_rnorm(const uint16_t* x, float eps, float* s_red) {
-  const int t = threadIdx.x;
-  const u32x4* p = reinterpret_cast<const u32x4*>(x + 16 * t);
-  u32x4 a = p[0], b = p[1];
+// The one RMSNorm factor every kernel uses, so all of them agree bit for bit:
+// partial t = sequential fma of x[16t .. 16t+16)^2; total = DPP tree over
+// lanes of (p[4l] + p[4l+1]) + (p[4l+2] + p[4l+3]); r = rsqrt(total/H + eps).
+__device__ __forceinline__ float ssq16(const float v[16]) {
   float s = 0.0f;
 #pragma unroll
-  for (int d = 0; d < 4; ++d) {
-    float v0 = half_lo(a[d]), v1 = half_hi(a[d]), v2 = half_lo(b[d]), v3 = half_hi(b[d]);
-    s += v0 * v0 + v1 * v1 + v2 * v2 + v3 * v3;
-  }
-  s = wave_sum(s);
-  if (lane_id() == 0) s_red[t >> 6] = s;
-  __syncthreads();
-  float tot = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
-  __syncthreads();
-  return rsqrtf(tot * (1.0f / kH) + eps);
+  for (int e = 0; e < 16; ++e) s = fmaf(v[e], v[e], s);
+  return s;
 }
 
-// 16 normalised elements x_n[e0 .. e0+16) as floats holding fp16 values:
-// fp16(x * r * w), or x itself when w is null.
-__device__ __forceinline__ void load_xn16(const uint16_t* x, const uint16_t* w, float r, int e0,
-                                          float v[16]) {
+__device__ __forceinline__ float r_from_parts(const float* parts, float eps) {
+  const f32x4 p = reinterpret_cast<const f32x4*>(parts)[lane_id()];
+  const float s = wave_sum((p.x + p.y) + (p.z + p.w));
+  return rsqrtf(s * (1.0f / kH) + eps);
+}
+
+__device__ __forceinline__ void load_h16(const uint16_t* x, int e0, float v[16]) {
   const u32x4* px = reinterpret_cast<const u32x4*>(x + e0);
-  u32x4 xa = px[0], xb = px[1];
-  if (w) {
-    const u32x4* pw = reinterpret_cast<const u32x4*>(w + e0);
-    u32x4 wa = pw[0], wb = pw[1];
+  const u32x4 a = px[0], b = px[1];
 #pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      v[2 * d] = round_f16(half_lo(xa[d]) * r * half_lo(wa[d]));
-      v[2 * d + 1] = round_f16(half_hi(xa[d]) * r * half_hi(wa[d]));
-      v[8 + 2 * d] = round_f16(half_lo(xb[d]) * r * half_lo(wb[d]));
-      v[8 + 2 * d + 1] = round_f16(half_hi(xb[d]) * r * half_hi(wb[d]));
-    }
-  } else {
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      v[2 * d] = half_lo(xa[d]);
-      v[2 * d + 1] = half_hi(xa[d]);
-      v[8 + 2 * d] = half_lo(xb[d]);
-      v[8 + 2 * d + 1] = half_hi(xb[d]);
-    }
+  for (int d = 0; d < 4; ++d) {
+    v[2 * d] = half_lo(a[d]);
+    v[2 * d + 1] = half_hi(a[d]);
+    v[8 + 2 * d] = half_lo(b[d]);
+    v[8 + 2 * d + 1] = half_hi(b[d]);
   }
 }
+
+// Block-wide canonical r for one H-row of x (every thread must call it).
+__device__ float block_rnorm(const uint16_t* x, float eps, float* s_parts) {
+  float v[16];
+  load_h16(x, 16 * threadIdx.x, v);
+  s_parts[threadIdx.x] = ssq16(v);
+  __syncthreads();
+  const float r = r_from_parts(s_parts, eps);
+  __syncthreads();
+  return r;
+}
+
+// x_n = fp16((x * r) * w): the normalised hidden state as nn.RMSNorm's fp16
+// output (engine.py:247-249); the predictor query and oi2_rmsnorm use it.
+__device__ __forceinline__ float xn_exact(float x, float r, float w) { return round_f16(x * r * w); }
 
 // Exclusive prefix of the (clamped) chunk counts into s_prefix[0..n_chunks].
 __device__ void chunk_prefix(const ActiveList& al, int* s_prefix) {
@@ -95,7 +92,6 @@ __device__ void chunk_prefix(const ActiveList& al, int* s_prefix) {
   s_prefix[t + 1] = c;
   if (t == 0) s_prefix[0] = 0;
   __syncthreads();
-  // Hillis-Steele inclusive scan over s_prefix[1..256]
   for (int off = 1; off < kThreads; off <<= 1) {
     int v = (t >= off) ? s_prefix[t + 1 - off] : 0;
     __syncthreads();
@@ -104,120 +100,215 @@ __device__ void chunk_prefix(const ActiveList& al, int* s_prefix) {
   }
 }
 
+// Exclusive prefix of the clamped chunk counts, per wave: lane k holds the
+// prefix of chunks k, k+64, k+128, k+192.  Returns the total.
+__device__ __forceinline__ int wave_chunk_prefix(const ActiveList& al, int excl[4]) {
+  const int lane = lane_id();
+  int total = 0;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    excl[m] = total;
+    if (64 * m < al.n_chunks) {
+      const int k = lane + 64 * m;
+      int c = 0;
+      if (k < al.n_chunks) {
+        c = al.counts[k];
+        c = c < 0 ? 0 : (c > al.chunk ? al.chunk : c);
+      }
+      int v = c;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const int t = __shfl_up(v, off, kWave);
+        if (lane >= off) v += t;
+      }
+      excl[m] = total + v - c;
+      total += __shfl(v, 63, kWave);
+    }
+  }
+  return total;
+}
+
+// Record slot of active item i (0 <= i < total), wave-uniform.
+__device__ __forceinline__ int item_slot(const ActiveList& al, const int excl[4], int i) {
+  const int lane = lane_id();
+  int c = -1;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const bool in = (lane + 64 * m) < al.n_chunks && excl[m] <= i;
+    c += __popcll(__ballot(in));
+  }
+  const int sel = c >> 6;
+  const int e = sel == 0 ? excl[0] : sel == 1 ? excl[1] : sel == 2 ? excl[2] : excl[3];
+  const int base = __shfl(e, c & 63, kWave);
+  return al.slots[(size_t)c * al.chunk + (i - base)];
+}
+
+// Stage xw into LDS in natural order (hot rows) and/or, per 8 elements, as
+// the pairs (e0,e4) (e1,e5) (e2,e6) (e3,e7) the INT4 unpack produces (cold).
+// Contains a barrier: call after issuing the role's HBM loads.
+__device__ __forceinline__ void stage_xw(const uint16_t* xw, uint32_t* s_nat, uint32_t* s_pair) {
+  const int t = threadIdx.x;
+  const u32x4* px = reinterpret_cast<const u32x4*>(xw + 16 * t);
+  const u32x4 a = px[0], b = px[1];
+  if (s_nat) {
+    reinterpret_cast<u32x4*>(s_nat)[2 * t] = a;
+    reinterpret_cast<u32x4*>(s_nat)[2 * t + 1] = b;
+  }
+  if (s_pair) {
+    u32x4 pa, pb;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      // element k is half (k & 1) of dword k >> 1; element k + 4 the same half
+      // of dword 2 + (k >> 1); v_perm picks the two halves into one dword
+      const uint32_t sel = (k & 1) ? 0x07060302u : 0x05040100u;
+      pa[k] = __builtin_amdgcn_perm(a[2 + (k >> 1)], a[k >> 1], sel);
+      pb[k] = __builtin_amdgcn_perm(b[2 + (k >> 1)], b[k >> 1], sel);
+    }
+    reinterpret_cast<u32x4*>(s_pair)[2 * t] = pa;
+    reinterpret_cast<u32x4*>(s_pair)[2 * t + 1] = pb;
+  }
+  __syncthreads();
+}
+
+__device__ __forceinline__ float token_r(const TokenIn& tk) {
+  return tk.use_norm ? r_from_parts(tk.ssq, tk.eps) : 1.0f;
+}
+
 // ── ffn_up roles ────────────────────────────────────────────────────────────
 
-__device__ void cold_role(const UpArgs& a, int wg, float r, float* s_lds, int* s_prefix) {
+__device__ void cold_role(const UpArgs& a, int wg, uint32_t* s_nat, uint32_t* s_pair,
+                          float* s_red) {
   const int w = threadIdx.x >> 6, lane = lane_id();
-  chunk_prefix(a.act, s_prefix);
-  const int n_chunks = a.act.n_chunks;
-  const int total = s_prefix[n_chunks];
-  // workgroups actually used: about kRecordsPerColdWG records each, so the
-  // number of 16 KB partial rows follows the active count, not the capacity
-  int n_eff = (total + kRecordsPerColdWG - 1) / kRecordsPerColdWG;
-  n_eff = n_eff < 1 ? 1 : (n_eff > a.wg_cold ? a.wg_cold : n_eff);
-  if (wg == 0 && threadIdx.x == 0 && a.n_part_out) *a.n_part_out = n_eff;
-  if (wg >= n_eff) return;
+  const int n_waves = a.wg_cold * 4;
+  const int gw = wg * 4 + w;
+  int excl[4];
+  int total = wave_chunk_prefix(a.act, excl);
+  total = total < a.cold_cap ? total : a.cold_cap;
+  if (wg == 0 && threadIdx.x == 0) *a.cold_total = total;
+  // workgroups with at least one item write a partial row; the rest leave
+  if (wg * 4 >= total) return;
 
-  // token values for elements [32 lane + 2048 it, +32), in nibble-pair order
-  f16x2 xc[2][16];
+  // first item: issue its loads before the barrier
+  int i = gw;
+  int slot = (i < total) ? item_slot(a.act, excl, i) : -1;
+  bool valid = i < total && slot >= 0 && slot < a.n_records;
+  u32x4 q[6];
+  float s[6];
+  const int g0 = lane >> 2;
+  auto load_rec = [&](int sl) {
+    const uint8_t* rec = a.records + (size_t)sl * kRecBytes;
 #pragma unroll
-  for (int it = 0; it < 2; ++it) {
-    float v[32];
-    const int e0 = 32 * lane + 2048 * it;
-    load_xn16(a.x, a.norm_w, r, e0, v);
-    load_xn16(a.x, a.norm_w, r, e0 + 16, v + 16);
+    for (int it = 0; it < 6; ++it) q[it] = load16_a2(rec + kOffGate + 16 * (lane + 64 * it));
+    const uint16_t* sc = reinterpret_cast<const uint16_t*>(rec + kOffScales);
 #pragma unroll
-    for (int d = 0; d < 4; ++d)
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        xc[it][4 * d + k].x = (_Float16)v[8 * d + k];
-        xc[it][4 * d + k].y = (_Float16)v[8 * d + k + 4];
-      }
-  }
-
+    for (int v = 0; v < 3; ++v) {
+      s[2 * v] = half_bits_to_float(sc[32 * v + g0]);
+      s[2 * v + 1] = half_bits_to_float(sc[32 * v + 16 + g0]);
+    }
+  };
+  if (valid) load_rec(slot);
+  stage_xw(a.tok.xw, s_nat, s_pair);
   float acc[64];
 #pragma unroll
-  for (int i = 0; i < 64; ++i) acc[i] = 0.0f;
-
-  const int n_waves = n_eff * 4;
-  for (int i = wg * 4 + w; i < total; i += n_waves) {
-    int lo = 0, hi = n_chunks;
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (s_prefix[mid] <= i) lo = mid; else hi = mid;
-    }
-    const int slot = a.act.slots[(size_t)lo * a.act.chunk + (i - s_prefix[lo])];
-    if (slot < 0 || slot >= a.n_records) continue;
-    const uint8_t* rec = a.records + (size_t)slot * kRecBytes;
-    u32x4 q[6];
+  for (int k = 0; k < 64; ++k) acc[k] = 0.0f;
+  if (i < total) {
+    const float r = token_r(a.tok);
+    // token pairs for elements [32 lane + 2048 it, +32), it = 0, 1
+    f16x2 xc[2][16];
 #pragma unroll
     for (int it = 0; it < 2; ++it) {
-      q[it] = load16_a2(rec + kOffGate + 16 * (lane + 64 * it));
-      q[2 + it] = load16_a2(rec + kOffUp + 16 * (lane + 64 * it));
-      q[4 + it] = load16_a2(rec + kOffDown + 16 * (lane + 64 * it));
+      const u32x4* p = reinterpret_cast<const u32x4*>(s_pair) + (32 * lane + 2048 * it) / 8;
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const u32x4 v = p[m];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) xc[it][4 * m + k] = as_f16x2(v[k]);
+      }
     }
-    const uint16_t* sc = reinterpret_cast<const uint16_t*>(rec + kOffScales);
-    const int g0 = lane >> 2;
-    const float sg0 = half_bits_to_float(sc[g0]), sg1 = half_bits_to_float(sc[16 + g0]);
-    const float su0 = half_bits_to_float(sc[32 + g0]), su1 = half_bits_to_float(sc[48 + g0]);
-    const float sd0 = half_bits_to_float(sc[64 + g0]), sd1 = half_bits_to_float(sc[80 + g0]);
-
-    float pg[2] = {0.0f, 0.0f}, pu[2] = {0.0f, 0.0f};
+    for (;;) {
+      if (valid) {
+        float pg[2] = {0.0f, 0.0f}, pu[2] = {0.0f, 0.0f};
 #pragma unroll
-    for (int it = 0; it < 2; ++it)
+        for (int it = 0; it < 2; ++it)
 #pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        f16x2 p[4];
-        int4x8_to_f16x2x4(q[it][d], p);
+          for (int d = 0; d < 4; ++d) {
+            f16x2 t[4];
+            int4x8_to_f16x2x4(q[it][d], t);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) pg[it] = dot2(p[k], xc[it][4 * d + k], pg[it]);
-        int4x8_to_f16x2x4(q[2 + it][d], p);
+            for (int k = 0; k < 4; ++k) pg[it] = dot2(t[k], xc[it][4 * d + k], pg[it]);
+            int4x8_to_f16x2x4(q[2 + it][d], t);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) pu[it] = dot2(p[k], xc[it][4 * d + k], pu[it]);
+            for (int k = 0; k < 4; ++k) pu[it] = dot2(t[k], xc[it][4 * d + k], pu[it]);
+          }
+        float g = r * wave_sum(pg[0] * s[0] + pg[1] * s[1]);
+        const float u = r * wave_sum(pu[0] * s[2] + pu[1] * s[3]);
+        if (a.cold_gbias) g += a.cold_gbias[slot];
+        const float h = gated_act(g, u, a.relu, a.both);
+        const float hs[2] = {h * s[4], h * s[5]};
+        // the record's down column, elements [32 lane + 2048 it, +32)
+#pragma unroll
+        for (int it = 0; it < 2; ++it)
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            f16x2 t[4];
+            int4x8_to_f16x2x4(q[4 + it][d], t);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              acc[32 * it + 8 * d + k] = fmaf(hs[it], (float)t[k].x, acc[32 * it + 8 * d + k]);
+              acc[32 * it + 8 * d + k + 4] = fmaf(hs[it], (float)t[k].y, acc[32 * it + 8 * d + k + 4]);
+            }
+          }
       }
-    float g = wave_sum(pg[0] * sg0 + pg[1] * sg1);
-    const float u = wave_sum(pu[0] * su0 + pu[1] * su1);
-    if (a.cold_gbias) g += a.cold_gbias[slot];
-    const float h = gated_act(g, u, a.relu, a.both);
-    const float hs[2] = {h * sd0, h * sd1};
-#pragma unroll
-    for (int it = 0; it < 2; ++it)
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        f16x2 p[4];
-        int4x8_to_f16x2x4(q[4 + it][d], p);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          acc[32 * it + 8 * d + k] += hs[it] * (float)p[k].x;
-          acc[32 * it + 8 * d + k + 4] += hs[it] * (float)p[k].y;
-        }
-      }
+      i += n_waves;
+      if (i >= total) break;
+      slot = item_slot(a.act, excl, i);
+      valid = slot >= 0 && slot < a.n_records;
+      if (valid) load_rec(slot);
+    }
   }
-
-  // sum the four waves in LDS (fixed order), then one coalesced partial row
-  for (int s = 0; s < 4; ++s) {
-    if (w == s) {
+  // sum the four waves in LDS (fixed order, padded against bank conflicts),
+  // then one coalesced 16 KB partial row
+  for (int st = 0; st < 4; ++st) {
+    if (w == st) {
 #pragma unroll
       for (int idx = 0; idx < 64; ++idx) {
         const int j = 32 * lane + 2048 * (idx >> 5) + (idx & 31);
         const int pj = j + (j >> 5);
-        s_lds[pj] = (s == 0) ? acc[idx] : s_lds[pj] + acc[idx];
+        s_red[pj] = (st == 0) ? acc[idx] : s_red[pj] + acc[idx];
       }
     }
     __syncthreads();
   }
-  float* dst = a.partials + (size_t)wg * kH;
+  float* dst = a.cold_part + (size_t)wg * kH;
 #pragma unroll
-  for (int m = 0; m < kH / kThreads; ++m) {
-    const int j = threadIdx.x + kThreads * m;
-    dst[j] = s_lds[j + (j >> 5)];
+  for (int m = 0; m < kH / kThreads / 4; ++m) {
+    const int j = 4 * (threadIdx.x + kThreads * m);
+    f32x4 v;
+    v.x = s_red[j + (j >> 5)];
+    v.y = s_red[j + 1 + ((j + 1) >> 5)];
+    v.z = s_red[j + 2 + ((j + 2) >> 5)];
+    v.w = s_red[j + 3 + ((j + 3) >> 5)];
+    *reinterpret_cast<f32x4*>(dst + j) = v;
   }
 }
 
-__device__ void pred_d_role(const UpArgs& a, int wg, float r) {
-  const int w = threadIdx.x >> 6, lane = lane_id();
-  const int row = wg * 4 + w;
-  if (row >= a.pd_rank) return;
+// bf16 weights of one predictor down row for this lane (elements
+// 8 (lane + 64 it) .. +8, it < 8), loaded before anything else.
+struct PredRowBf16 {
+  u32x4 v[8];
+};
+
+template <bool BF16>
+__device__ void pred_d_role_t(const UpArgs& a, int row) {
+  const int lane = lane_id();
+  PredRowBf16 dw;
+  if constexpr (BF16) {
+    const uint16_t* drow = reinterpret_cast<const uint16_t*>(a.pd_w) + (size_t)row * kH;
+#pragma unroll
+    for (int it = 0; it < 8; ++it) dw.v[it] = load16(reinterpret_cast<const uint8_t*>(drow + 8 * (lane + 64 * it)));
+  }
+  const bool norm = a.pd_norm_w && !a.pd_q;
+  const float r = norm ? r_from_parts(a.tok.ssq, a.tok.eps) : 1.0f;
   float acc = 0.0f;
 #pragma unroll
   for (int it = 0; it < 8; ++it) {
@@ -227,27 +318,25 @@ __device__ void pred_d_role(const UpArgs& a, int wg, float r) {
 #pragma unroll
       for (int k = 0; k < 8; ++k) q[k] = a.pd_q[e0 + k];
     } else {
-      const u32x4 xv = *reinterpret_cast<const u32x4*>(a.x + e0);
+      const u32x4 xv = *reinterpret_cast<const u32x4*>(a.tok.x + e0);
       u32x4 wv = {0, 0, 0, 0};
-      if (a.pd_norm_w) wv = *reinterpret_cast<const u32x4*>(a.pd_norm_w + e0);
+      if (norm) wv = *reinterpret_cast<const u32x4*>(a.pd_norm_w + e0);
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
         float v0 = half_lo(xv[d]), v1 = half_hi(xv[d]);
-        if (a.pd_norm_w) {
-          v0 = round_f16(v0 * r * half_lo(wv[d]));
-          v1 = round_f16(v1 * r * half_hi(wv[d]));
+        if (norm) {
+          v0 = xn_exact(v0, r, half_lo(wv[d]));
+          v1 = xn_exact(v1, r, half_hi(wv[d]));
         }
-        q[2 * d] = a.pd_bf16 ? round_bf16(v0) : v0;
-        q[2 * d + 1] = a.pd_bf16 ? round_bf16(v1) : v1;
+        q[2 * d] = BF16 ? round_bf16(v0) : v0;
+        q[2 * d + 1] = BF16 ? round_bf16(v1) : v1;
       }
     }
-    if (a.pd_bf16) {
-      const uint16_t* drow = reinterpret_cast<const uint16_t*>(a.pd_w) + (size_t)row * kH;
-      const u32x4 dv = *reinterpret_cast<const u32x4*>(drow + e0);
+    if constexpr (BF16) {
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
-        acc = fmaf(bf16_bits_to_float((uint16_t)(dv[d] & 0xFFFFu)), q[2 * d], acc);
-        acc = fmaf(bf16_bits_to_float((uint16_t)(dv[d] >> 16)), q[2 * d + 1], acc);
+        acc = fmaf(bf16_bits_to_float((uint16_t)(dw.v[it][d] & 0xFFFFu)), q[2 * d], acc);
+        acc = fmaf(bf16_bits_to_float((uint16_t)(dw.v[it][d] >> 16)), q[2 * d + 1], acc);
       }
     } else {
       const float* drow = reinterpret_cast<const float*>(a.pd_w) + (size_t)row * kH;
@@ -264,48 +353,48 @@ __device__ void pred_d_role(const UpArgs& a, int wg, float r) {
   if (lane == 0) a.pd_z[row] = acc;
 }
 
-__device__ void hot_up_role(const UpArgs& a, int wg, float r) {
+__device__ void pred_d_role(const UpArgs& a, int wg) {
+  const int row = wg * 4 + (threadIdx.x >> 6);
+  if (row >= a.pd_rank) return;
+  if (a.pd_bf16)
+    pred_d_role_t<true>(a, row);
+  else
+    pred_d_role_t<false>(a, row);
+}
+
+__device__ void hot_up_role(const UpArgs& a, int wg, uint32_t* s_nat, uint32_t* s_pair) {
   const int w = threadIdx.x >> 6, lane = lane_id();
   const int k0 = (wg * 4 + w) * 2;
-  if (k0 >= a.n_hot) return;
-  const bool two = (k0 + 1) < a.n_hot;
+  const bool one = k0 < a.n_hot, two = (k0 + 1) < a.n_hot;
   u32x4 qg[2][4], qu[2][4];
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
     const size_t off = (size_t)k0 * kH + 1024 * it + 16 * lane;
-    qg[0][it] = load16(a.gate_q + off);
-    qu[0][it] = load16(a.up_q + off);
-    if (two) {
-      qg[1][it] = load16(a.gate_q + off + kH);
-      qu[1][it] = load16(a.up_q + off + kH);
-    } else {
-      qg[1][it] = u32x4{0, 0, 0, 0};
-      qu[1][it] = u32x4{0, 0, 0, 0};
-    }
+    qg[0][it] = one ? load16(a.gate_q + off) : u32x4{0, 0, 0, 0};
+    qu[0][it] = one ? load16(a.up_q + off) : u32x4{0, 0, 0, 0};
+    qg[1][it] = two ? load16(a.gate_q + off + kH) : u32x4{0, 0, 0, 0};
+    qu[1][it] = two ? load16(a.up_q + off + kH) : u32x4{0, 0, 0, 0};
   }
-  f16x2 xp[4][8];
-#pragma unroll
-  for (int it = 0; it < 4; ++it) {
-    float v[16];
-    load_xn16(a.x, a.norm_w, r, 1024 * it + 16 * lane, v);
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      xp[it][k].x = (_Float16)v[2 * k];
-      xp[it][k].y = (_Float16)v[2 * k + 1];
-    }
-  }
+  stage_xw(a.tok.xw, s_nat, s_pair);
+  if (!one) return;
+  const float r = token_r(a.tok);
   float g[2] = {0.0f, 0.0f}, u[2] = {0.0f, 0.0f};
 #pragma unroll
-  for (int n = 0; n < 2; ++n)
+  for (int it = 0; it < 4; ++it) {
+    const u32x4* p = reinterpret_cast<const u32x4*>(s_nat) + (1024 * it + 16 * lane) / 8;
+    const u32x4 xa = p[0], xb = p[1];
+    const f16x2 xp[8] = {as_f16x2(xa.x), as_f16x2(xa.y), as_f16x2(xa.z), as_f16x2(xa.w),
+                         as_f16x2(xb.x), as_f16x2(xb.y), as_f16x2(xb.z), as_f16x2(xb.w)};
 #pragma unroll
-    for (int it = 0; it < 4; ++it)
+    for (int n = 0; n < 2; ++n)
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
-        g[n] = dot2(fp8x2_to_f16x2(qg[n][it][d], false), xp[it][2 * d], g[n]);
-        g[n] = dot2(fp8x2_to_f16x2(qg[n][it][d], true), xp[it][2 * d + 1], g[n]);
-        u[n] = dot2(fp8x2_to_f16x2(qu[n][it][d], false), xp[it][2 * d], u[n]);
-        u[n] = dot2(fp8x2_to_f16x2(qu[n][it][d], true), xp[it][2 * d + 1], u[n]);
+        g[n] = dot2(fp8x2_to_f16x2(qg[n][it][d], false), xp[2 * d], g[n]);
+        g[n] = dot2(fp8x2_to_f16x2(qg[n][it][d], true), xp[2 * d + 1], g[n]);
+        u[n] = dot2(fp8x2_to_f16x2(qu[n][it][d], false), xp[2 * d], u[n]);
+        u[n] = dot2(fp8x2_to_f16x2(qu[n][it][d], true), xp[2 * d + 1], u[n]);
       }
+  }
 #pragma unroll
   for (int n = 0; n < 2; ++n) {
     g[n] = wave_sum(g[n]);
@@ -313,42 +402,52 @@ __device__ void hot_up_role(const UpArgs& a, int wg, float r) {
   }
   if (lane < 2 && (lane == 0 || two)) {
     const int k = k0 + lane;
-    float gg = (lane ? g[1] : g[0]) * a.gate_s[k];
-    const float uu = (lane ? u[1] : u[0]) * a.up_s[k];
+    float gg = r * (lane ? g[1] : g[0]) * a.gate_s[k];
+    const float uu = r * (lane ? u[1] : u[0]) * a.up_s[k];
     if (a.hot_gbias) gg += a.hot_gbias[k];
     a.h_hot[k] = gated_act(gg, uu, a.relu, a.both);
   }
 }
 
 __global__ __launch_bounds__(kThreads) void k_ffn_up(UpArgs a) {
-  __shared__ float s_lds[kLdsRed];
-  __shared__ int s_prefix[kMaxChunks + 1];
-  __shared__ float s_red[4];
-  const bool need_r = (a.norm_w != nullptr) || (a.wg_pred > 0 && a.pd_norm_w != nullptr && a.pd_q == nullptr);
-  float r = 1.0f;
-  if (need_r) r = block_rnorm(a.x, a.eps, s_red);
+  // hot: natural xw (8 KB); cold: paired xw (8 KB) + padded reduction (16.5 KB)
+  __shared__ u32x4 s_xw4[kH / 8];
+  __shared__ float s_red[kH + kH / 32];
+  uint32_t* s_xw = reinterpret_cast<uint32_t*>(s_xw4);
   int b = blockIdx.x;
   if (b < a.wg_cold) {
-    cold_role(a, b, r, s_lds, s_prefix);
+    cold_role(a, b, nullptr, s_xw, s_red);
     return;
   }
   b -= a.wg_cold;
   if (b < a.wg_pred) {
-    pred_d_role(a, b, r);
+    pred_d_role(a, b);
     return;
   }
   b -= a.wg_pred;
-  hot_up_role(a, b, r);
+  hot_up_role(a, b, s_xw, nullptr);
 }
 
 // Predictor-only launches (layer 0's lookahead, the standalone predictor
 // entry points) use their own symbols so per-kernel statistics of k_ffn_up /
 // k_ffn_down cover whole FFN layers only.
-__global__ __launch_bounds__(kThreads) void k_pred_up(UpArgs a) {
-  __shared__ float s_red[4];
-  float r = 1.0f;
-  if (a.pd_norm_w != nullptr && a.pd_q == nullptr) r = block_rnorm(a.x, a.eps, s_red);
-  pred_d_role(a, blockIdx.x, r);
+__global__ __launch_bounds__(kThreads) void k_pred_up(UpArgs a) { pred_d_role(a, blockIdx.x); }
+
+// x -> (xw = fp16(x * w) or x, 256 canonical sum-of-squares partials).  One
+// workgroup; 16 elements per thread.
+__global__ __launch_bounds__(kThreads) void k_prep(const uint16_t* x, const uint16_t* w, uint16_t* xw,
+                                                   float* ssq) {
+  const int t = threadIdx.x;
+  float v[16];
+  load_h16(x, 16 * t, v);
+  ssq[t] = ssq16(v);
+  if (xw) {
+    float wv[16];
+    if (w) load_h16(w, 16 * t, wv);
+    uint16_t* o = xw + 16 * t;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) o[e] = float_to_half_bits(w ? v[e] * wv[e] : v[e]);
+  }
 }
 
 // ── ffn_down roles ──────────────────────────────────────────────────────────
@@ -402,41 +501,82 @@ __device__ void pred_u_role(const DownArgs& a, int c, int* s_wcnt) {
   if (t == 0) a.sel_counts[c] = s_wcnt[0] + s_wcnt[1] + s_wcnt[2] + s_wcnt[3];
 }
 
-__device__ void down_role(const DownArgs& a, int wg, float* s_part, float* s_yhot) {
+struct DownShared {
+  float cold[4][kRowsPerDownWG];     // per-wave cold sums
+  float yhot[kRowsPerDownWG];
+  float out[kRowsPerDownWG];
+};
+
+// Accumulate the 16 down nibbles at rows [j0, j0+16) of one record, times hs.
+__device__ __forceinline__ void cold_down16(uint32_t n0, uint32_t n1, float hs, float acc[16]) {
+  f16x2 t[4];
+  int4x8_to_f16x2x4(n0, t);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    acc[k] = fmaf(hs, (float)t[k].x, acc[k]);
+    acc[k + 4] = fmaf(hs, (float)t[k].y, acc[k + 4]);
+  }
+  int4x8_to_f16x2x4(n1, t);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    acc[8 + k] = fmaf(hs, (float)t[k].x, acc[8 + k]);
+    acc[12 + k] = fmaf(hs, (float)t[k].y, acc[12 + k]);
+  }
+}
+
+__device__ void down_role(const DownArgs& a, int b, DownShared& sh) {
   const int t = threadIdx.x, w = t >> 6, lane = lane_id();
-  const int j0 = wg * kRowsPerDownWG;
-  float yh[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-  if (a.n_hot > 0) {
-    const int nch = a.down_stride >> 4;
-    u32x4 q[4][4];
+  // XCD-aware tiling: consecutive blockIdx go to different XCDs (b % 8), so
+  // give each XCD a contiguous 512-row band; its 32 tiles then share the L2
+  // lines holding those rows' nibbles of every cold record.
+  const int tile = (b & 7) * (kDownWG / 8) + (b >> 3);
+  const int j0 = tile * kRowsPerDownWG;
+
+  // 1. hot down rows: 4 per wave (chunks past the row stride are zero)
+  const int nch = a.down_stride >> 4;
+  u32x4 q[4][4];
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const uint8_t* row = a.down_q + (size_t)(j0 + 4 * w + rr) * a.down_stride;
-#pragma unroll
-      for (int it = 0; it < 4; ++it) {
-        const int c = lane + 64 * it;
-        q[rr][it] = (c < nch) ? load16(row + 16 * c) : u32x4{0, 0, 0, 0};
-      }
-    }
-    float hv[4][16];
+  for (int rr = 0; rr < 4; ++rr) {
+    const uint8_t* row = a.down_q + (size_t)(j0 + 4 * w + rr) * a.down_stride;
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
-      const int k0 = 16 * (lane + 64 * it);
-      if (k0 + 16 <= a.n_hot) {
-        const f32x4* ph = reinterpret_cast<const f32x4*>(a.h_hot + k0);
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          const f32x4 v = ph[m];
-          hv[it][4 * m] = v[0];
-          hv[it][4 * m + 1] = v[1];
-          hv[it][4 * m + 2] = v[2];
-          hv[it][4 * m + 3] = v[3];
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) hv[it][e] = (k0 + e < a.n_hot) ? a.h_hot[k0 + e] : 0.0f;
-      }
+      const int c = lane + 64 * it;
+      q[rr][it] = (a.n_hot > 0 && c < nch) ? load16(row + 16 * c) : u32x4{0, 0, 0, 0};
     }
+  }
+  // h values for this lane's chunks (L2-resident, written by ffn_up)
+  float hv[4][16];
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int k0 = 16 * (lane + 64 * it);
+    if (k0 + 16 <= a.n_hot) {
+      const f32x4* ph = reinterpret_cast<const f32x4*>(a.h_hot + k0);
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const f32x4 v = ph[m];
+        hv[it][4 * m] = v[0];
+        hv[it][4 * m + 1] = v[1];
+        hv[it][4 * m + 2] = v[2];
+        hv[it][4 * m + 3] = v[3];
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) hv[it][e] = (k0 + e < a.n_hot) ? a.h_hot[k0 + e] : 0.0f;
+    }
+  }
+  // 2. cold: sum the partial rows of ffn_up's cold workgroups for rows
+  //    [j0, j0+16): thread t reads 4 rows (t & 3) of partials p = t/4 + 64 m.
+  f32x4 cp = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (a.cold_total) {
+    const int total = *a.cold_total;
+    int n_part = (total + kColdPerWG - 1) / kColdPerWG;
+    n_part = n_part < a.cold_wg ? n_part : a.cold_wg;
+    for (int p = t >> 2; p < n_part; p += kThreads / 4)
+      cp += *reinterpret_cast<const f32x4*>(a.cold_part + (size_t)p * kH + j0 + 4 * (t & 3));
+  }
+  // 3. hot rows
+  float yh[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  if (a.n_hot > 0) {
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       float acc = 0.0f;
@@ -454,36 +594,52 @@ __device__ void down_role(const DownArgs& a, int wg, float* s_part, float* s_yho
       yh[rr] = wave_sum(acc);
     }
   }
+  // 4. cold sums: lanes with the same (t & 3) hold the same 4 rows
+  {
+    f32x4 v = cp;
+#pragma unroll
+    for (int off = 4; off < 64; off <<= 1) {
+      v.x += __shfl_xor(v.x, off, kWave);
+      v.y += __shfl_xor(v.y, off, kWave);
+      v.z += __shfl_xor(v.z, off, kWave);
+      v.w += __shfl_xor(v.w, off, kWave);
+    }
+    if (lane < 4) {
+      sh.cold[w][4 * lane] = v.x;
+      sh.cold[w][4 * lane + 1] = v.y;
+      sh.cold[w][4 * lane + 2] = v.z;
+      sh.cold[w][4 * lane + 3] = v.w;
+    }
+  }
   if (lane == 0) {
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       const int j = j0 + 4 * w + rr;
-      s_yhot[4 * w + rr] = (a.n_hot > 0) ? yh[rr] * a.down_s[j] : 0.0f;
+      sh.yhot[4 * w + rr] = (a.n_hot > 0) ? yh[rr] * a.down_s[j] : 0.0f;
     }
   }
-  const int row = t & 15, ps = t >> 4;
-  float s = 0.0f;
-  const int n_part = a.n_part_in ? *a.n_part_in : a.n_partials;
-  for (int p = ps; p < n_part; p += 16) s += a.partials[(size_t)p * kH + j0 + row];
-  s_part[t] = s;
   __syncthreads();
-  if (t < 16) {
-    float yc = 0.0f;
-#pragma unroll
-    for (int m = 0; m < 16; ++m) yc += s_part[16 * m + t];
-    const float y = s_yhot[t] + yc;
+  if (t < kRowsPerDownWG) {
+    const float yc = (sh.cold[0][t] + sh.cold[1][t]) + (sh.cold[2][t] + sh.cold[3][t]);
+    const float y = sh.yhot[t] + yc;
     const int j = j0 + t;
     if (a.y32) a.y32[j] = y;
-    const float o = (a.res ? half_bits_to_float(a.res[j]) : 0.0f) + y;
-    const uint16_t ob = float_to_half_bits(o);
+    const uint16_t ob = float_to_half_bits((a.res ? half_bits_to_float(a.res[j]) : 0.0f) + y);
     if (a.out) a.out[j] = ob;
     if (a.out2) a.out2[j] = ob;
+    const float o = half_bits_to_float(ob);
+    sh.out[t] = o;
+    if (a.xw_out)
+      a.xw_out[j] = float_to_half_bits(a.next_norm_w ? o * half_bits_to_float(a.next_norm_w[j]) : o);
+  }
+  if (a.ssq_out) {
+    __syncthreads();
+    if (t == 0) a.ssq_out[tile] = ssq16(sh.out);
   }
 }
 
 __global__ __launch_bounds__(kThreads) void k_ffn_down(DownArgs a) {
-  __shared__ float s_part[kThreads];
-  __shared__ float s_yhot[kRowsPerDownWG];
+  __shared__ DownShared sh;
   __shared__ int s_wcnt[4];
   int b = blockIdx.x;
   if (b < a.wg_pred) {
@@ -491,7 +647,7 @@ __global__ __launch_bounds__(kThreads) void k_ffn_down(DownArgs a) {
     return;
   }
   b -= a.wg_pred;
-  down_role(a, b, s_part, s_yhot);
+  down_role(a, b, sh);
 }
 
 __global__ __launch_bounds__(kThreads) void k_pred_down(DownArgs a) {
@@ -541,31 +697,34 @@ __global__ __launch_bounds__(kThreads) void k_dequant(const uint8_t* records, in
 
 __global__ __launch_bounds__(kThreads) void k_rmsnorm(const uint16_t* x, const uint16_t* w,
                                                       float eps, uint16_t* out) {
-  __shared__ float s_red[4];
+  __shared__ float s_parts[kThreads];
   const uint16_t* xr = x + (size_t)blockIdx.x * kH;
-  const float r = block_rnorm(xr, eps, s_red);
-  float v[16];
-  load_xn16(xr, w, r, 16 * threadIdx.x, v);
+  const float r = block_rnorm(xr, eps, s_parts);
+  float v[16], wv[16];
+  load_h16(xr, 16 * threadIdx.x, v);
+  load_h16(w, 16 * threadIdx.x, wv);
   uint16_t* o = out + (size_t)blockIdx.x * kH + 16 * threadIdx.x;
 #pragma unroll
-  for (int e = 0; e < 16; ++e) o[e] = float_to_half_bits(v[e]);
+  for (int e = 0; e < 16; ++e) o[e] = float_to_half_bits(xn_exact(v[e], r, wv[e]));
 }
 
 // Query for batch > 1 (engine.py:277): mean over rows of RMSNorm(x), fp16
 // rounded, then cast to the predictor dtype.  One workgroup.
 __global__ __launch_bounds__(kThreads) void k_query(const uint16_t* x, int rows, const uint16_t* w,
                                                     float eps, int to_bf16, float* q) {
-  __shared__ float s_red[4];
+  __shared__ float s_parts[kThreads];
   float sum[16];
 #pragma unroll
   for (int e = 0; e < 16; ++e) sum[e] = 0.0f;
+  float wv[16];
+  if (w) load_h16(w, 16 * threadIdx.x, wv);
   for (int b = 0; b < rows; ++b) {
     const uint16_t* xr = x + (size_t)b * kH;
-    const float r = w ? block_rnorm(xr, eps, s_red) : 1.0f;
+    const float r = w ? block_rnorm(xr, eps, s_parts) : 1.0f;
     float v[16];
-    load_xn16(xr, w, r, 16 * threadIdx.x, v);
+    load_h16(xr, 16 * threadIdx.x, v);
 #pragma unroll
-    for (int e = 0; e < 16; ++e) sum[e] += v[e];
+    for (int e = 0; e < 16; ++e) sum[e] += w ? xn_exact(v[e], r, wv[e]) : v[e];
   }
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
@@ -609,14 +768,14 @@ void clear_error() { g_err.clear(); }
 
 static int n_chunks_for(int inter) { return (inter + kSelChunk - 1) / kSelChunk; }
 
-static int cold_wg_for(int capacity) {
-  int wg = (capacity + kRecordsPerColdWG - 1) / kRecordsPerColdWG;
+int cold_wg_for(int expected) {
+  int wg = (expected + kColdPerWG - 1) / kColdPerWG;
   return wg < 1 ? 1 : (wg > kMaxColdWG ? kMaxColdWG : wg);
 }
 
 static int validate_hot(const oi2_hot* hot) {
   if (!hot || hot->n_hot == 0) return OI2_OK;
-  OI2_CHECK_ARG(hot->n_hot > 0, "n_hot must be >= 0");
+  OI2_CHECK_ARG(hot->n_hot > 0 && hot->n_hot <= kH, "n_hot %d must be in 0..%d", hot->n_hot, kH);
   OI2_CHECK_ARG(hot->down_stride >= hot->n_hot && hot->down_stride % 16 == 0 &&
                     hot->down_stride <= 4096,
                 "down_stride %d must be >= n_hot %d, a multiple of 16 and <= 4096",
@@ -637,6 +796,37 @@ static int validate_pred(const oi2_predictor* p) {
   OI2_CHECK_ARG(p->dtype == OI2_DTYPE_F32 || p->dtype == OI2_DTYPE_BF16, "predictor dtype %d",
                 p->dtype);
   return OI2_OK;
+}
+
+// Workspace carve-up shared by the FFN entry points.
+struct FfnWs {
+  float* h_hot;
+  float* cold_part;
+  int32_t* cold_total;
+  uint16_t* xw;
+  float* ssq;
+};
+
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+size_t ffn_ws_bytes(int n_hot, int cold_wg) {
+  return align256((size_t)(n_hot > 0 ? n_hot : 0) * 4 + 64) + align256((size_t)cold_wg * kH * 4) +
+         align256(64) + align256(kH * 2) + align256(kDownWG * 4);
+}
+
+static FfnWs ffn_ws(void* base, int n_hot, int cold_wg) {
+  char* p = reinterpret_cast<char*>(base);
+  FfnWs w;
+  w.h_hot = reinterpret_cast<float*>(p);
+  p += align256((size_t)(n_hot > 0 ? n_hot : 0) * 4 + 64);
+  w.cold_part = reinterpret_cast<float*>(p);
+  p += align256((size_t)cold_wg * kH * 4);
+  w.cold_total = reinterpret_cast<int32_t*>(p);
+  p += align256(64);
+  w.xw = reinterpret_cast<uint16_t*>(p);
+  p += align256(kH * 2);
+  w.ssq = reinterpret_cast<float*>(p);
+  return w;
 }
 
 }  // namespace oi2
@@ -675,10 +865,9 @@ int oi2_rmsnorm(const uint16_t* x, const uint16_t* w, int32_t rows, float eps, u
   return OI2_OK;
 }
 
-size_t oi2_ffn_workspace_bytes(int32_t batch, int32_t n_hot) {
+size_t oi2_ffn_workspace_bytes(int32_t batch, int32_t n_hot, int32_t cold_capacity) {
   (void)batch;
-  const size_t hot = (size_t)((n_hot > 0 ? n_hot : 0) + 64) * sizeof(float);
-  return hot + (size_t)kMaxColdWG * kH * sizeof(float) + 256;
+  return ffn_ws_bytes(n_hot, cold_capacity > 0 ? cold_wg_for(cold_capacity) : 0);
 }
 
 int oi2_ffn_forward(const uint16_t* x, int32_t batch, const uint16_t* norm_w, float eps,
@@ -696,6 +885,7 @@ int oi2_ffn_forward(const uint16_t* x, int32_t batch, const uint16_t* norm_w, fl
   if (rc) return rc;
   const int n_hot = hot ? hot->n_hot : 0;
   const bool has_cold = cold && active && cold->n_records > 0 && active->n_chunks > 0;
+  int cap = 0;
   if (has_cold) {
     OI2_CHECK_ARG(cold->records && (uintptr_t)cold->records % 16 == 0,
                   "cold records must be non-null and 16-byte aligned");
@@ -703,24 +893,24 @@ int oi2_ffn_forward(const uint16_t* x, int32_t batch, const uint16_t* norm_w, fl
     OI2_CHECK_ARG(active->n_chunks <= kMaxChunks && active->chunk > 0,
                   "active list: n_chunks %d (max %d), chunk %d", active->n_chunks, kMaxChunks,
                   active->chunk);
+    cap = active->n_chunks * active->chunk;
   }
-  OI2_CHECK_ARG(workspace && workspace_bytes >= oi2_ffn_workspace_bytes(batch, n_hot),
+  const int expected = has_cold ? (active->expected > 0 && active->expected < cap ? active->expected : cap) : 0;
+  const int wg_cold = has_cold ? cold_wg_for(expected) : 0;
+  const int ws_wg = has_cold ? cold_wg_for(cap) : 0;
+  OI2_CHECK_ARG(workspace && workspace_bytes >= ffn_ws_bytes(n_hot, ws_wg),
                 "workspace of %zu bytes is smaller than the %zu required", workspace_bytes,
-                oi2_ffn_workspace_bytes(batch, n_hot));
-  float* h_hot = reinterpret_cast<float*>(workspace);
-  float* partials = h_hot + ((n_hot + 64) & ~63);
-  int* n_part = reinterpret_cast<int*>(partials + (size_t)kMaxColdWG * kH);
-  const int wg_cold = has_cold ? cold_wg_for(active->n_chunks * active->chunk < cold->n_records
-                                                 ? active->n_chunks * active->chunk
-                                                 : cold->n_records)
-                               : 0;
+                ffn_ws_bytes(n_hot, ws_wg));
+  FfnWs ws = ffn_ws(workspace, n_hot, ws_wg);
   hipStream_t st = (hipStream_t)stream;
   for (int b = 0; b < batch; ++b) {
     const uint16_t* xb = x + (size_t)b * kH;
+    if (norm_w) {
+      hipLaunchKernelGGL(k_prep, dim3(1), dim3(kThreads), 0, st, xb, norm_w, ws.xw, ws.ssq);
+      OI2_CHECK_LAUNCH();
+    }
     UpArgs ua{};
-    ua.x = xb;
-    ua.norm_w = norm_w;
-    ua.eps = eps;
+    ua.tok = TokenIn{xb, norm_w ? ws.xw : xb, ws.ssq, eps, norm_w ? 1 : 0};
     ua.relu = act == OI2_ACT_RELU;
     ua.both = act_on_both != 0;
     ua.n_hot = n_hot;
@@ -731,15 +921,16 @@ int oi2_ffn_forward(const uint16_t* x, int32_t batch, const uint16_t* norm_w, fl
       ua.up_s = hot->up_scale;
       ua.hot_gbias = hot->gate_bias;
     }
-    ua.h_hot = h_hot;
+    ua.h_hot = ws.h_hot;
     if (has_cold) {
       ua.records = cold->records;
       ua.n_records = cold->n_records;
       ua.cold_gbias = cold->gate_bias;
       ua.act = ActiveList{active->slots, active->counts, active->n_chunks, active->chunk};
+      ua.cold_part = ws.cold_part;
+      ua.cold_total = ws.cold_total;
+      ua.cold_cap = cap;
     }
-    ua.partials = partials;
-    ua.n_part_out = n_part;
     ua.wg_cold = wg_cold;
     ua.wg_pred = 0;
     ua.wg_hot = (n_hot + 7) / 8;
@@ -750,20 +941,23 @@ int oi2_ffn_forward(const uint16_t* x, int32_t batch, const uint16_t* norm_w, fl
     }
     DownArgs da{};
     da.res = add_residual ? xb : nullptr;
-    da.h_hot = h_hot;
+    da.h_hot = ws.h_hot;
     da.n_hot = n_hot;
     if (n_hot) {
       da.down_stride = hot->down_stride;
       da.down_q = hot->down_q;
       da.down_s = hot->down_scale;
     }
-    da.partials = partials;
-    da.n_partials = 0;
-    da.n_part_in = wg_cold ? n_part : nullptr;
+    if (has_cold) {
+      da.cold_part = ws.cold_part;
+      da.cold_total = ws.cold_total;
+      da.cold_cap = cap;
+      da.cold_wg = wg_cold;
+    }
     da.out = out ? out + (size_t)b * kH : nullptr;
     da.y32 = y32 ? y32 + (size_t)b * kH : nullptr;
     da.wg_pred = 0;
-    da.wg_down = kH / kRowsPerDownWG;
+    da.wg_down = kDownWG;
     hipLaunchKernelGGL(k_ffn_down, dim3(da.wg_down), dim3(kThreads), 0, st, da);
     OI2_CHECK_LAUNCH();
   }
@@ -772,16 +966,15 @@ int oi2_ffn_forward(const uint16_t* x, int32_t batch, const uint16_t* norm_w, fl
 
 size_t oi2_predict_workspace_bytes(const oi2_predictor* p) {
   const int rank = p ? p->rank : 256;
-  return (size_t)(kH + rank + 64) * sizeof(float);
+  return (size_t)(kH + rank + 64 + kDownWG) * sizeof(float);
 }
 
-static int launch_predictor(const uint16_t* x, const uint16_t* norm_w, float eps, const float* q,
-                            const oi2_predictor* p, float thr, const int32_t* lut, int32_t* slots,
-                            int32_t* ids, int32_t* counts, float* logits, float* probs,
-                            uint8_t* mask, float* z, hipStream_t st) {
+int launch_predictor(const TokenIn& tok, const uint16_t* norm_w, const float* q,
+                     const oi2_predictor* p, float thr, const int32_t* lut, int32_t* slots,
+                     int32_t* ids, int32_t* counts, float* logits, float* probs, uint8_t* mask,
+                     float* z, hipStream_t st) {
   UpArgs ua{};
-  ua.x = x;
-  ua.eps = eps;
+  ua.tok = tok;
   ua.pd_w = p->down_w;
   ua.pd_rank = p->rank;
   ua.pd_bf16 = p->dtype == OI2_DTYPE_BF16;
@@ -826,8 +1019,10 @@ int oi2_predict(const uint16_t* h, int32_t rows, const oi2_predictor* p, float t
                 "predict workspace too small");
   float* z = reinterpret_cast<float*>(workspace) + kH;
   for (int b = 0; b < rows; ++b) {
-    rc = launch_predictor(h + (size_t)b * kH, nullptr, 0.0f, nullptr, p, threshold_logit, nullptr,
-                          nullptr, nullptr, nullptr, logits ? logits + (size_t)b * p->inter : nullptr,
+    const uint16_t* hb = h + (size_t)b * kH;
+    rc = launch_predictor(TokenIn{hb, nullptr, nullptr, 0.0f, 0}, nullptr, nullptr, p,
+                          threshold_logit, nullptr, nullptr, nullptr, nullptr,
+                          logits ? logits + (size_t)b * p->inter : nullptr,
                           probs ? probs + (size_t)b * p->inter : nullptr,
                           mask ? mask + (size_t)b * p->inter : nullptr, z, (hipStream_t)stream);
     if (rc) return rc;
@@ -853,15 +1048,19 @@ int oi2_predict_select(const uint16_t* x, int32_t batch, const uint16_t* norm_w,
   hipStream_t st = (hipStream_t)stream;
   float* q = reinterpret_cast<float*>(workspace);
   float* z = q + kH;
+  float* ssq = z + p->rank + 64;
   const float* qp = nullptr;
   if (batch > 1) {
     hipLaunchKernelGGL(k_query, dim3(1), dim3(kThreads), 0, st, x, batch, norm_w, eps,
                        p->dtype == OI2_DTYPE_BF16 ? 1 : 0, q);
     OI2_CHECK_LAUNCH();
     qp = q;
+  } else if (norm_w) {
+    hipLaunchKernelGGL(k_prep, dim3(1), dim3(kThreads), 0, st, x, nullptr, nullptr, ssq);
+    OI2_CHECK_LAUNCH();
   }
-  rc = launch_predictor(x, norm_w, eps, qp, p, threshold_logit, lut, slots, ids, counts, nullptr,
-                        nullptr, nullptr, z, st);
+  rc = launch_predictor(TokenIn{x, nullptr, ssq, eps, norm_w ? 1 : 0}, norm_w, qp,
+                        p, threshold_logit, lut, slots, ids, counts, nullptr, nullptr, nullptr, z, st);
   if (rc) return rc;
   if (total) {
     hipLaunchKernelGGL(k_compact_dense, dim3(1), dim3(kThreads), 0, st, slots, ids, counts,

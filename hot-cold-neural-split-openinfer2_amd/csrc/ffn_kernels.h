@@ -6,11 +6,11 @@ namespace oi2 {
 
 constexpr int kThreads = 256;
 constexpr int kRowsPerDownWG = 16;
+constexpr int kDownWG = kH / kRowsPerDownWG;   // 256 output tiles
 constexpr int kSelChunk = 256;
 constexpr int kMaxChunks = 256;
-constexpr int kMaxColdWG = 256;
-constexpr int kRecordsPerColdWG = 8;   // target records per cold workgroup (2 per wave)
-constexpr int kLdsRed = kH + kH / 32;
+constexpr int kColdPerWG = 4;                  // one cold record per wave
+constexpr int kMaxColdWG = 1024;
 
 struct ActiveList {
   const int32_t* slots;
@@ -19,49 +19,66 @@ struct ActiveList {
   int chunk;
 };
 
-struct UpArgs {
-  const uint16_t* x;        // (H) fp16 token
-  const uint16_t* norm_w;   // (H) fp16 or null: x is already normalised
+// Normalised-token inputs every FFN workgroup shares: xw = fp16(x * w) (the
+// norm weight applied, not yet scaled) and 256 partial sums of x^2 from which
+// each wave derives r = rsqrt(mean(x^2) + eps); x_n = r * xw.
+struct TokenIn {
+  const uint16_t* x;        // (H) fp16 token (the predictor normalises it exactly)
+  const uint16_t* xw;       // (H) fp16 x * norm weight, or x when use_norm == 0
+  const float* ssq;         // 256 partial sums of x^2
   float eps;
+  int use_norm;
+};
+
+struct UpArgs {
+  TokenIn tok;
   int relu, both;
-  // hot
+  // hot gate/up
   int n_hot;
   const uint8_t* gate_q;
   const uint8_t* up_q;
   const float* gate_s;
   const float* up_s;
   const float* hot_gbias;
-  float* h_hot;
-  // cold
+  float* h_hot;             // (n_hot)
+  // cold gate/up: one wave per active record
   const uint8_t* records;
   int n_records;
   const float* cold_gbias;
   ActiveList act;
-  float* partials;          // (wg_cold, H)
-  int* n_part_out;          // cold workgroup 0 publishes how many partial rows it used
-  // predictor down projection of the lookahead layer
+  float* cold_part;         // (wg_cold, H) partial down sums, one row per workgroup
+  int32_t* cold_total;      // number of active items
+  int cold_cap;             // items beyond this are ignored
+  // predictor down projection (lookahead layer): z = D q, q = cast(fp16(x r w'))
   const void* pd_w;
   int pd_rank;
   int pd_bf16;
-  const uint16_t* pd_norm_w;  // norm applied to x for the query, or null
+  const uint16_t* pd_norm_w;  // null: q = cast(x)
   const float* pd_q;          // precomputed query (H), or null
-  float* pd_z;                // (rank)
+  float* pd_z;
   int wg_cold, wg_pred, wg_hot;
 };
 
 struct DownArgs {
   const uint16_t* res;      // residual (H) fp16 or null
+  // hot down
   const float* h_hot;
   int n_hot;
   int down_stride;
   const uint8_t* down_q;
   const float* down_s;
-  const float* partials;
-  int n_partials;           // used when n_part_in is null
-  const int* n_part_in;     // partial rows written by ffn_up's cold workgroups
+  // cold down: partial rows from ffn_up's cold workgroups
+  const float* cold_part;
+  const int32_t* cold_total;
+  int cold_cap;
+  int cold_wg;              // ffn_up's cold workgroup count
+  // outputs
   uint16_t* out;
   uint16_t* out2;
   float* y32;
+  const uint16_t* next_norm_w;  // norm weight of the next layer, or null
+  uint16_t* xw_out;             // fp16(out * next_norm_w)
+  float* ssq_out;               // 256 partial sums of out^2
   // predictor up projection + selection
   const void* pu_w;
   const void* pu_b;
@@ -80,6 +97,7 @@ struct DownArgs {
   int wg_pred, wg_down;
 };
 
+__global__ void k_prep(const uint16_t* x, const uint16_t* w, uint16_t* xw, float* ssq);
 __global__ void k_ffn_up(UpArgs a);
 __global__ void k_ffn_down(DownArgs a);
 __global__ void k_pred_up(UpArgs a);

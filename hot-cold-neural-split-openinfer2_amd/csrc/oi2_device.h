@@ -32,6 +32,12 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
+// Bit reinterpretation of one dword.  Take the dword by value: clang's
+// __builtin_bit_cast applied directly to an ext-vector element expression
+// (v.y, v[k]) reads element 0 instead.
+__device__ __forceinline__ f16x2 as_f16x2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
+__device__ __forceinline__ float as_f32(uint32_t v) { return __builtin_bit_cast(float, v); }
+
 // 16 payload bytes at a 2-byte aligned address (one global_load_dwordx4).
 __device__ __forceinline__ u32x4 load16_a2(const uint8_t* p) {
   return *reinterpret_cast<const u32x4_a2*>(p);
@@ -92,11 +98,43 @@ __device__ __forceinline__ f32x2 fp8x2_to_f32x2(uint32_t d, bool hi) {
   return hi ? __builtin_amdgcn_cvt_pk_f32_fp8(d, true) : __builtin_amdgcn_cvt_pk_f32_fp8(d, false);
 }
 
-// Sum over the 64 lanes of a wave; every lane receives the total.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                                ROW_MASK, 0xF, false));
+}
+
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// Sum over the 64 lanes of a wave with DPP (quad swaps, row mirrors, then
+// row_bcast:15 / row_bcast:31 to carry row sums up to lane 63); every lane
+// receives the total.  Fixed order, so the result is deterministic.
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, kWave);
-  return v;
+  v += dpp_f<0xB1>(v);        // quad_perm [1,0,3,2]
+  v += dpp_f<0x4E>(v);        // quad_perm [2,3,0,1]
+  v += dpp_f<0x141>(v);       // row_half_mirror
+  v += dpp_f<0x140>(v);       // row_mirror
+  v += dpp_f<0x142, 0xA>(v);  // row_bcast:15 into rows 1, 3
+  v += dpp_f<0x143, 0xC>(v);  // row_bcast:31 into rows 2, 3
+  return readlane_f(v, 63);
+}
+
+// Lane i receives lane i+1's value (DPP wave_shl:1); lane 63 receives `fill`.
+__device__ __forceinline__ uint32_t wave_shl1(uint32_t v, uint32_t fill) {
+  return (uint32_t)__builtin_amdgcn_update_dpp((int)fill, (int)v, 0x130, 0xF, 0xF, false);
+}
+
+// 16 bytes starting 2 bytes into aligned chunk `a`, completed by the first
+// two bytes of the next chunk (`next0` = that chunk's first dword).
+__device__ __forceinline__ u32x4 realign2(u32x4 a, uint32_t next0) {
+  u32x4 r;
+  r.x = __builtin_amdgcn_alignbyte(a.y, a.x, 2);
+  r.y = __builtin_amdgcn_alignbyte(a.z, a.y, 2);
+  r.z = __builtin_amdgcn_alignbyte(a.w, a.z, 2);
+  r.w = __builtin_amdgcn_alignbyte(next0, a.w, 2);
+  return r;
 }
 
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (kWave - 1)); }

@@ -33,9 +33,12 @@ struct oi2_stack {
   int n_layers = 0, inter = 0, n_chunks = 0, relu = 0, both = 0, max_hot = 0, max_rank = 0;
   float eps = 0.0f, thr = 0.0f;
   uint16_t* xbuf = nullptr;      // (n_layers, H): output of each layer
+  uint16_t* xw = nullptr;        // (H) fp16 x * w of the layer about to run
+  float* ssq = nullptr;          // 256 sum-of-squares partials of that x
   float* h_hot = nullptr;
-  float* partials = nullptr;     // (kMaxColdWG, H)
-  int* n_part = nullptr;         // partial rows used by the current layer
+  float* cold_part = nullptr;    // (kMaxColdWG, H) partial rows of the current layer
+  int32_t* cold_total = nullptr;
+  int cold_cap = 0;
   float* z = nullptr;
   int32_t* sel_counts = nullptr; // (n_layers, n_chunks)
   int32_t* sel_slots = nullptr;  // (n_layers, n_chunks * 256)
@@ -53,16 +56,20 @@ struct oi2_stack {
 
 namespace oi2 {
 
+int cold_wg_for(int expected);
+
 static int stack_launch(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, hipStream_t st,
                         hipEvent_t* ev = nullptr) {
   const int n = s->n_layers;
   const size_t sel_stride = (size_t)s->n_chunks * kSelChunk;
+  hipLaunchKernelGGL(k_prep, dim3(1), dim3(kThreads), 0, st, x_in, s->layers[0].l.norm_w, s->xw,
+                     s->ssq);
+  OI2_CHECK_LAUNCH();
   // layer 0's active set from the token itself
   if (s->layers[0].has_pred) {
     const oi2_layer& l0 = s->layers[0].l;
     UpArgs ua{};
-    ua.x = x_in;
-    ua.eps = s->eps;
+    ua.tok = TokenIn{x_in, s->xw, s->ssq, s->eps, 1};
     ua.pd_w = l0.pred.down_w;
     ua.pd_rank = l0.pred.rank;
     ua.pd_bf16 = l0.pred.dtype == OI2_DTYPE_BF16;
@@ -94,9 +101,7 @@ static int stack_launch(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, hip
     const uint16_t* xl = (L == 0) ? x_in : s->xbuf + (size_t)(L - 1) * kH;
 
     UpArgs ua{};
-    ua.x = xl;
-    ua.norm_w = l.norm_w;
-    ua.eps = s->eps;
+    ua.tok = TokenIn{xl, s->xw, s->ssq, s->eps, 1};
     ua.relu = s->relu;
     ua.both = s->both;
     ua.n_hot = l.hot.n_hot;
@@ -116,10 +121,11 @@ static int stack_launch(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, hip
                             s->sel_counts + (size_t)L * s->n_chunks, s->n_chunks, kSelChunk};
       else
         ua.act = ActiveList{SL.all_slots, SL.all_count, 1, SL.n_all};
+      ua.cold_part = s->cold_part;
+      ua.cold_total = s->cold_total;
+      ua.cold_cap = s->cold_cap;
     }
-    ua.partials = s->partials;
-    ua.n_part_out = s->n_part;
-    ua.wg_cold = has_cold ? s->cold_wg : 0;
+    ua.wg_cold = has_cold ? (SL.has_pred ? s->cold_wg : cold_wg_for(SL.n_all)) : 0;
     ua.wg_hot = (l.hot.n_hot + 7) / 8;
     if (pred_next) {
       const oi2_layer& ln = s->layers[L + 1].l;
@@ -145,11 +151,19 @@ static int stack_launch(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, hip
     da.down_stride = l.hot.down_stride;
     da.down_q = l.hot.down_q;
     da.down_s = l.hot.down_scale;
-    da.partials = s->partials;
-    da.n_partials = 0;
-    da.n_part_in = ua.wg_cold ? s->n_part : nullptr;
+    if (has_cold) {
+      da.cold_part = s->cold_part;
+      da.cold_total = s->cold_total;
+      da.cold_cap = s->cold_cap;
+      da.cold_wg = ua.wg_cold;
+    }
     da.out = s->xbuf + (size_t)L * kH;
     da.out2 = (L == n - 1) ? x_out : nullptr;
+    if (L + 1 < n) {
+      da.next_norm_w = s->layers[L + 1].l.norm_w;
+      da.xw_out = s->xw;
+      da.ssq_out = s->ssq;
+    }
     if (pred_next) {
       const oi2_layer& ln = s->layers[L + 1].l;
       da.pu_w = ln.pred.up_w;
@@ -165,7 +179,7 @@ static int stack_launch(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, hip
       da.sel_counts = s->sel_counts + (size_t)(L + 1) * s->n_chunks;
       da.wg_pred = s->n_chunks;
     }
-    da.wg_down = kH / kRowsPerDownWG;
+    da.wg_down = kDownWG;
     hipLaunchKernelGGL(k_ffn_down, dim3(da.wg_pred + da.wg_down), dim3(kThreads), 0, st, da);
     OI2_CHECK_LAUNCH();
     if (ev) OI2_CHECK_HIP(hipEventRecord(ev[3 * L + 2], st));
@@ -180,8 +194,9 @@ static void stack_free(oi2_stack* s) {
   }
   for (auto& g : s->graphs) (void)hipGraphExecDestroy(g.exec);
   s->graphs.clear();
-  for (void* p : {(void*)s->xbuf, (void*)s->h_hot, (void*)s->partials, (void*)s->n_part, (void*)s->z,
-                  (void*)s->sel_counts, (void*)s->sel_slots, (void*)s->sel_ids})
+  for (void* p : {(void*)s->xbuf, (void*)s->xw, (void*)s->ssq, (void*)s->h_hot, (void*)s->cold_part,
+                  (void*)s->cold_total, (void*)s->z, (void*)s->sel_counts,
+                  (void*)s->sel_slots, (void*)s->sel_ids})
     if (p) (void)hipFree(p);
 }
 
@@ -242,16 +257,19 @@ int oi2_stack_create(const oi2_layer* layers, int32_t n_layers, int32_t inter, f
     max_records = std::max(max_records, SL.l.cold.n_records);
     s->layers.push_back(SL);
   }
-  s->cold_wg = std::max(1, std::min(kMaxColdWG, (max_records + kRecordsPerColdWG - 1) / kRecordsPerColdWG));
+  s->cold_wg = cold_wg_for(max_records);
+  s->cold_cap = std::max(s->n_chunks * kSelChunk, max_records);
   const size_t sel = (size_t)n_layers * s->n_chunks * kSelChunk;
   hipError_t e = hipSuccess;
   auto alloc = [&](void** p, size_t bytes) {
     if (e == hipSuccess) e = hipMalloc(p, bytes);
   };
   alloc((void**)&s->xbuf, (size_t)n_layers * kH * 2);
+  alloc((void**)&s->xw, (size_t)kH * 2);
+  alloc((void**)&s->ssq, (size_t)kDownWG * 4);
   alloc((void**)&s->h_hot, (size_t)(s->max_hot + 64) * 4);
-  alloc((void**)&s->partials, (size_t)kMaxColdWG * kH * 4);
-  alloc((void**)&s->n_part, 64);
+  alloc((void**)&s->cold_part, (size_t)kMaxColdWG * kH * 4);
+  alloc((void**)&s->cold_total, 64);
   alloc((void**)&s->z, (size_t)(s->max_rank + 64) * 4);
   alloc((void**)&s->sel_counts, (size_t)n_layers * s->n_chunks * 4);
   alloc((void**)&s->sel_slots, sel * 4);
@@ -313,6 +331,15 @@ int oi2_stack_decode(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, void* 
   OI2_CHECK_HIP(ei);
   s->graphs.push_back({exec, x_in, x_out, st});
   OI2_CHECK_HIP(hipGraphLaunch(exec, st));
+  return OI2_OK;
+}
+
+int oi2_stack_set_expected_active(oi2_stack* s, int32_t expected) {
+  clear_error();
+  OI2_CHECK_ARG(s && expected >= 0, "bad argument");
+  s->cold_wg = cold_wg_for(expected > 0 ? expected : s->cold_cap);
+  for (auto& g : s->graphs) (void)hipGraphExecDestroy(g.exec);
+  s->graphs.clear();
   return OI2_OK;
 }
 

@@ -37,7 +37,7 @@ class Cold(Structure):
 
 class Active(Structure):
     _fields_ = [("slots", c_void_p), ("counts", c_void_p), ("n_chunks", c_int32),
-                ("chunk", c_int32)]
+                ("chunk", c_int32), ("expected", c_int32)]
 
 
 class Predictor(Structure):
@@ -57,7 +57,7 @@ _SIGS = {
     "oi2_dequant_records": (c_int32, [c_void_p, c_int32, c_void_p, c_int32, c_void_p, c_void_p,
                                       c_void_p, c_void_p]),
     "oi2_rmsnorm": (c_int32, [c_void_p, c_void_p, c_int32, c_float, c_void_p, c_void_p]),
-    "oi2_ffn_workspace_bytes": (c_size_t, [c_int32, c_int32]),
+    "oi2_ffn_workspace_bytes": (c_size_t, [c_int32, c_int32, c_int32]),
     "oi2_ffn_forward": (c_int32, [c_void_p, c_int32, c_void_p, c_float, POINTER(Hot), POINTER(Cold),
                                   POINTER(Active), c_int32, c_int32, c_int32, c_void_p, c_void_p,
                                   c_void_p, c_size_t, c_void_p]),
@@ -71,6 +71,7 @@ _SIGS = {
                                    c_float, POINTER(c_void_p)]),
     "oi2_stack_decode": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p]),
     "oi2_stack_set_graph": (c_int32, [c_void_p, c_int32]),
+    "oi2_stack_set_expected_active": (c_int32, [c_void_p, c_int32]),
     "oi2_stack_profile": (c_int32, [c_void_p, c_void_p, c_void_p, POINTER(c_float),
                                     POINTER(c_float), c_void_p]),
     "oi2_stack_trace": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),

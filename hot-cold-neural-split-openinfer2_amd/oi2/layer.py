@@ -34,7 +34,8 @@ class ColdNeurons:
 
     def __init__(self, section: ColdSection | None, slots: torch.Tensor | None,
                  counts: torch.Tensor | None, n_chunks: int, chunk: int, ids=None,
-                 gate_bias: torch.Tensor | None = None):
+                 gate_bias: torch.Tensor | None = None, expected: int = 0):
+        self.expected = expected
         self.section = section
         self.slots = slots
         self.counts = counts
@@ -71,7 +72,10 @@ class ColdNeurons:
             return None, None
         return (self.section.struct(self.gate_bias),
                 _lib.Active(self.slots.data_ptr(), self.counts.data_ptr(), self.n_chunks,
-                            self.chunk))
+                            self.chunk, self.expected))
+
+    def capacity(self) -> int:
+        return 0 if self.empty() else self.n_chunks * self.chunk
 
     def count(self) -> int:
         """Number of active records (synchronises with the device)."""
@@ -115,7 +119,7 @@ def _ffn(x2d, norm_w, eps, hot: HotWeights | None, cold: ColdNeurons | None, act
     hot_s = hot.struct() if hot is not None and hot.n_hot > 0 else None
     cold_s, act_s = cold.structs() if cold is not None else (None, None)
     n_hot = hot.n_hot if hot_s is not None else 0
-    ws_bytes = L.oi2_ffn_workspace_bytes(B, n_hot)
+    ws_bytes = L.oi2_ffn_workspace_bytes(B, n_hot, cold.capacity() if cold is not None else 0)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     out = torch.empty_like(x2d)
     y32 = torch.empty((B, HIDDEN), dtype=torch.float32, device=dev) if want_y32 else None

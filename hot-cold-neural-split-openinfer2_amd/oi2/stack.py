@@ -49,6 +49,10 @@ class DecodeStack:
         self._h = h
         _lib.check(L.oi2_stack_set_graph(h, int(bool(use_graph))))
 
+    def set_expected_active(self, n: int):
+        """Size the cold pass for about n active records per layer."""
+        _lib.check(_lib.lib().oi2_stack_set_expected_active(self._h, int(n)))
+
     def decode(self, x_in: torch.Tensor, x_out: torch.Tensor, stream=None):
         """x_out (H) fp16 = the token after every FFN layer."""
         s = stream.cuda_stream if stream is not None else _lib.stream_handle(x_in.device)

@@ -77,6 +77,9 @@ typedef struct oi2_active {
   const int32_t* counts;
   int32_t n_chunks;           /* 1..256 */
   int32_t chunk;
+  int32_t expected;           /* expected active count sizing the launch
+                                 (0: the capacity n_chunks * chunk); any
+                                 count up to the capacity is handled */
 } oi2_active;
 
 /* NeuronPredictor weights (predictor.py:55-75): sigmoid(up(down(x))). */
@@ -110,8 +113,9 @@ int oi2_rmsnorm(const uint16_t* x, const uint16_t* w, int32_t rows, float eps,
                 uint16_t* out, void* stream);
 
 /* ---- FFN ---------------------------------------------------------------- */
-/* Workspace bytes for oi2_ffn_forward at this batch / hot size. */
-size_t oi2_ffn_workspace_bytes(int32_t batch, int32_t n_hot);
+/* Workspace bytes for oi2_ffn_forward at this batch / hot size and an active
+ * list of capacity cold_capacity (n_chunks * chunk). */
+size_t oi2_ffn_workspace_bytes(int32_t batch, int32_t n_hot, int32_t cold_capacity);
 
 /* sparse_ffn (engine.py:173-209) and SparseFFNLayer.forward
  * (engine.py:292-312) for `batch` tokens sharing one active cold set:
@@ -178,6 +182,10 @@ int oi2_stack_create(const oi2_layer* layers, int32_t n_layers, int32_t inter, f
                      oi2_stack** out);
 /* One token through all layers: x_out (H) fp16 from x_in (H) fp16. */
 int oi2_stack_decode(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, void* stream);
+/* Size the cold gather launch for about `expected` active cold records per
+ * layer (any count up to the capacity is still processed; this only sets how
+ * many workgroups the pass uses).  0 restores the capacity. */
+int oi2_stack_set_expected_active(oi2_stack* s, int32_t expected);
 /* Replay the launch sequence through a captured hipGraph (default 1) or launch
  * it directly (0).  Graphs are never used on the NULL stream. */
 int oi2_stack_set_graph(oi2_stack* s, int32_t enable);

@@ -28,6 +28,7 @@ def stack4():
     thr = calibrate_threshold(layers, g, 0.05)
     st = DecodeStack([StackLayer(l.hot, l.records, l.lut, l.norm_w, l.predictor) for l in layers],
                      inter, EPS, "silu", False, thr)
+    st.set_expected_active(300)     # below the real ~540: cold waves loop over extra items
     return dev, g, layers, st, thr
 
 
@@ -88,13 +89,22 @@ def test_graph_replay_is_deterministic(stack4):
             _ = (x_out.float() * 2).sum()          # eager work between replays
         stream.synchronize()
         outs.append(x_out.clone())
+    # the cold partial-sum grouping follows the workgroup count: same setting,
+    # same bits; another setting, the same result within rounding
     direct = DecodeStack(st.layers, st.inter, EPS, "silu", False, thr, use_graph=False)
+    direct.set_expected_active(300)
     x_d = torch.empty_like(x_in)
     direct.decode(x_in, x_d, None)
+    other = DecodeStack(st.layers, st.inter, EPS, "silu", False, thr, use_graph=False)
+    x_o = torch.empty_like(x_in)
+    other.decode(x_in, x_o, None)
     torch.cuda.synchronize()
     for o in outs[1:]:
         assert torch.equal(o, outs[0])
     assert torch.equal(outs[0], x_d)
+    assert_ffn_close(x_o.double().cpu().numpy(), x_d.double().cpu().numpy(), tol=2e-3,
+                     cos_min=0.99999, what="other grouping")
+    other.close()
     up, down = direct.profile(x_in, x_d)
     assert len(up) == 4 and all(t > 0 for t in up + down)
     direct.close()

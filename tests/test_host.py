@@ -46,7 +46,7 @@ def test_argument_validation_without_gpu():
     import ctypes
     rc = lib.oi2_predict(1, 1, ctypes.byref(p), 0.0, None, None, None, None, 0, None)
     assert rc == 1 and b"rank" in lib.oi2_last_error()
-    assert lib.oi2_ffn_workspace_bytes(1, 3584) >= (3584 + 64 * 4096) * 4
+    assert lib.oi2_ffn_workspace_bytes(1, 3584, 14336) >= (3584 + 2 * 14336 + 2048) * 4
 
 
 def test_compute_entry_points_fail_loudly_without_gpu():
