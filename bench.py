@@ -11,9 +11,10 @@ Weights are N(0, 0.02) from a fixed seed (synthetic data, nothing loaded).
 
 Prints one JSON line.  `value` is tokens/s with every input already in HBM.
 `roofline` is the ffn_up kernel (hot gate/up + cold gather/dequant/act/down +
-lookahead predictor projection), timed per launch with hipEvents on its
-stream; `cpu_baseline` is the restated reference CPU path (per-neuron
-record decode loop + F.linear FFN) on a bounded sample of the same token.
+lookahead predictor projection): its mean duration comes from every layer's
+ffn_up launched back to back between two hipEvents on the launch stream;
+`cpu_baseline` is the restated reference CPU path (per-neuron record decode
+loop + F.linear FFN) over a few recorded tokens, bounded to ~20 s.
 """
 import argparse
 import json
@@ -31,6 +32,10 @@ H, INTER, N_LAYERS, N_HOT, RANK = 4096, 14336, 32, 3584, 64
 ACTIVE_FRAC = 0.05
 EPS = 1e-5
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per k_ffn_up launch on this workload, from rocprofv3 --pmc runs:
+# FETCH_SIZE 16593.7 KiB x 2.000 + WRITE_SIZE 2103.6 KiB x 1.000, the factors
+# being what each counter reads for a plain 256 MiB copy (--copy-calibration)
+UP_TRAFFIC_BYTES = (16593.7 * 2.0 + 2103.6) * 1024
 
 
 def log(msg):
@@ -69,39 +74,55 @@ def down_launch_bytes(active_next):
             + 2 * H * 2 + active_next * 8)
 
 
-def cpu_baseline(layers, xs_in, active_ids, n_sample, dev):
-    """Restated reference CPU path over the first n_sample layers of one token."""
-    import numpy as np
+def _hot_dense_cpu(hot):
+    import torch
+    gate = (hot.gate_q.view(torch.float8_e4m3fn).float() * hot.gate_scale[:, None]).cpu()
+    up = (hot.up_q.view(torch.float8_e4m3fn).float() * hot.up_scale[:, None]).cpu()
+    down = (hot.down_q[:, :hot.n_hot].contiguous().view(torch.float8_e4m3fn).float()
+            * hot.down_scale[:, None]).cpu()
+    return gate, up, down
+
+
+def cpu_baseline(layers, tokens, max_seconds):
+    """The restated reference CPU path (oracle.baseline_cpu) over the recorded
+    tokens, layer by layer, until max_seconds of timed CPU work.
+
+    tokens: list of (xs_in (32 fp16 layer inputs), active cold ids per layer)."""
     import torch
     from oracle import baseline_cpu as B
-    samples = []
-    for L in range(n_sample):
+    secs = cold_secs = 0.0
+    neurons = n_steps = 0
+    for L in range(N_LAYERS):
+        if secs >= max_seconds:
+            break
         lay = layers[L]
-        recs = lay.records.cpu().numpy()
-        buf = memoryview(recs.reshape(-1))
-        nids = lay.cold_ids.cpu().numpy()
-        offs = {int(n): int(k) * 6400 for k, n in enumerate(nids)}
-        hot = lay.hot
-        gate = (hot.gate_q.view(torch.float8_e4m3fn).float() * hot.gate_scale[:, None]).cpu()
-        up = (hot.up_q.view(torch.float8_e4m3fn).float() * hot.up_scale[:, None]).cpu()
-        down = (hot.down_q[:, :hot.n_hot].contiguous().view(torch.float8_e4m3fn).float()
-                * hot.down_scale[:, None]).cpu()
-        x = xs_in[L].float().cpu()[None]
-        xn = x * torch.rsqrt((x * x).mean(-1, keepdim=True) + EPS) * lay.norm_w.float().cpu()
-        samples.append((xn, (gate, up, down), buf, offs, active_ids[L]))
-    secs, neurons, nbytes = B.time_layers(samples, threads=1)
-    per_layer = secs / n_sample
+        buf = memoryview(lay.records.cpu().numpy().reshape(-1))
+        offs = {int(n): k * 6400 for k, n in enumerate(lay.cold_ids.cpu().tolist())}
+        hot = _hot_dense_cpu(lay.hot)
+        w = lay.norm_w.float().cpu()
+        samples = []
+        for xs_in, active in tokens:
+            x = xs_in[L].float().cpu()[None]
+            xn = x * torch.rsqrt((x * x).mean(-1, keepdim=True) + EPS) * w
+            samples.append((xn, hot, buf, offs, active[L]))
+        dt, dc, nn = B.time_layers(samples, threads=1)
+        secs += dt
+        cold_secs += dc
+        neurons += nn
+        n_steps += len(samples)
+    per_layer = secs / n_steps
     return {
         "value": 1.0 / (per_layer * N_LAYERS),
         "unit": "tok/s",
         "cores": 1,
         "kind": "port",
-        "sample": (f"{n_sample} of 32 layers of one token ({neurons} cold neurons, "
-                   f"{nbytes / 1e6:.1f} MB of records) through the restated reference CPU path "
-                   f"(per-neuron bytes/frombuffer/dequantize_int4 loop + fp32 F.linear FFN), "
-                   f"1 torch thread, {secs:.1f} s; scaled to 32 layers"),
-        "cold_neurons_per_s": neurons / secs,
+        "sample": (f"{n_steps} layer-steps ({len(tokens)} tokens x {n_steps // len(tokens)} of 32 "
+                   f"layers, {neurons} cold neurons) through the restated reference CPU path "
+                   f"(per-neuron bytes/frombuffer/dequantize_int4 record loop + fp32 F.linear "
+                   f"hot and cold FFN), 1 torch thread, {secs:.1f} s timed; scaled to 32 layers"),
         "seconds": secs,
+        "cold_seconds": cold_secs,
+        "cold_neurons_per_s": neurons / cold_secs,
     }
 
 
@@ -111,9 +132,13 @@ def main():
     ap.add_argument("--steps", type=int, default=256)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--profile-tokens", type=int, default=8)
-    ap.add_argument("--cpu-sample-layers", type=int, default=16)
+    ap.add_argument("--profile-reps", type=int, default=8)
+    ap.add_argument("--cpu-tokens", type=int, default=6)
+    ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 256 MiB device copy 8 times (the reference kernel "
+                         "for scaling FETCH_SIZE / WRITE_SIZE counter readings) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
@@ -124,6 +149,14 @@ def main():
     import oi2  # noqa: F401
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.copy_calibration:
+        src = torch.ones(64 << 20, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(8):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copied {src.numel() * 4} bytes 8 times")
+        return
     t0 = time.time()
     layers, st, thr, g = build_stack(args.seed, dev)
     torch.cuda.synchronize()
@@ -157,43 +190,42 @@ def main():
     tok_s = args.steps / secs
     log(f"timed {args.steps} tokens: {secs * 1e3:.2f} ms ({tok_s:.1f} tok/s)")
 
-    # per-launch kernel timing with hipEvents on the launch stream
-    up_t, down_t, up_b, down_b, act_counts = [], [], [], [], []
-    x_last_in = None
+    # mean kernel durations: every layer's ffn_up launched back to back between
+    # two hipEvents on the launch stream, then every layer's ffn_down
     k = base + args.steps
-    for p in range(args.profile_tokens):
-        xi, xo = bufs[(k + p) % 2], bufs[(k + p + 1) % 2]
-        x_last_in = xi.clone()
-        with torch.cuda.stream(stream):
-            u, d = st.profile(xi, xo, stream)
-        xs, counts, slots, ids = st.trace()
-        torch.cuda.synchronize()
-        c = counts.sum(1).cpu().tolist()
-        act_counts.append(c)
-        for L in range(N_LAYERS):
-            up_t.append(u[L])
-            down_t.append(d[L])
-            up_b.append(up_launch_bytes(c[L]))
-            down_b.append(down_launch_bytes(c[L + 1] if L + 1 < N_LAYERS else 0))
-    up_ms = sum(up_t) / len(up_t)
-    down_ms = sum(down_t) / len(down_t)
-    up_gbs = sum(up_b) / (sum(up_t) / 1e3) / 1e9
-    down_gbs = sum(down_b) / (sum(down_t) / 1e3) / 1e9
-    mean_active = sum(sum(c) for c in act_counts) / (len(act_counts) * N_LAYERS)
-    token_bytes = sum(up_b) / args.profile_tokens + sum(down_b) / args.profile_tokens
-    log(f"ffn_up {up_ms * 1e3:.2f} us/launch {up_gbs:.0f} GB/s; ffn_down {down_ms * 1e3:.2f} us "
+    xi, xo = bufs[k % 2], bufs[(k + 1) % 2]
+    with torch.cuda.stream(stream):
+        up_us, down_us = st.profile(xi, xo, stream, reps=args.profile_reps)
+    xs, counts, slots, ids = st.trace()
+    torch.cuda.synchronize()
+    c = counts.sum(1).cpu().tolist()
+    up_b = sum(up_launch_bytes(c[L]) for L in range(N_LAYERS)) / N_LAYERS
+    down_b = sum(down_launch_bytes(c[L + 1] if L + 1 < N_LAYERS else 0)
+                 for L in range(N_LAYERS)) / N_LAYERS
+    up_gbs = up_b / (up_us * 1e-6) / 1e9
+    down_gbs = down_b / (down_us * 1e-6) / 1e9
+    mean_active = sum(c) / N_LAYERS
+    token_bytes = N_LAYERS * (up_b + down_b)
+    log(f"ffn_up {up_us:.2f} us/launch {up_gbs:.0f} GB/s; ffn_down {down_us:.2f} us "
         f"{down_gbs:.0f} GB/s; mean active cold {mean_active:.0f}")
 
     cpu = None
-    if not args.no_cpu_baseline and args.cpu_sample_layers > 0:
-        xs, counts, slots, ids = st.trace()
-        torch.cuda.synchronize()
-        xs_in = [x_last_in] + [xs[i] for i in range(N_LAYERS - 1)]
-        active = [st.active_ids(L, counts, ids) for L in range(N_LAYERS)]
-        # cold ids -> the restated loop looks them up by neuron id
-        n = min(args.cpu_sample_layers, N_LAYERS)
-        cpu = cpu_baseline(layers, xs_in, active, n, dev)
-        log(f"cpu baseline {cpu['value']:.4f} tok/s over {cpu['seconds']:.1f}s")
+    if not args.no_cpu_baseline and args.cpu_tokens > 0:
+        tokens = []
+        x = xi.clone()
+        y = torch.empty_like(x)
+        for t in range(args.cpu_tokens):
+            with torch.cuda.stream(stream):
+                st.decode(x, y, stream)
+            stream.synchronize()
+            xs, counts, slots, ids = st.trace()
+            torch.cuda.synchronize()
+            xs_in = [x.clone()] + [xs[i].clone() for i in range(N_LAYERS - 1)]
+            tokens.append((xs_in, [st.active_ids(L, counts, ids) for L in range(N_LAYERS)]))
+            x, y = y.clone(), x
+        cpu = cpu_baseline(layers, tokens, args.cpu_seconds)
+        log(f"cpu baseline {cpu['value']:.4f} tok/s over {cpu['seconds']:.1f}s, "
+            f"{cpu['cold_neurons_per_s']:.0f} cold neurons/s")
 
     out = {
         "metric": "FFN decode tok/s (32L, 4096x14336, bs1); cold INT4 dequant GB/s vs HBM",
@@ -214,13 +246,13 @@ def main():
                    "batch": 1, "mean_active_cold": round(mean_active, 1),
                    "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "achieved": up_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": up_gbs / HBM_PEAK_GBS, "traffic": None,
-                     "kernel": "k_ffn_up", "us_per_launch": up_ms * 1e3,
-                     "bytes_per_launch": sum(up_b) / len(up_b)},
-        "kernels": {"k_ffn_down": {"us_per_launch": down_ms * 1e3, "achieved_gbs": down_gbs,
-                                   "bytes_per_launch": sum(down_b) / len(down_b)}},
+                     "frac": up_gbs / HBM_PEAK_GBS, "traffic": UP_TRAFFIC_BYTES,
+                     "kernel": "k_ffn_up", "us_per_launch": up_us, "bytes_per_launch": up_b},
+        "kernels": {"k_ffn_down": {"us_per_launch": down_us, "achieved_gbs": down_gbs,
+                                   "bytes_per_launch": down_b}},
         "token_bytes": token_bytes,
         "hbm_frac_end_to_end": token_bytes * tok_s / (HBM_PEAK_GBS * 1e9),
+        "cold_neurons_per_s": mean_active * N_LAYERS * tok_s,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -74,15 +74,6 @@ __device__ __forceinline__ void int4x8_to_f16x2x4(uint32_t d, f16x2 p[4]) {
   }
 }
 
-// x pairs matching int4x8_to_f16x2x4's output order for 8 consecutive elements.
-__device__ __forceinline__ void pack_x8(const float* x, f16x2 q[4]) {
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    q[k].x = (_Float16)x[k];
-    q[k].y = (_Float16)x[k + 4];
-  }
-}
-
 __device__ __forceinline__ float dot2(f16x2 a, f16x2 b, float c) {
   return __builtin_amdgcn_fdot2(a, b, c, false);
 }
@@ -119,22 +110,6 @@ __device__ __forceinline__ float wave_sum(float v) {
   v += dpp_f<0x142, 0xA>(v);  // row_bcast:15 into rows 1, 3
   v += dpp_f<0x143, 0xC>(v);  // row_bcast:31 into rows 2, 3
   return readlane_f(v, 63);
-}
-
-// Lane i receives lane i+1's value (DPP wave_shl:1); lane 63 receives `fill`.
-__device__ __forceinline__ uint32_t wave_shl1(uint32_t v, uint32_t fill) {
-  return (uint32_t)__builtin_amdgcn_update_dpp((int)fill, (int)v, 0x130, 0xF, 0xF, false);
-}
-
-// 16 bytes starting 2 bytes into aligned chunk `a`, completed by the first
-// two bytes of the next chunk (`next0` = that chunk's first dword).
-__device__ __forceinline__ u32x4 realign2(u32x4 a, uint32_t next0) {
-  u32x4 r;
-  r.x = __builtin_amdgcn_alignbyte(a.y, a.x, 2);
-  r.y = __builtin_amdgcn_alignbyte(a.z, a.y, 2);
-  r.z = __builtin_amdgcn_alignbyte(a.w, a.z, 2);
-  r.w = __builtin_amdgcn_alignbyte(next0, a.w, 2);
-  return r;
 }
 
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (kWave - 1)); }

@@ -58,10 +58,108 @@ namespace oi2 {
 
 int cold_wg_for(int expected);
 
-static int stack_launch(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, hipStream_t st,
-                        hipEvent_t* ev = nullptr) {
+// Launch arguments of layer L's two kernels.  x_in is the token entering the
+// stack and x_out the buffer that receives the last layer's output.
+static void layer_args(const oi2_stack* s, int L, const uint16_t* x_in, uint16_t* x_out,
+                       UpArgs& ua, DownArgs& da) {
   const int n = s->n_layers;
   const size_t sel_stride = (size_t)s->n_chunks * kSelChunk;
+  const StackLayer& SL = s->layers[L];
+  const oi2_layer& l = SL.l;
+  const bool pred_next = (L + 1 < n) && s->layers[L + 1].has_pred;
+  const uint16_t* xl = (L == 0) ? x_in : s->xbuf + (size_t)(L - 1) * kH;
+
+  ua = UpArgs{};
+  ua.tok = TokenIn{xl, s->xw, s->ssq, s->eps, 1};
+  ua.relu = s->relu;
+  ua.both = s->both;
+  ua.n_hot = l.hot.n_hot;
+  ua.gate_q = l.hot.gate_q;
+  ua.up_q = l.hot.up_q;
+  ua.gate_s = l.hot.gate_scale;
+  ua.up_s = l.hot.up_scale;
+  ua.hot_gbias = l.hot.gate_bias;
+  ua.h_hot = s->h_hot;
+  const bool has_cold = l.cold.n_records > 0;
+  if (has_cold) {
+    ua.records = l.cold.records;
+    ua.n_records = l.cold.n_records;
+    ua.cold_gbias = l.cold.gate_bias;
+    if (SL.has_pred)
+      ua.act = ActiveList{s->sel_slots + (size_t)L * sel_stride,
+                          s->sel_counts + (size_t)L * s->n_chunks, s->n_chunks, kSelChunk};
+    else
+      ua.act = ActiveList{SL.all_slots, SL.all_count, 1, SL.n_all};
+    ua.cold_part = s->cold_part;
+    ua.cold_total = s->cold_total;
+    ua.cold_cap = s->cold_cap;
+  }
+  ua.wg_cold = has_cold ? (SL.has_pred ? s->cold_wg : cold_wg_for(SL.n_all)) : 0;
+  ua.wg_hot = (l.hot.n_hot + 7) / 8;
+  if (pred_next) {
+    const oi2_layer& ln = s->layers[L + 1].l;
+    ua.pd_w = ln.pred.down_w;
+    ua.pd_rank = ln.pred.rank;
+    ua.pd_bf16 = ln.pred.dtype == OI2_DTYPE_BF16;
+    ua.pd_norm_w = ln.norm_w;
+    ua.pd_z = s->z;
+    ua.wg_pred = (ln.pred.rank + 3) / 4;
+  }
+
+  da = DownArgs{};
+  da.res = xl;
+  da.h_hot = s->h_hot;
+  da.n_hot = l.hot.n_hot;
+  da.down_stride = l.hot.down_stride;
+  da.down_q = l.hot.down_q;
+  da.down_s = l.hot.down_scale;
+  if (has_cold) {
+    da.cold_part = s->cold_part;
+    da.cold_total = s->cold_total;
+    da.cold_cap = s->cold_cap;
+    da.cold_wg = ua.wg_cold;
+  }
+  da.out = s->xbuf + (size_t)L * kH;
+  da.out2 = (L == n - 1) ? x_out : nullptr;
+  if (L + 1 < n) {
+    da.next_norm_w = s->layers[L + 1].l.norm_w;
+    da.xw_out = s->xw;
+    da.ssq_out = s->ssq;
+  }
+  if (pred_next) {
+    const oi2_layer& ln = s->layers[L + 1].l;
+    da.pu_w = ln.pred.up_w;
+    da.pu_b = ln.pred.up_b;
+    da.pu_rank = ln.pred.rank;
+    da.pu_bf16 = ln.pred.dtype == OI2_DTYPE_BF16;
+    da.inter = ln.pred.inter;
+    da.pd_z = s->z;
+    da.thr = s->thr;
+    da.lut = ln.lut;
+    da.sel_slots = s->sel_slots + (size_t)(L + 1) * sel_stride;
+    da.sel_ids = s->sel_ids + (size_t)(L + 1) * sel_stride;
+    da.sel_counts = s->sel_counts + (size_t)(L + 1) * s->n_chunks;
+    da.wg_pred = s->n_chunks;
+  }
+  da.wg_down = kDownWG;
+}
+
+static int launch_up(const UpArgs& ua, hipStream_t st) {
+  const int grid = ua.wg_cold + ua.wg_pred + ua.wg_hot;
+  if (grid > 0) {
+    hipLaunchKernelGGL(k_ffn_up, dim3(grid), dim3(kThreads), 0, st, ua);
+    OI2_CHECK_LAUNCH();
+  }
+  return OI2_OK;
+}
+
+static int launch_down(const DownArgs& da, hipStream_t st) {
+  hipLaunchKernelGGL(k_ffn_down, dim3(da.wg_pred + da.wg_down), dim3(kThreads), 0, st, da);
+  OI2_CHECK_LAUNCH();
+  return OI2_OK;
+}
+
+static int stack_launch(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, hipStream_t st) {
   hipLaunchKernelGGL(k_prep, dim3(1), dim3(kThreads), 0, st, x_in, s->layers[0].l.norm_w, s->xw,
                      s->ssq);
   OI2_CHECK_LAUNCH();
@@ -94,95 +192,13 @@ static int stack_launch(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, hip
     hipLaunchKernelGGL(k_pred_down, dim3(da.wg_pred), dim3(kThreads), 0, st, da);
     OI2_CHECK_LAUNCH();
   }
-  for (int L = 0; L < n; ++L) {
-    const StackLayer& SL = s->layers[L];
-    const oi2_layer& l = SL.l;
-    const bool pred_next = (L + 1 < n) && s->layers[L + 1].has_pred;
-    const uint16_t* xl = (L == 0) ? x_in : s->xbuf + (size_t)(L - 1) * kH;
-
-    UpArgs ua{};
-    ua.tok = TokenIn{xl, s->xw, s->ssq, s->eps, 1};
-    ua.relu = s->relu;
-    ua.both = s->both;
-    ua.n_hot = l.hot.n_hot;
-    ua.gate_q = l.hot.gate_q;
-    ua.up_q = l.hot.up_q;
-    ua.gate_s = l.hot.gate_scale;
-    ua.up_s = l.hot.up_scale;
-    ua.hot_gbias = l.hot.gate_bias;
-    ua.h_hot = s->h_hot;
-    const bool has_cold = l.cold.n_records > 0;
-    if (has_cold) {
-      ua.records = l.cold.records;
-      ua.n_records = l.cold.n_records;
-      ua.cold_gbias = l.cold.gate_bias;
-      if (SL.has_pred)
-        ua.act = ActiveList{s->sel_slots + (size_t)L * sel_stride,
-                            s->sel_counts + (size_t)L * s->n_chunks, s->n_chunks, kSelChunk};
-      else
-        ua.act = ActiveList{SL.all_slots, SL.all_count, 1, SL.n_all};
-      ua.cold_part = s->cold_part;
-      ua.cold_total = s->cold_total;
-      ua.cold_cap = s->cold_cap;
-    }
-    ua.wg_cold = has_cold ? (SL.has_pred ? s->cold_wg : cold_wg_for(SL.n_all)) : 0;
-    ua.wg_hot = (l.hot.n_hot + 7) / 8;
-    if (pred_next) {
-      const oi2_layer& ln = s->layers[L + 1].l;
-      ua.pd_w = ln.pred.down_w;
-      ua.pd_rank = ln.pred.rank;
-      ua.pd_bf16 = ln.pred.dtype == OI2_DTYPE_BF16;
-      ua.pd_norm_w = ln.norm_w;
-      ua.pd_z = s->z;
-      ua.wg_pred = (ln.pred.rank + 3) / 4;
-    }
-    const int grid_up = ua.wg_cold + ua.wg_pred + ua.wg_hot;
-    if (ev) OI2_CHECK_HIP(hipEventRecord(ev[3 * L], st));
-    if (grid_up > 0) {
-      hipLaunchKernelGGL(k_ffn_up, dim3(grid_up), dim3(kThreads), 0, st, ua);
-      OI2_CHECK_LAUNCH();
-    }
-    if (ev) OI2_CHECK_HIP(hipEventRecord(ev[3 * L + 1], st));
-
-    DownArgs da{};
-    da.res = xl;
-    da.h_hot = s->h_hot;
-    da.n_hot = l.hot.n_hot;
-    da.down_stride = l.hot.down_stride;
-    da.down_q = l.hot.down_q;
-    da.down_s = l.hot.down_scale;
-    if (has_cold) {
-      da.cold_part = s->cold_part;
-      da.cold_total = s->cold_total;
-      da.cold_cap = s->cold_cap;
-      da.cold_wg = ua.wg_cold;
-    }
-    da.out = s->xbuf + (size_t)L * kH;
-    da.out2 = (L == n - 1) ? x_out : nullptr;
-    if (L + 1 < n) {
-      da.next_norm_w = s->layers[L + 1].l.norm_w;
-      da.xw_out = s->xw;
-      da.ssq_out = s->ssq;
-    }
-    if (pred_next) {
-      const oi2_layer& ln = s->layers[L + 1].l;
-      da.pu_w = ln.pred.up_w;
-      da.pu_b = ln.pred.up_b;
-      da.pu_rank = ln.pred.rank;
-      da.pu_bf16 = ln.pred.dtype == OI2_DTYPE_BF16;
-      da.inter = ln.pred.inter;
-      da.pd_z = s->z;
-      da.thr = s->thr;
-      da.lut = ln.lut;
-      da.sel_slots = s->sel_slots + (size_t)(L + 1) * sel_stride;
-      da.sel_ids = s->sel_ids + (size_t)(L + 1) * sel_stride;
-      da.sel_counts = s->sel_counts + (size_t)(L + 1) * s->n_chunks;
-      da.wg_pred = s->n_chunks;
-    }
-    da.wg_down = kDownWG;
-    hipLaunchKernelGGL(k_ffn_down, dim3(da.wg_pred + da.wg_down), dim3(kThreads), 0, st, da);
-    OI2_CHECK_LAUNCH();
-    if (ev) OI2_CHECK_HIP(hipEventRecord(ev[3 * L + 2], st));
+  for (int L = 0; L < s->n_layers; ++L) {
+    UpArgs ua;
+    DownArgs da;
+    layer_args(s, L, x_in, x_out, ua, da);
+    int rc = launch_up(ua, st);
+    if (rc == OI2_OK) rc = launch_down(da, st);
+    if (rc) return rc;
   }
   return OI2_OK;
 }
@@ -350,31 +366,49 @@ int oi2_stack_set_graph(oi2_stack* s, int32_t enable) {
   return OI2_OK;
 }
 
-int oi2_stack_profile(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, float* up_ms,
-                      float* down_ms, void* stream) {
+int oi2_stack_profile(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, int32_t reps,
+                      float* up_us, float* down_us, void* stream) {
   clear_error();
-  OI2_CHECK_ARG(s && x_in && x_out && up_ms && down_ms, "null argument");
+  OI2_CHECK_ARG(s && x_in && x_out && up_us && down_us, "null argument");
+  OI2_CHECK_ARG(reps > 0 && reps <= 1024, "reps %d out of range", reps);
   hipStream_t st = (hipStream_t)stream;
-  std::vector<hipEvent_t> ev(3 * (size_t)s->n_layers, nullptr);
+  hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
   int rc = OI2_OK;
-  for (auto& e : ev) {
-    if (hipEventCreate(&e) != hipSuccess) {
+  for (auto& e : ev)
+    if (rc == OI2_OK && hipEventCreate(&e) != hipSuccess) {
       set_error("hipEventCreate failed");
       rc = OI2_EHIP;
-      break;
     }
-  }
-  if (rc == OI2_OK) rc = stack_launch(s, x_in, x_out, st, ev.data());
+  // one real token fixes every layer's active set; then every layer's ffn_up
+  // back to back, reps times, then every layer's ffn_down the same way
+  if (rc == OI2_OK) rc = stack_launch(s, x_in, x_out, st);
+  std::vector<UpArgs> ua(s->n_layers);
+  std::vector<DownArgs> da(s->n_layers);
+  for (int L = 0; L < s->n_layers; ++L) layer_args(s, L, x_in, x_out, ua[L], da[L]);
+  if (rc == OI2_OK && hipEventRecord(ev[0], st) != hipSuccess) rc = OI2_EHIP;
+  for (int r = 0; rc == OI2_OK && r < reps; ++r)
+    for (int L = 0; rc == OI2_OK && L < s->n_layers; ++L) rc = launch_up(ua[L], st);
+  if (rc == OI2_OK && hipEventRecord(ev[1], st) != hipSuccess) rc = OI2_EHIP;
+  for (int r = 0; rc == OI2_OK && r < reps; ++r)
+    for (int L = 0; rc == OI2_OK && L < s->n_layers; ++L) rc = launch_down(da[L], st);
+  if (rc == OI2_OK && hipEventRecord(ev[2], st) != hipSuccess) rc = OI2_EHIP;
+  // the timing launches overwrite the selections: run the token again so the
+  // stack's state (and x_out) is that of x_in
+  if (rc == OI2_OK) rc = stack_launch(s, x_in, x_out, st);
   if (rc == OI2_OK && hipStreamSynchronize(st) != hipSuccess) {
     set_error("hipStreamSynchronize failed");
     rc = OI2_EHIP;
   }
-  for (int L = 0; rc == OI2_OK && L < s->n_layers; ++L) {
-    if (hipEventElapsedTime(&up_ms[L], ev[3 * L], ev[3 * L + 1]) != hipSuccess ||
-        hipEventElapsedTime(&down_ms[L], ev[3 * L + 1], ev[3 * L + 2]) != hipSuccess) {
-      set_error("hipEventElapsedTime failed");
-      rc = OI2_EHIP;
-    }
+  float t_up = 0.0f, t_down = 0.0f;
+  if (rc == OI2_OK && (hipEventElapsedTime(&t_up, ev[0], ev[1]) != hipSuccess ||
+                       hipEventElapsedTime(&t_down, ev[1], ev[2]) != hipSuccess)) {
+    set_error("hipEventElapsedTime failed");
+    rc = OI2_EHIP;
+  }
+  if (rc == OI2_OK) {
+    const double n = (double)reps * s->n_layers;
+    *up_us = (float)(t_up * 1e3 / n);
+    *down_us = (float)(t_down * 1e3 / n);
   }
   for (auto& e : ev)
     if (e) (void)hipEventDestroy(e);

@@ -72,7 +72,7 @@ _SIGS = {
     "oi2_stack_decode": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p]),
     "oi2_stack_set_graph": (c_int32, [c_void_p, c_int32]),
     "oi2_stack_set_expected_active": (c_int32, [c_void_p, c_int32]),
-    "oi2_stack_profile": (c_int32, [c_void_p, c_void_p, c_void_p, POINTER(c_float),
+    "oi2_stack_profile": (c_int32, [c_void_p, c_void_p, c_void_p, c_int32, POINTER(c_float),
                                     POINTER(c_float), c_void_p]),
     "oi2_stack_trace": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "oi2_stack_destroy": (c_int32, [c_void_p]),

@@ -58,15 +58,15 @@ class DecodeStack:
         s = stream.cuda_stream if stream is not None else _lib.stream_handle(x_in.device)
         _lib.check(_lib.lib().oi2_stack_decode(self._h, x_in.data_ptr(), x_out.data_ptr(), s or None))
 
-    def profile(self, x_in: torch.Tensor, x_out: torch.Tensor, stream=None):
-        """Per-layer (ffn_up ms, ffn_down ms) from hipEvents on the launch stream."""
-        n = self.n_layers
-        up = (ctypes.c_float * n)()
-        down = (ctypes.c_float * n)()
+    def profile(self, x_in: torch.Tensor, x_out: torch.Tensor, stream=None, reps: int = 8):
+        """Mean (ffn_up us, ffn_down us) per launch: every layer's kernel
+        launched back to back `reps` times between two hipEvents on the launch
+        stream.  Leaves the stack in the state of decoding x_in."""
+        up, down = ctypes.c_float(), ctypes.c_float()
         s = stream.cuda_stream if stream is not None else _lib.stream_handle(x_in.device)
-        _lib.check(_lib.lib().oi2_stack_profile(self._h, x_in.data_ptr(), x_out.data_ptr(), up, down,
-                                                s or None))
-        return list(up), list(down)
+        _lib.check(_lib.lib().oi2_stack_profile(self._h, x_in.data_ptr(), x_out.data_ptr(), int(reps),
+                                                ctypes.byref(up), ctypes.byref(down), s or None))
+        return up.value, down.value
 
     def trace(self):
         """(xs (n_layers, H) fp16 layer outputs, counts (n_layers, n_chunks),

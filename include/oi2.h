@@ -189,15 +189,17 @@ int oi2_stack_set_expected_active(oi2_stack* s, int32_t expected);
 /* Replay the launch sequence through a captured hipGraph (default 1) or launch
  * it directly (0).  Graphs are never used on the NULL stream. */
 int oi2_stack_set_graph(oi2_stack* s, int32_t enable);
-/* Per-layer inputs x_L (n_layers, H) fp16 and active sets of the last
+/* Average kernel durations on the decode path.  Decodes x_in once (fixing
+ * every layer's active set), then launches every layer's ffn_up kernel back
+ * to back `reps` times between two hipEvents on `stream`, then every layer's
+ * ffn_down the same way, then decodes x_in again so the stack's state and
+ * x_out are those of x_in.  Waits for the stream and writes the mean
+ * microseconds per ffn_up launch and per ffn_down launch. */
+int oi2_stack_profile(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, int32_t reps,
+                      float* up_us, float* down_us, void* stream);
+/* Each layer's output (n_layers, H) fp16 and the active sets of the last
  * decode: counts (n_layers, n_chunks) and slots/ids (n_layers, n_chunks*256),
  * copied to device buffers supplied by the caller (any may be NULL). */
-/* One token like oi2_stack_decode, launched directly with a hipEvent
- * recorded around every layer's two launches; waits for the stream and
- * writes each layer's ffn_up and ffn_down durations (n_layers floats each,
- * milliseconds). */
-int oi2_stack_profile(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, float* up_ms,
-                      float* down_ms, void* stream);
 int oi2_stack_trace(oi2_stack* s, uint16_t* xs, int32_t* counts, int32_t* slots, int32_t* ids,
                     void* stream);
 int oi2_stack_destroy(oi2_stack* s);
