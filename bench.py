@@ -126,6 +126,72 @@ def cpu_baseline(layers, tokens, max_seconds):
     }
 
 
+def measure_staging(layers, st, thr, x0, stream, steps, mean_active):
+    """The same 32-layer decode with every layer's cold records in pinned host
+    memory: each layer's active records are copied over PCIe on a side stream
+    while the previous layer computes.  Reports tok/s, the copy's rate, and a
+    plain pinned host-to-device copy as the link reference."""
+    import torch
+    from oi2.stack import DecodeStack, StackLayer
+    t0 = time.time()
+    pinned = [l.records.cpu().pin_memory() for l in layers]
+    sst = DecodeStack([StackLayer(l.hot, p, l.lut, l.norm_w, l.predictor)
+                       for l, p in zip(layers, pinned)], INTER, EPS, "silu", False, thr,
+                      staging=16)
+    sst.set_expected_active(int(1.3 * ACTIVE_FRAC * (INTER - N_HOT)))
+    log(f"pinned host store {sum(p.numel() for p in pinned) / 1e9:.2f} GB in {time.time() - t0:.1f}s")
+    bufs = [x0.clone(), torch.empty_like(x0)]
+    with torch.cuda.stream(stream):
+        for i in range(8):
+            sst.decode(bufs[i % 2], bufs[(i + 1) % 2], stream)
+    stream.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t_start = time.perf_counter()
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        for i in range(steps):
+            sst.decode(bufs[i % 2], bufs[(i + 1) % 2], stream)
+        e1.record(stream)
+    stream.synchronize()
+    secs = max(time.perf_counter() - t_start, e0.elapsed_time(e1) / 1e3)
+    with torch.cuda.stream(stream):
+        gather_us = sst.profile_staging(bufs[0], bufs[1], stream, reps=2)
+    _, counts, _, _ = sst.trace()
+    torch.cuda.synchronize()
+    active = counts.sum(1).float().mean().item()
+    # link reference: one 256 MiB pinned host -> device copy
+    src = torch.empty(256 << 20, dtype=torch.uint8).pin_memory()
+    dst = torch.empty(256 << 20, dtype=torch.uint8, device=x0.device)
+    dst.copy_(src, non_blocking=True)
+    torch.cuda.synchronize()
+    c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    c0.record()
+    for _ in range(4):
+        dst.copy_(src, non_blocking=True)
+    c1.record()
+    torch.cuda.synchronize()
+    h2d_gbs = 4 * src.numel() / (c0.elapsed_time(c1) / 1e3) / 1e9
+    gather_gbs = active * 6400 / (gather_us * 1e-6) / 1e9
+    tok_s = steps / secs
+    out = {
+        "tok_s": tok_s,
+        "steps": steps,
+        "store": "pinned host memory (hipHostMalloc via torch pin_memory), 32 x 68.8 MB",
+        "copy_us_per_layer": gather_us,
+        "copy_gbs": gather_gbs,
+        "h2d_bytes_per_token": N_LAYERS * active * 6400,
+        "h2d_gbs_end_to_end": N_LAYERS * active * 6400 * tok_s / 1e9,
+        "h2d_link_gbs_pinned_memcpy": h2d_gbs,
+        "pcie_bound_tok_s": h2d_gbs * 1e9 / (N_LAYERS * active * 6400),
+        "mean_active_cold": active,
+    }
+    log(f"staged: {tok_s:.1f} tok/s; copy {gather_us:.1f} us/layer ({gather_gbs:.1f} GB/s); "
+        f"pinned memcpy {h2d_gbs:.1f} GB/s")
+    sst.close()
+    del pinned
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -134,6 +200,8 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--profile-reps", type=int, default=8)
     ap.add_argument("--cpu-tokens", type=int, default=6)
+    ap.add_argument("--staging-steps", type=int, default=64,
+                    help="tokens timed with the cold store in pinned host memory (0: skip)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -209,6 +277,10 @@ def main():
     log(f"ffn_up {up_us:.2f} us/launch {up_gbs:.0f} GB/s; ffn_down {down_us:.2f} us "
         f"{down_gbs:.0f} GB/s; mean active cold {mean_active:.0f}")
 
+    staging = None
+    if args.staging_steps > 0:
+        staging = measure_staging(layers, st, thr, xi, stream, args.staging_steps, mean_active)
+
     cpu = None
     if not args.no_cpu_baseline and args.cpu_tokens > 0:
         tokens = []
@@ -254,6 +326,7 @@ def main():
         "hbm_frac_end_to_end": token_bytes * tok_s / (HBM_PEAK_GBS * 1e9),
         "cold_neurons_per_s": mean_active * N_LAYERS * tok_s,
         "cpu_baseline": cpu,
+        "staging": staging,
     }
     print(json.dumps(out), flush=True)
     st.close()

@@ -128,8 +128,9 @@ __device__ __forceinline__ int wave_chunk_prefix(const ActiveList& al, int excl[
   return total;
 }
 
-// Record slot of active item i (0 <= i < total), wave-uniform.
-__device__ __forceinline__ int item_slot(const ActiveList& al, const int excl[4], int i) {
+// Position (chunk * chunk_size + index in chunk) of active item i
+// (0 <= i < total) in the chunked list, wave-uniform.
+__device__ __forceinline__ int item_pos(const ActiveList& al, const int excl[4], int i) {
   const int lane = lane_id();
   int c = -1;
 #pragma unroll
@@ -140,7 +141,14 @@ __device__ __forceinline__ int item_slot(const ActiveList& al, const int excl[4]
   const int sel = c >> 6;
   const int e = sel == 0 ? excl[0] : sel == 1 ? excl[1] : sel == 2 ? excl[2] : excl[3];
   const int base = __shfl(e, c & 63, kWave);
-  return al.slots[(size_t)c * al.chunk + (i - base)];
+  return c * al.chunk + (i - base);
+}
+
+// Record slot of active item i; a list without slots maps position p to
+// record p (records staged in list order).
+__device__ __forceinline__ int item_slot(const ActiveList& al, const int excl[4], int i) {
+  const int p = item_pos(al, excl, i);
+  return al.slots ? al.slots[p] : p;
 }
 
 // Stage xw into LDS in natural order (hot rows) and/or, per 8 elements, as
@@ -656,6 +664,48 @@ __global__ __launch_bounds__(kThreads) void k_pred_down(DownArgs a) {
 }
 
 // ── standalone kernels ──────────────────────────────────────────────────────
+
+// Cold-record staging: copy every active record of one layer from its source
+// (HBM, or pinned host memory read over PCIe) to the staging buffer, record p
+// of the chunked list to dst + 6400 p, so the FFN reads the staged records
+// through a slot-less list.  One wave per record: 400 16-byte chunks, all
+// loads issued before the stores.  Invalid slots stage an all-zero record,
+// which contributes exactly zero to the FFN.
+//
+// The copy's loads wait on PCIe for microseconds; a CU that hosts one of its
+// waves serves the FFN's HBM loads behind them.  The kernel therefore holds
+// the whole 160 KB of its CU's LDS, so no FFN workgroup lands on a CU that
+// is copying.
+constexpr int kStageLdsWords = 160 * 1024 / 4;
+__global__ __launch_bounds__(kThreads) void k_stage_gather(StageArgs a) {
+  __shared__ uint32_t s_reserve[kStageLdsWords];
+  if (a.cap < 0) reinterpret_cast<volatile uint32_t*>(s_reserve)[threadIdx.x] = 0;  // never runs
+  int excl[4];
+  int total = wave_chunk_prefix(a.act, excl);
+  total = total < a.cap ? total : a.cap;
+  const int lane = lane_id();
+  const int n_waves = gridDim.x * (kThreads / kWave);
+  constexpr int kChunks = kRecBytes / 16;   // 400
+  for (int i = blockIdx.x * (kThreads / kWave) + (int)(threadIdx.x >> 6); i < total; i += n_waves) {
+    const int p = item_pos(a.act, excl, i);
+    const int slot = a.act.slots ? a.act.slots[p] : p;
+    const bool valid = slot >= 0 && slot < a.n_records;
+    const u32x4* src = reinterpret_cast<const u32x4*>(a.src + (size_t)(valid ? slot : 0) * kRecBytes);
+    u32x4* dst = reinterpret_cast<u32x4*>(a.dst + (size_t)p * kRecBytes);
+    u32x4 v[7];
+#pragma unroll
+    for (int it = 0; it < 7; ++it) {
+      const int c = lane + 64 * it;
+      v[it] = (valid && c < kChunks) ? __builtin_nontemporal_load(src + c) : u32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int it = 0; it < 7; ++it) {
+      const int c = lane + 64 * it;
+      if (c < kChunks) dst[c] = v[it];
+    }
+  }
+}
+
 
 // One workgroup per record: 384 16-byte payload chunks (gate 0-127, up
 // 128-255, down 256-383), 32 elements each, times the group's fp16 scale.

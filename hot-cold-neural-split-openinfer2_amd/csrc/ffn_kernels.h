@@ -12,6 +12,8 @@ constexpr int kMaxChunks = 256;
 constexpr int kColdPerWG = 4;                  // one cold record per wave
 constexpr int kMaxColdWG = 1024;
 
+// Active items in chunks: chunk c holds counts[c] items at slots[c * chunk ..].
+// slots == nullptr: item at position p uses record p.
 struct ActiveList {
   const int32_t* slots;
   const int32_t* counts;
@@ -97,6 +99,16 @@ struct DownArgs {
   int wg_pred, wg_down;
 };
 
+// Staging of one layer's active cold records (see k_stage_gather).
+struct StageArgs {
+  const uint8_t* src;       // record 0 of the layer's records, 16-byte aligned
+  int n_records;
+  ActiveList act;
+  int cap;                  // items beyond this are ignored
+  uint8_t* dst;             // staging records, list position p at dst + 6400 p
+};
+
+__global__ void k_stage_gather(StageArgs a);
 __global__ void k_prep(const uint16_t* x, const uint16_t* w, uint16_t* xw, float* ssq);
 __global__ void k_ffn_up(UpArgs a);
 __global__ void k_ffn_down(DownArgs a);

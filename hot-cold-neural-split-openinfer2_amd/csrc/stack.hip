@@ -45,6 +45,15 @@ struct oi2_stack {
   int32_t* sel_ids = nullptr;
   int cold_wg = 1;
   bool use_graph = true;
+  // staging: each layer's active records are copied one layer ahead, on a
+  // side stream, from their source (device or pinned host memory) into one
+  // of two HBM buffers, and the FFN reads them there
+  bool staged = false;
+  int copy_wg = 0;                           // workgroups of the staging copy kernel
+  hipStream_t side = nullptr;
+  uint8_t* stage[2] = {nullptr, nullptr};
+  std::vector<const uint8_t*> src;           // per layer: device-visible address of the records
+  std::vector<hipEvent_t> ev_sel, ev_ready;
   struct GraphEntry {
     hipGraphExec_t exec;
     const void* in;
@@ -60,13 +69,23 @@ int cold_wg_for(int expected);
 
 // Launch arguments of layer L's two kernels.  x_in is the token entering the
 // stack and x_out the buffer that receives the last layer's output.
+static ActiveList layer_list(const oi2_stack* s, int L) {
+  const StackLayer& SL = s->layers[L];
+  if (SL.has_pred)
+    return ActiveList{s->sel_slots + (size_t)L * s->n_chunks * kSelChunk,
+                      s->sel_counts + (size_t)L * s->n_chunks, s->n_chunks, kSelChunk};
+  return ActiveList{SL.all_slots, SL.all_count, 1, SL.n_all};
+}
+
 static void layer_args(const oi2_stack* s, int L, const uint16_t* x_in, uint16_t* x_out,
                        UpArgs& ua, DownArgs& da) {
   const int n = s->n_layers;
   const size_t sel_stride = (size_t)s->n_chunks * kSelChunk;
   const StackLayer& SL = s->layers[L];
   const oi2_layer& l = SL.l;
-  const bool pred_next = (L + 1 < n) && s->layers[L + 1].has_pred;
+  // staged: the next layer's predictor runs in its own launches, ahead of
+  // this layer's FFN, so its selection can start the next copy early
+  const bool pred_next = (L + 1 < n) && s->layers[L + 1].has_pred && !s->staged;
   const uint16_t* xl = (L == 0) ? x_in : s->xbuf + (size_t)(L - 1) * kH;
 
   ua = UpArgs{};
@@ -82,14 +101,16 @@ static void layer_args(const oi2_stack* s, int L, const uint16_t* x_in, uint16_t
   ua.h_hot = s->h_hot;
   const bool has_cold = l.cold.n_records > 0;
   if (has_cold) {
-    ua.records = l.cold.records;
-    ua.n_records = l.cold.n_records;
     ua.cold_gbias = l.cold.gate_bias;
-    if (SL.has_pred)
-      ua.act = ActiveList{s->sel_slots + (size_t)L * sel_stride,
-                          s->sel_counts + (size_t)L * s->n_chunks, s->n_chunks, kSelChunk};
-    else
-      ua.act = ActiveList{SL.all_slots, SL.all_count, 1, SL.n_all};
+    ua.act = layer_list(s, L);
+    if (s->staged) {
+      ua.records = s->stage[L & 1];
+      ua.n_records = s->cold_cap;
+      ua.act.slots = nullptr;
+    } else {
+      ua.records = s->src[L];
+      ua.n_records = l.cold.n_records;
+    }
     ua.cold_part = s->cold_part;
     ua.cold_total = s->cold_total;
     ua.cold_cap = s->cold_cap;
@@ -159,38 +180,107 @@ static int launch_down(const DownArgs& da, hipStream_t st) {
   return OI2_OK;
 }
 
+// Layer P's predictor on x (its RMSNorm from the shared sum-of-squares
+// partials of x): logits, threshold and the compacted active set sel[P].
+static int launch_predictor(oi2_stack* s, int P, const uint16_t* x, hipStream_t st) {
+  const oi2_layer& lp = s->layers[P].l;
+  const size_t sel_stride = (size_t)s->n_chunks * kSelChunk;
+  UpArgs ua{};
+  ua.tok = TokenIn{x, s->xw, s->ssq, s->eps, 1};
+  ua.pd_w = lp.pred.down_w;
+  ua.pd_rank = lp.pred.rank;
+  ua.pd_bf16 = lp.pred.dtype == OI2_DTYPE_BF16;
+  ua.pd_norm_w = lp.norm_w;
+  ua.pd_z = s->z;
+  ua.wg_pred = (lp.pred.rank + 3) / 4;
+  hipLaunchKernelGGL(k_pred_up, dim3(ua.wg_pred), dim3(kThreads), 0, st, ua);
+  OI2_CHECK_LAUNCH();
+  DownArgs da{};
+  da.pu_w = lp.pred.up_w;
+  da.pu_b = lp.pred.up_b;
+  da.pu_rank = lp.pred.rank;
+  da.pu_bf16 = lp.pred.dtype == OI2_DTYPE_BF16;
+  da.inter = lp.pred.inter;
+  da.pd_z = s->z;
+  da.thr = s->thr;
+  da.lut = lp.lut;
+  da.sel_slots = s->sel_slots + (size_t)P * sel_stride;
+  da.sel_ids = s->sel_ids + (size_t)P * sel_stride;
+  da.sel_counts = s->sel_counts + (size_t)P * s->n_chunks;
+  da.wg_pred = s->n_chunks;
+  hipLaunchKernelGGL(k_pred_down, dim3(da.wg_pred), dim3(kThreads), 0, st, da);
+  OI2_CHECK_LAUNCH();
+  return OI2_OK;
+}
+
+static StageArgs stage_args(const oi2_stack* s, int L) {
+  StageArgs g{};
+  g.src = s->src[L];
+  g.n_records = s->layers[L].l.cold.n_records;
+  g.act = layer_list(s, L);
+  g.cap = s->cold_cap;
+  g.dst = s->stage[L & 1];
+  return g;
+}
+
+static int launch_gather(const oi2_stack* s, int L, hipStream_t st) {
+  if (s->layers[L].l.cold.n_records == 0) return OI2_OK;
+  const StageArgs g = stage_args(s, L);
+  hipLaunchKernelGGL(k_stage_gather, dim3(s->copy_wg), dim3(kThreads), 0, st, g);
+  OI2_CHECK_LAUNCH();
+  return OI2_OK;
+}
+
+static inline const uint16_t* layer_input(const oi2_stack* s, int L, const uint16_t* x_in) {
+  return L == 0 ? x_in : s->xbuf + (size_t)(L - 1) * kH;
+}
+
+// Staged token.  Main stream: predictor(L+1) on x_L, wait for layer L's
+// records, FFN(L).  Side stream: once sel[L+1] exists, copy layer L+1's
+// records.  The copy of L+1 thus runs
+// under FFN(L), and the side stream rejoins the main one before the last FFN.
+static int stack_launch_staged(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, hipStream_t st) {
+  const int n = s->n_layers;
+  hipLaunchKernelGGL(k_prep, dim3(1), dim3(kThreads), 0, st, x_in, s->layers[0].l.norm_w, s->xw,
+                     s->ssq);
+  OI2_CHECK_LAUNCH();
+  int rc = OI2_OK;
+  if (s->layers[0].has_pred) rc = launch_predictor(s, 0, x_in, st);
+  if (rc) return rc;
+  OI2_CHECK_HIP(hipEventRecord(s->ev_sel[0], st));
+  OI2_CHECK_HIP(hipStreamWaitEvent(s->side, s->ev_sel[0], 0));
+  if ((rc = launch_gather(s, 0, s->side))) return rc;
+  OI2_CHECK_HIP(hipEventRecord(s->ev_ready[0], s->side));
+  for (int L = 0; L < n; ++L) {
+    if (L + 1 < n) {
+      if (s->layers[L + 1].has_pred &&
+          (rc = launch_predictor(s, L + 1, layer_input(s, L, x_in), st)))
+        return rc;
+      OI2_CHECK_HIP(hipEventRecord(s->ev_sel[L + 1], st));
+      // ev_sel[L+1] follows FFN(L-1) on the main stream, so FFN(L-1) has
+      // finished with the buffer this copy overwrites
+      OI2_CHECK_HIP(hipStreamWaitEvent(s->side, s->ev_sel[L + 1], 0));
+      if ((rc = launch_gather(s, L + 1, s->side))) return rc;
+      OI2_CHECK_HIP(hipEventRecord(s->ev_ready[L + 1], s->side));
+    }
+    OI2_CHECK_HIP(hipStreamWaitEvent(st, s->ev_ready[L], 0));
+    UpArgs ua;
+    DownArgs da;
+    layer_args(s, L, x_in, x_out, ua, da);
+    if ((rc = launch_up(ua, st)) || (rc = launch_down(da, st))) return rc;
+  }
+  return OI2_OK;
+}
+
 static int stack_launch(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, hipStream_t st) {
+  if (s->staged) return stack_launch_staged(s, x_in, x_out, st);
   hipLaunchKernelGGL(k_prep, dim3(1), dim3(kThreads), 0, st, x_in, s->layers[0].l.norm_w, s->xw,
                      s->ssq);
   OI2_CHECK_LAUNCH();
   // layer 0's active set from the token itself
   if (s->layers[0].has_pred) {
-    const oi2_layer& l0 = s->layers[0].l;
-    UpArgs ua{};
-    ua.tok = TokenIn{x_in, s->xw, s->ssq, s->eps, 1};
-    ua.pd_w = l0.pred.down_w;
-    ua.pd_rank = l0.pred.rank;
-    ua.pd_bf16 = l0.pred.dtype == OI2_DTYPE_BF16;
-    ua.pd_norm_w = l0.norm_w;
-    ua.pd_z = s->z;
-    ua.wg_pred = (l0.pred.rank + 3) / 4;
-    hipLaunchKernelGGL(k_pred_up, dim3(ua.wg_pred), dim3(kThreads), 0, st, ua);
-    OI2_CHECK_LAUNCH();
-    DownArgs da{};
-    da.pu_w = l0.pred.up_w;
-    da.pu_b = l0.pred.up_b;
-    da.pu_rank = l0.pred.rank;
-    da.pu_bf16 = l0.pred.dtype == OI2_DTYPE_BF16;
-    da.inter = l0.pred.inter;
-    da.pd_z = s->z;
-    da.thr = s->thr;
-    da.lut = l0.lut;
-    da.sel_slots = s->sel_slots;
-    da.sel_ids = s->sel_ids;
-    da.sel_counts = s->sel_counts;
-    da.wg_pred = s->n_chunks;
-    hipLaunchKernelGGL(k_pred_down, dim3(da.wg_pred), dim3(kThreads), 0, st, da);
-    OI2_CHECK_LAUNCH();
+    int rc = launch_predictor(s, 0, x_in, st);
+    if (rc) return rc;
   }
   for (int L = 0; L < s->n_layers; ++L) {
     UpArgs ua;
@@ -203,7 +293,45 @@ static int stack_launch(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, hip
   return OI2_OK;
 }
 
+// Device-visible address of a record array: device memory as is, pinned host
+// memory through its mapping.  Anything else (pageable memory) is rejected,
+// since a kernel reading it would fault.
+static int device_view(const uint8_t* p, const uint8_t** out) {
+  hipPointerAttribute_t at{};
+  if (hipPointerGetAttributes(&at, p) != hipSuccess ||
+      (at.type != hipMemoryTypeDevice && at.type != hipMemoryTypeHost)) {
+    (void)hipGetLastError();
+    return OI2_EINVAL;
+  }
+  if (at.type == hipMemoryTypeHost) {
+    void* dp = nullptr;
+    if (hipHostGetDevicePointer(&dp, (void*)p, 0) != hipSuccess || !dp) {
+      (void)hipGetLastError();
+      return OI2_EINVAL;
+    }
+    p = (const uint8_t*)dp;
+  }
+  *out = p;
+  return OI2_OK;
+}
+
+static void staging_free(oi2_stack* s) {
+  for (auto* v : {&s->ev_sel, &s->ev_ready}) {
+    for (auto e : *v)
+      if (e) (void)hipEventDestroy(e);
+    v->clear();
+  }
+  for (auto& b : s->stage) {
+    if (b) (void)hipFree(b);
+    b = nullptr;
+  }
+  if (s->side) (void)hipStreamDestroy(s->side);
+  s->side = nullptr;
+  s->staged = false;
+}
+
 static void stack_free(oi2_stack* s) {
+  staging_free(s);
   for (auto& L : s->layers) {
     if (L.all_slots) (void)hipFree(L.all_slots);
     if (L.all_count) (void)hipFree(L.all_count);
@@ -258,6 +386,16 @@ int oi2_stack_create(const oi2_layer* layers, int32_t n_layers, int32_t inter, f
       delete s;
       return OI2_EINVAL;
     }
+    // records: device memory, or pinned host memory read over PCIe
+    const uint8_t* src = nullptr;
+    if (SL.l.cold.n_records > 0 &&
+        ((uintptr_t)SL.l.cold.records % 16 || device_view(SL.l.cold.records, &src) != OI2_OK)) {
+      set_error("layer %d: records must be 16-byte aligned device or pinned host memory", L);
+      stack_free(s);
+      delete s;
+      return OI2_EINVAL;
+    }
+    s->src.push_back(src);
     if (SL.has_pred) {
       const oi2_predictor& p = SL.l.pred;
       if (!p.up_w || !p.up_b || p.inter != inter || p.rank <= 0 || p.rank > 256 || p.rank % 8 ||
@@ -366,11 +504,73 @@ int oi2_stack_set_graph(oi2_stack* s, int32_t enable) {
   return OI2_OK;
 }
 
+int oi2_stack_set_staging(oi2_stack* s, int32_t copy_workgroups) {
+  clear_error();
+  OI2_CHECK_ARG(s, "null stack");
+  OI2_CHECK_ARG(copy_workgroups >= 0 && copy_workgroups <= 1024, "copy_workgroups %d out of range",
+                copy_workgroups);
+  for (auto& g : s->graphs) (void)hipGraphExecDestroy(g.exec);
+  s->graphs.clear();
+  OI2_CHECK_HIP(hipDeviceSynchronize());
+  staging_free(s);
+  if (!copy_workgroups) return OI2_OK;
+  hipError_t e = hipStreamCreateWithFlags(&s->side, hipStreamNonBlocking);
+  for (int b = 0; b < 2 && e == hipSuccess; ++b)
+    e = hipMalloc((void**)&s->stage[b], (size_t)s->cold_cap * kRecBytes);
+  for (auto* v : {&s->ev_sel, &s->ev_ready}) {
+    v->assign(s->n_layers, nullptr);
+    for (auto& ev : *v)
+      if (e == hipSuccess) e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+  }
+  if (e != hipSuccess) {
+    set_error("staging set-up failed: %s", hipGetErrorString(e));
+    staging_free(s);
+    return OI2_ENOMEM;
+  }
+  s->staged = true;
+  s->copy_wg = copy_workgroups;
+  return OI2_OK;
+}
+
+int oi2_stack_profile_staging(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, int32_t reps,
+                              float* gather_us, void* stream) {
+  clear_error();
+  OI2_CHECK_ARG(s && x_in && x_out && gather_us, "null argument");
+  OI2_CHECK_ARG(s->staged, "staging is not enabled on this stack");
+  OI2_CHECK_ARG(reps > 0 && reps <= 1024, "reps %d out of range", reps);
+  hipStream_t st = (hipStream_t)stream;
+  hipEvent_t ev[2] = {nullptr, nullptr};
+  int rc = OI2_OK;
+  for (auto& e : ev)
+    if (rc == OI2_OK && hipEventCreate(&e) != hipSuccess) {
+      set_error("hipEventCreate failed");
+      rc = OI2_EHIP;
+    }
+  // one token fixes the active sets; then every layer's copy back to back on
+  // the launch stream; then the token again, so the buffers hold its state
+  if (rc == OI2_OK) rc = stack_launch(s, x_in, x_out, st);
+  if (rc == OI2_OK && hipStreamSynchronize(st) != hipSuccess) rc = OI2_EHIP;
+  if (rc == OI2_OK && hipEventRecord(ev[0], st) != hipSuccess) rc = OI2_EHIP;
+  for (int r = 0; rc == OI2_OK && r < reps; ++r)
+    for (int L = 0; rc == OI2_OK && L < s->n_layers; ++L) rc = launch_gather(s, L, st);
+  if (rc == OI2_OK && hipEventRecord(ev[1], st) != hipSuccess) rc = OI2_EHIP;
+  if (rc == OI2_OK) rc = stack_launch(s, x_in, x_out, st);
+  if (rc == OI2_OK && hipStreamSynchronize(st) != hipSuccess) rc = OI2_EHIP;
+  float t = 0.0f;
+  if (rc == OI2_OK && hipEventElapsedTime(&t, ev[0], ev[1]) != hipSuccess) rc = OI2_EHIP;
+  if (rc == OI2_EHIP && !oi2_last_error()[0]) set_error("HIP call failed while profiling");
+  if (rc == OI2_OK) *gather_us = (float)(t * 1e3 / ((double)reps * s->n_layers));
+  for (auto& e : ev)
+    if (e) (void)hipEventDestroy(e);
+  return rc;
+}
+
 int oi2_stack_profile(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, int32_t reps,
                       float* up_us, float* down_us, void* stream) {
   clear_error();
   OI2_CHECK_ARG(s && x_in && x_out && up_us && down_us, "null argument");
   OI2_CHECK_ARG(reps > 0 && reps <= 1024, "reps %d out of range", reps);
+  OI2_CHECK_ARG(!s->staged, "kernel profiling needs staging disabled");
   hipStream_t st = (hipStream_t)stream;
   hipEvent_t ev[3] = {nullptr, nullptr, nullptr};
   int rc = OI2_OK;

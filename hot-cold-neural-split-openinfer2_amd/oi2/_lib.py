@@ -74,6 +74,9 @@ _SIGS = {
     "oi2_stack_set_expected_active": (c_int32, [c_void_p, c_int32]),
     "oi2_stack_profile": (c_int32, [c_void_p, c_void_p, c_void_p, c_int32, POINTER(c_float),
                                     POINTER(c_float), c_void_p]),
+    "oi2_stack_set_staging": (c_int32, [c_void_p, c_int32]),
+    "oi2_stack_profile_staging": (c_int32, [c_void_p, c_void_p, c_void_p, c_int32, POINTER(c_float),
+                                            c_void_p]),
     "oi2_stack_trace": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "oi2_stack_destroy": (c_int32, [c_void_p]),
 }

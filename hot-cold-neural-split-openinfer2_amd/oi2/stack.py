@@ -27,7 +27,8 @@ class StackLayer:
 
 class DecodeStack:
     def __init__(self, layers: list[StackLayer], inter: int, eps: float, activation: str = "silu",
-                 act_on_both: bool = False, threshold_logit: float = 0.0, use_graph: bool = True):
+                 act_on_both: bool = False, threshold_logit: float = 0.0, use_graph: bool = True,
+                 staging: int = 0):
         self.layers = layers
         self.inter = inter
         self.n_layers = len(layers)
@@ -48,6 +49,15 @@ class DecodeStack:
                                       ctypes.byref(h)))
         self._h = h
         _lib.check(L.oi2_stack_set_graph(h, int(bool(use_graph))))
+        if staging:
+            self.set_staging(staging)
+
+    def set_staging(self, copy_workgroups: int):
+        """Copy each layer's active records one layer ahead on a side stream
+        into HBM staging buffers, with a copy kernel of `copy_workgroups`
+        workgroups (records may then live in pinned host memory); 0: the FFN
+        reads the records where they are."""
+        _lib.check(_lib.lib().oi2_stack_set_staging(self._h, int(copy_workgroups)))
 
     def set_expected_active(self, n: int):
         """Size the cold pass for about n active records per layer."""
@@ -67,6 +77,14 @@ class DecodeStack:
         _lib.check(_lib.lib().oi2_stack_profile(self._h, x_in.data_ptr(), x_out.data_ptr(), int(reps),
                                                 ctypes.byref(up), ctypes.byref(down), s or None))
         return up.value, down.value
+
+    def profile_staging(self, x_in: torch.Tensor, x_out: torch.Tensor, stream=None, reps: int = 4):
+        """Mean microseconds of one layer's record copy (staging enabled)."""
+        us = ctypes.c_float()
+        s = stream.cuda_stream if stream is not None else _lib.stream_handle(x_in.device)
+        _lib.check(_lib.lib().oi2_stack_profile_staging(self._h, x_in.data_ptr(), x_out.data_ptr(),
+                                                        int(reps), ctypes.byref(us), s or None))
+        return us.value
 
     def trace(self):
         """(xs (n_layers, H) fp16 layer outputs, counts (n_layers, n_chunks),

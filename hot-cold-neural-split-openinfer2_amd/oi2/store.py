@@ -23,13 +23,14 @@ from . import format as fmt
 
 
 class ColdSection:
-    """One (layer, expert) section resident in device memory."""
+    """One (layer, expert) section: records in device or pinned host memory,
+    LUT on the device."""
 
     def __init__(self, layer: int, nids: np.ndarray, records: torch.Tensor, lut: torch.Tensor,
                  lut_host: np.ndarray, inter: int):
         self.layer = layer
         self.nids = nids                  # (n,) int64 on-disk order
-        self.records = records            # (n, 6400) uint8, device
+        self.records = records            # (n, 6400) uint8, device or pinned host
         self.lut = lut                    # (inter,) int32 device: nid -> slot or -1
         self.lut_host = lut_host
         self.inter = inter
@@ -56,14 +57,19 @@ class ColdSection:
             order = np.argsort(self.nids, kind="stable")
             # a duplicated id resolves to the slot the lut keeps
             keep = self.lut_host[self.nids[order]] == order.astype(np.int32)
-            self._all = torch.as_tensor(order[keep].astype(np.int32)).to(self.records.device)
+            self._all = torch.as_tensor(order[keep].astype(np.int32)).to(self.lut.device)
         return self._all
 
 
 class ColdWeightStore:
-    """splitter.py:307-407 with a device-resident section cache."""
+    """splitter.py:307-407 with a section cache: each section's records are
+    copied once out of the mapped file, into device memory, or with
+    ``pinned=True`` into pinned host memory (read by the GPU over PCIe; a
+    decode stack with staging copies the active ones into HBM one layer
+    ahead).  The nid -> slot LUT always lives on the device."""
 
-    def __init__(self, cold_bin: str, cold_index: str, config: dict, device="cuda"):
+    def __init__(self, cold_bin: str, cold_index: str, config: dict, device="cuda",
+                 pinned: bool = False):
         self.config = config
         self.index = np.load(cold_index)
         self._f = open(cold_bin, "rb")
@@ -75,6 +81,7 @@ class ColdWeightStore:
             raise ValueError(f"hidden_dim {self.H}: the cold-record layout is sized for "
                              f"{fmt.HIDDEN_DIM}")
         self.device = torch.device(device)
+        self.pinned = bool(pinned)
         self._offset_cache: dict[tuple[int, int], dict[int, int]] = {}
         self._sections: dict[tuple[int, int], ColdSection | None] = {}
         self._lock = threading.Lock()
@@ -106,7 +113,7 @@ class ColdWeightStore:
         return m
 
     def section(self, layer_idx: int, expert_idx: int = 0) -> ColdSection | None:
-        """Upload (once) and return the section's device records and LUT."""
+        """Copy (once) and return the section's records and device LUT."""
         key = (layer_idx, expert_idx)
         with self._lock:
             if key in self._sections:
@@ -120,7 +127,12 @@ class ColdWeightStore:
             inter = max(int(self.I or 0), int(nids.max()) + 1)
             host = np.frombuffer(self._mm, dtype=np.uint8, count=n * fmt.NEURON_RECORD_BYTES,
                                  offset=base).reshape(n, fmt.NEURON_RECORD_BYTES)
-            records = torch.from_numpy(host.copy()).to(self.device)
+            if self.pinned:
+                records = torch.empty((n, fmt.NEURON_RECORD_BYTES), dtype=torch.uint8,
+                                      pin_memory=True)
+                records.numpy()[:] = host
+            else:
+                records = torch.from_numpy(host.copy()).to(self.device)
             lut = np.full(inter, -1, dtype=np.int32)
             # a duplicated id maps to its last record, as the reference's dict does
             uniq, first_rev = np.unique(nids[::-1], return_index=True)

@@ -7,8 +7,8 @@
  * error code, with a message available from oi2_last_error() on the calling
  * thread.  Nothing throws across the ABI.  Entry points that need scratch
  * memory take a caller-provided workspace (size from the matching *_bytes
- * query) and allocate nothing; the stack and stager handles allocate once,
- * at creation.
+ * query) and allocate nothing; the stack handle allocates once, at creation
+ * (and when staging is switched on).
  *
  * Layouts (H = 4096, the hidden size the cold-record format is sized for):
  *   activations   fp16, row-major (batch, H)
@@ -60,8 +60,9 @@ typedef struct oi2_hot {
   const float* gate_bias;     /* (n_hot) gate pre-activation shift, or NULL */
 } oi2_hot;
 
-/* One layer's cold section resident in device memory: the records that
- * ColdWeightStore.read_neurons decodes (splitter.py:354-403). */
+/* One layer's cold section: the records that ColdWeightStore.read_neurons
+ * decodes (splitter.py:354-403), in device memory (or, for a decode stack,
+ * pinned host memory, read over PCIe). */
 typedef struct oi2_cold {
   const uint8_t* records;     /* record slot 0 */
   int32_t n_records;
@@ -189,6 +190,26 @@ int oi2_stack_set_expected_active(oi2_stack* s, int32_t expected);
 /* Replay the launch sequence through a captured hipGraph (default 1) or launch
  * it directly (0).  Graphs are never used on the NULL stream. */
 int oi2_stack_set_graph(oi2_stack* s, int32_t enable);
+/* Cold-record staging, the device counterpart of the prefetch pipeline
+ * (SparseFFNLayer.submit_cold_fetch / _fetch_cold, engine.py:266-272,
+ * 285-290, submitted one layer ahead at engine.py:432-436).  Enabled, each
+ * token runs layer L+1's predictor on x_L ahead of layer L's FFN; a copy
+ * kernel on a side stream then moves layer L+1's active records from the
+ * layer's record pointer into one of two HBM staging buffers while layer L
+ * computes, and layer L+1's FFN reads them there.  The record pointers may
+ * then be pinned host memory (hipHostMalloc, or a pinned torch tensor): the
+ * copy reads it over PCIe.  Device memory also works (pageable memory is
+ * rejected at creation).  copy_workgroups: workgroups of the copy kernel
+ * (256 threads, one record per wave at a time), 0 disables staging; a few
+ * dozen keep the PCIe link busy without crowding the FFN's HBM traffic.
+ * Synchronises the device; drops captured graphs. */
+int oi2_stack_set_staging(oi2_stack* s, int32_t copy_workgroups);
+/* With staging enabled: decode x_in once (fixing the active sets), time
+ * every layer's record copy back to back `reps` times between two hipEvents
+ * on `stream`, decode x_in again, and write the mean microseconds per
+ * layer copy. */
+int oi2_stack_profile_staging(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, int32_t reps,
+                              float* gather_us, void* stream);
 /* Average kernel durations on the decode path.  Decodes x_in once (fixing
  * every layer's active set), then launches every layer's ffn_up kernel back
  * to back `reps` times between two hipEvents on `stream`, then every layer's

@@ -121,6 +121,16 @@ def test_store_read_neurons_matches_reference_truth(dev):
             assert (1, 0) in store._offset_cache
             for a, b in zip(again, store.read_neurons(1, 0, layers[1][0][:4])):
                 assert torch.equal(a, b)
+            # records in pinned host memory, decoded over PCIe: same bits
+            pstore = oi2.ColdWeightStore(cold_bin, cold_idx, config, device=dev, pinned=True)
+            try:
+                for li in range(4):
+                    assert pstore.section(li).records.is_pinned()
+                    req = layers[li][0][::-1] + [absent]
+                    for a, b in zip(pstore.read_neurons(li, 0, req), store.read_neurons(li, 0, req)):
+                        assert a.device == b.device and torch.equal(a, b)
+            finally:
+                pstore.close()
         finally:
             store.close()
 

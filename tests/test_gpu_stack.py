@@ -110,3 +110,54 @@ def test_graph_replay_is_deterministic(stack4):
     assert up_us > 0 and down_us > 0
     assert torch.equal(x_d, outs[0])     # profiling leaves the state of decoding x_in
     direct.close()
+
+
+def test_staged_store_matches_resident(stack4):
+    """Records in pinned host memory, copied one layer ahead on a side stream
+    (graph-captured fork/join), give the same bits as the HBM-resident stack:
+    the FFN consumes the same records in the same order."""
+    dev, g, layers, st, thr = stack4
+    stream = torch.cuda.Stream(device=dev)
+    x_in = torch.randn(H, generator=g, device=dev).half()
+    ref = torch.empty_like(x_in)
+    with torch.cuda.stream(stream):
+        st.decode(x_in, ref, stream)
+    stream.synchronize()
+    _, c_ref, _, i_ref = st.trace()
+
+    pinned = [l.records.cpu().pin_memory() for l in layers]
+    staged = DecodeStack([StackLayer(l.hot, p, l.lut, l.norm_w, l.predictor)
+                          for l, p in zip(layers, pinned)], st.inter, EPS, "silu", False, thr,
+                         staging=16)
+    staged.set_expected_active(300)
+    out = torch.empty_like(x_in)
+    for k in range(3):                       # capture, then replays
+        with torch.cuda.stream(stream):
+            staged.decode(x_in, out, stream)
+            _ = (out.float() * 3).sum()
+        stream.synchronize()
+        assert torch.equal(out, ref), f"replay {k}"
+    _, c, _, i = staged.trace()
+    torch.cuda.synchronize()
+    assert torch.equal(c, c_ref)
+    for L in range(4):      # entries past each chunk's count are unspecified
+        assert _active_ids(c, i, L) == _active_ids(c_ref, i_ref, L)
+    # direct launches on the default stream, and device-memory sources
+    direct = DecodeStack(st.layers, st.inter, EPS, "silu", False, thr, use_graph=False, staging=16)
+    direct.set_expected_active(300)
+    out2 = torch.empty_like(x_in)
+    direct.decode(x_in, out2, None)
+    torch.cuda.synchronize()
+    assert torch.equal(out2, ref)
+    us = staged.profile_staging(x_in, out, stream, reps=1)
+    torch.cuda.synchronize()
+    assert us > 0 and torch.equal(out, ref)
+    direct.close()
+    staged.close()
+
+
+def test_pageable_records_rejected(stack4):
+    dev, g, layers, st, thr = stack4
+    pageable = [StackLayer(l.hot, l.records.cpu(), l.lut, l.norm_w, l.predictor) for l in layers]
+    with pytest.raises(oi2.OI2Error, match="pinned host"):
+        DecodeStack(pageable, st.inter, EPS, "silu", False, thr)
