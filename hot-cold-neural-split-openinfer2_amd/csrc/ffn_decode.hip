@@ -81,24 +81,6 @@ __device__ float block_rnorm(const uint16_t* x, float eps, float* s_parts) {
 // output (engine.py:247-249); the predictor query and oi2_rmsnorm use it.
 __device__ __forceinline__ float xn_exact(float x, float r, float w) { return round_f16(x * r * w); }
 
-// Exclusive prefix of the (clamped) chunk counts into s_prefix[0..n_chunks].
-__device__ void chunk_prefix(const ActiveList& al, int* s_prefix) {
-  const int t = threadIdx.x;
-  int c = 0;
-  if (t < al.n_chunks) {
-    c = al.counts[t];
-    c = c < 0 ? 0 : (c > al.chunk ? al.chunk : c);
-  }
-  s_prefix[t + 1] = c;
-  if (t == 0) s_prefix[0] = 0;
-  __syncthreads();
-  for (int off = 1; off < kThreads; off <<= 1) {
-    int v = (t >= off) ? s_prefix[t + 1 - off] : 0;
-    __syncthreads();
-    s_prefix[t + 1] += v;
-    __syncthreads();
-  }
-}
 
 // Exclusive prefix of the clamped chunk counts, per wave: lane k holds the
 // prefix of chunks k, k+64, k+128, k+192.  Returns the total.
@@ -916,7 +898,7 @@ int oi2_rmsnorm(const uint16_t* x, const uint16_t* w, int32_t rows, float eps, u
 }
 
 size_t oi2_ffn_workspace_bytes(int32_t batch, int32_t n_hot, int32_t cold_capacity) {
-  (void)batch;
+  if (batch >= 2) return batch_ws_bytes(batch, n_hot, cold_capacity > 0 ? cold_capacity : 0);
   return ffn_ws_bytes(n_hot, cold_capacity > 0 ? cold_wg_for(cold_capacity) : 0);
 }
 
@@ -945,6 +927,11 @@ int oi2_ffn_forward(const uint16_t* x, int32_t batch, const uint16_t* norm_w, fl
                   active->chunk);
     cap = active->n_chunks * active->chunk;
   }
+  hipStream_t st = (hipStream_t)stream;
+  if (batch >= 2)
+    return batch_ffn(x, batch, norm_w, eps, hot, has_cold ? cold : nullptr, has_cold ? active : nullptr,
+                     act == OI2_ACT_RELU, act_on_both != 0, add_residual, out, y32, workspace,
+                     workspace_bytes, st);
   const int expected = has_cold ? (active->expected > 0 && active->expected < cap ? active->expected : cap) : 0;
   const int wg_cold = has_cold ? cold_wg_for(expected) : 0;
   const int ws_wg = has_cold ? cold_wg_for(cap) : 0;
@@ -952,7 +939,6 @@ int oi2_ffn_forward(const uint16_t* x, int32_t batch, const uint16_t* norm_w, fl
                 "workspace of %zu bytes is smaller than the %zu required", workspace_bytes,
                 ffn_ws_bytes(n_hot, ws_wg));
   FfnWs ws = ffn_ws(workspace, n_hot, ws_wg);
-  hipStream_t st = (hipStream_t)stream;
   for (int b = 0; b < batch; ++b) {
     const uint16_t* xb = x + (size_t)b * kH;
     if (norm_w) {

@@ -1,5 +1,6 @@
 // Argument blocks and kernel declarations shared by the decode-path sources.
 #pragma once
+#include "oi2.h"
 #include "oi2_device.h"
 
 namespace oi2 {
@@ -109,6 +110,79 @@ struct StageArgs {
 };
 
 __global__ void k_stage_gather(StageArgs a);
+
+// Multi-token FFN on the matrix cores (ffn_batch.hip).
+struct BUpArgs {
+  const uint16_t* xn;       // (M, H) fp16 normalised tokens
+  int M;
+  int relu, both;
+  int n_hot;
+  const uint8_t* gate_q;
+  const uint8_t* up_q;
+  const float* gate_s;
+  const float* up_s;
+  const float* hot_gbias;
+  uint16_t* hh;             // (Mpad, ldh) fp16 hot activations, zero past n_hot
+  int ldh;
+  int hot_wg;               // ldh / 64 workgroups of hot columns
+  const uint8_t* records;
+  int n_records;
+  const float* cold_gbias;
+  const int32_t* dslots;    // dense active list
+  const int32_t* total;
+  int cap;
+  uint16_t* hc;             // (Mpad, ldc) fp16 cold activations
+  int ldc;
+};
+
+struct BDownArgs {
+  int M, Mpad;
+  const uint16_t* hh;
+  int ldh;
+  const uint8_t* down_q;
+  int down_stride;
+  const float* down_s;
+  int hot_blocks;           // 128-wide K blocks of the hot product
+  int hot_splits;
+  const uint16_t* hc;
+  int ldc;
+  const uint8_t* records;
+  int n_records;
+  const int32_t* dslots;
+  const int32_t* total;
+  int cap;
+  int cold_splits;
+  float* part;              // (hot_splits + cold_splits, Mpad, H) fp32 partial sums
+};
+
+__global__ void k_bup(BUpArgs a);
+__global__ void k_bdown(BDownArgs a);
+__global__ void k_rmsnorm(const uint16_t* x, const uint16_t* w, float eps, uint16_t* out);
+
+size_t batch_ws_bytes(int M, int n_hot, int cap);
+int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const oi2_hot* hot,
+              const oi2_cold* cold, const oi2_active* active, int relu, int both, int add_residual,
+              uint16_t* out, float* y32, void* workspace, size_t workspace_bytes, hipStream_t st);
+
+// Exclusive prefix of the (clamped) chunk counts into s_prefix[0..n_chunks];
+// all threads of a 256-thread workgroup call it (it contains barriers).
+__device__ __forceinline__ void chunk_prefix(const ActiveList& al, int* s_prefix) {
+  const int t = threadIdx.x;
+  int c = 0;
+  if (t < al.n_chunks) {
+    c = al.counts[t];
+    c = c < 0 ? 0 : (c > al.chunk ? al.chunk : c);
+  }
+  s_prefix[t + 1] = c;
+  if (t == 0) s_prefix[0] = 0;
+  __syncthreads();
+  for (int off = 1; off < kThreads; off <<= 1) {
+    int v = (t >= off) ? s_prefix[t + 1 - off] : 0;
+    __syncthreads();
+    s_prefix[t + 1] += v;
+    __syncthreads();
+  }
+}
 __global__ void k_prep(const uint16_t* x, const uint16_t* w, uint16_t* xw, float* ssq);
 __global__ void k_ffn_up(UpArgs a);
 __global__ void k_ffn_down(DownArgs a);

@@ -1,0 +1,152 @@
+"""Multi-token FFN (batch decode with a shared active set, prefill chunks) on
+the MFMA path, through oi2_ffn_forward with batch >= 2, against the float64
+oracle over the same quantised weights.  Bar: max rel err <= 1e-2 and cosine
+>= 0.9999 per checked row set."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oi2.layer import ColdNeurons, _ffn
+from oi2.store import ColdSection
+from oi2.synth import SyntheticLayer
+from oracle import oracle as O
+from tests.gpu_helpers import EPS, assert_ffn_close, cold_dense, hot_dense, normed_f16
+
+pytestmark = pytest.mark.gpu
+H = 4096
+
+
+@pytest.fixture(scope="module")
+def dev():
+    assert torch.cuda.is_available(), "GPU tests need a visible GPU"
+    return torch.device("cuda:0")
+
+
+def _section(lay):
+    return ColdSection(0, lay.cold_ids.cpu().numpy(), lay.records, lay.lut, lay.lut.cpu().numpy(),
+                       lay.inter)
+
+
+@pytest.fixture(scope="module")
+def layer25(dev):
+    g = torch.Generator(device=dev).manual_seed(31)
+    return SyntheticLayer(g, 14336, 3584, device=dev), g
+
+
+@pytest.mark.parametrize("B", [2, 8, 64])
+def test_batch_decode_shared_active_set(dev, layer25, B):
+    lay, g = layer25
+    n_cold = lay.records.shape[0]
+    slots = torch.randperm(n_cold, generator=g, device=dev)[: int(0.15 * n_cold)].int()
+    cold = ColdNeurons.from_slots(_section(lay), slots)
+    x = torch.randn((B, H), generator=g, device=dev).half()
+    out, y32 = _ffn(x, lay.norm_w, EPS, lay.hot, cold, "silu", False, add_residual=True,
+                    want_y32=True)
+    torch.cuda.synchronize()
+    rows = list(range(B)) if B <= 8 else [0, 1, 17, 31, 32, 63]
+    xn = normed_f16(x[rows], lay.norm_w)
+    Gh, Uh, Dh = hot_dense(lay.hot)
+    Gc, Uc, Dc = cold_dense(lay.records, slots)
+    ref = O.sparse_ffn(xn, "silu", False, Gh, Uh, Dh, Gc, Uc, Dc)
+    y = y32[rows].cpu().numpy()
+    for r in range(len(rows)):
+        assert_ffn_close(y[r], ref[r], what=f"B={B} row {rows[r]}")
+    assert_ffn_close(out[rows].float().cpu().numpy(), x[rows].float().cpu().numpy() + ref,
+                     tol=2e-3, cos_min=0.99999, what="residual out")
+    # every row of the batch equals the same token run alone (decode path)
+    one = _ffn(x[rows[-1]:rows[-1] + 1], lay.norm_w, EPS, lay.hot, cold, "silu", False, True,
+               want_y32=True)[1]
+    assert_ffn_close(y32[rows[-1]].cpu().numpy(), one[0].cpu().numpy(), tol=2e-3, cos_min=0.99999,
+                     what="batch row vs single token")
+
+
+def test_batch_drelu_union_of_firing_sets_equals_dense(dev):
+    """16 independent dReLU tokens over the union of their true firing sets:
+    a neuron outside a token's set contributes exactly zero to it, so the
+    union reproduces each token's dense FFN (survey config 2 at B=16)."""
+    g = torch.Generator(device=dev).manual_seed(22)
+    inter, B = 14336, 16
+    sigma = 0.02 * math.sqrt(H)
+    lay = SyntheticLayer(g, inter, 3584, device=dev, gate_bias_shift=-1.3 * sigma)
+    x = torch.randn((B, H), generator=g, device=dev).half()
+    xn = normed_f16(x, lay.norm_w)
+    Gc_all, Uc_all, Dc_all = cold_dense(lay.records, np.arange(lay.records.shape[0]))
+    bc = lay.cold_gate_bias.cpu().numpy().astype(np.float64)
+    fire = (np.maximum(xn @ Gc_all.T + bc, 0) * np.maximum(xn @ Uc_all.T, 0)) != 0
+    union = np.nonzero(fire.any(axis=0))[0]
+    assert 0.2 * inter < union.size < 0.8 * inter
+    cold = ColdNeurons.from_slots(_section(lay), union, gate_bias=lay.cold_gate_bias)
+    _, y32 = _ffn(x, lay.norm_w, EPS, lay.hot, cold, "relu", True, False, want_y32=True)
+    Gh, Uh, Dh = hot_dense(lay.hot)
+    bh = lay.hot.gate_bias.cpu().numpy().astype(np.float64)
+    dense = O.sparse_ffn(xn, "relu", True, Gh, Uh, Dh, Gc_all, Uc_all, Dc_all, bh, bc)
+    y = y32.cpu().numpy()
+    for r in range(B):
+        assert_ffn_close(y[r], dense[r], what=f"dReLU row {r}")
+
+
+def test_batch_edge_shapes(dev):
+    """Token count not a multiple of the 64-row tile, n_hot not a multiple of
+    the 128 K block, a chunked active list with an empty chunk, duplicates and
+    invalid slots, one half missing."""
+    g = torch.Generator(device=dev).manual_seed(6)
+    lay = SyntheticLayer(g, 2000, 1000, device=dev)
+    sec = _section(lay)
+    B = 70
+    x = torch.randn((B, H), generator=g, device=dev).half()
+    rows = [0, 5, 63, 64, 69]
+    xn = normed_f16(x[rows], lay.norm_w)
+    Gh, Uh, Dh = hot_dense(lay.hot)
+    sl = torch.full((3 * 40,), -7, dtype=torch.int32, device=dev)
+    sl[0:37] = torch.arange(37, dtype=torch.int32) * 3
+    sl[80:93] = torch.tensor([5, 5, 900, -1, 10 ** 6, 17, 999, 998, 1, 2, 3, 4, 700],
+                             dtype=torch.int32)
+    counts = torch.tensor([37, 0, 13], dtype=torch.int32, device=dev)
+    cold = ColdNeurons(sec, sl, counts, 3, 40)
+    valid = [s for s in sl[0:37].tolist() + sl[80:93].tolist() if 0 <= s < lay.records.shape[0]]
+    Gc, Uc, Dc = cold_dense(lay.records, valid)
+    for hot, c, what in ((lay.hot, cold, "both"), (None, cold, "cold only"),
+                         (lay.hot, None, "hot only")):
+        _, y32 = _ffn(x, lay.norm_w, EPS, hot, c, "silu", False, False, want_y32=True)
+        ref = O.sparse_ffn(xn, "silu", False, *(hot_dense(hot) if hot is not None else
+                                                  (None, None, None)),
+                           *((Gc, Uc, Dc) if c is not None else (None, None, None)))
+        y = y32[rows].cpu().numpy()
+        for r in range(len(rows)):
+            assert_ffn_close(y[r], ref[r], what=f"{what} row {rows[r]}")
+    # both halves empty: zeros
+    _, y32 = _ffn(x[:3], lay.norm_w, EPS, None, None, "silu", False, False, want_y32=True)
+    assert torch.count_nonzero(y32) == 0
+
+
+def test_prefill_chunk_512(dev):
+    """A 512-token prefill chunk (survey config 5 geometry, one layer): hot
+    fp8 dense product plus the chunk's union of cold neurons (40 %).  Oracle
+    rows spread over every 64-row tile; all rows against a float32 torch
+    reference over the same dequantised weights."""
+    g = torch.Generator(device=dev).manual_seed(51)
+    lay = SyntheticLayer(g, 14336, 3584, device=dev)
+    n_cold = lay.records.shape[0]
+    slots = torch.randperm(n_cold, generator=g, device=dev)[: int(0.4 * n_cold)].int()
+    cold = ColdNeurons.from_slots(_section(lay), slots)
+    M = 512
+    x = torch.randn((M, H), generator=g, device=dev).to(torch.bfloat16).half()
+    out, y32 = _ffn(x, lay.norm_w, EPS, lay.hot, cold, "silu", False, True, want_y32=True)
+    torch.cuda.synchronize()
+    rows = [0, 70, 141, 200, 255, 300, 383, 447, 511]
+    xn = normed_f16(x[rows], lay.norm_w)
+    Gh, Uh, Dh = hot_dense(lay.hot)
+    Gc, Uc, Dc = cold_dense(lay.records, slots)
+    ref = O.sparse_ffn(xn, "silu", False, Gh, Uh, Dh, Gc, Uc, Dc)
+    y = y32[rows].cpu().numpy()
+    for r in range(len(rows)):
+        assert_ffn_close(y[r], ref[r], what=f"prefill row {rows[r]}")
+    # all 512 rows: float32 torch over the dequantised weights
+    f32 = lambda a: torch.as_tensor(a, dtype=torch.float32, device=dev)
+    xn_all = torch.as_tensor(normed_f16(x, lay.norm_w), dtype=torch.float32, device=dev)
+    hh = torch.nn.functional.silu(xn_all @ f32(Gh).T) * (xn_all @ f32(Uh).T)
+    hc = torch.nn.functional.silu(xn_all @ f32(Gc).T) * (xn_all @ f32(Uc).T)
+    ref_all = (hh @ f32(Dh).T + hc @ f32(Dc).T).double().cpu().numpy()
+    assert_ffn_close(y32.cpu().numpy(), ref_all, what="prefill all rows")
