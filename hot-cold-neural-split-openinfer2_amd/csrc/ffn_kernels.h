@@ -124,7 +124,7 @@ struct BUpArgs {
   const float* hot_gbias;
   uint16_t* hh;             // (Mpad, ldh) fp16 hot activations, zero past n_hot
   int ldh;
-  int hot_wg;               // ldh / 64 workgroups of hot columns
+  int hot_wg;               // workgroups of hot columns (ldh / 64, or ldh / 16 for M <= 64)
   const uint8_t* records;
   int n_records;
   const float* cold_gbias;
@@ -133,10 +133,15 @@ struct BUpArgs {
   int cap;
   uint16_t* hc;             // (Mpad, ldc) fp16 cold activations
   int ldc;
+  int ksplit;               // K splits of the tiled kernel (1: it applies the activation)
+  float* pg;                // (ksplit, Mpad, ldp) partial gate sums, hot columns then cold
+  float* pu;
+  int ldp;                  // ldh + ldc
+  int Mpad;
 };
 
 struct BDownArgs {
-  int M, Mpad;
+  int M;
   const uint16_t* hh;
   int ldh;
   const uint8_t* down_q;
@@ -151,12 +156,10 @@ struct BDownArgs {
   const int32_t* dslots;
   const int32_t* total;
   int cap;
-  int cold_splits;
-  float* part;              // (hot_splits + cold_splits, Mpad, H) fp32 partial sums
+  float* y;                 // (M, H) fp32 output, accumulated with atomics
 };
 
 __global__ void k_bup(BUpArgs a);
-__global__ void k_bdown(BDownArgs a);
 __global__ void k_rmsnorm(const uint16_t* x, const uint16_t* w, float eps, uint16_t* out);
 
 size_t batch_ws_bytes(int M, int n_hot, int cap);

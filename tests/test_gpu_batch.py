@@ -35,7 +35,7 @@ def layer25(dev):
     return SyntheticLayer(g, 14336, 3584, device=dev), g
 
 
-@pytest.mark.parametrize("B", [2, 8, 64])
+@pytest.mark.parametrize("B", [2, 8, 17, 64])
 def test_batch_decode_shared_active_set(dev, layer25, B):
     lay, g = layer25
     n_cold = lay.records.shape[0]
@@ -45,7 +45,8 @@ def test_batch_decode_shared_active_set(dev, layer25, B):
     out, y32 = _ffn(x, lay.norm_w, EPS, lay.hot, cold, "silu", False, add_residual=True,
                     want_y32=True)
     torch.cuda.synchronize()
-    rows = list(range(B)) if B <= 8 else [0, 1, 17, 31, 32, 63]
+    rows = list(range(B)) if B <= 8 else sorted({0, 1, B // 2, B - 2, B - 1})
+    assert max(rows) < B
     xn = normed_f16(x[rows], lay.norm_w)
     Gh, Uh, Dh = hot_dense(lay.hot)
     Gc, Uc, Dc = cold_dense(lay.records, slots)
