@@ -192,6 +192,55 @@ def measure_staging(layers, st, thr, x0, stream, steps, mean_active):
     return out
 
 
+def measure_multi_token(layers, dev, M, frac, reps, seed=1):
+    """M tokens through the 32 layers on the matrix-core path (batch decode at
+    small M, a prefill chunk at M = 512): each layer's cold half is a fixed
+    random `frac` of its cold neurons (the batch's union).  The 32-layer
+    chain is captured once in a graph and replayed, so `us` is GPU time."""
+    import torch
+    from oi2.layer import ColdNeurons, _ffn
+    from oi2.store import ColdSection
+    g = torch.Generator(device=dev).manual_seed(seed)
+    colds = []
+    for l in layers:
+        n = l.records.shape[0]
+        slots = torch.randperm(n, generator=g, device=dev)[: int(frac * n)].int()
+        sec = ColdSection(0, l.cold_ids.cpu().numpy(), l.records, l.lut, l.lut.cpu().numpy(), INTER)
+        colds.append(ColdNeurons.from_slots(sec, slots))
+    x0 = torch.randn((M, H), generator=g, device=dev).half()
+    stream = torch.cuda.Stream(device=dev)
+
+    def chain(x):
+        for l, c in zip(layers, colds):
+            x = _ffn(x, l.norm_w, EPS, l.hot, c, "silu", False, add_residual=True)
+        return x
+
+    with torch.cuda.stream(stream):
+        chain(x0)                                   # warm (workspaces, library)
+    stream.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        y = chain(x0)
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    n_act = int(frac * (INTER - N_HOT))
+    flop = N_LAYERS * 2 * M * H * (N_HOT + n_act) * 3
+    weight_bytes = N_LAYERS * (3 * N_HOT * H + n_act * 6400)
+    assert torch.isfinite(y.float()).all()
+    del graph
+    return {"tokens": M, "active_cold_frac": frac, "us_per_32_layers": us,
+            "tok_s": M / (us * 1e-6), "tflops": flop / (us * 1e-6) / 1e12,
+            "mfma_frac_fp16_dense": flop / (us * 1e-6) / 2.5e15,
+            "weight_gbs": weight_bytes / (us * 1e-6) / 1e9}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -200,6 +249,8 @@ def main():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--profile-reps", type=int, default=8)
     ap.add_argument("--cpu-tokens", type=int, default=6)
+    ap.add_argument("--no-multi-token", dest="multi_token", action="store_false",
+                    help="skip the 8 / 64 / 512-token matrix-core measurements")
     ap.add_argument("--staging-steps", type=int, default=64,
                     help="tokens timed with the cold store in pinned host memory (0: skip)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
@@ -277,6 +328,14 @@ def main():
     log(f"ffn_up {up_us:.2f} us/launch {up_gbs:.0f} GB/s; ffn_down {down_us:.2f} us "
         f"{down_gbs:.0f} GB/s; mean active cold {mean_active:.0f}")
 
+    multi = None
+    if args.multi_token:
+        multi = {}
+        for M, frac in ((8, 0.15), (64, 0.50), (512, 0.40)):
+            multi[f"m{M}"] = measure_multi_token(layers, dev, M, frac, reps=5)
+            log(f"{M} tokens x 32 layers: {multi[f'm{M}']['us_per_32_layers']:.0f} us, "
+                f"{multi[f'm{M}']['tflops']:.1f} TFLOP/s, {multi[f'm{M}']['weight_gbs']:.0f} GB/s")
+
     staging = None
     if args.staging_steps > 0:
         staging = measure_staging(layers, st, thr, xi, stream, args.staging_steps, mean_active)
@@ -327,6 +386,7 @@ def main():
         "cold_neurons_per_s": mean_active * N_LAYERS * tok_s,
         "cpu_baseline": cpu,
         "staging": staging,
+        "multi_token": multi,
     }
     print(json.dumps(out), flush=True)
     st.close()
