@@ -48,10 +48,19 @@ __device__ __forceinline__ float ssq16(const float v[16]) {
   return s;
 }
 
-__device__ __forceinline__ float r_from_parts(const float* parts, float eps) {
-  const f32x4 p = reinterpret_cast<const f32x4*>(parts)[lane_id()];
+// r from this lane's four partials (loaded early by the caller; all 64 lanes
+// of the wave take part).
+__device__ __forceinline__ float r_from_part(f32x4 p, float eps) {
   const float s = wave_sum((p.x + p.y) + (p.z + p.w));
   return rsqrtf(s * (1.0f / kH) + eps);
+}
+
+__device__ __forceinline__ f32x4 load_part(const float* parts) {
+  return reinterpret_cast<const f32x4*>(parts)[lane_id()];
+}
+
+__device__ __forceinline__ float r_from_parts(const float* parts, float eps) {
+  return r_from_part(load_part(parts), eps);
 }
 
 __device__ __forceinline__ void load_h16(const uint16_t* x, int e0, float v[16]) {
@@ -160,12 +169,25 @@ __device__ __forceinline__ void stage_xw(const uint16_t* xw, uint32_t* s_nat, ui
   __syncthreads();
 }
 
-__device__ __forceinline__ float token_r(const TokenIn& tk) {
-  return tk.use_norm ? r_from_parts(tk.ssq, tk.eps) : 1.0f;
+// This lane's sum-of-squares partials of the token (zero without a norm):
+// load before the role's barrier, turn into r after it.
+__device__ __forceinline__ f32x4 token_part(const TokenIn& tk) {
+  return tk.use_norm ? load_part(tk.ssq) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+}
+
+__device__ __forceinline__ float token_r(const TokenIn& tk, f32x4 part) {
+  return tk.use_norm ? r_from_part(part, tk.eps) : 1.0f;
 }
 
 // ── ffn_up roles ────────────────────────────────────────────────────────────
 
+// ── cold gate/up/act/down ───────────────────────────────────────────────────
+
+// One active item per wave at a time, taken 4 wg + w, + 4 wg_cold, ... from
+// the (chunked) list: gate and up against the paired x (fp16 dot2 over the
+// exact INT4 decode), h = act(...), and h * s * q over the item's down column
+// into 64 accumulators per lane; the four waves sum in LDS and the workgroup
+// writes one fp32 partial row of y, which ffn_down sums.
 __device__ void cold_role(const UpArgs& a, int wg, uint32_t* s_nat, uint32_t* s_pair,
                           float* s_red) {
   const int w = threadIdx.x >> 6, lane = lane_id();
@@ -197,12 +219,14 @@ __device__ void cold_role(const UpArgs& a, int wg, uint32_t* s_nat, uint32_t* s_
     }
   };
   if (valid) load_rec(slot);
+  float gbias = (valid && a.cold_gbias) ? a.cold_gbias[slot] : 0.0f;
+  const f32x4 part = token_part(a.tok);
   stage_xw(a.tok.xw, s_nat, s_pair);
   float acc[64];
 #pragma unroll
   for (int k = 0; k < 64; ++k) acc[k] = 0.0f;
   if (i < total) {
-    const float r = token_r(a.tok);
+    const float r = token_r(a.tok, part);
     // token pairs for elements [32 lane + 2048 it, +32), it = 0, 1
     f16x2 xc[2][16];
 #pragma unroll
@@ -232,7 +256,7 @@ __device__ void cold_role(const UpArgs& a, int wg, uint32_t* s_nat, uint32_t* s_
           }
         float g = r * wave_sum(pg[0] * s[0] + pg[1] * s[1]);
         const float u = r * wave_sum(pu[0] * s[2] + pu[1] * s[3]);
-        if (a.cold_gbias) g += a.cold_gbias[slot];
+        g += gbias;
         const float h = gated_act(g, u, a.relu, a.both);
         const float hs[2] = {h * s[4], h * s[5]};
         // the record's down column, elements [32 lane + 2048 it, +32)
@@ -254,6 +278,7 @@ __device__ void cold_role(const UpArgs& a, int wg, uint32_t* s_nat, uint32_t* s_
       slot = item_slot(a.act, excl, i);
       valid = slot >= 0 && slot < a.n_records;
       if (valid) load_rec(slot);
+      gbias = (valid && a.cold_gbias) ? a.cold_gbias[slot] : 0.0f;
     }
   }
   // sum the four waves in LDS (fixed order, padded against bank conflicts),
@@ -298,7 +323,18 @@ __device__ void pred_d_role_t(const UpArgs& a, int row) {
     for (int it = 0; it < 8; ++it) dw.v[it] = load16(reinterpret_cast<const uint8_t*>(drow + 8 * (lane + 64 * it)));
   }
   const bool norm = a.pd_norm_w && !a.pd_q;
-  const float r = norm ? r_from_parts(a.tok.ssq, a.tok.eps) : 1.0f;
+  // every input of the row issued before the first use
+  u32x4 xv[8], wv[8];
+  if (!a.pd_q) {
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int e0 = 8 * (lane + 64 * it);
+      xv[it] = *reinterpret_cast<const u32x4*>(a.tok.x + e0);
+      wv[it] = norm ? *reinterpret_cast<const u32x4*>(a.pd_norm_w + e0) : u32x4{0, 0, 0, 0};
+    }
+  }
+  const f32x4 part = norm ? load_part(a.tok.ssq) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  const float r = norm ? r_from_part(part, a.tok.eps) : 1.0f;
   float acc = 0.0f;
 #pragma unroll
   for (int it = 0; it < 8; ++it) {
@@ -308,15 +344,12 @@ __device__ void pred_d_role_t(const UpArgs& a, int row) {
 #pragma unroll
       for (int k = 0; k < 8; ++k) q[k] = a.pd_q[e0 + k];
     } else {
-      const u32x4 xv = *reinterpret_cast<const u32x4*>(a.tok.x + e0);
-      u32x4 wv = {0, 0, 0, 0};
-      if (norm) wv = *reinterpret_cast<const u32x4*>(a.pd_norm_w + e0);
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
-        float v0 = half_lo(xv[d]), v1 = half_hi(xv[d]);
+        float v0 = half_lo(xv[it][d]), v1 = half_hi(xv[it][d]);
         if (norm) {
-          v0 = xn_exact(v0, r, half_lo(wv[d]));
-          v1 = xn_exact(v1, r, half_hi(wv[d]));
+          v0 = xn_exact(v0, r, half_lo(wv[it][d]));
+          v1 = xn_exact(v1, r, half_hi(wv[it][d]));
         }
         q[2 * d] = BF16 ? round_bf16(v0) : v0;
         q[2 * d + 1] = BF16 ? round_bf16(v1) : v1;
@@ -365,9 +398,15 @@ __device__ void hot_up_role(const UpArgs& a, int wg, uint32_t* s_nat, uint32_t* 
     qg[1][it] = two ? load16(a.gate_q + off + kH) : u32x4{0, 0, 0, 0};
     qu[1][it] = two ? load16(a.up_q + off + kH) : u32x4{0, 0, 0, 0};
   }
+  // scales of neuron k0 + lane for lanes 0 and 1, and the norm partials
+  const int kl = k0 + (lane & 1);
+  const bool kv = lane < 2 && kl < a.n_hot;
+  const float gsc = kv ? a.gate_s[kl] : 0.0f, usc = kv ? a.up_s[kl] : 0.0f;
+  const float gbi = (kv && a.hot_gbias) ? a.hot_gbias[kl] : 0.0f;
+  const f32x4 part = token_part(a.tok);
   stage_xw(a.tok.xw, s_nat, s_pair);
   if (!one) return;
-  const float r = token_r(a.tok);
+  const float r = token_r(a.tok, part);
   float g[2] = {0.0f, 0.0f}, u[2] = {0.0f, 0.0f};
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
@@ -392,9 +431,8 @@ __device__ void hot_up_role(const UpArgs& a, int wg, uint32_t* s_nat, uint32_t* 
   }
   if (lane < 2 && (lane == 0 || two)) {
     const int k = k0 + lane;
-    float gg = r * (lane ? g[1] : g[0]) * a.gate_s[k];
-    const float uu = r * (lane ? u[1] : u[0]) * a.up_s[k];
-    if (a.hot_gbias) gg += a.hot_gbias[k];
+    const float gg = r * (lane ? g[1] : g[0]) * gsc + gbi;
+    const float uu = r * (lane ? u[1] : u[0]) * usc;
     a.h_hot[k] = gated_act(gg, uu, a.relu, a.both);
   }
 }
@@ -446,35 +484,55 @@ __device__ void pred_u_role(const DownArgs& a, int c, int* s_wcnt) {
   const int t = threadIdx.x, w = t >> 6, lane = lane_id();
   const int n = c * kSelChunk + t;
   bool keep = false;
+  const int lutv = (n < a.inter && a.lut) ? a.lut[n] : n;
   if (n < a.inter) {
+    // the row in batches of 64 rank entries, each batch's loads issued together
     float logit;
+    float acc = 0.0f;
     if (a.pu_bf16) {
       const uint16_t* urow = reinterpret_cast<const uint16_t*>(a.pu_w) + (size_t)n * a.pu_rank;
-      float acc = 0.0f;
-      for (int r0 = 0; r0 < a.pu_rank; r0 += 8) {
-        const u32x4 uv = *reinterpret_cast<const u32x4*>(urow + r0);
+      const float bias = bf16_bits_to_float(reinterpret_cast<const uint16_t*>(a.pu_b)[n]);
+      for (int rb = 0; rb < a.pu_rank; rb += 64) {
+        u32x4 uv[8];
 #pragma unroll
-        for (int d = 0; d < 4; ++d) {
-          acc = fmaf(bf16_bits_to_float((uint16_t)(uv[d] & 0xFFFFu)), a.pd_z[r0 + 2 * d], acc);
-          acc = fmaf(bf16_bits_to_float((uint16_t)(uv[d] >> 16)), a.pd_z[r0 + 2 * d + 1], acc);
+        for (int k = 0; k < 8; ++k)
+          uv[k] = rb + 8 * k < a.pu_rank ? *reinterpret_cast<const u32x4*>(urow + rb + 8 * k)
+                                         : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          if (rb + 8 * k >= a.pu_rank) break;
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            const int r = rb + 8 * k + 2 * d;
+            acc = fmaf(bf16_bits_to_float((uint16_t)(uv[k][d] & 0xFFFFu)), a.pd_z[r], acc);
+            acc = fmaf(bf16_bits_to_float((uint16_t)(uv[k][d] >> 16)), a.pd_z[r + 1], acc);
+          }
         }
       }
-      logit = acc + bf16_bits_to_float(reinterpret_cast<const uint16_t*>(a.pu_b)[n]);
+      logit = acc + bias;
     } else {
       const float* urow = reinterpret_cast<const float*>(a.pu_w) + (size_t)n * a.pu_rank;
-      float acc = 0.0f;
-      for (int r0 = 0; r0 < a.pu_rank; r0 += 4) {
-        const f32x4 uv = *reinterpret_cast<const f32x4*>(urow + r0);
+      const float bias = reinterpret_cast<const float*>(a.pu_b)[n];
+      for (int rb = 0; rb < a.pu_rank; rb += 64) {
+        f32x4 uv[16];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) acc = fmaf(uv[k], a.pd_z[r0 + k], acc);
+        for (int k = 0; k < 16; ++k)
+          uv[k] = rb + 4 * k < a.pu_rank ? *reinterpret_cast<const f32x4*>(urow + rb + 4 * k)
+                                         : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+          if (rb + 4 * k >= a.pu_rank) break;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc = fmaf(uv[k][e], a.pd_z[rb + 4 * k + e], acc);
+        }
       }
-      logit = acc + reinterpret_cast<const float*>(a.pu_b)[n];
+      logit = acc + bias;
     }
     if (a.logits_out) a.logits_out[n] = logit;
     if (a.probs_out) a.probs_out[n] = 1.0f / (1.0f + __expf(-logit));
     const bool fire = logit >= a.thr;
     if (a.mask_out) a.mask_out[n] = fire ? 1 : 0;
-    keep = fire && (a.lut == nullptr || a.lut[n] >= 0);
+    keep = fire && lutv >= 0;
   }
   if (a.sel_counts == nullptr) return;
   const uint64_t bal = __ballot(keep);
@@ -485,7 +543,7 @@ __device__ void pred_u_role(const DownArgs& a, int c, int* s_wcnt) {
   for (int ww = 0; ww < w; ++ww) base += s_wcnt[ww];
   if (keep) {
     const size_t pos = (size_t)c * kSelChunk + base + wpos;
-    a.sel_slots[pos] = a.lut ? a.lut[n] : n;
+    a.sel_slots[pos] = lutv;
     a.sel_ids[pos] = n;
   }
   if (t == 0) a.sel_counts[c] = s_wcnt[0] + s_wcnt[1] + s_wcnt[2] + s_wcnt[3];
@@ -521,6 +579,14 @@ __device__ void down_role(const DownArgs& a, int b, DownShared& sh) {
   // lines holding those rows' nibbles of every cold record.
   const int tile = (b & 7) * (kDownWG / 8) + (b >> 3);
   const int j0 = tile * kRowsPerDownWG;
+  const int cold_total = a.cold_total ? *a.cold_total : 0;
+  // per-row operands of the epilogue, loaded with everything else
+  float dsc[4];
+#pragma unroll
+  for (int rr = 0; rr < 4; ++rr) dsc[rr] = a.n_hot > 0 ? a.down_s[j0 + 4 * w + rr] : 0.0f;
+  const int je = j0 + (t & (kRowsPerDownWG - 1));
+  const float res_v = a.res ? half_bits_to_float(a.res[je]) : 0.0f;
+  const float nw_v = a.next_norm_w ? half_bits_to_float(a.next_norm_w[je]) : 1.0f;
 
   // 1. hot down rows: 4 per wave (chunks past the row stride are zero)
   const int nch = a.down_stride >> 4;
@@ -556,12 +622,24 @@ __device__ void down_role(const DownArgs& a, int b, DownShared& sh) {
   }
   // 2. cold: sum the partial rows of ffn_up's cold workgroups for rows
   //    [j0, j0+16): thread t reads 4 rows (t & 3) of partials p = t/4 + 64 m.
+  //    The first 256 rows are loaded without waiting for the active count
+  //    (rows past it hold stale data and are dropped below).
   f32x4 cp = {0.0f, 0.0f, 0.0f, 0.0f};
-  if (a.cold_total) {
-    const int total = *a.cold_total;
-    int n_part = (total + kColdPerWG - 1) / kColdPerWG;
+  if (a.cold_part && a.cold_wg > 0) {
+    constexpr int kPre = 4;
+    f32x4 pv[kPre];
+#pragma unroll
+    for (int k = 0; k < kPre; ++k) {
+      const int p = (t >> 2) + 64 * k;
+      pv[k] = p < a.cold_wg ? *reinterpret_cast<const f32x4*>(a.cold_part + (size_t)p * kH + j0 + 4 * (t & 3))
+                            : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+    int n_part = (cold_total + kColdPerWG - 1) / kColdPerWG;
     n_part = n_part < a.cold_wg ? n_part : a.cold_wg;
-    for (int p = t >> 2; p < n_part; p += kThreads / 4)
+#pragma unroll
+    for (int k = 0; k < kPre; ++k)
+      if ((t >> 2) + 64 * k < n_part) cp += pv[k];
+    for (int p = (t >> 2) + 64 * kPre; p < n_part; p += kThreads / 4)
       cp += *reinterpret_cast<const f32x4*>(a.cold_part + (size_t)p * kH + j0 + 4 * (t & 3));
   }
   // 3. hot rows
@@ -605,7 +683,7 @@ __device__ void down_role(const DownArgs& a, int b, DownShared& sh) {
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       const int j = j0 + 4 * w + rr;
-      sh.yhot[4 * w + rr] = (a.n_hot > 0) ? yh[rr] * a.down_s[j] : 0.0f;
+      sh.yhot[4 * w + rr] = (a.n_hot > 0) ? yh[rr] * dsc[rr] : 0.0f;
     }
   }
   __syncthreads();
@@ -614,13 +692,12 @@ __device__ void down_role(const DownArgs& a, int b, DownShared& sh) {
     const float y = sh.yhot[t] + yc;
     const int j = j0 + t;
     if (a.y32) a.y32[j] = y;
-    const uint16_t ob = float_to_half_bits((a.res ? half_bits_to_float(a.res[j]) : 0.0f) + y);
+    const uint16_t ob = float_to_half_bits(res_v + y);
     if (a.out) a.out[j] = ob;
     if (a.out2) a.out2[j] = ob;
     const float o = half_bits_to_float(ob);
     sh.out[t] = o;
-    if (a.xw_out)
-      a.xw_out[j] = float_to_half_bits(a.next_norm_w ? o * half_bits_to_float(a.next_norm_w[j]) : o);
+    if (a.xw_out) a.xw_out[j] = float_to_half_bits(a.next_norm_w ? o * nw_v : o);
   }
   if (a.ssq_out) {
     __syncthreads();

@@ -514,6 +514,11 @@ int oi2_stack_set_staging(oi2_stack* s, int32_t copy_workgroups) {
   OI2_CHECK_HIP(hipDeviceSynchronize());
   staging_free(s);
   if (!copy_workgroups) return OI2_OK;
+  for (int L = 0; L < s->n_layers; ++L)
+    if (s->layers[L].l.cold.n_records > 0 && s->layers[L].l.cold.gate_bias) {
+      set_error("layer %d: staging does not support a cold gate bias", L);
+      return OI2_EUNSUPPORTED;
+    }
   hipError_t e = hipStreamCreateWithFlags(&s->side, hipStreamNonBlocking);
   for (int b = 0; b < 2 && e == hipSuccess; ++b)
     e = hipMalloc((void**)&s->stage[b], (size_t)s->cold_cap * kRecBytes);
