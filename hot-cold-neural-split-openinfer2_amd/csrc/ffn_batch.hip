@@ -35,6 +35,7 @@
 namespace oi2 {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32_a2 __attribute__((aligned(2)));
 
@@ -63,6 +64,32 @@ __device__ __forceinline__ h8 int4x8_h8(uint32_t d) {
   int4x8_to_f16x2x4(d, p);
   return cat8(p[0], p[1], p[2], p[3]);
 }
+
+// 8 INT4 (one dword, K order) times an fp16 scale, in int4x8_h8's order.
+// ((d >> 4k) & 0x000F000F) ^ 0x64086408 is the fp16 1024 + (n ^ 8) for the
+// nibble pair (k, k + 4); minus 1032 that is the signed nibble, exactly, and
+// the product with the scale rounds once.
+__device__ __forceinline__ h8 int4x8_h8_scaled(uint32_t d, _Float16 sc) {
+  u32x4 m;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) m[k] = ((d >> (4 * k)) & 0x000F000Fu) ^ 0x64086408u;
+  return (__builtin_bit_cast(h8, m) + (_Float16)-1032.0f) * sc;
+}
+
+// Raw buffer loads: one descriptor per operand, a 32-bit per-lane offset and a
+// uniform (SGPR) offset, instead of a 64-bit address per row.  Reads at or
+// past `bytes` return zero.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t buf_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4 bload16(rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)voff, (int)soff, 0));
+}
+__device__ __forceinline__ uint16_t bload2(rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, (int)voff, (int)soff, 0);
+}
+constexpr uint32_t kNoOffset = 0x80000000u;   // a lane offset past every buffer
 
 __device__ __forceinline__ f32x4 mfma16(h8 a, h8 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
@@ -271,6 +298,311 @@ __global__ __launch_bounds__(kThreads) void k_bact(BUpArgs a) {
       a.hc[(size_t)m * a.ldc + i] = float_to_half_bits(h);
     }
   }
+}
+
+// ── gate/up and hot down for prefill-sized token counts ─────────────────────
+//
+// v_mfma_f32_32x32x16_f16 (lane l, element i): A[l%32][8(l/32)+i],
+// B[8(l/32)+i][l%32]; output element j is D[8(j/4) + 4(l/32) + j%4][l%32].
+// It sustains about 1.45x the 16x16x32 rate on gfx950.  Each 128-wide K block
+// is split between the two lane halves as 64 contiguous K, 8 per MFMA step.
+//
+// Workgroup tile: 32 MS tokens x 4 waves, each wave one 32-column B tile per
+// NB: 32 weight rows as gate and up, or 64 down rows.  The token tile (A) goes
+// through two LDS buffers, one barrier per K block.  Each wave streams its own
+// B rows from global memory into registers a whole block ahead, so the
+// weights are read once per token tile and never touch LDS.  The barrier
+// waits for LDS traffic only (lgkmcnt), not for the global loads in flight.
+//
+// Cold rows: INT4 nibbles times their group scale, rounded once to fp16 (the
+// product needs up to 14 significant bits), so every K block accumulates
+// straight into the fp32 tile.
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ f32x16 mfma32(h8 a, h8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// A tile rows m0 .. m0 + 32 MS - 1: thread t loads 16-byte chunk t & 15 of
+// rows t / 16 + 16 i; rows >= M lie past the descriptor's range and read as
+// zero.  The K block goes in the uniform offset.
+template <int MS>
+struct ARows {
+  rsrc_t r;
+  uint32_t voff[2 * MS];
+  __device__ __forceinline__ ARows(const uint16_t* A, int ld, int M, int m0) {
+    const int t = threadIdx.x;
+    r = buf_rsrc(A, (uint32_t)M * ld * 2);
+#pragma unroll
+    for (int i = 0; i < 2 * MS; ++i) voff[i] = ((uint32_t)(m0 + (t >> 4) + 16 * i) * ld + 8 * (t & 15)) * 2;
+  }
+  __device__ __forceinline__ void load(int kb, u32x4 (&ra)[2 * MS]) const {
+#pragma unroll
+    for (int i = 0; i < 2 * MS; ++i) ra[i] = bload16(r, voff[i], kb * kBK * 2);
+  }
+};
+
+// The loaded chunks into s[32 MS][kLdA]; PAIR as in stage_a.
+template <int NR, bool PAIR>
+__device__ __forceinline__ void store_a_rows(const u32x4 (&r)[NR], uint16_t* s) {
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < NR; ++i) {
+    u32x4 v = r[i];
+    if (PAIR) {
+      const uint32_t d0 = v.x, d1 = v.y, d2 = v.z, d3 = v.w;
+      v.x = (d0 & 0xFFFFu) | (d2 << 16);
+      v.y = (d0 >> 16) | (d2 & 0xFFFF0000u);
+      v.z = (d1 & 0xFFFFu) | (d3 << 16);
+      v.w = (d1 >> 16) | (d3 & 0xFFFF0000u);
+    }
+    *reinterpret_cast<u32x4*>(s + ((t >> 4) + 16 * i) * kLdA + 8 * (t & 15)) = v;
+  }
+}
+
+// A fragment of 32-row subtile ms, K step s (0..7) of the staged block.
+__device__ __forceinline__ h8 a_frag32(const uint16_t* s, int ms, int step) {
+  const int l = lane_id();
+  return *reinterpret_cast<const h8*>(s + (32 * ms + (l & 31)) * kLdA + 64 * (l >> 5) + 8 * step);
+}
+
+// One wave's B operand for a K block: NB tiles of 32 rows (lane row l & 31),
+// 64 contiguous K per lane half, held per 8-wide K step s: fp8 rows as two
+// dwords, INT4 records as one dword plus the group scale.
+template <int NB, bool INT4>
+struct BRegs {
+  uint32_t q[8][NB][INT4 ? 1 : 2];
+  uint16_t sc[NB];
+};
+
+// The wave's B fragments of K step s (0..7) in fp16.
+template <int NB, bool INT4>
+__device__ __forceinline__ void b_frags(const BRegs<NB, INT4>& b, int s, h8 (&bf)[NB]) {
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    if constexpr (INT4)
+      bf[nb] = int4x8_h8_scaled(b.q[s][nb][0], __builtin_bit_cast(_Float16, b.sc[nb]));
+    else
+      bf[nb] = fp8x8_h8(b.q[s][nb][0], b.q[s][nb][1]);
+  }
+}
+
+// MS x NB MFMA tiles for the eight K steps of one block.  While step s
+// multiplies, the B fragments of step s + 1 are converted, the raw B
+// registers of a load group (16 bytes per lane: two fp8 steps or four INT4
+// steps) are refilled with block kn's data (the next block, loaded a whole
+// block ahead) once its last step is converted, and each A fragment is
+// re-read from LDS for step s + 1 as soon as its last MFMA of step s is
+// issued.  The scheduling groups interleave each MFMA with VALU work and
+// spread the LDS reads, so the matrix core, the VALU and LDS overlap.
+template <int MS, int NB, bool INT4, typename LoadGroup>
+__device__ __forceinline__ void mma_block(BRegs<NB, INT4>& b, const uint16_t* sA, int kn,
+                                          LoadGroup load_group, f32x16 (&acc)[MS][NB]) {
+  constexpr int kValuPerMfma = INT4 ? 4 : 1;
+  constexpr int G = INT4 ? 4 : 2;   // steps per load group
+  h8 av[MS], bf[2][NB];
+#pragma unroll
+  for (int ms = 0; ms < MS; ++ms) av[ms] = a_frag32(sA, ms, 0);
+  b_frags<NB, INT4>(b, 0, bf[0]);
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    if (s < 7) {
+      b_frags<NB, INT4>(b, s + 1, bf[(s + 1) & 1]);
+      if ((s + 1) % G == G - 1) load_group(kn, (s + 1) / G, b);
+    }
+#pragma unroll
+    for (int ms = 0; ms < MS; ++ms) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) acc[ms][nb] = mfma32(av[ms], bf[s & 1][nb], acc[ms][nb]);
+      if (s < 7) av[ms] = a_frag32(sA, ms, s + 1);
+    }
+#pragma unroll
+    for (int i = 0; i < MS * NB; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);               // one MFMA
+      if (s < 7) {
+        __builtin_amdgcn_sched_group_barrier(0x002, kValuPerMfma, 0);  // VALU
+        if (i % NB == NB - 1) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+      }
+    }
+  }
+}
+
+// K blocks [kb0, kb1) of A (ld halves per row) times the wave's B rows, into
+// acc.  load_group(kb, g, BRegs&) loads load group g of block kb.  sA holds two
+// 32 MS x kLdA buffers.  Every iteration loads the next block (the last one
+// reloads itself), so the loop body has no branches.
+template <int MS, int NB, bool INT4, bool PAIR, typename LoadGroup>
+__device__ __forceinline__ void pgemm_loop(const uint16_t* A, int ld, int M, int m0, int kb0, int kb1,
+                                           uint16_t* sA, LoadGroup load_group, f32x16 (&acc)[MS][NB]) {
+  const ARows<MS> arows(A, ld, M, m0);
+  u32x4 ra[2 * MS];
+  BRegs<NB, INT4> b;
+  arows.load(kb0, ra);
+#pragma unroll
+  for (int g = 0; g < (INT4 ? 2 : 4); ++g) load_group(kb0, g, b);
+  store_a_rows<2 * MS, PAIR>(ra, sA);
+  lds_barrier();
+  for (int kb = kb0; kb < kb1; ++kb) {
+    const int kn = min(kb + 1, kb1 - 1);
+    uint16_t* cur = sA + ((kb - kb0) & 1) * (32 * MS * kLdA);
+    uint16_t* nxt = sA + ((kb - kb0 + 1) & 1) * (32 * MS * kLdA);
+    arows.load(kn, ra);
+    // sched_barrier(0) keeps these loads issued before the MFMAs (the
+    // scheduler would otherwise sink them to shorten register lifetimes)
+    __builtin_amdgcn_sched_barrier(0);
+    mma_block<MS, NB, INT4>(b, cur, kn, load_group, acc);
+    __builtin_amdgcn_sched_barrier(0);
+    store_a_rows<2 * MS, PAIR>(ra, nxt);
+    lds_barrier();
+  }
+}
+
+// Gate/up for 32 MS tokens x 128 weight rows (hot rows first, then items of
+// the dense active list).  Wave w: rows r0 + 32 w + (l & 31); B tile 0 is the
+// gate row, tile 1 the up row.  The linear workgroup index is mapped so that
+// the token tiles of one row tile run on the same XCD (workgroups go
+// round-robin over the 8 XCDs), sharing its L2 for the weights.
+template <int MS>
+__global__ __launch_bounds__(kThreads) void k_pgemm_up(BUpArgs a, int hot_tiles, int n_tiles, int mt) {
+  __shared__ __attribute__((aligned(16))) uint16_t sA[2 * 32 * MS * kLdA];
+  const int b = blockIdx.x;
+  const int q = b >> 3;
+  const int nt = (q / mt) * 8 + (b & 7), mtile = q % mt;
+  if (nt >= n_tiles) return;   // the whole workgroup
+  const int m0 = mtile * 32 * MS;
+  const int w = threadIdx.x >> 6, l = lane_id();
+  f32x16 acc[MS][2];
+#pragma unroll
+  for (int ms = 0; ms < MS; ++ms) acc[ms][0] = acc[ms][1] = f32x16{};
+
+  if (nt < hot_tiles) {
+    const int row = nt * 128 + 32 * w + (l & 31);
+    const bool ok = row < a.n_hot;
+    // rows >= n_hot lie past the descriptors and read as zero
+    const uint32_t voff = (uint32_t)row * kH + 64 * (l >> 5);
+    const rsrc_t rg = buf_rsrc(a.gate_q, (uint32_t)a.n_hot * kH);
+    const rsrc_t ru = buf_rsrc(a.up_q, (uint32_t)a.n_hot * kH);
+    const float sg = ok ? a.gate_s[row] : 0.f, su = ok ? a.up_s[row] : 0.f;
+    const float gb = (ok && a.hot_gbias) ? a.hot_gbias[row] : 0.f;
+    auto load_b = [&](int kb, int g, BRegs<2, false>& bb) {   // steps 2g, 2g + 1
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) {
+        const u32x4 v = bload16(nb == 0 ? rg : ru, voff + 16 * g, kb * kBK);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bb.q[2 * g + e / 2][nb][e & 1] = v[e];
+      }
+    };
+    pgemm_loop<MS, 2, false, false>(a.xn, kH, a.M, m0, 0, kH / kBK, sA, load_b, acc);
+#pragma unroll
+    for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int m = m0 + 32 * ms + 8 * (j >> 2) + 4 * (l >> 5) + (j & 3);
+        if (m >= a.M) continue;
+        const float h = ok ? gated_act(fmaf(acc[ms][0][j], sg, gb), acc[ms][1][j] * su, a.relu, a.both) : 0.f;
+        a.hh[(size_t)m * a.ldh + row] = float_to_half_bits(h);
+      }
+    return;
+  }
+
+  const int total = min(*a.total, a.cap);
+  const int i0 = (nt - hot_tiles) * 128;
+  if (i0 >= total) return;   // the whole workgroup
+  const int item = i0 + 32 * w + (l & 31);
+  const int slot = item < total ? a.dslots[item] : -1;
+  const bool ok = slot >= 0 && slot < a.n_records;
+  // invalid items point past the records and read as zero
+  const uint32_t vrec = ok ? (uint32_t)slot * kRecBytes : kNoOffset;
+  const rsrc_t rr = buf_rsrc(a.records, (uint32_t)a.n_records * kRecBytes);
+  const float gb = (ok && a.cold_gbias) ? a.cold_gbias[slot] : 0.f;
+  // gate nibbles at kOffGate + 64 kb, up at kOffUp + 64 kb (this lane's 32
+  // bytes at 32 (l / 32)); the block's scales at kOffScales + 2 kb and + 64
+  auto load_b = [&](int kb, int g, BRegs<2, true>& bb) {   // steps 4g .. 4g + 3
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      const u32x4 v = bload16(rr, vrec + (nb == 0 ? kOffGate : kOffUp) + 32 * (l >> 5) + 16 * g, 64 * kb);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bb.q[4 * g + e][nb][0] = v[e];
+      // the scale serves all eight steps: refill it with the last group
+      if (g == 1) bb.sc[nb] = bload2(rr, vrec + (nb == 0 ? 0 : 2 * kGroups), kOffScales + 2 * kb);
+    }
+  };
+  pgemm_loop<MS, 2, true, true>(a.xn, kH, a.M, m0, 0, kH / kBK, sA, load_b, acc);
+#pragma unroll
+  for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int m = m0 + 32 * ms + 8 * (j >> 2) + 4 * (l >> 5) + (j & 3);
+      if (m >= a.M) continue;
+      const float h = ok ? gated_act(acc[ms][0][j] + gb, acc[ms][1][j], a.relu, a.both) : 0.f;
+      a.hc[(size_t)m * a.ldc + item] = float_to_half_bits(h);
+    }
+}
+
+// Hot down for 32 MS tokens x (4 waves x 32 NB outputs) over the K blocks of
+// one of `splits` ranges; y gets the scaled sums (stored when splits == 1,
+// else added atomically into a zeroed y).  Same XCD-aware index mapping.
+template <int MS, int NB>
+__global__ __launch_bounds__(kThreads) void k_pgemm_down_hot(BDownArgs a, int mt, int splits) {
+  __shared__ __attribute__((aligned(16))) uint16_t sA[2 * 32 * MS * kLdA];
+  constexpr int kTileN = 4 * 32 * NB;
+  constexpr int kTiles = kH / kTileN;
+  const int b = blockIdx.x;
+  const int q = b >> 3, per = mt * splits;
+  const int nt = (q / per) * 8 + (b & 7), rem = q % per;
+  if (nt >= kTiles) return;   // the whole workgroup
+  const int mtile = rem % mt, split = rem / mt;
+  const int kb0 = split * a.hot_blocks / splits, kb1 = (split + 1) * a.hot_blocks / splits;
+  if (kb0 >= kb1) return;
+  const int m0 = mtile * 32 * MS;
+  const int w = threadIdx.x >> 6, l = lane_id();
+  int row[NB];
+  uint32_t voff[NB];
+  const rsrc_t rd = buf_rsrc(a.down_q, (uint32_t)kH * a.down_stride);
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    row[nb] = nt * kTileN + 32 * NB * w + 32 * nb + (l & 31);
+    voff[nb] = (uint32_t)row[nb] * a.down_stride + 64 * (l >> 5);
+  }
+  f32x16 acc[MS][NB];
+#pragma unroll
+  for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[ms][nb] = f32x16{};
+  // K bytes past the row stride are zero (the hot activations there are zero
+  // too, but the bytes belong to the next row)
+  auto load_b = [&](int kb, int g, BRegs<NB, false>& bb) {   // steps 2g, 2g + 1
+    const bool in = kb * kBK + 64 * (l >> 5) + 16 * g < a.down_stride;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const u32x4 v = bload16(rd, voff[nb] + 16 * g, kb * kBK);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bb.q[2 * g + e / 2][nb][e & 1] = in ? v[e] : 0u;
+    }
+  };
+  pgemm_loop<MS, NB, false, false>(a.hh, a.ldh, a.M, m0, kb0, kb1, sA, load_b, acc);
+  float sd[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) sd[nb] = a.down_s[row[nb]];
+#pragma unroll
+  for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int m = m0 + 32 * ms + 8 * (j >> 2) + 4 * (l >> 5) + (j & 3);
+        if (m >= a.M) continue;
+        float* p = a.y + (size_t)m * kH + row[nb];
+        if (splits == 1)
+          *p = acc[ms][nb][j] * sd[nb];   // the first and only hot writer
+        else
+          unsafeAtomicAdd(p, acc[ms][nb][j] * sd[nb]);
+      }
 }
 
 // ── gate/up for at most 64 tokens ───────────────────────────────────────────
@@ -693,12 +1025,17 @@ __global__ __launch_bounds__(kThreads) void k_bcompact(ActiveList al, int cap, i
 
 struct BatchPlan {
   int M, Mpad, mt, ldh, hot_blocks, cap, ldc, hot_splits, ksplit;
+  bool prefill;
+  int pms, pmt;   // prefill tiles: 32-token subtiles per tile, token tiles
   size_t off_xn, off_hh, off_hc, off_dslots, off_total, off_y, off_pg, off_pu, bytes;
 };
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-constexpr int kSkinnyMax = 16;   // token counts up to this use the one-tile split-K kernels
+constexpr int kSkinnyMax = 16;    // token counts up to this use the one-tile split-K kernels
+constexpr int kPrefillMin = 192;  // token counts from this use the 128-row tile kernels
+
+static int prefill_ms(int M) { return M >= 384 ? 4 : 2; }   // 32-token subtiles per tile
 
 static BatchPlan batch_plan(int M, int n_hot, int cap) {
   BatchPlan p{};
@@ -708,10 +1045,18 @@ static BatchPlan batch_plan(int M, int n_hot, int cap) {
   p.ldh = n_hot > 0 ? (n_hot + kBK - 1) / kBK * kBK : 0;
   p.hot_blocks = p.ldh / kBK;
   p.cap = cap;
-  p.ldc = cap > 0 ? (cap + kBN - 1) / kBN * kBN : 0;
-  p.hot_splits = p.mt >= 4 ? 1 : 4 / p.mt;
+  p.ldc = cap > 0 ? (cap + 127) / 128 * 128 : 0;
+  p.prefill = M >= kPrefillMin;
+  if (p.prefill) {
+    p.pms = prefill_ms(M);
+    p.pmt = (M + 32 * p.pms - 1) / (32 * p.pms);
+    // hot down: 16 output tiles x token tiles x K splits, about 256 workgroups
+    p.hot_splits = std::max(1, std::min(p.hot_blocks, 256 / (16 * p.pmt)));
+  } else {
+    p.hot_splits = p.mt >= 4 ? 1 : 4 / p.mt;
+  }
   // tiled gate/up with few token tiles: split K over workgroups
-  p.ksplit = (M > kSkinnyMax && p.mt < 4) ? 4 / p.mt : 1;
+  p.ksplit = (M > kSkinnyMax && !p.prefill && p.mt < 4) ? 4 / p.mt : 1;
   size_t o = 0;
   p.off_xn = o;
   o = align256(o + (size_t)M * kH * 2);
@@ -832,11 +1177,19 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
   da.y = y;
 
   if (p.ldh + p.ldc > 0) {
-    if (skinny)
+    if (skinny) {
       launch_skinny(ua, da, true, st);
-    else
+    } else if (p.prefill) {
+      const int hot_tiles = p.ldh / 128, n_tiles = hot_tiles + p.ldc / 128;
+      const dim3 grid((n_tiles + 7) / 8 * 8 * p.pmt);
+      if (p.pms == 4)
+        hipLaunchKernelGGL(k_pgemm_up<4>, grid, dim3(kThreads), 0, st, ua, hot_tiles, n_tiles, p.pmt);
+      else
+        hipLaunchKernelGGL(k_pgemm_up<2>, grid, dim3(kThreads), 0, st, ua, hot_tiles, n_tiles, p.pmt);
+    } else {
       hipLaunchKernelGGL(k_bup, dim3(p.ldh / kBN + p.ldc / kBN, p.mt, ua.ksplit), dim3(kThreads), 0,
                          st, ua);
+    }
     OI2_CHECK_LAUNCH();
     if (ua.ksplit > 1) {
       const int n = M * ua.ldp;
@@ -854,11 +1207,18 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
     OI2_CHECK_LAUNCH();
   }
   if (n_hot) {
-    if (skinny)
+    if (skinny) {
       launch_skinny(ua, da, false, st);
-    else
+    } else if (p.prefill) {
+      const dim3 grid(16 * p.pmt * p.hot_splits);
+      if (p.pms == 4)
+        hipLaunchKernelGGL((k_pgemm_down_hot<4, 2>), grid, dim3(kThreads), 0, st, da, p.pmt, p.hot_splits);
+      else
+        hipLaunchKernelGGL((k_pgemm_down_hot<2, 2>), grid, dim3(kThreads), 0, st, da, p.pmt, p.hot_splits);
+    } else {
       hipLaunchKernelGGL(k_bdown_hot, dim3((kH / kBN) * p.hot_splits, p.mt), dim3(kThreads), 0, st,
                          da);
+    }
     OI2_CHECK_LAUNCH();
   }
   if (has_cold) {

@@ -88,16 +88,18 @@ def test_batch_drelu_union_of_firing_sets_equals_dense(dev):
         assert_ffn_close(y[r], dense[r], what=f"dReLU row {r}")
 
 
-def test_batch_edge_shapes(dev):
-    """Token count not a multiple of the 64-row tile, n_hot not a multiple of
-    the 128 K block, a chunked active list with an empty chunk, duplicates and
-    invalid slots, one half missing."""
+@pytest.mark.parametrize("B", [70, 200, 400])
+def test_batch_edge_shapes(dev, B):
+    """Token count not a multiple of the 64- or 128-row tile (70 on the
+    64-token tiles, 200 and 400 on the prefill tiles), n_hot not a multiple
+    of the 128 K block, a chunked active list with an empty chunk, duplicates
+    and invalid slots, one half missing."""
     g = torch.Generator(device=dev).manual_seed(6)
     lay = SyntheticLayer(g, 2000, 1000, device=dev)
     sec = _section(lay)
-    B = 70
     x = torch.randn((B, H), generator=g, device=dev).half()
-    rows = [0, 5, 63, 64, 69]
+    rows = sorted({0, 5, 63, 64, B // 2, B - 2, B - 1})
+    assert max(rows) < B
     xn = normed_f16(x[rows], lay.norm_w)
     Gh, Uh, Dh = hot_dense(lay.hot)
     sl = torch.full((3 * 40,), -7, dtype=torch.int32, device=dev)
