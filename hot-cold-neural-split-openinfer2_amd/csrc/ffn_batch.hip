@@ -605,6 +605,173 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_down_hot(BDownArgs a, int mt
       }
 }
 
+// Cold down for 128 tokens x 256 outputs (4 waves x 64) over a range of the
+// dense active list, 64 items per K block.  The records hold each item's down
+// nibbles contiguous along the outputs, while the MFMA wants 8 consecutive
+// items per lane, so every block is transposed on the way into LDS: thread
+// (ig = t & 7, jg = t >> 3) loads one dword (8 outputs) from each of the
+// items 8 ig .. 8 ig + 7, transposes the 8 x 8 nibble block in registers,
+// decodes each output's 8 items times their group scales (rounded once to
+// fp16, in int4x8_h8's pair order; the H tile is staged in the same order)
+// and writes 16-byte rows of the tile T[output][item].  The next block's
+// record dwords and H tile are loaded a block ahead; the record offsets of
+// the whole range sit in an LDS table, so no load waits for another.
+constexpr int kDcItems = 64;                // items per K block
+constexpr int kLdC = kDcItems + 8;          // LDS row of T and of the H tile, halves (144 B)
+constexpr int kDcMaxItems = 2048;           // items per workgroup (record offset table)
+
+// 8 x 8 nibble transpose: r[k] nibble n -> r[n] nibble k.
+__device__ __forceinline__ void nibble_transpose8(uint32_t (&r)[8]) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {   // 16-bit halves between rows k and k + 4
+    const uint32_t a = r[k], b = r[k + 4];
+    r[k] = (a & 0x0000FFFFu) | (b << 16);
+    r[k + 4] = (a >> 16) | (b & 0xFFFF0000u);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {   // bytes between rows k and k + 2
+    const int k = (i & 1) + 4 * (i >> 1);
+    const uint32_t a = r[k], b = r[k + 2];
+    r[k] = (a & 0x00FF00FFu) | ((b << 8) & 0xFF00FF00u);
+    r[k + 2] = ((a >> 8) & 0x00FF00FFu) | (b & 0xFF00FF00u);
+  }
+#pragma unroll
+  for (int k = 0; k < 8; k += 2) {   // nibbles between rows k and k + 1
+    const uint32_t a = r[k], b = r[k + 1];
+    r[k] = (a & 0x0F0F0F0Fu) | ((b << 4) & 0xF0F0F0F0u);
+    r[k + 1] = ((a >> 4) & 0x0F0F0F0Fu) | (b & 0xF0F0F0F0u);
+  }
+}
+
+__global__ __launch_bounds__(kThreads) void k_pgemm_down_cold(BDownArgs a, int mt, int splits) {
+  constexpr int MS = 4, NB = 2;
+  constexpr int kT = 256 * kLdC, kA = 128 * kLdC;   // halves per buffer
+  __shared__ __attribute__((aligned(16))) uint16_t sT[2 * kT];
+  __shared__ __attribute__((aligned(16))) uint16_t sH[2 * kA];
+  __shared__ uint32_t s_rec[kDcMaxItems];
+  const int b = blockIdx.x;
+  const int q = b >> 3, per = mt * splits;
+  const int jt = (q / per) * 8 + (b & 7), rem = q % per;
+  if (jt >= kH / 256) return;   // the whole workgroup
+  const int mtile = rem % mt, split = rem / mt;
+  const int total = min(*a.total, a.cap);
+  const int n_blk = (total + kDcItems - 1) / kDcItems;
+  const int kb0 = split * n_blk / splits, kb1 = (split + 1) * n_blk / splits;
+  if (kb0 >= kb1) return;   // the whole workgroup
+  const int t = threadIdx.x, w = t >> 6, l = lane_id();
+  const int m0 = mtile * 128, j0 = jt * 256;
+  const int i_base = kb0 * kDcItems, n_items = (kb1 - kb0) * kDcItems;
+
+  // record offsets of the range (items past the list or with invalid slots
+  // point past the records and read as zero)
+  for (int i = t; i < n_items; i += kThreads) {
+    const int it = i_base + i;
+    const int slot = it < total ? a.dslots[it] : -1;
+    s_rec[i] = (slot >= 0 && slot < a.n_records) ? (uint32_t)slot * kRecBytes : kNoOffset;
+  }
+  __syncthreads();
+
+  const rsrc_t rr = buf_rsrc(a.records, (uint32_t)a.n_records * kRecBytes);
+  const rsrc_t rh = buf_rsrc(a.hc, (uint32_t)a.M * a.ldc * 2);
+  const int ig = t & 7, jg = t >> 3;
+  const uint32_t dbyte = kOffDown + (j0 + 8 * jg) / 2;                        // this thread's dword
+  const uint32_t sbyte = kOffScales + 2 * (2 * kGroups + (j0 + 8 * jg) / kGroup);  // its down scale
+  // H tile: thread t loads chunk t & 7 (8 items) of token rows t / 8 + 32 r
+  uint32_t hoff[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) hoff[r] = ((uint32_t)(m0 + (t >> 3) + 32 * r) * a.ldc + 8 * (t & 7)) * 2;
+
+  uint32_t dq[8];
+  uint16_t dsc[8];
+  u32x4 hv[4];
+  auto load_block = [&](int kb) {
+    const int ib = (kb - kb0) * kDcItems + 8 * ig;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t vr = s_rec[ib + k];
+      dq[k] = __builtin_amdgcn_raw_buffer_load_b32(rr, (int)(vr + dbyte), 0, 0);
+      dsc[k] = bload2(rr, vr + sbyte, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) hv[r] = bload16(rh, hoff[r], kb * kDcItems * 2);
+  };
+  // decode the loaded block into buffer `buf`
+  auto store_block = [&](int buf) {
+    uint32_t c[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) c[k] = dq[k];
+    nibble_transpose8(c);
+    h8 sv;   // the items' scales in pair order (i0, i4, i1, i5, ...)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      sv[2 * k] = __builtin_bit_cast(_Float16, dsc[k]);
+      sv[2 * k + 1] = __builtin_bit_cast(_Float16, dsc[k + 4]);
+    }
+    uint16_t* T = sT + buf * kT;
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+      u32x4 m;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) m[k] = ((c[n] >> (4 * k)) & 0x000F000Fu) ^ 0x64086408u;
+      const h8 v = (__builtin_bit_cast(h8, m) + (_Float16)-1032.0f) * sv;
+      *reinterpret_cast<h8*>(T + (8 * jg + n) * kLdC + 8 * ig) = v;
+    }
+    uint16_t* Hs = sH + buf * kA;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const uint32_t d0 = hv[r].x, d1 = hv[r].y, d2 = hv[r].z, d3 = hv[r].w;
+      u32x4 v;
+      v.x = (d0 & 0xFFFFu) | (d2 << 16);
+      v.y = (d0 >> 16) | (d2 & 0xFFFF0000u);
+      v.z = (d1 & 0xFFFFu) | (d3 << 16);
+      v.w = (d1 >> 16) | (d3 & 0xFFFF0000u);
+      *reinterpret_cast<u32x4*>(Hs + ((t >> 3) + 32 * r) * kLdC + 8 * (t & 7)) = v;
+    }
+  };
+
+  f32x16 acc[MS][NB];
+#pragma unroll
+  for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[ms][nb] = f32x16{};
+  load_block(kb0);
+  store_block(0);
+  lds_barrier();
+  for (int kb = kb0; kb < kb1; ++kb) {
+    const int cur = (kb - kb0) & 1;
+    load_block(min(kb + 1, kb1 - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    const uint16_t* T = sT + cur * kT;
+    const uint16_t* Hs = sH + cur * kA;
+#pragma unroll
+    for (int st = 0; st < kDcItems / 16; ++st) {
+      const int col = 16 * st + 8 * (l >> 5);
+      h8 bf[NB], av[MS];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+        bf[nb] = *reinterpret_cast<const h8*>(T + (64 * w + 32 * nb + (l & 31)) * kLdC + col);
+#pragma unroll
+      for (int ms = 0; ms < MS; ++ms) av[ms] = *reinterpret_cast<const h8*>(Hs + (32 * ms + (l & 31)) * kLdC + col);
+#pragma unroll
+      for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) acc[ms][nb] = mfma32(av[ms], bf[nb], acc[ms][nb]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    store_block(cur ^ 1);
+    lds_barrier();
+  }
+#pragma unroll
+  for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int m = m0 + 32 * ms + 8 * (e >> 2) + 4 * (l >> 5) + (e & 3);
+        if (m < a.M) unsafeAtomicAdd(a.y + (size_t)m * kH + j0 + 64 * w + 32 * nb + (l & 31), acc[ms][nb][e]);
+      }
+}
+
 // ── gate/up for at most 64 tokens ───────────────────────────────────────────
 
 // Workgroup = 16 weight rows (hot rows, or items of the dense active list);
@@ -1051,7 +1218,8 @@ static BatchPlan batch_plan(int M, int n_hot, int cap) {
     p.pms = prefill_ms(M);
     p.pmt = (M + 32 * p.pms - 1) / (32 * p.pms);
     // hot down: 16 output tiles x token tiles x K splits, about 256 workgroups
-    p.hot_splits = std::max(1, std::min(p.hot_blocks, 256 / (16 * p.pmt)));
+    // hot down: 32 output tiles x token tiles x K splits, about 256 workgroups
+    p.hot_splits = std::max(1, std::min(p.hot_blocks, 256 / (32 * p.pmt)));
   } else {
     p.hot_splits = p.mt >= 4 ? 1 : 4 / p.mt;
   }
@@ -1210,18 +1378,27 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
     if (skinny) {
       launch_skinny(ua, da, false, st);
     } else if (p.prefill) {
-      const dim3 grid(16 * p.pmt * p.hot_splits);
+      const dim3 grid(32 * p.pmt * p.hot_splits);
       if (p.pms == 4)
-        hipLaunchKernelGGL((k_pgemm_down_hot<4, 2>), grid, dim3(kThreads), 0, st, da, p.pmt, p.hot_splits);
+        hipLaunchKernelGGL((k_pgemm_down_hot<4, 1>), grid, dim3(kThreads), 0, st, da, p.pmt, p.hot_splits);
       else
-        hipLaunchKernelGGL((k_pgemm_down_hot<2, 2>), grid, dim3(kThreads), 0, st, da, p.pmt, p.hot_splits);
+        hipLaunchKernelGGL((k_pgemm_down_hot<2, 1>), grid, dim3(kThreads), 0, st, da, p.pmt, p.hot_splits);
     } else {
       hipLaunchKernelGGL(k_bdown_hot, dim3((kH / kBN) * p.hot_splits, p.mt), dim3(kThreads), 0, st,
                          da);
     }
     OI2_CHECK_LAUNCH();
   }
-  if (has_cold) {
+  if (has_cold && p.prefill) {
+    // 16 output tiles x 128-token tiles x item ranges, about 256 workgroups;
+    // a range holds at most kDcMaxItems items
+    const int mtc = (M + 127) / 128;
+    const int n_blk = (cap + kDcItems - 1) / kDcItems;
+    const int min_splits = (n_blk + kDcMaxItems / kDcItems - 1) / (kDcMaxItems / kDcItems);
+    const int splits = std::max(min_splits, std::min(n_blk, std::max(1, 256 / (16 * mtc))));
+    hipLaunchKernelGGL(k_pgemm_down_cold, dim3(16 * mtc * splits), dim3(kThreads), 0, st, da, mtc, splits);
+    OI2_CHECK_LAUNCH();
+  } else if (has_cold) {
     // item ranges per output tile: ~512 workgroups in all, at least 2 steps each
     const int steps = (cap + kCI - 1) / kCI;
     int splits = (512 / (kH / kCT)) / p.mt;
