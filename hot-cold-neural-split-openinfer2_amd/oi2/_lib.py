@@ -79,6 +79,10 @@ _SIGS = {
                                             c_void_p]),
     "oi2_stack_trace": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "oi2_stack_destroy": (c_int32, [c_void_p]),
+    "oi2_section_bytes": (c_size_t, [c_int32]),
+    "oi2_quantize_section": (c_int32, [c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p,
+                                       c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t,
+                                       c_void_p]),
 }
 
 _lib = None

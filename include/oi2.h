@@ -225,6 +225,28 @@ int oi2_stack_trace(oi2_stack* s, uint16_t* xs, int32_t* counts, int32_t* slots,
                     void* stream);
 int oi2_stack_destroy(oi2_stack* s);
 
+/* ---- split writer ------------------------------------------------------- */
+/* Bytes of one cold_weights.bin section with n_cold records: the 16-byte
+ * <HHIq header, n_cold x 6400, zero padding to a 4096 multiple
+ * (splitter.py:229-254).  0 for a negative count. */
+size_t oi2_section_bytes(int32_t n_cold);
+/* The cold half of split_dense's per-layer loop on the device
+ * (splitter.py:229-256, quantize_int4 splitter.py:81-108): quantise n
+ * neurons to INT4 records and frame them as one section, byte-identical to
+ * the reference writer's.  Record k stores nids[k]; its gate, up and down
+ * vectors are read as
+ *   src[m][rows[k] * row_stride[m] + e * elem_stride[m]],  e = 0 .. 4095,
+ * for m = 0 (gate), 1 (up), 2 (down), fp32 device memory.  With the model's
+ * gate/up (I, H), down (H, I), rows = nids, row_stride = {H, H, 1} and
+ * elem_stride = {1, 1, I} this is gate[nid], up[nid] and down[:, nid].
+ * nids and rows are device arrays of n; row_stride and elem_stride are host
+ * arrays of 3.  section: 16-byte aligned device memory of at least
+ * oi2_section_bytes(n) bytes (header, records and padding all written). */
+int oi2_quantize_section(int32_t layer, int32_t expert, int32_t n, const uint16_t* nids,
+                         const int32_t* rows, const float* gate, const float* up, const float* down,
+                         const int64_t* row_stride, const int64_t* elem_stride, uint8_t* section,
+                         size_t section_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -49,6 +49,26 @@ def test_argument_validation_without_gpu():
     assert lib.oi2_ffn_workspace_bytes(1, 3584, 14336) >= (3584 + 2 * 14336 + 2048) * 4
 
 
+def test_split_writer_host_side():
+    """Section size is the reference writer's framing (16-byte header, 6400
+    per record, padding to 4096; splitter.py:229-254), and bad arguments are
+    rejected before any device work."""
+    lib = oi2.load_library()
+    for n in (0, 1, 16, 639, 640, 10752):
+        body = 16 + 6400 * n
+        assert lib.oi2_section_bytes(n) == (body + 4095) // 4096 * 4096
+        assert lib.oi2_section_bytes(n) == len(fmt.section_bytes(0, np.zeros((n, 6400), np.uint8)))
+    assert lib.oi2_section_bytes(-1) == 0
+    assert lib.oi2_quantize_section(0, 0, -1, None, None, None, None, None, None, None, None, 0,
+                                    None) == 1
+    assert b"non-negative" in lib.oi2_last_error()
+    assert lib.oi2_quantize_section(70000, 0, 0, None, None, None, None, None, None, None, None, 0,
+                                    None) == 1
+    assert lib.oi2_quantize_section(0, 0, 1, None, None, None, None, None, None, None, 64, 4096,
+                                    None) == 1   # section smaller than one record needs
+    assert b"smaller" in lib.oi2_last_error()
+
+
 def test_compute_entry_points_fail_loudly_without_gpu():
     if torch.cuda.is_available():
         pytest.skip("a GPU is present")
