@@ -241,6 +241,69 @@ def measure_multi_token(layers, dev, M, frac, reps, seed=1):
             "weight_gbs": weight_bytes / (us * 1e-6) / 1e9}
 
 
+def measure_gemm_reference(dev, n=8192, reps=10):
+    """The attainable fp16 matrix rate on this GPU: a vendor-library
+    (hipBLASLt through torch.matmul) n x n x n fp16 GEMM, fp32 accumulate."""
+    import torch
+    a = torch.randn((n, n), device=dev).half()
+    b = torch.randn((n, n), device=dev).half()
+    for _ in range(2):
+        torch.matmul(a, b)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        torch.matmul(a, b)
+    e1.record()
+    torch.cuda.synchronize()
+    s = e0.elapsed_time(e1) / 1e3 / reps
+    return 2.0 * n ** 3 / s / 1e12
+
+
+def measure_split_writer(dev, reps=5):
+    """The device split writer on one full layer: 10752 cold neurons of a
+    (14336, 4096) gate/up and (4096, 14336) down in fp32, quantised and framed
+    as one cold_weights.bin section; plus the restated reference quantiser
+    (one vector at a time, as splitter.py:229-247 does) on a CPU sample."""
+    import numpy as np
+    import torch
+    from oi2.split import quantize_section
+    from oracle import oracle as O
+    g = torch.Generator(device=dev).manual_seed(5)
+    gate = torch.randn((INTER, H), generator=g, device=dev) * 0.02
+    up = torch.randn((INTER, H), generator=g, device=dev) * 0.02
+    down = torch.randn((H, INTER), generator=g, device=dev) * 0.02
+    cold = np.arange(N_HOT, INTER)
+    sec = quantize_section(0, gate, up, down, cold)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        sec = quantize_section(0, gate, up, down, cold)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    n = cold.size
+    in_bytes = n * 3 * H * 4
+    # CPU: the reference quantises each neuron's three vectors in turn
+    sample = 48
+    vecs = [(gate[i].cpu().numpy(), up[i].cpu().numpy(), down[:, i].cpu().numpy())
+            for i in range(N_HOT, N_HOT + sample)]
+    t0 = time.perf_counter()
+    for gv, uv, dv in vecs:
+        for v in (gv, uv, dv):
+            O.quantize_int4_ref(v)
+    cpu_s = (time.perf_counter() - t0) / sample
+    del gate, up, down, sec
+    return {"neurons": int(n), "ms_per_layer": ms, "neurons_per_s": n / (ms * 1e-3),
+            "input_gbs": in_bytes / (ms * 1e-3) / 1e9,
+            "section_bytes": int(16 + n * 6400),
+            "model_32_layers_s": N_LAYERS * ms / 1e3,
+            "cpu_port_us_per_neuron": cpu_s * 1e6,
+            "cpu_port_model_32_layers_s": cpu_s * n * N_LAYERS,
+            "cpu_sample": f"{sample} neurons x 3 vectors through the restated quantize_int4, 1 thread"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -254,6 +317,8 @@ def main():
     ap.add_argument("--staging-steps", type=int, default=64,
                     help="tokens timed with the cold store in pinned host memory (0: skip)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--no-split-writer", dest="split_writer", action="store_false",
+                    help="skip the device split writer measurement")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 256 MiB device copy 8 times (the reference kernel "
@@ -330,11 +395,21 @@ def main():
 
     multi = None
     if args.multi_token:
-        multi = {}
-        for M, frac in ((8, 0.15), (64, 0.50), (512, 0.40)):
-            multi[f"m{M}"] = measure_multi_token(layers, dev, M, frac, reps=5)
-            log(f"{M} tokens x 32 layers: {multi[f'm{M}']['us_per_32_layers']:.0f} us, "
-                f"{multi[f'm{M}']['tflops']:.1f} TFLOP/s, {multi[f'm{M}']['weight_gbs']:.0f} GB/s")
+        multi = {"fp16_gemm_ref_tflops": measure_gemm_reference(dev)}
+        log(f"vendor fp16 GEMM 8192^3: {multi['fp16_gemm_ref_tflops']:.0f} TFLOP/s")
+        for M, frac in ((8, 0.15), (64, 0.50), (512, 0.40), (1024, 0.40)):
+            r = measure_multi_token(layers, dev, M, frac, reps=5)
+            r["frac_of_fp16_gemm_ref"] = r["tflops"] / multi["fp16_gemm_ref_tflops"]
+            multi[f"m{M}"] = r
+            log(f"{M} tokens x 32 layers: {r['us_per_32_layers']:.0f} us, "
+                f"{r['tflops']:.1f} TFLOP/s, {r['weight_gbs']:.0f} GB/s")
+
+    writer = None
+    if args.split_writer:
+        writer = measure_split_writer(dev)
+        log(f"split writer: {writer['neurons']} cold neurons in {writer['ms_per_layer']:.2f} ms "
+            f"({writer['input_gbs']:.0f} GB/s of fp32 input); restated CPU quantiser "
+            f"{writer['cpu_port_us_per_neuron']:.0f} us/neuron")
 
     staging = None
     if args.staging_steps > 0:
@@ -387,6 +462,7 @@ def main():
         "cpu_baseline": cpu,
         "staging": staging,
         "multi_token": multi,
+        "split_writer": writer,
     }
     print(json.dumps(out), flush=True)
     st.close()
