@@ -5,23 +5,23 @@
 // After the norm and a compaction of the active list:
 //   gate/up  H_hot  (M, n_hot) = act(s_g * X G^T + b, s_u * X U^T)   fp8 rows
 //            H_cold (M, n_act) = act(sum_g s_g,g (X Q_g^T)_g + b, ...)  INT4 records
-//            k_bup_s (M <= 64): 16 weight rows per workgroup, the 4 waves
-//            split K and meet in LDS, A fragments straight from L2, every
-//            weight load of a wave issued up front; k_bup (M > 64): 64 rows x
-//            64 tokens per workgroup, A tiles shared through LDS
-//   down     Y (M, H) fp32, zeroed, accumulated with fp32 atomics:
-//            hot  H_hot D_hot^T (fp8 rows, row scale), k_bdown_hot_s / k_bdown_hot
-//            cold H_cold D_cold: 128 outputs x 256 items per workgroup, the
-//            items' down nibbles decoded and scaled into LDS, transposed for
-//            the MFMA B operand (k_bdown_cold)
+//            k_bup_s (M <= 16): 16 weight rows per workgroup, the 4 waves
+//            split K and meet in LDS, every weight load issued up front;
+//            k_bup + k_bact (M < 192): 64 tokens x 64 rows, split K;
+//            k_pgemm_up (M >= 192): 32x32x16 tiles, weights streamed in registers
+//   down     Y (M, H) fp32, accumulated with fp32 atomics after the first writer:
+//            hot  H_hot D_hot^T (fp8 rows, row scale): k_bdown_hot_s,
+//                 k_bdown_hot, k_pgemm_down_hot
+//            cold H_cold D_cold: k_pgemm_down_cold for every M, the records'
+//                 down nibbles transposed into a decoded LDS tile
 //   k_bfinal out = x + Y (fp16), y32 = Y
 // Summation order across workgroups follows the atomics, so repeated runs
 // can differ in the last bits (well inside the FFN tolerance).
-// Every product is v_mfma_f32_16x16x32_f16 with fp32 accumulation.  fp8 and
-// INT4 weights convert to fp16 exactly; INT4 group scales (one per 128 K) are
-// applied to each 128-wide K block's partial sums in fp32, so the gate/up
-// products are exact up to fp32 accumulation.  Down weights of cold records
-// are rounded once to fp16 (q * s needs 15 significant bits).
+// fp8 and INT4 weights convert to fp16 exactly.  The small-batch gate/up
+// kernels apply INT4 group scales (one per 128 K) to each block's fp32
+// partial sums, exact up to accumulation; the prefill gate/up and every cold
+// down multiply nibble and scale in fp16, rounded once (q * s needs up to 14
+// significant bits).
 //
 // MFMA 16x16x32 f16 operand layout (lane l, element i): A[l%16][8(l/16)+i],
 // B[8(l/16)+i][l%16], D[4(l/16)+i][l%16].  Only the pairing of A and B
@@ -43,8 +43,6 @@ constexpr int kBM = 64;          // token rows per tile
 constexpr int kBN = 64;          // output columns per workgroup (4 waves x 16)
 constexpr int kBK = 128;         // K block = INT4 scale group
 constexpr int kLdA = kBK + 8;    // LDS row of the A tile, halves (272 B)
-constexpr int kBKc = 32;         // items per step of the cold down product
-constexpr int kLdT = kBKc + 8;   // LDS row of the decoded cold down tile, halves (80 B)
 
 __device__ __forceinline__ h8 cat8(f16x2 a, f16x2 b, f16x2 c, f16x2 d) {
   const h4 lo = __builtin_shufflevector(a, b, 0, 1, 2, 3);
@@ -684,7 +682,9 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_down_cold(BDownArgs a, int m
   uint32_t dq[8];
   uint16_t dsc[8];
   u32x4 hv[4];
+  int hkb = kb0;   // block held in dq / dsc / hv
   auto load_block = [&](int kb) {
+    hkb = kb;
     const int ib = (kb - kb0) * kDcItems + 8 * ig;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
@@ -717,9 +717,16 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_down_cold(BDownArgs a, int m
       *reinterpret_cast<h8*>(T + (8 * jg + n) * kLdC + 8 * ig) = v;
     }
     uint16_t* Hs = sH + buf * kA;
+    // H columns past the list's end may hold anything (the gate/up kernels
+    // write only the item tiles they own): keep items < total only
+    const int keep = total - (hkb * kDcItems + 8 * (t & 7));
+    uint32_t km[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+      km[d] = (2 * d < keep ? 0x0000FFFFu : 0u) | (2 * d + 1 < keep ? 0xFFFF0000u : 0u);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const uint32_t d0 = hv[r].x, d1 = hv[r].y, d2 = hv[r].z, d3 = hv[r].w;
+      const uint32_t d0 = hv[r].x & km[0], d1 = hv[r].y & km[1], d2 = hv[r].z & km[2], d3 = hv[r].w & km[3];
       u32x4 v;
       v.x = (d0 & 0xFFFFu) | (d2 << 16);
       v.y = (d0 >> 16) | (d2 & 0xFFFF0000u);
@@ -1031,118 +1038,6 @@ __global__ __launch_bounds__(kThreads) void k_bdown_hot(BDownArgs a) {
     }
 }
 
-// Cold half: workgroup = 128 outputs (4 waves x 32) x 64 tokens x a range of
-// the dense active list, taken 256 items per step.  Per step each thread
-// decodes 64 down values of two items (q * s rounded to fp16) into the LDS
-// tile T[h][item], the A tile (64 tokens x 256 items of H_cold) is staged
-// once for the 4 waves, and each wave runs 8 MFMA steps of 32 items.  The
-// range's sum is added into y.
-constexpr int kCT = 128;
-constexpr int kCI = 256;
-constexpr int kLdT2 = kCI + 8;   // 528-byte LDS rows
-
-__global__ __launch_bounds__(kThreads) void k_bdown_cold(BDownArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t sT[kCT * kLdT2];
-  __shared__ __attribute__((aligned(16))) uint16_t sH[kBM * kLdT2];
-  const int t = threadIdx.x, w = t >> 6, l = lane_id();
-  const int h0 = blockIdx.x * kCT, m0 = blockIdx.z * kBM;
-  const int total = min(*a.total, a.cap);
-  const int n_steps = (total + kCI - 1) / kCI;
-  const int st0 = blockIdx.y * n_steps / gridDim.y, st1 = (blockIdx.y + 1) * n_steps / gridDim.y;
-  if (st0 >= st1) return;   // the whole workgroup
-  const int ms_n = min(4, (a.M - m0 + 15) / 16);
-  const int p = t & 127, q = t >> 7;
-  f32x4 acc[4][2];
-#pragma unroll
-  for (int ms = 0; ms < 4; ++ms) acc[ms][0] = acc[ms][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int stp = st0; stp < st1; ++stp) {
-    const int ig = stp * kCI;
-    u32x4 raw[2][2];
-    float sc[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int it = ig + 2 * p + j;
-      const int slot = it < total ? a.dslots[it] : -1;
-      const bool v = slot >= 0 && slot < a.n_records;
-      const uint8_t* rec = a.records + (size_t)(v ? slot : 0) * kRecBytes;
-      const u32x4 z = {0u, 0u, 0u, 0u};
-      raw[j][0] = v ? load16_a2(rec + kOffDown + (h0 + 64 * q) / 2) : z;
-      raw[j][1] = v ? load16_a2(rec + kOffDown + (h0 + 64 * q) / 2 + 16) : z;
-      sc[j] = v ? half_bits_to_float(
-                      reinterpret_cast<const uint16_t*>(rec + kOffScales)[2 * kGroups + h0 / kGroup])
-                : 0.f;
-    }
-    // A tile: thread t -> row t >> 2, items 64 (t & 3) .. +64 of the step
-    u32x4 hv[8];
-    {
-      const int r = t >> 2, c0 = ig + 64 * (t & 3);
-      const int m = m0 + r;
-#pragma unroll
-      for (int c = 0; c < 8; ++c) {
-        const int ka = c0 + 8 * c;
-        u32x4 x = {0u, 0u, 0u, 0u};
-        if (m < a.M && ka < total) {
-          x = *reinterpret_cast<const u32x4*>(a.hc + (size_t)m * a.ldc + ka);
-          // items past the end of the list read as zero
-          if (ka + 8 > total) {
-            const int keep = total - ka;   // 1..7 halves
-#pragma unroll
-            for (int d = 0; d < 4; ++d) {
-              const uint32_t lo_ok = (2 * d) < keep ? 0xFFFFu : 0u;
-              const uint32_t hi_ok = (2 * d + 1) < keep ? 0xFFFF0000u : 0u;
-              x[d] &= lo_ok | hi_ok;
-            }
-          }
-        }
-        hv[c] = x;
-      }
-    }
-    __syncthreads();   // the previous step's MFMAs are done with sT / sH
-#pragma unroll
-    for (int jj = 0; jj < 64; ++jj) {
-      const uint32_t d0 = dword_of(raw[0][0], raw[0][1], jj >> 3);
-      const uint32_t d1 = dword_of(raw[1][0], raw[1][1], jj >> 3);
-      const int q0 = (int)((d0 >> (4 * (jj & 7))) & 0xFu) ^ 8;
-      const int q1 = (int)((d1 >> (4 * (jj & 7))) & 0xFu) ^ 8;
-      const uint32_t pr = (uint32_t)float_to_half_bits((float)(q0 - 8) * sc[0]) |
-                          ((uint32_t)float_to_half_bits((float)(q1 - 8) * sc[1]) << 16);
-      *reinterpret_cast<uint32_t*>(sT + (64 * q + jj) * kLdT2 + 2 * p) = pr;
-    }
-    {
-      const int r = t >> 2, c0 = 64 * (t & 3);
-#pragma unroll
-      for (int c = 0; c < 8; ++c)
-        *reinterpret_cast<u32x4*>(sH + r * kLdT2 + c0 + 8 * c) = hv[c];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      h8 av[4];
-#pragma unroll
-      for (int ms = 0; ms < 4; ++ms)
-        av[ms] = *reinterpret_cast<const h8*>(sH + (16 * ms + (l & 15)) * kLdT2 + 32 * s + 8 * (l >> 4));
-#pragma unroll
-      for (int ns = 0; ns < 2; ++ns) {
-        const h8 b = *reinterpret_cast<const h8*>(sT + (32 * w + 16 * ns + (l & 15)) * kLdT2 +
-                                                  32 * s + 8 * (l >> 4));
-#pragma unroll
-        for (int ms = 0; ms < 4; ++ms)
-          if (ms < ms_n) acc[ms][ns] = mfma16(av[ms], b, acc[ms][ns]);
-      }
-    }
-  }
-#pragma unroll
-  for (int ms = 0; ms < 4; ++ms)
-#pragma unroll
-    for (int ns = 0; ns < 2; ++ns)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int m = m0 + 16 * ms + 4 * (l >> 4) + e;
-        const int h = h0 + 32 * w + 16 * ns + (l & 15);
-        if (ms < ms_n && m < a.M) unsafeAtomicAdd(a.y + (size_t)m * kH + h, acc[ms][ns][e]);
-      }
-}
-
 // y = 0 over M rows.
 __global__ __launch_bounds__(kThreads) void k_bfill(float* y, int n4) {
   for (int q = blockIdx.x * kThreads + threadIdx.x; q < n4; q += gridDim.x * kThreads)
@@ -1389,7 +1284,7 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
     }
     OI2_CHECK_LAUNCH();
   }
-  if (has_cold && p.prefill) {
+  if (has_cold) {
     // 16 output tiles x 128-token tiles x item ranges, about 256 workgroups;
     // a range holds at most kDcMaxItems items
     const int mtc = (M + 127) / 128;
@@ -1397,13 +1292,6 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
     const int min_splits = (n_blk + kDcMaxItems / kDcItems - 1) / (kDcMaxItems / kDcItems);
     const int splits = std::max(min_splits, std::min(n_blk, std::max(1, 256 / (16 * mtc))));
     hipLaunchKernelGGL(k_pgemm_down_cold, dim3(16 * mtc * splits), dim3(kThreads), 0, st, da, mtc, splits);
-    OI2_CHECK_LAUNCH();
-  } else if (has_cold) {
-    // item ranges per output tile: ~512 workgroups in all, at least 2 steps each
-    const int steps = (cap + kCI - 1) / kCI;
-    int splits = (512 / (kH / kCT)) / p.mt;
-    splits = std::max(1, std::min(splits, (steps + 1) / 2));
-    hipLaunchKernelGGL(k_bdown_cold, dim3(kH / kCT, splits, p.mt), dim3(kThreads), 0, st, da);
     OI2_CHECK_LAUNCH();
   }
   hipLaunchKernelGGL(k_bfinal, dim3(grid), dim3(kThreads), 0, st, y, M, add_residual ? x : nullptr,

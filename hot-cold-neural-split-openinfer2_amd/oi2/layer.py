@@ -110,8 +110,17 @@ def rmsnorm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
     return out.reshape(shape)
 
 
+def workspace_bytes(batch: int, hot: HotWeights | None, cold: ColdNeurons | None) -> int:
+    """Bytes of the scratch buffer oi2_ffn_forward needs for this batch and halves."""
+    n_hot = hot.n_hot if hot is not None and hot.n_hot > 0 else 0
+    return int(_lib.lib().oi2_ffn_workspace_bytes(batch, n_hot, cold.capacity() if cold is not None else 0))
+
+
 def _ffn(x2d, norm_w, eps, hot: HotWeights | None, cold: ColdNeurons | None, activation,
-         act_on_both, add_residual, out_dtype=torch.float16, want_y32=False):
+         act_on_both, add_residual, out_dtype=torch.float16, want_y32=False, workspace=None):
+    """One oi2_ffn_forward call.  ``workspace`` (uint8 device tensor of at least
+    workspace_bytes(...)) is used instead of a fresh allocation when given; its
+    contents on entry do not matter."""
     dev = x2d.device
     x2d = x2d.to(torch.float16).contiguous()
     B = x2d.shape[0]
@@ -120,7 +129,12 @@ def _ffn(x2d, norm_w, eps, hot: HotWeights | None, cold: ColdNeurons | None, act
     cold_s, act_s = cold.structs() if cold is not None else (None, None)
     n_hot = hot.n_hot if hot_s is not None else 0
     ws_bytes = L.oi2_ffn_workspace_bytes(B, n_hot, cold.capacity() if cold is not None else 0)
-    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    if workspace is not None:
+        if workspace.dtype != torch.uint8 or workspace.device != dev or workspace.numel() < ws_bytes:
+            raise ValueError(f"workspace must be a uint8 tensor of >= {ws_bytes} bytes on {dev}")
+        ws = workspace
+    else:
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
     out = torch.empty_like(x2d)
     y32 = torch.empty((B, HIDDEN), dtype=torch.float32, device=dev) if want_y32 else None
     act = _lib.ACT_RELU if activation == "relu" else _lib.ACT_SILU

@@ -153,3 +153,25 @@ def test_prefill_chunk_512(dev):
     hc = torch.nn.functional.silu(xn_all @ f32(Gc).T) * (xn_all @ f32(Uc).T)
     ref_all = (hh @ f32(Dh).T + hc @ f32(Dc).T).double().cpu().numpy()
     assert_ffn_close(y32.cpu().numpy(), ref_all, what="prefill all rows")
+
+
+@pytest.mark.parametrize("B", [3, 17, 96, 300])
+def test_batch_ignores_workspace_contents(dev, layer25, B):
+    """The workspace is scratch: filled with NaN before the call (every byte
+    0xFF), the result is the same as with a zeroed one.  Covers the columns
+    past the active list's end, which no gate/up kernel writes."""
+    from oi2.layer import workspace_bytes
+    lay, g = layer25
+    n_cold = lay.records.shape[0]
+    slots = torch.randperm(n_cold, generator=g, device=dev)[:1001].int()   # not a tile multiple
+    cold = ColdNeurons.from_slots(_section(lay), slots)
+    x = torch.randn((B, H), generator=g, device=dev).half()
+    nbytes = workspace_bytes(B, lay.hot, cold)
+    outs = []
+    for fill in (0xFF, 0x00):
+        ws = torch.full((nbytes,), fill, dtype=torch.uint8, device=dev)
+        outs.append(_ffn(x, lay.norm_w, EPS, lay.hot, cold, "silu", False, True, want_y32=True,
+                         workspace=ws)[1].cpu().numpy())
+    assert np.isfinite(outs[0]).all()
+    assert_ffn_close(outs[0].reshape(-1), outs[1].reshape(-1), tol=1e-5, cos_min=0.999999,
+                     what=f"B={B} NaN-filled vs zeroed workspace")
