@@ -461,85 +461,198 @@ __device__ __forceinline__ void pgemm_loop(const uint16_t* A, int ld, int M, int
 }
 
 // Gate/up for 32 MS tokens x 128 weight rows (hot rows first, then items of
-// the dense active list).  Wave w: rows r0 + 32 w + (l & 31); B tile 0 is the
-// gate row, tile 1 the up row.  The linear workgroup index is mapped so that
-// the token tiles of one row tile run on the same XCD (workgroups go
-// round-robin over the 8 XCDs), sharing its L2 for the weights.
-template <int MS>
-__global__ __launch_bounds__(kThreads) void k_pgemm_up(BUpArgs a, int hot_tiles, int n_tiles, int mt) {
-  __shared__ __attribute__((aligned(16))) uint16_t sA[2 * 32 * MS * kLdA];
-  const int b = blockIdx.x;
-  const int q = b >> 3;
-  const int nt = (q / mt) * 8 + (b & 7), mtile = q % mt;
-  if (nt >= n_tiles) return;   // the whole workgroup
-  const int m0 = mtile * 32 * MS;
+// the dense active list).  Both operands go through two LDS buffers: each K
+// block's token rows and weight rows are loaded a block ahead as whole
+// 16-byte chunks (eight lanes per 128-byte weight row, so every load
+// instruction reads full cache lines) and written to LDS after the block's
+// MFMAs.  Weight rows are padded to 136 bytes (fp8) or 72 bytes (INT4): the
+// 32 rows a wave reads at one column then fall on distinct banks.  Wave w
+// owns rows 32 w + (l & 31); B tile 0 is the gate row, tile 1 the up row.
+// The linear workgroup index is mapped so that the token tiles of one row
+// tile run on the same XCD (workgroups go round-robin over the 8 XCDs),
+// sharing its L2 for the weights.
+constexpr int kLdB8 = 128 + 8;   // bytes per fp8 weight row of a K block in LDS
+constexpr int kLdB4 = 64 + 8;    // bytes per INT4 weight row of a K block in LDS
+
+// MS x 2 MFMA tiles for the eight K steps of one block, both operands from
+// LDS; the next step's fragments are read and converted while a step
+// multiplies (scheduling groups interleave MFMAs, VALU and LDS reads).
+template <int MS, bool INT4>
+__device__ __forceinline__ void mma_block_lds(const uint16_t* sA, const uint8_t* sB, const uint16_t* sSc,
+                                              f32x16 (&acc)[MS][2]) {
+  constexpr int kValuPerMfma = INT4 ? 4 : 1;
   const int w = threadIdx.x >> 6, l = lane_id();
+  const int row = 32 * w + (l & 31), h = l >> 5;
+  _Float16 sc[2] = {(_Float16)0.0f, (_Float16)0.0f};
+  if constexpr (INT4) {
+    sc[0] = __builtin_bit_cast(_Float16, sSc[row]);
+    sc[1] = __builtin_bit_cast(_Float16, sSc[128 + row]);
+  }
+  auto b_frag = [&](int st, h8 (&bf)[2]) {
+#pragma unroll
+    for (int nb = 0; nb < 2; ++nb) {
+      if constexpr (INT4) {
+        const uint32_t d = *reinterpret_cast<const uint32_t*>(sB + (128 * nb + row) * kLdB4 + 32 * h + 4 * st);
+        bf[nb] = int4x8_h8_scaled(d, sc[nb]);
+      } else {
+        const u32x2 v = *reinterpret_cast<const u32x2*>(sB + (128 * nb + row) * kLdB8 + 64 * h + 8 * st);
+        bf[nb] = fp8x8_h8(v[0], v[1]);
+      }
+    }
+  };
+  h8 av[MS], bf[2][2];
+#pragma unroll
+  for (int ms = 0; ms < MS; ++ms) av[ms] = a_frag32(sA, ms, 0);
+  b_frag(0, bf[0]);
+#pragma unroll
+  for (int st = 0; st < 8; ++st) {
+    if (st < 7) b_frag(st + 1, bf[(st + 1) & 1]);
+#pragma unroll
+    for (int ms = 0; ms < MS; ++ms) {
+#pragma unroll
+      for (int nb = 0; nb < 2; ++nb) acc[ms][nb] = mfma32(av[ms], bf[st & 1][nb], acc[ms][nb]);
+      if (st < 7) av[ms] = a_frag32(sA, ms, st + 1);
+    }
+#pragma unroll
+    for (int i = 0; i < 2 * MS; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);               // one MFMA
+      if (st < 7) {
+        __builtin_amdgcn_sched_group_barrier(0x002, kValuPerMfma, 0);  // VALU
+        if (i < MS + 2) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+      }
+    }
+  }
+}
+
+template <int MS, bool HOT>
+__device__ __forceinline__ void pgemm_up_tile(const BUpArgs& a, int nt, int m0, int total, int i0,
+                                              uint16_t* sA, uint8_t* sB, uint16_t* sSc) {
+  constexpr int kAbuf = 32 * MS * kLdA;   // halves per A buffer
+  constexpr int kBbuf = 256 * kLdB8;      // bytes per B buffer (INT4 rows use kLdB4 of it)
+  constexpr int NR = HOT ? 8 : 4;         // 16-byte weight chunks staged per thread
+  const int t = threadIdx.x, w = t >> 6, l = lane_id();
+  const ARows<MS> arows(a.xn, kH, a.M, m0);
   f32x16 acc[MS][2];
 #pragma unroll
   for (int ms = 0; ms < MS; ++ms) acc[ms][0] = acc[ms][1] = f32x16{};
+  u32x4 ra[2 * MS], rb[NR];
+  uint16_t rsc = 0;
 
-  if (nt < hot_tiles) {
-    const int row = nt * 128 + 32 * w + (l & 31);
+  // this thread's staging rows: hot, chunk t & 7 of tile rows (t >> 3) + 32 i
+  // (i < 4 gate, else up); cold, chunk t & 3 of items (t >> 2) + 64 (i & 1),
+  // gate for i < 2, up for i >= 2, and the scale of item t & 127 (gate, up
+  // by t >> 7).  Rows past n_hot and invalid items read as zero.
+  const rsrc_t rw = HOT ? buf_rsrc(a.gate_q, (uint32_t)a.n_hot * kH)
+                        : buf_rsrc(a.records, (uint32_t)a.n_records * kRecBytes);
+  const rsrc_t ru = buf_rsrc(a.up_q, HOT ? (uint32_t)a.n_hot * kH : 0u);
+  uint32_t voff[4], vsc = 0;
+  auto item_rec = [&](int it) {
+    const int slot = it < total ? a.dslots[it] : -1;
+    return (slot >= 0 && slot < a.n_records) ? (uint32_t)slot * kRecBytes : kNoOffset;
+  };
+  if constexpr (HOT) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) voff[i] = (uint32_t)(nt * 128 + (t >> 3) + 32 * i) * kH + 16 * (t & 7);
+  } else {
+    const uint32_t v0 = item_rec(i0 + (t >> 2)), v1 = item_rec(i0 + (t >> 2) + 64);
+    voff[0] = v0 + kOffGate + 16 * (t & 3);
+    voff[1] = v1 + kOffGate + 16 * (t & 3);
+    voff[2] = v0 + kOffUp + 16 * (t & 3);
+    voff[3] = v1 + kOffUp + 16 * (t & 3);
+    vsc = item_rec(i0 + (t & 127)) + (t >> 7) * 2 * kGroups;
+  }
+  auto load_b = [&](int kb) {
+    if constexpr (HOT) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) rb[i] = bload16(i < 4 ? rw : ru, voff[i & 3], kb * kBK);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) rb[i] = bload16(rw, voff[i], 64 * kb);
+      rsc = bload2(rw, vsc, kOffScales + 2 * kb);
+    }
+  };
+  auto store_b = [&](int buf) {
+    uint8_t* B = sB + buf * kBbuf;
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+      uint8_t* d = HOT ? B + ((t >> 3) + 32 * i) * kLdB8 + 16 * (t & 7)
+                       : B + ((t >> 2) + 64 * i) * kLdB4 + 16 * (t & 3);
+      reinterpret_cast<u32x2*>(d)[0] = u32x2{rb[i].x, rb[i].y};
+      reinterpret_cast<u32x2*>(d)[1] = u32x2{rb[i].z, rb[i].w};
+    }
+    if constexpr (!HOT) sSc[buf * 256 + t] = rsc;
+  };
+
+  arows.load(0, ra);
+  load_b(0);
+  store_a_rows<2 * MS, !HOT>(ra, sA);
+  store_b(0);
+  lds_barrier();
+  for (int kb = 0; kb < kH / kBK; ++kb) {
+    const int kn = min(kb + 1, kH / kBK - 1), cur = kb & 1;
+    arows.load(kn, ra);
+    load_b(kn);
+    // sched_barrier(0) keeps these loads issued before the MFMAs (the
+    // scheduler would otherwise sink them to shorten register lifetimes)
+    __builtin_amdgcn_sched_barrier(0);
+    mma_block_lds<MS, !HOT>(sA + cur * kAbuf, sB + cur * kBbuf, sSc + cur * 256, acc);
+    __builtin_amdgcn_sched_barrier(0);
+    store_a_rows<2 * MS, !HOT>(ra, sA + (cur ^ 1) * kAbuf);
+    store_b(cur ^ 1);
+    lds_barrier();
+  }
+
+  // epilogue: this lane's column, rows m0 + 32 ms + 8 (j / 4) + 4 (l / 32) + j % 4
+  const int col = 32 * w + (l & 31);
+  if constexpr (HOT) {
+    const int row = nt * 128 + col;
     const bool ok = row < a.n_hot;
-    // rows >= n_hot lie past the descriptors and read as zero
-    const uint32_t voff = (uint32_t)row * kH + 64 * (l >> 5);
-    const rsrc_t rg = buf_rsrc(a.gate_q, (uint32_t)a.n_hot * kH);
-    const rsrc_t ru = buf_rsrc(a.up_q, (uint32_t)a.n_hot * kH);
     const float sg = ok ? a.gate_s[row] : 0.f, su = ok ? a.up_s[row] : 0.f;
     const float gb = (ok && a.hot_gbias) ? a.hot_gbias[row] : 0.f;
-    auto load_b = [&](int kb, int g, BRegs<2, false>& bb) {   // steps 2g, 2g + 1
-#pragma unroll
-      for (int nb = 0; nb < 2; ++nb) {
-        const u32x4 v = bload16(nb == 0 ? rg : ru, voff + 16 * g, kb * kBK);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) bb.q[2 * g + e / 2][nb][e & 1] = v[e];
-      }
-    };
-    pgemm_loop<MS, 2, false, false>(a.xn, kH, a.M, m0, 0, kH / kBK, sA, load_b, acc);
 #pragma unroll
     for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         const int m = m0 + 32 * ms + 8 * (j >> 2) + 4 * (l >> 5) + (j & 3);
         if (m >= a.M) continue;
-        const float h = ok ? gated_act(fmaf(acc[ms][0][j], sg, gb), acc[ms][1][j] * su, a.relu, a.both) : 0.f;
-        a.hh[(size_t)m * a.ldh + row] = float_to_half_bits(h);
+        const float hv = ok ? gated_act(fmaf(acc[ms][0][j], sg, gb), acc[ms][1][j] * su, a.relu, a.both) : 0.f;
+        a.hh[(size_t)m * a.ldh + row] = float_to_half_bits(hv);
       }
+  } else {
+    const int item = i0 + col;
+    const int slot = item < total ? a.dslots[item] : -1;
+    const bool ok = slot >= 0 && slot < a.n_records;
+    const float gb = (ok && a.cold_gbias) ? a.cold_gbias[slot] : 0.f;
+#pragma unroll
+    for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int m = m0 + 32 * ms + 8 * (j >> 2) + 4 * (l >> 5) + (j & 3);
+        if (m >= a.M) continue;
+        const float hv = ok ? gated_act(acc[ms][0][j] + gb, acc[ms][1][j], a.relu, a.both) : 0.f;
+        a.hc[(size_t)m * a.ldc + item] = float_to_half_bits(hv);
+      }
+  }
+}
+
+template <int MS>
+__global__ __launch_bounds__(kThreads) void k_pgemm_up(BUpArgs a, int hot_tiles, int n_tiles, int mt) {
+  __shared__ __attribute__((aligned(16))) uint16_t sA[2 * 32 * MS * kLdA];
+  __shared__ __attribute__((aligned(16))) uint8_t sB[2 * 256 * kLdB8];
+  __shared__ uint16_t sSc[2 * 256];
+  const int b = blockIdx.x;
+  const int q = b >> 3;
+  const int nt = (q / mt) * 8 + (b & 7), mtile = q % mt;
+  if (nt >= n_tiles) return;   // the whole workgroup
+  const int m0 = mtile * 32 * MS;
+  if (nt < hot_tiles) {
+    pgemm_up_tile<MS, true>(a, nt, m0, 0, 0, sA, sB, sSc);
     return;
   }
-
   const int total = min(*a.total, a.cap);
   const int i0 = (nt - hot_tiles) * 128;
   if (i0 >= total) return;   // the whole workgroup
-  const int item = i0 + 32 * w + (l & 31);
-  const int slot = item < total ? a.dslots[item] : -1;
-  const bool ok = slot >= 0 && slot < a.n_records;
-  // invalid items point past the records and read as zero
-  const uint32_t vrec = ok ? (uint32_t)slot * kRecBytes : kNoOffset;
-  const rsrc_t rr = buf_rsrc(a.records, (uint32_t)a.n_records * kRecBytes);
-  const float gb = (ok && a.cold_gbias) ? a.cold_gbias[slot] : 0.f;
-  // gate nibbles at kOffGate + 64 kb, up at kOffUp + 64 kb (this lane's 32
-  // bytes at 32 (l / 32)); the block's scales at kOffScales + 2 kb and + 64
-  auto load_b = [&](int kb, int g, BRegs<2, true>& bb) {   // steps 4g .. 4g + 3
-#pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
-      const u32x4 v = bload16(rr, vrec + (nb == 0 ? kOffGate : kOffUp) + 32 * (l >> 5) + 16 * g, 64 * kb);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) bb.q[4 * g + e][nb][0] = v[e];
-      // the scale serves all eight steps: refill it with the last group
-      if (g == 1) bb.sc[nb] = bload2(rr, vrec + (nb == 0 ? 0 : 2 * kGroups), kOffScales + 2 * kb);
-    }
-  };
-  pgemm_loop<MS, 2, true, true>(a.xn, kH, a.M, m0, 0, kH / kBK, sA, load_b, acc);
-#pragma unroll
-  for (int ms = 0; ms < MS; ++ms)
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int m = m0 + 32 * ms + 8 * (j >> 2) + 4 * (l >> 5) + (j & 3);
-      if (m >= a.M) continue;
-      const float h = ok ? gated_act(acc[ms][0][j] + gb, acc[ms][1][j], a.relu, a.both) : 0.f;
-      a.hc[(size_t)m * a.ldc + item] = float_to_half_bits(h);
-    }
+  pgemm_up_tile<MS, false>(a, nt, m0, total, i0, sA, sB, sSc);
 }
 
 // Hot down for 32 MS tokens x (4 waves x 32 NB outputs) over the K blocks of
