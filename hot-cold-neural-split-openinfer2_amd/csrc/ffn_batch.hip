@@ -306,11 +306,10 @@ __global__ __launch_bounds__(kThreads) void k_bact(BUpArgs a) {
 // is split between the two lane halves as 64 contiguous K, 8 per MFMA step.
 //
 // Workgroup tile: 32 MS tokens x 4 waves, each wave one 32-column B tile per
-// NB: 32 weight rows as gate and up, or 64 down rows.  The token tile (A) goes
-// through two LDS buffers, one barrier per K block.  Each wave streams its own
-// B rows from global memory into registers a whole block ahead, so the
-// weights are read once per token tile and never touch LDS.  The barrier
-// waits for LDS traffic only (lgkmcnt), not for the global loads in flight.
+// NB (32 weight rows as gate and up, or 32 down rows).  Both operands go
+// through two LDS buffers, one barrier per K block; each block's global loads
+// are issued a block ahead.  The barrier waits for LDS traffic only
+// (lgkmcnt), not for the global loads in flight.
 //
 // Cold rows: INT4 nibbles times their group scale, rounded once to fp16 (the
 // product needs up to 14 significant bits), so every K block accumulates
@@ -369,97 +368,6 @@ __device__ __forceinline__ h8 a_frag32(const uint16_t* s, int ms, int step) {
   return *reinterpret_cast<const h8*>(s + (32 * ms + (l & 31)) * kLdA + 64 * (l >> 5) + 8 * step);
 }
 
-// One wave's B operand for a K block: NB tiles of 32 rows (lane row l & 31),
-// 64 contiguous K per lane half, held per 8-wide K step s: fp8 rows as two
-// dwords, INT4 records as one dword plus the group scale.
-template <int NB, bool INT4>
-struct BRegs {
-  uint32_t q[8][NB][INT4 ? 1 : 2];
-  uint16_t sc[NB];
-};
-
-// The wave's B fragments of K step s (0..7) in fp16.
-template <int NB, bool INT4>
-__device__ __forceinline__ void b_frags(const BRegs<NB, INT4>& b, int s, h8 (&bf)[NB]) {
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    if constexpr (INT4)
-      bf[nb] = int4x8_h8_scaled(b.q[s][nb][0], __builtin_bit_cast(_Float16, b.sc[nb]));
-    else
-      bf[nb] = fp8x8_h8(b.q[s][nb][0], b.q[s][nb][1]);
-  }
-}
-
-// MS x NB MFMA tiles for the eight K steps of one block.  While step s
-// multiplies, the B fragments of step s + 1 are converted, the raw B
-// registers of a load group (16 bytes per lane: two fp8 steps or four INT4
-// steps) are refilled with block kn's data (the next block, loaded a whole
-// block ahead) once its last step is converted, and each A fragment is
-// re-read from LDS for step s + 1 as soon as its last MFMA of step s is
-// issued.  The scheduling groups interleave each MFMA with VALU work and
-// spread the LDS reads, so the matrix core, the VALU and LDS overlap.
-template <int MS, int NB, bool INT4, typename LoadGroup>
-__device__ __forceinline__ void mma_block(BRegs<NB, INT4>& b, const uint16_t* sA, int kn,
-                                          LoadGroup load_group, f32x16 (&acc)[MS][NB]) {
-  constexpr int kValuPerMfma = INT4 ? 4 : 1;
-  constexpr int G = INT4 ? 4 : 2;   // steps per load group
-  h8 av[MS], bf[2][NB];
-#pragma unroll
-  for (int ms = 0; ms < MS; ++ms) av[ms] = a_frag32(sA, ms, 0);
-  b_frags<NB, INT4>(b, 0, bf[0]);
-#pragma unroll
-  for (int s = 0; s < 8; ++s) {
-    if (s < 7) {
-      b_frags<NB, INT4>(b, s + 1, bf[(s + 1) & 1]);
-      if ((s + 1) % G == G - 1) load_group(kn, (s + 1) / G, b);
-    }
-#pragma unroll
-    for (int ms = 0; ms < MS; ++ms) {
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) acc[ms][nb] = mfma32(av[ms], bf[s & 1][nb], acc[ms][nb]);
-      if (s < 7) av[ms] = a_frag32(sA, ms, s + 1);
-    }
-#pragma unroll
-    for (int i = 0; i < MS * NB; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);               // one MFMA
-      if (s < 7) {
-        __builtin_amdgcn_sched_group_barrier(0x002, kValuPerMfma, 0);  // VALU
-        if (i % NB == NB - 1) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
-      }
-    }
-  }
-}
-
-// K blocks [kb0, kb1) of A (ld halves per row) times the wave's B rows, into
-// acc.  load_group(kb, g, BRegs&) loads load group g of block kb.  sA holds two
-// 32 MS x kLdA buffers.  Every iteration loads the next block (the last one
-// reloads itself), so the loop body has no branches.
-template <int MS, int NB, bool INT4, bool PAIR, typename LoadGroup>
-__device__ __forceinline__ void pgemm_loop(const uint16_t* A, int ld, int M, int m0, int kb0, int kb1,
-                                           uint16_t* sA, LoadGroup load_group, f32x16 (&acc)[MS][NB]) {
-  const ARows<MS> arows(A, ld, M, m0);
-  u32x4 ra[2 * MS];
-  BRegs<NB, INT4> b;
-  arows.load(kb0, ra);
-#pragma unroll
-  for (int g = 0; g < (INT4 ? 2 : 4); ++g) load_group(kb0, g, b);
-  store_a_rows<2 * MS, PAIR>(ra, sA);
-  lds_barrier();
-  for (int kb = kb0; kb < kb1; ++kb) {
-    const int kn = min(kb + 1, kb1 - 1);
-    uint16_t* cur = sA + ((kb - kb0) & 1) * (32 * MS * kLdA);
-    uint16_t* nxt = sA + ((kb - kb0 + 1) & 1) * (32 * MS * kLdA);
-    arows.load(kn, ra);
-    // sched_barrier(0) keeps these loads issued before the MFMAs (the
-    // scheduler would otherwise sink them to shorten register lifetimes)
-    __builtin_amdgcn_sched_barrier(0);
-    mma_block<MS, NB, INT4>(b, cur, kn, load_group, acc);
-    __builtin_amdgcn_sched_barrier(0);
-    store_a_rows<2 * MS, PAIR>(ra, nxt);
-    lds_barrier();
-  }
-}
-
 // Gate/up for 32 MS tokens x 128 weight rows (hot rows first, then items of
 // the dense active list).  Both operands go through two LDS buffers: each K
 // block's token rows and weight rows are loaded a block ahead as whole
@@ -474,12 +382,13 @@ __device__ __forceinline__ void pgemm_loop(const uint16_t* A, int ld, int M, int
 constexpr int kLdB8 = 128 + 8;   // bytes per fp8 weight row of a K block in LDS
 constexpr int kLdB4 = 64 + 8;    // bytes per INT4 weight row of a K block in LDS
 
-// MS x 2 MFMA tiles for the eight K steps of one block, both operands from
-// LDS; the next step's fragments are read and converted while a step
-// multiplies (scheduling groups interleave MFMAs, VALU and LDS reads).
-template <int MS, bool INT4>
+// MS x NB MFMA tiles for the eight K steps of one block, both operands from
+// LDS (B tile nb is weight rows 128 nb + 32 w + (l & 31)); the next step's
+// fragments are read and converted while a step multiplies (scheduling
+// groups interleave MFMAs, VALU and LDS reads).
+template <int MS, int NB, bool INT4>
 __device__ __forceinline__ void mma_block_lds(const uint16_t* sA, const uint8_t* sB, const uint16_t* sSc,
-                                              f32x16 (&acc)[MS][2]) {
+                                              f32x16 (&acc)[MS][NB]) {
   constexpr int kValuPerMfma = INT4 ? 4 : 1;
   const int w = threadIdx.x >> 6, l = lane_id();
   const int row = 32 * w + (l & 31), h = l >> 5;
@@ -488,9 +397,9 @@ __device__ __forceinline__ void mma_block_lds(const uint16_t* sA, const uint8_t*
     sc[0] = __builtin_bit_cast(_Float16, sSc[row]);
     sc[1] = __builtin_bit_cast(_Float16, sSc[128 + row]);
   }
-  auto b_frag = [&](int st, h8 (&bf)[2]) {
+  auto b_frag = [&](int st, h8 (&bf)[NB]) {
 #pragma unroll
-    for (int nb = 0; nb < 2; ++nb) {
+    for (int nb = 0; nb < NB; ++nb) {
       if constexpr (INT4) {
         const uint32_t d = *reinterpret_cast<const uint32_t*>(sB + (128 * nb + row) * kLdB4 + 32 * h + 4 * st);
         bf[nb] = int4x8_h8_scaled(d, sc[nb]);
@@ -500,7 +409,7 @@ __device__ __forceinline__ void mma_block_lds(const uint16_t* sA, const uint8_t*
       }
     }
   };
-  h8 av[MS], bf[2][2];
+  h8 av[MS], bf[2][NB];
 #pragma unroll
   for (int ms = 0; ms < MS; ++ms) av[ms] = a_frag32(sA, ms, 0);
   b_frag(0, bf[0]);
@@ -510,15 +419,15 @@ __device__ __forceinline__ void mma_block_lds(const uint16_t* sA, const uint8_t*
 #pragma unroll
     for (int ms = 0; ms < MS; ++ms) {
 #pragma unroll
-      for (int nb = 0; nb < 2; ++nb) acc[ms][nb] = mfma32(av[ms], bf[st & 1][nb], acc[ms][nb]);
+      for (int nb = 0; nb < NB; ++nb) acc[ms][nb] = mfma32(av[ms], bf[st & 1][nb], acc[ms][nb]);
       if (st < 7) av[ms] = a_frag32(sA, ms, st + 1);
     }
 #pragma unroll
-    for (int i = 0; i < 2 * MS; ++i) {
+    for (int i = 0; i < NB * MS; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);               // one MFMA
       if (st < 7) {
         __builtin_amdgcn_sched_group_barrier(0x002, kValuPerMfma, 0);  // VALU
-        if (i < MS + 2) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
+        if (i < MS + NB) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one LDS read
       }
     }
   }
@@ -595,7 +504,7 @@ __device__ __forceinline__ void pgemm_up_tile(const BUpArgs& a, int nt, int m0, 
     // sched_barrier(0) keeps these loads issued before the MFMAs (the
     // scheduler would otherwise sink them to shorten register lifetimes)
     __builtin_amdgcn_sched_barrier(0);
-    mma_block_lds<MS, !HOT>(sA + cur * kAbuf, sB + cur * kBbuf, sSc + cur * 256, acc);
+    mma_block_lds<MS, 2, !HOT>(sA + cur * kAbuf, sB + cur * kBbuf, sSc + cur * 256, acc);
     __builtin_amdgcn_sched_barrier(0);
     store_a_rows<2 * MS, !HOT>(ra, sA + (cur ^ 1) * kAbuf);
     store_b(cur ^ 1);
@@ -655,14 +564,20 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_up(BUpArgs a, int hot_tiles,
   pgemm_up_tile<MS, false>(a, nt, m0, total, i0, sA, sB, sSc);
 }
 
-// Hot down for 32 MS tokens x (4 waves x 32 NB outputs) over the K blocks of
+// Hot down for 32 MS tokens x 128 outputs (4 waves x 32) over the K blocks of
 // one of `splits` ranges; y gets the scaled sums (stored when splits == 1,
-// else added atomically into a zeroed y).  Same XCD-aware index mapping.
-template <int MS, int NB>
+// else added atomically into a zeroed y).  The down rows of each K block are
+// staged through padded LDS like the gate/up weights (thread t: chunk t & 7
+// of rows t / 8 + 32 i); chunks past the row stride read as zero (the stride
+// is a multiple of 64, so a chunk never straddles it).  Same XCD-aware
+// index mapping.
+template <int MS>
 __global__ __launch_bounds__(kThreads) void k_pgemm_down_hot(BDownArgs a, int mt, int splits) {
-  __shared__ __attribute__((aligned(16))) uint16_t sA[2 * 32 * MS * kLdA];
-  constexpr int kTileN = 4 * 32 * NB;
-  constexpr int kTiles = kH / kTileN;
+  constexpr int kAbuf = 32 * MS * kLdA;
+  constexpr int kBbuf = 128 * kLdB8;
+  constexpr int kTiles = kH / 128;
+  __shared__ __attribute__((aligned(16))) uint16_t sA[2 * kAbuf];
+  __shared__ __attribute__((aligned(16))) uint8_t sB[2 * kBbuf];
   const int b = blockIdx.x;
   const int q = b >> 3, per = mt * splits;
   const int nt = (q / per) * 8 + (b & 7), rem = q % per;
@@ -671,49 +586,62 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_down_hot(BDownArgs a, int mt
   const int kb0 = split * a.hot_blocks / splits, kb1 = (split + 1) * a.hot_blocks / splits;
   if (kb0 >= kb1) return;
   const int m0 = mtile * 32 * MS;
-  const int w = threadIdx.x >> 6, l = lane_id();
-  int row[NB];
-  uint32_t voff[NB];
+  const int t = threadIdx.x, w = t >> 6, l = lane_id();
+  const ARows<MS> arows(a.hh, a.ldh, a.M, m0);
   const rsrc_t rd = buf_rsrc(a.down_q, (uint32_t)kH * a.down_stride);
+  uint32_t voff[4];
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    row[nb] = nt * kTileN + 32 * NB * w + 32 * nb + (l & 31);
-    voff[nb] = (uint32_t)row[nb] * a.down_stride + 64 * (l >> 5);
-  }
-  f32x16 acc[MS][NB];
+  for (int i = 0; i < 4; ++i) voff[i] = (uint32_t)(nt * 128 + (t >> 3) + 32 * i) * a.down_stride + 16 * (t & 7);
+  f32x16 acc[MS][1];
 #pragma unroll
-  for (int ms = 0; ms < MS; ++ms)
+  for (int ms = 0; ms < MS; ++ms) acc[ms][0] = f32x16{};
+  u32x4 ra[2 * MS], rb[4];
+  auto load_b = [&](int kb) {
+    const bool in = kb * kBK + 16 * (t & 7) < a.down_stride;
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) acc[ms][nb] = f32x16{};
-  // K bytes past the row stride are zero (the hot activations there are zero
-  // too, but the bytes belong to the next row)
-  auto load_b = [&](int kb, int g, BRegs<NB, false>& bb) {   // steps 2g, 2g + 1
-    const bool in = kb * kBK + 64 * (l >> 5) + 16 * g < a.down_stride;
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      const u32x4 v = bload16(rd, voff[nb] + 16 * g, kb * kBK);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) bb.q[2 * g + e / 2][nb][e & 1] = in ? v[e] : 0u;
+    for (int i = 0; i < 4; ++i) {
+      const u32x4 v = bload16(rd, voff[i], kb * kBK);
+      rb[i] = in ? v : u32x4{0u, 0u, 0u, 0u};
     }
   };
-  pgemm_loop<MS, NB, false, false>(a.hh, a.ldh, a.M, m0, kb0, kb1, sA, load_b, acc);
-  float sd[NB];
+  auto store_b = [&](int buf) {
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) sd[nb] = a.down_s[row[nb]];
+    for (int i = 0; i < 4; ++i) {
+      uint8_t* d = sB + buf * kBbuf + ((t >> 3) + 32 * i) * kLdB8 + 16 * (t & 7);
+      reinterpret_cast<u32x2*>(d)[0] = u32x2{rb[i].x, rb[i].y};
+      reinterpret_cast<u32x2*>(d)[1] = u32x2{rb[i].z, rb[i].w};
+    }
+  };
+  arows.load(kb0, ra);
+  load_b(kb0);
+  store_a_rows<2 * MS, false>(ra, sA);
+  store_b(0);
+  lds_barrier();
+  for (int kb = kb0; kb < kb1; ++kb) {
+    const int kn = min(kb + 1, kb1 - 1), cur = (kb - kb0) & 1;
+    arows.load(kn, ra);
+    load_b(kn);
+    __builtin_amdgcn_sched_barrier(0);
+    mma_block_lds<MS, 1, false>(sA + cur * kAbuf, sB + cur * kBbuf, nullptr, acc);
+    __builtin_amdgcn_sched_barrier(0);
+    store_a_rows<2 * MS, false>(ra, sA + (cur ^ 1) * kAbuf);
+    store_b(cur ^ 1);
+    lds_barrier();
+  }
+  const int row = nt * 128 + 32 * w + (l & 31);
+  const float sd = a.down_s[row];
 #pragma unroll
   for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int m = m0 + 32 * ms + 8 * (j >> 2) + 4 * (l >> 5) + (j & 3);
-        if (m >= a.M) continue;
-        float* p = a.y + (size_t)m * kH + row[nb];
-        if (splits == 1)
-          *p = acc[ms][nb][j] * sd[nb];   // the first and only hot writer
-        else
-          unsafeAtomicAdd(p, acc[ms][nb][j] * sd[nb]);
-      }
+    for (int j = 0; j < 16; ++j) {
+      const int m = m0 + 32 * ms + 8 * (j >> 2) + 4 * (l >> 5) + (j & 3);
+      if (m >= a.M) continue;
+      float* p = a.y + (size_t)m * kH + row;
+      if (splits == 1)
+        *p = acc[ms][0][j] * sd;   // the first and only hot writer
+      else
+        unsafeAtomicAdd(p, acc[ms][0][j] * sd);
+    }
 }
 
 // Cold down for 128 tokens x 256 outputs (4 waves x 64) over a range of the
@@ -1388,9 +1316,9 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
     } else if (p.prefill) {
       const dim3 grid(32 * p.pmt * p.hot_splits);
       if (p.pms == 4)
-        hipLaunchKernelGGL((k_pgemm_down_hot<4, 1>), grid, dim3(kThreads), 0, st, da, p.pmt, p.hot_splits);
+        hipLaunchKernelGGL(k_pgemm_down_hot<4>, grid, dim3(kThreads), 0, st, da, p.pmt, p.hot_splits);
       else
-        hipLaunchKernelGGL((k_pgemm_down_hot<2, 1>), grid, dim3(kThreads), 0, st, da, p.pmt, p.hot_splits);
+        hipLaunchKernelGGL(k_pgemm_down_hot<2>, grid, dim3(kThreads), 0, st, da, p.pmt, p.hot_splits);
     } else {
       hipLaunchKernelGGL(k_bdown_hot, dim3((kH / kBN) * p.hot_splits, p.mt), dim3(kThreads), 0, st,
                          da);
