@@ -824,11 +824,16 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_down_cold(BDownArgs a, int m
 
 // Workgroup = 16 weight rows (hot rows, or items of the dense active list);
 // wave w takes K blocks [8w, 8w+8).  MS = token subtiles of 16 (M <= 16 MS).
+// Hot rows are loaded as whole cache lines (8 lanes per 128-byte segment of
+// a row, every block's loads issued up front) and re-laid through a
+// wave-private LDS area into the MFMA operand layout; a cold record's block
+// (64 bytes per vector) is read by the 4 lanes that use it.
 template <int MS>
 __global__ __launch_bounds__(kThreads) void k_bup_s(BUpArgs a) {
   constexpr int NB = kH / kBK / 4;
   constexpr int PF = MS >= 4 ? 4 : 8;   // K blocks whose weight loads are in flight together
   __shared__ f32x4 s_red[3][2 * MS][kWave];
+  __shared__ __attribute__((aligned(16))) uint8_t s_w[4][32 * kLdB8];   // per wave: 16 gate + 16 up rows
   const int w = threadIdx.x >> 6, l = lane_id();
   const int kb0 = w * NB;
   const uint16_t* xr[MS];
@@ -847,31 +852,42 @@ __global__ __launch_bounds__(kThreads) void k_bup_s(BUpArgs a) {
   bool cv;
   int slot = -1;
   if (hot) {
-    col = blockIdx.x * 16 + (l & 15);
+    const int r0 = blockIdx.x * 16;
+    col = r0 + (l & 15);
     cv = col < a.n_hot;
-    const uint8_t* gr = a.gate_q + (size_t)(cv ? col : 0) * kH + 32 * (l >> 4);
-    const uint8_t* ur = a.up_q + (size_t)(cv ? col : 0) * kH + 32 * (l >> 4);
+    // load j (0..3) of a block: matrix j / 2 (gate, up), rows 8 (j & 1) + l / 8,
+    // 16-byte chunk l & 7; rows past n_hot read as zero
+    const rsrc_t rg = buf_rsrc(a.gate_q, (uint32_t)a.n_hot * kH);
+    const rsrc_t ru = buf_rsrc(a.up_q, (uint32_t)a.n_hot * kH);
+    uint32_t voff[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) voff[h] = (uint32_t)(r0 + 8 * h + (l >> 3)) * kH + 16 * (l & 7);
+    uint8_t* sw = s_w[w];
     for (int ph = 0; ph < NB; ph += PF) {
-      u32x4 G[PF][2], U[PF][2];
+      u32x4 W[PF][4];
+#pragma unroll
+      for (int b = 0; b < PF; ++b)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) W[b][j] = bload16(j < 2 ? rg : ru, voff[j & 1], (kb0 + ph + b) * kBK);
 #pragma unroll
       for (int b = 0; b < PF; ++b) {
-        const int k = (kb0 + ph + b) * kBK;
-        const u32x4 z = {0u, 0u, 0u, 0u};
-        G[b][0] = cv ? load16(gr + k) : z;
-        G[b][1] = cv ? load16(gr + k + 16) : z;
-        U[b][0] = cv ? load16(ur + k) : z;
-        U[b][1] = cv ? load16(ur + k + 16) : z;
-      }
+        // block b into the wave's rows: gate rows 0..15, up rows 16..31
 #pragma unroll
-      for (int b = 0; b < PF; ++b) {
+        for (int j = 0; j < 4; ++j) {
+          uint8_t* d = sw + (16 * (j >> 1) + 8 * (j & 1) + (l >> 3)) * kLdB8 + 16 * (l & 7);
+          reinterpret_cast<u32x2*>(d)[0] = u32x2{W[b][j].x, W[b][j].y};
+          reinterpret_cast<u32x2*>(d)[1] = u32x2{W[b][j].z, W[b][j].w};
+        }
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
           h8 A[MS];
 #pragma unroll
           for (int ms = 0; ms < MS; ++ms)
             A[ms] = av[ms] ? *reinterpret_cast<const h8*>(xr[ms] + (kb0 + ph + b) * kBK + 8 * s) : h8{};
-          const h8 bg = fp8x8_h8(dword_of(G[b][0], G[b][1], 2 * s), dword_of(G[b][0], G[b][1], 2 * s + 1));
-          const h8 bu = fp8x8_h8(dword_of(U[b][0], U[b][1], 2 * s), dword_of(U[b][0], U[b][1], 2 * s + 1));
+          const u32x2 g2 = *reinterpret_cast<const u32x2*>(sw + (l & 15) * kLdB8 + 32 * (l >> 4) + 8 * s);
+          const u32x2 u2 = *reinterpret_cast<const u32x2*>(sw + (16 + (l & 15)) * kLdB8 + 32 * (l >> 4) + 8 * s);
+          const h8 bg = fp8x8_h8(g2[0], g2[1]);
+          const h8 bu = fp8x8_h8(u2[0], u2[1]);
 #pragma unroll
           for (int ms = 0; ms < MS; ++ms) {
             accg[ms] = mfma16(A[ms], bg, accg[ms]);
@@ -881,11 +897,17 @@ __global__ __launch_bounds__(kThreads) void k_bup_s(BUpArgs a) {
       }
     }
   } else {
-    const int total = min(*a.total, a.cap);
+    // the list length and this lane's slot are loaded together (the list has
+    // cap entries, those past the length are ignored): one dependent hop
+    // fewer before the record loads
     const int i0 = ((int)blockIdx.x - a.hot_wg) * 16;
-    if (i0 >= total) return;   // the whole workgroup
     col = i0 + (l & 15);
-    slot = col < total ? a.dslots[col] : -1;
+    const int raw_total = *a.total;
+    const int raw_slot = a.dslots[min(col, a.cap - 1)];
+    asm volatile("" ::"v"(raw_slot), "s"(raw_total));   // both loads in flight before either is used
+    const int total = min(raw_total, a.cap);
+    if (i0 >= total) return;   // the whole workgroup
+    slot = col < total ? raw_slot : -1;
     cv = slot >= 0 && slot < a.n_records;
     const uint8_t* rec = a.records + (size_t)(cv ? slot : 0) * kRecBytes;
     const uint16_t* sc = reinterpret_cast<const uint16_t*>(rec + kOffScales);
