@@ -186,6 +186,72 @@ __device__ __forceinline__ void chunk_prefix(const ActiveList& al, int* s_prefix
     __syncthreads();
   }
 }
+// ── persistent token kernel (token.hip) ─────────────────────────────────────
+
+constexpr int kTokGroups = 256;            // workgroups per role (U and D)
+constexpr int kTokGrid = 2 * kTokGroups;
+constexpr int kTokChunks = 256;            // active-list chunks: one per U / D group
+constexpr int kTokMaxChunk = 64;           // ids per chunk (one lane each)
+constexpr int kTokMaxRank = 64;
+constexpr int kTokMaxHot = 4096;           // h staged in LDS
+constexpr int kTokSyncWords = 2048 + 192;
+constexpr int kTokSyncErr = 2048 + 128;       // nonzero: a wait ran past its bound
+
+// One layer as the token kernel reads it (a device-resident table).
+struct TokLayer {
+  // hot half
+  int n_hot, down_stride;
+  const uint8_t* gate_q;
+  const uint8_t* up_q;
+  const float* gate_s;
+  const float* up_s;
+  const float* hot_gbias;
+  const uint8_t* down_q;
+  const float* down_s;
+  // cold half and the active list it reads (kTokChunks chunks of act_chunk)
+  int n_records, act_chunk;
+  const uint8_t* records;
+  const float* cold_gbias;
+  const int32_t* act_slots;
+  const int32_t* act_counts;
+  const uint16_t* norm_w;
+  // this layer's predictor (run one layer ahead); pd_w null: none
+  int rank, inter;
+  const uint16_t* pd_w;     // (rank, H) bf16
+  const uint16_t* pu_w;     // (inter, rank) bf16
+  const uint16_t* pu_b;     // (inter) bf16
+  const int32_t* lut;
+  int32_t* sel_slots;       // where its list is written: chunk c at c * sel_chunk
+  int32_t* sel_ids;
+  int32_t* sel_counts;
+  int sel_chunk;
+};
+
+struct TokArgs {
+  const TokLayer* layers;
+  int n_layers;
+  const uint16_t* x_in;
+  uint16_t* x_out;
+  // Everything below is written at most once per launch and read only after
+  // the signal that completes it, so it is read with cached loads: one slice
+  // per layer.
+  uint16_t* xbuf;           // (n_layers, H) layer outputs
+  uint16_t* xw;             // (n_layers, H) x_L * norm weight of layer L
+  float* ssq;               // (n_layers, 256) sum-of-squares partials of x_L
+  float* h;                 // (n_layers, hstride) hot activations
+  float* hc;                // (n_layers, kTokChunks * kTokMaxChunk) cold activations, list order
+  float* z;                 // (n_layers, kTokMaxRank) predictor down projection of layer L
+  int hstride;
+  uint32_t* sync;           // kTokSyncWords, zero at launch
+  float eps, thr;
+  int relu, both;
+};
+
+__global__ void k_tok_prep(const uint16_t* x, const uint16_t* w, uint16_t* xw, float* ssq,
+                           uint32_t* sync);
+int tok_launch(const TokArgs& a, int npw, hipStream_t st);
+int tok_resident(int npw, int* resident);
+
 __global__ void k_prep(const uint16_t* x, const uint16_t* w, uint16_t* xw, float* ssq);
 __global__ void k_ffn_up(UpArgs a);
 __global__ void k_ffn_down(DownArgs a);

@@ -11,6 +11,7 @@
 // so there is no host synchronisation inside a token.  The launch sequence
 // is captured once into a hipGraph per (x_in, x_out, stream) and replayed.
 #include <algorithm>
+#include <string>
 #include <vector>
 
 #include "capi_util.h"
@@ -61,6 +62,24 @@ struct oi2_stack {
     hipStream_t stream;
   };
   std::vector<GraphEntry> graphs;   // small cache keyed by (x_in, x_out, stream)
+  // persistent token kernel: its own active lists (kTokChunks chunks of
+  // tok_chunk ids per layer), signal area and cold activations
+  bool tok_ok = false;       // this configuration supports it
+  bool tok = false;          // decodes use it (when not staged)
+  std::string tok_why;
+  int tok_npw = 0, tok_chunk = 0;
+  oi2::TokLayer* tok_layers = nullptr;
+  uint32_t* tok_sync = nullptr;
+  uint16_t* tok_xw = nullptr;    // one slice per layer of everything the launch writes
+  float* tok_ssq = nullptr;
+  float* tok_h = nullptr;
+  float* tok_hc = nullptr;
+  float* tok_z = nullptr;
+  int tok_hstride = 0;
+  int32_t* tok_sel_counts = nullptr;
+  int32_t* tok_sel_slots = nullptr;
+  int32_t* tok_sel_ids = nullptr;
+  std::vector<int32_t*> tok_static;   // all-record lists of layers without a predictor
 };
 
 namespace oi2 {
@@ -272,7 +291,46 @@ static int stack_launch_staged(oi2_stack* s, const uint16_t* x_in, uint16_t* x_o
   return OI2_OK;
 }
 
-static int stack_launch(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, hipStream_t st) {
+static inline bool use_tok(const oi2_stack* s) { return s->tok && s->tok_ok && !s->staged; }
+
+static TokArgs tok_args(const oi2_stack* s, const uint16_t* x_in, uint16_t* x_out) {
+  TokArgs a{};
+  a.layers = s->tok_layers;
+  a.n_layers = s->n_layers;
+  a.x_in = x_in;
+  a.x_out = x_out;
+  a.xbuf = s->xbuf;
+  a.xw = s->tok_xw;
+  a.ssq = s->tok_ssq;
+  a.h = s->tok_h;
+  a.hc = s->tok_hc;
+  a.z = s->tok_z;
+  a.hstride = s->tok_hstride;
+  a.sync = s->tok_sync;
+  a.eps = s->eps;
+  a.thr = s->thr;
+  a.relu = s->relu;
+  a.both = s->both;
+  return a;
+}
+
+// Layer 0's x * w and sum-of-squares partials from x_in, and a cleared
+// signal area: the launch before each persistent token kernel.
+static int launch_tok_prep(oi2_stack* s, const uint16_t* x_in, hipStream_t st) {
+  hipLaunchKernelGGL(k_tok_prep, dim3(1), dim3(kThreads), 0, st, x_in, s->layers[0].l.norm_w, s->tok_xw,
+                     s->tok_ssq, s->tok_sync);
+  OI2_CHECK_LAUNCH();
+  return OI2_OK;
+}
+
+// The token as one persistent launch.
+static int stack_launch_tok(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, hipStream_t st) {
+  const int rc = launch_tok_prep(s, x_in, st);
+  return rc ? rc : tok_launch(tok_args(s, x_in, x_out), s->tok_npw, st);
+}
+
+// The two-launch-per-layer sequence (or the staged one).
+static int stack_launch_layers(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, hipStream_t st) {
   if (s->staged) return stack_launch_staged(s, x_in, x_out, st);
   hipLaunchKernelGGL(k_prep, dim3(1), dim3(kThreads), 0, st, x_in, s->layers[0].l.norm_w, s->xw,
                      s->ssq);
@@ -291,6 +349,10 @@ static int stack_launch(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, hip
     if (rc) return rc;
   }
   return OI2_OK;
+}
+
+static int stack_launch(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, hipStream_t st) {
+  return use_tok(s) ? stack_launch_tok(s, x_in, x_out, st) : stack_launch_layers(s, x_in, x_out, st);
 }
 
 // Device-visible address of a record array: device memory as is, pinned host
@@ -338,10 +400,159 @@ static void stack_free(oi2_stack* s) {
   }
   for (auto& g : s->graphs) (void)hipGraphExecDestroy(g.exec);
   s->graphs.clear();
+  for (int32_t* p : s->tok_static)
+    if (p) (void)hipFree(p);
+  s->tok_static.clear();
+  for (void* p : {(void*)s->tok_layers, (void*)s->tok_sync, (void*)s->tok_xw, (void*)s->tok_ssq,
+                  (void*)s->tok_h, (void*)s->tok_hc, (void*)s->tok_z, (void*)s->tok_sel_counts,
+                  (void*)s->tok_sel_slots, (void*)s->tok_sel_ids})
+    if (p) (void)hipFree(p);
   for (void* p : {(void*)s->xbuf, (void*)s->xw, (void*)s->ssq, (void*)s->h_hot, (void*)s->cold_part,
                   (void*)s->cold_total, (void*)s->z, (void*)s->sel_counts,
                   (void*)s->sel_slots, (void*)s->sel_ids})
     if (p) (void)hipFree(p);
+}
+
+// Decide whether the persistent token kernel can run this stack and, if so,
+// allocate its buffers and build the device-resident layer table.  An
+// unsupported configuration is not an error (tok_why says why); an
+// allocation failure is.
+static int tok_setup(oi2_stack* s) {
+  s->tok_ok = false;
+  s->tok = false;
+  char why[160] = {0};
+  const int n = s->n_layers;
+  const int chunk = (s->inter + kTokChunks - 1) / kTokChunks;
+  int max_hot = 0, max_rank = 0;
+  for (int L = 0; L < n && !why[0]; ++L) {
+    const StackLayer& SL = s->layers[L];
+    const oi2_layer& l = SL.l;
+    max_hot = std::max(max_hot, l.hot.n_hot);
+    if (l.hot.n_hot > kTokMaxHot) snprintf(why, sizeof why, "layer %d: n_hot %d > %d", L, l.hot.n_hot, kTokMaxHot);
+    if (SL.has_pred) {
+      max_rank = std::max(max_rank, l.pred.rank);
+      if (l.pred.dtype != OI2_DTYPE_BF16 || l.pred.rank > kTokMaxRank)
+        snprintf(why, sizeof why, "layer %d: the predictor is not bf16 of rank <= %d", L, kTokMaxRank);
+    }
+    if (l.cold.n_records > 0) {
+      hipPointerAttribute_t at{};
+      if (hipPointerGetAttributes(&at, l.cold.records) != hipSuccess || at.type != hipMemoryTypeDevice) {
+        (void)hipGetLastError();
+        snprintf(why, sizeof why, "layer %d: cold records are not in device memory", L);
+      }
+    }
+  }
+  const int npw = max_hot <= 2 * 4 * kTokGroups ? 2 : 4;
+  if (!why[0] && chunk > kTokMaxChunk)
+    snprintf(why, sizeof why, "inter %d > %d", s->inter, kTokChunks * kTokMaxChunk);
+  if (!why[0] && (max_hot + npw - 1) / npw + max_rank > 4 * kTokGroups)
+    snprintf(why, sizeof why, "n_hot %d with predictor rank %d exceeds the U waves", max_hot, max_rank);
+  int resident = 0;
+  if (!why[0] && tok_resident(npw, &resident) != OI2_OK) return OI2_EHIP;
+  if (!why[0] && resident < kTokGrid)
+    snprintf(why, sizeof why, "the device holds %d of the %d workgroups at once", resident, kTokGrid);
+  if (why[0]) {
+    s->tok_why = why;
+    return OI2_OK;
+  }
+  hipError_t e = hipSuccess;
+  auto alloc = [&](void** p, size_t bytes) {
+    if (e == hipSuccess) e = hipMalloc(p, bytes);
+  };
+  const size_t sel = (size_t)n * kTokChunks * chunk;
+  alloc((void**)&s->tok_layers, (size_t)n * sizeof(TokLayer));
+  alloc((void**)&s->tok_sync, (size_t)kTokSyncWords * 4);
+  s->tok_hstride = (max_hot + 63) / 64 * 64;
+  alloc((void**)&s->tok_xw, (size_t)n * kH * 2);
+  alloc((void**)&s->tok_ssq, (size_t)n * kTokGroups * 4);
+  alloc((void**)&s->tok_h, (size_t)n * std::max(s->tok_hstride, 64) * 4);
+  alloc((void**)&s->tok_hc, (size_t)n * kTokChunks * kTokMaxChunk * 4);
+  alloc((void**)&s->tok_z, (size_t)n * kTokMaxRank * 4);
+  alloc((void**)&s->tok_sel_counts, (size_t)n * kTokChunks * 4);
+  alloc((void**)&s->tok_sel_slots, sel * 4);
+  alloc((void**)&s->tok_sel_ids, sel * 4);
+  if (e == hipSuccess) e = hipMemset(s->tok_sel_counts, 0, (size_t)n * kTokChunks * 4);
+  // h slices past n_hot are never written and must read as zero
+  if (e == hipSuccess) e = hipMemset(s->tok_h, 0, (size_t)n * std::max(s->tok_hstride, 64) * 4);
+  std::vector<TokLayer> tab(n);
+  for (int L = 0; L < n && e == hipSuccess; ++L) {
+    const StackLayer& SL = s->layers[L];
+    const oi2_layer& l = SL.l;
+    TokLayer& T = tab[L];
+    T = TokLayer{};
+    T.n_hot = l.hot.n_hot;
+    T.down_stride = l.hot.down_stride;
+    T.gate_q = l.hot.gate_q;
+    T.up_q = l.hot.up_q;
+    T.gate_s = l.hot.gate_scale;
+    T.up_s = l.hot.up_scale;
+    T.hot_gbias = l.hot.gate_bias;
+    T.down_q = l.hot.down_q;
+    T.down_s = l.hot.down_scale;
+    T.norm_w = l.norm_w;
+    T.n_records = l.cold.n_records;
+    T.records = l.cold.records;
+    T.cold_gbias = l.cold.gate_bias;
+    int32_t* own_slots = s->tok_sel_slots + (size_t)L * kTokChunks * chunk;
+    int32_t* own_ids = s->tok_sel_ids + (size_t)L * kTokChunks * chunk;
+    int32_t* own_counts = s->tok_sel_counts + (size_t)L * kTokChunks;
+    if (SL.has_pred) {
+      T.rank = l.pred.rank;
+      T.inter = l.pred.inter;
+      T.pd_w = static_cast<const uint16_t*>(l.pred.down_w);
+      T.pu_w = static_cast<const uint16_t*>(l.pred.up_w);
+      T.pu_b = static_cast<const uint16_t*>(l.pred.up_b);
+      T.lut = l.lut;
+      T.sel_slots = own_slots;
+      T.sel_ids = own_ids;
+      T.sel_counts = own_counts;
+      T.sel_chunk = chunk;
+    }
+    if (l.cold.n_records > 0) {
+      if (SL.has_pred) {
+        T.act_slots = own_slots;
+        T.act_counts = own_counts;
+        T.act_chunk = chunk;
+      } else {
+        // every cold record, ascending neuron id (engine.py:282-283), cut into
+        // kTokChunks chunks
+        std::vector<int32_t> lut(s->inter);
+        e = hipMemcpy(lut.data(), l.lut, (size_t)s->inter * 4, hipMemcpyDeviceToHost);
+        std::vector<int32_t> all;
+        for (int i = 0; i < s->inter; ++i)
+          if (lut[i] >= 0 && lut[i] < l.cold.n_records) all.push_back(lut[i]);
+        const int ca = std::max<int>(1, ((int)all.size() + kTokChunks - 1) / kTokChunks);
+        std::vector<int32_t> host((size_t)kTokChunks * ca + kTokChunks, -1);
+        for (int c = 0; c < kTokChunks; ++c) {
+          const int b = c * ca, m = std::max(0, std::min(ca, (int)all.size() - b));
+          for (int k = 0; k < m; ++k) host[(size_t)c * ca + k] = all[b + k];
+          host[(size_t)kTokChunks * ca + c] = m;
+        }
+        int32_t* buf = nullptr;
+        alloc((void**)&buf, host.size() * 4);
+        if (buf) s->tok_static.push_back(buf);
+        if (e == hipSuccess) e = hipMemcpy(buf, host.data(), host.size() * 4, hipMemcpyHostToDevice);
+        T.act_slots = buf;
+        T.act_counts = buf + (size_t)kTokChunks * ca;
+        T.act_chunk = ca;
+      }
+    }
+  }
+  if (e == hipSuccess) e = hipMemcpy(s->tok_layers, tab.data(), (size_t)n * sizeof(TokLayer), hipMemcpyHostToDevice);
+  if (e != hipSuccess) {
+    set_error("token kernel allocation failed: %s", hipGetErrorString(e));
+    return OI2_ENOMEM;
+  }
+  s->tok_npw = npw;
+  s->tok_chunk = chunk;
+  s->tok_ok = true;
+  s->tok = true;
+  return OI2_OK;
+}
+
+static void drop_graphs(oi2_stack* s) {
+  for (auto& g : s->graphs) (void)hipGraphExecDestroy(g.exec);
+  s->graphs.clear();
 }
 
 }  // namespace oi2
@@ -450,6 +661,12 @@ int oi2_stack_create(const oi2_layer* layers, int32_t n_layers, int32_t inter, f
     stack_free(s);
     delete s;
     return OI2_ENOMEM;
+  }
+  const int rc = tok_setup(s);
+  if (rc != OI2_OK) {
+    stack_free(s);
+    delete s;
+    return rc;
   }
   *out = s;
   return OI2_OK;
@@ -584,9 +801,10 @@ int oi2_stack_profile(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, int32
       set_error("hipEventCreate failed");
       rc = OI2_EHIP;
     }
-  // one real token fixes every layer's active set; then every layer's ffn_up
-  // back to back, reps times, then every layer's ffn_down the same way
-  if (rc == OI2_OK) rc = stack_launch(s, x_in, x_out, st);
+  // one real token (two-launch sequence) fixes every layer's active set; then
+  // every layer's ffn_up back to back, reps times, then every layer's ffn_down
+  // the same way
+  if (rc == OI2_OK) rc = stack_launch_layers(s, x_in, x_out, st);
   std::vector<UpArgs> ua(s->n_layers);
   std::vector<DownArgs> da(s->n_layers);
   for (int L = 0; L < s->n_layers; ++L) layer_args(s, L, x_in, x_out, ua[L], da[L]);
@@ -625,14 +843,90 @@ int oi2_stack_trace(oi2_stack* s, uint16_t* xs, int32_t* counts, int32_t* slots,
   clear_error();
   OI2_CHECK_ARG(s, "null stack");
   hipStream_t st = (hipStream_t)stream;
-  const size_t sel = (size_t)s->n_layers * s->n_chunks * kSelChunk;
+  const bool tk = use_tok(s);
+  const int nc = tk ? kTokChunks : s->n_chunks;
+  const size_t sel = (size_t)s->n_layers * nc * (tk ? s->tok_chunk : kSelChunk);
   if (xs) OI2_CHECK_HIP(hipMemcpyAsync(xs, s->xbuf, (size_t)s->n_layers * kH * 2, hipMemcpyDeviceToDevice, st));
   if (counts)
-    OI2_CHECK_HIP(hipMemcpyAsync(counts, s->sel_counts, (size_t)s->n_layers * s->n_chunks * 4,
+    OI2_CHECK_HIP(hipMemcpyAsync(counts, tk ? s->tok_sel_counts : s->sel_counts, (size_t)s->n_layers * nc * 4,
                                  hipMemcpyDeviceToDevice, st));
-  if (slots) OI2_CHECK_HIP(hipMemcpyAsync(slots, s->sel_slots, sel * 4, hipMemcpyDeviceToDevice, st));
-  if (ids) OI2_CHECK_HIP(hipMemcpyAsync(ids, s->sel_ids, sel * 4, hipMemcpyDeviceToDevice, st));
+  if (slots)
+    OI2_CHECK_HIP(hipMemcpyAsync(slots, tk ? s->tok_sel_slots : s->sel_slots, sel * 4, hipMemcpyDeviceToDevice, st));
+  if (ids) OI2_CHECK_HIP(hipMemcpyAsync(ids, tk ? s->tok_sel_ids : s->sel_ids, sel * 4, hipMemcpyDeviceToDevice, st));
   return OI2_OK;
+}
+
+int oi2_stack_selection_layout(const oi2_stack* s, int32_t* n_chunks, int32_t* chunk) {
+  clear_error();
+  OI2_CHECK_ARG(s && n_chunks && chunk, "null argument");
+  const bool tk = use_tok(s);
+  *n_chunks = tk ? kTokChunks : s->n_chunks;
+  *chunk = tk ? s->tok_chunk : kSelChunk;
+  return OI2_OK;
+}
+
+int oi2_stack_set_token_kernel(oi2_stack* s, int32_t enable) {
+  clear_error();
+  OI2_CHECK_ARG(s, "null stack");
+  if (enable && !s->tok_ok) {
+    set_error("the persistent token kernel does not support this stack: %s", s->tok_why.c_str());
+    return OI2_EUNSUPPORTED;
+  }
+  drop_graphs(s);
+  s->tok = enable != 0;
+  return OI2_OK;
+}
+
+int32_t oi2_stack_token_kernel(const oi2_stack* s) { return (s && use_tok(s)) ? 1 : 0; }
+
+int oi2_stack_status(oi2_stack* s, void* stream) {
+  clear_error();
+  OI2_CHECK_ARG(s, "null stack");
+  OI2_CHECK_HIP(hipStreamSynchronize((hipStream_t)stream));
+  if (!use_tok(s)) return OI2_OK;
+  uint32_t err = 0;
+  OI2_CHECK_HIP(hipMemcpy(&err, s->tok_sync + kTokSyncErr, 4, hipMemcpyDeviceToHost));
+  if (err) {
+    set_error("persistent token kernel: a device-wide wait ran past its bound");
+    return OI2_EHIP;
+  }
+  return OI2_OK;
+}
+
+int oi2_stack_profile_token(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, int32_t reps,
+                            float* token_us, void* stream) {
+  clear_error();
+  OI2_CHECK_ARG(s && x_in && x_out && token_us, "null argument");
+  OI2_CHECK_ARG(reps > 0 && reps <= 4096, "reps %d out of range", reps);
+  OI2_CHECK_ARG(use_tok(s), "the persistent token kernel is not in use on this stack");
+  hipStream_t st = (hipStream_t)stream;
+  std::vector<hipEvent_t> ev(2 * (size_t)reps, nullptr);
+  int rc = OI2_OK;
+  for (auto& e : ev)
+    if (rc == OI2_OK && hipEventCreate(&e) != hipSuccess) {
+      set_error("hipEventCreate failed");
+      rc = OI2_EHIP;
+    }
+  if (rc == OI2_OK) rc = stack_launch_tok(s, x_in, x_out, st);
+  const TokArgs a = tok_args(s, x_in, x_out);
+  for (int r = 0; rc == OI2_OK && r < reps; ++r) {
+    rc = launch_tok_prep(s, x_in, st);
+    if (rc == OI2_OK && hipEventRecord(ev[2 * r], st) != hipSuccess) rc = OI2_EHIP;
+    if (rc == OI2_OK) rc = tok_launch(a, s->tok_npw, st);
+    if (rc == OI2_OK && hipEventRecord(ev[2 * r + 1], st) != hipSuccess) rc = OI2_EHIP;
+  }
+  if (rc == OI2_OK && hipStreamSynchronize(st) != hipSuccess) rc = OI2_EHIP;
+  double total = 0.0;
+  for (int r = 0; rc == OI2_OK && r < reps; ++r) {
+    float ms = 0.0f;
+    if (hipEventElapsedTime(&ms, ev[2 * r], ev[2 * r + 1]) != hipSuccess) rc = OI2_EHIP;
+    total += ms;
+  }
+  if (rc == OI2_EHIP && !oi2_last_error()[0]) set_error("HIP call failed while profiling");
+  if (rc == OI2_OK) *token_us = (float)(total * 1e3 / reps);
+  for (auto& e : ev)
+    if (e) (void)hipEventDestroy(e);
+  return rc;
 }
 
 int oi2_stack_destroy(oi2_stack* s) {

@@ -78,6 +78,12 @@ _SIGS = {
     "oi2_stack_profile_staging": (c_int32, [c_void_p, c_void_p, c_void_p, c_int32, POINTER(c_float),
                                             c_void_p]),
     "oi2_stack_trace": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "oi2_stack_selection_layout": (c_int32, [c_void_p, POINTER(c_int32), POINTER(c_int32)]),
+    "oi2_stack_set_token_kernel": (c_int32, [c_void_p, c_int32]),
+    "oi2_stack_token_kernel": (c_int32, [c_void_p]),
+    "oi2_stack_status": (c_int32, [c_void_p, c_void_p]),
+    "oi2_stack_profile_token": (c_int32, [c_void_p, c_void_p, c_void_p, c_int32, POINTER(c_float),
+                                          c_void_p]),
     "oi2_stack_destroy": (c_int32, [c_void_p]),
     "oi2_section_bytes": (c_size_t, [c_int32]),
     "oi2_quantize_section": (c_int32, [c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p,

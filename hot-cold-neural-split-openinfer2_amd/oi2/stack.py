@@ -59,6 +59,36 @@ class DecodeStack:
         reads the records where they are."""
         _lib.check(_lib.lib().oi2_stack_set_staging(self._h, int(copy_workgroups)))
 
+    def set_token_kernel(self, enable: bool):
+        """Run each token as one persistent kernel (the default where the
+        configuration allows it) or as two launches per layer."""
+        _lib.check(_lib.lib().oi2_stack_set_token_kernel(self._h, int(bool(enable))))
+
+    @property
+    def token_kernel(self) -> bool:
+        return bool(_lib.lib().oi2_stack_token_kernel(self._h))
+
+    def status(self, stream=None):
+        """Wait for the stream; raise OI2Error if a device-wide wait of the
+        persistent kernel ran past its bound in the last token."""
+        dev = self.layers[0].norm_w.device
+        s = stream.cuda_stream if stream is not None else _lib.stream_handle(dev)
+        _lib.check(_lib.lib().oi2_stack_status(self._h, s or None))
+
+    def profile_token(self, x_in: torch.Tensor, x_out: torch.Tensor, stream=None, reps: int = 16):
+        """Mean microseconds of the persistent token kernel alone."""
+        us = ctypes.c_float()
+        s = stream.cuda_stream if stream is not None else _lib.stream_handle(x_in.device)
+        _lib.check(_lib.lib().oi2_stack_profile_token(self._h, x_in.data_ptr(), x_out.data_ptr(),
+                                                      int(reps), ctypes.byref(us), s or None))
+        return us.value
+
+    def selection_layout(self) -> tuple[int, int]:
+        """(n_chunks, chunk) of the active sets trace() returns."""
+        nc, ch = ctypes.c_int32(), ctypes.c_int32()
+        _lib.check(_lib.lib().oi2_stack_selection_layout(self._h, ctypes.byref(nc), ctypes.byref(ch)))
+        return nc.value, ch.value
+
     def set_expected_active(self, n: int):
         """Size the cold pass for about n active records per layer."""
         _lib.check(_lib.lib().oi2_stack_set_expected_active(self._h, int(n)))
@@ -88,26 +118,30 @@ class DecodeStack:
 
     def trace(self):
         """(xs (n_layers, H) fp16 layer outputs, counts (n_layers, n_chunks),
-        slots, ids (n_layers, n_chunks*256)) of the last decode."""
+        slots, ids (n_layers, n_chunks * chunk)) of the last decode, in the
+        chunking selection_layout() reports."""
         dev = self.layers[0].norm_w.device
-        n, nc = self.n_layers, self.n_chunks
+        n = self.n_layers
+        nc, ch = self.selection_layout()
         xs = torch.empty((n, HIDDEN), dtype=torch.float16, device=dev)
         counts = torch.empty((n, nc), dtype=torch.int32, device=dev)
-        slots = torch.empty((n, nc * _lib.SEL_CHUNK), dtype=torch.int32, device=dev)
-        ids = torch.empty((n, nc * _lib.SEL_CHUNK), dtype=torch.int32, device=dev)
+        slots = torch.empty((n, nc * ch), dtype=torch.int32, device=dev)
+        ids = torch.empty((n, nc * ch), dtype=torch.int32, device=dev)
         _lib.check(_lib.lib().oi2_stack_trace(self._h, xs.data_ptr(), counts.data_ptr(),
                                               slots.data_ptr(), ids.data_ptr(),
                                               _lib.stream_handle(dev)))
         return xs, counts, slots, ids
 
     def active_ids(self, layer: int, counts=None, ids=None) -> list[int]:
+        """Layer `layer`'s active cold ids of the last decode, ascending."""
         if counts is None:
             _, counts, _, ids = self.trace()
+        _, ch = self.selection_layout()
         c = counts[layer].cpu().tolist()
         row = ids[layer].cpu()
         out = []
-        for k, n in enumerate(c):
-            out.extend(row[k * _lib.SEL_CHUNK: k * _lib.SEL_CHUNK + n].tolist())
+        for k, m in enumerate(c):
+            out.extend(row[k * ch: k * ch + m].tolist())
         return out
 
     def close(self):

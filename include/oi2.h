@@ -219,10 +219,35 @@ int oi2_stack_profile_staging(oi2_stack* s, const uint16_t* x_in, uint16_t* x_ou
 int oi2_stack_profile(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, int32_t reps,
                       float* up_us, float* down_us, void* stream);
 /* Each layer's output (n_layers, H) fp16 and the active sets of the last
- * decode: counts (n_layers, n_chunks) and slots/ids (n_layers, n_chunks*256),
- * copied to device buffers supplied by the caller (any may be NULL). */
+ * decode: counts (n_layers, n_chunks) and slots/ids (n_layers, n_chunks*chunk)
+ * in the layout oi2_stack_selection_layout reports, copied to device buffers
+ * supplied by the caller (any may be NULL).  Chunk c holds counts[c] ids,
+ * ascending; the chunks in order give _cold_ids_for's list (engine.py:274-283). */
 int oi2_stack_trace(oi2_stack* s, uint16_t* xs, int32_t* counts, int32_t* slots, int32_t* ids,
                     void* stream);
+/* The chunking of the active sets oi2_stack_trace returns: n_chunks chunks of
+ * at most `chunk` ids per layer (n_chunks * chunk >= inter). */
+int oi2_stack_selection_layout(const oi2_stack* s, int32_t* n_chunks, int32_t* chunk);
+/* The whole token as one persistent kernel (default on where supported):
+ * every layer's FFN and the lookahead predictor run in a single launch of
+ * 512 co-resident workgroups that hand the phases over through device-wide
+ * counters, each loading its next layer's weights before it waits (the same
+ * layer loop, engine.py:421-438, with no launch boundary between layers).
+ * Needs HBM-resident records, bf16 predictors of rank <= 64, n_hot <= 4096
+ * and inter <= 16384, and no staging; returns OI2_EUNSUPPORTED otherwise.
+ * 0 selects the two-launch-per-layer sequence.  Drops captured graphs. */
+int oi2_stack_set_token_kernel(oi2_stack* s, int32_t enable);
+/* 1 when decodes run as the persistent token kernel, else 0. */
+int32_t oi2_stack_token_kernel(const oi2_stack* s);
+/* Waits for `stream`; OI2_EHIP if a device-wide wait of the last
+ * persistent-kernel token ran past its bound (that token's output is then
+ * invalid), else OI2_OK. */
+int oi2_stack_status(oi2_stack* s, void* stream);
+/* Mean microseconds of the persistent token kernel alone: decodes x_in once,
+ * then `reps` times the token's two launches, timing the persistent kernel
+ * between hipEvents on `stream`; leaves the state of decoding x_in. */
+int oi2_stack_profile_token(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, int32_t reps,
+                            float* token_us, void* stream);
 int oi2_stack_destroy(oi2_stack* s);
 
 /* ---- split writer ------------------------------------------------------- */

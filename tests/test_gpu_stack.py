@@ -32,23 +32,41 @@ def stack4():
     return dev, g, layers, st, thr
 
 
-def _active_ids(counts, ids, L):
+def _ids_two_launch(counts, ids, L):
+    """Active ids of layer L from a trace taken on the two-launch path
+    (chunks of 256)."""
     out = []
     for c, n in enumerate(counts[L].cpu().tolist()):
         out.extend(ids[L, c * 256: c * 256 + n].cpu().tolist())
     return out
 
 
-def test_stack_layers_match_oracle(stack4):
+def test_token_kernel_selected_by_default(stack4):
+    """This geometry (n_hot 3584, bf16 rank-64 predictors, HBM records) runs
+    as the persistent token kernel unless told otherwise."""
     dev, g, layers, st, thr = stack4
+    assert st.token_kernel
+    assert st.selection_layout() == (256, 56)
+    st.set_token_kernel(False)
+    try:
+        assert not st.token_kernel and st.selection_layout() == (56, 256)
+    finally:
+        st.set_token_kernel(True)
+
+
+@pytest.mark.parametrize("token", [True, False], ids=["token_kernel", "two_launches"])
+def test_stack_layers_match_oracle(stack4, token):
+    dev, g, layers, st, thr = stack4
+    st.set_token_kernel(token)
     stream = torch.cuda.Stream(device=dev)
     x_in = torch.randn(H, generator=g, device=dev).half()
     x_out = torch.empty_like(x_in)
     with torch.cuda.stream(stream):
         st.decode(x_in, x_out, stream)
-    stream.synchronize()
+    st.status(stream)
     xs, counts, slots, ids = st.trace()
     torch.cuda.synchronize()
+    st.set_token_kernel(True)
     assert torch.equal(xs[-1], x_out)
     inputs = [x_in] + [xs[i] for i in range(3)]
     for L, lay in enumerate(layers):
@@ -61,7 +79,7 @@ def test_stack_layers_match_oracle(stack4):
             D, U, b = pred_weights(lay.predictor)
             logits = O.predictor_logits(q, D, U, b)
             want = O.cold_ids_for(logits >= thr, lay.hot_ids.cpu().tolist(), lay.inter)
-            got = _active_ids(counts, ids, L)
+            got = st.active_ids(L, counts, ids) if token else _ids_two_launch(counts, ids, L)
             assert got == sorted(got)
             amb = np.abs(logits - thr) <= 1e-6
             assert all(amb[i] for i in set(got) ^ set(want)), f"layer {L}: index sets differ"
@@ -96,6 +114,7 @@ def test_graph_replay_is_deterministic(stack4):
     x_d = torch.empty_like(x_in)
     direct.decode(x_in, x_d, None)
     other = DecodeStack(st.layers, st.inter, EPS, "silu", False, thr, use_graph=False)
+    other.set_token_kernel(False)
     x_o = torch.empty_like(x_in)
     other.decode(x_in, x_o, None)
     torch.cuda.synchronize()
@@ -109,6 +128,9 @@ def test_graph_replay_is_deterministic(stack4):
     torch.cuda.synchronize()
     assert up_us > 0 and down_us > 0
     assert torch.equal(x_d, outs[0])     # profiling leaves the state of decoding x_in
+    tok_us = direct.profile_token(x_in, x_d, reps=3)
+    direct.status()
+    assert tok_us > 0 and torch.equal(x_d, outs[0])
     direct.close()
 
 
@@ -120,10 +142,15 @@ def test_staged_store_matches_resident(stack4):
     stream = torch.cuda.Stream(device=dev)
     x_in = torch.randn(H, generator=g, device=dev).half()
     ref = torch.empty_like(x_in)
-    with torch.cuda.stream(stream):
-        st.decode(x_in, ref, stream)
-    stream.synchronize()
-    _, c_ref, _, i_ref = st.trace()
+    st.set_token_kernel(False)          # the staged path runs the same two launches per layer
+    try:
+        with torch.cuda.stream(stream):
+            st.decode(x_in, ref, stream)
+        stream.synchronize()
+        _, c_ref, _, i_ref = st.trace()
+        torch.cuda.synchronize()
+    finally:
+        st.set_token_kernel(True)
 
     pinned = [l.records.cpu().pin_memory() for l in layers]
     staged = DecodeStack([StackLayer(l.hot, p, l.lut, l.norm_w, l.predictor)
@@ -141,7 +168,7 @@ def test_staged_store_matches_resident(stack4):
     torch.cuda.synchronize()
     assert torch.equal(c, c_ref)
     for L in range(4):      # entries past each chunk's count are unspecified
-        assert _active_ids(c, i, L) == _active_ids(c_ref, i_ref, L)
+        assert _ids_two_launch(c, i, L) == _ids_two_launch(c_ref, i_ref, L)
     # direct launches on the default stream, and device-memory sources
     direct = DecodeStack(st.layers, st.inter, EPS, "silu", False, thr, use_graph=False, staging=16)
     direct.set_expected_active(300)
@@ -161,3 +188,29 @@ def test_pageable_records_rejected(stack4):
     pageable = [StackLayer(l.hot, l.records.cpu(), l.lut, l.norm_w, l.predictor) for l in layers]
     with pytest.raises(oi2.OI2Error, match="pinned host"):
         DecodeStack(pageable, st.inter, EPS, "silu", False, thr)
+
+
+def test_token_kernel_matches_two_launches(stack4):
+    """The persistent kernel against the two-launch sequence on one token.
+    Layers 0 and 1 are selected from x_in itself by the same arithmetic, so
+    their active sets are identical; the outputs differ only in the order
+    the cold down terms are summed."""
+    dev, g, layers, st, thr = stack4
+    x_in = torch.randn(H, generator=g, device=dev).half()
+    res = {}
+    for token in (True, False):
+        st.set_token_kernel(token)
+        out = torch.empty_like(x_in)
+        st.decode(x_in, out, None)
+        st.status()
+        xs, counts, _, ids = st.trace()
+        torch.cuda.synchronize()
+        sel = [st.active_ids(L, counts, ids) for L in (0, 1)]
+        res[token] = (out.clone(), xs.clone(), sel)
+    st.set_token_kernel(True)
+    assert res[True][2] == res[False][2]
+    assert all(len(s) > 0 for s in res[True][2])
+    for L in range(4):
+        assert_ffn_close(res[True][1][L].double().cpu().numpy(), res[False][1][L].double().cpu().numpy(),
+                         tol=2e-3, cos_min=0.99999, what=f"layer {L} output")
+    assert torch.equal(res[True][0], res[True][1][-1])
