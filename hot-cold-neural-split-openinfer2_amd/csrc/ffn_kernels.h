@@ -188,12 +188,13 @@ __device__ __forceinline__ void chunk_prefix(const ActiveList& al, int* s_prefix
 }
 // ── persistent token kernel (token.hip) ─────────────────────────────────────
 
-constexpr int kTokGroups = 256;            // workgroups per role (U and D)
-constexpr int kTokGrid = 2 * kTokGroups;
-constexpr int kTokChunks = 256;            // active-list chunks: one per U / D group
+constexpr int kTokGroups = 256;            // workgroups (one per CU), one output tile each
+constexpr int kTokThreads = 512;           // a control wave and 7 worker waves
+constexpr int kTokWorkers = kTokThreads / 64 - 1;
+constexpr int kTokChunks = 256;            // active-list chunks: one per group
 constexpr int kTokMaxChunk = 64;           // ids per chunk (one lane each)
 constexpr int kTokMaxRank = 64;
-constexpr int kTokMaxHot = 4096;           // h staged in LDS
+constexpr int kTokMaxHot = 4096;           // h staged in LDS; also the per-layer h slice
 constexpr int kTokSyncWords = 2048 + 192;
 constexpr int kTokSyncErr = 2048 + 128;       // nonzero: a wait ran past its bound
 
@@ -238,10 +239,9 @@ struct TokArgs {
   uint16_t* xbuf;           // (n_layers, H) layer outputs
   uint16_t* xw;             // (n_layers, H) x_L * norm weight of layer L
   float* ssq;               // (n_layers, 256) sum-of-squares partials of x_L
-  float* h;                 // (n_layers, hstride) hot activations
+  float* h;                 // (n_layers, kTokMaxHot) hot activations, zero past n_hot
   float* hc;                // (n_layers, kTokChunks * kTokMaxChunk) cold activations, list order
   float* z;                 // (n_layers, kTokMaxRank) predictor down projection of layer L
-  int hstride;
   uint32_t* sync;           // kTokSyncWords, zero at launch
   float eps, thr;
   int relu, both;

@@ -75,7 +75,6 @@ struct oi2_stack {
   float* tok_h = nullptr;
   float* tok_hc = nullptr;
   float* tok_z = nullptr;
-  int tok_hstride = 0;
   int32_t* tok_sel_counts = nullptr;
   int32_t* tok_sel_slots = nullptr;
   int32_t* tok_sel_ids = nullptr;
@@ -305,7 +304,6 @@ static TokArgs tok_args(const oi2_stack* s, const uint16_t* x_in, uint16_t* x_ou
   a.h = s->tok_h;
   a.hc = s->tok_hc;
   a.z = s->tok_z;
-  a.hstride = s->tok_hstride;
   a.sync = s->tok_sync;
   a.eps = s->eps;
   a.thr = s->thr;
@@ -442,15 +440,13 @@ static int tok_setup(oi2_stack* s) {
       }
     }
   }
-  const int npw = max_hot <= 2 * 4 * kTokGroups ? 2 : 4;
+  const int npw = max_hot <= 2 * kTokWorkers * kTokGroups ? 2 : 3;   // hot neurons per worker wave
   if (!why[0] && chunk > kTokMaxChunk)
     snprintf(why, sizeof why, "inter %d > %d", s->inter, kTokChunks * kTokMaxChunk);
-  if (!why[0] && (max_hot + npw - 1) / npw + max_rank > 4 * kTokGroups)
-    snprintf(why, sizeof why, "n_hot %d with predictor rank %d exceeds the U waves", max_hot, max_rank);
   int resident = 0;
   if (!why[0] && tok_resident(npw, &resident) != OI2_OK) return OI2_EHIP;
-  if (!why[0] && resident < kTokGrid)
-    snprintf(why, sizeof why, "the device holds %d of the %d workgroups at once", resident, kTokGrid);
+  if (!why[0] && resident < kTokGroups)
+    snprintf(why, sizeof why, "the device holds %d of the %d workgroups at once", resident, kTokGroups);
   if (why[0]) {
     s->tok_why = why;
     return OI2_OK;
@@ -462,10 +458,9 @@ static int tok_setup(oi2_stack* s) {
   const size_t sel = (size_t)n * kTokChunks * chunk;
   alloc((void**)&s->tok_layers, (size_t)n * sizeof(TokLayer));
   alloc((void**)&s->tok_sync, (size_t)kTokSyncWords * 4);
-  s->tok_hstride = (max_hot + 63) / 64 * 64;
   alloc((void**)&s->tok_xw, (size_t)n * kH * 2);
   alloc((void**)&s->tok_ssq, (size_t)n * kTokGroups * 4);
-  alloc((void**)&s->tok_h, (size_t)n * std::max(s->tok_hstride, 64) * 4);
+  alloc((void**)&s->tok_h, (size_t)n * kTokMaxHot * 4);
   alloc((void**)&s->tok_hc, (size_t)n * kTokChunks * kTokMaxChunk * 4);
   alloc((void**)&s->tok_z, (size_t)n * kTokMaxRank * 4);
   alloc((void**)&s->tok_sel_counts, (size_t)n * kTokChunks * 4);
@@ -473,7 +468,7 @@ static int tok_setup(oi2_stack* s) {
   alloc((void**)&s->tok_sel_ids, sel * 4);
   if (e == hipSuccess) e = hipMemset(s->tok_sel_counts, 0, (size_t)n * kTokChunks * 4);
   // h slices past n_hot are never written and must read as zero
-  if (e == hipSuccess) e = hipMemset(s->tok_h, 0, (size_t)n * std::max(s->tok_hstride, 64) * 4);
+  if (e == hipSuccess) e = hipMemset(s->tok_h, 0, (size_t)n * kTokMaxHot * 4);
   std::vector<TokLayer> tab(n);
   for (int L = 0; L < n && e == hipSuccess; ++L) {
     const StackLayer& SL = s->layers[L];

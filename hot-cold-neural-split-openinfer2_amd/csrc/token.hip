@@ -2,32 +2,45 @@
 // launch -- DesdemonaEngine.forward's FFN loop (engine.py:421-438), each
 // layer's active set predicted one layer ahead (engine.py:432-436).
 //
-// 512 workgroups of 256 threads, all resident together (two per CU):
-//   256 U groups  gate/up of 4 hot neurons per wave (fp8 rows), the cold
-//                 records of one active-list chunk (INT4 gate/up -> h_cold),
-//                 and one row of the next layer's predictor z = D q
-//   256 D groups  one 16-row output tile: fp8 down rows x h_hot plus the 16
-//                 down nibbles of every active cold record x h_cold, the
-//                 residual, the next layer's x * w and sum-of-squares
-//                 partial; and one chunk of the next layer's logits,
-//                 threshold and ascending compaction
-// Per layer the U groups run, then the D groups.  A group signals the end of
-// its phase on a device-wide counter and only then issues the loads of its
-// weights for the next layer, before it waits for the other role: the weight
-// stream stays in flight across every phase boundary.
+// 256 workgroups of 512 threads, one per CU, all resident together.  Group g
+// owns, in every layer:
+//   hot      neurons [14 g, 14 g + 14) of the gate/up half (fp8 rows)
+//   cold     chunk g of the layer's active list (INT4 gate/up -> h_cold)
+//   down     output tile g: 16 rows (fp8 down rows x h_hot, plus the 16 down
+//            nibbles of every active cold record x h_cold), the residual and
+//            the next layer's x * w and sum-of-squares partial
+//   predictor row g of the next layer's z = D q (g < rank), and chunk g of the
+//            next layer's logits, threshold and ascending compaction
+// Each layer is a U phase (gate/up) and a D phase (down), and each phase ends
+// with a device-wide signal.
+//
+// Wave 0 is the control wave: it polls the signals, loads the phase's
+// cross-group inputs (mostly straight into LDS), runs the predictor, stores
+// every cross-group output and signals.  Waves 1..7 are workers: they hold
+// the phase's weights in registers, loaded one phase ahead, and compute from
+// LDS.  The split matters because a wave's loads complete in order: the
+// control wave never has weight loads in flight ahead of the loads the
+// phase waits on, and the workers never wait on a cross-group input.
+// Worker loads, in issue order per layer: gather nibbles and half the next
+// gate/up rows (end of U), the next chunk's records and the other half (D1),
+// the next layer's first down row (end of D), its other down rows (B1).  Each
+// phase's compute needs only loads older than the ones still streaming, and
+// the halves issued at B1 / D1 go out after the phase's cross-group inputs:
+// a CU's memory pipeline is in order, and a backlog of weight loads ahead of
+// those inputs would delay the whole phase.
 //
 // Signals: per-XCD arrival counters (32 groups each), then one counter per
-// role, whose last arrival writes a per-XCD release flag that the groups of
-// that XCD poll; the signal words are accessed agent-coherently (sc1).
-// Data that crosses workgroups inside the launch (h, h_cold, z, x, x * w, the
-// partials, the active lists) is stored write-through (sc1), and a group
-// signals only after s_waitcnt vmcnt(0) on its stores.  Every such buffer has
-// one slice per layer, so each address is written at most once per launch
-// and read only after the signal that completes its writes: no L2 or L1 can
-// hold a stale copy of it (the launch starts with the caches invalidated),
-// and readers use ordinary cached loads -- the 32 groups of an XCD share the
-// lines in L2.  No L2 writeback or invalidate is issued inside the launch: on
-// this part those stall every in-flight weight load of the XCD.
+// phase, whose last arrival writes a per-XCD release flag that the groups of
+// that XCD poll; the signal words are accessed agent-coherently (sc1).  Data
+// that crosses groups inside the launch (h, h_cold, z, x, x * w, the
+// partials, the active lists) is stored write-through (sc1), and a control
+// wave signals only after s_waitcnt vmcnt(0) on its stores.  Every such
+// buffer has one slice per layer, so each address is written at most once per
+// launch and read only after the signal that completes its writes: no L2 or
+// L1 can hold a stale copy (the launch starts with the caches invalidated)
+// and readers use ordinary cached loads.  No L2 writeback or invalidate is
+// issued inside the launch: on this part those stall every in-flight weight
+// load of the XCD.
 //
 // Every wait is bounded: past kSpinLimit polls a group sets the error word and
 // goes on (the token is then garbage and the host reports it), so every wave
@@ -42,11 +55,29 @@ namespace {
 constexpr int kPerXcd = kTokGroups / 8;
 constexpr uint32_t kSpinLimit = 1u << 20;
 constexpr int kSyncGo = 0, kSyncXcd = 1024, kSyncAll = 2048, kSyncErr = kTokSyncErr;
-constexpr int kSc1 = 16;             // cache-policy operand: agent-coherent access
-constexpr int kColdPerRound = 2;     // cold records in flight per U wave
-constexpr int kGather = 4;           // cold items per D thread per batch (the first before the U signal)
+constexpr int kSc1 = 16;                       // cache-policy operand: agent-coherent access
+constexpr int kWorkers = kTokThreads / kWave - 1;
+constexpr int kColdR = 1;                      // cold records per worker (items wi + 7 i)
+constexpr int kCtlCold = 2;                    // the control wave's items, right after the workers'
+constexpr int kGat = 2;                        // gather items per worker lane per batch
+constexpr int kBatch = kWorkers * kWave * kGat;
+constexpr int kCtlItems = kBatch / kWave;      // gather items per control lane per batch
+constexpr int kRows = kH / kTokGroups;         // 16 output rows per group
+static_assert(kWorkers == 7, "the row split and the epilogue's sum assume 7 workers");
+static_assert(kTokWorkers == kWorkers, "host and kernel agree on the worker count");
 
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
+typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+typedef __attribute__((address_space(3))) void lds_void;
+constexpr uint32_t kNoOff = 0x80000000u;       // an offset past every range: reads zero
+
+// The layer table through the constant address space: its fields load with
+// scalar loads, which wait on their own counter, so reading them never makes
+// a wave wait for its vector loads (the weights in flight).
+typedef const __attribute__((address_space(4))) TokLayer CLayer;
+__device__ __forceinline__ CLayer* layer_table(const TokArgs& a) {
+  return reinterpret_cast<CLayer*>(reinterpret_cast<uintptr_t>(a.layers));
+}
 
 // A buffer descriptor over [p, p + bytes).  Every call site passes
 // wave-uniform values; readfirstlane lets the compiler see that (otherwise it
@@ -60,12 +91,9 @@ __device__ __forceinline__ rsrc_t rsrc(const void* p, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(u), (short)0,
                                            __builtin_amdgcn_readfirstlane(bytes), 0x00020000);
 }
-// Plain buffer loads.  A lane whose offset is past the descriptor's range
-// (kNoOff, or any offset of a zero-size descriptor) reads zero: masked loads
-// stay unconditional, so the compiler never has to wait for one before
-// issuing the next.
-typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
-constexpr uint32_t kNoOff = 0x80000000u;
+// Plain buffer loads: a lane whose offset is past the range reads zero, so
+// masked loads stay unconditional and the compiler never has to wait for one
+// before issuing the next.
 __device__ __forceinline__ u32x4 bld16(rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
 }
@@ -77,6 +105,11 @@ __device__ __forceinline__ uint32_t bld4(rsrc_t r, uint32_t off) {
 }
 __device__ __forceinline__ uint16_t bld2(rsrc_t r, uint32_t off) {
   return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+}
+// 16 bytes per lane straight into LDS: lane l lands at dst + 16 l (a lane past
+// the range writes zero).  dst is the wave's 1 KB destination.
+__device__ __forceinline__ void bld16_lds(rsrc_t r, void* dst, uint32_t off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)dst, 16, off, 0, 0, 0);
 }
 __device__ __forceinline__ void cst2(rsrc_t r, uint32_t off, uint16_t v) {
   __builtin_amdgcn_raw_buffer_store_b16(v, r, off, 0, kSc1);
@@ -90,12 +123,25 @@ __device__ __forceinline__ void cst(T* p, T v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ void lds_sync() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// 8 halves e0..e7 (natural order) as the pairs (e0,e4) (e1,e5) (e2,e6)
+// (e3,e7) the INT4 decode produces.
+__device__ __forceinline__ u32x4 pair_layout(u32x4 x) {
+  u32x4 p;
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    p[k] = __builtin_amdgcn_perm(x[2 + (k >> 1)], x[k >> 1], (k & 1) ? 0x07060302u : 0x05040100u);
+  return p;
+}
 
-// End of a phase for group g of role r (0 U, 1 D): epoch e.
+// Workgroup barrier that waits for LDS traffic only (never for vector memory
+// loads: the workers' weight loads stay in flight across it).
+__device__ __forceinline__ void bar() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+__device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Control wave: end of phase r (0 U, 1 D) for group g, epoch e.
 __device__ __forceinline__ void tok_arrive(uint32_t* sync, int r, int g, uint32_t e) {
-  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)\n\ts_barrier" ::: "memory");
-  if (threadIdx.x == 0) {
+  asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+  if (lane_id() == 0) {
     const uint32_t o1 = __hip_atomic_fetch_add(sync + kSyncXcd + 64 * (8 * r + (g & 7)), 1u,
                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (o1 + 1 == (uint32_t)kPerXcd * e) {
@@ -107,585 +153,691 @@ __device__ __forceinline__ void tok_arrive(uint32_t* sync, int r, int g, uint32_
   }
 }
 
-// Wait until every group of role r has ended epoch e.
+// Control wave: wait until every group has ended epoch e of phase r.
 __device__ __forceinline__ void tok_wait(uint32_t* sync, int r, int g, uint32_t e) {
-  if (threadIdx.x < kWave) {
-    const uint32_t* go = sync + kSyncGo + 64 * (8 * r + (g & 7));
-    uint32_t n = 0;
-    while (cld(go) < e) {
-      __builtin_amdgcn_s_sleep(1);
-      if (++n >= kSpinLimit) {
-        cst(sync + kSyncErr, 1u);
-        break;
-      }
-      if ((n & 63) == 0 && cld(sync + kSyncErr)) break;
+  const uint32_t* go = sync + kSyncGo + 64 * (8 * r + (g & 7));
+  uint32_t n = 0;
+  while (cld(go) < e) {
+    __builtin_amdgcn_s_sleep(1);
+    if (++n >= kSpinLimit) {
+      cst(sync + kSyncErr, 1u);
+      break;
     }
+    if ((n & 63) == 0 && cld(sync + kSyncErr)) break;
   }
-  lds_sync();
 }
 
-struct TokShared {
-  union {
-    struct {
-      uint32_t nat[kH / 2];     // x * w, natural order
-      uint32_t pair[kH / 2];    // x * w, the (e0,e4) (e1,e5).. pairs of the INT4 decode
-      uint32_t q[kH / 2];       // the next layer's predictor query, bf16 pairs
-    } u;
-    struct {
-      float h[kTokMaxHot];
-      float z[kTokMaxRank];
-      float cold[4][16];
-      float yhot[16];
-      float out[16];
-      int wcnt[4];
-      int wsum[4];
-      int pfx[kTokChunks + 1];  // exclusive prefix of the list's chunk counts
-    } d;
-    uint8_t pad[64 * 1024];     // two groups per CU: one U, one D on most CUs
-  };
+struct alignas(16) TokShared {
+  uint32_t nat[kH / 2];       // x * w of the layer
+  uint32_t xq[kH / 2];        // predictor group: x_L,
+  uint32_t wq[kH / 2];        //   the next layer's norm weight,
+  uint32_t pd[kH / 2];        //   its predictor down row (bf16)
+  float h[kTokMaxHot];        // the layer's hot activations
+  uint32_t pu[8 * kWave * 4]; // predictor up rows of chunk g: 16-byte piece m of neuron l at 64 m + l
+  int pfx[kTokChunks + 1];    // exclusive prefix of the list's chunk counts
+  int it_slot[kBatch];        // gather items of the current batch: record slot,
+  int it_pos[kBatch];         //   list position,
+  float it_hc[kBatch];        //   cold activation
+  int lst_slot[kTokMaxChunk]; // chunk g of the next layer's list
+  int lst_id[kTokMaxChunk];
+  float h_out[kWorkers * 3];  // this group's hot activations
+  float hc_out[kTokMaxChunk]; // this group's cold activations (chunk order)
+  float yhot[kRows];
+  float cpart[kWorkers][kRows];
+  float cpart_ctl[kRows];     // the control wave's share of long gather lists
+  float out[kRows];
+  float z[kTokMaxRank];
+  float r;
+  int total, lst_cnt;
 };
 
-// ── U groups ────────────────────────────────────────────────────────────────
+// Items of the list: item i (0 <= i < total) is item i - pfx[c] of chunk c.
+// The control lane that owns chunks 4 l .. 4 l + 3 writes list positions of
+// the items of batch b into it_pos.
+__device__ __forceinline__ void ctl_positions(TokShared& sh, const int cnt4[4], int chunk, int b) {
+  const int l = lane_id();
+  const int lo = b * kBatch, hi = lo + kBatch;
+  for (int q = 0; q < 4; ++q) {
+    const int c = 4 * l + q;
+    const int first = sh.pfx[c];
+    for (int k = max(0, lo - first); k < cnt4[q] && first + k < hi; ++k) sh.it_pos[first + k - lo] = c * chunk + k;
+  }
+}
+
+// Control: slots of the items of batch b.
+__device__ __forceinline__ void ctl_gather_table(TokShared& sh, rsrc_t rslots, int n_records, int b, int total) {
+  const int l = lane_id();
+  int sl[kCtlItems];
+#pragma unroll
+  for (int m = 0; m < kCtlItems; ++m) {
+    const int i = l + kWave * m;
+    sl[m] = (int)bld4(rslots, b * kBatch + i < total ? 4 * (uint32_t)sh.it_pos[i] : kNoOff);
+  }
+#pragma unroll
+  for (int m = 0; m < kCtlItems; ++m) {
+    const int i = l + kWave * m;
+    const bool v = b * kBatch + i < total && sl[m] >= 0 && sl[m] < n_records;
+    sh.it_slot[i] = v ? sl[m] : -1;
+  }
+}
+
+// Control: cold activations of the items of batch b.
+__device__ __forceinline__ void ctl_gather_hc(TokShared& sh, rsrc_t rhc, int b, int total) {
+  const int l = lane_id();
+  float hv[kCtlItems];
+#pragma unroll
+  for (int m = 0; m < kCtlItems; ++m) {
+    const int i = l + kWave * m;
+    hv[m] = as_f32(bld4(rhc, (b * kBatch + i < total && sh.it_slot[i] >= 0) ? 4 * (uint32_t)sh.it_pos[i] : kNoOff));
+  }
+#pragma unroll
+  for (int m = 0; m < kCtlItems; ++m) sh.it_hc[l + kWave * m] = hv[m];
+}
+
+// ── the control wave ────────────────────────────────────────────────────────
 
 template <int NPW>
-__device__ void u_group(const TokArgs& a, int g, TokShared& sh) {
-  const int t = threadIdx.x, lane = lane_id();
-  const int w = __builtin_amdgcn_readfirstlane(t >> 6);   // wave-uniform, and known to be
-  const int gw = 4 * g + w;                       // U wave 0..1023
-  const int prow = 4 * kTokGroups - 1 - gw;       // predictor row of this wave
+__device__ void control(const TokArgs& a, int g, TokShared& sh) {
+  const int l = lane_id();
   const int n = a.n_layers;
-  // this iteration's weights: hot gate (0..3) and up (4..7) chunks of
-  // neurons gw * NPW + j, or in W[0] the next layer's predictor row
-  u32x4 W[NPW][8];
-  float gsc = 0.0f, usc = 0.0f, gbi = 0.0f;       // lane j < NPW: neuron gw * NPW + j
-  auto hot_of = [&](int L) { return L >= 0 ? a.layers[L].n_hot : 0; };
-  // wave v runs row 1023 - v of layer L+1's predictor (waves without hot rows)
-  auto pred_row_of = [&](int L, int v) {
-    if (L + 1 >= n) return false;
-    const TokLayer& P = a.layers[L + 1];
-    return P.pd_w != nullptr && 4 * kTokGroups - 1 - v < P.rank && v * NPW >= hot_of(L);
-  };
-  auto pred_row = [&](int L) { return pred_row_of(L, gw); };
-  auto prefetch = [&](int L) {
-    const bool pr = pred_row(L);
-    rsrc_t ra = rsrc(nullptr, 0), rb = ra, rgs = ra, rus = ra, rgb = ra;
-    if (pr) {
-      const TokLayer& P = a.layers[L + 1];
-      ra = rb = rsrc(P.pd_w, (uint32_t)P.rank * kH * 2);
-    } else if (L >= 0) {
-      const TokLayer& T = a.layers[L];
-      const uint32_t nh = (uint32_t)T.n_hot;
-      ra = rsrc(T.gate_q, nh * kH);
-      rb = rsrc(T.up_q, nh * kH);
-      rgs = rsrc(T.gate_s, nh * 4);
-      rus = rsrc(T.up_s, nh * 4);
-      rgb = rsrc(T.hot_gbias, T.hot_gbias ? nh * 4 : 0u);
-    }
-#pragma unroll
-    for (int j = 0; j < NPW; ++j)
-#pragma unroll
-      for (int it = 0; it < 4; ++it) {
-        uint32_t oa, ob;
-        if (pr) {     // slot 0 holds the row; the other slots read zero
-          oa = j == 0 ? (uint32_t)prow * kH * 2 + 16 * (lane + 64 * it) : kNoOff;
-          ob = j == 0 ? (uint32_t)prow * kH * 2 + 16 * (lane + 64 * (4 + it)) : kNoOff;
-        } else {      // neurons past n_hot are past the range: zero
-          oa = ob = (uint32_t)(gw * NPW + j) * kH + 1024 * it + 16 * lane;
-        }
-        W[j][it] = bld16(ra, oa);
-        W[j][4 + it] = bld16(rb, ob);
-      }
-    const uint32_t so = lane < NPW ? (uint32_t)(gw * NPW + lane) * 4 : kNoOff;
-    gsc = as_f32(bld4(rgs, so));
-    usc = as_f32(bld4(rus, so));
-    gbi = as_f32(bld4(rgb, so));
-  };
-
-  // Each iteration first issues its own weight loads, then waits for the
-  // other role: for L >= 0 that is right after this group's previous signal.
-  // (Loads issued in one iteration and consumed in the next would be copied
-  // between registers at the loop edge, and each copy waits for its load.)
+  const int tile = (g & 7) * (kTokGroups / 8) + (g >> 3);   // XCD-aware: an XCD owns 512 rows
+  const int j0 = tile * kRows;
+  const int g0 = l >> 2;
+  CLayer* LT = layer_table(a);
   for (int L = -1; L < n; ++L) {
-    prefetch(L);
+    CLayer* T = L >= 0 ? LT + L : nullptr;
+    CLayer* N = L + 1 < n ? LT + L + 1 : nullptr;
+    // ================= U phase of layer L (L = -1: only layer 0's predictor)
     if (L >= 0) tok_wait(a.sync, 1, g, (uint32_t)(L + 1));
-    const uint16_t* xl = L <= 0 ? a.x_in : a.xbuf + (size_t)(L - 1) * kH;   // input of layer max(L, 0)
-    const bool prd = pred_row(L);
-    const int nh = hot_of(L);
-    // 1. this group's chunk of layer L's active list: count and first slots together
-    int act_chunk = 0, n_records = 0;
-    const uint8_t* records = nullptr;
-    const float* cgb = nullptr;
-    rsrc_t rcnt = rsrc(nullptr, 0), rslt = rcnt, rrec = rcnt;
-    if (L >= 0 && a.layers[L].n_records > 0 && a.layers[L].act_counts) {
-      const TokLayer& T = a.layers[L];
-      act_chunk = T.act_chunk;
-      n_records = T.n_records;
-      records = T.records;
-      cgb = T.cold_gbias;
-      rcnt = rsrc(T.act_counts, kTokChunks * 4);
-      rslt = rsrc(T.act_slots, (uint32_t)kTokChunks * act_chunk * 4);
-      rrec = rsrc(T.records, (uint32_t)n_records * kRecBytes);
+    const bool has_cold = T && T->n_records > 0 && T->act_counts;
+    const int chunk = has_cold ? T->act_chunk : 0;
+    const bool pred = N && N->pd_w && g < N->rank;
+    // inputs: x * w into LDS, the sum-of-squares partials, the list's counts,
+    // and for a predictor group x_L, the next norm weight and the D row
+    if (T) {
+      const rsrc_t rx = rsrc(a.xw + (size_t)L * kH, kH * 2);
+#pragma unroll
+      for (int it = 0; it < 8; ++it) bld16_lds(rx, sh.nat + 256 * it, 16 * (l + 64 * it));
     }
-    const uint32_t c_raw = bld4(rcnt, 4 * g);
-    int s_raw[kColdPerRound];
+    const u32x4 pp = bld16(rsrc(a.ssq + (size_t)(L < 0 ? 0 : L) * kTokGroups, kTokGroups * 4), 16 * l);
+    const rsrc_t rcnt = rsrc(has_cold ? T->act_counts : nullptr, has_cold ? kTokChunks * 4 : 0u);
+    int cnt4[4];
 #pragma unroll
-    for (int i = 0; i < kColdPerRound; ++i) {
-      const int k = w + 4 * i;
-      s_raw[i] = (int)bld4(rslt, k < act_chunk ? 4 * (uint32_t)(g * act_chunk + k) : kNoOff);
+    for (int q = 0; q < 4; ++q) cnt4[q] = (int)bld4(rcnt, 4 * (4 * l + q));
+    if (pred) {
+      const uint16_t* xl = L <= 0 ? a.x_in : a.xbuf + (size_t)(L - 1) * kH;
+      const rsrc_t rx = rsrc(xl, kH * 2), rw = rsrc(N->norm_w, kH * 2);
+      const rsrc_t rd = rsrc(N->pd_w + (size_t)g * kH, kH * 2);
+#pragma unroll
+      for (int it = 0; it < 8; ++it) {
+        bld16_lds(rx, sh.xq + 256 * it, 16 * (l + 64 * it));
+        bld16_lds(rw, sh.wq + 256 * it, 16 * (l + 64 * it));
+        bld16_lds(rd, sh.pd + 256 * it, 16 * (l + 64 * it));
+      }
     }
-    // 2. the token: x * w (hot, cold) and the sum-of-squares partials
-    const u32x4* pxw = reinterpret_cast<const u32x4*>(a.xw + (size_t)(L < 0 ? 0 : L) * kH) + 2 * t;
-    const u32x4 xa = pxw[0], xb = pxw[1];
-    const u32x4 pr = reinterpret_cast<const u32x4*>(a.ssq + (size_t)(L < 0 ? 0 : L) * kTokGroups)[lane];
-    // 3. cold records of the chunk: gate and up halves, their scales
-    const int cnt = act_chunk ? (int)min(c_raw, (uint32_t)act_chunk) : 0;
-    u32x4 q[kColdPerRound][4];
-    float s[kColdPerRound][4];
-    int slot[kColdPerRound];
-    const int g0 = lane >> 2;
-    auto load_records = [&](int base, bool first) {
+    // the chunk's items past the workers' share: records with the inputs
+    const int ccnt = has_cold ? sh.lst_cnt : 0;
+    const rsrc_t rrec = rsrc(has_cold ? T->records : nullptr, has_cold ? (uint32_t)T->n_records * kRecBytes : 0u);
+    const rsrc_t rcgb = rsrc(has_cold ? T->cold_gbias : nullptr,
+                             (has_cold && T->cold_gbias) ? (uint32_t)T->n_records * 4 : 0u);
+    u32x4 CQ[kCtlCold][4];
+    float CS[kCtlCold][4], CG[kCtlCold];
+    int CSL[kCtlCold];
 #pragma unroll
-      for (int i = 0; i < kColdPerRound; ++i) {
-        const int k = base + w + 4 * i;
-        const int sl = first ? s_raw[i] : (int)bld4(rslt, k < act_chunk ? 4 * (uint32_t)(g * act_chunk + k) : kNoOff);
-        const bool v = k < cnt && sl >= 0 && sl < n_records;
-        slot[i] = v ? sl : -1;
-        const uint32_t ro = v ? (uint32_t)sl * kRecBytes : kNoOff;
+    for (int i = 0; i < kCtlCold; ++i) {
+      const int k = kWorkers * kColdR + i;
+      const int sl = k < ccnt ? sh.lst_slot[k] : -1;
+      const bool vv = has_cold && sl >= 0 && sl < T->n_records;
+      CSL[i] = vv ? sl : -1;
+      const uint32_t ro = vv ? (uint32_t)sl * kRecBytes : kNoOff;
 #pragma unroll
-        for (int it = 0; it < 2; ++it) {
-          q[i][it] = bld16(rrec, ro + kOffGate + 16 * (lane + 64 * it));
-          q[i][2 + it] = bld16(rrec, ro + kOffUp + 16 * (lane + 64 * it));
-        }
-#pragma unroll
-        for (int vv = 0; vv < 2; ++vv) {
-          s[i][2 * vv] = half_bits_to_float(bld2(rrec, ro + kOffScales + 2 * (32 * vv + g0)));
-          s[i][2 * vv + 1] = half_bits_to_float(bld2(rrec, ro + kOffScales + 2 * (32 * vv + 16 + g0)));
-        }
+      for (int it = 0; it < 2; ++it) {
+        CQ[i][it] = bld16(rrec, ro + kOffGate + 16 * (l + 64 * it));
+        CQ[i][2 + it] = bld16(rrec, ro + kOffUp + 16 * (l + 64 * it));
       }
-    };
-    // 4. x * w into LDS; in workgroups with predictor rows, the query
-    //    q = bf16(fp16(x r w')) with the next layer's norm weight w'
-    //    (pred_d_role's arithmetic)
-    const float r = r_from_part(f32x4{as_f32(pr.x), as_f32(pr.y), as_f32(pr.z), as_f32(pr.w)}, a.eps);
-    const bool pred_wg = pred_row_of(L, 4 * g + 3);
-    if (pred_wg) {
-      const u32x4* px = reinterpret_cast<const u32x4*>(xl) + 2 * t;
-      const uint8_t* nw = reinterpret_cast<const uint8_t*>(a.layers[L + 1].norm_w);
-      const u32x4 x0 = px[0], x1 = px[1];
-      const u32x4 w0 = load16(nw + 32 * t), w1 = load16(nw + 32 * t + 16);
-      u32x4 q0, q1;
 #pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        q0[d] = (__builtin_bit_cast(uint32_t, round_bf16(xn_exact(half_lo(x0[d]), r, half_lo(w0[d])))) >> 16) |
-                (__builtin_bit_cast(uint32_t, round_bf16(xn_exact(half_hi(x0[d]), r, half_hi(w0[d])))) & 0xFFFF0000u);
-        q1[d] = (__builtin_bit_cast(uint32_t, round_bf16(xn_exact(half_lo(x1[d]), r, half_lo(w1[d])))) >> 16) |
-                (__builtin_bit_cast(uint32_t, round_bf16(xn_exact(half_hi(x1[d]), r, half_hi(w1[d])))) & 0xFFFF0000u);
+      for (int q = 0; q < 2; ++q) {
+        CS[i][2 * q] = half_bits_to_float(bld2(rrec, ro + kOffScales + 2 * (32 * q + g0)));
+        CS[i][2 * q + 1] = half_bits_to_float(bld2(rrec, ro + kOffScales + 2 * (32 * q + 16 + g0)));
       }
-      reinterpret_cast<u32x4*>(sh.u.q)[2 * t] = q0;
-      reinterpret_cast<u32x4*>(sh.u.q)[2 * t + 1] = q1;
+      CG[i] = as_f32(bld4(rcgb, vv ? 4 * (uint32_t)sl : kNoOff));
     }
-    if (L >= 0) {
-      reinterpret_cast<u32x4*>(sh.u.nat)[2 * t] = xa;
-      reinterpret_cast<u32x4*>(sh.u.nat)[2 * t + 1] = xb;
-      u32x4 pa, pb;
+    const float r = r_from_part(f32x4{as_f32(pp.x), as_f32(pp.y), as_f32(pp.z), as_f32(pp.w)}, a.eps);
+    // exclusive prefix of the chunk counts (lane l: chunks 4 l .. 4 l + 3)
+    int tot4 = 0;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const uint32_t sel = (k & 1) ? 0x07060302u : 0x05040100u;
-        pa[k] = __builtin_amdgcn_perm(xa[2 + (k >> 1)], xa[k >> 1], sel);
-        pb[k] = __builtin_amdgcn_perm(xb[2 + (k >> 1)], xb[k >> 1], sel);
-      }
-      reinterpret_cast<u32x4*>(sh.u.pair)[2 * t] = pa;
-      reinterpret_cast<u32x4*>(sh.u.pair)[2 * t + 1] = pb;
+    for (int q = 0; q < 4; ++q) {
+      cnt4[q] = min(max(cnt4[q], 0), chunk);
+      tot4 += cnt4[q];
     }
-    lds_sync();
-    // 5. hot neurons (same accumulation order as the two-launch path)
-    if (gw * NPW < nh) {
-      float gg[NPW], uu[NPW];
+    int v = tot4;
 #pragma unroll
-      for (int j = 0; j < NPW; ++j) gg[j] = uu[j] = 0.0f;
-#pragma unroll
-      for (int it = 0; it < 4; ++it) {
-        const u32x4* p = reinterpret_cast<const u32x4*>(sh.u.nat) + (1024 * it + 16 * lane) / 8;
-        const u32x4 x0 = p[0], x1 = p[1];
-        const f16x2 xp[8] = {as_f16x2(x0.x), as_f16x2(x0.y), as_f16x2(x0.z), as_f16x2(x0.w),
-                             as_f16x2(x1.x), as_f16x2(x1.y), as_f16x2(x1.z), as_f16x2(x1.w)};
-#pragma unroll
-        for (int j = 0; j < NPW; ++j)
-#pragma unroll
-          for (int d = 0; d < 4; ++d) {
-            gg[j] = dot2(fp8x2_to_f16x2(W[j][it][d], false), xp[2 * d], gg[j]);
-            gg[j] = dot2(fp8x2_to_f16x2(W[j][it][d], true), xp[2 * d + 1], gg[j]);
-            uu[j] = dot2(fp8x2_to_f16x2(W[j][4 + it][d], false), xp[2 * d], uu[j]);
-            uu[j] = dot2(fp8x2_to_f16x2(W[j][4 + it][d], true), xp[2 * d + 1], uu[j]);
-          }
-      }
-      float hg = 0.0f, hu = 0.0f;
-#pragma unroll
-      for (int j = 0; j < NPW; ++j) {
-        const float sg = wave_sum(gg[j]), su = wave_sum(uu[j]);
-        if (lane == j) {
-          hg = sg;
-          hu = su;
-        }
-      }
-      const int k = gw * NPW + lane;
-      if (lane < NPW && k < nh) cst(a.h + (size_t)L * a.hstride + k, gated_act(r * hg * gsc + gbi, r * hu * usc, a.relu, a.both));
+    for (int off = 1; off < kWave; off <<= 1) {
+      const int u = __shfl_up(v, off, kWave);
+      if (l >= off) v += u;
     }
-    // the chunk's first cold records, issued once the hot rows are consumed
-    // (both sets together do not fit the register budget)
-    if (cnt > 0) load_records(0, true);
-    // 6. the next layer's predictor row: z = D q
-    if (prd) {
+    const int total = __shfl(v, kWave - 1, kWave);
+    int run = v - tot4;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      sh.pfx[4 * l + q] = run;
+      run += cnt4[q];
+    }
+    if (l == 0) {
+      sh.pfx[kTokChunks] = total;
+      sh.total = total;
+      sh.r = r;
+    }
+    wait_vm();
+    bar();   // B1: x * w, r and the list prefix are in LDS
+    // the gather table of batch 0 (its slots; the cold activations come in D)
+    if (has_cold) ctl_positions(sh, cnt4, chunk, 0);
+    __builtin_amdgcn_wave_barrier();
+    if (has_cold) ctl_gather_table(sh, rsrc(T->act_slots, (uint32_t)kTokChunks * chunk * 4), T->n_records, 0, total);
+    // the next layer's predictor row: z = D q, q = bf16(fp16(x r w'))
+    // (pred_d_role's arithmetic)
+    if (pred) {
       float acc = 0.0f;
 #pragma unroll
       for (int it = 0; it < 8; ++it) {
-        const u32x4 qv = reinterpret_cast<const u32x4*>(sh.u.q)[lane + 64 * it];
+        const u32x4 xv = reinterpret_cast<const u32x4*>(sh.xq)[l + 64 * it];
+        const u32x4 wv = reinterpret_cast<const u32x4*>(sh.wq)[l + 64 * it];
+        const u32x4 dv = reinterpret_cast<const u32x4*>(sh.pd)[l + 64 * it];
 #pragma unroll
         for (int d = 0; d < 4; ++d) {
-          acc = fmaf(bf16_bits_to_float((uint16_t)(W[0][it][d] & 0xFFFFu)),
-                     bf16_bits_to_float((uint16_t)(qv[d] & 0xFFFFu)), acc);
-          acc = fmaf(bf16_bits_to_float((uint16_t)(W[0][it][d] >> 16)),
-                     bf16_bits_to_float((uint16_t)(qv[d] >> 16)), acc);
+          const float q0 = round_bf16(xn_exact(half_lo(xv[d]), r, half_lo(wv[d])));
+          const float q1 = round_bf16(xn_exact(half_hi(xv[d]), r, half_hi(wv[d])));
+          acc = fmaf(bf16_bits_to_float((uint16_t)(dv[d] & 0xFFFFu)), q0, acc);
+          acc = fmaf(bf16_bits_to_float((uint16_t)(dv[d] >> 16)), q1, acc);
         }
       }
       acc = wave_sum(acc);
-      if (lane == 0) cst(a.z + (size_t)(L + 1) * kTokMaxRank + prow, acc);
+      if (l == 0) cst(a.z + (size_t)(L + 1) * kTokMaxRank + g, acc);
     }
-    // 7. cold records of the chunk: h = act(gate, up) in list order
-    for (int base = 0; base < cnt; base += 4 * kColdPerRound) {
-      if (base > 0) load_records(base, false);
+    // the chunk's items past the workers' share (cold_role's arithmetic);
+    // past kCtlCold more, one at a time
+    for (int k = kWorkers * kColdR; k < ccnt; ++k) {
+      const int i = k - kWorkers * kColdR;
+      if (i >= kCtlCold) {   // rare: load this record now into slot 0
+        const int sl = sh.lst_slot[k];
+        const bool vv = sl >= 0 && sl < T->n_records;
+        CSL[0] = vv ? sl : -1;
+        const uint32_t ro = vv ? (uint32_t)sl * kRecBytes : kNoOff;
 #pragma unroll
-      for (int i = 0; i < kColdPerRound; ++i) {
-        if (slot[i] < 0) continue;
+        for (int it = 0; it < 2; ++it) {
+          CQ[0][it] = bld16(rrec, ro + kOffGate + 16 * (l + 64 * it));
+          CQ[0][2 + it] = bld16(rrec, ro + kOffUp + 16 * (l + 64 * it));
+        }
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          CS[0][2 * q] = half_bits_to_float(bld2(rrec, ro + kOffScales + 2 * (32 * q + g0)));
+          CS[0][2 * q + 1] = half_bits_to_float(bld2(rrec, ro + kOffScales + 2 * (32 * q + 16 + g0)));
+        }
+        CG[0] = as_f32(bld4(rcgb, vv ? 4 * (uint32_t)sl : kNoOff));
+      }
+      const int c = i >= kCtlCold ? 0 : i;
+      float hv = 0.0f;
+#pragma unroll
+      for (int cc = 0; cc < kCtlCold; ++cc) {
+        if (cc != c) continue;
+        if (CSL[cc] < 0) break;
         float pg[2] = {0.0f, 0.0f}, pu[2] = {0.0f, 0.0f};
 #pragma unroll
         for (int it = 0; it < 2; ++it) {
-          const u32x4* p = reinterpret_cast<const u32x4*>(sh.u.pair) + (32 * lane + 2048 * it) / 8;
+          const u32x4* p = reinterpret_cast<const u32x4*>(sh.nat) + (32 * l + 2048 * it) / 8;
 #pragma unroll
           for (int d = 0; d < 4; ++d) {
-            const u32x4 xq = p[d];
+            const u32x4 xq = pair_layout(p[d]);
             f16x2 tq[4];
-            int4x8_to_f16x2x4(q[i][it][d], tq);
+            int4x8_to_f16x2x4(CQ[cc][it][d], tq);
 #pragma unroll
-            for (int k = 0; k < 4; ++k) pg[it] = dot2(tq[k], as_f16x2(xq[k]), pg[it]);
-            int4x8_to_f16x2x4(q[i][2 + it][d], tq);
+            for (int e = 0; e < 4; ++e) pg[it] = dot2(tq[e], as_f16x2(xq[e]), pg[it]);
+            int4x8_to_f16x2x4(CQ[cc][2 + it][d], tq);
 #pragma unroll
-            for (int k = 0; k < 4; ++k) pu[it] = dot2(tq[k], as_f16x2(xq[k]), pu[it]);
+            for (int e = 0; e < 4; ++e) pu[it] = dot2(tq[e], as_f16x2(xq[e]), pu[it]);
           }
         }
-        float gv = r * wave_sum(pg[0] * s[i][0] + pg[1] * s[i][1]);
-        const float uv = r * wave_sum(pu[0] * s[i][2] + pu[1] * s[i][3]);
-        gv += cgb ? cgb[slot[i]] : 0.0f;
-        const float h = gated_act(gv, uv, a.relu, a.both);
-        if (lane == 0) cst(a.hc + (size_t)L * kTokChunks * kTokMaxChunk + (size_t)g * act_chunk + base + w + 4 * i, h);
+        const float gv = r * wave_sum(pg[0] * CS[cc][0] + pg[1] * CS[cc][1]) + CG[cc];
+        const float uv = r * wave_sum(pu[0] * CS[cc][2] + pu[1] * CS[cc][3]);
+        hv = gated_act(gv, uv, a.relu, a.both);
       }
+      if (l == 0) sh.hc_out[k] = hv;
+    }
+    bar();   // B2: the workers' activations are in LDS
+    if (T) {
+      const int k = g * kWorkers * NPW + l;
+      if (l < kWorkers * NPW && k < T->n_hot) cst(a.h + (size_t)L * kTokMaxHot + k, sh.h_out[l]);
+      if (has_cold && l < sh.lst_cnt)
+        cst(a.hc + (size_t)L * kTokChunks * kTokMaxChunk + (size_t)g * chunk + l, sh.hc_out[l]);
     }
     tok_arrive(a.sync, 0, g, (uint32_t)(L + 2));
-  }
-}
 
-// ── D groups ────────────────────────────────────────────────────────────────
-
-__device__ void d_group(const TokArgs& a, int g, TokShared& sh) {
-  const int t = threadIdx.x, lane = lane_id();
-  const int w = __builtin_amdgcn_readfirstlane(t >> 6);   // wave-uniform, and known to be
-  const int n = a.n_layers;
-  // XCD-aware tiling: the 32 groups of an XCD (g & 7) own one contiguous
-  // 512-row band, so they share the L2 lines of every cold record's down nibbles
-  const int tile = (g & 7) * (kTokGroups / 8) + (g >> 3);
-  const int j0 = tile * 16;
-  const int je = j0 + (t & 15);
-  // this iteration's weights: the wave's 4 down rows (chunks lane + 64 it),
-  // and for lanes < 16 one predictor-up row of the next layer (chunk g)
-  u32x4 Q[4][4];
-  float dsc[4];
-  uint16_t nwv_bits = 0, pbias_bits = 0;
-  u32x4 P[8];
-  int plut_raw = 0;
-  auto pred_n = [&](int L) {            // predictor-up neuron of this lane, or -1
-    if (L + 1 >= n || lane >= 16) return -1;
-    const TokLayer& P1 = a.layers[L + 1];
-    const int kk = 16 * w + lane;
-    const int nn = g * P1.sel_chunk + kk;
-    return (P1.pd_w && kk < P1.sel_chunk && nn < P1.inter) ? nn : -1;
-  };
-  auto prefetch = [&](int L) {
-    rsrc_t rq = rsrc(nullptr, 0), rds = rq, rnw = rq, rpu = rq, rpb = rq, rlut = rq;
-    int stride = 0, nch = 0;
-    if (L >= 0) {
-      const TokLayer& T = a.layers[L];
-      stride = T.down_stride;
-      nch = T.n_hot > 0 ? stride >> 4 : 0;
-      rq = rsrc(T.down_q, T.n_hot > 0 ? (uint32_t)kH * stride : 0u);
-      rds = rsrc(T.down_s, T.n_hot > 0 ? kH * 4 : 0u);
-      rnw = rsrc(a.layers[L + 1 < n ? L + 1 : L].norm_w, kH * 2);
-    }
+    // ================= D phase of layer L (L = -1: only layer 0's selection)
+    tok_wait(a.sync, 0, g, (uint32_t)(L + 2));
+    const bool psel = N && N->pd_w;                      // the next layer's list is predicted
+    const bool pstat = N && !N->pd_w && N->n_records > 0 && N->act_counts;   // or fixed
+    float res_v = 0.0f, nwv = 1.0f;
+    if (T) {
+      const rsrc_t rh = rsrc(a.h + (size_t)L * kTokMaxHot, kTokMaxHot * 4);
 #pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int row = j0 + 4 * w + rr;
-#pragma unroll
-      for (int it = 0; it < 4; ++it) {
-        const int c = lane + 64 * it;
-        Q[rr][it] = bld16(rq, c < nch ? (uint32_t)(row * stride + 16 * c) : kNoOff);
-      }
-      dsc[rr] = as_f32(bld4(rds, 4 * row));
-    }
-    nwv_bits = bld2(rnw, 2 * je);
-    const int nn = pred_n(L);
-    int rank = 0;
-    if (L + 1 < n && a.layers[L + 1].pd_w) {
-      const TokLayer& P1 = a.layers[L + 1];
-      rank = P1.rank;
-      rpu = rsrc(P1.pu_w, (uint32_t)P1.inter * P1.rank * 2);
-      rpb = rsrc(P1.pu_b, (uint32_t)P1.inter * 2);
-      if (P1.lut) rlut = rsrc(P1.lut, (uint32_t)P1.inter * 4);
-    }
-#pragma unroll
-    for (int k = 0; k < 8; ++k)
-      P[k] = bld16(rpu, (nn >= 0 && 8 * k < rank) ? (uint32_t)(nn * rank + 8 * k) * 2 : kNoOff);
-    pbias_bits = bld2(rpb, nn >= 0 ? 2 * (uint32_t)nn : kNoOff);
-    plut_raw = (int)bld4(rlut, nn >= 0 ? 4 * (uint32_t)nn : kNoOff);
-  };
-
-  for (int L = -1; L < n; ++L) {
-    prefetch(L);   // issued right after the previous signal (see u_group)
-    // cold items of layer L's list, spread evenly: item i (list order) goes
-    // to thread i mod 256, a batch of kGather at a time.  The first batch's
-    // slots, down nibbles of rows [j0, j0 + 16) and their scales load while
-    // the U groups run; only the cold activations wait for them.
-    int total = 0, act_chunk = 0, n_records = 0;
-    const uint8_t* records = nullptr;
-    const int32_t* act_slots = nullptr;
-    int gpos[kGather], gslot[kGather];
-    u32x2v gnib[kGather];
-    rsrc_t rgs = rsrc(nullptr, 0), rgr = rgs;
-    float gsc[kGather];
-    // list position and record data of items t + 256 (b + m), m < kGather
-    auto gather = [&](int b) {
-#pragma unroll
-      for (int m = 0; m < kGather; ++m) {
-        const int i = t + kThreads * (b + m);
-        gpos[m] = -1;
-        if (i < total) {
-          int lo = 0, hi = kTokChunks;            // pfx[lo] <= i < pfx[hi]
-          while (hi - lo > 1) {
-            const int mid = (lo + hi) >> 1;
-            if (sh.d.pfx[mid] <= i) lo = mid;
-            else hi = mid;
-          }
-          gpos[m] = lo * act_chunk + (i - sh.d.pfx[lo]);
-        }
-      }
-      int sl[kGather];
-#pragma unroll
-      for (int m = 0; m < kGather; ++m) sl[m] = (int)bld4(rgs, gpos[m] >= 0 ? 4 * (uint32_t)gpos[m] : kNoOff);
-#pragma unroll
-      for (int m = 0; m < kGather; ++m) {
-        const bool v = gpos[m] >= 0 && sl[m] >= 0 && sl[m] < n_records;
-        gslot[m] = v ? sl[m] : -1;
-        const uint32_t ro = v ? (uint32_t)sl[m] * kRecBytes : kNoOff;
-        gnib[m] = bld8(rgr, ro + kOffDown + j0 / 2);
-        gsc[m] = half_bits_to_float(bld2(rgr, ro + kOffScales + 2 * (64 + j0 / kGroup)));
-      }
-    };
-#pragma unroll
-    for (int m = 0; m < kGather; ++m) {
-      gpos[m] = gslot[m] = -1;
-      gnib[m] = u32x2v{0, 0};
-      gsc[m] = 0.0f;
-    }
-    if (L >= 0) {
-      tok_wait(a.sync, 1, g, (uint32_t)(L + 1));     // layer L's list is complete
-      const TokLayer& T = a.layers[L];
-      if (T.n_records > 0 && T.act_counts) {
-        act_chunk = T.act_chunk;
-        n_records = T.n_records;
-        records = T.records;
-        act_slots = T.act_slots;
-        rgs = rsrc(act_slots, (uint32_t)kTokChunks * act_chunk * 4);
-        rgr = rsrc(records, (uint32_t)n_records * kRecBytes);
-        const int c = (int)min((uint32_t)T.act_counts[t], (uint32_t)act_chunk);
-        int v = c;
-#pragma unroll
-        for (int off = 1; off < kWave; off <<= 1) {
-          const int u = __shfl_up(v, off, kWave);
-          if (lane >= off) v += u;
-        }
-        if (lane == kWave - 1) sh.d.wsum[w] = v;
-        lds_sync();
-        int base = 0;
-        for (int ww = 0; ww < w; ++ww) base += sh.d.wsum[ww];
-        total = sh.d.wsum[0] + sh.d.wsum[1] + sh.d.wsum[2] + sh.d.wsum[3];
-        sh.d.pfx[t] = base + v - c;
-        if (t == 0) sh.d.pfx[kTokChunks] = total;
-        lds_sync();
-        gather(0);
-      }
-    }
-    tok_wait(a.sync, 0, g, (uint32_t)(L + 2));       // U(L) done: h, h_cold, z
-    const TokLayer* T = L >= 0 ? &a.layers[L] : nullptr;
-    const int nh = T ? T->n_hot : 0;
-    // h and z into LDS; this thread's cold activations; the residual
-    {
-      // the slice is zero past n_hot up to the next multiple of 4 (never
-      // written), and the range ends there: quads past it read zero
-      const rsrc_t rh = rsrc(a.h + (size_t)(L < 0 ? 0 : L) * a.hstride, (uint32_t)(nh + 3) / 4 * 16);
-#pragma unroll
-      for (int m = 0; m < kTokMaxHot / 4 / kThreads; ++m)
-        reinterpret_cast<u32x4*>(sh.d.h)[t + kThreads * m] = bld16(rh, 16 * (t + kThreads * m));
-    }
-    const int pn = pred_n(L);
-    const int rank = (L + 1 < n) ? a.layers[L + 1].rank : 0;
-    if (t < kTokMaxRank / 4 && 4 * t < rank) {
-      const u32x4 v = reinterpret_cast<const u32x4*>(a.z + (size_t)(L + 1) * kTokMaxRank)[t];
-      reinterpret_cast<u32x4*>(sh.d.z)[t] = v;
-    }
-    const rsrc_t rhc = rsrc(a.hc + (size_t)(L < 0 ? 0 : L) * kTokChunks * kTokMaxChunk,
-                            kTokChunks * kTokMaxChunk * 4);
-    float ghc[kGather];
-#pragma unroll
-    for (int m = 0; m < kGather; ++m) ghc[m] = as_f32(bld4(rhc, gslot[m] >= 0 ? 4 * (uint32_t)gpos[m] : kNoOff));
-    float res_v = 0.0f;
-    if (L >= 0 && t < 16) {
+      for (int it = 0; it < kTokMaxHot * 4 / 1024; ++it) bld16_lds(rh, sh.h + 256 * it, 16 * (l + 64 * it));
       const uint16_t* xl = L == 0 ? a.x_in : a.xbuf + (size_t)(L - 1) * kH;
-      res_v = half_bits_to_float(xl[je]);
+      const uint16_t rb = bld2(rsrc(xl, kH * 2), l < kRows ? 2 * (uint32_t)(j0 + l) : kNoOff);
+      const uint16_t nb = bld2(rsrc(N ? N->norm_w : nullptr, N ? kH * 2 : 0u), l < kRows ? 2 * (uint32_t)(j0 + l) : kNoOff);
+      res_v = half_bits_to_float(rb);
+      nwv = half_bits_to_float(nb);
+      if (has_cold)
+        ctl_gather_hc(sh, rsrc(a.hc + (size_t)L * kTokChunks * kTokMaxChunk, kTokChunks * kTokMaxChunk * 4), 0, total);
     }
-    lds_sync();
-    // 1. next layer's logits, threshold, LUT hot filter, ascending compaction
-    //    (the fma order of the two-launch path)
-    if (L + 1 < n && a.layers[L + 1].pd_w) {
-      const TokLayer& P1 = a.layers[L + 1];
+    int ch_n = 0, nn = -1;
+    float zl = 0.0f;
+    uint16_t pbits = 0;
+    int plut = -1;
+    if (psel) {   // chunk g of the next layer's predictor: lane l = neuron g * chunk + l
+      ch_n = N->sel_chunk;
+      const int rank = N->rank;
+      nn = (l < ch_n && g * ch_n + l < N->inter) ? g * ch_n + l : -1;
+      zl = as_f32(bld4(rsrc(a.z + (size_t)(L + 1) * kTokMaxRank, (uint32_t)rank * 4), 4 * (uint32_t)l));
+      const rsrc_t ru = rsrc(N->pu_w, (uint32_t)N->inter * rank * 2);
+#pragma unroll
+      for (int m = 0; m < 8; ++m)
+        bld16_lds(ru, sh.pu + 256 * m, (nn >= 0 && 8 * m < rank) ? (uint32_t)(nn * rank + 8 * m) * 2 : kNoOff);
+      pbits = bld2(rsrc(N->pu_b, (uint32_t)N->inter * 2), nn >= 0 ? 2 * (uint32_t)nn : kNoOff);
+      plut = N->lut ? (int)bld4(rsrc(N->lut, (uint32_t)N->inter * 4), nn >= 0 ? 4 * (uint32_t)nn : kNoOff) : nn;
+    }
+    int scnt = 0, sslot = -1;
+    if (pstat) {   // a layer without a predictor: chunk g of its fixed list
+      ch_n = N->act_chunk;
+      scnt = (int)bld4(rsrc(N->act_counts, kTokChunks * 4), 4 * (uint32_t)g);
+      sslot = (int)bld4(rsrc(N->act_slots, (uint32_t)kTokChunks * ch_n * 4),
+                        l < ch_n ? 4 * (uint32_t)(g * ch_n + l) : kNoOff);
+    }
+    if (l < kTokMaxRank) sh.z[l] = zl;
+    wait_vm();
+    __builtin_amdgcn_wave_barrier();
+    // the next layer's logits in the fma order of the two-launch path,
+    // threshold, LUT hot filter and ascending compaction
+    if (psel) {
+      const int rank = N->rank;
       bool keep = false;
-      const int nn = pn;
-      const int plut = P1.lut ? plut_raw : nn;
       if (nn >= 0) {
         float acc = 0.0f;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          if (8 * k >= rank) break;
+        for (int m = 0; m < 8; ++m) {
+          if (8 * m >= rank) break;
+          const u32x4 pv = reinterpret_cast<const u32x4*>(sh.pu)[64 * m + l];
 #pragma unroll
           for (int d = 0; d < 4; ++d) {
-            const int rr = 8 * k + 2 * d;
-            acc = fmaf(bf16_bits_to_float((uint16_t)(P[k][d] & 0xFFFFu)), sh.d.z[rr], acc);
-            acc = fmaf(bf16_bits_to_float((uint16_t)(P[k][d] >> 16)), sh.d.z[rr + 1], acc);
+            acc = fmaf(bf16_bits_to_float((uint16_t)(pv[d] & 0xFFFFu)), sh.z[8 * m + 2 * d], acc);
+            acc = fmaf(bf16_bits_to_float((uint16_t)(pv[d] >> 16)), sh.z[8 * m + 2 * d + 1], acc);
           }
         }
-        const float logit = acc + bf16_bits_to_float(pbias_bits);
-        keep = logit >= a.thr && plut >= 0;
+        keep = acc + bf16_bits_to_float(pbits) >= a.thr && plut >= 0;
       }
       const uint64_t bal = __ballot(keep);
-      if (lane == 0) sh.d.wcnt[w] = __popcll(bal);
-      lds_sync();
-      int base = 0;
-      for (int ww = 0; ww < w; ++ww) base += sh.d.wcnt[ww];
       if (keep) {
-        const int pos = g * P1.sel_chunk + base + __popcll(bal & ((1ull << lane) - 1ull));
-        cst(P1.sel_slots + pos, plut);
-        cst(P1.sel_ids + pos, nn);
+        const int pos = __popcll(bal & ((1ull << l) - 1ull));
+        sh.lst_slot[pos] = plut;
+        sh.lst_id[pos] = nn;
       }
-      if (t == 0) cst(P1.sel_counts + g, sh.d.wcnt[0] + sh.d.wcnt[1] + sh.d.wcnt[2] + sh.d.wcnt[3]);
+      if (l == 0) sh.lst_cnt = __popcll(bal);
+    } else if (pstat) {
+      const int c = min(max(scnt, 0), ch_n);
+      if (l < c) sh.lst_slot[l] = sslot;
+      if (l == 0) sh.lst_cnt = c;
+    } else if (l == 0) {
+      sh.lst_cnt = 0;
     }
-    if (L >= 0) {
-      // 2. hot down rows: 4 per wave
-      float yh[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-      if (nh > 0) {
-        float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int it = 0; it < 4; ++it) {
-          const f32x4* ph = reinterpret_cast<const f32x4*>(sh.d.h) + 4 * (lane + 64 * it);
-          float hv[16];
-#pragma unroll
-          for (int m = 0; m < 4; ++m) {
-            const f32x4 v = ph[m];
-            hv[4 * m] = v[0];
-            hv[4 * m + 1] = v[1];
-            hv[4 * m + 2] = v[2];
-            hv[4 * m + 3] = v[3];
-          }
-#pragma unroll
-          for (int rr = 0; rr < 4; ++rr)
-#pragma unroll
-            for (int d = 0; d < 4; ++d) {
-              const f32x2 lo = fp8x2_to_f32x2(Q[rr][it][d], false);
-              const f32x2 hi = fp8x2_to_f32x2(Q[rr][it][d], true);
-              acc[rr] = fmaf(lo.x, hv[4 * d], acc[rr]);
-              acc[rr] = fmaf(lo.y, hv[4 * d + 1], acc[rr]);
-              acc[rr] = fmaf(hi.x, hv[4 * d + 2], acc[rr]);
-              acc[rr] = fmaf(hi.y, hv[4 * d + 3], acc[rr]);
-            }
-        }
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) yh[rr] = wave_sum(acc[rr]);
+    bar();   // D1: h, the gather activations and the next chunk's list are in LDS
+    if (psel) {
+      const int c = sh.lst_cnt;
+      if (l < c) {
+        cst(N->sel_slots + (size_t)g * ch_n + l, sh.lst_slot[l]);
+        cst(N->sel_ids + (size_t)g * ch_n + l, sh.lst_id[l]);
       }
-      // 3. cold: this thread's items (chunk t) x their 16 down nibbles
-      float yc[16];
+      if (l == 0) cst(N->sel_counts + g, c);
+    }
+    // gather items past the first batch (long lists): this wave, a batch of
+    // 64 at a time, while the workers run the first
+    float ycc[kRows];
 #pragma unroll
-      for (int e = 0; e < 16; ++e) yc[e] = 0.0f;
-      auto cold_item = [&](u32x2v nib, float hs) {
+    for (int e = 0; e < kRows; ++e) ycc[e] = 0.0f;
+    if (T && has_cold && total > kBatch) {
+      const rsrc_t rsl = rsrc(T->act_slots, (uint32_t)kTokChunks * chunk * 4);
+      const rsrc_t rhc = rsrc(a.hc + (size_t)L * kTokChunks * kTokMaxChunk, kTokChunks * kTokMaxChunk * 4);
+      for (int i0 = kBatch; i0 < total; i0 += kWave) {
+        const int i = i0 + l;
+        int pos = -1;
+        if (i < total) {
+          int lo = 0, hi = kTokChunks;        // pfx[lo] <= i < pfx[hi]
+          while (hi - lo > 1) {
+            const int mid = (lo + hi) >> 1;
+            if (sh.pfx[mid] <= i) lo = mid;
+            else hi = mid;
+          }
+          pos = lo * chunk + (i - sh.pfx[lo]);
+        }
+        const int sl = (int)bld4(rsl, pos >= 0 ? 4 * (uint32_t)pos : kNoOff);
+        const bool vv = pos >= 0 && sl >= 0 && sl < T->n_records;
+        const uint32_t ro = vv ? (uint32_t)sl * kRecBytes : kNoOff;
+        const u32x2v nib = bld8(rrec, ro + kOffDown + j0 / 2);
+        const float sc = half_bits_to_float(bld2(rrec, ro + kOffScales + 2 * (64 + j0 / kGroup)));
+        const float hs = as_f32(bld4(rhc, vv ? 4 * (uint32_t)pos : kNoOff)) * sc;
         f16x2 tq[4];
         int4x8_to_f16x2x4(nib.x, tq);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          yc[k] = fmaf(hs, (float)tq[k].x, yc[k]);
-          yc[k + 4] = fmaf(hs, (float)tq[k].y, yc[k + 4]);
+          ycc[k] = fmaf(hs, (float)tq[k].x, ycc[k]);
+          ycc[k + 4] = fmaf(hs, (float)tq[k].y, ycc[k + 4]);
         }
         int4x8_to_f16x2x4(nib.y, tq);
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-          yc[8 + k] = fmaf(hs, (float)tq[k].x, yc[8 + k]);
-          yc[12 + k] = fmaf(hs, (float)tq[k].y, yc[12 + k]);
+          ycc[8 + k] = fmaf(hs, (float)tq[k].x, ycc[8 + k]);
+          ycc[12 + k] = fmaf(hs, (float)tq[k].y, ycc[12 + k]);
         }
-      };
-#pragma unroll
-      for (int m = 0; m < kGather; ++m)
-        if (gslot[m] >= 0) cold_item(gnib[m], ghc[m] * gsc[m]);
-      // lists longer than 256 kGather items: further batches, loaded now
-      for (int b = kGather; t + kThreads * b < total; b += kGather) {
-        gather(b);
-#pragma unroll
-        for (int m = 0; m < kGather; ++m) ghc[m] = as_f32(bld4(rhc, gslot[m] >= 0 ? 4 * (uint32_t)gpos[m] : kNoOff));
-#pragma unroll
-        for (int m = 0; m < kGather; ++m)
-          if (gslot[m] >= 0) cold_item(gnib[m], ghc[m] * gsc[m]);
       }
+    }
+    if (T && has_cold && total > kBatch) {
 #pragma unroll
-      for (int e = 0; e < 16; ++e) yc[e] = wave_sum(yc[e]);
-      if (lane == 0) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) sh.d.cold[w][e] = yc[e];
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) sh.d.yhot[4 * w + rr] = nh > 0 ? yh[rr] * dsc[rr] : 0.0f;
+      for (int e = 0; e < kRows; ++e) {
+        const float sv = wave_sum(ycc[e]);
+        if (l == 0) sh.cpart_ctl[e] = sv;
       }
-      lds_sync();
-      // 4. x_{L+1} = x_L + y; the next layer's x * w and sum-of-squares partial
-      if (t < 16) {
-        const float yct = (sh.d.cold[0][t] + sh.d.cold[1][t]) + (sh.d.cold[2][t] + sh.d.cold[3][t]);
-        const float y = sh.d.yhot[t] + yct;
+    } else if (l < kRows) {
+      sh.cpart_ctl[l] = 0.0f;
+    }
+    bar();   // D2: the workers' row sums are in LDS
+    if (T) {
+      if (l < kRows) {
+        const float yc = (((sh.cpart[0][l] + sh.cpart[1][l]) + (sh.cpart[2][l] + sh.cpart[3][l])) +
+                          ((sh.cpart[4][l] + sh.cpart[5][l]) + sh.cpart[6][l])) + sh.cpart_ctl[l];
+        const float y = sh.yhot[l] + yc;
         const uint16_t ob = float_to_half_bits(res_v + y);
-        cst2(rsrc(a.xbuf + (size_t)L * kH, kH * 2), 2 * je, ob);
-        if (L == n - 1) a.x_out[je] = ob;
+        cst2(rsrc(a.xbuf + (size_t)L * kH, kH * 2), 2 * (uint32_t)(j0 + l), ob);
+        if (L == n - 1) a.x_out[j0 + l] = ob;
         const float o = half_bits_to_float(ob);
-        sh.d.out[t] = o;
-        if (L + 1 < n) cst2(rsrc(a.xw + (size_t)(L + 1) * kH, kH * 2), 2 * je, float_to_half_bits(o * half_bits_to_float(nwv_bits)));
+        sh.out[l] = o;
+        if (N) cst2(rsrc(a.xw + (size_t)(L + 1) * kH, kH * 2), 2 * (uint32_t)(j0 + l), float_to_half_bits(o * nwv));
       }
-      if (L + 1 < n) {
-        lds_sync();
-        if (t == 0) cst(a.ssq + (size_t)(L + 1) * kTokGroups + tile, ssq16(sh.d.out));
+      if (N) {
+        __builtin_amdgcn_wave_barrier();
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (l == 0) cst(a.ssq + (size_t)(L + 1) * kTokGroups + tile, ssq16(sh.out));
       }
     }
     tok_arrive(a.sync, 1, g, (uint32_t)(L + 2));
   }
 }
 
+// ── the worker waves ────────────────────────────────────────────────────────
+
+// Every worker load is unconditional (absent data reads as zero through an
+// empty or short descriptor) and issued in the same order each layer --
+// gather nibbles, next gate/up rows (end of U), next chunk's records (D1),
+// next down rows (end of D) -- so the compiler can wait for exactly the loads
+// a compute step needs and leave the younger ones streaming.
 template <int NPW>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_token(TokArgs a) {
+__device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
+  const int l = lane_id();
+  const int n = a.n_layers;
+  const int tile = (g & 7) * (kTokGroups / 8) + (g >> 3);
+  const int j0 = tile * kRows;
+  const int rs = wi < 2 ? 3 * wi : 2 * wi + 2;   // down rows [rs, rs + rc) of the tile
+  const int rc = wi < 2 ? 3 : 2;
+  const int k0 = (g * kWorkers + wi) * NPW;       // hot neurons [k0, k0 + NPW)
+  const int g0 = l >> 2;
+  CLayer* LT = layer_table(a);
+  // weights, each loaded one phase ahead of its use
+  u32x4 WU[NPW][8];           // gate (0..3) and up (4..7) chunks of the hot neurons
+  float gsc = 0.0f, usc = 0.0f, gbi = 0.0f;       // lane j < NPW: neuron k0 + j
+  u32x4 WD[3][4];             // down rows
+  float dsc[3];
+  u32x4 RQ[kColdR][4];        // cold records of the chunk: gate and up halves,
+  float RS[kColdR][4];        //   their group scales,
+  float RG[kColdR];           //   gate bias
+  int RSL[kColdR];            //   and slots
+  u32x2v NB[kGat];            // gather items: down nibbles of the tile's rows,
+  float NS[kGat];             //   their scale
+  // neurons [j0h, j1h) of the gate/up rows (and, with the first, the scales)
+  auto load_hot = [&](int L, int j0h, int j1h) {          // L may be n: reads zero
+    const bool v = L < n;
+    CLayer& T = LT[v ? L : n - 1];
+    const uint32_t nh = v ? (uint32_t)T.n_hot : 0u;
+    const rsrc_t ra = rsrc(T.gate_q, nh * kH), rb = rsrc(T.up_q, nh * kH);
+#pragma unroll
+    for (int j = 0; j < NPW; ++j) {
+      if (j < j0h || j >= j1h) continue;
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        const uint32_t o = (uint32_t)(k0 + j) * kH + 1024 * it + 16 * l;   // past n_hot: zero
+        WU[j][it] = bld16(ra, o);
+        WU[j][4 + it] = bld16(rb, o);
+      }
+    }
+    if (j0h == 0) {
+      const uint32_t so = l < NPW ? 4 * (uint32_t)(k0 + l) : kNoOff;
+      gsc = as_f32(bld4(rsrc(T.gate_s, nh * 4), so));
+      usc = as_f32(bld4(rsrc(T.up_s, nh * 4), so));
+      gbi = as_f32(bld4(rsrc(T.hot_gbias, T.hot_gbias ? nh * 4 : 0u), so));
+    }
+  };
+  // down rows [rs + r0, rs + r1) (those of the wave)
+  auto load_down = [&](int L, int r0, int r1) {         // L may be n (or -1): reads zero
+    const bool v = L >= 0 && L < n;
+    CLayer& T = LT[v ? L : 0];
+    const int stride = T.down_stride;
+    const bool hv = v && T.n_hot > 0;
+    const int nch = hv ? stride >> 4 : 0;
+    const rsrc_t rq = rsrc(T.down_q, hv ? (uint32_t)kH * stride : 0u);
+    const rsrc_t rd = rsrc(T.down_s, hv ? kH * 4 : 0u);
+#pragma unroll
+    for (int rr = 0; rr < 3; ++rr) {
+      if (rr < r0 || rr >= r1) continue;
+      const bool rv = rr < rc;
+      const int row = j0 + rs + rr;
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        const int c = l + 64 * it;
+        WD[rr][it] = bld16(rq, (rv && c < nch) ? (uint32_t)(row * stride + 16 * c) : kNoOff);
+      }
+      dsc[rr] = as_f32(bld4(rd, rv ? 4 * (uint32_t)row : kNoOff));
+    }
+  };
+  // records of chunk items k = wi + kWorkers i of layer L (the list in LDS)
+  auto load_records = [&](int L) {      // L may be n: reads zero
+    const bool v = L < n;
+    CLayer& T = LT[v ? L : n - 1];
+    const int cnt = v ? sh.lst_cnt : 0;
+    const uint32_t nr = v ? (uint32_t)T.n_records : 0u;
+    const rsrc_t rr = rsrc(T.records, nr * kRecBytes);
+    const rsrc_t rb = rsrc(T.cold_gbias, T.cold_gbias ? nr * 4 : 0u);
+#pragma unroll
+    for (int i = 0; i < kColdR; ++i) {
+      const int k = wi + kWorkers * i;
+      const int sl = k < cnt ? sh.lst_slot[k] : -1;
+      const bool ok = sl >= 0 && (uint32_t)sl < nr;
+      RSL[i] = ok ? sl : -1;
+      const uint32_t ro = ok ? (uint32_t)sl * kRecBytes : kNoOff;
+#pragma unroll
+      for (int it = 0; it < 2; ++it) {
+        RQ[i][it] = bld16(rr, ro + kOffGate + 16 * (l + 64 * it));
+        RQ[i][2 + it] = bld16(rr, ro + kOffUp + 16 * (l + 64 * it));
+      }
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        RS[i][2 * q] = half_bits_to_float(bld2(rr, ro + kOffScales + 2 * (32 * q + g0)));
+        RS[i][2 * q + 1] = half_bits_to_float(bld2(rr, ro + kOffScales + 2 * (32 * q + 16 + g0)));
+      }
+      RG[i] = as_f32(bld4(rb, ok ? 4 * (uint32_t)sl : kNoOff));
+    }
+  };
+  // down nibbles of the first gather batch of layer L (the table in LDS)
+  auto load_nibbles = [&](int L) {
+    const bool v = L >= 0 && LT[L].n_records > 0 && LT[L].act_counts;
+    CLayer& T = LT[L >= 0 ? L : 0];
+    const rsrc_t rr = rsrc(T.records, v ? (uint32_t)T.n_records * kRecBytes : 0u);
+#pragma unroll
+    for (int m = 0; m < kGat; ++m) {
+      const int sl = sh.it_slot[wi * kWave + l + kWorkers * kWave * m];
+      const uint32_t ro = sl >= 0 ? (uint32_t)sl * kRecBytes : kNoOff;
+      NB[m] = bld8(rr, ro + kOffDown + j0 / 2);
+      NS[m] = half_bits_to_float(bld2(rr, ro + kOffScales + 2 * (64 + j0 / kGroup)));
+    }
+  };
+
+  for (int L = -1; L < n; ++L) {
+    CLayer* T = L >= 0 ? LT + L : nullptr;
+    const bool has_cold = T && T->n_records > 0 && T->act_counts;
+    // ================= U phase
+    bar();   // B1: the control's inputs have landed
+    load_down(L, 1, 3);          // the rest of this layer's down rows
+    if (T) {
+      const float r = sh.r;
+      // hot neurons (the accumulation order of the two-launch path)
+      if (k0 < T->n_hot) {
+        float gg[NPW], uu[NPW];
+#pragma unroll
+        for (int j = 0; j < NPW; ++j) gg[j] = uu[j] = 0.0f;
+#pragma unroll
+        for (int it = 0; it < 4; ++it) {
+          const u32x4* p = reinterpret_cast<const u32x4*>(sh.nat) + (1024 * it + 16 * l) / 8;
+          const u32x4 x0 = p[0], x1 = p[1];
+          const f16x2 xp[8] = {as_f16x2(x0.x), as_f16x2(x0.y), as_f16x2(x0.z), as_f16x2(x0.w),
+                               as_f16x2(x1.x), as_f16x2(x1.y), as_f16x2(x1.z), as_f16x2(x1.w)};
+#pragma unroll
+          for (int j = 0; j < NPW; ++j)
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+              gg[j] = dot2(fp8x2_to_f16x2(WU[j][it][d], false), xp[2 * d], gg[j]);
+              gg[j] = dot2(fp8x2_to_f16x2(WU[j][it][d], true), xp[2 * d + 1], gg[j]);
+              uu[j] = dot2(fp8x2_to_f16x2(WU[j][4 + it][d], false), xp[2 * d], uu[j]);
+              uu[j] = dot2(fp8x2_to_f16x2(WU[j][4 + it][d], true), xp[2 * d + 1], uu[j]);
+            }
+        }
+        float hg = 0.0f, hu = 0.0f;
+#pragma unroll
+        for (int j = 0; j < NPW; ++j) {
+          const float sg = wave_sum(gg[j]), su = wave_sum(uu[j]);
+          if (l == j) {
+            hg = sg;
+            hu = su;
+          }
+        }
+        if (l < NPW) sh.h_out[wi * NPW + l] = gated_act(r * hg * gsc + gbi, r * hu * usc, a.relu, a.both);
+      }
+      // this worker's cold items of chunk g: h = act(gate, up) (cold_role's arithmetic)
+      if (has_cold) {
+#pragma unroll
+        for (int i = 0; i < kColdR; ++i) {
+          if (RSL[i] < 0) continue;
+          float pg[2] = {0.0f, 0.0f}, pu[2] = {0.0f, 0.0f};
+#pragma unroll
+          for (int it = 0; it < 2; ++it) {
+            const u32x4* p = reinterpret_cast<const u32x4*>(sh.nat) + (32 * l + 2048 * it) / 8;
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+              const u32x4 xq = pair_layout(p[d]);
+              f16x2 tq[4];
+              int4x8_to_f16x2x4(RQ[i][it][d], tq);
+#pragma unroll
+              for (int k = 0; k < 4; ++k) pg[it] = dot2(tq[k], as_f16x2(xq[k]), pg[it]);
+              int4x8_to_f16x2x4(RQ[i][2 + it][d], tq);
+#pragma unroll
+              for (int k = 0; k < 4; ++k) pu[it] = dot2(tq[k], as_f16x2(xq[k]), pu[it]);
+            }
+          }
+          const float gv = r * wave_sum(pg[0] * RS[i][0] + pg[1] * RS[i][1]) + RG[i];
+          const float uv = r * wave_sum(pu[0] * RS[i][2] + pu[1] * RS[i][3]);
+          if (l == 0) sh.hc_out[wi + kWorkers * i] = gated_act(gv, uv, a.relu, a.both);
+        }
+      }
+    }
+    bar();   // B2
+    load_nibbles(L);
+    load_hot(L + 1, 0, 1);       // half the next gate/up rows now ...
+    // ================= D phase
+    bar();   // D1: the control's inputs have landed
+    load_records(L + 1);
+    load_hot(L + 1, 1, NPW);     // ... the rest once the phase's inputs are in
+    float yc[kRows];
+#pragma unroll
+    for (int e = 0; e < kRows; ++e) yc[e] = 0.0f;
+    if (T) {
+      // hot down rows (down_role's accumulation order)
+      float acc[3] = {0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        const f32x4* ph = reinterpret_cast<const f32x4*>(sh.h) + 4 * (l + 64 * it);
+        float hv[16];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+          const f32x4 v = ph[m];
+          hv[4 * m] = v[0];
+          hv[4 * m + 1] = v[1];
+          hv[4 * m + 2] = v[2];
+          hv[4 * m + 3] = v[3];
+        }
+#pragma unroll
+        for (int rr = 0; rr < 3; ++rr)
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            const f32x2 lo = fp8x2_to_f32x2(WD[rr][it][d], false);
+            const f32x2 hi = fp8x2_to_f32x2(WD[rr][it][d], true);
+            acc[rr] = fmaf(lo.x, hv[4 * d], acc[rr]);
+            acc[rr] = fmaf(lo.y, hv[4 * d + 1], acc[rr]);
+            acc[rr] = fmaf(hi.x, hv[4 * d + 2], acc[rr]);
+            acc[rr] = fmaf(hi.y, hv[4 * d + 3], acc[rr]);
+          }
+      }
+#pragma unroll
+      for (int rr = 0; rr < 3; ++rr) {
+        const float sv = wave_sum(acc[rr]);
+        if (l == 0 && rr < rc) sh.yhot[rs + rr] = T->n_hot > 0 ? sv * dsc[rr] : 0.0f;
+      }
+      // cold: this lane's items of the first gather batch x their 16 down nibbles
+      if (has_cold) {
+#pragma unroll
+        for (int m = 0; m < kGat; ++m) {
+          const int i = wi * kWave + l + kWorkers * kWave * m;
+          if (sh.it_slot[i] >= 0) {
+            const float hs = sh.it_hc[i] * NS[m];
+            f16x2 tq[4];
+            int4x8_to_f16x2x4(NB[m].x, tq);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              yc[k] = fmaf(hs, (float)tq[k].x, yc[k]);
+              yc[k + 4] = fmaf(hs, (float)tq[k].y, yc[k + 4]);
+            }
+            int4x8_to_f16x2x4(NB[m].y, tq);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+              yc[8 + k] = fmaf(hs, (float)tq[k].x, yc[8 + k]);
+              yc[12 + k] = fmaf(hs, (float)tq[k].y, yc[12 + k]);
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < kRows; ++e) {
+        const float sv = wave_sum(yc[e]);
+        if (l == 0) sh.cpart[wi][e] = sv;
+      }
+    }
+    bar();   // D2
+    load_down(L + 1, 0, 1);      // the next layer's first down row (the rest at B1)
+  }
+}
+
+template <int NPW>
+__global__ __launch_bounds__(kTokThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_token(TokArgs a) {
   __shared__ TokShared sh;
-  const int b = blockIdx.x;
-  const int g = (b >> 4) * 8 + (b & 7);      // index within the role; g & 7 = b & 7 (the XCD)
-  if (((b >> 3) & 1) == 0)
-    u_group<NPW>(a, g, sh);
+  const int g = blockIdx.x;   // consecutive groups run on different XCDs (g & 7)
+  const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  if (w == 0)
+    control<NPW>(a, g, sh);
   else
-    d_group(a, g, sh);
+    worker<NPW>(a, g, w - 1, sh);
 }
 
 }  // namespace
@@ -706,23 +858,23 @@ __global__ __launch_bounds__(kThreads) void k_tok_prep(const uint16_t* x, const 
 
 int tok_launch(const TokArgs& a, int npw, hipStream_t st) {
   if (npw == 2)
-    hipLaunchKernelGGL(k_token<2>, dim3(kTokGrid), dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL(k_token<2>, dim3(kTokGroups), dim3(kTokThreads), 0, st, a);
   else
-    hipLaunchKernelGGL(k_token<4>, dim3(kTokGrid), dim3(kThreads), 0, st, a);
+    hipLaunchKernelGGL(k_token<3>, dim3(kTokGroups), dim3(kTokThreads), 0, st, a);
   OI2_CHECK_LAUNCH();
   return OI2_OK;
 }
 
 // Number of token-kernel workgroups the device holds at once (the launch
-// needs all kTokGrid of them resident).
+// needs all kTokGroups of them resident).
 int tok_resident(int npw, int* resident) {
   int dev = 0, cus = 0, per_cu = 0;
   OI2_CHECK_HIP(hipGetDevice(&dev));
   OI2_CHECK_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
   if (npw == 2)
-    OI2_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_token<2>, kThreads, 0));
+    OI2_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_token<2>, kTokThreads, 0));
   else
-    OI2_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_token<4>, kThreads, 0));
+    OI2_CHECK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k_token<3>, kTokThreads, 0));
   *resident = per_cu * cus;
   return OI2_OK;
 }
