@@ -37,6 +37,7 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 // (v.y, v[k]) reads element 0 instead.
 __device__ __forceinline__ f16x2 as_f16x2(uint32_t v) { return __builtin_bit_cast(f16x2, v); }
 __device__ __forceinline__ float as_f32(uint32_t v) { return __builtin_bit_cast(float, v); }
+__device__ __forceinline__ uint32_t as_u32(float v) { return __builtin_bit_cast(uint32_t, v); }
 
 // 16 payload bytes at a 2-byte aligned address (one global_load_dwordx4).
 __device__ __forceinline__ u32x4 load16_a2(const uint8_t* p) {

@@ -79,9 +79,10 @@ __device__ __forceinline__ CLayer* layer_table(const TokArgs& a) {
   return reinterpret_cast<CLayer*>(reinterpret_cast<uintptr_t>(a.layers));
 }
 
-// A buffer descriptor over [p, p + bytes).  Every call site passes
-// wave-uniform values; readfirstlane lets the compiler see that (otherwise it
-// wraps each load in a loop over the distinct descriptors of the wave).
+// A buffer descriptor over [p, p + bytes).  p and bytes must be wave-uniform
+// (lane 0's are taken for the whole wave); lane-dependent parts go in the
+// access offset.  readfirstlane lets the compiler see the uniformity
+// (otherwise it wraps each access in a loop over the wave's descriptors).
 __device__ __forceinline__ rsrc_t rsrc(const void* p, uint32_t bytes) {
   const uint64_t v = reinterpret_cast<uint64_t>(p);
   // readfirstlane returns int: widen each half as uint32_t, or a low half
@@ -111,8 +112,13 @@ __device__ __forceinline__ uint16_t bld2(rsrc_t r, uint32_t off) {
 __device__ __forceinline__ void bld16_lds(rsrc_t r, void* dst, uint32_t off) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)dst, 16, off, 0, 0, 0);
 }
+// Agent-coherent (write-through) stores at a descriptor + lane offset: one
+// offset register per lane rather than a 64-bit address.
 __device__ __forceinline__ void cst2(rsrc_t r, uint32_t off, uint16_t v) {
   __builtin_amdgcn_raw_buffer_store_b16(v, r, off, 0, kSc1);
+}
+__device__ __forceinline__ void cst4(rsrc_t r, uint32_t off, uint32_t v) {
+  __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, kSc1);
 }
 template <typename T>
 __device__ __forceinline__ T cld(const T* p) {
@@ -136,7 +142,14 @@ __device__ __forceinline__ u32x4 pair_layout(u32x4 x) {
 // Workgroup barrier that waits for LDS traffic only (never for vector memory
 // loads: the workers' weight loads stay in flight across it).
 __device__ __forceinline__ void bar() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-__device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// vmcnt(0), issued both as asm (a fence the compiler cannot move) and as the
+// builtin, which tells the compiler's counter model that every load has
+// landed: otherwise, once stores are in flight too, it waits for those
+// stores before the next use of any earlier load's register.
+__device__ __forceinline__ void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0) expcnt(7) lgkmcnt(15)
+}
 
 // Control wave: end of phase r (0 U, 1 D) for group g, epoch e.
 __device__ __forceinline__ void tok_arrive(uint32_t* sync, int r, int g, uint32_t e) {
@@ -335,7 +348,8 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
     __builtin_amdgcn_wave_barrier();
     if (has_cold) ctl_gather_table(sh, rsrc(T->act_slots, (uint32_t)kTokChunks * chunk * 4), T->n_records, 0, total);
     // the next layer's predictor row: z = D q, q = bf16(fp16(x r w'))
-    // (pred_d_role's arithmetic)
+    // (pred_d_role's arithmetic); stored with the phase's other outputs
+    float zrow = 0.0f;
     if (pred) {
       float acc = 0.0f;
 #pragma unroll
@@ -351,8 +365,7 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
           acc = fmaf(bf16_bits_to_float((uint16_t)(dv[d] >> 16)), q1, acc);
         }
       }
-      acc = wave_sum(acc);
-      if (l == 0) cst(a.z + (size_t)(L + 1) * kTokMaxRank + g, acc);
+      zrow = wave_sum(acc);
     }
     // the chunk's items past the workers' share (cold_role's arithmetic);
     // past kCtlCold more, one at a time
@@ -404,11 +417,14 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
       if (l == 0) sh.hc_out[k] = hv;
     }
     bar();   // B2: the workers' activations are in LDS
+    if (pred && l == 0) cst4(rsrc(a.z + (size_t)(L + 1) * kTokMaxRank, kTokMaxRank * 4), 4 * (uint32_t)g, as_u32(zrow));
     if (T) {
       const int k = g * kWorkers * NPW + l;
-      if (l < kWorkers * NPW && k < T->n_hot) cst(a.h + (size_t)L * kTokMaxHot + k, sh.h_out[l]);
+      if (l < kWorkers * NPW && k < T->n_hot)
+        cst4(rsrc(a.h + (size_t)L * kTokMaxHot, kTokMaxHot * 4), 4 * (uint32_t)k, as_u32(sh.h_out[l]));
       if (has_cold && l < sh.lst_cnt)
-        cst(a.hc + (size_t)L * kTokChunks * kTokMaxChunk + (size_t)g * chunk + l, sh.hc_out[l]);
+        cst4(rsrc(a.hc + (size_t)L * kTokChunks * kTokMaxChunk, kTokChunks * kTokMaxChunk * 4),
+             4 * (uint32_t)(g * chunk + l), as_u32(sh.hc_out[l]));
     }
     tok_arrive(a.sync, 0, g, (uint32_t)(L + 2));
 
@@ -454,6 +470,8 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
     }
     if (l < kTokMaxRank) sh.z[l] = zl;
     wait_vm();
+    // take the loaded values into plain registers now, before any store
+    asm volatile("" : "+v"(res_v), "+v"(nwv));
     __builtin_amdgcn_wave_barrier();
     // the next layer's logits in the fma order of the two-launch path,
     // threshold, LUT hot filter and ascending compaction
@@ -489,14 +507,6 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
       sh.lst_cnt = 0;
     }
     bar();   // D1: h, the gather activations and the next chunk's list are in LDS
-    if (psel) {
-      const int c = sh.lst_cnt;
-      if (l < c) {
-        cst(N->sel_slots + (size_t)g * ch_n + l, sh.lst_slot[l]);
-        cst(N->sel_ids + (size_t)g * ch_n + l, sh.lst_id[l]);
-      }
-      if (l == 0) cst(N->sel_counts + g, c);
-    }
     // gather items past the first batch (long lists): this wave, a batch of
     // 64 at a time, while the workers run the first
     float ycc[kRows];
@@ -547,6 +557,17 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
     } else if (l < kRows) {
       sh.cpart_ctl[l] = 0.0f;
     }
+    // the next layer's list, after every use of a loaded value: the compiler
+    // makes a wave wait for its outstanding stores before it uses a load
+    // issued ahead of them
+    if (psel) {
+      const int c = sh.lst_cnt;
+      if (l < c) {
+        cst4(rsrc(N->sel_slots + (size_t)g * ch_n, (uint32_t)ch_n * 4), 4 * (uint32_t)l, (uint32_t)sh.lst_slot[l]);
+        cst4(rsrc(N->sel_ids + (size_t)g * ch_n, (uint32_t)ch_n * 4), 4 * (uint32_t)l, (uint32_t)sh.lst_id[l]);
+      }
+      if (l == 0) cst4(rsrc(N->sel_counts, kTokChunks * 4), 4 * (uint32_t)g, (uint32_t)c);
+    }
     bar();   // D2: the workers' row sums are in LDS
     if (T) {
       if (l < kRows) {
@@ -555,7 +576,7 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
         const float y = sh.yhot[l] + yc;
         const uint16_t ob = float_to_half_bits(res_v + y);
         cst2(rsrc(a.xbuf + (size_t)L * kH, kH * 2), 2 * (uint32_t)(j0 + l), ob);
-        if (L == n - 1) a.x_out[j0 + l] = ob;
+        if (L == n - 1) __builtin_amdgcn_raw_buffer_store_b16(ob, rsrc(a.x_out, kH * 2), 2 * (uint32_t)(j0 + l), 0, 0);
         const float o = half_bits_to_float(ob);
         sh.out[l] = o;
         if (N) cst2(rsrc(a.xw + (size_t)(L + 1) * kH, kH * 2), 2 * (uint32_t)(j0 + l), float_to_half_bits(o * nwv));
@@ -563,7 +584,7 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
       if (N) {
         __builtin_amdgcn_wave_barrier();
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        if (l == 0) cst(a.ssq + (size_t)(L + 1) * kTokGroups + tile, ssq16(sh.out));
+        if (l == 0) cst4(rsrc(a.ssq + (size_t)(L + 1) * kTokGroups, kTokGroups * 4), 4 * (uint32_t)tile, as_u32(ssq16(sh.out)));
       }
     }
     tok_arrive(a.sync, 1, g, (uint32_t)(L + 2));
