@@ -9,12 +9,18 @@ format, resident in HBM; a random-init bf16 predictor per layer
 predicted active, selecting layer L+1's cold neurons from layer L's input.
 Weights are N(0, 0.02) from a fixed seed (synthetic data, nothing loaded).
 
-Prints one JSON line.  `value` is tokens/s with every input already in HBM.
-`roofline` is the ffn_up kernel (hot gate/up + cold gather/dequant/act/down +
-lookahead predictor projection): its mean duration comes from every layer's
-ffn_up launched back to back between two hipEvents on the launch stream;
-`cpu_baseline` is the restated reference CPU path (per-neuron record decode
-loop + F.linear FFN) over a few recorded tokens, bounded to ~20 s.
+Prints one JSON line.  `value` is tokens/s with every input already in HBM,
+on the stack's default path: one persistent kernel per token (k_token, all 32
+layers in one launch) where the configuration allows it, else two launches
+per layer.  `roofline` is that dominant kernel: k_token's mean duration comes
+from back-to-back launches between two hipEvents on the launch stream, and its
+algorithmic bytes are the 32 layers' weights it must read (hot gate/up/down
+fp8 rows and scales, every active cold record, both predictor projections)
+plus the token and per-layer activations.  `kernels` gives the two-launch
+path's k_ffn_up / k_ffn_down the same way, and `two_launch_tok_s` that path's
+whole-token rate.  `cpu_baseline` is the restated reference CPU path
+(per-neuron record decode loop + F.linear FFN) over a few recorded tokens,
+bounded to ~20 s.
 """
 import argparse
 import json
@@ -32,10 +38,11 @@ H, INTER, N_LAYERS, N_HOT, RANK = 4096, 14336, 32, 3584, 64
 ACTIVE_FRAC = 0.05
 EPS = 1e-5
 HBM_PEAK_GBS = 8000.0
-# HBM bytes per k_ffn_up launch on this workload, from rocprofv3 --pmc runs:
-# FETCH_SIZE 16593.7 KiB x 2.000 + WRITE_SIZE 2103.6 KiB x 1.000, the factors
-# being what each counter reads for a plain 256 MiB copy (--copy-calibration)
-UP_TRAFFIC_BYTES = (16593.7 * 2.0 + 2103.6) * 1024
+# HBM bytes per launch on this workload, from rocprofv3 --pmc runs
+# (FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000 KiB, the factors being what each
+# counter reads for a plain 256 MiB copy, --copy-calibration)
+UP_TRAFFIC_BYTES = (16593.7 * 2.0 + 2103.6) * 1024       # k_ffn_up
+TOKEN_TRAFFIC_BYTES = (811323.5 * 2.0 + 2936.3) * 1024      # k_token
 
 
 def log(msg):
@@ -374,11 +381,37 @@ def main():
     tok_s = args.steps / secs
     log(f"timed {args.steps} tokens: {secs * 1e3:.2f} ms ({tok_s:.1f} tok/s)")
 
-    # mean kernel durations: every layer's ffn_up launched back to back between
-    # two hipEvents on the launch stream, then every layer's ffn_down
+    token_path = st.token_kernel
+    # the two-launch path's whole-token rate, for comparison
+    two_tok_s = None
+    if token_path:
+        st.set_token_kernel(False)
+        n2 = min(args.steps, 128)
+        with torch.cuda.stream(stream):
+            for i in range(4):
+                st.decode(bufs[i % 2], bufs[(i + 1) % 2], stream)
+        stream.synchronize()
+        torch.cuda.synchronize()
+        t2 = time.perf_counter()
+        with torch.cuda.stream(stream):
+            ev0.record(stream)
+            for i in range(n2):
+                st.decode(bufs[i % 2], bufs[(i + 1) % 2], stream)
+            ev1.record(stream)
+        stream.synchronize()
+        two_tok_s = n2 / max(time.perf_counter() - t2, ev0.elapsed_time(ev1) / 1e3)
+        st.set_token_kernel(True)
+        log(f"two-launch path: {two_tok_s:.1f} tok/s")
+
+    # mean kernel durations: the token kernel launched back to back between two
+    # hipEvents on the launch stream; then every layer's ffn_up of the
+    # two-launch path the same way, then every layer's ffn_down
     k = base + args.steps
     xi, xo = bufs[k % 2], bufs[(k + 1) % 2]
+    tok_us = None
     with torch.cuda.stream(stream):
+        if token_path:
+            tok_us = st.profile_token(xi, xo, stream, reps=args.profile_reps)
         up_us, down_us = st.profile(xi, xo, stream, reps=args.profile_reps)
     xs, counts, slots, ids = st.trace()
     torch.cuda.synchronize()
@@ -392,6 +425,16 @@ def main():
     token_bytes = N_LAYERS * (up_b + down_b)
     log(f"ffn_up {up_us:.2f} us/launch {up_gbs:.0f} GB/s; ffn_down {down_us:.2f} us "
         f"{down_gbs:.0f} GB/s; mean active cold {mean_active:.0f}")
+    if token_path:
+        tok_gbs = token_bytes / (tok_us * 1e-6) / 1e9
+        log(f"token kernel {tok_us:.1f} us/launch {tok_gbs:.0f} GB/s ({token_bytes / 1e6:.1f} MB)")
+        roofline = {"bound": "hbm", "achieved": tok_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": tok_gbs / HBM_PEAK_GBS, "traffic": TOKEN_TRAFFIC_BYTES,
+                    "kernel": "k_token", "us_per_launch": tok_us, "bytes_per_launch": token_bytes}
+    else:
+        roofline = {"bound": "hbm", "achieved": up_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": up_gbs / HBM_PEAK_GBS, "traffic": UP_TRAFFIC_BYTES,
+                    "kernel": "k_ffn_up", "us_per_launch": up_us, "bytes_per_launch": up_b}
 
     multi = None
     if args.multi_token:
@@ -451,10 +494,12 @@ def main():
                    "layers": N_LAYERS, "hidden": H, "intermediate": INTER, "n_hot": N_HOT,
                    "batch": 1, "mean_active_cold": round(mean_active, 1),
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "achieved": up_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": up_gbs / HBM_PEAK_GBS, "traffic": UP_TRAFFIC_BYTES,
-                     "kernel": "k_ffn_up", "us_per_launch": up_us, "bytes_per_launch": up_b},
-        "kernels": {"k_ffn_down": {"us_per_launch": down_us, "achieved_gbs": down_gbs,
+        "roofline": roofline,
+        "path": "token kernel" if token_path else "two launches per layer",
+        "two_launch_tok_s": two_tok_s,
+        "kernels": {"k_ffn_up": {"us_per_launch": up_us, "achieved_gbs": up_gbs, "bytes_per_launch": up_b,
+                                 "traffic": UP_TRAFFIC_BYTES},
+                    "k_ffn_down": {"us_per_launch": down_us, "achieved_gbs": down_gbs,
                                    "bytes_per_launch": down_b}},
         "token_bytes": token_bytes,
         "hbm_frac_end_to_end": token_bytes * tok_s / (HBM_PEAK_GBS * 1e9),
