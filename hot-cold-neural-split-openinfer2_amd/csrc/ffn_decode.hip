@@ -270,9 +270,13 @@ __device__ void pred_d_role_t(const UpArgs& a, int row) {
   }
   const f32x4 part = norm ? load_part(a.tok.ssq) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   const float r = norm ? r_from_part(part, a.tok.eps) : 1.0f;
-  float acc = 0.0f;
+  // four partial sums, one per quarter of the row (elements [1024 q, 1024 q +
+  // 1024)), combined as (p0 + p1) + (p2 + p3): the persistent token kernel
+  // splits a row over four workgroups in exactly this order
+  float accq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int it = 0; it < 8; ++it) {
+    float& acc = accq[it >> 1];
     const int e0 = 8 * (lane + 64 * it);
     float q[8];
     if (a.pd_q) {
@@ -307,8 +311,8 @@ __device__ void pred_d_role_t(const UpArgs& a, int row) {
       }
     }
   }
-  acc = wave_sum(acc);
-  if (lane == 0) a.pd_z[row] = acc;
+  const float z = (wave_sum(accq[0]) + wave_sum(accq[1])) + (wave_sum(accq[2]) + wave_sum(accq[3]));
+  if (lane == 0) a.pd_z[row] = z;
 }
 
 __device__ void pred_d_role(const UpArgs& a, int wg) {

@@ -195,6 +195,7 @@ constexpr int kTokChunks = 256;            // active-list chunks: one per group
 constexpr int kTokMaxChunk = 64;           // ids per chunk (one lane each)
 constexpr int kTokMaxRank = 64;
 constexpr int kTokMaxHot = 4096;           // h staged in LDS; also the per-layer h slice
+constexpr int kTokBatch = 896;             // gather items the worker waves take per layer (list order)
 constexpr int kTokSyncWords = 2048 + 192;
 constexpr int kTokSyncErr = 2048 + 128;       // nonzero: a wait ran past its bound
 
@@ -241,7 +242,10 @@ struct TokArgs {
   float* ssq;               // (n_layers, 256) sum-of-squares partials of x_L
   float* h;                 // (n_layers, kTokMaxHot) hot activations, zero past n_hot
   float* hc;                // (n_layers, kTokChunks * kTokMaxChunk) cold activations, list order
-  float* z;                 // (n_layers, kTokMaxRank) predictor down projection of layer L
+  float* z;                 // (n_layers, 4 * kTokMaxRank) predictor down projection of layer L:
+                            // quarter q of row r at 4 r + q
+  float* hcs;               // (n_layers, kGroups, kTokBatch) cold activation x down scale of each
+                            // row group, list positions < kTokBatch
   uint32_t* sync;           // kTokSyncWords, zero at launch
   float eps, thr;
   int relu, both;

@@ -65,6 +65,7 @@ constexpr int kCtlItems = kBatch / kWave;      // gather items per control lane 
 constexpr int kRows = kH / kTokGroups;         // 16 output rows per group
 static_assert(kWorkers == 7, "the row split and the epilogue's sum assume 7 workers");
 static_assert(kTokWorkers == kWorkers, "host and kernel agree on the worker count");
+static_assert(kTokBatch == kBatch, "host and kernel agree on the gather batch");
 
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
@@ -182,15 +183,17 @@ __device__ __forceinline__ void tok_wait(uint32_t* sync, int r, int g, uint32_t 
 
 struct alignas(16) TokShared {
   uint32_t nat[kH / 2];       // x * w of the layer
-  uint32_t xq[kH / 2];        // predictor group: x_L,
-  uint32_t wq[kH / 2];        //   the next layer's norm weight,
-  uint32_t pd[kH / 2];        //   its predictor down row (bf16)
+  uint32_t xq[kH / 8];        // predictor group: a quarter of x_L,
+  uint32_t wq[kH / 8];        //   of the next layer's norm weight,
+  uint32_t pd[kH / 8];        //   and of its predictor down row (bf16)
   float h[kTokMaxHot];        // the layer's hot activations
   uint32_t pu[8 * kWave * 4]; // predictor up rows of chunk g: 16-byte piece m of neuron l at 64 m + l
+  float it_hcs[1024];         // gather items of the current batch: cold activation x down scale
+                              // of the tile's row group (list order; 4 KB, one copy's reach),
+  int it_slot[kBatch];        //   record slot,
+  int it_pos[kBatch];         //   list position
+  float hcs_out[kGroups][kTokMaxChunk];   // this group's items: activation x down scale, per row group
   int pfx[kTokChunks + 1];    // exclusive prefix of the list's chunk counts
-  int it_slot[kBatch];        // gather items of the current batch: record slot,
-  int it_pos[kBatch];         //   list position,
-  float it_hc[kBatch];        //   cold activation
   int lst_slot[kTokMaxChunk]; // chunk g of the next layer's list
   int lst_id[kTokMaxChunk];
   float h_out[kWorkers * 3];  // this group's hot activations
@@ -203,6 +206,11 @@ struct alignas(16) TokShared {
   float r;
   int total, lst_cnt;
 };
+static_assert(offsetof(TokShared, nat) % 16 == 0 && offsetof(TokShared, xq) % 16 == 0 &&
+              offsetof(TokShared, wq) % 16 == 0 && offsetof(TokShared, pd) % 16 == 0 &&
+              offsetof(TokShared, h) % 16 == 0 && offsetof(TokShared, pu) % 16 == 0 &&
+              offsetof(TokShared, it_hcs) % 16 == 0,
+              "LDS DMA targets and 16-byte reads are 16-byte aligned");
 
 // Items of the list: item i (0 <= i < total) is item i - pfx[c] of chunk c.
 // The control lane that owns chunks 4 l .. 4 l + 3 writes list positions of
@@ -234,19 +242,6 @@ __device__ __forceinline__ void ctl_gather_table(TokShared& sh, rsrc_t rslots, i
   }
 }
 
-// Control: cold activations of the items of batch b.
-__device__ __forceinline__ void ctl_gather_hc(TokShared& sh, rsrc_t rhc, int b, int total) {
-  const int l = lane_id();
-  float hv[kCtlItems];
-#pragma unroll
-  for (int m = 0; m < kCtlItems; ++m) {
-    const int i = l + kWave * m;
-    hv[m] = as_f32(bld4(rhc, (b * kBatch + i < total && sh.it_slot[i] >= 0) ? 4 * (uint32_t)sh.it_pos[i] : kNoOff));
-  }
-#pragma unroll
-  for (int m = 0; m < kCtlItems; ++m) sh.it_hc[l + kWave * m] = hv[m];
-}
-
 // ── the control wave ────────────────────────────────────────────────────────
 
 template <int NPW>
@@ -264,7 +259,8 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
     if (L >= 0) tok_wait(a.sync, 1, g, (uint32_t)(L + 1));
     const bool has_cold = T && T->n_records > 0 && T->act_counts;
     const int chunk = has_cold ? T->act_chunk : 0;
-    const bool pred = N && N->pd_w && g < N->rank;
+    // the next layer's predictor: group g sums quarter g & 3 of row g >> 2
+    const bool pred = N && N->pd_w && g < 4 * N->rank;
     // inputs: x * w into LDS, the sum-of-squares partials, the list's counts,
     // and for a predictor group x_L, the next norm weight and the D row
     if (T) {
@@ -280,12 +276,13 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
     if (pred) {
       const uint16_t* xl = L <= 0 ? a.x_in : a.xbuf + (size_t)(L - 1) * kH;
       const rsrc_t rx = rsrc(xl, kH * 2), rw = rsrc(N->norm_w, kH * 2);
-      const rsrc_t rd = rsrc(N->pd_w + (size_t)g * kH, kH * 2);
+      const rsrc_t rd = rsrc(N->pd_w + (size_t)(g >> 2) * kH, kH * 2);
 #pragma unroll
-      for (int it = 0; it < 8; ++it) {
-        bld16_lds(rx, sh.xq + 256 * it, 16 * (l + 64 * it));
-        bld16_lds(rw, sh.wq + 256 * it, 16 * (l + 64 * it));
-        bld16_lds(rd, sh.pd + 256 * it, 16 * (l + 64 * it));
+      for (int it = 0; it < 2; ++it) {
+        const uint32_t off = 16 * (uint32_t)(l + 64 * (2 * (g & 3) + it));
+        bld16_lds(rx, sh.xq + 256 * it, off);
+        bld16_lds(rw, sh.wq + 256 * it, off);
+        bld16_lds(rd, sh.pd + 256 * it, off);
       }
     }
     // the chunk's items past the workers' share: records with the inputs
@@ -294,7 +291,7 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
     const rsrc_t rcgb = rsrc(has_cold ? T->cold_gbias : nullptr,
                              (has_cold && T->cold_gbias) ? (uint32_t)T->n_records * 4 : 0u);
     u32x4 CQ[kCtlCold][4];
-    float CS[kCtlCold][4], CG[kCtlCold];
+    float CS[kCtlCold][4], CG[kCtlCold], CD[kCtlCold];   // CD: down scale of row group l
     int CSL[kCtlCold];
 #pragma unroll
     for (int i = 0; i < kCtlCold; ++i) {
@@ -314,6 +311,7 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
         CS[i][2 * q + 1] = half_bits_to_float(bld2(rrec, ro + kOffScales + 2 * (32 * q + 16 + g0)));
       }
       CG[i] = as_f32(bld4(rcgb, vv ? 4 * (uint32_t)sl : kNoOff));
+      CD[i] = half_bits_to_float(bld2(rrec, ro + kOffScales + 2 * (2 * kGroups + (l & (kGroups - 1)))));
     }
     const float r = r_from_part(f32x4{as_f32(pp.x), as_f32(pp.y), as_f32(pp.z), as_f32(pp.w)}, a.eps);
     // exclusive prefix of the chunk counts (lane l: chunks 4 l .. 4 l + 3)
@@ -347,13 +345,14 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
     if (has_cold) ctl_positions(sh, cnt4, chunk, 0);
     __builtin_amdgcn_wave_barrier();
     if (has_cold) ctl_gather_table(sh, rsrc(T->act_slots, (uint32_t)kTokChunks * chunk * 4), T->n_records, 0, total);
-    // the next layer's predictor row: z = D q, q = bf16(fp16(x r w'))
-    // (pred_d_role's arithmetic); stored with the phase's other outputs
+    // a quarter of the next layer's predictor row: z = D q, q =
+    // bf16(fp16(x r w')) (pred_d_role's arithmetic and partial sums);
+    // stored with the phase's other outputs
     float zrow = 0.0f;
     if (pred) {
       float acc = 0.0f;
 #pragma unroll
-      for (int it = 0; it < 8; ++it) {
+      for (int it = 0; it < 2; ++it) {
         const u32x4 xv = reinterpret_cast<const u32x4*>(sh.xq)[l + 64 * it];
         const u32x4 wv = reinterpret_cast<const u32x4*>(sh.wq)[l + 64 * it];
         const u32x4 dv = reinterpret_cast<const u32x4*>(sh.pd)[l + 64 * it];
@@ -387,9 +386,10 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
           CS[0][2 * q + 1] = half_bits_to_float(bld2(rrec, ro + kOffScales + 2 * (32 * q + 16 + g0)));
         }
         CG[0] = as_f32(bld4(rcgb, vv ? 4 * (uint32_t)sl : kNoOff));
+        CD[0] = half_bits_to_float(bld2(rrec, ro + kOffScales + 2 * (2 * kGroups + (l & (kGroups - 1)))));
       }
       const int c = i >= kCtlCold ? 0 : i;
-      float hv = 0.0f;
+      float hv = 0.0f, hs = 0.0f;
 #pragma unroll
       for (int cc = 0; cc < kCtlCold; ++cc) {
         if (cc != c) continue;
@@ -413,11 +413,14 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
         const float gv = r * wave_sum(pg[0] * CS[cc][0] + pg[1] * CS[cc][1]) + CG[cc];
         const float uv = r * wave_sum(pu[0] * CS[cc][2] + pu[1] * CS[cc][3]);
         hv = gated_act(gv, uv, a.relu, a.both);
+        hs = hv * CD[cc];
       }
       if (l == 0) sh.hc_out[k] = hv;
+      if (l < kGroups) sh.hcs_out[l][k] = hs;
     }
     bar();   // B2: the workers' activations are in LDS
-    if (pred && l == 0) cst4(rsrc(a.z + (size_t)(L + 1) * kTokMaxRank, kTokMaxRank * 4), 4 * (uint32_t)g, as_u32(zrow));
+    if (pred && l == 0)
+      cst4(rsrc(a.z + (size_t)(L + 1) * 4 * kTokMaxRank, 4 * kTokMaxRank * 4), 4 * (uint32_t)g, as_u32(zrow));
     if (T) {
       const int k = g * kWorkers * NPW + l;
       if (l < kWorkers * NPW && k < T->n_hot)
@@ -425,6 +428,18 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
       if (has_cold && l < sh.lst_cnt)
         cst4(rsrc(a.hc + (size_t)L * kTokChunks * kTokMaxChunk, kTokChunks * kTokMaxChunk * 4),
              4 * (uint32_t)(g * chunk + l), as_u32(sh.hc_out[l]));
+      // activation x down scale of every row group, at the items' list
+      // positions (those the workers gather): lane l takes group l & 31 of
+      // item k0 + (l >> 5)
+      if (has_cold) {
+        const int p0 = sh.pfx[g], cnt = sh.lst_cnt;
+        const rsrc_t rs = rsrc(a.hcs + (size_t)L * kGroups * kBatch, kGroups * kBatch * 4);
+        for (int k0 = 0; k0 < cnt && p0 + k0 < kBatch; k0 += 2) {
+          const int k = k0 + (l >> 5), gi = l & (kGroups - 1);
+          if (k < cnt && p0 + k < kBatch)
+            cst4(rs, 4 * (uint32_t)(gi * kBatch + p0 + k), as_u32(sh.hcs_out[gi][k]));
+        }
+      }
     }
     tok_arrive(a.sync, 0, g, (uint32_t)(L + 2));
 
@@ -442,8 +457,11 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
       const uint16_t nb = bld2(rsrc(N ? N->norm_w : nullptr, N ? kH * 2 : 0u), l < kRows ? 2 * (uint32_t)(j0 + l) : kNoOff);
       res_v = half_bits_to_float(rb);
       nwv = half_bits_to_float(nb);
-      if (has_cold)
-        ctl_gather_hc(sh, rsrc(a.hc + (size_t)L * kTokChunks * kTokMaxChunk, kTokChunks * kTokMaxChunk * 4), 0, total);
+      if (has_cold) {   // the batch's activations x the tile group's down scale, in list order
+        const rsrc_t rg = rsrc(a.hcs + ((size_t)L * kGroups + j0 / kGroup) * kBatch, kBatch * 4);
+#pragma unroll
+        for (int it = 0; it < 4; ++it) bld16_lds(rg, sh.it_hcs + 256 * it, 16 * (l + 64 * it));
+      }
     }
     int ch_n = 0, nn = -1;
     float zl = 0.0f;
@@ -453,7 +471,8 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
       ch_n = N->sel_chunk;
       const int rank = N->rank;
       nn = (l < ch_n && g * ch_n + l < N->inter) ? g * ch_n + l : -1;
-      zl = as_f32(bld4(rsrc(a.z + (size_t)(L + 1) * kTokMaxRank, (uint32_t)rank * 4), 4 * (uint32_t)l));
+      const u32x4 zp = bld16(rsrc(a.z + (size_t)(L + 1) * 4 * kTokMaxRank, (uint32_t)rank * 16), 16 * (uint32_t)l);
+      zl = (as_f32(zp.x) + as_f32(zp.y)) + (as_f32(zp.z) + as_f32(zp.w));
       const rsrc_t ru = rsrc(N->pu_w, (uint32_t)N->inter * rank * 2);
 #pragma unroll
       for (int m = 0; m < 8; ++m)
@@ -617,9 +636,9 @@ __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
   u32x4 RQ[kColdR][4];        // cold records of the chunk: gate and up halves,
   float RS[kColdR][4];        //   their group scales,
   float RG[kColdR];           //   gate bias
-  int RSL[kColdR];            //   and slots
-  u32x2v NB[kGat];            // gather items: down nibbles of the tile's rows,
-  float NS[kGat];             //   their scale
+  int RSL[kColdR];            //   slots,
+  float RD[kColdR];           //   and the down scale of row group l (lanes < kGroups)
+  u32x2v NB[kGat];            // gather items: down nibbles of the tile's rows
   // neurons [j0h, j1h) of the gate/up rows (and, with the first, the scales)
   auto load_hot = [&](int L, int j0h, int j1h) {          // L may be n: reads zero
     const bool v = L < n;
@@ -691,6 +710,7 @@ __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
         RS[i][2 * q + 1] = half_bits_to_float(bld2(rr, ro + kOffScales + 2 * (32 * q + 16 + g0)));
       }
       RG[i] = as_f32(bld4(rb, ok ? 4 * (uint32_t)sl : kNoOff));
+      RD[i] = half_bits_to_float(bld2(rr, ro + kOffScales + 2 * (2 * kGroups + (l & (kGroups - 1)))));
     }
   };
   // down nibbles of the first gather batch of layer L (the table in LDS)
@@ -703,7 +723,6 @@ __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
       const int sl = sh.it_slot[wi * kWave + l + kWorkers * kWave * m];
       const uint32_t ro = sl >= 0 ? (uint32_t)sl * kRecBytes : kNoOff;
       NB[m] = bld8(rr, ro + kOffDown + j0 / 2);
-      NS[m] = half_bits_to_float(bld2(rr, ro + kOffScales + 2 * (64 + j0 / kGroup)));
     }
   };
 
@@ -770,7 +789,9 @@ __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
           }
           const float gv = r * wave_sum(pg[0] * RS[i][0] + pg[1] * RS[i][1]) + RG[i];
           const float uv = r * wave_sum(pu[0] * RS[i][2] + pu[1] * RS[i][3]);
-          if (l == 0) sh.hc_out[wi + kWorkers * i] = gated_act(gv, uv, a.relu, a.both);
+          const float hv = gated_act(gv, uv, a.relu, a.both);
+          if (l == 0) sh.hc_out[wi + kWorkers * i] = hv;
+          if (l < kGroups) sh.hcs_out[l][wi + kWorkers * i] = hv * RD[i];
         }
       }
     }
@@ -822,7 +843,7 @@ __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
         for (int m = 0; m < kGat; ++m) {
           const int i = wi * kWave + l + kWorkers * kWave * m;
           if (sh.it_slot[i] >= 0) {
-            const float hs = sh.it_hc[i] * NS[m];
+            const float hs = sh.it_hcs[i];
             f16x2 tq[4];
             int4x8_to_f16x2x4(NB[m].x, tq);
 #pragma unroll
