@@ -197,7 +197,8 @@ constexpr int kTokMaxRank = 64;
 constexpr int kTokMaxHot = 4096;           // h staged in LDS; also the per-layer h slice
 constexpr int kTokBatch = 896;             // gather items the worker waves take per layer (list order)
 constexpr int kTokSyncWords = 2048 + 192;
-constexpr int kTokSyncErr = 2048 + 128;       // nonzero: a wait ran past its bound
+constexpr int kTokSyncErr = 2048 + 128;       // epoch base + 1 of a launch whose wait ran past its bound
+constexpr int kTokSyncGoD = 64 * 8;           // the D phase's release flag of XCD 0
 
 // One layer as the token kernel reads it (a device-resident table).
 struct TokLayer {
@@ -251,8 +252,6 @@ struct TokArgs {
   int relu, both;
 };
 
-__global__ void k_tok_prep(const uint16_t* x, const uint16_t* w, uint16_t* xw, float* ssq,
-                           uint32_t* sync);
 int tok_launch(const TokArgs& a, int npw, hipStream_t st);
 int tok_resident(int npw, int* resident);
 

@@ -314,19 +314,10 @@ static TokArgs tok_args(const oi2_stack* s, const uint16_t* x_in, uint16_t* x_ou
   return a;
 }
 
-// Layer 0's x * w and sum-of-squares partials from x_in, and a cleared
-// signal area: the launch before each persistent token kernel.
-static int launch_tok_prep(oi2_stack* s, const uint16_t* x_in, hipStream_t st) {
-  hipLaunchKernelGGL(k_tok_prep, dim3(1), dim3(kThreads), 0, st, x_in, s->layers[0].l.norm_w, s->tok_xw,
-                     s->tok_ssq, s->tok_sync);
-  OI2_CHECK_LAUNCH();
-  return OI2_OK;
-}
-
-// The token as one persistent launch.
+// The token as one persistent launch (it computes layer 0's x * w and
+// sum-of-squares partials itself, and its signal words need no clearing).
 static int stack_launch_tok(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, hipStream_t st) {
-  const int rc = launch_tok_prep(s, x_in, st);
-  return rc ? rc : tok_launch(tok_args(s, x_in, x_out), s->tok_npw, st);
+  return tok_launch(tok_args(s, x_in, x_out), s->tok_npw, st);
 }
 
 // The two-launch-per-layer sequence (or the staged one).
@@ -472,6 +463,8 @@ static int tok_setup(oi2_stack* s) {
   if (e == hipSuccess) e = hipMemset(s->tok_sel_counts, 0, (size_t)n * kTokChunks * 4);
   // h slices past n_hot are never written and must read as zero
   if (e == hipSuccess) e = hipMemset(s->tok_h, 0, (size_t)n * kTokMaxHot * 4);
+  // the signal words start at zero once; launches count on from there
+  if (e == hipSuccess) e = hipMemset(s->tok_sync, 0, (size_t)kTokSyncWords * 4);
   std::vector<TokLayer> tab(n);
   for (int L = 0; L < n && e == hipSuccess; ++L) {
     const StackLayer& SL = s->layers[L];
@@ -882,9 +875,14 @@ int oi2_stack_status(oi2_stack* s, void* stream) {
   OI2_CHECK_ARG(s, "null stack");
   OI2_CHECK_HIP(hipStreamSynchronize((hipStream_t)stream));
   if (!use_tok(s)) return OI2_OK;
-  uint32_t err = 0;
+  // the error word holds (epoch base + 1) of a launch whose wait ran past its
+  // bound; the last launch's base is the D release flag's value minus the
+  // epochs of one launch (n_layers + 1)
+  uint32_t err = 0, go = 0;
   OI2_CHECK_HIP(hipMemcpy(&err, s->tok_sync + kTokSyncErr, 4, hipMemcpyDeviceToHost));
-  if (err) {
+  OI2_CHECK_HIP(hipMemcpy(&go, s->tok_sync + kTokSyncGoD, 4, hipMemcpyDeviceToHost));
+  if (err != 0 && err == go - (uint32_t)(s->n_layers + 1) + 1u) {
+    OI2_CHECK_HIP(hipMemset(s->tok_sync + kTokSyncErr, 0, 4));
     set_error("persistent token kernel: a device-wide wait ran past its bound");
     return OI2_EHIP;
   }
@@ -908,8 +906,7 @@ int oi2_stack_profile_token(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out,
   if (rc == OI2_OK) rc = stack_launch_tok(s, x_in, x_out, st);
   const TokArgs a = tok_args(s, x_in, x_out);
   for (int r = 0; rc == OI2_OK && r < reps; ++r) {
-    rc = launch_tok_prep(s, x_in, st);
-    if (rc == OI2_OK && hipEventRecord(ev[2 * r], st) != hipSuccess) rc = OI2_EHIP;
+    if (hipEventRecord(ev[2 * r], st) != hipSuccess) rc = OI2_EHIP;
     if (rc == OI2_OK) rc = tok_launch(a, s->tok_npw, st);
     if (rc == OI2_OK && hipEventRecord(ev[2 * r + 1], st) != hipSuccess) rc = OI2_EHIP;
   }

@@ -55,6 +55,7 @@ namespace {
 constexpr int kPerXcd = kTokGroups / 8;
 constexpr uint32_t kSpinLimit = 1u << 20;
 constexpr int kSyncGo = 0, kSyncXcd = 1024, kSyncAll = 2048, kSyncErr = kTokSyncErr;
+static_assert(kTokSyncGoD == kSyncGo + 64 * 8, "the host reads the D release flag of XCD 0");
 constexpr int kSc1 = 16;                       // cache-policy operand: agent-coherent access
 constexpr int kWorkers = kTokThreads / kWave - 1;
 constexpr int kColdR = 1;                      // cold records per worker (items wi + 7 i)
@@ -152,7 +153,13 @@ __device__ __forceinline__ void wait_vm() {
   __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0) expcnt(7) lgkmcnt(15)
 }
 
-// Control wave: end of phase r (0 U, 1 D) for group g, epoch e.
+// Signal epochs count on across launches, so the signal words are never
+// cleared: a launch's epoch e of a phase is E = base + e, base being the D
+// release flag's value when the launch starts (every group reads it before
+// any D release of the launch can happen; the launch leaves base + n + 1).
+// Counter and flag comparisons are modulo 2^32.
+
+// Control wave: end of phase r (0 U, 1 D) for group g, epoch E.
 __device__ __forceinline__ void tok_arrive(uint32_t* sync, int r, int g, uint32_t e) {
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
   if (lane_id() == 0) {
@@ -167,18 +174,25 @@ __device__ __forceinline__ void tok_arrive(uint32_t* sync, int r, int g, uint32_
   }
 }
 
-// Control wave: wait until every group has ended epoch e of phase r.
-__device__ __forceinline__ void tok_wait(uint32_t* sync, int r, int g, uint32_t e) {
+// Control wave: wait until every group has ended epoch E of phase r.  Past
+// kSpinLimit polls it records the launch (base + 1) in the error word and
+// goes on; so do the waits of other groups once they see that record.
+__device__ __forceinline__ void tok_wait(uint32_t* sync, int r, int g, uint32_t e, uint32_t base) {
   const uint32_t* go = sync + kSyncGo + 64 * (8 * r + (g & 7));
   uint32_t n = 0;
-  while (cld(go) < e) {
+  while ((int32_t)(cld(go) - e) < 0) {
     __builtin_amdgcn_s_sleep(1);
     if (++n >= kSpinLimit) {
-      cst(sync + kSyncErr, 1u);
+      cst(sync + kSyncErr, base + 1u);
       break;
     }
-    if ((n & 63) == 0 && cld(sync + kSyncErr)) break;
+    if ((n & 63) == 0 && cld(sync + kSyncErr) == base + 1u) break;
   }
+}
+
+// The epoch base of this launch (see above).
+__device__ __forceinline__ uint32_t tok_base(const uint32_t* sync, int g) {
+  return cld(sync + kSyncGo + 64 * (8 + (g & 7)));
 }
 
 struct alignas(16) TokShared {
@@ -252,11 +266,12 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
   const int j0 = tile * kRows;
   const int g0 = l >> 2;
   CLayer* LT = layer_table(a);
+  const uint32_t base = tok_base(a.sync, g);
   for (int L = -1; L < n; ++L) {
     CLayer* T = L >= 0 ? LT + L : nullptr;
     CLayer* N = L + 1 < n ? LT + L + 1 : nullptr;
     // ================= U phase of layer L (L = -1: only layer 0's predictor)
-    if (L >= 0) tok_wait(a.sync, 1, g, (uint32_t)(L + 1));
+    if (L >= 0) tok_wait(a.sync, 1, g, base + (uint32_t)(L + 1), base);
     const bool has_cold = T && T->n_records > 0 && T->act_counts;
     const int chunk = has_cold ? T->act_chunk : 0;
     // the next layer's predictor: group g sums quarter g & 3 of row g >> 2
@@ -268,7 +283,28 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
 #pragma unroll
       for (int it = 0; it < 8; ++it) bld16_lds(rx, sh.nat + 256 * it, 16 * (l + 64 * it));
     }
-    const u32x4 pp = bld16(rsrc(a.ssq + (size_t)(L < 0 ? 0 : L) * kTokGroups, kTokGroups * 4), 16 * l);
+    // the layer's 256 sum-of-squares partials, this lane's four (layer 0's
+    // come from x_in itself, k_prep's arithmetic: partial t sums x[16 t ..
+    // 16 t + 16))
+    u32x4 pp;
+    if (L >= 0) {
+      pp = bld16(rsrc(a.ssq + (size_t)L * kTokGroups, kTokGroups * 4), 16 * l);
+    } else {
+      const rsrc_t rx0 = rsrc(a.x_in, kH * 2);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const u32x4 v0 = bld16(rx0, 16 * (uint32_t)(8 * l + 2 * q)), v1 = bld16(rx0, 16 * (uint32_t)(8 * l + 2 * q + 1));
+        float v[16];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          v[2 * d] = half_lo(v0[d]);
+          v[2 * d + 1] = half_hi(v0[d]);
+          v[8 + 2 * d] = half_lo(v1[d]);
+          v[8 + 2 * d + 1] = half_hi(v1[d]);
+        }
+        pp[q] = as_u32(ssq16(v));
+      }
+    }
     const rsrc_t rcnt = rsrc(has_cold ? T->act_counts : nullptr, has_cold ? kTokChunks * 4 : 0u);
     int cnt4[4];
 #pragma unroll
@@ -441,10 +477,10 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
         }
       }
     }
-    tok_arrive(a.sync, 0, g, (uint32_t)(L + 2));
+    tok_arrive(a.sync, 0, g, base + (uint32_t)(L + 2));
 
     // ================= D phase of layer L (L = -1: only layer 0's selection)
-    tok_wait(a.sync, 0, g, (uint32_t)(L + 2));
+    tok_wait(a.sync, 0, g, base + (uint32_t)(L + 2), base);
     const bool psel = N && N->pd_w;                      // the next layer's list is predicted
     const bool pstat = N && !N->pd_w && N->n_records > 0 && N->act_counts;   // or fixed
     float res_v = 0.0f, nwv = 1.0f;
@@ -462,6 +498,9 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
 #pragma unroll
         for (int it = 0; it < 4; ++it) bld16_lds(rg, sh.it_hcs + 256 * it, 16 * (l + 64 * it));
       }
+    } else if (N) {   // layer 0's x and norm weight of the tile
+      res_v = half_bits_to_float(bld2(rsrc(a.x_in, kH * 2), l < kRows ? 2 * (uint32_t)(j0 + l) : kNoOff));
+      nwv = half_bits_to_float(bld2(rsrc(N->norm_w, kH * 2), l < kRows ? 2 * (uint32_t)(j0 + l) : kNoOff));
     }
     int ch_n = 0, nn = -1;
     float zl = 0.0f;
@@ -605,8 +644,16 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         if (l == 0) cst4(rsrc(a.ssq + (size_t)(L + 1) * kTokGroups, kTokGroups * 4), 4 * (uint32_t)tile, as_u32(ssq16(sh.out)));
       }
+    } else if (N) {   // layer 0's x * w and sum-of-squares partial of the tile (k_prep's arithmetic)
+      if (l < kRows) {
+        sh.out[l] = res_v;
+        cst2(rsrc(a.xw, kH * 2), 2 * (uint32_t)(j0 + l), float_to_half_bits(res_v * nwv));
+      }
+      __builtin_amdgcn_wave_barrier();
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      if (l == 0) cst4(rsrc(a.ssq, kTokGroups * 4), 4 * (uint32_t)tile, as_u32(ssq16(sh.out)));
     }
-    tok_arrive(a.sync, 1, g, (uint32_t)(L + 2));
+    tok_arrive(a.sync, 1, g, base + (uint32_t)(L + 2));
   }
 }
 
@@ -883,20 +930,6 @@ __global__ __launch_bounds__(kTokThreads) __attribute__((amdgpu_waves_per_eu(2))
 }
 
 }  // namespace
-
-// x -> x * w of layer 0 and its 256 sum-of-squares partials (k_prep's
-// arithmetic), and a zeroed signal area for the token kernel that follows.
-__global__ __launch_bounds__(kThreads) void k_tok_prep(const uint16_t* x, const uint16_t* w, uint16_t* xw,
-                                                       float* ssq, uint32_t* sync) {
-  const int t = threadIdx.x;
-  float v[16], wv[16];
-  load_h16(x, 16 * t, v);
-  ssq[t] = ssq16(v);
-  load_h16(w, 16 * t, wv);
-#pragma unroll
-  for (int e = 0; e < 16; ++e) xw[16 * t + e] = float_to_half_bits(v[e] * wv[e]);
-  for (int i = t; i < kTokSyncWords; i += kThreads) sync[i] = 0u;
-}
 
 int tok_launch(const TokArgs& a, int npw, hipStream_t st) {
   if (npw == 2)
