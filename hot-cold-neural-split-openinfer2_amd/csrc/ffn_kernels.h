@@ -247,7 +247,8 @@ struct TokArgs {
                             // quarter q of row r at 4 r + q
   float* hcs;               // (n_layers, kGroups, kTokBatch) cold activation x down scale of each
                             // row group, list positions < kTokBatch
-  uint32_t* sync;           // kTokSyncWords, zero at launch
+  uint32_t* sync;           // kTokSyncWords, zero at allocation
+  uint32_t spin;            // poll bound of every device-wide wait
   float eps, thr;
   int relu, both;
 };

@@ -70,6 +70,7 @@ struct oi2_stack {
   int tok_npw = 0, tok_chunk = 0;
   oi2::TokLayer* tok_layers = nullptr;
   uint32_t* tok_sync = nullptr;
+  uint32_t tok_spin = 1u << 20;       // poll bound of the kernel's device-wide waits
   uint16_t* tok_xw = nullptr;    // one slice per layer of everything the launch writes
   float* tok_ssq = nullptr;
   float* tok_h = nullptr;
@@ -307,6 +308,7 @@ static TokArgs tok_args(const oi2_stack* s, const uint16_t* x_in, uint16_t* x_ou
   a.z = s->tok_z;
   a.hcs = s->tok_hcs;
   a.sync = s->tok_sync;
+  a.spin = s->tok_spin;
   a.eps = s->eps;
   a.thr = s->thr;
   a.relu = s->relu;
@@ -870,6 +872,15 @@ int oi2_stack_set_token_kernel(oi2_stack* s, int32_t enable) {
 
 int32_t oi2_stack_token_kernel(const oi2_stack* s) { return (s && use_tok(s)) ? 1 : 0; }
 
+int oi2_stack_set_wait_bound(oi2_stack* s, int32_t polls) {
+  clear_error();
+  OI2_CHECK_ARG(s, "null stack");
+  OI2_CHECK_ARG(polls >= 1 && polls <= (1 << 24), "wait bound %d out of range 1 .. %d", polls, 1 << 24);
+  s->tok_spin = (uint32_t)polls;
+  drop_graphs(s);   // the bound is a kernel argument
+  return OI2_OK;
+}
+
 int oi2_stack_status(oi2_stack* s, void* stream) {
   clear_error();
   OI2_CHECK_ARG(s, "null stack");
@@ -882,7 +893,9 @@ int oi2_stack_status(oi2_stack* s, void* stream) {
   OI2_CHECK_HIP(hipMemcpy(&err, s->tok_sync + kTokSyncErr, 4, hipMemcpyDeviceToHost));
   OI2_CHECK_HIP(hipMemcpy(&go, s->tok_sync + kTokSyncGoD, 4, hipMemcpyDeviceToHost));
   if (err != 0 && err == go - (uint32_t)(s->n_layers + 1) + 1u) {
-    OI2_CHECK_HIP(hipMemset(s->tok_sync + kTokSyncErr, 0, 4));
+    // a wait that gave up lets its group run ahead of an epoch, so the
+    // counters may no longer line up with the epochs: start them over
+    OI2_CHECK_HIP(hipMemset(s->tok_sync, 0, (size_t)kTokSyncWords * 4));
     set_error("persistent token kernel: a device-wide wait ran past its bound");
     return OI2_EHIP;
   }

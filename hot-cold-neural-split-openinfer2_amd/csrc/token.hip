@@ -42,9 +42,9 @@
 // issued inside the launch: on this part those stall every in-flight weight
 // load of the XCD.
 //
-// Every wait is bounded: past kSpinLimit polls a group sets the error word and
-// goes on (the token is then garbage and the host reports it), so every wave
-// reaches the end of the kernel.
+// Every wait is bounded: past a host-set number of polls a group sets the
+// error word and goes on (the token is then garbage and the host reports it,
+// clearing the signal words), so every wave reaches the end of the kernel.
 #include "capi_util.h"
 #include "decode_util.h"
 #include "ffn_kernels.h"
@@ -53,7 +53,6 @@ namespace oi2 {
 namespace {
 
 constexpr int kPerXcd = kTokGroups / 8;
-constexpr uint32_t kSpinLimit = 1u << 20;
 constexpr int kSyncGo = 0, kSyncXcd = 1024, kSyncAll = 2048, kSyncErr = kTokSyncErr;
 static_assert(kTokSyncGoD == kSyncGo + 64 * 8, "the host reads the D release flag of XCD 0");
 constexpr int kSc1 = 16;                       // cache-policy operand: agent-coherent access
@@ -175,14 +174,14 @@ __device__ __forceinline__ void tok_arrive(uint32_t* sync, int r, int g, uint32_
 }
 
 // Control wave: wait until every group has ended epoch E of phase r.  Past
-// kSpinLimit polls it records the launch (base + 1) in the error word and
-// goes on; so do the waits of other groups once they see that record.
-__device__ __forceinline__ void tok_wait(uint32_t* sync, int r, int g, uint32_t e, uint32_t base) {
+// `spin` polls it records the launch (base + 1) in the error word and goes
+// on; so do the waits of other groups once they see that record.
+__device__ __forceinline__ void tok_wait(uint32_t* sync, int r, int g, uint32_t e, uint32_t base, uint32_t spin) {
   const uint32_t* go = sync + kSyncGo + 64 * (8 * r + (g & 7));
   uint32_t n = 0;
   while ((int32_t)(cld(go) - e) < 0) {
     __builtin_amdgcn_s_sleep(1);
-    if (++n >= kSpinLimit) {
+    if (++n >= spin) {
       cst(sync + kSyncErr, base + 1u);
       break;
     }
@@ -271,7 +270,7 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
     CLayer* T = L >= 0 ? LT + L : nullptr;
     CLayer* N = L + 1 < n ? LT + L + 1 : nullptr;
     // ================= U phase of layer L (L = -1: only layer 0's predictor)
-    if (L >= 0) tok_wait(a.sync, 1, g, base + (uint32_t)(L + 1), base);
+    if (L >= 0) tok_wait(a.sync, 1, g, base + (uint32_t)(L + 1), base, a.spin);
     const bool has_cold = T && T->n_records > 0 && T->act_counts;
     const int chunk = has_cold ? T->act_chunk : 0;
     // the next layer's predictor: group g sums quarter g & 3 of row g >> 2
@@ -480,7 +479,7 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
     tok_arrive(a.sync, 0, g, base + (uint32_t)(L + 2));
 
     // ================= D phase of layer L (L = -1: only layer 0's selection)
-    tok_wait(a.sync, 0, g, base + (uint32_t)(L + 2), base);
+    tok_wait(a.sync, 0, g, base + (uint32_t)(L + 2), base, a.spin);
     const bool psel = N && N->pd_w;                      // the next layer's list is predicted
     const bool pstat = N && !N->pd_w && N->n_records > 0 && N->act_counts;   // or fixed
     float res_v = 0.0f, nwv = 1.0f;

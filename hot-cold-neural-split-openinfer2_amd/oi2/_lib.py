@@ -82,6 +82,7 @@ _SIGS = {
     "oi2_stack_set_token_kernel": (c_int32, [c_void_p, c_int32]),
     "oi2_stack_token_kernel": (c_int32, [c_void_p]),
     "oi2_stack_status": (c_int32, [c_void_p, c_void_p]),
+    "oi2_stack_set_wait_bound": (c_int32, [c_void_p, c_int32]),
     "oi2_stack_profile_token": (c_int32, [c_void_p, c_void_p, c_void_p, c_int32, POINTER(c_float),
                                           c_void_p]),
     "oi2_stack_destroy": (c_int32, [c_void_p]),

@@ -75,6 +75,12 @@ class DecodeStack:
         s = stream.cuda_stream if stream is not None else _lib.stream_handle(dev)
         _lib.check(_lib.lib().oi2_stack_status(self._h, s or None))
 
+    def set_wait_bound(self, polls: int):
+        """Bound, in polls, of the persistent kernel's device-wide waits
+        (default 1 << 20).  Past it a wait gives up and status() raises for
+        that token; meant for tests of that path."""
+        _lib.check(_lib.lib().oi2_stack_set_wait_bound(self._h, int(polls)))
+
     def profile_token(self, x_in: torch.Tensor, x_out: torch.Tensor, stream=None, reps: int = 16):
         """Mean microseconds of the persistent token kernel alone."""
         us = ctypes.c_float()

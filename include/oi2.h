@@ -230,9 +230,10 @@ int oi2_stack_trace(oi2_stack* s, uint16_t* xs, int32_t* counts, int32_t* slots,
 int oi2_stack_selection_layout(const oi2_stack* s, int32_t* n_chunks, int32_t* chunk);
 /* The whole token as one persistent kernel (default on where supported):
  * every layer's FFN and the lookahead predictor run in a single launch of
- * 512 co-resident workgroups that hand the phases over through device-wide
- * counters, each loading its next layer's weights before it waits (the same
- * layer loop, engine.py:421-438, with no launch boundary between layers).
+ * 256 co-resident workgroups (one per CU) that hand the phases over through
+ * device-wide counters, each loading its next layer's weights before it waits
+ * (the same layer loop, engine.py:421-438, with no launch boundary between
+ * layers).
  * Needs HBM-resident records, bf16 predictors of rank <= 64, n_hot <= 4096
  * and inter <= 16384, and no staging; returns OI2_EUNSUPPORTED otherwise.
  * 0 selects the two-launch-per-layer sequence.  Drops captured graphs. */
@@ -243,9 +244,15 @@ int32_t oi2_stack_token_kernel(const oi2_stack* s);
  * persistent-kernel token ran past its bound (that token's output is then
  * invalid), else OI2_OK. */
 int oi2_stack_status(oi2_stack* s, void* stream);
+/* No counterpart in the reference: the bound, in polls, of every device-wide
+ * wait of the persistent kernel (default 1 << 20; 1 .. 1 << 24).  A wait past
+ * it gives up, so the token is invalid and oi2_stack_status reports it; the
+ * kernel still runs to its end and the next token is unaffected.  For tests
+ * of that failure path.  Drops captured graphs. */
+int oi2_stack_set_wait_bound(oi2_stack* s, int32_t polls);
 /* Mean microseconds of the persistent token kernel alone: decodes x_in once,
- * then `reps` times the token's two launches, timing the persistent kernel
- * between hipEvents on `stream`; leaves the state of decoding x_in. */
+ * then `reps` more launches timed between hipEvents on `stream`; leaves the
+ * state of decoding x_in. */
 int oi2_stack_profile_token(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, int32_t reps,
                             float* token_us, void* stream);
 int oi2_stack_destroy(oi2_stack* s);

@@ -54,6 +54,32 @@ def test_token_kernel_selected_by_default(stack4):
         st.set_token_kernel(True)
 
 
+def test_token_kernel_wait_past_bound_is_reported_and_recovers(stack4):
+    """A device-wide wait past its bound (forced from the host: a bound of one
+    poll) makes status() raise for that token; the kernel still runs to its
+    end, and the next token with the default bound equals a clean decode."""
+    dev, g, layers, st, thr = stack4
+    assert st.token_kernel
+    stream = torch.cuda.Stream(device=dev)
+    x_in = torch.randn(H, generator=g, device=dev).half()
+    ref, bad, out = (torch.empty_like(x_in) for _ in range(3))
+    with torch.cuda.stream(stream):
+        st.decode(x_in, ref, stream)
+    st.status(stream)
+    st.set_wait_bound(1)
+    try:
+        with torch.cuda.stream(stream):
+            st.decode(x_in, bad, stream)
+        with pytest.raises(oi2.OI2Error, match="past its bound"):
+            st.status(stream)
+    finally:
+        st.set_wait_bound(1 << 20)
+    with torch.cuda.stream(stream):
+        st.decode(x_in, out, stream)
+    st.status(stream)
+    assert torch.equal(out, ref)
+
+
 @pytest.mark.parametrize("token", [True, False], ids=["token_kernel", "two_launches"])
 def test_stack_layers_match_oracle(stack4, token):
     dev, g, layers, st, thr = stack4
