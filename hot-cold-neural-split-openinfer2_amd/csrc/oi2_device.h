@@ -113,6 +113,26 @@ __device__ __forceinline__ float wave_sum(float v) {
   return readlane_f(v, 63);
 }
 
+// N wave_sum reductions at once, one DPP step at a time for all N values, so
+// the steps of different values overlap instead of waiting on each other.
+// Each value goes through exactly wave_sum's additions; its total ends in
+// lane 63.
+template <int N>
+__device__ __forceinline__ void wave_sums_to_last(float (&v)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_f<0xB1>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_f<0x4E>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_f<0x141>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_f<0x140>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_f<0x142, 0xA>(v[i]);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] += dpp_f<0x143, 0xC>(v[i]);
+}
+
 __device__ __forceinline__ int lane_id() { return (int)(threadIdx.x & (kWave - 1)); }
 
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }

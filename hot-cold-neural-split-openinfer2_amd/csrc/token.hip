@@ -801,10 +801,17 @@ __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
               uu[j] = dot2(fp8x2_to_f16x2(WU[j][4 + it][d], true), xp[2 * d + 1], uu[j]);
             }
         }
+        float gu[2 * NPW];
+#pragma unroll
+        for (int j = 0; j < NPW; ++j) {
+          gu[j] = gg[j];
+          gu[NPW + j] = uu[j];
+        }
+        wave_sums_to_last(gu);
         float hg = 0.0f, hu = 0.0f;
 #pragma unroll
         for (int j = 0; j < NPW; ++j) {
-          const float sg = wave_sum(gg[j]), su = wave_sum(uu[j]);
+          const float sg = readlane_f(gu[j], kWave - 1), su = readlane_f(gu[NPW + j], kWave - 1);
           if (l == j) {
             hg = sg;
             hu = su;
@@ -833,8 +840,10 @@ __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
               for (int k = 0; k < 4; ++k) pu[it] = dot2(tq[k], as_f16x2(xq[k]), pu[it]);
             }
           }
-          const float gv = r * wave_sum(pg[0] * RS[i][0] + pg[1] * RS[i][1]) + RG[i];
-          const float uv = r * wave_sum(pu[0] * RS[i][2] + pu[1] * RS[i][3]);
+          float su[2] = {pg[0] * RS[i][0] + pg[1] * RS[i][1], pu[0] * RS[i][2] + pu[1] * RS[i][3]};
+          wave_sums_to_last(su);
+          const float gv = r * readlane_f(su[0], kWave - 1) + RG[i];
+          const float uv = r * readlane_f(su[1], kWave - 1);
           const float hv = gated_act(gv, uv, a.relu, a.both);
           if (l == 0) sh.hc_out[wi + kWorkers * i] = hv;
           if (l < kGroups) sh.hcs_out[l][wi + kWorkers * i] = hv * RD[i];
@@ -878,10 +887,11 @@ __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
             acc[rr] = fmaf(hi.y, hv[4 * d + 3], acc[rr]);
           }
       }
+      wave_sums_to_last(acc);
+      if (l == kWave - 1) {
 #pragma unroll
-      for (int rr = 0; rr < 3; ++rr) {
-        const float sv = wave_sum(acc[rr]);
-        if (l == 0 && rr < rc) sh.yhot[rs + rr] = T->n_hot > 0 ? sv * dsc[rr] : 0.0f;
+        for (int rr = 0; rr < 3; ++rr)
+          if (rr < rc) sh.yhot[rs + rr] = T->n_hot > 0 ? acc[rr] * dsc[rr] : 0.0f;
       }
       // cold: this lane's items of the first gather batch x their 16 down nibbles
       if (has_cold) {
@@ -906,10 +916,10 @@ __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
           }
         }
       }
+      wave_sums_to_last(yc);
+      if (l == kWave - 1) {
 #pragma unroll
-      for (int e = 0; e < kRows; ++e) {
-        const float sv = wave_sum(yc[e]);
-        if (l == 0) sh.cpart[wi][e] = sv;
+        for (int e = 0; e < kRows; ++e) sh.cpart[wi][e] = yc[e];
       }
     }
     bar();   // D2
