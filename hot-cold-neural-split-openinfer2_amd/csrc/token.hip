@@ -238,15 +238,20 @@ __device__ __forceinline__ void ctl_positions(TokShared& sh, const int cnt4[4], 
   }
 }
 
-// Control: slots of the items of batch b.
-__device__ __forceinline__ void ctl_gather_table(TokShared& sh, rsrc_t rslots, int n_records, int b, int total) {
+// Control: slots of the items of batch b -- issued here, written into the
+// table by ctl_table_store once the wave has done other work meanwhile.
+__device__ __forceinline__ void ctl_table_load(const TokShared& sh, rsrc_t rslots, int b, int total,
+                                               int (&sl)[kCtlItems]) {
   const int l = lane_id();
-  int sl[kCtlItems];
 #pragma unroll
   for (int m = 0; m < kCtlItems; ++m) {
     const int i = l + kWave * m;
     sl[m] = (int)bld4(rslots, b * kBatch + i < total ? 4 * (uint32_t)sh.it_pos[i] : kNoOff);
   }
+}
+__device__ __forceinline__ void ctl_table_store(TokShared& sh, const int (&sl)[kCtlItems], int n_records, int b,
+                                                int total) {
+  const int l = lane_id();
 #pragma unroll
   for (int m = 0; m < kCtlItems; ++m) {
     const int i = l + kWave * m;
@@ -379,7 +384,9 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
     // the gather table of batch 0 (its slots; the cold activations come in D)
     if (has_cold) ctl_positions(sh, cnt4, chunk, 0);
     __builtin_amdgcn_wave_barrier();
-    if (has_cold) ctl_gather_table(sh, rsrc(T->act_slots, (uint32_t)kTokChunks * chunk * 4), T->n_records, 0, total);
+    int tsl[kCtlItems];
+    ctl_table_load(sh, rsrc(has_cold ? T->act_slots : nullptr, has_cold ? (uint32_t)kTokChunks * chunk * 4 : 0u), 0,
+                   has_cold ? total : 0, tsl);
     // a quarter of the next layer's predictor row: z = D q, q =
     // bf16(fp16(x r w')) (pred_d_role's arithmetic and partial sums);
     // stored with the phase's other outputs
@@ -453,7 +460,8 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
       if (l == 0) sh.hc_out[k] = hv;
       if (l < kGroups) sh.hcs_out[l][k] = hs;
     }
-    bar();   // B2: the workers' activations are in LDS
+    if (has_cold) ctl_table_store(sh, tsl, T->n_records, 0, total);
+    bar();   // B2: the workers' activations and the gather table are in LDS
     if (pred && l == 0)
       cst4(rsrc(a.z + (size_t)(L + 1) * 4 * kTokMaxRank, 4 * kTokMaxRank * 4), 4 * (uint32_t)g, as_u32(zrow));
     if (T) {
