@@ -22,8 +22,10 @@
 // control wave never has weight loads in flight ahead of the loads the
 // phase waits on, and the workers never wait on a cross-group input.
 // Worker loads, in issue order per layer: gather nibbles and half the next
-// gate/up rows (end of U), the next chunk's records and the other half (D1),
-// the next layer's first down row (end of D), its other down rows (B1).  Each
+// gate/up rows (end of U), the other half (D1a, once the phase's inputs are
+// in), the next chunk's records (D1b, once the control wave has computed the
+// next list, which overlaps the workers' down products), the next layer's
+// first down row (end of D), its other down rows (B1).  Each
 // phase's compute needs only loads older than the ones still streaming, and
 // the halves issued at B1 / D1 go out after the phase's cross-group inputs:
 // a CU's memory pipeline is in order, and a backlog of weight loads ahead of
@@ -537,7 +539,7 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
     wait_vm();
     // take the loaded values into plain registers now, before any store
     asm volatile("" : "+v"(res_v), "+v"(nwv));
-    __builtin_amdgcn_wave_barrier();
+    bar();   // D1a: h and the gather activations are in LDS (the workers start)
     // the next layer's logits in the fma order of the two-launch path,
     // threshold, LUT hot filter and ascending compaction
     if (psel) {
@@ -571,7 +573,7 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
     } else if (l == 0) {
       sh.lst_cnt = 0;
     }
-    bar();   // D1: h, the gather activations and the next chunk's list are in LDS
+    bar();   // D1b: the next chunk's list is in LDS
     // gather items past the first batch (long lists): this wave, a batch of
     // 64 at a time, while the workers run the first
     float ycc[kRows];
@@ -668,9 +670,9 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
 
 // Every worker load is unconditional (absent data reads as zero through an
 // empty or short descriptor) and issued in the same order each layer --
-// gather nibbles, next gate/up rows (end of U), next chunk's records (D1),
-// next down rows (end of D) -- so the compiler can wait for exactly the loads
-// a compute step needs and leave the younger ones streaming.
+// gather nibbles, next gate/up rows (end of U and D1a), next chunk's records
+// (D1b), next down rows (end of D) -- so the compiler can wait for exactly
+// the loads a compute step needs and leave the younger ones streaming.
 template <int NPW>
 __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
   const int l = lane_id();
@@ -862,8 +864,7 @@ __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
     load_nibbles(L);
     load_hot(L + 1, 0, 1);       // half the next gate/up rows now ...
     // ================= D phase
-    bar();   // D1: the control's inputs have landed
-    load_records(L + 1);
+    bar();   // D1a: the control's inputs have landed
     load_hot(L + 1, 1, NPW);     // ... the rest once the phase's inputs are in
     float yc[kRows];
 #pragma unroll
@@ -930,6 +931,8 @@ __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
         for (int e = 0; e < kRows; ++e) sh.cpart[wi][e] = yc[e];
       }
     }
+    bar();   // D1b: the next chunk's list (computed meanwhile) is in LDS
+    load_records(L + 1);
     bar();   // D2
     load_down(L + 1, 0, 1);      // the next layer's first down row (the rest at B1)
   }
