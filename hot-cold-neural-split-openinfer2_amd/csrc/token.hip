@@ -205,8 +205,6 @@ struct alignas(16) TokShared {
   uint32_t pu[8 * kWave * 4]; // predictor up rows of chunk g: 16-byte piece m of neuron l at 64 m + l
   float it_hcs[1024];         // gather items of the current batch: cold activation x down scale
                               // of the tile's row group (list order; 4 KB, one copy's reach),
-  int it_slot[kBatch];        //   record slot,
-  int it_pos[kBatch];         //   list position
   float hcs_out[kGroups][kTokMaxChunk];   // this group's items: activation x down scale, per row group
   int pfx[kTokChunks + 1];    // exclusive prefix of the list's chunk counts
   int lst_slot[kTokMaxChunk]; // chunk g of the next layer's list
@@ -227,39 +225,16 @@ static_assert(offsetof(TokShared, nat) % 16 == 0 && offsetof(TokShared, xq) % 16
               offsetof(TokShared, it_hcs) % 16 == 0,
               "LDS DMA targets and 16-byte reads are 16-byte aligned");
 
-// Items of the list: item i (0 <= i < total) is item i - pfx[c] of chunk c.
-// The control lane that owns chunks 4 l .. 4 l + 3 writes list positions of
-// the items of batch b into it_pos.
-__device__ __forceinline__ void ctl_positions(TokShared& sh, const int cnt4[4], int chunk, int b) {
-  const int l = lane_id();
-  const int lo = b * kBatch, hi = lo + kBatch;
-  for (int q = 0; q < 4; ++q) {
-    const int c = 4 * l + q;
-    const int first = sh.pfx[c];
-    for (int k = max(0, lo - first); k < cnt4[q] && first + k < hi; ++k) sh.it_pos[first + k - lo] = c * chunk + k;
+// List position of item i (0 <= i < total): item i - pfx[c] of the chunk c
+// with pfx[c] <= i < pfx[c + 1].
+__device__ __forceinline__ int list_pos(const TokShared& sh, int i, int chunk) {
+  int lo = 0, hi = kTokChunks;
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (sh.pfx[mid] <= i) lo = mid;
+    else hi = mid;
   }
-}
-
-// Control: slots of the items of batch b -- issued here, written into the
-// table by ctl_table_store once the wave has done other work meanwhile.
-__device__ __forceinline__ void ctl_table_load(const TokShared& sh, rsrc_t rslots, int b, int total,
-                                               int (&sl)[kCtlItems]) {
-  const int l = lane_id();
-#pragma unroll
-  for (int m = 0; m < kCtlItems; ++m) {
-    const int i = l + kWave * m;
-    sl[m] = (int)bld4(rslots, b * kBatch + i < total ? 4 * (uint32_t)sh.it_pos[i] : kNoOff);
-  }
-}
-__device__ __forceinline__ void ctl_table_store(TokShared& sh, const int (&sl)[kCtlItems], int n_records, int b,
-                                                int total) {
-  const int l = lane_id();
-#pragma unroll
-  for (int m = 0; m < kCtlItems; ++m) {
-    const int i = l + kWave * m;
-    const bool v = b * kBatch + i < total && sl[m] >= 0 && sl[m] < n_records;
-    sh.it_slot[i] = v ? sl[m] : -1;
-  }
+  return lo * chunk + (i - sh.pfx[lo]);
 }
 
 // ── the control wave ────────────────────────────────────────────────────────
@@ -383,12 +358,6 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
     }
     wait_vm();
     bar();   // B1: x * w, r and the list prefix are in LDS
-    // the gather table of batch 0 (its slots; the cold activations come in D)
-    if (has_cold) ctl_positions(sh, cnt4, chunk, 0);
-    __builtin_amdgcn_wave_barrier();
-    int tsl[kCtlItems];
-    ctl_table_load(sh, rsrc(has_cold ? T->act_slots : nullptr, has_cold ? (uint32_t)kTokChunks * chunk * 4 : 0u), 0,
-                   has_cold ? total : 0, tsl);
     // a quarter of the next layer's predictor row: z = D q, q =
     // bf16(fp16(x r w')) (pred_d_role's arithmetic and partial sums);
     // stored with the phase's other outputs
@@ -462,8 +431,7 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
       if (l == 0) sh.hc_out[k] = hv;
       if (l < kGroups) sh.hcs_out[l][k] = hs;
     }
-    if (has_cold) ctl_table_store(sh, tsl, T->n_records, 0, total);
-    bar();   // B2: the workers' activations and the gather table are in LDS
+    bar();   // B2: the workers' activations are in LDS
     if (pred && l == 0)
       cst4(rsrc(a.z + (size_t)(L + 1) * 4 * kTokMaxRank, 4 * kTokMaxRank * 4), 4 * (uint32_t)g, as_u32(zrow));
     if (T) {
@@ -694,7 +662,8 @@ __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
   float RG[kColdR];           //   gate bias
   int RSL[kColdR];            //   slots,
   float RD[kColdR];           //   and the down scale of row group l (lanes < kGroups)
-  u32x2v NB[kGat];            // gather items: down nibbles of the tile's rows
+  int NPOS[kGat], NSL[kGat];  // gather items (list positions wi 64 + l + 448 m): position and slot,
+  u32x2v NB[kGat];            //   down nibbles of the tile's rows
   // neurons [j0h, j1h) of the gate/up rows (and, with the first, the scales)
   auto load_hot = [&](int L, int j0h, int j1h) {          // L may be n: reads zero
     const bool v = L < n;
@@ -769,15 +738,31 @@ __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
       RD[i] = half_bits_to_float(bld2(rr, ro + kOffScales + 2 * (2 * kGroups + (l & (kGroups - 1)))));
     }
   };
-  // down nibbles of the first gather batch of layer L (the table in LDS)
+  // record slots of this lane's gather items of layer L: list positions from
+  // the prefix in LDS, slots loaded here and checked when used
+  auto load_slots = [&](int L) {
+    const bool v = L >= 0 && LT[L].n_records > 0 && LT[L].act_counts;
+    CLayer& T = LT[L >= 0 ? L : 0];
+    const int chunk = v ? T.act_chunk : 0;
+    const int total = v ? sh.total : 0;
+    const rsrc_t rs = rsrc(T.act_slots, v ? (uint32_t)kTokChunks * chunk * 4 : 0u);
+#pragma unroll
+    for (int m = 0; m < kGat; ++m) {
+      const int i = wi * kWave + l + kWorkers * kWave * m;
+      NPOS[m] = i < total ? list_pos(sh, i, chunk) : -1;
+      NSL[m] = (int)bld4(rs, NPOS[m] >= 0 ? 4 * (uint32_t)NPOS[m] : kNoOff);
+    }
+  };
+  // down nibbles of those items
   auto load_nibbles = [&](int L) {
     const bool v = L >= 0 && LT[L].n_records > 0 && LT[L].act_counts;
     CLayer& T = LT[L >= 0 ? L : 0];
+    const int nr = v ? T.n_records : 0;
     const rsrc_t rr = rsrc(T.records, v ? (uint32_t)T.n_records * kRecBytes : 0u);
 #pragma unroll
     for (int m = 0; m < kGat; ++m) {
-      const int sl = sh.it_slot[wi * kWave + l + kWorkers * kWave * m];
-      const uint32_t ro = sl >= 0 ? (uint32_t)sl * kRecBytes : kNoOff;
+      NSL[m] = (NPOS[m] >= 0 && NSL[m] >= 0 && NSL[m] < nr) ? NSL[m] : -1;
+      const uint32_t ro = NSL[m] >= 0 ? (uint32_t)NSL[m] * kRecBytes : kNoOff;
       NB[m] = bld8(rr, ro + kOffDown + j0 / 2);
     }
   };
@@ -787,6 +772,7 @@ __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
     const bool has_cold = T && T->n_records > 0 && T->act_counts;
     // ================= U phase
     bar();   // B1: the control's inputs have landed
+    load_slots(L);               // the slots of this lane's gather items,
     load_down(L, 1, 3);          // the rest of this layer's down rows
     if (T) {
       const float r = sh.r;
@@ -907,7 +893,7 @@ __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
 #pragma unroll
         for (int m = 0; m < kGat; ++m) {
           const int i = wi * kWave + l + kWorkers * kWave * m;
-          if (sh.it_slot[i] >= 0) {
+          if (NSL[m] >= 0) {
             const float hs = sh.it_hcs[i];
             f16x2 tq[4];
             int4x8_to_f16x2x4(NB[m].x, tq);
