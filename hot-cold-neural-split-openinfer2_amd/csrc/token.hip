@@ -22,10 +22,11 @@
 // control wave never has weight loads in flight ahead of the loads the
 // phase waits on, and the workers never wait on a cross-group input.
 // Worker loads, in issue order per layer: gather nibbles and half the next
-// gate/up rows (end of U), the other half (D1a, once the phase's inputs are
-// in), the next chunk's records (D1b, once the control wave has computed the
-// next list, which overlaps the workers' down products), the next layer's
-// first down row (end of D), its other down rows (B1).  Each
+// gate/up rows (end of U, after the control wave has issued the phase's
+// stores: B3), the other half (D1a, once the phase's inputs are in), the next
+// chunk's records (D1b, once the control wave has computed the next list,
+// which overlaps the workers' down products), the next layer's first down row
+// (end of D), the gather items' slots and its other down rows (B1).  Each
 // phase's compute needs only loads older than the ones still streaming, and
 // the halves issued at B1 / D1 go out after the phase's cross-group inputs:
 // a CU's memory pipeline is in order, and a backlog of weight loads ahead of
@@ -454,6 +455,7 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
         }
       }
     }
+    bar();   // B3: the stores are issued, ahead of the workers' next loads
     tok_arrive(a.sync, 0, g, base + (uint32_t)(L + 2));
 
     // ================= D phase of layer L (L = -1: only layer 0's selection)
@@ -847,6 +849,7 @@ __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
       }
     }
     bar();   // B2
+    bar();   // B3
     load_nibbles(L);
     load_hot(L + 1, 0, 1);       // half the next gate/up rows now ...
     // ================= D phase
