@@ -26,7 +26,9 @@
 // stores: B3), the other half (D1a, once the phase's inputs are in), the next
 // chunk's records (D1b, once the control wave has computed the next list,
 // which overlaps the workers' down products), the next layer's first down row
-// (end of D), the gather items' slots and its other down rows (B1).  Each
+// (end of D), the gather items' slots and its other down rows (after the U
+// products: issued earlier they would stall those products while the CU's
+// memory queue is full).  Each
 // phase's compute needs only loads older than the ones still streaming, and
 // the halves issued at B1 / D1 go out after the phase's cross-group inputs:
 // a CU's memory pipeline is in order, and a backlog of weight loads ahead of
@@ -774,8 +776,6 @@ __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
     const bool has_cold = T && T->n_records > 0 && T->act_counts;
     // ================= U phase
     bar();   // B1: the control's inputs have landed
-    load_slots(L);               // the slots of this lane's gather items,
-    load_down(L, 1, 3);          // the rest of this layer's down rows
     if (T) {
       const float r = sh.r;
       // hot neurons (the accumulation order of the two-launch path)
@@ -848,6 +848,8 @@ __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
         }
       }
     }
+    load_slots(L);               // the slots of this lane's gather items,
+    load_down(L, 1, 3);          // the rest of this layer's down rows
     bar();   // B2
     bar();   // B3
     load_nibbles(L);
