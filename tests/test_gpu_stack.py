@@ -240,3 +240,40 @@ def test_token_kernel_matches_two_launches(stack4):
         assert_ffn_close(res[True][1][L].double().cpu().numpy(), res[False][1][L].double().cpu().numpy(),
                          tol=2e-3, cos_min=0.99999, what=f"layer {L} output")
     assert torch.equal(res[True][0], res[True][1][-1])
+
+
+@pytest.mark.parametrize("n_hot,activation,both,shift", [(4000, "silu", False, 0.0), (3584, "relu", True, -1.66)],
+                         ids=["three_hot_rows_per_wave", "drelu_with_gate_bias"])
+def test_token_kernel_other_geometries(n_hot, activation, both, shift):
+    """The persistent kernel's other shapes against the two-launch sequence:
+    n_hot 4000 runs the variant with three hot neurons per worker wave, and
+    dReLU (relu on both halves, engine.py:163-170) with a gate bias runs the
+    bias and activation paths.  Layers 0 and 1 select from x_in, so their
+    active sets are identical; outputs agree to the summation order."""
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(5)
+    layers = [SyntheticLayer(g, 14336, n_hot, device=dev, with_predictor=True, gate_bias_shift=shift)
+              for _ in range(3)]
+    thr = calibrate_threshold(layers, g, 0.05)
+    st = DecodeStack([StackLayer(l.hot, l.records, l.lut, l.norm_w, l.predictor, l.cold_gate_bias)
+                      for l in layers], 14336, EPS, activation, both, thr)
+    try:
+        assert st.token_kernel
+        x_in = torch.randn(H, generator=g, device=dev).half()
+        res = {}
+        for token in (True, False):
+            st.set_token_kernel(token)
+            out = torch.empty_like(x_in)
+            st.decode(x_in, out, None)
+            st.status()
+            xs, counts, _, ids = st.trace()
+            torch.cuda.synchronize()
+            res[token] = (xs.clone(), [st.active_ids(L, counts, ids) for L in (0, 1)])
+        st.set_token_kernel(True)
+        assert res[True][1] == res[False][1]
+        assert all(len(s) > 0 for s in res[True][1])
+        for L in range(3):
+            assert_ffn_close(res[True][0][L].double().cpu().numpy(), res[False][0][L].double().cpu().numpy(),
+                             tol=2e-3, cos_min=0.99999, what=f"layer {L} output")
+    finally:
+        st.close()
