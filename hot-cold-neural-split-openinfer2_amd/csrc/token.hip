@@ -209,12 +209,12 @@ struct alignas(16) TokShared {
   float it_hcs[1024];         // gather items of the current batch: cold activation x down scale
                               // of the tile's row group (list order; 4 KB, one copy's reach),
   float hcs_out[kGroups][kTokMaxChunk];   // this group's items: activation x down scale, per row group
+  float dsc[kRows];           // the tile's down row scales
   int pfx[kTokChunks + 1];    // exclusive prefix of the list's chunk counts
   int lst_slot[kTokMaxChunk]; // chunk g of the next layer's list
   int lst_id[kTokMaxChunk];
   float h_out[kWorkers * 3];  // this group's hot activations
   float hc_out[kTokMaxChunk]; // this group's cold activations (chunk order)
-  float yhot[kRows];
   float cpart[kWorkers][kRows];
   float cpart_ctl[kRows];     // the control wave's share of long gather lists
   float out[kRows];
@@ -225,7 +225,7 @@ struct alignas(16) TokShared {
 static_assert(offsetof(TokShared, nat) % 16 == 0 && offsetof(TokShared, xq) % 16 == 0 &&
               offsetof(TokShared, wq) % 16 == 0 && offsetof(TokShared, pd) % 16 == 0 &&
               offsetof(TokShared, h) % 16 == 0 && offsetof(TokShared, pu) % 16 == 0 &&
-              offsetof(TokShared, it_hcs) % 16 == 0,
+              offsetof(TokShared, it_hcs) % 16 == 0 && offsetof(TokShared, dsc) % 16 == 0,
               "LDS DMA targets and 16-byte reads are 16-byte aligned");
 
 // List position of item i (0 <= i < total): item i - pfx[c] of the chunk c
@@ -465,6 +465,7 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
     const bool psel = N && N->pd_w;                      // the next layer's list is predicted
     const bool pstat = N && !N->pd_w && N->n_records > 0 && N->act_counts;   // or fixed
     float res_v = 0.0f, nwv = 1.0f;
+    u32x4 dsv = {0u, 0u, 0u, 0u};                        // the tile's down row scales (lanes < 4)
     if (T) {
       const rsrc_t rh = rsrc(a.h + (size_t)L * kTokMaxHot, kTokMaxHot * 4);
 #pragma unroll
@@ -474,6 +475,7 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
       const uint16_t nb = bld2(rsrc(N ? N->norm_w : nullptr, N ? kH * 2 : 0u), l < kRows ? 2 * (uint32_t)(j0 + l) : kNoOff);
       res_v = half_bits_to_float(rb);
       nwv = half_bits_to_float(nb);
+      dsv = bld16(rsrc(T->down_s + j0, T->n_hot > 0 ? kRows * 4 : 0u), l < kRows / 4 ? 16 * (uint32_t)l : kNoOff);
       if (has_cold) {   // the batch's activations x the tile group's down scale, in list order
         const rsrc_t rg = rsrc(a.hcs + ((size_t)L * kGroups + j0 / kGroup) * kBatch, kBatch * 4);
 #pragma unroll
@@ -509,6 +511,7 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
     }
     if (l < kTokMaxRank) sh.z[l] = zl;
     wait_vm();
+    if (l < kRows / 4) reinterpret_cast<u32x4*>(sh.dsc)[l] = dsv;
     // take the loaded values into plain registers now, before any store
     asm volatile("" : "+v"(res_v), "+v"(nwv));
     bar();   // D1a: h and the gather activations are in LDS (the workers start)
@@ -610,9 +613,8 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
     bar();   // D2: the workers' row sums are in LDS
     if (T) {
       if (l < kRows) {
-        const float yc = (((sh.cpart[0][l] + sh.cpart[1][l]) + (sh.cpart[2][l] + sh.cpart[3][l])) +
-                          ((sh.cpart[4][l] + sh.cpart[5][l]) + sh.cpart[6][l])) + sh.cpart_ctl[l];
-        const float y = sh.yhot[l] + yc;
+        const float y = (((sh.cpart[0][l] + sh.cpart[1][l]) + (sh.cpart[2][l] + sh.cpart[3][l])) +
+                         ((sh.cpart[4][l] + sh.cpart[5][l]) + sh.cpart[6][l])) + sh.cpart_ctl[l];
         const uint16_t ob = float_to_half_bits(res_v + y);
         cst2(rsrc(a.xbuf + (size_t)L * kH, kH * 2), 2 * (uint32_t)(j0 + l), ob);
         if (L == n - 1) __builtin_amdgcn_raw_buffer_store_b16(ob, rsrc(a.x_out, kH * 2), 2 * (uint32_t)(j0 + l), 0, 0);
@@ -651,16 +653,21 @@ __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
   const int n = a.n_layers;
   const int tile = (g & 7) * (kTokGroups / 8) + (g >> 3);
   const int j0 = tile * kRows;
-  const int rs = wi < 2 ? 3 * wi : 2 * wi + 2;   // down rows [rs, rs + rc) of the tile
-  const int rc = wi < 2 ? 3 : 2;
+  // down rows: every worker lane takes kpl columns of all 16 rows of the tile
+  // (columns k0 .. k0 + kpl), so the h reads and the products are split
+  // evenly; its per-row sums join the cold terms' before one reduction
+  constexpr int kpl = NPW == 2 ? 8 : 16;
+  static_assert(kWorkers * kWave * kpl >= (NPW == 2 ? NPW * kWorkers * kTokGroups : kTokMaxHot),
+                "the worker columns cover every hot neuron");
+  const int kc = (wi * kWave + l) * kpl;
   const int k0 = (g * kWorkers + wi) * NPW;       // hot neurons [k0, k0 + NPW)
   const int g0 = l >> 2;
   CLayer* LT = layer_table(a);
   // weights, each loaded one phase ahead of its use
   u32x4 WU[NPW][8];           // gate (0..3) and up (4..7) chunks of the hot neurons
   float gsc = 0.0f, usc = 0.0f, gbi = 0.0f;       // lane j < NPW: neuron k0 + j
-  u32x4 WD[3][4];             // down rows
-  float dsc[3];
+  typedef typename std::conditional<NPW == 2, u32x2v, u32x4>::type dcol_t;
+  dcol_t WD[kRows];           // down rows: this lane's columns of each row
   u32x4 RQ[kColdR][4];        // cold records of the chunk: gate and up halves,
   float RS[kColdR][4];        //   their group scales,
   float RG[kColdR];           //   gate bias
@@ -691,26 +698,20 @@ __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
       gbi = as_f32(bld4(rsrc(T.hot_gbias, T.hot_gbias ? nh * 4 : 0u), so));
     }
   };
-  // down rows [rs + r0, rs + r1) (those of the wave)
+  // down rows [r0, r1) of the tile: this lane's columns (stride is a multiple
+  // of 16, so a run that starts inside the row ends inside it)
   auto load_down = [&](int L, int r0, int r1) {         // L may be n (or -1): reads zero
     const bool v = L >= 0 && L < n;
     CLayer& T = LT[v ? L : 0];
     const int stride = T.down_stride;
     const bool hv = v && T.n_hot > 0;
-    const int nch = hv ? stride >> 4 : 0;
     const rsrc_t rq = rsrc(T.down_q, hv ? (uint32_t)kH * stride : 0u);
-    const rsrc_t rd = rsrc(T.down_s, hv ? kH * 4 : 0u);
 #pragma unroll
-    for (int rr = 0; rr < 3; ++rr) {
-      if (rr < r0 || rr >= r1) continue;
-      const bool rv = rr < rc;
-      const int row = j0 + rs + rr;
-#pragma unroll
-      for (int it = 0; it < 4; ++it) {
-        const int c = l + 64 * it;
-        WD[rr][it] = bld16(rq, (rv && c < nch) ? (uint32_t)(row * stride + 16 * c) : kNoOff);
-      }
-      dsc[rr] = as_f32(bld4(rd, rv ? 4 * (uint32_t)row : kNoOff));
+    for (int r = 0; r < kRows; ++r) {
+      if (r < r0 || r >= r1) continue;
+      const uint32_t o = kc < stride ? (uint32_t)((j0 + r) * stride + kc) : kNoOff;
+      if constexpr (NPW == 2) WD[r] = bld8(rq, o);
+      else WD[r] = bld16(rq, o);
     }
   };
   // records of chunk items k = wi + kWorkers i of layer L (the list in LDS)
@@ -849,7 +850,7 @@ __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
       }
     }
     load_slots(L);               // the slots of this lane's gather items,
-    load_down(L, 1, 3);          // the rest of this layer's down rows
+    load_down(L, 6, kRows);      // the rest of this layer's down rows
     bar();   // B2
     bar();   // B3
     load_nibbles(L);
@@ -861,37 +862,30 @@ __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
 #pragma unroll
     for (int e = 0; e < kRows; ++e) yc[e] = 0.0f;
     if (T) {
-      // hot down rows (down_role's accumulation order)
-      float acc[3] = {0.0f, 0.0f, 0.0f};
+      // hot: this lane's columns of the tile's 16 down rows, each row's sum
+      // times its scale (the cold terms join these sums)
+      float hv[kpl];
 #pragma unroll
-      for (int it = 0; it < 4; ++it) {
-        const f32x4* ph = reinterpret_cast<const f32x4*>(sh.h) + 4 * (l + 64 * it);
-        float hv[16];
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          const f32x4 v = ph[m];
-          hv[4 * m] = v[0];
-          hv[4 * m + 1] = v[1];
-          hv[4 * m + 2] = v[2];
-          hv[4 * m + 3] = v[3];
-        }
-#pragma unroll
-        for (int rr = 0; rr < 3; ++rr)
-#pragma unroll
-          for (int d = 0; d < 4; ++d) {
-            const f32x2 lo = fp8x2_to_f32x2(WD[rr][it][d], false);
-            const f32x2 hi = fp8x2_to_f32x2(WD[rr][it][d], true);
-            acc[rr] = fmaf(lo.x, hv[4 * d], acc[rr]);
-            acc[rr] = fmaf(lo.y, hv[4 * d + 1], acc[rr]);
-            acc[rr] = fmaf(hi.x, hv[4 * d + 2], acc[rr]);
-            acc[rr] = fmaf(hi.y, hv[4 * d + 3], acc[rr]);
-          }
+      for (int m = 0; m < kpl / 4; ++m) {
+        const f32x4 v = kc < kTokMaxHot ? reinterpret_cast<const f32x4*>(sh.h + kc)[m] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        hv[4 * m] = v[0];
+        hv[4 * m + 1] = v[1];
+        hv[4 * m + 2] = v[2];
+        hv[4 * m + 3] = v[3];
       }
-      wave_sums_to_last(acc);
-      if (l == kWave - 1) {
 #pragma unroll
-        for (int rr = 0; rr < 3; ++rr)
-          if (rr < rc) sh.yhot[rs + rr] = T->n_hot > 0 ? acc[rr] * dsc[rr] : 0.0f;
+      for (int r = 0; r < kRows; ++r) {
+        float p = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kpl / 4; ++w) {
+          const f32x2 lo = fp8x2_to_f32x2(WD[r][w], false);
+          const f32x2 hi = fp8x2_to_f32x2(WD[r][w], true);
+          p = fmaf(lo.x, hv[4 * w], p);
+          p = fmaf(lo.y, hv[4 * w + 1], p);
+          p = fmaf(hi.x, hv[4 * w + 2], p);
+          p = fmaf(hi.y, hv[4 * w + 3], p);
+        }
+        yc[r] = p * sh.dsc[r];
       }
       // cold: this lane's items of the first gather batch x their 16 down nibbles
       if (has_cold) {
@@ -925,7 +919,7 @@ __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
     bar();   // D1b: the next chunk's list (computed meanwhile) is in LDS
     load_records(L + 1);
     bar();   // D2
-    load_down(L + 1, 0, 1);      // the next layer's first down row (the rest at B1)
+    load_down(L + 1, 0, 6);      // the next layer's first down rows (the rest after the U products)
   }
 }
 

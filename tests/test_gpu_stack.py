@@ -220,7 +220,7 @@ def test_token_kernel_matches_two_launches(stack4):
     """The persistent kernel against the two-launch sequence on one token.
     Layers 0 and 1 are selected from x_in itself by the same arithmetic, so
     their active sets are identical; the outputs differ only in the order
-    the cold down terms are summed."""
+    the down terms are summed."""
     dev, g, layers, st, thr = stack4
     x_in = torch.randn(H, generator=g, device=dev).half()
     res = {}
