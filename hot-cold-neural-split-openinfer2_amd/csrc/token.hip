@@ -228,16 +228,30 @@ static_assert(offsetof(TokShared, nat) % 16 == 0 && offsetof(TokShared, xq) % 16
               offsetof(TokShared, it_hcs) % 16 == 0 && offsetof(TokShared, dsc) % 16 == 0,
               "LDS DMA targets and 16-byte reads are 16-byte aligned");
 
-// List position of item i (0 <= i < total): item i - pfx[c] of the chunk c
-// with pfx[c] <= i < pfx[c + 1].
-__device__ __forceinline__ int list_pos(const TokShared& sh, int i, int chunk) {
-  int lo = 0, hi = kTokChunks;
-  while (hi - lo > 1) {
-    const int mid = (lo + hi) >> 1;
-    if (sh.pfx[mid] <= i) lo = mid;
-    else hi = mid;
+// List positions of items i[m] (0 <= i[m] < total): item i - pfx[c] of the
+// chunk c with pfx[c] <= i < pfx[c + 1], that is the last c < kTokChunks
+// with pfx[c] <= i (empty chunks before it have smaller c, those after it a
+// larger prefix).  A four-way search over the 256 chunks, 4 steps of 3 LDS
+// reads each, the M searches interleaved so that their reads overlap.
+template <int M>
+__device__ __forceinline__ void list_pos(const TokShared& sh, const int (&i)[M], int chunk, int (&pos)[M]) {
+  static_assert(kTokChunks == 256, "four steps of a four-way search");
+  int lo[M];
+#pragma unroll
+  for (int m = 0; m < M; ++m) lo[m] = 0;
+#pragma unroll
+  for (int st = 64; st >= 1; st >>= 2) {
+    int p[M][3];
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+#pragma unroll
+      for (int q = 0; q < 3; ++q) p[m][q] = sh.pfx[lo[m] + st * (q + 1)];
+#pragma unroll
+    for (int m = 0; m < M; ++m)
+      lo[m] += st * ((int)(p[m][0] <= i[m]) + (int)(p[m][1] <= i[m]) + (int)(p[m][2] <= i[m]));
   }
-  return lo * chunk + (i - sh.pfx[lo]);
+#pragma unroll
+  for (int m = 0; m < M; ++m) pos[m] = lo[m] * chunk + (i[m] - sh.pfx[lo[m]]);
 }
 
 // ── the control wave ────────────────────────────────────────────────────────
@@ -751,10 +765,13 @@ __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
     const int chunk = v ? T.act_chunk : 0;
     const int total = v ? sh.total : 0;
     const rsrc_t rs = rsrc(T.act_slots, v ? (uint32_t)kTokChunks * chunk * 4 : 0u);
+    int it[kGat];
+#pragma unroll
+    for (int m = 0; m < kGat; ++m) it[m] = wi * kWave + l + kWorkers * kWave * m;
+    list_pos(sh, it, chunk, NPOS);
 #pragma unroll
     for (int m = 0; m < kGat; ++m) {
-      const int i = wi * kWave + l + kWorkers * kWave * m;
-      NPOS[m] = i < total ? list_pos(sh, i, chunk) : -1;
+      if (it[m] >= total) NPOS[m] = -1;
       NSL[m] = (int)bld4(rs, NPOS[m] >= 0 ? 4 * (uint32_t)NPOS[m] : kNoOff);
     }
   };
