@@ -269,13 +269,54 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
     CLayer* T = L >= 0 ? LT + L : nullptr;
     CLayer* N = L + 1 < n ? LT + L + 1 : nullptr;
     // ================= U phase of layer L (L = -1: only layer 0's predictor)
-    if (L >= 0) tok_wait(a.sync, 1, g, base + (uint32_t)(L + 1), base, a.spin);
     const bool has_cold = T && T->n_records > 0 && T->act_counts;
     const int chunk = has_cold ? T->act_chunk : 0;
     // the next layer's predictor: group g sums quarter g & 3 of row g >> 2
     const bool pred = N && N->pd_w && g < 4 * N->rank;
-    // inputs: x * w into LDS, the sum-of-squares partials, the list's counts,
-    // and for a predictor group x_L, the next norm weight and the D row
+    // loaded ahead of the wait (weights, and the records of this group's own
+    // list, computed by this wave in the previous D phase): a predictor
+    // group's quarter of the next norm weight and D row, and the chunk's
+    // items past the workers' share
+    if (pred) {
+      const rsrc_t rw = rsrc(N->norm_w, kH * 2);
+      const rsrc_t rd = rsrc(N->pd_w + (size_t)(g >> 2) * kH, kH * 2);
+#pragma unroll
+      for (int it = 0; it < 2; ++it) {
+        const uint32_t off = 16 * (uint32_t)(l + 64 * (2 * (g & 3) + it));
+        bld16_lds(rw, sh.wq + 256 * it, off);
+        bld16_lds(rd, sh.pd + 256 * it, off);
+      }
+    }
+    const int ccnt = has_cold ? sh.lst_cnt : 0;
+    const rsrc_t rrec = rsrc(has_cold ? T->records : nullptr, has_cold ? (uint32_t)T->n_records * kRecBytes : 0u);
+    const rsrc_t rcgb = rsrc(has_cold ? T->cold_gbias : nullptr,
+                             (has_cold && T->cold_gbias) ? (uint32_t)T->n_records * 4 : 0u);
+    u32x4 CQ[kCtlCold][4];
+    float CS[kCtlCold][4], CG[kCtlCold], CD[kCtlCold];   // CD: down scale of row group l
+    int CSL[kCtlCold];
+#pragma unroll
+    for (int i = 0; i < kCtlCold; ++i) {
+      const int k = kWorkers * kColdR + i;
+      const int sl = k < ccnt ? sh.lst_slot[k] : -1;
+      const bool vv = has_cold && sl >= 0 && sl < T->n_records;
+      CSL[i] = vv ? sl : -1;
+      const uint32_t ro = vv ? (uint32_t)sl * kRecBytes : kNoOff;
+#pragma unroll
+      for (int it = 0; it < 2; ++it) {
+        CQ[i][it] = bld16(rrec, ro + kOffGate + 16 * (l + 64 * it));
+        CQ[i][2 + it] = bld16(rrec, ro + kOffUp + 16 * (l + 64 * it));
+      }
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        CS[i][2 * q] = half_bits_to_float(bld2(rrec, ro + kOffScales + 2 * (32 * q + g0)));
+        CS[i][2 * q + 1] = half_bits_to_float(bld2(rrec, ro + kOffScales + 2 * (32 * q + 16 + g0)));
+      }
+      CG[i] = as_f32(bld4(rcgb, vv ? 4 * (uint32_t)sl : kNoOff));
+      CD[i] = half_bits_to_float(bld2(rrec, ro + kOffScales + 2 * (2 * kGroups + (l & (kGroups - 1)))));
+    }
+    if (L >= 0) tok_wait(a.sync, 1, g, base + (uint32_t)(L + 1), base, a.spin);
+    // inputs the previous phase produced: x * w into LDS, the sum-of-squares
+    // partials, the list's counts, and for a predictor group x_L
     if (T) {
       const rsrc_t rx = rsrc(a.xw + (size_t)L * kH, kH * 2);
 #pragma unroll
@@ -309,43 +350,10 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
     for (int q = 0; q < 4; ++q) cnt4[q] = (int)bld4(rcnt, 4 * (4 * l + q));
     if (pred) {
       const uint16_t* xl = L <= 0 ? a.x_in : a.xbuf + (size_t)(L - 1) * kH;
-      const rsrc_t rx = rsrc(xl, kH * 2), rw = rsrc(N->norm_w, kH * 2);
-      const rsrc_t rd = rsrc(N->pd_w + (size_t)(g >> 2) * kH, kH * 2);
+      const rsrc_t rx = rsrc(xl, kH * 2);
 #pragma unroll
-      for (int it = 0; it < 2; ++it) {
-        const uint32_t off = 16 * (uint32_t)(l + 64 * (2 * (g & 3) + it));
-        bld16_lds(rx, sh.xq + 256 * it, off);
-        bld16_lds(rw, sh.wq + 256 * it, off);
-        bld16_lds(rd, sh.pd + 256 * it, off);
-      }
-    }
-    // the chunk's items past the workers' share: records with the inputs
-    const int ccnt = has_cold ? sh.lst_cnt : 0;
-    const rsrc_t rrec = rsrc(has_cold ? T->records : nullptr, has_cold ? (uint32_t)T->n_records * kRecBytes : 0u);
-    const rsrc_t rcgb = rsrc(has_cold ? T->cold_gbias : nullptr,
-                             (has_cold && T->cold_gbias) ? (uint32_t)T->n_records * 4 : 0u);
-    u32x4 CQ[kCtlCold][4];
-    float CS[kCtlCold][4], CG[kCtlCold], CD[kCtlCold];   // CD: down scale of row group l
-    int CSL[kCtlCold];
-#pragma unroll
-    for (int i = 0; i < kCtlCold; ++i) {
-      const int k = kWorkers * kColdR + i;
-      const int sl = k < ccnt ? sh.lst_slot[k] : -1;
-      const bool vv = has_cold && sl >= 0 && sl < T->n_records;
-      CSL[i] = vv ? sl : -1;
-      const uint32_t ro = vv ? (uint32_t)sl * kRecBytes : kNoOff;
-#pragma unroll
-      for (int it = 0; it < 2; ++it) {
-        CQ[i][it] = bld16(rrec, ro + kOffGate + 16 * (l + 64 * it));
-        CQ[i][2 + it] = bld16(rrec, ro + kOffUp + 16 * (l + 64 * it));
-      }
-#pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        CS[i][2 * q] = half_bits_to_float(bld2(rrec, ro + kOffScales + 2 * (32 * q + g0)));
-        CS[i][2 * q + 1] = half_bits_to_float(bld2(rrec, ro + kOffScales + 2 * (32 * q + 16 + g0)));
-      }
-      CG[i] = as_f32(bld4(rcgb, vv ? 4 * (uint32_t)sl : kNoOff));
-      CD[i] = half_bits_to_float(bld2(rrec, ro + kOffScales + 2 * (2 * kGroups + (l & (kGroups - 1)))));
+      for (int it = 0; it < 2; ++it)
+        bld16_lds(rx, sh.xq + 256 * it, 16 * (uint32_t)(l + 64 * (2 * (g & 3) + it)));
     }
     const float r = r_from_part(f32x4{as_f32(pp.x), as_f32(pp.y), as_f32(pp.z), as_f32(pp.w)}, a.eps);
     // exclusive prefix of the chunk counts (lane l: chunks 4 l .. 4 l + 3)
@@ -475,40 +483,28 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
     tok_arrive(a.sync, 0, g, base + (uint32_t)(L + 2));
 
     // ================= D phase of layer L (L = -1: only layer 0's selection)
-    tok_wait(a.sync, 0, g, base + (uint32_t)(L + 2), base, a.spin);
     const bool psel = N && N->pd_w;                      // the next layer's list is predicted
     const bool pstat = N && !N->pd_w && N->n_records > 0 && N->act_counts;   // or fixed
+    // loaded ahead of the wait (weights, and x_L, which the U phase's wait
+    // already covers): the tile's residual, next norm weight and down row
+    // scales, and the next layer's predictor up rows, bias and LUT entries
+    // of chunk g (lane l = neuron g * chunk + l) or its fixed list
     float res_v = 0.0f, nwv = 1.0f;
     u32x4 dsv = {0u, 0u, 0u, 0u};                        // the tile's down row scales (lanes < 4)
-    if (T) {
-      const rsrc_t rh = rsrc(a.h + (size_t)L * kTokMaxHot, kTokMaxHot * 4);
-#pragma unroll
-      for (int it = 0; it < kTokMaxHot * 4 / 1024; ++it) bld16_lds(rh, sh.h + 256 * it, 16 * (l + 64 * it));
-      const uint16_t* xl = L == 0 ? a.x_in : a.xbuf + (size_t)(L - 1) * kH;
-      const uint16_t rb = bld2(rsrc(xl, kH * 2), l < kRows ? 2 * (uint32_t)(j0 + l) : kNoOff);
-      const uint16_t nb = bld2(rsrc(N ? N->norm_w : nullptr, N ? kH * 2 : 0u), l < kRows ? 2 * (uint32_t)(j0 + l) : kNoOff);
-      res_v = half_bits_to_float(rb);
-      nwv = half_bits_to_float(nb);
-      dsv = bld16(rsrc(T->down_s + j0, T->n_hot > 0 ? kRows * 4 : 0u), l < kRows / 4 ? 16 * (uint32_t)l : kNoOff);
-      if (has_cold) {   // the batch's activations x the tile group's down scale, in list order
-        const rsrc_t rg = rsrc(a.hcs + ((size_t)L * kGroups + j0 / kGroup) * kBatch, kBatch * 4);
-#pragma unroll
-        for (int it = 0; it < 4; ++it) bld16_lds(rg, sh.it_hcs + 256 * it, 16 * (l + 64 * it));
-      }
-    } else if (N) {   // layer 0's x and norm weight of the tile
-      res_v = half_bits_to_float(bld2(rsrc(a.x_in, kH * 2), l < kRows ? 2 * (uint32_t)(j0 + l) : kNoOff));
-      nwv = half_bits_to_float(bld2(rsrc(N->norm_w, kH * 2), l < kRows ? 2 * (uint32_t)(j0 + l) : kNoOff));
+    if (T || N) {
+      const uint16_t* xl = L <= 0 ? a.x_in : a.xbuf + (size_t)(L - 1) * kH;
+      const uint32_t ro = l < kRows ? 2 * (uint32_t)(j0 + l) : kNoOff;
+      res_v = half_bits_to_float(bld2(rsrc(xl, kH * 2), ro));
+      nwv = N ? half_bits_to_float(bld2(rsrc(N->norm_w, kH * 2), ro)) : 1.0f;
     }
+    if (T) dsv = bld16(rsrc(T->down_s + j0, T->n_hot > 0 ? kRows * 4 : 0u), l < kRows / 4 ? 16 * (uint32_t)l : kNoOff);
     int ch_n = 0, nn = -1;
-    float zl = 0.0f;
     uint16_t pbits = 0;
     int plut = -1;
-    if (psel) {   // chunk g of the next layer's predictor: lane l = neuron g * chunk + l
+    if (psel) {
       ch_n = N->sel_chunk;
       const int rank = N->rank;
       nn = (l < ch_n && g * ch_n + l < N->inter) ? g * ch_n + l : -1;
-      const u32x4 zp = bld16(rsrc(a.z + (size_t)(L + 1) * 4 * kTokMaxRank, (uint32_t)rank * 16), 16 * (uint32_t)l);
-      zl = (as_f32(zp.x) + as_f32(zp.y)) + (as_f32(zp.z) + as_f32(zp.w));
       const rsrc_t ru = rsrc(N->pu_w, (uint32_t)N->inter * rank * 2);
 #pragma unroll
       for (int m = 0; m < 8; ++m)
@@ -522,6 +518,24 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
       scnt = (int)bld4(rsrc(N->act_counts, kTokChunks * 4), 4 * (uint32_t)g);
       sslot = (int)bld4(rsrc(N->act_slots, (uint32_t)kTokChunks * ch_n * 4),
                         l < ch_n ? 4 * (uint32_t)(g * ch_n + l) : kNoOff);
+    }
+    tok_wait(a.sync, 0, g, base + (uint32_t)(L + 2), base, a.spin);
+    // inputs the U phase produced: h, the batch's activations x the tile
+    // group's down scale (list order), and the next layer's z
+    if (T) {
+      const rsrc_t rh = rsrc(a.h + (size_t)L * kTokMaxHot, kTokMaxHot * 4);
+#pragma unroll
+      for (int it = 0; it < kTokMaxHot * 4 / 1024; ++it) bld16_lds(rh, sh.h + 256 * it, 16 * (l + 64 * it));
+      if (has_cold) {
+        const rsrc_t rg = rsrc(a.hcs + ((size_t)L * kGroups + j0 / kGroup) * kBatch, kBatch * 4);
+#pragma unroll
+        for (int it = 0; it < 4; ++it) bld16_lds(rg, sh.it_hcs + 256 * it, 16 * (l + 64 * it));
+      }
+    }
+    float zl = 0.0f;
+    if (psel) {
+      const u32x4 zp = bld16(rsrc(a.z + (size_t)(L + 1) * 4 * kTokMaxRank, (uint32_t)N->rank * 16), 16 * (uint32_t)l);
+      zl = (as_f32(zp.x) + as_f32(zp.y)) + (as_f32(zp.z) + as_f32(zp.w));
     }
     if (l < kTokMaxRank) sh.z[l] = zl;
     wait_vm();
