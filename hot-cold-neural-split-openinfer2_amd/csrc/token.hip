@@ -22,8 +22,8 @@
 // control wave never has weight loads in flight ahead of the loads the
 // phase waits on, and the workers never wait on a cross-group input.
 // Worker loads, in issue order per layer: gather nibbles and half the next
-// gate/up rows (end of U, after the control wave has issued the phase's
-// stores: B3), the other half (D1a, once the phase's inputs are in), the next
+// gate/up rows (end of U, after the control wave's stores are acknowledged
+// and its arrival is issued: B3), the other half (D1a, once the phase's inputs are in), the next
 // chunk's records (D1b, once the control wave has computed the next list,
 // which overlaps the workers' down products), the next layer's first down row
 // (end of D), the gather items' slots and its other down rows (after the U
@@ -163,12 +163,24 @@ __device__ __forceinline__ void wait_vm() {
 // any D release of the launch can happen; the launch leaves base + n + 1).
 // Counter and flag comparisons are modulo 2^32.
 
-// Control wave: end of phase r (0 U, 1 D) for group g, epoch E.
-__device__ __forceinline__ void tok_arrive(uint32_t* sync, int r, int g, uint32_t e) {
+// Control wave: end of phase r (0 U, 1 D) for group g, epoch E.  With
+// `release_workers` the workgroup barrier that lets the worker waves issue
+// their next loads comes right after the first atomic is issued, so that the
+// atomic is ahead of those loads in the CU's memory pipeline.
+__device__ __forceinline__ void tok_arrive(uint32_t* sync, int r, int g, uint32_t e, bool release_workers = false) {
   asm volatile("s_waitcnt vmcnt(0) lgkmcnt(0)" ::: "memory");
+  // a zero the compiler takes for a per-lane value: with a per-lane address
+  // it leaves the one-lane atomic alone instead of broadcasting its result
+  // to the wave, which would wait for the result before the barrier
+  uint32_t zo;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(zo));
+  uint32_t o1 = 0u;
+  if (lane_id() == 0)
+    o1 = __hip_atomic_fetch_add(sync + kSyncXcd + 64 * (8 * r + (g & 7)) + zo, 1u, __ATOMIC_RELAXED,
+                                __HIP_MEMORY_SCOPE_AGENT);
+  if (release_workers) bar();
+  asm volatile("" : "+v"(o1));   // the result is first touched here, past the barrier
   if (lane_id() == 0) {
-    const uint32_t o1 = __hip_atomic_fetch_add(sync + kSyncXcd + 64 * (8 * r + (g & 7)), 1u,
-                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (o1 + 1 == (uint32_t)kPerXcd * e) {
       const uint32_t o2 = __hip_atomic_fetch_add(sync + kSyncAll + 64 * r, 1u, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_AGENT);
@@ -479,8 +491,9 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
         }
       }
     }
-    bar();   // B3: the stores are issued, ahead of the workers' next loads
-    tok_arrive(a.sync, 0, g, base + (uint32_t)(L + 2));
+    // B3 (inside): the stores are acknowledged and the arrival is issued,
+    // ahead of the workers' next loads
+    tok_arrive(a.sync, 0, g, base + (uint32_t)(L + 2), true);
 
     // ================= D phase of layer L (L = -1: only layer 0's selection)
     const bool psel = N && N->pd_w;                      // the next layer's list is predicted
