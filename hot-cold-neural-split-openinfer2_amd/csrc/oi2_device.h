@@ -62,17 +62,22 @@ __device__ __forceinline__ float bf16_bits_to_float(uint16_t b) {
 
 // Signed INT4 nibbles of one dword as exact fp16 pairs, splitter.py:111-124:
 // byte b holds element 2k in bits 0-3 and 2k+1 in bits 4-7, two's complement.
-// Bias each nibble by 8 (xor), place it in the mantissa of 1024.0 (0x6400),
-// then subtract 1032: the result is the signed value, exactly.
-// Output pairs: p[0] = (e0, e4), p[1] = (e1, e5), p[2] = (e2, e6), p[3] = (e3, e7).
+// Output pairs: p[0] = (e0, e4), p[1] = (e1, e5), p[2] = (e2, e6), p[3] = (e3, e7),
+// nibble k & 1 of each 16-bit half of d >> (8 (k >> 1)).
+// A nibble at bits 0-3 of a half, its top bit flipped (n + 8, 0..15), in the
+// mantissa of 1024.0 (0x6400) reads 1024 + n + 8: one and-xor,
+// ((d & 0x000F000F) ^ 0x64086408), then - 1032.  A nibble at bits 4-7 reads
+// 1024 + 16 (n + 8) the same way ((d & 0x00F000F0) ^ 0x64806480); times
+// 1/16 minus 72 it is n.  Every step is exact in fp16.
 __device__ __forceinline__ void int4x8_to_f16x2x4(uint32_t d, f16x2 p[4]) {
-  const uint32_t t = d ^ 0x88888888u;
-  const f16x2 bias = {(_Float16)-1032.0f, (_Float16)-1032.0f};
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const uint32_t m = ((t >> (4 * k)) & 0x000F000Fu) | 0x64006400u;
-    p[k] = __builtin_bit_cast(f16x2, m) + bias;
-  }
+  const f16x2 b0 = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+  const f16x2 s1 = {(_Float16)0.0625f, (_Float16)0.0625f};
+  const f16x2 b1 = {(_Float16)-72.0f, (_Float16)-72.0f};
+  const uint32_t d8 = d >> 8;
+  p[0] = __builtin_bit_cast(f16x2, (d & 0x000F000Fu) ^ 0x64086408u) + b0;
+  p[1] = __builtin_elementwise_fma(__builtin_bit_cast(f16x2, (d & 0x00F000F0u) ^ 0x64806480u), s1, b1);
+  p[2] = __builtin_bit_cast(f16x2, (d8 & 0x000F000Fu) ^ 0x64086408u) + b0;
+  p[3] = __builtin_elementwise_fma(__builtin_bit_cast(f16x2, (d8 & 0x00F000F0u) ^ 0x64806480u), s1, b1);
 }
 
 __device__ __forceinline__ float dot2(f16x2 a, f16x2 b, float c) {
