@@ -198,7 +198,7 @@ constexpr int kTokMaxHot = 4096;           // h staged in LDS; also the per-laye
 constexpr int kTokBatch = 896;             // gather items the worker waves take per layer (list order)
 constexpr int kTokSyncWords = 2048 + 192;
 constexpr int kTokSyncErr = 2048 + 128;       // epoch base + 1 of a launch whose wait ran past its bound
-constexpr int kTokSyncGoD = 64 * 8;           // the D phase's release flag of XCD 0
+constexpr int kTokSyncGoD = 64 * 8;           // XCD 0's flag of the D phase
 
 // One layer as the token kernel reads it (a device-resident table).
 struct TokLayer {

@@ -887,7 +887,7 @@ int oi2_stack_status(oi2_stack* s, void* stream) {
   OI2_CHECK_HIP(hipStreamSynchronize((hipStream_t)stream));
   if (!use_tok(s)) return OI2_OK;
   // the error word holds (epoch base + 1) of a launch whose wait ran past its
-  // bound; the last launch's base is the D release flag's value minus the
+  // bound; the last launch's base is XCD 0's D flag minus the
   // epochs of one launch (n_layers + 1)
   uint32_t err = 0, go = 0;
   OI2_CHECK_HIP(hipMemcpy(&err, s->tok_sync + kTokSyncErr, 4, hipMemcpyDeviceToHost));

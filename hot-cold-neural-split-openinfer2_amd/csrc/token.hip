@@ -34,9 +34,10 @@
 // a CU's memory pipeline is in order, and a backlog of weight loads ahead of
 // those inputs would delay the whole phase.
 //
-// Signals: per-XCD arrival counters (32 groups each), then one counter per
-// phase, whose last arrival writes a per-XCD release flag that the groups of
-// that XCD poll; the signal words are accessed agent-coherently (sc1).  Data
+// Signals: per-XCD arrival counters (32 groups each); the last arrival of an
+// XCD writes that XCD's flag for the phase, and a waiting group polls all 8
+// flags with one load (lane l reads XCD l & 7's).  No signal takes a second,
+// cross-XCD atomic.  The signal words are accessed agent-coherently (sc1).  Data
 // that crosses groups inside the launch (h, h_cold, z, x, x * w, the
 // partials, the active lists) is stored write-through (sc1), and a control
 // wave signals only after s_waitcnt vmcnt(0) on its stores.  Every such
@@ -58,8 +59,8 @@ namespace oi2 {
 namespace {
 
 constexpr int kPerXcd = kTokGroups / 8;
-constexpr int kSyncGo = 0, kSyncXcd = 1024, kSyncAll = 2048, kSyncErr = kTokSyncErr;
-static_assert(kTokSyncGoD == kSyncGo + 64 * 8, "the host reads the D release flag of XCD 0");
+constexpr int kSyncGo = 0, kSyncXcd = 1024, kSyncErr = kTokSyncErr;
+static_assert(kTokSyncGoD == kSyncGo + 64 * 8, "the host reads the D flag of XCD 0");
 constexpr int kSc1 = 16;                       // cache-policy operand: agent-coherent access
 constexpr int kWorkers = kTokThreads / kWave - 1;
 constexpr int kColdR = 1;                      // cold records per worker (items wi + 7 i)
@@ -159,8 +160,9 @@ __device__ __forceinline__ void wait_vm() {
 
 // Signal epochs count on across launches, so the signal words are never
 // cleared: a launch's epoch e of a phase is E = base + e, base being the D
-// release flag's value when the launch starts (every group reads it before
-// any D release of the launch can happen; the launch leaves base + n + 1).
+// flag of the group's XCD when the launch starts (a group reads it before its
+// own first arrival, so before that flag can move; the launch leaves every
+// flag at base + n + 1).
 // Counter and flag comparisons are modulo 2^32.
 
 // Control wave: end of phase r (0 U, 1 D) for group g, epoch E.  With
@@ -180,23 +182,18 @@ __device__ __forceinline__ void tok_arrive(uint32_t* sync, int r, int g, uint32_
                                 __HIP_MEMORY_SCOPE_AGENT);
   if (release_workers) bar();
   asm volatile("" : "+v"(o1));   // the result is first touched here, past the barrier
-  if (lane_id() == 0) {
-    if (o1 + 1 == (uint32_t)kPerXcd * e) {
-      const uint32_t o2 = __hip_atomic_fetch_add(sync + kSyncAll + 64 * r, 1u, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
-      if (o2 + 1 == 8u * e)
-        for (int x = 0; x < 8; ++x) cst(sync + kSyncGo + 64 * (8 * r + x), e);
-    }
-  }
+  if (lane_id() == 0 && o1 + 1 == (uint32_t)kPerXcd * e)   // the XCD's last arrival
+    cst(sync + kSyncGo + 64 * (8 * r + (g & 7)), e);
 }
 
 // Control wave: wait until every group has ended epoch E of phase r.  Past
 // `spin` polls it records the launch (base + 1) in the error word and goes
 // on; so do the waits of other groups once they see that record.
 __device__ __forceinline__ void tok_wait(uint32_t* sync, int r, int g, uint32_t e, uint32_t base, uint32_t spin) {
-  const uint32_t* go = sync + kSyncGo + 64 * (8 * r + (g & 7));
+  (void)g;
+  const uint32_t* xf = sync + kSyncGo + 64 * (8 * r + (lane_id() & 7));   // lane l: XCD l & 7
   uint32_t n = 0;
-  while ((int32_t)(cld(go) - e) < 0) {
+  while (__builtin_amdgcn_ballot_w64((int32_t)(cld(xf) - e) < 0) != 0) {
     __builtin_amdgcn_s_sleep(1);
     if (++n >= spin) {
       cst(sync + kSyncErr, base + 1u);
