@@ -648,7 +648,7 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
       }
       if (l == 0) cst4(rsrc(N->sel_counts, kTokChunks * 4), 4 * (uint32_t)g, (uint32_t)c);
     }
-    bar();   // D2: the workers' row sums are in LDS
+    // the epilogue: the workers' row sums were in LDS at D1b
     if (T) {
       if (l < kRows) {
         const float y = (((sh.cpart[0][l] + sh.cpart[1][l]) + (sh.cpart[2][l] + sh.cpart[3][l])) +
@@ -674,6 +674,7 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       if (l == 0) cst4(rsrc(a.ssq, kTokGroups * 4), 4 * (uint32_t)tile, as_u32(ssq16(sh.out)));
     }
+    bar();   // D2: the phase's stores are issued, ahead of the workers' next loads
     tok_arrive(a.sync, 1, g, base + (uint32_t)(L + 2));
   }
 }
