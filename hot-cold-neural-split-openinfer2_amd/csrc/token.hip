@@ -23,12 +23,13 @@
 // phase waits on, and the workers never wait on a cross-group input.
 // Worker loads, in issue order per layer: gather nibbles and half the next
 // gate/up rows (end of U, after the control wave's stores are acknowledged
-// and its arrival is issued: B3), the other half (D1a, once the phase's inputs are in), the next
-// chunk's records (D1b, once the control wave has computed the next list,
-// which overlaps the workers' down products), the next layer's first down row
-// (end of D), the gather items' slots and its other down rows (after the U
-// products: issued earlier they would stall those products while the CU's
-// memory queue is full).  Each
+// and its arrival is issued: B3), the other half (D1a, once the phase's
+// inputs are in), then at the end of D (D2, once the control wave has
+// computed the next list, which overlaps the workers' down products, and
+// issued the phase's stores) the next chunk's records and the next layer's
+// first down rows, and the gather items' slots and the other down rows after
+// the U products (issued earlier they would stall those products while the
+// CU's memory queue is full).  Each
 // phase's compute needs only loads older than the ones still streaming, and
 // the halves issued at B1 / D1 go out after the phase's cross-group inputs:
 // a CU's memory pipeline is in order, and a backlog of weight loads ahead of
@@ -684,7 +685,7 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
 // Every worker load is unconditional (absent data reads as zero through an
 // empty or short descriptor) and issued in the same order each layer --
 // gather nibbles, next gate/up rows (end of U and D1a), next chunk's records
-// (D1b), next down rows (end of D) -- so the compiler can wait for exactly
+// and down rows (end of D) -- so the compiler can wait for exactly
 // the loads a compute step needs and leave the younger ones streaming.
 template <int NPW>
 __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
@@ -959,8 +960,8 @@ __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
       }
     }
     bar();   // D1b: the next chunk's list (computed meanwhile) is in LDS
+    bar();   // D2: the control wave's stores of the phase are issued
     load_records(L + 1);
-    bar();   // D2
     load_down(L + 1, 0, 6);      // the next layer's first down rows (the rest after the U products)
   }
 }
