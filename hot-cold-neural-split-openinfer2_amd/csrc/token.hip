@@ -953,11 +953,8 @@ __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
           }
         }
       }
-      wave_sums_to_last(yc);
-      if (l == kWave - 1) {
-#pragma unroll
-        for (int e = 0; e < kRows; ++e) sh.cpart[wi][e] = yc[e];
-      }
+      const float yt = wave_sums16_transposed(yc);   // lane l: row l & 15
+      if (l < kRows) sh.cpart[wi][l] = yt;
     }
     bar();   // D1b: the next chunk's list (computed meanwhile) is in LDS
     bar();   // D2: the control wave's stores of the phase are issued
