@@ -27,9 +27,10 @@
 // inputs are in), then at the end of D (D2, once the control wave has
 // computed the next list, which overlaps the workers' down products, and
 // issued the phase's stores) the next chunk's records and the next layer's
-// first down rows, and the gather items' slots and the other down rows after
-// the U products (issued earlier they would stall those products while the
-// CU's memory queue is full).  Each
+// first down rows; the gather items' slots at B1 (a few loads, found by an
+// LDS search that the SIMD's other wave overlaps with its products), and the
+// other down rows after the U products (issued earlier they would stall
+// those products while the CU's memory queue is full).  Each
 // phase's compute needs only loads older than the ones still streaming, and
 // the halves issued at B1 / D1 go out after the phase's cross-group inputs:
 // a CU's memory pipeline is in order, and a backlog of weight loads ahead of
@@ -820,6 +821,7 @@ __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
     const bool has_cold = T && T->n_records > 0 && T->act_counts;
     // ================= U phase
     bar();   // B1: the control's inputs have landed
+    load_slots(L);               // the slots of this lane's gather items (the prefix is in LDS)
     if (T) {
       const float r = sh.r;
       // hot neurons (the accumulation order of the two-launch path)
@@ -892,7 +894,6 @@ __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
         }
       }
     }
-    load_slots(L);               // the slots of this lane's gather items,
     load_down(L, 6, kRows);      // the rest of this layer's down rows
     bar();   // B2
     bar();   // B3
