@@ -42,7 +42,7 @@ HBM_PEAK_GBS = 8000.0
 # (FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000 KiB, the factors being what each
 # counter reads for a plain 256 MiB copy, --copy-calibration)
 UP_TRAFFIC_BYTES = (16570.2 * 2.0 + 2084.7) * 1024       # k_ffn_up
-TOKEN_TRAFFIC_BYTES = (800557.2 * 2.0 + 14292.8) * 1024     # k_token
+TOKEN_TRAFFIC_BYTES = (800563.6 * 2.0 + 14292.8) * 1024     # k_token
 
 
 def log(msg):
