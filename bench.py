@@ -50,20 +50,8 @@ def log(msg):
 
 
 def build_stack(seed, dev):
-    import torch
-    from oi2.stack import DecodeStack, StackLayer
-    from oi2.synth import SyntheticLayer, calibrate_threshold
-    g = torch.Generator(device=dev).manual_seed(seed)
-    layers = []
-    for i in range(N_LAYERS):
-        layers.append(SyntheticLayer(g, INTER, N_HOT, std=0.02, device=dev, with_predictor=True,
-                                     pred_rank=RANK, pred_dtype=torch.bfloat16))
-    thr = calibrate_threshold(layers, g, ACTIVE_FRAC)
-    st = DecodeStack([StackLayer(l.hot, l.records, l.lut, l.norm_w, l.predictor) for l in layers],
-                     INTER, EPS, "silu", False, thr)
-    # size the cold pass for the calibrated active fraction with headroom
-    st.set_expected_active(int(1.3 * ACTIVE_FRAC * (INTER - N_HOT)))
-    return layers, st, thr, g
+    from oi2.synth import build_decode_stack
+    return build_decode_stack(seed, dev, N_LAYERS, INTER, N_HOT, RANK, ACTIVE_FRAC, EPS)
 
 
 def up_launch_bytes(active):
@@ -359,6 +347,7 @@ def main():
         for i in range(args.warmup):
             st.decode(bufs[i % 2], bufs[(i + 1) % 2], stream)
     stream.synchronize()
+    st.status(stream)          # raises if any warmup token's device-wide wait ran past its bound
     torch.cuda.synchronize()
     log(f"warmup {args.warmup} tokens done")
 
@@ -376,6 +365,7 @@ def main():
     stream.synchronize()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t_start
+    st.status(stream)          # every timed token's waits ended within their bound
     gpu_ms = ev0.elapsed_time(ev1)
     secs = max(wall, gpu_ms / 1e3)
     tok_s = args.steps / secs

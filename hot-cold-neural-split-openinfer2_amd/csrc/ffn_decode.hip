@@ -272,11 +272,14 @@ __device__ void pred_d_role_t(const UpArgs& a, int row) {
   const float r = norm ? r_from_part(part, a.tok.eps) : 1.0f;
   // four partial sums, one per quarter of the row (elements [1024 q, 1024 q +
   // 1024)), combined as (p0 + p1) + (p2 + p3): the persistent token kernel
-  // splits a row over four workgroups in exactly this order
-  float accq[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  // splits a row over four workgroups in exactly this order.  Double
+  // precision: each product of two floats is exact in a double, and the
+  // logits built from z stay within ~1e-15 of exact arithmetic, far inside
+  // the 1e-6 band the active-set contract exempts.
+  double accq[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
   for (int it = 0; it < 8; ++it) {
-    float& acc = accq[it >> 1];
+    double& acc = accq[it >> 1];
     const int e0 = 8 * (lane + 64 * it);
     float q[8];
     if (a.pd_q) {
@@ -297,8 +300,8 @@ __device__ void pred_d_role_t(const UpArgs& a, int row) {
     if constexpr (BF16) {
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
-        acc = fmaf(bf16_bits_to_float((uint16_t)(dw.v[it][d] & 0xFFFFu)), q[2 * d], acc);
-        acc = fmaf(bf16_bits_to_float((uint16_t)(dw.v[it][d] >> 16)), q[2 * d + 1], acc);
+        acc = fma((double)bf16_bits_to_float((uint16_t)(dw.v[it][d] & 0xFFFFu)), (double)q[2 * d], acc);
+        acc = fma((double)bf16_bits_to_float((uint16_t)(dw.v[it][d] >> 16)), (double)q[2 * d + 1], acc);
       }
     } else {
       const float* drow = reinterpret_cast<const float*>(a.pd_w) + (size_t)row * kH;
@@ -306,12 +309,12 @@ __device__ void pred_d_role_t(const UpArgs& a, int row) {
       const f32x4 d1 = *reinterpret_cast<const f32x4*>(drow + e0 + 4);
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        acc = fmaf(d0[k], q[k], acc);
-        acc = fmaf(d1[k], q[4 + k], acc);
+        acc = fma((double)d0[k], (double)q[k], acc);
+        acc = fma((double)d1[k], (double)q[4 + k], acc);
       }
     }
   }
-  const float z = (wave_sum(accq[0]) + wave_sum(accq[1])) + (wave_sum(accq[2]) + wave_sum(accq[3]));
+  const double z = (wave_sum_d(accq[0]) + wave_sum_d(accq[1])) + (wave_sum_d(accq[2]) + wave_sum_d(accq[3]));
   if (lane == 0) a.pd_z[row] = z;
 }
 
@@ -425,12 +428,13 @@ __device__ void pred_u_role(const DownArgs& a, int c, int* s_wcnt) {
   bool keep = false;
   const int lutv = (n < a.inter && a.lut) ? a.lut[n] : n;
   if (n < a.inter) {
-    // the row in batches of 64 rank entries, each batch's loads issued together
-    float logit;
-    float acc = 0.0f;
+    // the row in batches of 64 rank entries, each batch's loads issued
+    // together; the sum and the threshold test in double precision
+    double logit;
+    double acc = 0.0;
     if (a.pu_bf16) {
       const uint16_t* urow = reinterpret_cast<const uint16_t*>(a.pu_w) + (size_t)n * a.pu_rank;
-      const float bias = bf16_bits_to_float(reinterpret_cast<const uint16_t*>(a.pu_b)[n]);
+      const double bias = bf16_bits_to_float(reinterpret_cast<const uint16_t*>(a.pu_b)[n]);
       for (int rb = 0; rb < a.pu_rank; rb += 64) {
         u32x4 uv[8];
 #pragma unroll
@@ -443,15 +447,15 @@ __device__ void pred_u_role(const DownArgs& a, int c, int* s_wcnt) {
 #pragma unroll
           for (int d = 0; d < 4; ++d) {
             const int r = rb + 8 * k + 2 * d;
-            acc = fmaf(bf16_bits_to_float((uint16_t)(uv[k][d] & 0xFFFFu)), a.pd_z[r], acc);
-            acc = fmaf(bf16_bits_to_float((uint16_t)(uv[k][d] >> 16)), a.pd_z[r + 1], acc);
+            acc = fma((double)bf16_bits_to_float((uint16_t)(uv[k][d] & 0xFFFFu)), a.pd_z[r], acc);
+            acc = fma((double)bf16_bits_to_float((uint16_t)(uv[k][d] >> 16)), a.pd_z[r + 1], acc);
           }
         }
       }
       logit = acc + bias;
     } else {
       const float* urow = reinterpret_cast<const float*>(a.pu_w) + (size_t)n * a.pu_rank;
-      const float bias = reinterpret_cast<const float*>(a.pu_b)[n];
+      const double bias = reinterpret_cast<const float*>(a.pu_b)[n];
       for (int rb = 0; rb < a.pu_rank; rb += 64) {
         f32x4 uv[16];
 #pragma unroll
@@ -462,14 +466,15 @@ __device__ void pred_u_role(const DownArgs& a, int c, int* s_wcnt) {
         for (int k = 0; k < 16; ++k) {
           if (rb + 4 * k >= a.pu_rank) break;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) acc = fmaf(uv[k][e], a.pd_z[rb + 4 * k + e], acc);
+          for (int e = 0; e < 4; ++e) acc = fma((double)uv[k][e], a.pd_z[rb + 4 * k + e], acc);
         }
       }
       logit = acc + bias;
     }
-    if (a.logits_out) a.logits_out[n] = logit;
-    if (a.probs_out) a.probs_out[n] = 1.0f / (1.0f + __expf(-logit));
-    const bool fire = logit >= a.thr;
+    const float logit32 = (float)logit;
+    if (a.logits_out) a.logits_out[n] = logit32;
+    if (a.probs_out) a.probs_out[n] = 1.0f / (1.0f + __expf(-logit32));
+    const bool fire = logit >= (double)a.thr;
     if (a.mask_out) a.mask_out[n] = fire ? 1 : 0;
     keep = fire && lutv >= 0;
   }
@@ -781,6 +786,40 @@ __global__ __launch_bounds__(kThreads) void k_query(const uint16_t* x, int rows,
   }
 }
 
+// One hidden-state row of any supported dtype cast to the predictor dtype
+// (predictor.py:455: hidden_state.to(parameter dtype)), as fp32 values: fp16
+// and bf16 widen exactly; fp32 is kept, or rounded to bf16 for a bf16
+// predictor.  One workgroup, 16 elements per thread.
+__global__ __launch_bounds__(kThreads) void k_cast_query(const void* h, int h_dtype, int to_bf16,
+                                                         float* q) {
+  const int e0 = 16 * threadIdx.x;
+  float v[16];
+  if (h_dtype == OI2_DTYPE_F32) {
+    const f32x4* p = reinterpret_cast<const f32x4*>(reinterpret_cast<const float*>(h) + e0);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const f32x4 t = p[m];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[4 * m + k] = t[k];
+    }
+  } else if (h_dtype == OI2_DTYPE_BF16) {
+    const u32x4* p = reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(h) + e0);
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      const u32x4 t = p[m];
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        v[8 * m + 2 * d] = bf16_bits_to_float((uint16_t)(t[d] & 0xFFFFu));
+        v[8 * m + 2 * d + 1] = bf16_bits_to_float((uint16_t)(t[d] >> 16));
+      }
+    }
+  } else {
+    load_h16(reinterpret_cast<const uint16_t*>(h), e0, v);
+  }
+#pragma unroll
+  for (int e = 0; e < 16; ++e) q[e0 + e] = to_bf16 ? round_bf16(v[e]) : v[e];
+}
+
 // Chunked selection -> dense ascending list + total.  One workgroup.
 __global__ __launch_bounds__(kThreads) void k_compact_dense(const int32_t* slots, const int32_t* ids,
                                                             const int32_t* counts, int n_chunks,
@@ -1016,15 +1055,20 @@ int oi2_ffn_forward(const uint16_t* x, int32_t batch, const uint16_t* norm_w, fl
   return OI2_OK;
 }
 
+// Predictor workspace: the query q (H floats), z (rank + 64 doubles), the
+// norm's sum-of-squares partials (kDownWG floats).
+static size_t pred_ws_z_off() { return (size_t)kH * sizeof(float); }
+static size_t pred_ws_ssq_off(int rank) { return pred_ws_z_off() + (size_t)(rank + 64) * sizeof(double); }
+
 size_t oi2_predict_workspace_bytes(const oi2_predictor* p) {
   const int rank = p ? p->rank : 256;
-  return (size_t)(kH + rank + 64 + kDownWG) * sizeof(float);
+  return pred_ws_ssq_off(rank) + (size_t)kDownWG * sizeof(float);
 }
 
 int launch_predictor(const TokenIn& tok, const uint16_t* norm_w, const float* q,
                      const oi2_predictor* p, float thr, const int32_t* lut, int32_t* slots,
                      int32_t* ids, int32_t* counts, float* logits, float* probs, uint8_t* mask,
-                     float* z, hipStream_t st) {
+                     double* z, hipStream_t st) {
   UpArgs ua{};
   ua.tok = tok;
   ua.pd_w = p->down_w;
@@ -1058,25 +1102,33 @@ int launch_predictor(const TokenIn& tok, const uint16_t* norm_w, const float* q,
   return OI2_OK;
 }
 
-int oi2_predict(const uint16_t* h, int32_t rows, const oi2_predictor* p, float threshold_logit,
-                float* logits, float* probs, uint8_t* mask, void* workspace,
-                size_t workspace_bytes, void* stream) {
+int oi2_predict(const void* h, int32_t h_dtype, int32_t rows, const oi2_predictor* p,
+                float threshold_logit, float* logits, float* probs, uint8_t* mask,
+                void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
   OI2_CHECK_ARG(rows >= 0, "rows must be >= 0");
+  OI2_CHECK_ARG(h_dtype == OI2_DTYPE_F16 || h_dtype == OI2_DTYPE_F32 || h_dtype == OI2_DTYPE_BF16,
+                "h_dtype %d is not OI2_DTYPE_F16, _F32 or _BF16", h_dtype);
   int rc = validate_pred(p);
   if (rc) return rc;
   if (rows == 0) return OI2_OK;
   OI2_CHECK_ARG(h && (uintptr_t)h % 16 == 0, "h must be non-null and 16-byte aligned");
   OI2_CHECK_ARG(workspace && workspace_bytes >= oi2_predict_workspace_bytes(p),
                 "predict workspace too small");
-  float* z = reinterpret_cast<float*>(workspace) + kH;
+  hipStream_t st = (hipStream_t)stream;
+  float* q = reinterpret_cast<float*>(workspace);
+  double* z = reinterpret_cast<double*>(reinterpret_cast<uint8_t*>(workspace) + pred_ws_z_off());
+  const size_t row_bytes = (size_t)kH * (h_dtype == OI2_DTYPE_F32 ? 4 : 2);
   for (int b = 0; b < rows; ++b) {
-    const uint16_t* hb = h + (size_t)b * kH;
-    rc = launch_predictor(TokenIn{hb, nullptr, nullptr, 0.0f, 0}, nullptr, nullptr, p,
+    const void* hb = reinterpret_cast<const uint8_t*>(h) + (size_t)b * row_bytes;
+    hipLaunchKernelGGL(k_cast_query, dim3(1), dim3(kThreads), 0, st, hb, (int)h_dtype,
+                       p->dtype == OI2_DTYPE_BF16 ? 1 : 0, q);
+    OI2_CHECK_LAUNCH();
+    rc = launch_predictor(TokenIn{nullptr, nullptr, nullptr, 0.0f, 0}, nullptr, q, p,
                           threshold_logit, nullptr, nullptr, nullptr, nullptr,
                           logits ? logits + (size_t)b * p->inter : nullptr,
                           probs ? probs + (size_t)b * p->inter : nullptr,
-                          mask ? mask + (size_t)b * p->inter : nullptr, z, (hipStream_t)stream);
+                          mask ? mask + (size_t)b * p->inter : nullptr, z, st);
     if (rc) return rc;
   }
   return OI2_OK;
@@ -1099,8 +1151,8 @@ int oi2_predict_select(const uint16_t* x, int32_t batch, const uint16_t* norm_w,
                 "predict workspace too small");
   hipStream_t st = (hipStream_t)stream;
   float* q = reinterpret_cast<float*>(workspace);
-  float* z = q + kH;
-  float* ssq = z + p->rank + 64;
+  double* z = reinterpret_cast<double*>(reinterpret_cast<uint8_t*>(workspace) + pred_ws_z_off());
+  float* ssq = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + pred_ws_ssq_off(p->rank));
   const float* qp = nullptr;
   if (batch > 1) {
     hipLaunchKernelGGL(k_query, dim3(1), dim3(kThreads), 0, st, x, batch, norm_w, eps,

@@ -58,7 +58,7 @@ struct UpArgs {
   int pd_bf16;
   const uint16_t* pd_norm_w;  // null: q = cast(x)
   const float* pd_q;          // precomputed query (H), or null
-  float* pd_z;
+  double* pd_z;
   int wg_cold, wg_pred, wg_hot;
 };
 
@@ -88,7 +88,7 @@ struct DownArgs {
   int pu_rank;
   int pu_bf16;
   int inter;
-  const float* pd_z;
+  const double* pd_z;
   float thr;
   const int32_t* lut;
   int32_t* sel_slots;
@@ -243,7 +243,7 @@ struct TokArgs {
   float* ssq;               // (n_layers, 256) sum-of-squares partials of x_L
   float* h;                 // (n_layers, kTokMaxHot) hot activations, zero past n_hot
   float* hc;                // (n_layers, kTokChunks * kTokMaxChunk) cold activations, list order
-  float* z;                 // (n_layers, 4 * kTokMaxRank) predictor down projection of layer L:
+  double* z;                // (n_layers, 4 * kTokMaxRank) predictor down projection of layer L:
                             // quarter q of row r at 4 r + q
   float* hcs;               // (n_layers, kGroups, kTokBatch) cold activation x down scale of each
                             // row group, list positions < kTokBatch

@@ -40,7 +40,7 @@ struct oi2_stack {
   float* cold_part = nullptr;    // (kMaxColdWG, H) partial rows of the current layer
   int32_t* cold_total = nullptr;
   int cold_cap = 0;
-  float* z = nullptr;
+  double* z = nullptr;
   int32_t* sel_counts = nullptr; // (n_layers, n_chunks)
   int32_t* sel_slots = nullptr;  // (n_layers, n_chunks * 256)
   int32_t* sel_ids = nullptr;
@@ -75,7 +75,7 @@ struct oi2_stack {
   float* tok_ssq = nullptr;
   float* tok_h = nullptr;
   float* tok_hc = nullptr;
-  float* tok_z = nullptr;
+  double* tok_z = nullptr;
   float* tok_hcs = nullptr;
   int32_t* tok_sel_counts = nullptr;
   int32_t* tok_sel_slots = nullptr;
@@ -457,7 +457,7 @@ static int tok_setup(oi2_stack* s) {
   alloc((void**)&s->tok_ssq, (size_t)n * kTokGroups * 4);
   alloc((void**)&s->tok_h, (size_t)n * kTokMaxHot * 4);
   alloc((void**)&s->tok_hc, (size_t)n * kTokChunks * kTokMaxChunk * 4);
-  alloc((void**)&s->tok_z, (size_t)n * 4 * kTokMaxRank * 4);
+  alloc((void**)&s->tok_z, (size_t)n * 4 * kTokMaxRank * sizeof(double));
   alloc((void**)&s->tok_hcs, (size_t)n * kGroups * kTokBatch * 4);
   alloc((void**)&s->tok_sel_counts, (size_t)n * kTokChunks * 4);
   alloc((void**)&s->tok_sel_slots, sel * 4);
@@ -628,7 +628,7 @@ int oi2_stack_create(const oi2_layer* layers, int32_t n_layers, int32_t inter, f
   alloc((void**)&s->h_hot, (size_t)(s->max_hot + 64) * 4);
   alloc((void**)&s->cold_part, (size_t)kMaxColdWG * kH * 4);
   alloc((void**)&s->cold_total, 64);
-  alloc((void**)&s->z, (size_t)(s->max_rank + 64) * 4);
+  alloc((void**)&s->z, (size_t)(s->max_rank + 64) * sizeof(double));
   alloc((void**)&s->sel_counts, (size_t)n_layers * s->n_chunks * 4);
   alloc((void**)&s->sel_slots, sel * 4);
   alloc((void**)&s->sel_ids, sel * 4);
@@ -886,17 +886,18 @@ int oi2_stack_status(oi2_stack* s, void* stream) {
   OI2_CHECK_ARG(s, "null stack");
   OI2_CHECK_HIP(hipStreamSynchronize((hipStream_t)stream));
   if (!use_tok(s)) return OI2_OK;
-  // the error word holds (epoch base + 1) of a launch whose wait ran past its
-  // bound; the last launch's base is XCD 0's D flag minus the
-  // epochs of one launch (n_layers + 1)
-  uint32_t err = 0, go = 0;
+  // the error word is nonzero once any launch since the signal words were
+  // last cleared had a wait run past its bound (it holds that launch's epoch
+  // base + 1); it stays set until reported here, so an overrun in any token
+  // since the previous status call is reported, not only in the last one
+  uint32_t err = 0;
   OI2_CHECK_HIP(hipMemcpy(&err, s->tok_sync + kTokSyncErr, 4, hipMemcpyDeviceToHost));
-  OI2_CHECK_HIP(hipMemcpy(&go, s->tok_sync + kTokSyncGoD, 4, hipMemcpyDeviceToHost));
-  if (err != 0 && err == go - (uint32_t)(s->n_layers + 1) + 1u) {
+  if (err != 0) {
     // a wait that gave up lets its group run ahead of an epoch, so the
     // counters may no longer line up with the epochs: start them over
     OI2_CHECK_HIP(hipMemset(s->tok_sync, 0, (size_t)kTokSyncWords * 4));
-    set_error("persistent token kernel: a device-wide wait ran past its bound");
+    set_error("persistent token kernel: a device-wide wait ran past its bound in a token "
+              "decoded since the previous status check");
     return OI2_EHIP;
   }
   return OI2_OK;

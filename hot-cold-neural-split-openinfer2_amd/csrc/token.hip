@@ -129,6 +129,16 @@ __device__ __forceinline__ void cst2(rsrc_t r, uint32_t off, uint16_t v) {
 __device__ __forceinline__ void cst4(rsrc_t r, uint32_t off, uint32_t v) {
   __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, kSc1);
 }
+__device__ __forceinline__ void cst8(rsrc_t r, uint32_t off, double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  u32x2v w;
+  w.x = (uint32_t)u;
+  w.y = (uint32_t)(u >> 32);
+  __builtin_amdgcn_raw_buffer_store_b64(w, r, off, 0, kSc1);
+}
+__device__ __forceinline__ double as_f64(uint32_t lo, uint32_t hi) {
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
 template <typename T>
 __device__ __forceinline__ T cld(const T* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -229,7 +239,7 @@ struct alignas(16) TokShared {
   float cpart[kWorkers][kRows];
   float cpart_ctl[kRows];     // the control wave's share of long gather lists
   float out[kRows];
-  float z[kTokMaxRank];
+  double z[kTokMaxRank];
   float r;
   int total, lst_cnt;
 };
@@ -397,9 +407,9 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
     // a quarter of the next layer's predictor row: z = D q, q =
     // bf16(fp16(x r w')) (pred_d_role's arithmetic and partial sums);
     // stored with the phase's other outputs
-    float zrow = 0.0f;
+    double zrow = 0.0;
     if (pred) {
-      float acc = 0.0f;
+      double acc = 0.0;
 #pragma unroll
       for (int it = 0; it < 2; ++it) {
         const u32x4 xv = reinterpret_cast<const u32x4*>(sh.xq)[l + 64 * it];
@@ -409,11 +419,11 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
         for (int d = 0; d < 4; ++d) {
           const float q0 = round_bf16(xn_exact(half_lo(xv[d]), r, half_lo(wv[d])));
           const float q1 = round_bf16(xn_exact(half_hi(xv[d]), r, half_hi(wv[d])));
-          acc = fmaf(bf16_bits_to_float((uint16_t)(dv[d] & 0xFFFFu)), q0, acc);
-          acc = fmaf(bf16_bits_to_float((uint16_t)(dv[d] >> 16)), q1, acc);
+          acc = fma((double)bf16_bits_to_float((uint16_t)(dv[d] & 0xFFFFu)), (double)q0, acc);
+          acc = fma((double)bf16_bits_to_float((uint16_t)(dv[d] >> 16)), (double)q1, acc);
         }
       }
-      zrow = wave_sum(acc);
+      zrow = wave_sum_d(acc);
     }
     // the chunk's items past the workers' share (cold_role's arithmetic);
     // past kCtlCold more, one at a time
@@ -469,7 +479,7 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
     }
     bar();   // B2: the workers' activations are in LDS
     if (pred && l == 0)
-      cst4(rsrc(a.z + (size_t)(L + 1) * 4 * kTokMaxRank, 4 * kTokMaxRank * 4), 4 * (uint32_t)g, as_u32(zrow));
+      cst8(rsrc(a.z + (size_t)(L + 1) * 4 * kTokMaxRank, 4 * kTokMaxRank * 8), 8 * (uint32_t)g, zrow);
     if (T) {
       const int k = g * kWorkers * NPW + l;
       if (l < kWorkers * NPW && k < T->n_hot)
@@ -544,10 +554,11 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
         for (int it = 0; it < 4; ++it) bld16_lds(rg, sh.it_hcs + 256 * it, 16 * (l + 64 * it));
       }
     }
-    float zl = 0.0f;
+    double zl = 0.0;
     if (psel) {
-      const u32x4 zp = bld16(rsrc(a.z + (size_t)(L + 1) * 4 * kTokMaxRank, (uint32_t)N->rank * 16), 16 * (uint32_t)l);
-      zl = (as_f32(zp.x) + as_f32(zp.y)) + (as_f32(zp.z) + as_f32(zp.w));
+      const rsrc_t rz = rsrc(a.z + (size_t)(L + 1) * 4 * kTokMaxRank, (uint32_t)N->rank * 32);
+      const u32x4 za = bld16(rz, 32 * (uint32_t)l), zb = bld16(rz, 32 * (uint32_t)l + 16);
+      zl = (as_f64(za.x, za.y) + as_f64(za.z, za.w)) + (as_f64(zb.x, zb.y) + as_f64(zb.z, zb.w));
     }
     if (l < kTokMaxRank) sh.z[l] = zl;
     wait_vm();
@@ -561,18 +572,18 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
       const int rank = N->rank;
       bool keep = false;
       if (nn >= 0) {
-        float acc = 0.0f;
+        double acc = 0.0;
 #pragma unroll
         for (int m = 0; m < 8; ++m) {
           if (8 * m >= rank) break;
           const u32x4 pv = reinterpret_cast<const u32x4*>(sh.pu)[64 * m + l];
 #pragma unroll
           for (int d = 0; d < 4; ++d) {
-            acc = fmaf(bf16_bits_to_float((uint16_t)(pv[d] & 0xFFFFu)), sh.z[8 * m + 2 * d], acc);
-            acc = fmaf(bf16_bits_to_float((uint16_t)(pv[d] >> 16)), sh.z[8 * m + 2 * d + 1], acc);
+            acc = fma((double)bf16_bits_to_float((uint16_t)(pv[d] & 0xFFFFu)), sh.z[8 * m + 2 * d], acc);
+            acc = fma((double)bf16_bits_to_float((uint16_t)(pv[d] >> 16)), sh.z[8 * m + 2 * d + 1], acc);
           }
         }
-        keep = acc + bf16_bits_to_float(pbits) >= a.thr && plut >= 0;
+        keep = acc + (double)bf16_bits_to_float(pbits) >= (double)a.thr && plut >= 0;
       }
       const uint64_t bal = __ballot(keep);
       if (keep) {

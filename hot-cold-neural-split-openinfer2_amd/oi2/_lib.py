@@ -16,7 +16,8 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "liboi2.so")
 
 OI2_OK = 0
 ACT_SILU, ACT_RELU = 0, 1
-DTYPE_F32, DTYPE_BF16 = 0, 1
+DTYPE_F32, DTYPE_BF16, DTYPE_F16 = 0, 1, 2
+ABI_VERSION = 2
 HIDDEN = 4096
 SEL_CHUNK = 256
 
@@ -61,9 +62,14 @@ _SIGS = {
     "oi2_ffn_forward": (c_int32, [c_void_p, c_int32, c_void_p, c_float, POINTER(Hot), POINTER(Cold),
                                   POINTER(Active), c_int32, c_int32, c_int32, c_void_p, c_void_p,
                                   c_void_p, c_size_t, c_void_p]),
+    "oi2_sparse_ffn_dense_workspace_bytes": (c_size_t, [c_int32, c_int32, c_int32]),
+    "oi2_sparse_ffn_dense": (c_int32, [c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32,
+                                       c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p,
+                                       c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t,
+                                       c_void_p]),
     "oi2_predict_workspace_bytes": (c_size_t, [POINTER(Predictor)]),
-    "oi2_predict": (c_int32, [c_void_p, c_int32, POINTER(Predictor), c_float, c_void_p, c_void_p,
-                              c_void_p, c_void_p, c_size_t, c_void_p]),
+    "oi2_predict": (c_int32, [c_void_p, c_int32, c_int32, POINTER(Predictor), c_float, c_void_p,
+                              c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     "oi2_predict_select": (c_int32, [c_void_p, c_int32, c_void_p, c_float, POINTER(Predictor),
                                      c_float, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                      c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
@@ -107,7 +113,7 @@ def load_library():
             fn = getattr(lib, name)
             fn.restype = res
             fn.argtypes = args
-        if lib.oi2_abi_version() != 1:
+        if lib.oi2_abi_version() != ABI_VERSION:
             raise OI2Error("liboi2.so ABI version mismatch")
         _lib = lib
     return _lib
@@ -133,15 +139,53 @@ def ptr(t) -> int | None:
     return t.data_ptr()
 
 
+def dtype_code(dtype) -> int:
+    """The ABI's dtype code of a torch floating dtype (fp16, fp32, bf16)."""
+    codes = {torch.float16: DTYPE_F16, torch.float32: DTYPE_F32, torch.bfloat16: DTYPE_BF16}
+    if dtype not in codes:
+        raise TypeError(f"dtype {dtype} is not float16, float32 or bfloat16")
+    return codes[dtype]
+
+
 def stream_handle(device=None) -> int | None:
     s = torch.cuda.current_stream(device).cuda_stream
     return s or None
 
 
 def logit_threshold(p: float) -> float:
-    """sigmoid(l) >= p  <=>  l >= log(p / (1 - p))."""
+    """The logit cut the kernels apply for predict_mask's ``sigmoid(l) >= p``
+    (predictor.py:77-79): l >= log(p / (1 - p)) for 0 < p < 1.  At the edges
+    the reference's float32 sigmoid decides: p <= 0 passes every logit, p == 1
+    passes the logits whose float32 sigmoid rounds to 1.0 (l >= 16.6355...),
+    and p > 1 passes none."""
     if p <= 0.0:
         return -math.inf
-    if p >= 1.0:
+    if p > 1.0:
         return math.inf
+    if p == 1.0:
+        return _sigmoid_f32_cut(1.0)
     return math.log(p / (1.0 - p))
+
+
+def _sigmoid_f32_cut(p: float) -> float:
+    """Smallest float32 l with torch.sigmoid(l) >= p in float32, by bisection
+    over the ordered float32 bit patterns."""
+    def key_to_f(k):
+        u = (k ^ 0xFFFFFFFF) if not k >> 31 else (k & 0x7FFFFFFF)
+        return torch.tensor([u], dtype=torch.int64).to(torch.int32).view(torch.float32)
+
+    def passes(k):
+        return bool(torch.sigmoid(key_to_f(k))[0] >= p)
+
+    lo, hi = 0x007FFFFF, 0xFF800000           # keys of -inf and +inf
+    if passes(lo):
+        return -math.inf
+    if not passes(hi - 1):
+        return math.inf
+    while hi - lo > 1:
+        mid = (lo + hi) // 2
+        if passes(mid):
+            hi = mid
+        else:
+            lo = mid
+    return float(key_to_f(hi)[0])

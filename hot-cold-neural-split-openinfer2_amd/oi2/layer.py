@@ -2,7 +2,9 @@
 reference's call surface (engine.py:163-312), computed by the fused HIP
 kernels.
 
-Differences in representation, not in meaning:
+``sparse_ffn`` takes the reference's own dense tensors (fp16 hot, fp32 cold)
+and runs them through dense-weight GEMV kernels; the layer below keeps its
+weights in compact form.  Differences in representation, not in meaning:
   * hot weights stay fp8 in HBM (``HotWeights``) instead of being widened to
     fp16 at load (engine.py:258-260);
   * the cold "fetch" result is a ``ColdNeurons`` handle - the layer's resident
@@ -148,24 +150,89 @@ def _ffn(x2d, norm_w, eps, hot: HotWeights | None, cold: ColdNeurons | None, act
     return (out, y32) if want_y32 else out
 
 
-def sparse_ffn(x: torch.Tensor, activation: str, act_on_both: bool,
-               gate_hot: Optional[HotWeights], up_hot=None, down_hot=None,
-               gate_cold: Optional[ColdNeurons] = None, up_cold=None, down_cold=None):
-    """engine.py:173-209: hot half + cold half of the gated FFN for x (B, H).
+_DENSE_DTYPES = (torch.float16, torch.float32, torch.bfloat16)
 
-    ``gate_hot`` carries the whole hot half (a HotWeights), ``gate_cold`` the
-    whole cold half (a ColdNeurons); the up/down arguments are accepted for
-    signature compatibility and must be None.  Either half may be None or
-    empty; both empty gives zeros.  Returns x.dtype (fp16)."""
-    if up_hot is not None or down_hot is not None or up_cold is not None or down_cold is not None:
-        raise TypeError("pass the hot half as one HotWeights and the cold half as one ColdNeurons")
-    if gate_hot is not None and not isinstance(gate_hot, HotWeights):
-        raise TypeError(f"gate_hot must be HotWeights, got {type(gate_hot).__name__}")
-    if gate_cold is not None and not isinstance(gate_cold, ColdNeurons):
-        raise TypeError(f"gate_cold must be ColdNeurons, got {type(gate_cold).__name__}")
-    out = _ffn(x.reshape(-1, HIDDEN), None, 0.0, gate_hot, gate_cold, activation, act_on_both,
-               add_residual=False)
-    return out.reshape(x.shape).to(x.dtype)
+
+def _dense_half(gate, up, down, what):
+    """Validate one half given as the reference's tensors: gate/up (n, H),
+    down (H, n), one float dtype; returns (n, dtype code, g, u, d) with the
+    tensors contiguous, or (0, ...) for an absent or empty half
+    (engine.py:194, :199: a half is used when gate.shape[0] > 0)."""
+    if gate is None or gate.shape[0] == 0:
+        return 0, _lib.DTYPE_F16, None, None, None
+    if up is None or down is None:
+        raise TypeError(f"{what}: gate, up and down must all be given")
+    n = int(gate.shape[0])
+    if tuple(gate.shape) != (n, HIDDEN) or tuple(up.shape) != (n, HIDDEN) or \
+            tuple(down.shape) != (HIDDEN, n):
+        raise ValueError(f"{what}: gate/up must be ({n}, {HIDDEN}) and down ({HIDDEN}, {n}); got "
+                         f"{tuple(gate.shape)}, {tuple(up.shape)}, {tuple(down.shape)}")
+    if gate.dtype not in _DENSE_DTYPES or up.dtype != gate.dtype or down.dtype != gate.dtype:
+        raise TypeError(f"{what}: weights must share one of fp16 / fp32 / bf16, got "
+                        f"{gate.dtype}, {up.dtype}, {down.dtype}")
+    return n, _lib.dtype_code(gate.dtype), gate.contiguous(), up.contiguous(), down.contiguous()
+
+
+def _sparse_ffn_dense(x2d, activation, act_on_both, hot, cold):
+    """oi2_sparse_ffn_dense: both halves as dense tensors; fp32 y."""
+    dev = x2d.device
+    n_hot, hdt, gh, uh, dh = hot
+    n_cold, cdt, gc, uc, dc = cold
+    B = x2d.shape[0]
+    L = _lib.lib()
+    ws_bytes = L.oi2_sparse_ffn_dense_workspace_bytes(B, n_hot, n_cold)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    y32 = torch.empty((B, HIDDEN), dtype=torch.float32, device=dev)
+    act = _lib.ACT_RELU if activation == "relu" else _lib.ACT_SILU
+    _lib.check(L.oi2_sparse_ffn_dense(
+        x2d.data_ptr(), B, act, int(bool(act_on_both)), n_hot, hdt, _lib.ptr(gh), _lib.ptr(uh),
+        _lib.ptr(dh), n_cold, cdt, _lib.ptr(gc), _lib.ptr(uc), _lib.ptr(dc), None, y32.data_ptr(),
+        ws.data_ptr(), ws_bytes, _lib.stream_handle(dev)))
+    return y32
+
+
+def sparse_ffn(x: torch.Tensor, activation: str, act_on_both: bool,
+               gate_hot=None, up_hot=None, down_hot=None,
+               gate_cold=None, up_cold=None, down_cold=None):
+    """engine.py:173-209: hot half + cold half of the gated FFN for x (B, H)
+    fp16, returned in x.dtype.
+
+    Each half comes in either of two forms:
+      * the reference's own tensors (what SparseFFNLayer and read_neurons
+        hand it): gate/up (n, H), down (H, n), fp16 (the widened hot file),
+        fp32 (dequantised cold records) or bf16 - computed by the dense-weight
+        HIP GEMV kernels (oi2_sparse_ffn_dense);
+      * this library's compact handles: the whole hot half as one HotWeights
+        in ``gate_hot`` (fp8 in HBM) and the whole cold half as one
+        ColdNeurons in ``gate_cold`` (INT4 records + active list), with the
+        up/down arguments None - computed by the fused fp8 / INT4 kernels.
+    Either half may be None or empty; both empty gives zeros (:207-208).
+    Accumulation is fp32 throughout; the halves are summed in fp32 and
+    rounded once to fp16."""
+    if x.dtype != torch.float16:
+        raise TypeError(f"x must be the engine's fp16 activations, got {x.dtype}")
+    x2d = x.reshape(-1, HIDDEN).contiguous()
+    hot_handle = isinstance(gate_hot, HotWeights)
+    cold_handle = isinstance(gate_cold, ColdNeurons)
+    if hot_handle and (up_hot is not None or down_hot is not None):
+        raise TypeError("with a HotWeights in gate_hot, up_hot and down_hot must be None")
+    if cold_handle and (up_cold is not None or down_cold is not None):
+        raise TypeError("with a ColdNeurons in gate_cold, up_cold and down_cold must be None")
+    for t, what in ((gate_hot, "gate_hot"), (gate_cold, "gate_cold")):
+        if t is not None and not isinstance(t, (HotWeights, ColdNeurons, torch.Tensor)):
+            raise TypeError(f"{what}: expected a tensor or a library handle, got {type(t).__name__}")
+    hot_dense = None if hot_handle else _dense_half(gate_hot, up_hot, down_hot, "hot half")
+    cold_dense = None if cold_handle else _dense_half(gate_cold, up_cold, down_cold, "cold half")
+    y = None
+    if hot_dense is not None or cold_dense is not None:
+        none = (0, _lib.DTYPE_F16, None, None, None)
+        y = _sparse_ffn_dense(x2d, activation, act_on_both, hot_dense or none, cold_dense or none)
+    if hot_handle or cold_handle:
+        _, y2 = _ffn(x2d, None, 0.0, gate_hot if hot_handle else None,
+                     gate_cold if cold_handle else None, activation, act_on_both,
+                     add_residual=False, want_y32=True)
+        y = y2 if y is None else y + y2
+    return y.to(x.dtype).reshape(x.shape)
 
 
 class SparseFFNLayer(torch.nn.Module):

@@ -2,8 +2,9 @@
 PredictorRegistry with the reference's interface (predictor.py:55-96,
 413-462), evaluated by the predictor kernels.
 
-Weights keep the file's dtype (fp32 as trained, or bf16); the hidden state is
-cast to that dtype first (predictor.py:455).  The mask is sigmoid(logit) >=
+Weights keep the file's dtype (fp32 as trained, or bf16) unless a dtype is
+asked for at load; the hidden state, of whatever float dtype the caller holds
+it in, is cast straight to that dtype first (predictor.py:455).  The mask is sigmoid(logit) >=
 threshold, decided in logit space (logit >= log(p / (1 - p))), which is the same
 set except for logits within float rounding of the threshold.
 """
@@ -39,9 +40,13 @@ class NeuronPredictor:
         self.device = down_w.device
 
     @classmethod
-    def load(cls, path: str, device="cuda", dtype=None) -> "NeuronPredictor":
+    def load(cls, path: str, device="cuda", dtype=torch.float32) -> "NeuronPredictor":
         """predictor.py:83-96 file layout: {"hidden_dim", "intermediate_dim",
-        "rank", "state_dict": {"down.weight", "up.weight", "up.bias"}}."""
+        "rank", "state_dict": {"down.weight", "up.weight", "up.bias"}}.  The
+        reference loads the state dict into a freshly built (float32) module,
+        so its parameters are float32 whatever the file holds; ``dtype`` keeps
+        that default (None keeps the file's own dtype, torch.bfloat16 halves
+        the predictor's bytes)."""
         ckpt = torch.load(path, map_location="cpu", weights_only=True)
         sd = ckpt["state_dict"]
         t = [sd["down.weight"], sd["up.weight"], sd["up.bias"]]
@@ -63,7 +68,10 @@ class NeuronPredictor:
     def _run(self, x: torch.Tensor, threshold: float, want_probs: bool, want_mask: bool,
              want_logits: bool = False):
         lead = x.shape[:-1]
-        h = x.reshape(-1, HIDDEN).to(device=self.device, dtype=torch.float16).contiguous()
+        h = x.reshape(-1, HIDDEN).to(device=self.device)
+        if h.dtype not in (torch.float16, torch.float32, torch.bfloat16):
+            h = h.float()
+        h = h.contiguous()
         rows = h.shape[0]
         I = self.intermediate_dim
         logits = torch.empty((rows, I), dtype=torch.float32, device=self.device) if want_logits else None
@@ -73,7 +81,8 @@ class NeuronPredictor:
         L = _lib.lib()
         ws_bytes = L.oi2_predict_workspace_bytes(ctypes_ref(p))
         ws = torch.empty(ws_bytes, dtype=torch.uint8, device=self.device)
-        _lib.check(L.oi2_predict(h.data_ptr(), rows, ctypes_ref(p), _lib.logit_threshold(threshold),
+        _lib.check(L.oi2_predict(h.data_ptr(), _lib.dtype_code(h.dtype), rows, ctypes_ref(p),
+                                 _lib.logit_threshold(threshold),
                                  _lib.ptr(logits), _lib.ptr(probs), _lib.ptr(mask), ws.data_ptr(),
                                  ws_bytes, _lib.stream_handle(self.device)))
         out = []
@@ -83,8 +92,9 @@ class NeuronPredictor:
         return out[0] if len(out) == 1 else tuple(out)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        """Probabilities (..., I) fp32.  The input is taken at fp16, as the
-        engine's hidden states are."""
+        """Probabilities (..., I) fp32.  x (fp16, fp32 or bf16; other float
+        dtypes go through fp32) is cast straight to the predictor's dtype, as
+        PredictorRegistry.predict does (predictor.py:455)."""
         return self._run(x, 0.5, want_probs=True, want_mask=False)
 
     __call__ = forward
@@ -106,7 +116,7 @@ class PredictorRegistry:
     """predictor.py:413-462: every ``layer_*_expert_*.pt`` in a directory,
     resident on the device, looked up by (layer, expert)."""
 
-    def __init__(self, predictor_dir: str, device="cuda", dtype=None):
+    def __init__(self, predictor_dir: str, device="cuda", dtype=torch.float32):
         self.predictors: dict[tuple[int, int], NeuronPredictor] = {}
         self.device = device
         for f in sorted(Path(predictor_dir).glob("layer_*_expert_*.pt")):

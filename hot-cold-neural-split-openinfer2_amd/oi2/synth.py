@@ -120,3 +120,26 @@ def calibrate_threshold(layers, gen, frac_active: float, n_states: int = 32, eps
     allv = torch.cat(vals)
     k = int(round((1.0 - frac_active) * (allv.numel() - 1)))
     return float(allv.kthvalue(k + 1).values.item())
+
+
+def build_decode_stack(seed: int, dev, n_layers: int = 32, inter: int = 14336, n_hot: int = 3584,
+                       rank: int = 64, active_frac: float = 0.05, eps: float = 1e-5,
+                       records_on=None):
+    """The 32-layer decode workload: ``n_layers`` seeded SwiGLU layers of
+    4096 x ``inter`` (N(0, 0.02) weights, ``n_hot`` hot fp8 neurons, the rest
+    INT4 records), each with a random-init bf16 rank-``rank`` predictor, the
+    logit threshold calibrated so ``active_frac`` of the neurons are predicted
+    active.  ``records_on`` maps each layer's device records to where the stack
+    reads them (e.g. pinned host copies); None keeps them in HBM.  Returns
+    (layers, stack, threshold logit, generator)."""
+    from .stack import DecodeStack, StackLayer
+    g = torch.Generator(device=dev).manual_seed(seed)
+    layers = [SyntheticLayer(g, inter, n_hot, std=0.02, device=dev, with_predictor=True,
+                             pred_rank=rank, pred_dtype=torch.bfloat16) for _ in range(n_layers)]
+    thr = calibrate_threshold(layers, g, active_frac, eps=eps)
+    recs = [records_on(l.records) if records_on is not None else l.records for l in layers]
+    st = DecodeStack([StackLayer(l.hot, r, l.lut, l.norm_w, l.predictor)
+                      for l, r in zip(layers, recs)], inter, eps, "silu", False, thr)
+    # size the cold pass for the calibrated active fraction with headroom
+    st.set_expected_active(int(1.3 * active_frac * (inter - n_hot)))
+    return layers, st, thr, g

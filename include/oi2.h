@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define OI2_ABI_VERSION 1
+#define OI2_ABI_VERSION 2
 
 enum {
   OI2_OK = 0,
@@ -42,7 +42,7 @@ enum {
 };
 
 enum { OI2_ACT_SILU = 0, OI2_ACT_RELU = 1 };          /* engine.py:165 */
-enum { OI2_DTYPE_F32 = 0, OI2_DTYPE_BF16 = 1 };
+enum { OI2_DTYPE_F32 = 0, OI2_DTYPE_BF16 = 1, OI2_DTYPE_F16 = 2 };
 
 /* Hot FP8 half of one layer: the tensors SparseFFNLayer loads from
  * hot_weights/layer_XXX_expert_000.pt (engine.py:252-264, written at
@@ -132,18 +132,42 @@ int oi2_ffn_forward(const uint16_t* x, int32_t batch, const uint16_t* norm_w, fl
                     int32_t act, int32_t act_on_both, int32_t add_residual, uint16_t* out,
                     float* y32, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Workspace bytes for oi2_sparse_ffn_dense. */
+size_t oi2_sparse_ffn_dense_workspace_bytes(int32_t rows, int32_t n_hot, int32_t n_cold);
+
+/* sparse_ffn (engine.py:173-209) on the dense tensors the reference passes
+ * it: the hot half as SparseFFNLayer's widened fp16 tensors
+ * (engine.py:255-261) and the cold half as ColdWeightStore.read_neurons's
+ * fp32 tensors (splitter.py:397-403), gate/up (n, H) row-major and down
+ * (H, n) row-major (any n: rows of down need no alignment), each half of one
+ * dtype (OI2_DTYPE_F16, _F32 or _BF16); x (rows, H) fp16.
+ *   y   = down_h act(gate_h x, up_h x) + down_c act(gate_c x, up_c x)
+ *         fp32 accumulation, the halves summed in fp32
+ *   y32 = y (may be NULL), out = fp16(y) (may be NULL; not both)
+ * n_hot or n_cold 0 drops that half; both 0 gives zeros (engine.py:207-208).
+ * gate/up must be 16-byte aligned, each matrix under 2 GiB. */
+int oi2_sparse_ffn_dense(const uint16_t* x, int32_t rows, int32_t act, int32_t act_on_both,
+                         int32_t n_hot, int32_t hot_dtype, const void* gate_hot, const void* up_hot,
+                         const void* down_hot, int32_t n_cold, int32_t cold_dtype,
+                         const void* gate_cold, const void* up_cold, const void* down_cold,
+                         uint16_t* out, float* y32, void* workspace, size_t workspace_bytes,
+                         void* stream);
+
 /* ---- predictor ---------------------------------------------------------- */
 size_t oi2_predict_workspace_bytes(const oi2_predictor* p);
 
 /* PredictorRegistry.predict (predictor.py:435-456) with NeuronPredictor's
- * forward / predict_mask (predictor.py:70-79) for `rows` query rows h (fp16,
- * cast to the predictor dtype as predictor.py:455 does): logits (rows, inter)
- * fp32, probs = sigmoid(logits) fp32 and/or mask (rows, inter) bytes =
- * sigmoid(logit) >= threshold, evaluated as logit >= threshold_logit =
- * log(p / (1 - p)).  Any output may be NULL. */
-int oi2_predict(const uint16_t* h, int32_t rows, const oi2_predictor* p, float threshold_logit,
-                float* logits, float* probs, uint8_t* mask, void* workspace,
-                size_t workspace_bytes, void* stream);
+ * forward / predict_mask (predictor.py:70-79) for `rows` query rows h of
+ * dtype h_dtype (OI2_DTYPE_F16, _F32 or _BF16), each cast straight to the
+ * predictor dtype as predictor.py:455 does (fp16 and bf16 widen exactly to
+ * an fp32 predictor; fp32 rounds to nearest-even for a bf16 one): logits
+ * (rows, inter) fp32, probs = sigmoid(logits) fp32 and/or mask (rows, inter)
+ * bytes = sigmoid(logit) >= threshold, evaluated as logit >= threshold_logit
+ * (log(p / (1 - p)); the float32 sigmoid's saturation point 16.6355 for
+ * p == 1).  Any output may be NULL. */
+int oi2_predict(const void* h, int32_t h_dtype, int32_t rows, const oi2_predictor* p,
+                float threshold_logit, float* logits, float* probs, uint8_t* mask,
+                void* workspace, size_t workspace_bytes, void* stream);
 
 /* SparseFFNLayer._cold_ids_for (engine.py:274-283) on device: query =
  * mean over the `batch` rows of RMSNorm(x) (norm_w may be NULL for an already
@@ -240,9 +264,10 @@ int oi2_stack_selection_layout(const oi2_stack* s, int32_t* n_chunks, int32_t* c
 int oi2_stack_set_token_kernel(oi2_stack* s, int32_t enable);
 /* 1 when decodes run as the persistent token kernel, else 0. */
 int32_t oi2_stack_token_kernel(const oi2_stack* s);
-/* Waits for `stream`; OI2_EHIP if a device-wide wait of the last
- * persistent-kernel token ran past its bound (that token's output is then
- * invalid), else OI2_OK. */
+/* Waits for `stream`; OI2_EHIP if a device-wide wait of any persistent-kernel
+ * token decoded since the previous call ran past its bound (the tokens
+ * decoded since then are to be taken as invalid; the signal words are reset
+ * so the next token is clean), else OI2_OK. */
 int oi2_stack_status(oi2_stack* s, void* stream);
 /* No counterpart in the reference: the bound, in polls, of every device-wide
  * wait of the persistent kernel (default 1 << 20; 1 .. 1 << 24).  A wait past

@@ -210,12 +210,57 @@ def predictor_logits(h, D, U, b):
 
 
 def logit_threshold(p: float) -> float:
-    """sigmoid(l) >= p  <=>  l >= log(p / (1 - p)) for 0 < p < 1."""
+    """sigmoid(l) >= p  <=>  l >= log(p / (1 - p)) for 0 < p < 1.  At the
+    edges the reference's float32 sigmoid decides (predictor.py:75-79): every
+    logit passes p <= 0; p == 1 passes the logits whose float32 sigmoid rounds
+    to 1.0 (sigmoid_f32_threshold); p > 1 passes none."""
     if p <= 0.0:
         return -math.inf
-    if p >= 1.0:
+    if p > 1.0:
         return math.inf
+    if p == 1.0:
+        return float(sigmoid_f32_threshold(1.0))
     return math.log(p / (1.0 - p))
+
+
+def sigmoid_f32(z):
+    """torch.sigmoid in float32 (predictor.py:75): 1 / (1 + exp(-z)), each
+    step rounded to float32."""
+    z = np.asarray(z, dtype=np.float32)
+    one = np.float32(1.0)
+    with np.errstate(over="ignore"):
+        return one / (one + np.exp(-z, dtype=np.float32))
+
+
+def _f32_key(v):
+    """float32 -> an integer that orders like the float (ordered bit pattern)."""
+    u = int(np.array(v, np.float32).view(np.uint32))
+    return u ^ 0xFFFFFFFF if u >> 31 else u | 0x80000000
+
+
+def _f32_from_key(k):
+    u = k ^ 0xFFFFFFFF if not k >> 31 else k & 0x7FFFFFFF
+    return np.array(u, np.uint32).view(np.float32)[()]
+
+
+def sigmoid_f32_threshold(p: float) -> np.float32:
+    """Smallest float32 logit z with sigmoid_f32(z) >= p (bisection over the
+    ordered float32 bit patterns; sigmoid_f32 is non-decreasing), so that
+    ``logit >= z`` is exactly the reference's float32 test
+    ``sigmoid(logit) >= p`` (predictor.py:79).  +inf when no finite logit
+    passes."""
+    lo, hi = _f32_key(np.float32(-np.inf)), _f32_key(np.float32(np.inf))
+    if sigmoid_f32(_f32_from_key(lo)) >= p:
+        return np.float32(-np.inf)
+    if not sigmoid_f32(_f32_from_key(hi - 1)) >= p:
+        return np.float32(np.inf)
+    while hi - lo > 1:                  # invariant: f(lo) < p <= f(hi)
+        mid = (lo + hi) // 2
+        if sigmoid_f32(_f32_from_key(mid)) >= p:
+            hi = mid
+        else:
+            lo = mid
+    return _f32_from_key(hi)
 
 
 def predict_mask(h, D, U, b, threshold: float = 0.5):
@@ -247,9 +292,12 @@ def query(x_rows_normed_f16):
 
 def to_bf16(v):
     """Round-to-nearest-even float32 -> bfloat16, returned as float32 values
-    (the cast predictor.py:455 applies for a bf16 predictor)."""
-    u = np.asarray(v, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    (the cast predictor.py:455 applies for a bf16 predictor).  Overflow past
+    the largest bfloat16 rounds to infinity; NaN stays NaN (a quiet NaN)."""
+    f = np.asarray(v, dtype=np.float32)
+    u = f.view(np.uint32).astype(np.uint64)
     u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    u = np.where(np.isnan(f), np.uint64(0x7FC00000), u)
     return u.astype(np.uint32).view(np.float32)
 
 

@@ -63,29 +63,55 @@ def test_batch_decode_shared_active_set(dev, layer25, B):
                      what="batch row vs single token")
 
 
-def test_batch_drelu_union_of_firing_sets_equals_dense(dev):
-    """16 independent dReLU tokens over the union of their true firing sets:
-    a neuron outside a token's set contributes exactly zero to it, so the
-    union reproduces each token's dense FFN (survey config 2 at B=16)."""
+@pytest.fixture(scope="module")
+def drelu_layer(dev):
+    """Config 2's layer: dReLU at 4096 x 14336, 25 % hot, gate pre-activation
+    shifted by -1.3 sigma so that ~10 % of gates are positive."""
     g = torch.Generator(device=dev).manual_seed(22)
-    inter, B = 14336, 16
     sigma = 0.02 * math.sqrt(H)
-    lay = SyntheticLayer(g, inter, 3584, device=dev, gate_bias_shift=-1.3 * sigma)
+    lay = SyntheticLayer(g, 14336, 3584, device=dev, gate_bias_shift=-1.3 * sigma)
+    dense = cold_dense(lay.records, np.arange(lay.records.shape[0]))
+    return lay, g, dense
+
+
+@pytest.mark.parametrize("B", [16, 64, 512])
+def test_batch_drelu_union_of_firing_sets_equals_dense(dev, drelu_layer, B):
+    """B independent dReLU tokens with a gate bias over the union of their
+    true firing sets: a neuron outside a token's set contributes exactly zero
+    to it, so the union reproduces each token's dense FFN.  B = 64 is survey
+    config 2; 16 runs the skinny small-batch kernels, 64 the 64-token tiles,
+    512 the prefill tiles (relu epilogues with the bias on each).  Rows spread
+    over the batch against the float64 oracle; for B >= 64 every row against a
+    float32 torch reference over the same dequantised weights."""
+    lay, g, (Gc_all, Uc_all, Dc_all) = drelu_layer
+    inter = lay.inter
     x = torch.randn((B, H), generator=g, device=dev).half()
     xn = normed_f16(x, lay.norm_w)
-    Gc_all, Uc_all, Dc_all = cold_dense(lay.records, np.arange(lay.records.shape[0]))
     bc = lay.cold_gate_bias.cpu().numpy().astype(np.float64)
     fire = (np.maximum(xn @ Gc_all.T + bc, 0) * np.maximum(xn @ Uc_all.T, 0)) != 0
+    per_token = fire.sum(axis=1) / Gc_all.shape[0]
+    assert 0.02 < per_token.mean() < 0.08          # ~4.8 % of cold neurons fire per token
     union = np.nonzero(fire.any(axis=0))[0]
     assert 0.2 * inter < union.size < 0.8 * inter
     cold = ColdNeurons.from_slots(_section(lay), union, gate_bias=lay.cold_gate_bias)
     _, y32 = _ffn(x, lay.norm_w, EPS, lay.hot, cold, "relu", True, False, want_y32=True)
+    torch.cuda.synchronize()
     Gh, Uh, Dh = hot_dense(lay.hot)
     bh = lay.hot.gate_bias.cpu().numpy().astype(np.float64)
-    dense = O.sparse_ffn(xn, "relu", True, Gh, Uh, Dh, Gc_all, Uc_all, Dc_all, bh, bc)
+    rows = list(range(B)) if B <= 16 else sorted({0, 1, 31, 63, B // 2, B - 2, B - 1})
+    assert max(rows) < B
+    dense = O.sparse_ffn(xn[rows], "relu", True, Gh, Uh, Dh, Gc_all, Uc_all, Dc_all, bh, bc)
     y = y32.cpu().numpy()
-    for r in range(B):
-        assert_ffn_close(y[r], dense[r], what=f"dReLU row {r}")
+    for k, r in enumerate(rows):
+        assert_ffn_close(y[r], dense[k], what=f"dReLU B={B} row {r}")
+    if B >= 64:
+        f32 = lambda a: torch.as_tensor(a, dtype=torch.float32, device=dev)
+        xa = f32(xn)
+        relu = torch.nn.functional.relu
+        hh = relu(xa @ f32(Gh).T + f32(bh)) * relu(xa @ f32(Uh).T)
+        hc = relu(xa @ f32(Gc_all).T + f32(bc)) * relu(xa @ f32(Uc_all).T)
+        ref_all = (hh @ f32(Dh).T + hc @ f32(Dc_all).T).double().cpu().numpy()
+        assert_ffn_close(y, ref_all, what=f"dReLU B={B} all rows")
 
 
 @pytest.mark.parametrize("B", [70, 200, 400])

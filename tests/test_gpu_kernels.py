@@ -242,27 +242,45 @@ def test_rmsnorm_within_one_fp16_ulp(dev):
 
 # ── predictor ────────────────────────────────────────────────────────────────
 
+LOGIT_BAND = 1e-6     # the contract's exemption band around the threshold
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_predictor_logits_mask_and_selection(dev, dtype):
+@pytest.mark.parametrize("h_dtype", [torch.float16, torch.float32, torch.bfloat16])
+def test_predictor_logits_mask_and_selection(dev, dtype, h_dtype):
+    """Logits within the 1e-6 band of the float64 oracle (the largest error is
+    printed), so that the mask equals the oracle's outside that band; the
+    hidden state, of any float dtype, is cast straight to the predictor dtype
+    (predictor.py:455)."""
     g = torch.Generator(device=dev).manual_seed(31)
     inter = 14336
     pred = random_predictor(g, inter, 64, dtype, dev)
     D, U, b = pred_weights(pred)
-    x = torch.randn((2, H), generator=g, device=dev).half()
+    x = (torch.randn((2, H), generator=g, device=dev) * 1.7).to(h_dtype)
     logits = pred.logits(x)
     probs = pred(x)
     mask = pred.predict_mask(x, 0.5)
     torch.cuda.synchronize()
+    worst = 0.0
     for r in range(2):
-        q = x[r].float().cpu().numpy().astype(np.float64)
+        q = x[r].float().cpu().numpy()
         if dtype == torch.bfloat16:
-            q = O.to_bf16(q.astype(np.float32)).astype(np.float64)
-        ref = O.predictor_logits(q, D, U, b)
+            q = O.to_bf16(q)
+        ref = O.predictor_logits(q.astype(np.float64), D, U, b)
         got = logits[r].double().cpu().numpy()
-        assert np.abs(got - ref).max() < 1e-5
-        amb = O.ambiguous(ref, 0.5)
+        worst = max(worst, float(np.abs(got - ref).max()))
+        # the sums run in double precision: the fp32 logits returned are the
+        # oracle's logits rounded once (at most one fp32 ulp away)
+        assert (got == ref.astype(np.float32)).mean() > 0.999
+        ulp = np.spacing(np.abs(ref).astype(np.float32)).astype(np.float64)
+        assert (np.abs(got - ref) <= ulp).all()
+        # and the mask is decided on the double logit: equal to the oracle's
+        # outside a band a thousand times narrower than the contract's
+        amb = O.ambiguous(ref, 0.5, band=1e-3 * LOGIT_BAND)
         assert np.array_equal(mask[r].cpu().numpy()[~amb], (ref >= 0.0)[~amb])
         assert np.allclose(probs[r].double().cpu().numpy(), 1 / (1 + np.exp(-ref)), atol=1e-6)
+    print(f"predictor {dtype} <- {h_dtype}: max |fp32 logit - oracle| = {worst:.3e}")
+    assert worst < LOGIT_BAND
     # on-device selection: RMSNorm -> query -> threshold -> LUT filter -> ascending
     norm_w = (1 + 0.05 * torch.randn(H, generator=g, device=dev)).half()
     hot_ids = torch.randperm(inter, generator=g, device=dev)[:3584]
@@ -303,6 +321,133 @@ def test_predictor_logits_mask_and_selection(dev, dtype):
         assert n == len(got)
         assert dids[:n].cpu().tolist() == got
         assert dslots[:n].cpu().tolist() == [3 * i for i in got]
+
+
+def test_predictor_registry_predict_from_files(dev):
+    """PredictorRegistry.predict exactly as _cold_ids_for calls it
+    (engine.py:277-278): an fp32 predictor file (as predictor.py saves it),
+    hidden states of each float dtype cast straight to fp32, masks equal to
+    the oracle outside the band; a layer without a file gives None; and the
+    p == 1 edge selects exactly the logits whose float32 sigmoid is 1.0."""
+    g = torch.Generator(device=dev).manual_seed(57)
+    inter = 4096
+    pred = random_predictor(g, inter, 64, torch.float32, dev)
+    # neurons 0..3 have zero up rows, so their logit is their bias alone,
+    # placed on either side of the float32 sigmoid's saturation point
+    z1 = np.float32(O.sigmoid_f32_threshold(1.0))
+    edge = [np.nextafter(z1, np.float32(0)), z1, np.nextafter(z1, np.float32(99)), np.float32(17)]
+    pred.up_w[:4] = 0.0
+    pred.up_b[:4] = torch.tensor(edge, dtype=torch.float32, device=dev)
+    with tempfile.TemporaryDirectory() as tmp:
+        pred.save(os.path.join(tmp, "layer_005_expert_000.pt"))
+        reg = oi2.PredictorRegistry(tmp, device=dev)
+        assert reg.predict(4, 0, torch.zeros(H, device=dev)) is None
+        D, U, b = pred_weights(pred)
+        for h_dtype in (torch.float16, torch.float32, torch.bfloat16):
+            h = (torch.randn((1, H), generator=g, device=dev) * 0.8).to(h_dtype)
+            for thr in (0.5, 0.6, 1.0):
+                mask = reg.predict(5, 0, h, thr)
+                assert mask.shape == (1, inter) and mask.dtype == torch.bool
+                ref = O.predictor_logits(h.float().cpu().numpy().astype(np.float64), D, U, b)[0]
+                want = ref >= O.logit_threshold(thr)
+                amb = O.ambiguous(ref, thr)
+                got = mask[0].cpu().numpy()
+                assert np.array_equal(got[~amb], want[~amb]), (h_dtype, thr)
+                if thr == 1.0:
+                    sig = torch.sigmoid(torch.tensor(edge, dtype=torch.float32))
+                    assert got[:4].tolist() == (sig >= 1.0).tolist() == [False, True, True, True]
+                    assert not got[4:].any()
+
+
+# ── sparse_ffn on the reference's own tensors ───────────────────────────────
+
+@pytest.fixture(scope="module")
+def config1_files(dev):
+    """Survey config 1's layer written as split files: 2867 hot neurons in a
+    reference-layout hot .pt (fp8, no scales) and the other 11469 as INT4
+    records in a cold file, plus the dense weights."""
+    g = torch.Generator(device=dev).manual_seed(61)
+    inter = 14336
+    lay = SyntheticLayer(g, inter, 2867, device=dev, keep_dense=True, per_row_scale=False)
+    tmp = tempfile.TemporaryDirectory()
+    w = oi2.format.ColdFileWriter(os.path.join(tmp.name, "cold_weights.bin"), 1)
+    w.add_section(0, lay.records.cpu().numpy())
+    w.close(os.path.join(tmp.name, "cold_index.npy"))
+    cfg = {"hidden_dim": H, "intermediate_dim": inter, "rms_norm_eps": EPS, "num_experts": 1}
+    store = oi2.ColdWeightStore(os.path.join(tmp.name, "cold_weights.bin"),
+                                os.path.join(tmp.name, "cold_index.npy"), cfg, device=dev)
+    gate, up, down = lay.dense
+    hid = lay.hot_ids
+    fp8 = {"gate": gate[hid].to(torch.float8_e4m3fn), "up": up[hid].to(torch.float8_e4m3fn),
+           "down": down[:, hid].to(torch.float8_e4m3fn)}
+    yield lay, g, store, fp8
+    store.close()
+    tmp.cleanup()
+
+
+@pytest.mark.parametrize("B,activation,both", [(1, "silu", False), (5, "silu", False),
+                                               (3, "relu", True)])
+def test_sparse_ffn_takes_the_reference_call(dev, config1_files, B, activation, both):
+    """sparse_ffn exactly as engine.py:302-307 calls it: hot gate/up/down as
+    SparseFFNLayer widens them from the hot file (fp16, engine.py:255-261),
+    cold gate/up/down as read_neurons returns them (fp32, (N,H)/(N,H)/(H,N)),
+    for 10 % of the cold neurons (config 1).  Against the float64 oracle over
+    the same tensors, and against the fused fp8/INT4 path on the same
+    weights; n_hot 2867 leaves the down rows unaligned."""
+    lay, g, store, fp8 = config1_files
+    gh, uh, dh = (fp8[k].to(torch.float16) for k in ("gate", "up", "down"))
+    cold_ids = lay.cold_ids[torch.randperm(lay.cold_ids.numel(), generator=g, device=dev)[:1147]]
+    ids = cold_ids.cpu().tolist()
+    gc, uc, dc = store.read_neurons(0, 0, ids)
+    assert gc.dtype == torch.float32 and dc.shape == (H, 1147)
+    x = rmsnorm(torch.randn((B, H), generator=g, device=dev).half(), lay.norm_w, EPS)
+    y = oi2.sparse_ffn(x, activation, both, gh, uh, dh, gc, uc, dc)
+    torch.cuda.synchronize()
+    assert y.dtype == torch.float16 and y.shape == (B, H)
+    f64 = lambda t: t.double().cpu().numpy()
+    ref = O.sparse_ffn(f64(x), activation, both, f64(gh), f64(uh), f64(dh), f64(gc), f64(uc), f64(dc))
+    for r in range(B):
+        assert_ffn_close(f64(y[r]), ref[r], what=f"dense sparse_ffn row {r}")
+    # the same weights through the fused kernels (fp8 codes, INT4 records)
+    hot = oi2.HotWeights(lay.hot_ids, fp8["gate"].view(torch.uint8), fp8["up"].view(torch.uint8),
+                         fp8["down"].view(torch.uint8), torch.ones(2867, device=dev),
+                         torch.ones(2867, device=dev), torch.ones(H, device=dev))
+    cold = ColdNeurons.from_ids(store.section(0), ids)
+    y_fused = oi2.sparse_ffn(x, activation, both, hot, None, None, cold)
+    assert_ffn_close(f64(y_fused), f64(y), tol=2e-3, cos_min=0.99999, what="fused vs dense")
+    # one half as tensors, the other as a handle
+    y_mixed = oi2.sparse_ffn(x, activation, both, gh, uh, dh, cold)
+    assert_ffn_close(f64(y_mixed), f64(y), tol=2e-3, cos_min=0.99999, what="mixed")
+
+
+def test_sparse_ffn_reference_call_edges(dev, config1_files):
+    """Either half missing or empty (engine.py:194, :199), both empty giving
+    zeros (:207-208), cold records read out of request order with duplicates,
+    bf16 weights, and non-fp16 activations refused."""
+    lay, g, store, fp8 = config1_files
+    gh, uh, dh = (fp8[k].to(torch.float16) for k in ("gate", "up", "down"))
+    ids = [int(lay.cold_ids[k]) for k in (40, 3, 3, 700, 11000, 5)]
+    gc, uc, dc = store.read_neurons(0, 0, ids)
+    x = rmsnorm(torch.randn((2, H), generator=g, device=dev).half(), lay.norm_w, EPS)
+    f64 = lambda t: t.double().cpu().numpy()
+    empty = torch.zeros((0, H), dtype=torch.float16, device=dev)
+    cases = [((gh, uh, dh), (None, None, None), "hot only"),
+             ((empty, empty, empty.t()), (gc, uc, dc), "cold only (empty hot tensors)"),
+             ((None, None, None), (gc, uc, dc), "cold only"),
+             ((gh.bfloat16(), uh.bfloat16(), dh.bfloat16()), (gc, uc, dc), "bf16 hot")]
+    for hot, cold, what in cases:
+        y = oi2.sparse_ffn(x, "silu", False, *hot, *cold)
+        torch.cuda.synchronize()
+        ref = O.sparse_ffn(f64(x), "silu", False, *(None if t is None else f64(t) for t in hot),
+                           *(None if t is None else f64(t) for t in cold))
+        for r in range(2):
+            assert_ffn_close(f64(y[r]), ref[r], what=f"{what} row {r}")
+    z = oi2.sparse_ffn(x, "silu", False, None, None, None, None, None, None)
+    assert z.dtype == torch.float16 and torch.count_nonzero(z) == 0
+    with pytest.raises(TypeError, match="fp16"):
+        oi2.sparse_ffn(x.float(), "silu", False, gh, uh, dh, None, None, None)
+    with pytest.raises(ValueError, match="gate/up must be"):
+        oi2.sparse_ffn(x, "silu", False, gh, uh, dh.t(), None, None, None)
 
 
 # ── drop-in layer from split files ───────────────────────────────────────────

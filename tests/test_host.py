@@ -31,7 +31,7 @@ def test_library_exports_every_declared_symbol():
     for n in names:
         assert hasattr(lib, n), f"liboi2.so does not export {n}"
     assert set(names) <= set(_lib._SIGS), "ctypes signatures missing for some entry points"
-    assert lib.oi2_abi_version() == 1
+    assert lib.oi2_abi_version() == _lib.ABI_VERSION == 2
     assert lib.oi2_record_bytes() == fmt.NEURON_RECORD_BYTES == 6400
 
 
@@ -44,8 +44,10 @@ def test_argument_validation_without_gpu():
     assert b"null" in lib.oi2_last_error()
     p = _lib.Predictor(100, 12, 0, 1, 1, 1)       # rank not a multiple of 8
     import ctypes
-    rc = lib.oi2_predict(1, 1, ctypes.byref(p), 0.0, None, None, None, None, 0, None)
+    rc = lib.oi2_predict(1, _lib.DTYPE_F16, 1, ctypes.byref(p), 0.0, None, None, None, None, 0, None)
     assert rc == 1 and b"rank" in lib.oi2_last_error()
+    rc = lib.oi2_predict(1, 7, 1, ctypes.byref(p), 0.0, None, None, None, None, 0, None)
+    assert rc == 1 and b"h_dtype" in lib.oi2_last_error()
     assert lib.oi2_ffn_workspace_bytes(1, 3584, 14336) >= (3584 + 2 * 14336 + 2048) * 4
 
 
@@ -152,4 +154,9 @@ def test_logit_threshold_equivalence():
     for p in (0.5, 0.05, 0.95, 0.3):
         t = _lib.logit_threshold(p)
         assert abs(1 / (1 + np.exp(-t)) - p) < 1e-12
-    assert _lib.logit_threshold(0.0) == -np.inf and _lib.logit_threshold(1.0) == np.inf
+    assert _lib.logit_threshold(0.0) == -np.inf and _lib.logit_threshold(1.01) == np.inf
+    # p == 1: the float32 sigmoid's saturation point, as the oracle finds it
+    t1 = _lib.logit_threshold(1.0)
+    assert t1 == float(O.sigmoid_f32_threshold(1.0))
+    z = torch.tensor([np.nextafter(np.float32(t1), np.float32(0)), t1], dtype=torch.float32)
+    assert (torch.sigmoid(z) >= 1.0).tolist() == [False, True]

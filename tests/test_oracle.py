@@ -261,3 +261,76 @@ def test_cold_ids_for_order_and_hot_filter():
     mask[[17, 2, 5, 9, 11]] = True
     assert O.cold_ids_for(mask, [5, 11, 13], 20) == [2, 9, 17]
     assert O.cold_ids_for(None, [0, 1, 2], 6) == [3, 4, 5]
+
+
+# ── casts and the batch query (predictor.py:455, engine.py:277) ─────────────
+
+def test_to_bf16_matches_torch_cast():
+    """oracle.to_bf16 against torch's own float32 -> bfloat16 cast, bit for
+    bit: round-half-even ties both ways, +-0, subnormals, the largest finite
+    values (which round to inf), infinities, and NaN (NaN either way)."""
+    rng = np.random.default_rng(11)
+    bits = [0x00000000, 0x80000000, 0x00000001, 0x807FFFFF, 0x00400000, 0x00008000, 0x00018000,
+            0x3F808000, 0x3F818000, 0x3F807FFF, 0x3F808001, 0xBF808000, 0xBF818000,
+            0x7F7FFFFF, 0xFF7FFFFF, 0x7F7F7FFF, 0x7F7F8000, 0x7F800000, 0xFF800000,
+            0x7FC00000, 0xFFC00000, 0x7F800001, 0x7FBFFFFF]
+    # ties: the low 16 bits exactly 0x8000, both parities of bit 16
+    ties = (rng.integers(0, 1 << 15, 20000, dtype=np.uint64) << 17) | 0x8000
+    ties |= rng.integers(0, 2, 20000, dtype=np.uint64) << 16
+    rand = rng.integers(0, 1 << 32, 200000, dtype=np.uint64)
+    f = np.concatenate([np.array(bits, np.uint64), ties, rand]).astype(np.uint32).view(np.float32)
+    got = O.to_bf16(f)
+    want = torch.from_numpy(f.copy()).to(torch.bfloat16).float().numpy()
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+    # the same through the usual path of the predictor query: fp16 values
+    h = rng.standard_normal(100000).astype(np.float16).astype(np.float32)
+    assert np.array_equal(O.to_bf16(h).view(np.uint32),
+                          torch.from_numpy(h).to(torch.bfloat16).float().numpy().view(np.uint32))
+
+
+@pytest.mark.parametrize("rows", [1, 3, 8])
+def test_query_matches_torch_fp16_batch_mean(rows):
+    """oracle.query is engine.py:277's ``x_normed[:, -1, :].mean(0)`` over fp16
+    rows: torch's fp16 mean, bit for bit, on normal rows and on rows of mixed
+    scale (where fp32 accumulation order could matter)."""
+    rng = np.random.default_rng(rows)
+    for scale in (1.0, None):
+        x = rng.standard_normal((rows, 100000))
+        if scale is None:
+            x *= 10.0 ** rng.integers(-4, 4, (rows, 1))
+        x16 = x.astype(np.float16)
+        want = torch.from_numpy(x16).mean(0).numpy()
+        got = O.query(x16)
+        assert got.dtype == np.float16
+        assert np.array_equal(got.view(np.uint16), want.view(np.uint16))
+    # the engine's own shape: (B, T, H) normalised states, last position
+    xt = torch.from_numpy(rng.standard_normal((rows, 3, 4096)).astype(np.float16))
+    want = xt[:, -1, :].mean(0, keepdim=True).numpy()
+    assert np.array_equal(O.query(xt[:, -1, :].numpy())[None].view(np.uint16),
+                          want.view(np.uint16))
+
+
+def test_threshold_edges_follow_float32_sigmoid():
+    """The logit cut at the threshold's edges: p == 1 passes exactly the
+    logits whose float32 sigmoid is 1.0, p > 1 none and p <= 0 all
+    (predictor.py:77-79 in float32); away from the edges the cut is within
+    the 1e-6 exemption band of torch's float32 decision."""
+    z0 = O.sigmoid_f32_threshold(1.0)
+    assert 16.6 < z0 < 16.7
+    z = np.array([np.nextafter(z0, np.float32(0)), z0, np.nextafter(z0, np.float32(99)), 20.0,
+                  -20.0, 0.0, 40.0], np.float32)
+    sig = torch.sigmoid(torch.from_numpy(z))
+    for p in (1.0, 1.5, 0.0, -0.5):
+        want = (sig >= p).numpy()
+        assert np.array_equal(z >= O.logit_threshold(p), want), p
+    assert O.logit_threshold(1.0) == float(z0)
+    rng = np.random.default_rng(4)
+    for p in (0.5, 0.05, 0.637, 0.9):
+        t = O.logit_threshold(p)
+        zz = (t + rng.uniform(-1e-5, 1e-5, 20000)).astype(np.float32)
+        want = (torch.sigmoid(torch.from_numpy(zz)) >= p).numpy()
+        got = zz.astype(np.float64) >= t
+        diff = got != want
+        assert (np.abs(zz[diff].astype(np.float64) - t) <= 1e-6).all(), p
