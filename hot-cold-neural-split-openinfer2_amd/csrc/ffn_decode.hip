@@ -885,23 +885,9 @@ static int validate_pred(const oi2_predictor* p) {
   return OI2_OK;
 }
 
-// Workspace carve-up shared by the FFN entry points.
-struct FfnWs {
-  float* h_hot;
-  float* cold_part;
-  int32_t* cold_total;
-  uint16_t* xw;
-  float* ssq;
-};
-
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-size_t ffn_ws_bytes(int n_hot, int cold_wg) {
-  return align256((size_t)(n_hot > 0 ? n_hot : 0) * 4 + 64) + align256((size_t)cold_wg * kH * 4) +
-         align256(64) + align256(kH * 2) + align256(kDownWG * 4);
-}
-
-static FfnWs ffn_ws(void* base, int n_hot, int cold_wg) {
+FfnWs ffn_ws(void* base, int n_hot, int cold_wg) {
   char* p = reinterpret_cast<char*>(base);
   FfnWs w;
   w.h_hot = reinterpret_cast<float*>(p);
@@ -962,7 +948,30 @@ int oi2_ffn_forward(const uint16_t* x, int32_t batch, const uint16_t* norm_w, fl
                     int32_t act, int32_t act_on_both, int32_t add_residual, uint16_t* out,
                     float* y32, void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
+  FfnCall c;
+  int rc = ffn_validate(x, batch, norm_w, hot, cold, active, act, &c);
+  if (rc || batch == 0) return rc;
+  hipStream_t st = (hipStream_t)stream;
+  if (batch >= 2)
+    return batch_ffn(x, batch, norm_w, eps, hot, c.has_cold ? cold : nullptr,
+                     c.has_cold ? active : nullptr, act == OI2_ACT_RELU, act_on_both != 0,
+                     add_residual, out, y32, workspace, workspace_bytes, st);
+  const int ws_wg = c.has_cold ? cold_wg_for(c.cap) : 0;
+  OI2_CHECK_ARG(workspace && workspace_bytes >= ffn_ws_bytes(c.n_hot, ws_wg),
+                "workspace of %zu bytes is smaller than the %zu required", workspace_bytes,
+                ffn_ws_bytes(c.n_hot, ws_wg));
+  return ffn_decode_tokens(x, batch, norm_w, eps, hot, cold, active, act, act_on_both, add_residual,
+                           out, y32, c, ffn_ws(workspace, c.n_hot, ws_wg), st);
+}
+
+}  // extern "C"
+
+namespace oi2 {
+
+int ffn_validate(const uint16_t* x, int batch, const uint16_t* norm_w, const oi2_hot* hot,
+                 const oi2_cold* cold, const oi2_active* active, int act, FfnCall* c) {
   OI2_CHECK_ARG(batch >= 0, "batch must be >= 0");
+  *c = FfnCall{};
   if (batch == 0) return OI2_OK;
   OI2_CHECK_ARG(x, "x is null");
   OI2_CHECK_ARG((uintptr_t)x % 16 == 0 && (!norm_w || (uintptr_t)norm_w % 16 == 0),
@@ -970,30 +979,34 @@ int oi2_ffn_forward(const uint16_t* x, int32_t batch, const uint16_t* norm_w, fl
   OI2_CHECK_ARG(act == OI2_ACT_SILU || act == OI2_ACT_RELU, "act %d", act);
   int rc = validate_hot(hot);
   if (rc) return rc;
-  const int n_hot = hot ? hot->n_hot : 0;
-  const bool has_cold = cold && active && cold->n_records > 0 && active->n_chunks > 0;
-  int cap = 0;
-  if (has_cold) {
+  c->n_hot = hot ? hot->n_hot : 0;
+  c->has_cold = cold && active && cold->n_records > 0 && active->n_chunks > 0;
+  if (c->has_cold) {
     OI2_CHECK_ARG(cold->records && (uintptr_t)cold->records % 16 == 0,
                   "cold records must be non-null and 16-byte aligned");
     OI2_CHECK_ARG(active->slots && active->counts, "active list pointers are null");
     OI2_CHECK_ARG(active->n_chunks <= kMaxChunks && active->chunk > 0,
                   "active list: n_chunks %d (max %d), chunk %d", active->n_chunks, kMaxChunks,
                   active->chunk);
-    cap = active->n_chunks * active->chunk;
+    c->cap = active->n_chunks * active->chunk;
+    const int expected = active->expected > 0 && active->expected < c->cap ? active->expected : c->cap;
+    c->wg_cold = cold_wg_for(expected);
   }
-  hipStream_t st = (hipStream_t)stream;
-  if (batch >= 2)
-    return batch_ffn(x, batch, norm_w, eps, hot, has_cold ? cold : nullptr, has_cold ? active : nullptr,
-                     act == OI2_ACT_RELU, act_on_both != 0, add_residual, out, y32, workspace,
-                     workspace_bytes, st);
-  const int expected = has_cold ? (active->expected > 0 && active->expected < cap ? active->expected : cap) : 0;
-  const int wg_cold = has_cold ? cold_wg_for(expected) : 0;
-  const int ws_wg = has_cold ? cold_wg_for(cap) : 0;
-  OI2_CHECK_ARG(workspace && workspace_bytes >= ffn_ws_bytes(n_hot, ws_wg),
-                "workspace of %zu bytes is smaller than the %zu required", workspace_bytes,
-                ffn_ws_bytes(n_hot, ws_wg));
-  FfnWs ws = ffn_ws(workspace, n_hot, ws_wg);
+  return OI2_OK;
+}
+
+// The decode kernels for `batch` tokens one after another (k_prep, k_ffn_up,
+// k_ffn_down per token), every token reusing the scratch buffers in `ws`,
+// whose cold partial rows must hold c.wg_cold rows.  Nothing in `ws` needs
+// to be cleared first: every buffer is written before it is read.
+int ffn_decode_tokens(const uint16_t* x, int batch, const uint16_t* norm_w, float eps,
+                      const oi2_hot* hot, const oi2_cold* cold, const oi2_active* active, int act,
+                      int act_on_both, int add_residual, uint16_t* out, float* y32,
+                      const FfnCall& c, const FfnWs& ws, hipStream_t st) {
+  const int n_hot = c.n_hot;
+  const bool has_cold = c.has_cold;
+  const int cap = c.cap;
+  const int wg_cold = c.wg_cold;
   for (int b = 0; b < batch; ++b) {
     const uint16_t* xb = x + (size_t)b * kH;
     if (norm_w) {
@@ -1054,6 +1067,11 @@ int oi2_ffn_forward(const uint16_t* x, int32_t batch, const uint16_t* norm_w, fl
   }
   return OI2_OK;
 }
+
+
+}  // namespace oi2
+
+extern "C" {
 
 // Predictor workspace: the query q (H floats), z (rank + 64 doubles), the
 // norm's sum-of-squares partials (kDownWG floats).

@@ -163,6 +163,44 @@ __global__ void k_bup(BUpArgs a);
 __global__ void k_rmsnorm(const uint16_t* x, const uint16_t* w, float eps, uint16_t* out);
 
 size_t batch_ws_bytes(int M, int n_hot, int cap);
+// Scratch carve-up of the single-token decode FFN (k_prep / k_ffn_up /
+// k_ffn_down): h_hot, cold partial rows (one per cold workgroup), the cold
+// item total, x * w and the norm's sum-of-squares partials.
+struct FfnWs {
+  float* h_hot;
+  float* cold_part;
+  int32_t* cold_total;
+  uint16_t* xw;
+  float* ssq;
+};
+
+__host__ __device__ constexpr size_t ffn_align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// Bytes of that scratch for n_hot hot neurons and cold_wg cold workgroups.
+__host__ __device__ constexpr size_t ffn_ws_bytes(int n_hot, int cold_wg) {
+  return ffn_align256((size_t)(n_hot > 0 ? n_hot : 0) * 4 + 64) +
+         ffn_align256((size_t)cold_wg * kH * 4) + ffn_align256(64) + ffn_align256(kH * 2) +
+         ffn_align256(kDownWG * 4);
+}
+
+FfnWs ffn_ws(void* base, int n_hot, int cold_wg);
+
+// A validated oi2_ffn_forward request.
+struct FfnCall {
+  int n_hot = 0;
+  bool has_cold = false;
+  int cap = 0;       // capacity of the active list
+  int wg_cold = 0;   // cold workgroups of the launch (from the expected count)
+};
+
+int ffn_validate(const uint16_t* x, int batch, const uint16_t* norm_w, const oi2_hot* hot,
+                 const oi2_cold* cold, const oi2_active* active, int act, FfnCall* c);
+int ffn_decode_tokens(const uint16_t* x, int batch, const uint16_t* norm_w, float eps,
+                      const oi2_hot* hot, const oi2_cold* cold, const oi2_active* active, int act,
+                      int act_on_both, int add_residual, uint16_t* out, float* y32,
+                      const FfnCall& c, const FfnWs& ws, hipStream_t st);
+int cold_wg_for(int expected);
+
 int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const oi2_hot* hot,
               const oi2_cold* cold, const oi2_active* active, int relu, int both, int add_residual,
               uint16_t* out, float* y32, void* workspace, size_t workspace_bytes, hipStream_t st);

@@ -67,6 +67,11 @@ _SIGS = {
                                        c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p,
                                        c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t,
                                        c_void_p]),
+    "oi2_ffn_forward_noalloc": (c_int32, [c_void_p, c_int32, c_void_p, c_float, POINTER(Hot),
+                                          POINTER(Cold), POINTER(Active), c_int32, c_int32, c_int32,
+                                          c_void_p, c_void_p, c_void_p]),
+    "oi2_ffn_noalloc_scratch_bytes": (c_size_t, []),
+    "oi2_ffn_noalloc_max_expected": (c_int32, []),
     "oi2_predict_workspace_bytes": (c_size_t, [POINTER(Predictor)]),
     "oi2_predict": (c_int32, [c_void_p, c_int32, c_int32, POINTER(Predictor), c_float, c_void_p,
                               c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),

@@ -153,6 +153,26 @@ int oi2_sparse_ffn_dense(const uint16_t* x, int32_t rows, int32_t act, int32_t a
                          uint16_t* out, float* y32, void* workspace, size_t workspace_bytes,
                          void* stream);
 
+/* No counterpart in the reference.  oi2_ffn_forward without a workspace, for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * serving loops, harnesses that forbid hipMalloc): the same single-token
+ * decode kernels, the tokens of a batch run one after another (batch >= 2 is
+ * not routed to the matrix-core path), their scratch in a static device
+ * array of oi2_ffn_noalloc_scratch_bytes() bytes per GPU, held until the
+ * process ends.  Limits: n_hot <= 4096 and an expected active count
+ * (oi2_active.expected, or the list capacity when 0) of at most
+ * oi2_ffn_noalloc_max_expected() records (more items than expected are still
+ * processed); larger requests fail with OI2_EINVAL.  Allocates nothing.
+ * Every call on a GPU shares that GPU's array: calls that overlap on one GPU
+ * (other streams, other threads) race. */
+int oi2_ffn_forward_noalloc(const uint16_t* x, int32_t batch, const uint16_t* norm_w, float eps,
+                            const oi2_hot* hot, const oi2_cold* cold, const oi2_active* active,
+                            int32_t act, int32_t act_on_both, int32_t add_residual, uint16_t* out,
+                            float* y32, void* stream);
+/* Bytes of that static scratch array, and its largest expected active count. */
+size_t oi2_ffn_noalloc_scratch_bytes(void);
+int32_t oi2_ffn_noalloc_max_expected(void);
+
 /* ---- predictor ---------------------------------------------------------- */
 size_t oi2_predict_workspace_bytes(const oi2_predictor* p);
 
