@@ -4,23 +4,27 @@ Workload (one "step" = one token through the stack): 32 FFN layers of
 4096 x 14336 SwiGLU, batch 1, the residual stream carried between layers with
 RMSNorm in front of every FFN; 25 % of each layer's neurons hot (fp8 e4m3 with
 per-row fp32 scales, resident in HBM), the rest cold INT4 records in the split
-format, resident in HBM; a random-init bf16 predictor per layer
-(4096 -> 64 -> 14336) with its threshold calibrated so ~5 % of neurons are
-predicted active, selecting layer L+1's cold neurons from layer L's input.
-Weights are N(0, 0.02) from a fixed seed (synthetic data, nothing loaded).
+format; a random-init bf16 predictor per layer (4096 -> 64 -> 14336) with its
+threshold calibrated so ~5 % of neurons are predicted active, selecting layer
+L+1's cold neurons from layer L's input.  Weights are N(0, 0.02) from a fixed
+seed (synthetic data, nothing loaded).
 
-Prints one JSON line.  `value` is tokens/s with every input already in HBM,
-on the stack's default path: one persistent kernel per token (k_token, all 32
-layers in one launch) where the configuration allows it, else two launches
-per layer.  `roofline` is that dominant kernel: k_token's mean duration comes
-from back-to-back launches between two hipEvents on the launch stream, and its
-algorithmic bytes are the 32 layers' weights it must read (hot gate/up/down
-fp8 rows and scales, every active cold record, both predictor projections)
-plus the token and per-layer activations.  `kernels` gives the two-launch
-path's k_ffn_up / k_ffn_down the same way, and `two_launch_tok_s` that path's
-whole-token rate.  `cpu_baseline` is the restated reference CPU path
-(per-neuron record decode loop + F.linear FFN) over a few recorded tokens,
-bounded to ~20 s.
+Prints one JSON line.  `value` is tokens/s of that workload with the cold
+store in pinned host memory and each layer's active records staged into HBM
+over PCIe one layer ahead (a copy kernel on a side stream beside the FFN,
+signalled on the device): the PCIe-bound configuration.  Every other input
+(hot weights, predictors, the token) is already in HBM.  `staging` reports the
+H2D rate against the measured link.  `hbm_resident` is the same workload with
+the records in HBM too, decoded by the persistent token kernel; `roofline` is
+that kernel (k_token), the decode path's dominant HBM kernel: its mean
+duration from back-to-back launches between two hipEvents on the launch
+stream, its algorithmic bytes the 32 layers' weights it must read (hot
+gate/up/down fp8 rows and scales, every active cold record, both predictor
+projections) plus the token and per-layer activations.  `cold_dequant` is the
+fused cold INT4 gather/dequant/FFN kernel alone, and the read_neurons
+dequant, in GB/s of records against the HBM peak.  `cpu_baseline` is the
+restated reference CPU path (per-neuron record decode loop + F.linear FFN)
+over a few recorded tokens, bounded to ~20 s.
 """
 import argparse
 import json
@@ -41,8 +45,10 @@ HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch on this workload, from rocprofv3 --pmc runs
 # (FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000 KiB, the factors being what each
 # counter reads for a plain 256 MiB copy, --copy-calibration)
-UP_TRAFFIC_BYTES = (16570.2 * 2.0 + 2084.7) * 1024       # k_ffn_up
-TOKEN_TRAFFIC_BYTES = (800563.6 * 2.0 + 14292.8) * 1024     # k_token
+TOKEN_TRAFFIC_BYTES = (800502.4 * 2.0 + 14267.4) * 1024     # k_token
+TOKEN_TRAFFIC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE of k_token on this workload, "
+                        "profiles/k_token_traffic_decode32_bs1.md")
+COPY_WORKGROUPS = 8          # the staging copy kernel's workgroups (swept: 6 / 8 / 10 / 12 / 16)
 
 
 def log(msg):
@@ -106,11 +112,18 @@ def cpu_baseline(layers, tokens, max_seconds):
         neurons += nn
         n_steps += len(samples)
     per_layer = secs / n_steps
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = os.cpu_count()
     return {
         "value": 1.0 / (per_layer * N_LAYERS),
         "unit": "tok/s",
         "cores": 1,
         "kind": "port",
+        "host_cpu_count": os.cpu_count(),
+        "host_affinity_cpus": affinity,
+        "torch_threads_default": torch.get_num_threads(),
         "sample": (f"{n_steps} layer-steps ({len(tokens)} tokens x {n_steps // len(tokens)} of 32 "
                    f"layers, {neurons} cold neurons) through the restated reference CPU path "
                    f"(per-neuron bytes/frombuffer/dequantize_int4 record loop + fp32 F.linear "
@@ -121,42 +134,57 @@ def cpu_baseline(layers, tokens, max_seconds):
     }
 
 
-def measure_staging(layers, st, thr, x0, stream, steps, mean_active):
-    """The same 32-layer decode with every layer's cold records in pinned host
-    memory: each layer's active records are copied over PCIe on a side stream
-    while the previous layer computes.  Reports tok/s, the copy's rate, and a
-    plain pinned host-to-device copy as the link reference."""
+def timed_decode(st, x0, stream, warmup, steps):
+    """Warm up, then time `steps` tokens back to back on `stream` (each fed
+    the previous output) between two events, bracketed by synchronisation;
+    status() after each phase raises if a device-side wait overran."""
     import torch
-    from oi2.stack import DecodeStack, StackLayer
-    t0 = time.time()
-    pinned = [l.records.cpu().pin_memory() for l in layers]
-    sst = DecodeStack([StackLayer(l.hot, p, l.lut, l.norm_w, l.predictor)
-                       for l, p in zip(layers, pinned)], INTER, EPS, "silu", False, thr,
-                      staging=16)
-    sst.set_expected_active(int(1.3 * ACTIVE_FRAC * (INTER - N_HOT)))
-    log(f"pinned host store {sum(p.numel() for p in pinned) / 1e9:.2f} GB in {time.time() - t0:.1f}s")
     bufs = [x0.clone(), torch.empty_like(x0)]
     with torch.cuda.stream(stream):
-        for i in range(8):
-            sst.decode(bufs[i % 2], bufs[(i + 1) % 2], stream)
+        for i in range(warmup):
+            st.decode(bufs[i % 2], bufs[(i + 1) % 2], stream)
     stream.synchronize()
+    st.status(stream)
+    torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t_start = time.perf_counter()
     with torch.cuda.stream(stream):
         e0.record(stream)
         for i in range(steps):
-            sst.decode(bufs[i % 2], bufs[(i + 1) % 2], stream)
+            k = warmup + i
+            st.decode(bufs[k % 2], bufs[(k + 1) % 2], stream)
         e1.record(stream)
     stream.synchronize()
-    secs = max(time.perf_counter() - t_start, e0.elapsed_time(e1) / 1e3)
-    with torch.cuda.stream(stream):
-        gather_us = sst.profile_staging(bufs[0], bufs[1], stream, reps=2)
-    _, counts, _, _ = sst.trace()
     torch.cuda.synchronize()
-    active = counts.sum(1).float().mean().item()
-    # link reference: one 256 MiB pinned host -> device copy
+    wall = time.perf_counter() - t_start
+    st.status(stream)
+    secs = max(wall, e0.elapsed_time(e1) / 1e3)
+    k = warmup + steps
+    return secs, bufs[k % 2]
+
+
+def mean_active_over(st, x, stream, n):
+    """Mean active cold records per layer over n tokens of the chain from x."""
+    import torch
+    tot = 0.0
+    a, b = x.clone(), torch.empty_like(x)
+    for _ in range(n):
+        with torch.cuda.stream(stream):
+            st.decode(a, b, stream)
+        stream.synchronize()
+        _, counts, _, _ = st.trace()
+        torch.cuda.synchronize()
+        tot += counts.sum(1).float().mean().item()
+        a, b = b, a
+    st.status(stream)
+    return tot / n
+
+
+def pcie_link_gbs(dev):
+    """The link reference: one 256 MiB pinned host -> device copy, 4 times."""
+    import torch
     src = torch.empty(256 << 20, dtype=torch.uint8).pin_memory()
-    dst = torch.empty(256 << 20, dtype=torch.uint8, device=x0.device)
+    dst = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
     dst.copy_(src, non_blocking=True)
     torch.cuda.synchronize()
     c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -165,26 +193,96 @@ def measure_staging(layers, st, thr, x0, stream, steps, mean_active):
         dst.copy_(src, non_blocking=True)
     c1.record()
     torch.cuda.synchronize()
-    h2d_gbs = 4 * src.numel() / (c0.elapsed_time(c1) / 1e3) / 1e9
-    gather_gbs = active * 6400 / (gather_us * 1e-6) / 1e9
-    tok_s = steps / secs
-    out = {
-        "tok_s": tok_s,
-        "steps": steps,
-        "store": "pinned host memory (hipHostMalloc via torch pin_memory), 32 x 68.8 MB",
-        "copy_us_per_layer": gather_us,
-        "copy_gbs": gather_gbs,
-        "h2d_bytes_per_token": N_LAYERS * active * 6400,
-        "h2d_gbs_end_to_end": N_LAYERS * active * 6400 * tok_s / 1e9,
-        "h2d_link_gbs_pinned_memcpy": h2d_gbs,
-        "pcie_bound_tok_s": h2d_gbs * 1e9 / (N_LAYERS * active * 6400),
-        "mean_active_cold": active,
-    }
-    log(f"staged: {tok_s:.1f} tok/s; copy {gather_us:.1f} us/layer ({gather_gbs:.1f} GB/s); "
-        f"pinned memcpy {h2d_gbs:.1f} GB/s")
-    sst.close()
-    del pinned
-    return out
+    gbs = 4 * src.numel() / (c0.elapsed_time(c1) / 1e3) / 1e9
+    del src, dst
+    return gbs
+
+
+def build_staged(layers, thr):
+    """The same 32 layers with every layer's cold records in pinned host
+    memory, staged into HBM one layer ahead by COPY_WORKGROUPS copy
+    workgroups."""
+    import torch
+    from oi2.stack import DecodeStack, StackLayer
+    t0 = time.time()
+    pinned = [l.records.cpu().pin_memory() for l in layers]
+    sst = DecodeStack([StackLayer(l.hot, p, l.lut, l.norm_w, l.predictor)
+                       for l, p in zip(layers, pinned)], INTER, EPS, "silu", False, thr,
+                      staging=COPY_WORKGROUPS)
+    sst.set_expected_active(int(1.3 * ACTIVE_FRAC * (INTER - N_HOT)))
+    log(f"pinned host store {sum(p.numel() for p in pinned) / 1e9:.2f} GB in {time.time() - t0:.1f}s")
+    return sst, pinned
+
+
+def measure_cold_dequant(layers, dev, reps=4):
+    """The cold INT4 path alone, in GB/s of records against the HBM peak.
+    fused: oi2_ffn_forward with no hot half over every cold record of a layer
+    (10752 records, 68.8 MB: the fetch-everything case of a layer without a
+    predictor), all 32 layers back to back (1.05 GB of distinct records), so
+    nothing is served from cache; the two launches per layer (gather,
+    dequantise, gate/up dot, activation, down accumulate into partial rows;
+    then the partial-row sum) are timed together.
+    read_neurons: oi2_dequant_records on config 1's active set (1147 records)
+    of each layer, fp32 gate/up/down out, as ColdWeightStore.read_neurons
+    returns them."""
+    import torch
+    from oi2.layer import ColdNeurons, _ffn, workspace_bytes
+    from oi2.store import ColdSection
+    from oi2 import _lib
+    x = torch.randn((1, H), device=dev).half()
+    colds, wss = [], []
+    for l in layers:
+        n = l.records.shape[0]
+        sec = ColdSection(0, l.cold_ids.cpu().numpy(), l.records, l.lut, l.lut.cpu().numpy(), INTER)
+        c = ColdNeurons.from_slots(sec, torch.arange(n, dtype=torch.int32, device=dev))
+        c.expected = 2048           # 512 cold workgroups, ~5 records per wave
+        colds.append(c)
+    ws = torch.empty(workspace_bytes(1, None, colds[0]), dtype=torch.uint8, device=dev)
+    for l, c in zip(layers, colds):
+        _ffn(x, l.norm_w, EPS, None, c, "silu", False, add_residual=True, workspace=ws)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        for l, c in zip(layers, colds):
+            _ffn(x, l.norm_w, EPS, None, c, "silu", False, add_residual=True, workspace=ws)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (reps * len(layers))
+    n_rec = layers[0].records.shape[0]
+    rec_bytes = n_rec * 6400
+    fused = {"records": n_rec, "us_per_layer": us, "record_gbs": rec_bytes / (us * 1e-6) / 1e9,
+             "frac_of_hbm_peak": rec_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS,
+             "neurons_per_s": n_rec / (us * 1e-6)}
+    # read_neurons: dequantised fp32 tensors out
+    L = _lib.lib()
+    g = torch.Generator(device=dev).manual_seed(3)
+    n_act = 1147
+    slots = [torch.randperm(l.records.shape[0], generator=g, device=dev)[:n_act].int() for l in layers]
+    outs = [torch.empty((n_act, H), dtype=torch.float32, device=dev) for _ in range(2)] + \
+        [torch.empty((H, n_act), dtype=torch.float32, device=dev)]
+
+    def dq(l, sl):
+        _lib.check(L.oi2_dequant_records(l.records.data_ptr(), l.records.shape[0], sl.data_ptr(), n_act,
+                                         outs[0].data_ptr(), outs[1].data_ptr(), outs[2].data_ptr(),
+                                         _lib.stream_handle(dev)))
+    for l, sl in zip(layers, slots):
+        dq(l, sl)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(reps):
+        for l, sl in zip(layers, slots):
+            dq(l, sl)
+    e1.record()
+    torch.cuda.synchronize()
+    us2 = e0.elapsed_time(e1) * 1e3 / (reps * len(layers))
+    rb = n_act * 6400
+    wb = 3 * n_act * H * 4
+    read = {"records": n_act, "us": us2, "record_gbs": rb / (us2 * 1e-6) / 1e9,
+            "hbm_gbs_records_plus_fp32_out": (rb + wb) / (us2 * 1e-6) / 1e9,
+            "frac_of_hbm_peak": (rb + wb) / (us2 * 1e-6) / 1e9 / HBM_PEAK_GBS,
+            "neurons_per_s": n_act / (us2 * 1e-6)}
+    return {"fused_cold_ffn": fused, "read_neurons_dequant": read}
 
 
 def measure_multi_token(layers, dev, M, frac, reps, seed=1):
@@ -309,15 +407,19 @@ def main():
     ap.add_argument("--cpu-tokens", type=int, default=6)
     ap.add_argument("--no-multi-token", dest="multi_token", action="store_false",
                     help="skip the 8 / 64 / 512-token matrix-core measurements")
-    ap.add_argument("--staging-steps", type=int, default=64,
-                    help="tokens timed with the cold store in pinned host memory (0: skip)")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--no-split-writer", dest="split_writer", action="store_false",
                     help="skip the device split writer measurement")
+    ap.add_argument("--no-cold-dequant", dest="cold_dequant", action="store_false",
+                    help="skip the cold INT4 dequant GB/s measurement")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 256 MiB device copy 8 times (the reference kernel "
                          "for scaling FETCH_SIZE / WRITE_SIZE counter readings) and exit")
+    ap.add_argument("--hbm-only", action="store_true",
+                    help="only the HBM-resident token kernel leg (for profiling k_token)")
+    ap.add_argument("--cold-only", action="store_true",
+                    help="only the cold INT4 dequant measurement (for profiling the cold kernels)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
@@ -340,69 +442,63 @@ def main():
     layers, st, thr, g = build_stack(args.seed, dev)
     torch.cuda.synchronize()
     log(f"built 32-layer stack in {time.time() - t0:.1f}s, threshold logit {thr:.4f}")
-
+    if args.cold_only:
+        cold = measure_cold_dequant(layers, dev)
+        print(json.dumps({"cold_dequant": cold}), flush=True)
+        return
     stream = torch.cuda.Stream(device=dev)
-    bufs = [torch.randn(H, generator=g, device=dev).half(), torch.empty(H, dtype=torch.float16, device=dev)]
-    with torch.cuda.stream(stream):
-        for i in range(args.warmup):
-            st.decode(bufs[i % 2], bufs[(i + 1) % 2], stream)
-    stream.synchronize()
-    st.status(stream)          # raises if any warmup token's device-wide wait ran past its bound
-    torch.cuda.synchronize()
-    log(f"warmup {args.warmup} tokens done")
+    x0 = torch.randn(H, generator=g, device=dev).half()
 
-    base = args.warmup
-    ev0 = torch.cuda.Event(enable_timing=True)
-    ev1 = torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    t_start = time.perf_counter()
-    with torch.cuda.stream(stream):
-        ev0.record(stream)
-        for i in range(args.steps):
-            k = base + i
-            st.decode(bufs[k % 2], bufs[(k + 1) % 2], stream)
-        ev1.record(stream)
-    stream.synchronize()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t_start
-    st.status(stream)          # every timed token's waits ended within their bound
-    gpu_ms = ev0.elapsed_time(ev1)
-    secs = max(wall, gpu_ms / 1e3)
-    tok_s = args.steps / secs
-    log(f"timed {args.steps} tokens: {secs * 1e3:.2f} ms ({tok_s:.1f} tok/s)")
+    # ---- the headline: config 3, cold store in pinned host memory, staged ----
+    staged = None
+    if not args.hbm_only:
+        sst, pinned = build_staged(layers, thr)
+        secs, x_last = timed_decode(sst, x0, stream, args.warmup, args.steps)
+        tok_s = args.steps / secs
+        log(f"staged: timed {args.steps} tokens in {secs * 1e3:.2f} ms ({tok_s:.1f} tok/s)")
+        # the bytes each token moves: active records per layer over 16 more
+        # tokens of the same chain
+        active_st = mean_active_over(sst, x_last, stream, 16)
+        with torch.cuda.stream(stream):
+            copy_us = sst.profile_staging(x0, torch.empty_like(x0), stream, reps=2)
+        torch.cuda.synchronize()
+        link = pcie_link_gbs(dev)
+        h2d_bytes = N_LAYERS * active_st * 6400
+        staged = {"tok_s": tok_s, "ms_per_token": secs * 1e3 / args.steps, "steps": args.steps,
+                  "store": "pinned host memory (hipHostMalloc via torch pin_memory), 32 x 68.8 MB",
+                  "copy_workgroups": COPY_WORKGROUPS,
+                  "copy_alone_us_per_layer": copy_us,
+                  "copy_alone_gbs": active_st * 6400 / (copy_us * 1e-6) / 1e9,
+                  "h2d_bytes_per_token": h2d_bytes,
+                  "h2d_gbs_end_to_end": h2d_bytes * tok_s / 1e9,
+                  "h2d_link_gbs_pinned_memcpy": link,
+                  "pcie_bound_tok_s": link * 1e9 / h2d_bytes,
+                  "frac_of_pcie_bound": tok_s / (link * 1e9 / h2d_bytes),
+                  "mean_active_cold": active_st}
+        log(f"staged: {tok_s:.1f} tok/s = {staged['frac_of_pcie_bound']:.3f} of the PCIe bound "
+            f"({staged['pcie_bound_tok_s']:.1f} tok/s at {link:.1f} GB/s); copy alone {copy_us:.1f} us/layer")
+        sst.close()
+        del pinned
 
+    # ---- the same workload with the records in HBM: the token kernel ----
+    secs_h, xi = timed_decode(st, x0, stream, args.warmup, args.steps)
+    hbm_tok_s = args.steps / secs_h
+    log(f"HBM-resident: timed {args.steps} tokens in {secs_h * 1e3:.2f} ms ({hbm_tok_s:.1f} tok/s)")
     token_path = st.token_kernel
-    # the two-launch path's whole-token rate, for comparison
     two_tok_s = None
     if token_path:
         st.set_token_kernel(False)
-        n2 = min(args.steps, 128)
-        with torch.cuda.stream(stream):
-            for i in range(4):
-                st.decode(bufs[i % 2], bufs[(i + 1) % 2], stream)
-        stream.synchronize()
-        torch.cuda.synchronize()
-        t2 = time.perf_counter()
-        with torch.cuda.stream(stream):
-            ev0.record(stream)
-            for i in range(n2):
-                st.decode(bufs[i % 2], bufs[(i + 1) % 2], stream)
-            ev1.record(stream)
-        stream.synchronize()
-        two_tok_s = n2 / max(time.perf_counter() - t2, ev0.elapsed_time(ev1) / 1e3)
+        s2, _ = timed_decode(st, x0, stream, 4, min(args.steps, 128))
+        two_tok_s = min(args.steps, 128) / s2
         st.set_token_kernel(True)
         log(f"two-launch path: {two_tok_s:.1f} tok/s")
-
-    # mean kernel durations: the token kernel launched back to back between two
-    # hipEvents on the launch stream; then every layer's ffn_up of the
-    # two-launch path the same way, then every layer's ffn_down
-    k = base + args.steps
-    xi, xo = bufs[k % 2], bufs[(k + 1) % 2]
+    xo = torch.empty_like(xi)
     tok_us = None
     with torch.cuda.stream(stream):
         if token_path:
             tok_us = st.profile_token(xi, xo, stream, reps=args.profile_reps)
         up_us, down_us = st.profile(xi, xo, stream, reps=args.profile_reps)
+    st.status(stream)
     xs, counts, slots, ids = st.trace()
     torch.cuda.synchronize()
     c = counts.sum(1).cpu().tolist()
@@ -420,14 +516,37 @@ def main():
         log(f"token kernel {tok_us:.1f} us/launch {tok_gbs:.0f} GB/s ({token_bytes / 1e6:.1f} MB)")
         roofline = {"bound": "hbm", "achieved": tok_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": tok_gbs / HBM_PEAK_GBS, "traffic": TOKEN_TRAFFIC_BYTES,
-                    "kernel": "k_token", "us_per_launch": tok_us, "bytes_per_launch": token_bytes}
+                    "traffic_source": TOKEN_TRAFFIC_SOURCE, "kernel": "k_token",
+                    "us_per_launch": tok_us, "bytes_per_launch": token_bytes,
+                    "workload": "the same 32 layers with the cold records in HBM (hbm_resident): "
+                                "the decode kernel on its own; the staged headline is bound by PCIe, "
+                                "see staging"}
     else:
         roofline = {"bound": "hbm", "achieved": up_gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": up_gbs / HBM_PEAK_GBS, "traffic": UP_TRAFFIC_BYTES,
-                    "kernel": "k_ffn_up", "us_per_launch": up_us, "bytes_per_launch": up_b}
+                    "frac": up_gbs / HBM_PEAK_GBS, "traffic": None, "kernel": "k_ffn_up",
+                    "us_per_launch": up_us, "bytes_per_launch": up_b}
+    hbm_resident = {"tok_s": hbm_tok_s, "ms_per_token": secs_h * 1e3 / args.steps,
+                    "path": "token kernel" if token_path else "two launches per layer",
+                    "two_launch_tok_s": two_tok_s, "token_bytes": token_bytes,
+                    "hbm_frac_end_to_end": token_bytes * hbm_tok_s / (HBM_PEAK_GBS * 1e9),
+                    "cold_neurons_per_s": mean_active * N_LAYERS * hbm_tok_s,
+                    "mean_active_cold": mean_active,
+                    "kernels": {"k_ffn_up": {"us_per_launch": up_us, "achieved_gbs": up_gbs,
+                                             "bytes_per_launch": up_b},
+                                "k_ffn_down": {"us_per_launch": down_us, "achieved_gbs": down_gbs,
+                                               "bytes_per_launch": down_b}}}
+
+    cold = None
+    if args.cold_dequant and not args.hbm_only:
+        cold = measure_cold_dequant(layers, dev)
+        f, r = cold["fused_cold_ffn"], cold["read_neurons_dequant"]
+        log(f"cold INT4 fused gather/dequant/FFN: {f['records']} records in {f['us_per_layer']:.1f} us "
+            f"= {f['record_gbs']:.0f} GB/s of records ({f['frac_of_hbm_peak']:.3f} of HBM peak); "
+            f"read_neurons dequant {r['records']} records in {r['us']:.1f} us "
+            f"({r['hbm_gbs_records_plus_fp32_out']:.0f} GB/s with its fp32 output)")
 
     multi = None
-    if args.multi_token:
+    if args.multi_token and not args.hbm_only:
         multi = {"fp16_gemm_ref_tflops": measure_gemm_reference(dev)}
         log(f"vendor fp16 GEMM 8192^3: {multi['fp16_gemm_ref_tflops']:.0f} TFLOP/s")
         for M, frac in ((8, 0.15), (64, 0.50), (512, 0.40), (1024, 0.40)):
@@ -438,18 +557,14 @@ def main():
                 f"{r['tflops']:.1f} TFLOP/s, {r['weight_gbs']:.0f} GB/s")
 
     writer = None
-    if args.split_writer:
+    if args.split_writer and not args.hbm_only:
         writer = measure_split_writer(dev)
         log(f"split writer: {writer['neurons']} cold neurons in {writer['ms_per_layer']:.2f} ms "
             f"({writer['input_gbs']:.0f} GB/s of fp32 input); restated CPU quantiser "
             f"{writer['cpu_port_us_per_neuron']:.0f} us/neuron")
 
-    staging = None
-    if args.staging_steps > 0:
-        staging = measure_staging(layers, st, thr, xi, stream, args.staging_steps, mean_active)
-
     cpu = None
-    if not args.no_cpu_baseline and args.cpu_tokens > 0:
+    if not args.no_cpu_baseline and args.cpu_tokens > 0 and not args.hbm_only:
         tokens = []
         x = xi.clone()
         y = torch.empty_like(x)
@@ -466,39 +581,42 @@ def main():
         log(f"cpu baseline {cpu['value']:.4f} tok/s over {cpu['seconds']:.1f}s, "
             f"{cpu['cold_neurons_per_s']:.0f} cold neurons/s")
 
+    if staged is not None:
+        value, secs_v, steps_v = staged["tok_s"], staged["ms_per_token"] * args.steps / 1e3, args.steps
+        workload = ("32-layer 4096x14336 SwiGLU hot/cold FFN decode, batch 1, 25% hot fp8 in HBM, "
+                    "cold INT4 records in pinned host memory staged into HBM over PCIe one layer "
+                    "ahead, bf16 predictor at 5% active")
+    else:
+        value, secs_v, steps_v = hbm_tok_s, secs_h, args.steps
+        workload = ("32-layer 4096x14336 SwiGLU hot/cold FFN decode, batch 1, 25% hot fp8 in HBM, "
+                    "cold INT4 records in HBM, bf16 predictor at 5% active")
     out = {
         "metric": "FFN decode tok/s (32L, 4096x14336, bs1); cold INT4 dequant GB/s vs HBM",
-        "value": tok_s,
+        "value": value,
         "unit": "tok/s",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": steps_v,
         "warmup": args.warmup,
-        "ms_per_step": secs * 1e3 / args.steps,
+        "ms_per_step": secs_v * 1e3 / steps_v,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp8e4m3+int4 weights, fp16 activations, fp32 accumulate",
         "data": "synthetic (seeded N(0,0.02) weights, random-init bf16 predictors)",
-        "config": {"workload": "32-layer 4096x14336 SwiGLU hot/cold FFN decode, batch 1, 25% hot "
-                               "fp8 in HBM, cold INT4 records in HBM, bf16 predictor at 5% active",
-                   "layers": N_LAYERS, "hidden": H, "intermediate": INTER, "n_hot": N_HOT,
-                   "batch": 1, "mean_active_cold": round(mean_active, 1),
+        "config": {"workload": workload, "layers": N_LAYERS, "hidden": H, "intermediate": INTER,
+                   "n_hot": N_HOT, "batch": 1, "mean_active_cold": round(mean_active, 1),
                    "parallelism": "single GPU"},
         "roofline": roofline,
-        "path": "token kernel" if token_path else "two launches per layer",
-        "two_launch_tok_s": two_tok_s,
-        "kernels": {"k_ffn_up": {"us_per_launch": up_us, "achieved_gbs": up_gbs, "bytes_per_launch": up_b,
-                                 "traffic": UP_TRAFFIC_BYTES},
-                    "k_ffn_down": {"us_per_launch": down_us, "achieved_gbs": down_gbs,
-                                   "bytes_per_launch": down_b}},
-        "token_bytes": token_bytes,
-        "hbm_frac_end_to_end": token_bytes * tok_s / (HBM_PEAK_GBS * 1e9),
-        "cold_neurons_per_s": mean_active * N_LAYERS * tok_s,
         "cpu_baseline": cpu,
-        "staging": staging,
+        "staging": staged,
+        "hbm_resident": hbm_resident,
+        "cold_dequant": cold,
         "multi_token": multi,
         "split_writer": writer,
     }
+    if cpu is not None and cold is not None:
+        out["cold_dequant"]["gpu_vs_cpu_cold_neurons"] = (
+            cold["fused_cold_ffn"]["neurons_per_s"] / cpu["cold_neurons_per_s"])
     print(json.dumps(out), flush=True)
     st.close()
 

@@ -26,8 +26,48 @@
 
 namespace oi2 {
 
+// Device-side signals between the staging copy and the kernels around it.
+// The data a signal publishes (an active list, a layer's staged records) is
+// written with agent-coherent write-through stores; each wave waits for its
+// stores' acknowledgements, the workgroup meets at a barrier, and one lane
+// adds 1 to the signal word.  A waiting wave polls that word with relaxed
+// agent-scope loads and then reads the data with ordinary loads: every
+// published address is read at most once per launch after its signal, and
+// each launch starts with clean caches, so no stale line can be hit.  No L2
+// writeback or invalidate is issued (either stalls every in-flight load of
+// the XCD).  Past `spin` polls a wait sets the error word and goes on, so
+// every wait ends.
+__device__ __forceinline__ void stage_wait(const uint32_t* word, uint32_t target, uint32_t* err,
+                                           uint32_t spin) {
+  uint32_t n = 0;
+  while (__hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+    __builtin_amdgcn_s_sleep(2);
+    if (++n >= spin) {
+      __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      break;
+    }
+  }
+}
+
+__device__ __forceinline__ void stage_signal_wg(uint32_t* word) {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_fetch_add(word, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <typename T>
+__device__ __forceinline__ void st_wt(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <typename T>
+__device__ __forceinline__ T ld_coherent(const T* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Exclusive prefix of the clamped chunk counts, per wave: lane k holds the
 // prefix of chunks k, k+64, k+128, k+192.  Returns the total.
+template <bool kCoherent = false>
 __device__ __forceinline__ int wave_chunk_prefix(const ActiveList& al, int excl[4]) {
   const int lane = lane_id();
   int total = 0;
@@ -38,7 +78,7 @@ __device__ __forceinline__ int wave_chunk_prefix(const ActiveList& al, int excl[
       const int k = lane + 64 * m;
       int c = 0;
       if (k < al.n_chunks) {
-        c = al.counts[k];
+        c = kCoherent ? ld_coherent(al.counts + k) : al.counts[k];
         c = c < 0 ? 0 : (c > al.chunk ? al.chunk : c);
       }
       int v = c;
@@ -123,8 +163,12 @@ __device__ __forceinline__ float token_r(const TokenIn& tk, f32x4 part) {
 // exact INT4 decode), h = act(...), and h * s * q over the item's down column
 // into 64 accumulators per lane; the four waves sum in LDS and the workgroup
 // writes one fp32 partial row of y, which ffn_down sums.
+// Record buffers per cold wave (measured: 2, 3 and 4 run alike; 2 needs the
+// fewest registers).
+constexpr int kColdRing = 2;
+
 __device__ void cold_role(const UpArgs& a, int wg, uint32_t* s_nat, uint32_t* s_pair,
-                          float* s_red) {
+                          float* s_red, int* s_pf) {
   const int w = threadIdx.x >> 6, lane = lane_id();
   const int n_waves = a.wg_cold * 4;
   const int gw = wg * 4 + w;
@@ -134,27 +178,67 @@ __device__ void cold_role(const UpArgs& a, int wg, uint32_t* s_nat, uint32_t* s_
   if (wg == 0 && threadIdx.x == 0) *a.cold_total = total;
   // workgroups with at least one item write a partial row; the rest leave
   if (wg * 4 >= total) return;
+  // staged records: wait for the copy to have written them
+  if (a.stage_ready) stage_wait(a.stage_ready, a.stage_target, a.stage_err, a.stage_spin);
 
-  // first item: issue its loads before the barrier
-  int i = gw;
-  int slot = (i < total) ? item_slot(a.act, excl, i) : -1;
-  bool valid = i < total && slot >= 0 && slot < a.n_records;
-  u32x4 q[6];
-  float s[6];
+  // This wave's items are k = 0, 1, ...: item i = gw + k n_waves.  Lane j
+  // holds the record slot of item kbase + j, found once for 64 items at a
+  // time by a binary search of the chunk prefix (kept in this wave's share
+  // of s_pf) and one load per lane, so no record load ever waits on a slot
+  // load behind the records in flight (a wave's loads complete in order).
+  int* pf = s_pf + w * (kMaxChunks + 4);
+#pragma unroll
+  for (int m = 0; m < 4; ++m)
+    if (lane + 64 * m < a.act.n_chunks) pf[lane + 64 * m] = excl[m];
+  int kbase = 0, lane_slot = -1;
+  auto find_slots = [&]() {
+    const int ik = gw + (kbase + lane) * n_waves;
+    lane_slot = -1;
+    if (ik < total) {
+      int lo = 0, hi = a.act.n_chunks;        // pf[lo] <= ik; hi: past the search
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (pf[mid] <= ik) lo = mid; else hi = mid;
+      }
+      const int p = lo * a.act.chunk + (ik - pf[lo]);
+      lane_slot = a.act.slots ? a.act.slots[p] : p;
+    }
+  };
+  find_slots();
+  // Items one at a time through a ring of kColdRing record buffers: while
+  // one item is computed the loads of the next kColdRing - 1 are in flight.
+  struct Rec {
+    u32x4 q[6];
+    float s[6];
+    float gbias;
+    bool valid;
+  };
   const int g0 = lane >> 2;
-  auto load_rec = [&](int sl) {
+  auto load_rec = [&](int k, Rec& R) {
+    if (k - kbase >= 64) {     // more than 64 items per wave: the next 64 slots
+      kbase += 64;
+      find_slots();
+    }
+    const int sl = gw + k * n_waves < total ? __builtin_amdgcn_readlane(lane_slot, k - kbase) : -1;
+    R.valid = sl >= 0 && sl < a.n_records;
+    if (!R.valid) return;
     const uint8_t* rec = a.records + (size_t)sl * kRecBytes;
 #pragma unroll
-    for (int it = 0; it < 6; ++it) q[it] = load16_a2(rec + kOffGate + 16 * (lane + 64 * it));
+    for (int it = 0; it < 6; ++it) R.q[it] = load16_a2(rec + kOffGate + 16 * (lane + 64 * it));
     const uint16_t* sc = reinterpret_cast<const uint16_t*>(rec + kOffScales);
 #pragma unroll
     for (int v = 0; v < 3; ++v) {
-      s[2 * v] = half_bits_to_float(sc[32 * v + g0]);
-      s[2 * v + 1] = half_bits_to_float(sc[32 * v + 16 + g0]);
+      R.s[2 * v] = half_bits_to_float(sc[32 * v + g0]);
+      R.s[2 * v + 1] = half_bits_to_float(sc[32 * v + 16 + g0]);
     }
+    R.gbias = a.cold_gbias ? a.cold_gbias[sl] : 0.0f;
   };
-  if (valid) load_rec(slot);
-  float gbias = (valid && a.cold_gbias) ? a.cold_gbias[slot] : 0.0f;
+  // the first items: their loads before the barrier
+  int i = gw;
+  Rec R[kColdRing];
+#pragma unroll
+  for (int k = 0; k < kColdRing; ++k) load_rec(k, R[k]);
+  int kn = kColdRing;           // the next item to load
   const f32x4 part = token_part(a.tok);
   stage_xw(a.tok.xw, s_nat, s_pair);
   float acc[64];
@@ -174,46 +258,51 @@ __device__ void cold_role(const UpArgs& a, int wg, uint32_t* s_nat, uint32_t* s_
         for (int k = 0; k < 4; ++k) xc[it][4 * m + k] = as_f16x2(v[k]);
       }
     }
-    for (;;) {
-      if (valid) {
-        float pg[2] = {0.0f, 0.0f}, pu[2] = {0.0f, 0.0f};
+    auto compute = [&](const Rec& R) {
+      if (!R.valid) return;
+      float pg[2] = {0.0f, 0.0f}, pu[2] = {0.0f, 0.0f};
 #pragma unroll
-        for (int it = 0; it < 2; ++it)
+      for (int it = 0; it < 2; ++it)
 #pragma unroll
-          for (int d = 0; d < 4; ++d) {
-            f16x2 t[4];
-            int4x8_to_f16x2x4(q[it][d], t);
+        for (int d = 0; d < 4; ++d) {
+          f16x2 t[4];
+          int4x8_to_f16x2x4(R.q[it][d], t);
 #pragma unroll
-            for (int k = 0; k < 4; ++k) pg[it] = dot2(t[k], xc[it][4 * d + k], pg[it]);
-            int4x8_to_f16x2x4(q[2 + it][d], t);
+          for (int k = 0; k < 4; ++k) pg[it] = dot2(t[k], xc[it][4 * d + k], pg[it]);
+          int4x8_to_f16x2x4(R.q[2 + it][d], t);
 #pragma unroll
-            for (int k = 0; k < 4; ++k) pu[it] = dot2(t[k], xc[it][4 * d + k], pu[it]);
+          for (int k = 0; k < 4; ++k) pu[it] = dot2(t[k], xc[it][4 * d + k], pu[it]);
+        }
+      float g = r * wave_sum(pg[0] * R.s[0] + pg[1] * R.s[1]);
+      const float u = r * wave_sum(pu[0] * R.s[2] + pu[1] * R.s[3]);
+      g += R.gbias;
+      const float h = gated_act(g, u, a.relu, a.both);
+      const float hs[2] = {h * R.s[4], h * R.s[5]};
+      // the record's down column, elements [32 lane + 2048 it, +32)
+#pragma unroll
+      for (int it = 0; it < 2; ++it)
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          f16x2 t[4];
+          int4x8_to_f16x2x4(R.q[4 + it][d], t);
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            acc[32 * it + 8 * d + k] = fmaf(hs[it], (float)t[k].x, acc[32 * it + 8 * d + k]);
+            acc[32 * it + 8 * d + k + 4] = fmaf(hs[it], (float)t[k].y, acc[32 * it + 8 * d + k + 4]);
           }
-        float g = r * wave_sum(pg[0] * s[0] + pg[1] * s[1]);
-        const float u = r * wave_sum(pu[0] * s[2] + pu[1] * s[3]);
-        g += gbias;
-        const float h = gated_act(g, u, a.relu, a.both);
-        const float hs[2] = {h * s[4], h * s[5]};
-        // the record's down column, elements [32 lane + 2048 it, +32)
+        }
+    };
+    bool more = true;
+    while (more) {
 #pragma unroll
-        for (int it = 0; it < 2; ++it)
-#pragma unroll
-          for (int d = 0; d < 4; ++d) {
-            f16x2 t[4];
-            int4x8_to_f16x2x4(q[4 + it][d], t);
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-              acc[32 * it + 8 * d + k] = fmaf(hs[it], (float)t[k].x, acc[32 * it + 8 * d + k]);
-              acc[32 * it + 8 * d + k + 4] = fmaf(hs[it], (float)t[k].y, acc[32 * it + 8 * d + k + 4]);
-            }
-          }
+      for (int k = 0; k < kColdRing; ++k) {
+        if (more) {
+          compute(R[k]);               // item i
+          load_rec(kn++, R[k]);        // refill: kColdRing items ahead
+          i += n_waves;
+          more = i < total;
+        }
       }
-      i += n_waves;
-      if (i >= total) break;
-      slot = item_slot(a.act, excl, i);
-      valid = slot >= 0 && slot < a.n_records;
-      if (valid) load_rec(slot);
-      gbias = (valid && a.cold_gbias) ? a.cold_gbias[slot] : 0.0f;
     }
   }
   // sum the four waves in LDS (fixed order, padded against bank conflicts),
@@ -383,10 +472,11 @@ __global__ __launch_bounds__(kThreads) void k_ffn_up(UpArgs a) {
   // hot: natural xw (8 KB); cold: paired xw (8 KB) + padded reduction (16.5 KB)
   __shared__ u32x4 s_xw4[kH / 8];
   __shared__ float s_red[kH + kH / 32];
+  __shared__ int s_pf[4 * (kMaxChunks + 4)];     // cold: each wave's chunk prefix
   uint32_t* s_xw = reinterpret_cast<uint32_t*>(s_xw4);
   int b = blockIdx.x;
   if (b < a.wg_cold) {
-    cold_role(a, b, nullptr, s_xw, s_red);
+    cold_role(a, b, nullptr, s_xw, s_red, s_pf);
     return;
   }
   b -= a.wg_cold;
@@ -487,10 +577,21 @@ __device__ void pred_u_role(const DownArgs& a, int c, int* s_wcnt) {
   for (int ww = 0; ww < w; ++ww) base += s_wcnt[ww];
   if (keep) {
     const size_t pos = (size_t)c * kSelChunk + base + wpos;
-    a.sel_slots[pos] = lutv;
-    a.sel_ids[pos] = n;
+    if (a.sel_flag) {
+      st_wt(a.sel_slots + pos, lutv);
+      st_wt(a.sel_ids + pos, n);
+    } else {
+      a.sel_slots[pos] = lutv;
+      a.sel_ids[pos] = n;
+    }
   }
-  if (t == 0) a.sel_counts[c] = s_wcnt[0] + s_wcnt[1] + s_wcnt[2] + s_wcnt[3];
+  if (t == 0) {
+    const int cnt = s_wcnt[0] + s_wcnt[1] + s_wcnt[2] + s_wcnt[3];
+    if (a.sel_flag)
+      st_wt(a.sel_counts + c, cnt);
+    else
+      a.sel_counts[c] = cnt;
+  }
 }
 
 struct DownShared {
@@ -664,6 +765,7 @@ __global__ __launch_bounds__(kThreads) void k_ffn_down(DownArgs a) {
 __global__ __launch_bounds__(kThreads) void k_pred_down(DownArgs a) {
   __shared__ int s_wcnt[4];
   pred_u_role(a, blockIdx.x, s_wcnt);
+  if (a.sel_flag) stage_signal_wg(a.sel_flag);   // this chunk of the list is written
 }
 
 // ── standalone kernels ──────────────────────────────────────────────────────
@@ -680,33 +782,100 @@ __global__ __launch_bounds__(kThreads) void k_pred_down(DownArgs a) {
 // the whole 160 KB of its CU's LDS, so no FFN workgroup lands on a CU that
 // is copying.
 constexpr int kStageLdsWords = 160 * 1024 / 4;
+
+
+// Copy one layer's active records (items of the chunked list, list position
+// p to dst + 6400 p), wave `first` of `n_waves` taking every n_waves-th item.
+// kPublish: the list is read with coherent loads and the records stored
+// write-through, for the persistent copy kernel that runs beside the kernels
+// publishing the list and reading the records.
+template <bool kPublish>
+__device__ void stage_copy_layer(const uint8_t* src_base, int n_records, const ActiveList& act, int cap,
+                                 uint8_t* dst_base, int first, int n_waves) {
+  int excl[4];
+  int total = wave_chunk_prefix<kPublish>(act, excl);
+  total = total < cap ? total : cap;
+  const int lane = lane_id();
+  constexpr int kChunks = kRecBytes / 16;   // 400
+  const __amdgpu_buffer_rsrc_t rdst =
+      __builtin_amdgcn_make_buffer_rsrc(dst_base, (short)0, (int)((uint32_t)cap * kRecBytes), 0x00020000);
+  // two records per wave in flight, both loaded before either is stored
+  // (measured: one leaves the PCIe link short of requests; three or four
+  // gain nothing over two)
+  constexpr int kInFlight = 2;
+  for (int i = first; i < total; i += kInFlight * n_waves) {
+    int p[kInFlight];
+    u32x4 v[kInFlight][7];
+#pragma unroll
+    for (int r = 0; r < kInFlight; ++r) {
+      const int ii = i + r * n_waves;
+      p[r] = ii < total ? item_pos(act, excl, ii) : -1;
+      const int slot = p[r] < 0 ? -1 : act.slots ? (kPublish ? ld_coherent(act.slots + p[r]) : act.slots[p[r]])
+                                                 : p[r];
+      const bool valid = slot >= 0 && slot < n_records;
+      const u32x4* src = reinterpret_cast<const u32x4*>(src_base + (size_t)(valid ? slot : 0) * kRecBytes);
+#pragma unroll
+      for (int it = 0; it < 7; ++it) {
+        const int c = lane + 64 * it;
+        v[r][it] = (valid && c < kChunks) ? __builtin_nontemporal_load(src + c) : u32x4{0, 0, 0, 0};
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < kInFlight; ++r) {
+      if (p[r] < 0) continue;
+#pragma unroll
+      for (int it = 0; it < 7; ++it) {
+        const int c = lane + 64 * it;
+        if (c < kChunks) {
+          if constexpr (kPublish)
+            __builtin_amdgcn_raw_buffer_store_b128(v[r][it], rdst,
+                                                   (uint32_t)p[r] * kRecBytes + 16u * (uint32_t)c, 0,
+                                                   16 /* sc1: agent-coherent write-through */);
+          else
+            reinterpret_cast<u32x4*>(dst_base + (size_t)p[r] * kRecBytes)[c] = v[r][it];
+        }
+      }
+    }
+  }
+}
+
 __global__ __launch_bounds__(kThreads) void k_stage_gather(StageArgs a) {
   __shared__ uint32_t s_reserve[kStageLdsWords];
   if (a.cap < 0) reinterpret_cast<volatile uint32_t*>(s_reserve)[threadIdx.x] = 0;  // never runs
-  int excl[4];
-  int total = wave_chunk_prefix(a.act, excl);
-  total = total < a.cap ? total : a.cap;
-  const int lane = lane_id();
-  const int n_waves = gridDim.x * (kThreads / kWave);
-  constexpr int kChunks = kRecBytes / 16;   // 400
-  for (int i = blockIdx.x * (kThreads / kWave) + (int)(threadIdx.x >> 6); i < total; i += n_waves) {
-    const int p = item_pos(a.act, excl, i);
-    const int slot = a.act.slots ? a.act.slots[p] : p;
-    const bool valid = slot >= 0 && slot < a.n_records;
-    const u32x4* src = reinterpret_cast<const u32x4*>(a.src + (size_t)(valid ? slot : 0) * kRecBytes);
-    u32x4* dst = reinterpret_cast<u32x4*>(a.dst + (size_t)p * kRecBytes);
-    u32x4 v[7];
-#pragma unroll
-    for (int it = 0; it < 7; ++it) {
-      const int c = lane + 64 * it;
-      v[it] = (valid && c < kChunks) ? __builtin_nontemporal_load(src + c) : u32x4{0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int it = 0; it < 7; ++it) {
-      const int c = lane + 64 * it;
-      if (c < kChunks) dst[c] = v[it];
-    }
+  stage_copy_layer<false>(a.src, a.n_records, a.act, a.cap, a.dst,
+                          blockIdx.x * (kThreads / kWave) + (int)(threadIdx.x >> 6),
+                          gridDim.x * (kThreads / kWave));
+}
+
+// The whole token's staging in one launch on the side stream: for each layer
+// in turn, wait until its active list is complete (sel[L]), copy its records
+// as k_stage_gather does, and signal ready[L] per workgroup (measured faster
+// than a signal per wave, which lets the waves drift apart).  Its workgroups
+// reserve their CUs' LDS like k_stage_gather.  The buffer a layer's records
+// go to was last read by the FFN two layers back, which the main stream
+// finishes before it signals this layer's selection.
+__global__ __launch_bounds__(kThreads) void k_stage_copy(StageCopyArgs a) {
+  __shared__ uint32_t s_reserve[kStageLdsWords];
+  if (a.cap < 0) reinterpret_cast<volatile uint32_t*>(s_reserve)[threadIdx.x] = 0;  // never runs
+  uint32_t* err = a.sync + stage_err_word(a.n_layers);
+  for (int L = 0; L < a.n_layers; ++L) {
+    const StageLayer T = a.layers[L];
+    if (T.n_records == 0) continue;
+    stage_wait(a.sync + stage_sel_word(L), T.sel_target, err, a.spin);
+    stage_copy_layer<true>(T.src, T.n_records, T.act, a.cap, T.dst,
+                           blockIdx.x * (kThreads / kWave) + (int)(threadIdx.x >> 6),
+                           gridDim.x * (kThreads / kWave));
+    stage_signal_wg(a.sync + stage_ready_word(L));
   }
+}
+
+// Main-stream signal of a layer whose list needs no selection kernel.
+__global__ void k_stage_signal(uint32_t* word) {
+  if (threadIdx.x == 0) __hip_atomic_fetch_add(word, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__global__ __launch_bounds__(kThreads) void k_fill_u32(uint32_t* p, int n, uint32_t v) {
+  for (int i = blockIdx.x * kThreads + threadIdx.x; i < n; i += gridDim.x * kThreads) p[i] = v;
 }
 
 

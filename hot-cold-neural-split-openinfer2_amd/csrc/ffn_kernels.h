@@ -60,6 +60,12 @@ struct UpArgs {
   const float* pd_q;          // precomputed query (H), or null
   double* pd_z;
   int wg_cold, wg_pred, wg_hot;
+  // staged records: the cold workgroups wait until *stage_ready reaches
+  // stage_target before reading them (null: no wait)
+  const uint32_t* stage_ready;
+  uint32_t stage_target;
+  uint32_t* stage_err;
+  uint32_t stage_spin;
 };
 
 struct DownArgs {
@@ -97,6 +103,7 @@ struct DownArgs {
   float* logits_out;
   float* probs_out;
   uint8_t* mask_out;
+  uint32_t* sel_flag;       // each selection workgroup adds 1 once its chunk is written (or null)
   int wg_pred, wg_down;
 };
 
@@ -110,6 +117,39 @@ struct StageArgs {
 };
 
 __global__ void k_stage_gather(StageArgs a);
+
+// Staged decode with device-side signals (one token at a time).  The sync
+// area holds, one 128-byte line each: sel[L] (workgroups of layer L's
+// selection kernel that have written their chunk of the active list, or 1
+// from k_stage_signal for a layer without a predictor), ready[L] (copy
+// workgroups done with layer L's records) and an error word set when a wait
+// runs past its bound.  The counters are cleared by k_fill_u32 at the start of
+// every token.
+constexpr int kStageLine = 32;    // words per counter
+__host__ __device__ constexpr int stage_sel_word(int L) { return kStageLine * (2 * L); }
+__host__ __device__ constexpr int stage_ready_word(int L) { return kStageLine * (2 * L + 1); }
+__host__ __device__ constexpr int stage_err_word(int n_layers) { return kStageLine * (2 * n_layers); }
+__host__ __device__ constexpr int stage_sync_words(int n_layers) { return kStageLine * (2 * n_layers + 1); }
+
+struct StageLayer {
+  const uint8_t* src;       // the layer's records (device or pinned host memory)
+  int n_records;            // 0: nothing to stage
+  ActiveList act;
+  uint8_t* dst;             // staging buffer: list position p at dst + 6400 p
+  uint32_t sel_target;      // sel[L] value meaning the list is complete
+};
+
+struct StageCopyArgs {
+  const StageLayer* layers; // (n_layers) device table
+  int n_layers;
+  int cap;
+  uint32_t* sync;
+  uint32_t spin;            // poll bound of each wait
+};
+
+__global__ void k_stage_copy(StageCopyArgs a);
+__global__ void k_stage_signal(uint32_t* word);
+__global__ void k_fill_u32(uint32_t* p, int n, uint32_t v);
 
 // Multi-token FFN on the matrix cores (ffn_batch.hip).
 struct BUpArgs {

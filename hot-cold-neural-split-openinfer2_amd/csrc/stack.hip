@@ -52,9 +52,13 @@ struct oi2_stack {
   bool staged = false;
   int copy_wg = 0;                           // workgroups of the staging copy kernel
   hipStream_t side = nullptr;
+  hipStream_t own = nullptr;                 // runs a staged token asked for on the NULL stream
   uint8_t* stage[2] = {nullptr, nullptr};
   std::vector<const uint8_t*> src;           // per layer: device-visible address of the records
-  std::vector<hipEvent_t> ev_sel, ev_ready;
+  uint32_t* stage_sync = nullptr;            // sel / ready counters and the error word
+  oi2::StageLayer* stage_tab = nullptr;      // per layer: what the copy kernel stages
+  uint32_t stage_spin = 1u << 20;            // poll bound of the staged waits
+  hipEvent_t ev_fork = nullptr, ev_join = nullptr, ev_null_in = nullptr, ev_null_out = nullptr;
   struct GraphEntry {
     hipGraphExec_t exec;
     const void* in;
@@ -127,6 +131,10 @@ static void layer_args(const oi2_stack* s, int L, const uint16_t* x_in, uint16_t
       ua.records = s->stage[L & 1];
       ua.n_records = s->cold_cap;
       ua.act.slots = nullptr;
+      ua.stage_ready = s->stage_sync + stage_ready_word(L);
+      ua.stage_target = (uint32_t)s->copy_wg;   // one arrival per copy workgroup
+      ua.stage_err = s->stage_sync + stage_err_word(n);
+      ua.stage_spin = s->stage_spin;
     } else {
       ua.records = s->src[L];
       ua.n_records = l.cold.n_records;
@@ -227,8 +235,19 @@ static int launch_predictor(oi2_stack* s, int P, const uint16_t* x, hipStream_t 
   da.sel_slots = s->sel_slots + (size_t)P * sel_stride;
   da.sel_ids = s->sel_ids + (size_t)P * sel_stride;
   da.sel_counts = s->sel_counts + (size_t)P * s->n_chunks;
+  da.sel_flag = s->staged ? s->stage_sync + stage_sel_word(P) : nullptr;
   da.wg_pred = s->n_chunks;
   hipLaunchKernelGGL(k_pred_down, dim3(da.wg_pred), dim3(kThreads), 0, st, da);
+  OI2_CHECK_LAUNCH();
+  return OI2_OK;
+}
+
+// Staged decode: layer P's list is complete (its predictor's selection
+// workgroups signal that themselves; a layer without one is signalled here,
+// at the point of the main stream where its predictor would run).
+static int launch_selection(oi2_stack* s, int P, const uint16_t* x, hipStream_t st) {
+  if (s->layers[P].has_pred) return launch_predictor(s, P, x, st);
+  hipLaunchKernelGGL(k_stage_signal, dim3(1), dim3(64), 0, st, s->stage_sync + stage_sel_word(P));
   OI2_CHECK_LAUNCH();
   return OI2_OK;
 }
@@ -255,40 +274,61 @@ static inline const uint16_t* layer_input(const oi2_stack* s, int L, const uint1
   return L == 0 ? x_in : s->xbuf + (size_t)(L - 1) * kH;
 }
 
-// Staged token.  Main stream: predictor(L+1) on x_L, wait for layer L's
-// records, FFN(L).  Side stream: once sel[L+1] exists, copy layer L+1's
-// records.  The copy of L+1 thus runs
-// under FFN(L), and the side stream rejoins the main one before the last FFN.
+// Staged token.  Main stream: clear the signal counters, then
+// selection(L+1) on x_L ahead of FFN(L) for every layer; FFN(L)'s cold
+// workgroups wait on the device until layer L's records are staged.  Side
+// stream: one k_stage_copy for the whole token, which copies each layer's
+// records as soon as its selection is signalled.  The two streams meet once
+// at the start of the token and once at its end; everything in between is
+// ordered by device-side signals with bounded waits.
+static int stack_launch_staged_on(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, hipStream_t st);
+
 static int stack_launch_staged(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, hipStream_t st) {
+  if (st != nullptr) return stack_launch_staged_on(s, x_in, x_out, st);
+  // On the NULL stream the token runs on the stack's own stream, ordered
+  // after the NULL stream's earlier work and before its later work: the
+  // NULL stream's implicit synchronisation with other streams must not come
+  // between the two streams that signal each other.
+  OI2_CHECK_HIP(hipEventRecord(s->ev_null_in, nullptr));
+  OI2_CHECK_HIP(hipStreamWaitEvent(s->own, s->ev_null_in, 0));
+  int rc = stack_launch_staged_on(s, x_in, x_out, s->own);
+  if (rc) return rc;
+  OI2_CHECK_HIP(hipEventRecord(s->ev_null_out, s->own));
+  OI2_CHECK_HIP(hipStreamWaitEvent(nullptr, s->ev_null_out, 0));
+  return OI2_OK;
+}
+
+static int stack_launch_staged_on(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, hipStream_t st) {
   const int n = s->n_layers;
+  // the counters start at zero every token; the error word is kept until
+  // oi2_stack_status reports it
+  hipLaunchKernelGGL(k_fill_u32, dim3(1), dim3(kThreads), 0, st, s->stage_sync,
+                     stage_err_word(n), 0u);
+  OI2_CHECK_LAUNCH();
   hipLaunchKernelGGL(k_prep, dim3(1), dim3(kThreads), 0, st, x_in, s->layers[0].l.norm_w, s->xw,
                      s->ssq);
   OI2_CHECK_LAUNCH();
-  int rc = OI2_OK;
-  if (s->layers[0].has_pred) rc = launch_predictor(s, 0, x_in, st);
+  OI2_CHECK_HIP(hipEventRecord(s->ev_fork, st));
+  OI2_CHECK_HIP(hipStreamWaitEvent(s->side, s->ev_fork, 0));
+  StageCopyArgs ca{};
+  ca.layers = s->stage_tab;
+  ca.n_layers = n;
+  ca.cap = s->cold_cap;
+  ca.sync = s->stage_sync;
+  ca.spin = s->stage_spin;
+  hipLaunchKernelGGL(k_stage_copy, dim3(s->copy_wg), dim3(kThreads), 0, s->side, ca);
+  OI2_CHECK_LAUNCH();
+  int rc = launch_selection(s, 0, x_in, st);
   if (rc) return rc;
-  OI2_CHECK_HIP(hipEventRecord(s->ev_sel[0], st));
-  OI2_CHECK_HIP(hipStreamWaitEvent(s->side, s->ev_sel[0], 0));
-  if ((rc = launch_gather(s, 0, s->side))) return rc;
-  OI2_CHECK_HIP(hipEventRecord(s->ev_ready[0], s->side));
   for (int L = 0; L < n; ++L) {
-    if (L + 1 < n) {
-      if (s->layers[L + 1].has_pred &&
-          (rc = launch_predictor(s, L + 1, layer_input(s, L, x_in), st)))
-        return rc;
-      OI2_CHECK_HIP(hipEventRecord(s->ev_sel[L + 1], st));
-      // ev_sel[L+1] follows FFN(L-1) on the main stream, so FFN(L-1) has
-      // finished with the buffer this copy overwrites
-      OI2_CHECK_HIP(hipStreamWaitEvent(s->side, s->ev_sel[L + 1], 0));
-      if ((rc = launch_gather(s, L + 1, s->side))) return rc;
-      OI2_CHECK_HIP(hipEventRecord(s->ev_ready[L + 1], s->side));
-    }
-    OI2_CHECK_HIP(hipStreamWaitEvent(st, s->ev_ready[L], 0));
+    if (L + 1 < n && (rc = launch_selection(s, L + 1, layer_input(s, L, x_in), st))) return rc;
     UpArgs ua;
     DownArgs da;
     layer_args(s, L, x_in, x_out, ua, da);
     if ((rc = launch_up(ua, st)) || (rc = launch_down(da, st))) return rc;
   }
+  OI2_CHECK_HIP(hipEventRecord(s->ev_join, s->side));
+  OI2_CHECK_HIP(hipStreamWaitEvent(st, s->ev_join, 0));
   return OI2_OK;
 }
 
@@ -371,15 +411,20 @@ static int device_view(const uint8_t* p, const uint8_t** out) {
 }
 
 static void staging_free(oi2_stack* s) {
-  for (auto* v : {&s->ev_sel, &s->ev_ready}) {
-    for (auto e : *v)
-      if (e) (void)hipEventDestroy(e);
-    v->clear();
+  if (s->own) (void)hipStreamDestroy(s->own);
+  s->own = nullptr;
+  for (auto* e : {&s->ev_fork, &s->ev_join, &s->ev_null_in, &s->ev_null_out}) {
+    if (*e) (void)hipEventDestroy(*e);
+    *e = nullptr;
   }
   for (auto& b : s->stage) {
     if (b) (void)hipFree(b);
     b = nullptr;
   }
+  if (s->stage_sync) (void)hipFree(s->stage_sync);
+  if (s->stage_tab) (void)hipFree(s->stage_tab);
+  s->stage_sync = nullptr;
+  s->stage_tab = nullptr;
   if (s->side) (void)hipStreamDestroy(s->side);
   s->side = nullptr;
   s->staged = false;
@@ -670,7 +715,10 @@ int oi2_stack_decode(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, void* 
   OI2_CHECK_ARG(s && x_in && x_out, "null argument");
   OI2_CHECK_ARG(((uintptr_t)x_in | (uintptr_t)x_out) % 16 == 0, "x must be 16-byte aligned");
   hipStream_t st = (hipStream_t)stream;
-  if (!s->use_graph || st == nullptr) return stack_launch(s, x_in, x_out, st);
+  // a staged token is launched directly: its two streams wait on each other
+  // on the device, so both must be running at once, which direct launches on
+  // two streams guarantee and a graph's branches need not
+  if (!s->use_graph || st == nullptr || s->staged) return stack_launch(s, x_in, x_out, st);
   for (auto& g : s->graphs)
     if (g.in == x_in && g.out == x_out && g.stream == st) {
       OI2_CHECK_HIP(hipGraphLaunch(g.exec, st));
@@ -729,13 +777,29 @@ int oi2_stack_set_staging(oi2_stack* s, int32_t copy_workgroups) {
       set_error("layer %d: staging does not support a cold gate bias", L);
       return OI2_EUNSUPPORTED;
     }
+  const int n = s->n_layers;
   hipError_t e = hipStreamCreateWithFlags(&s->side, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&s->own, hipStreamNonBlocking);
   for (int b = 0; b < 2 && e == hipSuccess; ++b)
     e = hipMalloc((void**)&s->stage[b], (size_t)s->cold_cap * kRecBytes);
-  for (auto* v : {&s->ev_sel, &s->ev_ready}) {
-    v->assign(s->n_layers, nullptr);
-    for (auto& ev : *v)
-      if (e == hipSuccess) e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipMalloc((void**)&s->stage_sync, (size_t)stage_sync_words(n) * 4);
+  if (e == hipSuccess) e = hipMemset(s->stage_sync, 0, (size_t)stage_sync_words(n) * 4);
+  if (e == hipSuccess) e = hipMalloc((void**)&s->stage_tab, (size_t)n * sizeof(StageLayer));
+  for (auto* ev : {&s->ev_fork, &s->ev_join, &s->ev_null_in, &s->ev_null_out})
+    if (e == hipSuccess) e = hipEventCreateWithFlags(ev, hipEventDisableTiming);
+  if (e == hipSuccess) {
+    // what the copy kernel stages per layer: the same lists the FFN reads
+    std::vector<StageLayer> tab(n);
+    for (int L = 0; L < n; ++L) {
+      tab[L] = StageLayer{};
+      if (s->layers[L].l.cold.n_records == 0) continue;
+      tab[L].src = s->src[L];
+      tab[L].n_records = s->layers[L].l.cold.n_records;
+      tab[L].act = layer_list(s, L);
+      tab[L].dst = s->stage[L & 1];
+      tab[L].sel_target = s->layers[L].has_pred ? (uint32_t)s->n_chunks : 1u;
+    }
+    e = hipMemcpy(s->stage_tab, tab.data(), (size_t)n * sizeof(StageLayer), hipMemcpyHostToDevice);
   }
   if (e != hipSuccess) {
     set_error("staging set-up failed: %s", hipGetErrorString(e));
@@ -877,6 +941,7 @@ int oi2_stack_set_wait_bound(oi2_stack* s, int32_t polls) {
   OI2_CHECK_ARG(s, "null stack");
   OI2_CHECK_ARG(polls >= 1 && polls <= (1 << 24), "wait bound %d out of range 1 .. %d", polls, 1 << 24);
   s->tok_spin = (uint32_t)polls;
+  s->stage_spin = (uint32_t)polls;
   drop_graphs(s);   // the bound is a kernel argument
   return OI2_OK;
 }
@@ -885,6 +950,22 @@ int oi2_stack_status(oi2_stack* s, void* stream) {
   clear_error();
   OI2_CHECK_ARG(s, "null stack");
   OI2_CHECK_HIP(hipStreamSynchronize((hipStream_t)stream));
+  if (s->staged) {
+    // the staged path's device-side waits keep their own error word, set
+    // until reported here
+    uint32_t err = 0;
+    uint32_t* ew = s->stage_sync + stage_err_word(s->n_layers);
+    OI2_CHECK_HIP(hipStreamSynchronize(s->side));
+    OI2_CHECK_HIP(hipStreamSynchronize(s->own));
+    OI2_CHECK_HIP(hipMemcpy(&err, ew, 4, hipMemcpyDeviceToHost));
+    if (err != 0) {
+      OI2_CHECK_HIP(hipMemset(ew, 0, 4));
+      set_error("staged decode: a device-side wait for records ran past its bound in a token "
+                "decoded since the previous status check");
+      return OI2_EHIP;
+    }
+    return OI2_OK;
+  }
   if (!use_tok(s)) return OI2_OK;
   // the error word is nonzero once any launch since the signal words were
   // last cleared had a wait run past its bound (it holds that launch's epoch

@@ -69,16 +69,17 @@ class DecodeStack:
         return bool(_lib.lib().oi2_stack_token_kernel(self._h))
 
     def status(self, stream=None):
-        """Wait for the stream; raise OI2Error if a device-wide wait of the
-        persistent kernel ran past its bound in the last token."""
+        """Wait for the stream; raise OI2Error if a device-side wait (of the
+        persistent kernel, or of the staged path) ran past its bound in any
+        token decoded since the previous call."""
         dev = self.layers[0].norm_w.device
         s = stream.cuda_stream if stream is not None else _lib.stream_handle(dev)
         _lib.check(_lib.lib().oi2_stack_status(self._h, s or None))
 
     def set_wait_bound(self, polls: int):
-        """Bound, in polls, of the persistent kernel's device-wide waits
-        (default 1 << 20).  Past it a wait gives up and status() raises for
-        that token; meant for tests of that path."""
+        """Bound, in polls, of the device-side waits of the persistent kernel
+        and of the staged path (default 1 << 20).  Past it a wait gives up and
+        the next status() raises; meant for tests of that path."""
         _lib.check(_lib.lib().oi2_stack_set_wait_bound(self._h, int(polls)))
 
     def profile_token(self, x_in: torch.Tensor, x_out: torch.Tensor, stream=None, reps: int = 16):

@@ -237,16 +237,20 @@ int oi2_stack_set_graph(oi2_stack* s, int32_t enable);
 /* Cold-record staging, the device counterpart of the prefetch pipeline
  * (SparseFFNLayer.submit_cold_fetch / _fetch_cold, engine.py:266-272,
  * 285-290, submitted one layer ahead at engine.py:432-436).  Enabled, each
- * token runs layer L+1's predictor on x_L ahead of layer L's FFN; a copy
- * kernel on a side stream then moves layer L+1's active records from the
- * layer's record pointer into one of two HBM staging buffers while layer L
- * computes, and layer L+1's FFN reads them there.  The record pointers may
- * then be pinned host memory (hipHostMalloc, or a pinned torch tensor): the
- * copy reads it over PCIe.  Device memory also works (pageable memory is
- * rejected at creation).  copy_workgroups: workgroups of the copy kernel
- * (256 threads, one record per wave at a time), 0 disables staging; a few
- * dozen keep the PCIe link busy without crowding the FFN's HBM traffic.
- * Synchronises the device; drops captured graphs. */
+ * token runs layer L+1's selection (predictor, or a signal for a layer
+ * without one) on x_L ahead of layer L's FFN.  One copy kernel on a side
+ * stream spans the token: as soon as a layer's list is signalled complete on
+ * the device it copies that layer's active records from the layer's record
+ * pointer into one of two HBM staging buffers and signals them ready; the
+ * FFN's cold workgroups wait on the device for that signal.  The record
+ * pointers may then be pinned host memory (hipHostMalloc, or a pinned torch
+ * tensor): the copy reads it over PCIe.  Device memory also works (pageable
+ * memory is rejected at creation).  copy_workgroups: workgroups of the copy
+ * kernel (256 threads, one record per wave at a time, each holding its CU's
+ * whole LDS so no FFN workgroup shares the CU), 0 disables staging.  Staged
+ * tokens are launched directly, never through a graph.  Every device-side
+ * wait is bounded (oi2_stack_set_wait_bound); oi2_stack_status reports one
+ * that ran past its bound.  Synchronises the device; drops captured graphs. */
 int oi2_stack_set_staging(oi2_stack* s, int32_t copy_workgroups);
 /* With staging enabled: decode x_in once (fixing the active sets), time
  * every layer's record copy back to back `reps` times between two hipEvents
@@ -285,15 +289,16 @@ int oi2_stack_set_token_kernel(oi2_stack* s, int32_t enable);
 /* 1 when decodes run as the persistent token kernel, else 0. */
 int32_t oi2_stack_token_kernel(const oi2_stack* s);
 /* Waits for `stream`; OI2_EHIP if a device-wide wait of any persistent-kernel
- * token decoded since the previous call ran past its bound (the tokens
- * decoded since then are to be taken as invalid; the signal words are reset
- * so the next token is clean), else OI2_OK. */
+ * token, or a staged token's wait for its records, decoded since the
+ * previous call ran past its bound (the tokens decoded since then are to be
+ * taken as invalid; the signal words are reset so the next token is clean),
+ * else OI2_OK. */
 int oi2_stack_status(oi2_stack* s, void* stream);
 /* No counterpart in the reference: the bound, in polls, of every device-wide
- * wait of the persistent kernel (default 1 << 20; 1 .. 1 << 24).  A wait past
- * it gives up, so the token is invalid and oi2_stack_status reports it; the
- * kernel still runs to its end and the next token is unaffected.  For tests
- * of that failure path.  Drops captured graphs. */
+ * wait of the persistent kernel and of the staged path (default 1 << 20;
+ * 1 .. 1 << 24).  A wait past it gives up, so the token is invalid and
+ * oi2_stack_status reports it; the kernels still run to their end.  For
+ * tests of that failure path.  Drops captured graphs. */
 int oi2_stack_set_wait_bound(oi2_stack* s, int32_t polls);
 /* Mean microseconds of the persistent token kernel alone: decodes x_in once,
  * then `reps` more launches timed between hipEvents on `stream`; leaves the

@@ -168,9 +168,11 @@ def test_graph_replay_is_deterministic(stack4):
 
 
 def test_staged_store_matches_resident(stack4):
-    """Records in pinned host memory, copied one layer ahead on a side stream
-    (graph-captured fork/join), give the same bits as the HBM-resident stack:
-    the FFN consumes the same records in the same order."""
+    """Records in pinned host memory, copied one layer ahead by a copy kernel
+    on a side stream that the FFN waits for on the device, give the same bits
+    as the HBM-resident stack: the FFN consumes the same records in the same
+    order.  Layer 2 has no predictor, so its list is signalled by the main
+    stream."""
     dev, g, layers, st, thr = stack4
     stream = torch.cuda.Stream(device=dev)
     x_in = torch.randn(H, generator=g, device=dev).half()
@@ -191,12 +193,13 @@ def test_staged_store_matches_resident(stack4):
                          staging=16)
     staged.set_expected_active(300)
     out = torch.empty_like(x_in)
-    for k in range(3):                       # capture, then replays
+    for k in range(3):                       # tokens back to back, eager work between
         with torch.cuda.stream(stream):
             staged.decode(x_in, out, stream)
             _ = (out.float() * 3).sum()
         stream.synchronize()
-        assert torch.equal(out, ref), f"replay {k}"
+        staged.status(stream)
+        assert torch.equal(out, ref), f"token {k}"
     _, c, _, i = staged.trace()
     torch.cuda.synchronize()
     assert torch.equal(c, c_ref)
@@ -208,12 +211,52 @@ def test_staged_store_matches_resident(stack4):
     out2 = torch.empty_like(x_in)
     direct.decode(x_in, out2, None)
     torch.cuda.synchronize()
+    direct.status()
     assert torch.equal(out2, ref)
     us = staged.profile_staging(x_in, out, stream, reps=1)
     torch.cuda.synchronize()
     assert us > 0 and torch.equal(out, ref)
     direct.close()
     staged.close()
+
+
+def test_staged_wait_past_bound_is_reported(stack4):
+    """The staged path's device-side waits (the copy kernel for a layer's
+    list, the FFN for its records) are bounded: forced to give up at once
+    (a bound of one poll), the token still completes, status() raises once,
+    and the next token with the default bound equals the resident result."""
+    dev, g, layers, st, thr = stack4
+    stream = torch.cuda.Stream(device=dev)
+    x_in = torch.randn(H, generator=g, device=dev).half()
+    ref = torch.empty_like(x_in)
+    st.set_token_kernel(False)
+    try:
+        with torch.cuda.stream(stream):
+            st.decode(x_in, ref, stream)
+        stream.synchronize()
+    finally:
+        st.set_token_kernel(True)
+    pinned = [l.records.cpu().pin_memory() for l in layers]
+    staged = DecodeStack([StackLayer(l.hot, p, l.lut, l.norm_w, l.predictor)
+                          for l, p in zip(layers, pinned)], st.inter, EPS, "silu", False, thr,
+                         staging=16)
+    try:
+        staged.set_expected_active(300)
+        out = torch.empty_like(x_in)
+        staged.set_wait_bound(1)
+        with torch.cuda.stream(stream):
+            staged.decode(x_in, out, stream)
+        staged.set_wait_bound(1 << 20)
+        with pytest.raises(oi2.OI2Error, match="past its bound"):
+            staged.status(stream)
+        staged.status(stream)
+        for _ in range(2):
+            with torch.cuda.stream(stream):
+                staged.decode(x_in, out, stream)
+            staged.status(stream)
+            assert torch.equal(out, ref)
+    finally:
+        staged.close()
 
 
 def test_pageable_records_rejected(stack4):
