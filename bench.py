@@ -285,6 +285,77 @@ def measure_cold_dequant(layers, dev, reps=4):
     return {"fused_cold_ffn": fused, "read_neurons_dequant": read}
 
 
+def measure_batch8_file(dev, steps, warmup, seed=4):
+    """Survey config 4: 32 layers, batch 8, Zipf(1.1) neuron popularity (hot =
+    the top 20 % by rank, 2867 fp8 neurons), the cold records read from the
+    page-aligned split file on every step (engine.py:266-290's fetch,
+    splitter.py:354-403) into pinned buffers and moved to HBM with
+    hipMemcpyAsync, each layer's set selected from the batch-mean query.
+    Timed twice: through the mapping with the file in the page cache (warm),
+    and with O_DIRECT page reads (the storage device itself).  Beside it, the
+    same 32 layers' batch kernels with the records in HBM (the kernels' own
+    HBM rate)."""
+    import tempfile
+    import torch
+    import oi2
+    from oi2.batch_stack import BatchDecodeStack, BatchLayer
+    from oi2.filestore import FileStore
+    from oi2.synth import zipf_layers
+    g = torch.Generator(device=dev).manual_seed(seed)
+    t0 = time.time()
+    layers = zipf_layers(g, N_LAYERS, INTER, device=dev)
+    tmp = tempfile.TemporaryDirectory(dir=ROOT)
+    cold_bin = os.path.join(tmp.name, "cold_weights.bin")
+    cold_idx = os.path.join(tmp.name, "cold_index.npy")
+    w = oi2.format.ColdFileWriter(cold_bin, N_LAYERS)
+    for li, l in enumerate(layers):
+        w.add_section(li, l.records.cpu().numpy())
+    w.close(cold_idx)
+    file_gb = os.path.getsize(cold_bin) / 1e9
+    log(f"batch 8: {N_LAYERS} Zipf layers and a {file_gb:.2f} GB split file in {time.time() - t0:.1f}s")
+    x0 = torch.randn((8, H), generator=g, device=dev).half()
+    out = {"tokens_per_step": 8, "layers": N_LAYERS, "n_hot": layers[0].hot.n_hot,
+           "file_gb": file_gb, "popularity": "Zipf(1.1) over the intermediate dimension"}
+    for mode, direct in (("page_cache", False), ("direct_io", True)):
+        try:
+            store = FileStore(cold_bin, cold_idx, direct=direct, threads=8)
+        except oi2.OI2Error as e:
+            out[mode] = {"error": str(e)}
+            continue
+        st = BatchDecodeStack([BatchLayer(l.hot, l.lut, l.norm_w, l.predictor, i)
+                               for i, l in enumerate(layers)], store, INTER, EPS, "silu", False, 0.0)
+        x = x0
+        for _ in range(warmup):
+            x = st.decode(x)
+        torch.cuda.synchronize()
+        b0 = st.bytes_read
+        t1 = time.perf_counter()
+        for _ in range(steps):
+            x = st.decode(x)
+        torch.cuda.synchronize()
+        secs = time.perf_counter() - t1
+        rec_bytes = st.bytes_read - b0
+        assert torch.isfinite(x.float()).all()
+        out[mode] = {"tok_s": 8 * steps / secs, "ms_per_step": secs * 1e3 / steps, "steps": steps,
+                     "record_bytes_per_step": rec_bytes / steps,
+                     "mean_active_cold": rec_bytes / steps / 6400 / N_LAYERS,
+                     "file_read_and_h2d_gbs": rec_bytes / secs / 1e9}
+        log(f"batch 8 ({mode}): {out[mode]['tok_s']:.1f} tok/s, {out[mode]['ms_per_step']:.2f} ms/step, "
+            f"{out[mode]['mean_active_cold']:.0f} active cold per layer, "
+            f"{out[mode]['file_read_and_h2d_gbs']:.2f} GB/s of records from the file")
+        st.close()
+        store.close()
+    frac = out["page_cache"]["mean_active_cold"] / (INTER - layers[0].hot.n_hot) \
+        if "tok_s" in out.get("page_cache", {}) else 0.15
+    k = measure_multi_token(layers, dev, 8, frac, reps=5)
+    out["kernels_records_in_hbm"] = k
+    log(f"batch 8 kernels alone (records in HBM): {k['us_per_32_layers']:.0f} us per step, "
+        f"{k['weight_gbs']:.0f} GB/s ({k['weight_gbs'] / HBM_PEAK_GBS:.3f} of HBM peak)")
+    del layers
+    tmp.cleanup()
+    return out
+
+
 def measure_multi_token(layers, dev, M, frac, reps, seed=1):
     """M tokens through the 32 layers on the matrix-core path (batch decode at
     small M, a prefill chunk at M = 512): each layer's cold half is a fixed
@@ -323,9 +394,10 @@ def measure_multi_token(layers, dev, M, frac, reps, seed=1):
     e1.record()
     torch.cuda.synchronize()
     us = e0.elapsed_time(e1) * 1e3 / reps
-    n_act = int(frac * (INTER - N_HOT))
-    flop = N_LAYERS * 2 * M * H * (N_HOT + n_act) * 3
-    weight_bytes = N_LAYERS * (3 * N_HOT * H + n_act * 6400)
+    n_hot = layers[0].hot.n_hot
+    n_act = int(frac * (INTER - n_hot))
+    flop = N_LAYERS * 2 * M * H * (n_hot + n_act) * 3
+    weight_bytes = N_LAYERS * (3 * n_hot * H + n_act * 6400)
     assert torch.isfinite(y.float()).all()
     del graph
     return {"tokens": M, "active_cold_frac": frac, "us_per_32_layers": us,
@@ -412,6 +484,9 @@ def main():
                     help="skip the device split writer measurement")
     ap.add_argument("--no-cold-dequant", dest="cold_dequant", action="store_false",
                     help="skip the cold INT4 dequant GB/s measurement")
+    ap.add_argument("--no-batch8", dest="batch8", action="store_false",
+                    help="skip the batch-8 Zipf decode with the records read from the file")
+    ap.add_argument("--batch8-steps", type=int, default=8)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 256 MiB device copy 8 times (the reference kernel "
@@ -556,6 +631,10 @@ def main():
             log(f"{M} tokens x 32 layers: {r['us_per_32_layers']:.0f} us, "
                 f"{r['tflops']:.1f} TFLOP/s, {r['weight_gbs']:.0f} GB/s")
 
+    batch8 = None
+    if args.batch8 and not args.hbm_only:
+        batch8 = measure_batch8_file(dev, args.batch8_steps, 2)
+
     writer = None
     if args.split_writer and not args.hbm_only:
         writer = measure_split_writer(dev)
@@ -611,6 +690,7 @@ def main():
         "staging": staged,
         "hbm_resident": hbm_resident,
         "cold_dequant": cold,
+        "batch8_file": batch8,
         "multi_token": multi,
         "split_writer": writer,
     }

@@ -15,6 +15,7 @@ import torch
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "liboi2.so")
 
 OI2_OK = 0
+OI2_EUNSUPPORTED = 4
 ACT_SILU, ACT_RELU = 0, 1
 DTYPE_F32, DTYPE_BF16, DTYPE_F16 = 0, 1, 2
 ABI_VERSION = 2
@@ -97,6 +98,10 @@ _SIGS = {
     "oi2_stack_profile_token": (c_int32, [c_void_p, c_void_p, c_void_p, c_int32, POINTER(c_float),
                                           c_void_p]),
     "oi2_stack_destroy": (c_int32, [c_void_p]),
+    "oi2_file_store_open": (c_int32, [ctypes.c_char_p, c_void_p, c_int32, c_int32, c_int32,
+                                      POINTER(c_void_p)]),
+    "oi2_file_store_read": (c_int32, [c_void_p, c_int32, c_void_p, c_int32, c_void_p]),
+    "oi2_file_store_close": (c_int32, [c_void_p]),
     "oi2_section_bytes": (c_size_t, [c_int32]),
     "oi2_quantize_section": (c_int32, [c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p,
                                        c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t,

@@ -143,3 +143,50 @@ def build_decode_stack(seed: int, dev, n_layers: int = 32, inter: int = 14336, n
     # size the cold pass for the calibrated active fraction with headroom
     st.set_expected_active(int(1.3 * active_frac * (inter - n_hot)))
     return layers, st, thr, g
+
+
+def zipf_layers(gen, n_layers: int, inter: int = 14336, hot_frac: float = 0.2, s: float = 1.1,
+                cold_active: float = 0.15, batch: int = 8, eps: float = 1e-5, device="cuda",
+                n_cal: int = 64, std: float = 0.02):
+    """Layers whose neuron firing popularity is Zipf(s) over the intermediate
+    dimension: each layer draws a random rank for every neuron; the top
+    ``hot_frac`` by rank are hot (fp8), the rest cold (INT4 records); the
+    random-init bf16 predictor's bias is set so that a neuron of rank r is
+    predicted active with probability a_r = min(0.95, K (r + 1)^-s) for the
+    batch-mean query of ``batch`` N(0, 1) tokens (engine.py:277), K chosen so
+    that ``cold_active`` of the cold neurons fire on average.  The bias is
+    b = -mu + sigma * Phi^-1(a) from the per-neuron mean mu and spread sigma
+    of the bias-free logits over ``n_cal`` seeded calibration batches, for the
+    threshold p = 0.5 (logit 0).  Returns the layers."""
+    dev = torch.device(device)
+    n_hot = int(round(hot_frac * inter))
+    layers = []
+    for _ in range(n_layers):
+        rank = torch.randperm(inter, generator=gen, device=dev)          # rank of each neuron
+        hot_ids = (rank < n_hot).nonzero().flatten().sort().values
+        lay = SyntheticLayer(gen, inter, n_hot, std=std, device=dev, hot_ids=hot_ids,
+                             with_predictor=True, pred_dtype=torch.bfloat16)
+        p = lay.predictor
+        # target activation probability by rank; K by bisection on the cold mean
+        r = rank.double() + 1.0
+        cold = rank >= n_hot
+        lo, hi = 0.0, 1e6
+        for _ in range(80):
+            K = 0.5 * (lo + hi)
+            a = torch.clamp(K * r.pow(-s), max=0.95)
+            if a[cold].mean().item() < cold_active:
+                lo = K
+            else:
+                hi = K
+        a = torch.clamp(0.5 * (lo + hi) * r.pow(-s), min=1e-6, max=0.95)
+        # bias-free logits of calibration batch-mean queries
+        x = torch.randn((n_cal, batch, H), generator=gen, device=dev)
+        xn = x * torch.rsqrt((x * x).mean(-1, keepdim=True) + eps) * lay.norm_w.float()
+        q = xn.half().float().mean(1).half().to(torch.bfloat16).float()
+        z = (q @ p.down_w.float().t()) @ p.up_w.float().t()
+        mu, sigma = z.mean(0).double(), z.std(0).double().clamp(min=1e-6)
+        b = -mu + sigma * torch.special.ndtri(a)
+        p.up_b = b.to(p.dtype).contiguous()
+        lay.zipf_rank = rank
+        layers.append(lay)
+    return layers

@@ -38,7 +38,8 @@ enum {
   OI2_EINVAL = 1,       /* bad argument (shape, pointer, size) */
   OI2_EHIP = 2,         /* a HIP runtime call failed */
   OI2_ENOMEM = 3,       /* workspace too small / allocation failed at creation */
-  OI2_EUNSUPPORTED = 4  /* valid request outside what this build implements */
+  OI2_EUNSUPPORTED = 4, /* valid request outside what this build implements */
+  OI2_EIO = 5           /* reading the cold-record file failed */
 };
 
 enum { OI2_ACT_SILU = 0, OI2_ACT_RELU = 1 };          /* engine.py:165 */
@@ -306,6 +307,33 @@ int oi2_stack_set_wait_bound(oi2_stack* s, int32_t polls);
 int oi2_stack_profile_token(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, int32_t reps,
                             float* token_us, void* stream);
 int oi2_stack_destroy(oi2_stack* s);
+
+/* ---- cold records read from the split file ------------------------------ */
+typedef struct oi2_file_store oi2_file_store;
+
+/* ColdWeightStore.__init__ (splitter.py:317-330) without a device copy: opens
+ * cold_weights.bin for reading.  index is cold_index.npy's data, n_sections
+ * pairs (section byte offset, n_cold) as uint64 (splitter.py:188, 256; the
+ * (layer, expert) grid flattened, section = layer * n_experts + expert).
+ * direct_io = 0 maps the file (splitter.py:322-323) and copies records out
+ * of the mapping; 1 opens it with O_DIRECT and reads whole 4 KB pages into
+ * aligned bounce buffers, bypassing the page cache (OI2_EUNSUPPORTED where
+ * the file system refuses O_DIRECT).  threads: reader threads (1 .. 64),
+ * each taking a contiguous run of a request's records in file order. */
+int oi2_file_store_open(const char* path, const uint64_t* index, int32_t n_sections, int32_t direct_io,
+                        int32_t threads, oi2_file_store** out);
+/* The byte side of ColdWeightStore.read_neurons (splitter.py:354-403):
+ * records slots[0..n) of `section` (record k at section offset + 16 + 6400 k)
+ * copied whole, in request order (duplicates kept), into host memory
+ * dst (n x 6400 bytes; pinned memory lets one hipMemcpyAsync move the
+ * batch to the device).  Slot lookup from neuron ids is the caller's (an
+ * absent id has no slot and is skipped before the call, as read_neurons
+ * skips it).  Synchronous: returns once every record is in place; OI2_EIO
+ * if a read fails.  One call at a time per handle. */
+int oi2_file_store_read(oi2_file_store* fs, int32_t section, const int32_t* slots, int32_t n,
+                        uint8_t* dst);
+/* ColdWeightStore.close (splitter.py:405-407). */
+int oi2_file_store_close(oi2_file_store* fs);
 
 /* ---- split writer ------------------------------------------------------- */
 /* Bytes of one cold_weights.bin section with n_cold records: the 16-byte

@@ -1,0 +1,91 @@
+"""Survey config 4's decode path: a batch of 8 tokens through a stack of
+Zipf(1.1)-popularity layers (hot = the top 20 % by rank), each layer's cold
+set selected on the device from the batch-mean query (engine.py:274-283) and
+its records read from the split file on every step (the native file store,
+mmap and O_DIRECT), staged through pinned memory into HBM, against the
+float64 oracle layer by layer on the GPU's own inputs (teacher forcing)."""
+import os
+import tempfile
+
+import numpy as np
+import pytest
+import torch
+
+import oi2
+from oi2.batch_stack import BatchDecodeStack, BatchLayer
+from oi2.filestore import FileStore
+from oi2.layer import rmsnorm
+from oi2.synth import zipf_layers
+from oracle import oracle as O
+from tests.gpu_helpers import (EPS, assert_ffn_close, cold_dense, hot_dense, normed_f16,
+                               pred_weights, query_for)
+
+pytestmark = pytest.mark.gpu
+H = 4096
+B = 8
+
+
+@pytest.fixture(scope="module")
+def zipf4():
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(404)
+    layers = zipf_layers(g, 4, device=dev)
+    tmp = tempfile.TemporaryDirectory(dir=os.path.dirname(os.path.abspath(__file__)))
+    w = oi2.format.ColdFileWriter(os.path.join(tmp.name, "cold_weights.bin"), 4)
+    for li, l in enumerate(layers):
+        w.add_section(li, l.records.cpu().numpy())
+    w.close(os.path.join(tmp.name, "cold_index.npy"))
+    yield dev, g, layers, tmp.name
+    tmp.cleanup()
+
+
+@pytest.mark.parametrize("direct", [False, True], ids=["mmap", "direct"])
+def test_zipf_batch8_file_backed_matches_oracle(zipf4, direct):
+    dev, g, layers, d = zipf4
+    try:
+        store = FileStore(os.path.join(d, "cold_weights.bin"), os.path.join(d, "cold_index.npy"),
+                          direct=direct, threads=4)
+    except oi2.OI2Error as e:
+        if direct and "O_DIRECT" in str(e):
+            pytest.skip(f"this file system refuses O_DIRECT: {e}")
+        raise
+    st = BatchDecodeStack([BatchLayer(l.hot, l.lut, l.norm_w, l.predictor, i)
+                           for i, l in enumerate(layers)], store, 14336, EPS, "silu", False, 0.0)
+    try:
+        st.trace = []
+        x0 = torch.randn((B, H), generator=g, device=dev).half()
+        out = st.decode(x0)
+        torch.cuda.synchronize()
+        tr = [(x.clone(), ids) for x, ids in st.trace]
+        # a second step from the first step's output: the buffers of both
+        # parities are reused
+        out2 = st.decode(out)
+        torch.cuda.synchronize()
+        assert torch.isfinite(out2.float()).all()
+        assert st.bytes_read > 0
+        xs = [t[0] for t in tr] + [out]
+        fracs = []
+        for L, lay in enumerate(layers):
+            x_l = xs[L]
+            ids = tr[L][1].tolist()
+            assert ids == sorted(ids)
+            # layer L's set comes from the batch mean of RMSNorm_L(x_{L-1}) (x_0 for L = 0)
+            src = xs[L - 1] if L > 0 else x0
+            q = query_for(rmsnorm(src, lay.norm_w, EPS).double().cpu().numpy(), torch.bfloat16)
+            D, U, b = pred_weights(lay.predictor)
+            logits = O.predictor_logits(q, D, U, b)
+            want = O.cold_ids_for(logits >= 0.0, lay.hot_ids.cpu().tolist(), lay.inter)
+            amb = O.ambiguous(logits, 0.5)
+            assert all(amb[i] for i in set(ids) ^ set(want)), f"layer {L}: index sets differ"
+            fracs.append(len(ids) / (lay.inter - lay.hot.n_hot))
+            slots = [int(lay.lut[i]) for i in ids]
+            xn = normed_f16(x_l, lay.norm_w)
+            ref = O.sparse_ffn(xn, "silu", False, *hot_dense(lay.hot), *cold_dense(lay.records, slots))
+            y = xs[L + 1].double().cpu().numpy() - x_l.double().cpu().numpy()
+            for r in range(B):
+                assert_ffn_close(y[r], ref[r], tol=1e-2, cos_min=0.9999, what=f"layer {L} row {r}")
+        # the Zipf bias puts ~15 % of the cold neurons in the batch's set
+        assert 0.05 < float(np.mean(fracs)) < 0.3, fracs
+    finally:
+        st.close()
+        store.close()

@@ -160,3 +160,55 @@ def test_logit_threshold_equivalence():
     assert t1 == float(O.sigmoid_f32_threshold(1.0))
     z = torch.tensor([np.nextafter(np.float32(t1), np.float32(0)), t1], dtype=torch.float32)
     assert (torch.sigmoid(z) >= 1.0).tolist() == [False, True]
+
+
+# ── native file store (host code: runs without a GPU) ───────────────────────
+
+def _file_store_or_skip(cold_bin, cold_idx, direct, threads):
+    from oi2.filestore import FileStore
+    try:
+        return FileStore(cold_bin, cold_idx, direct=direct, threads=threads)
+    except oi2.OI2Error as e:
+        if direct and "O_DIRECT" in str(e):
+            pytest.skip(f"this file system refuses O_DIRECT: {e}")
+        raise
+
+
+@pytest.mark.parametrize("direct,threads", [(False, 1), (False, 4), (True, 1), (True, 3)],
+                         ids=["mmap-1", "mmap-4", "direct-1", "direct-3"])
+def test_file_store_reads_records_in_request_order(direct, threads):
+    """oi2_file_store_read returns exactly the file's record bytes
+    (splitter.py:354-403's per-record slices), in request order with
+    duplicates kept, whether read through the mapping or with O_DIRECT page
+    reads (records straddling pages, neighbours merged into one read, the
+    last record of the file); bad slots and sections are refused."""
+    with tempfile.TemporaryDirectory(dir=os.path.dirname(os.path.abspath(__file__))) as tmp:
+        cold_bin, cold_idx, config, layers = synthetic_cold_file(tmp, 4, 40, 3)
+        raw = np.frombuffer(open(cold_bin, "rb").read(), np.uint8)
+        index = np.load(cold_idx)
+        fs = _file_store_or_skip(cold_bin, cold_idx, direct, threads)
+        try:
+            assert fs.sections == 4 and list(fs.n_records) == [40] * 4
+            rng = np.random.default_rng(0)
+            for li in range(4):
+                base = int(index[li, 0, 0]) + 16
+                reqs = [np.arange(40), np.arange(40)[::-1], rng.integers(0, 40, 97),
+                        np.array([39]), np.array([5, 5, 6, 0, 39, 20])]
+                for req in reqs:
+                    out = np.full((len(req), 6400), 0xAB, np.uint8)
+                    assert fs.read(li, req, out) == len(req)
+                    want = np.stack([raw[base + 6400 * s: base + 6400 * (s + 1)] for s in req])
+                    assert np.array_equal(out, want)
+                assert fs.nids(li).tolist() == layers[li][0]
+            pinned_like = torch.empty(3 * 6400, dtype=torch.uint8)
+            fs.read(2, [1, 2, 3], pinned_like)
+            assert np.array_equal(pinned_like.numpy(), raw[int(index[2, 0, 0]) + 16 + 6400:
+                                                           int(index[2, 0, 0]) + 16 + 4 * 6400])
+            with pytest.raises(oi2.OI2Error, match="outside section"):
+                fs.read(0, [40], np.empty((1, 6400), np.uint8))
+            with pytest.raises(oi2.OI2Error, match="section 9 out of range"):
+                fs.read(9, [0], np.empty((1, 6400), np.uint8))
+            with pytest.raises(ValueError, match="records need"):
+                fs.read(0, [0, 1], np.empty((1, 6400), np.uint8))
+        finally:
+            fs.close()
