@@ -36,6 +36,8 @@
 #include <thread>
 #include <vector>
 
+#include <hip/hip_runtime.h>
+
 #include "oi2.h"
 
 namespace oi2 {
@@ -296,6 +298,23 @@ int oi2_file_store_read(oi2_file_store* fs, int32_t section, const int32_t* slot
       oi2::set_error("file store: read of section %d failed: %s", section, strerror(err[p]));
       return OI2_EIO;
     }
+  return OI2_OK;
+}
+
+int oi2_file_store_stage(oi2_file_store* fs, int32_t section, const int32_t* slots, int32_t n,
+                         uint8_t* host_buf, uint8_t* dst, void* stream) {
+  int rc = oi2_file_store_read(fs, section, slots, n, host_buf);
+  if (rc != OI2_OK || n == 0) return rc;
+  if (!dst) {
+    oi2::set_error("file store: null device destination");
+    return OI2_EINVAL;
+  }
+  const hipError_t e = hipMemcpyAsync(dst, host_buf, (size_t)n * kRec, hipMemcpyHostToDevice,
+                                      (hipStream_t)stream);
+  if (e != hipSuccess) {
+    oi2::set_error("file store: hipMemcpyAsync of %d records failed: %s", n, hipGetErrorString(e));
+    return OI2_EHIP;
+  }
   return OI2_OK;
 }
 

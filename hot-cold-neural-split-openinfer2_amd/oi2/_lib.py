@@ -101,6 +101,8 @@ _SIGS = {
     "oi2_file_store_open": (c_int32, [ctypes.c_char_p, c_void_p, c_int32, c_int32, c_int32,
                                       POINTER(c_void_p)]),
     "oi2_file_store_read": (c_int32, [c_void_p, c_int32, c_void_p, c_int32, c_void_p]),
+    "oi2_file_store_stage": (c_int32, [c_void_p, c_int32, c_void_p, c_int32, c_void_p, c_void_p,
+                                       c_void_p]),
     "oi2_file_store_close": (c_int32, [c_void_p]),
     "oi2_section_bytes": (c_size_t, [c_int32]),
     "oi2_quantize_section": (c_int32, [c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p,

@@ -67,6 +67,20 @@ class FileStore:
         _lib.check(_lib.load_library().oi2_file_store_read(self._h, int(section), s.ctypes.data, n, ptr))
         return n
 
+    def stage(self, section: int, slots, host_buf: torch.Tensor, dst: torch.Tensor, stream) -> int:
+        """Read the records into ``host_buf`` (pinned) and enqueue their copy
+        to ``dst`` (device, contiguous) on ``stream``; returns the count.
+        ``host_buf`` must stay untouched until the copy has run."""
+        s = np.ascontiguousarray(np.asarray(slots, dtype=np.int32).reshape(-1))
+        n = int(s.shape[0])
+        need = n * fmt.NEURON_RECORD_BYTES
+        if host_buf.numel() < need or dst.numel() < need or not dst.is_cuda or host_buf.is_cuda:
+            raise ValueError(f"{n} records need {need} bytes of pinned host and device buffer")
+        _lib.check(_lib.load_library().oi2_file_store_stage(
+            self._h, int(section), s.ctypes.data, n, host_buf.data_ptr(), dst.data_ptr(),
+            stream.cuda_stream or None))
+        return n
+
     def close(self):
         if self._h:
             _lib.load_library().oi2_file_store_close(self._h)

@@ -19,6 +19,8 @@ from __future__ import annotations
 
 import ctypes
 from concurrent.futures import Future
+
+import numpy as np
 from pathlib import Path
 from typing import Optional
 
@@ -268,6 +270,16 @@ class SparseFFNLayer(torch.nn.Module):
         self._section = cold_store.section(layer_idx, self._EID) if cold_store is not None else None
         self._n_chunks = (self.inter_dim + _lib.SEL_CHUNK - 1) // _lib.SEL_CHUNK
         self._lut = self._section.lut if self._section is not None else None
+        # file residency: each fetch reads the records from the file on the
+        # executor (engine.py:266-272), copies them to the device on a copy
+        # stream, and hands the FFN a section over the copy
+        self._file = (cold_store is not None and getattr(cold_store, "residency", "hbm") == "file"
+                      and self._section is not None)
+        if self._file:
+            self._copy_stream = torch.cuda.Stream(device=self.device)
+            self._arange = torch.arange(max(self._section.n_records, 1), dtype=torch.int32,
+                                        device=self.device)
+            self._inflight = []          # (copy event, pinned buffer) until the copy has run
 
     # ── cold selection ──
     def _cold_ids_for(self, x_normed: torch.Tensor) -> list[int]:
@@ -315,21 +327,68 @@ class SparseFFNLayer(torch.nn.Module):
             None, ws.data_ptr(), ws_bytes, _lib.stream_handle(dev)))
         return ColdNeurons(sec, slots, counts, nc, _lib.SEL_CHUNK, ids=ids)
 
+    def _cold_slots_host(self, x: torch.Tensor, normed: bool) -> np.ndarray:
+        """The record slots of _cold_ids_for's list, ascending neuron id, on
+        the host (the list the reference hands its executor, engine.py:289)."""
+        sel = self._select(x, normed)
+        if sel.empty():
+            return np.zeros(0, np.int32)
+        counts = sel.counts.cpu().tolist()
+        slots = sel.slots.cpu().numpy()
+        parts = [slots[c * sel.chunk: c * sel.chunk + min(max(n, 0), sel.chunk)]
+                 for c, n in enumerate(counts)]
+        return np.concatenate(parts).astype(np.int32) if parts else np.zeros(0, np.int32)
+
+    def _fetch_file(self, slots: np.ndarray) -> ColdNeurons:
+        """engine.py:266-272 (_fetch_cold) with file residency: read the
+        records from the file into pinned memory and copy them to the device
+        on the copy stream; the result carries the copy's event."""
+        n = int(slots.shape[0])
+        if n == 0:
+            return ColdNeurons(None, None, None, 0, 0)
+        cs = self._copy_stream
+        with torch.cuda.stream(cs):
+            counts = torch.full((1,), n, dtype=torch.int32, device=self.device)
+            staged = self.cold_store.fetch_records(self._section, slots, cs)
+        cold = ColdNeurons(staged, self._arange[:n], counts, 1, n)
+        cold.event = staged.event
+        return cold
+
     def submit_cold_fetch(self, x: torch.Tensor):
         """engine.py:285-290: predict this layer's cold set from x (normalised
         with this layer's norm) and return an object with ``.result()``.  With
-        the device-resident store the work is only enqueued on the stream, so
-        the returned future is already complete."""
+        a device-resident store the work is only enqueued on the stream, so
+        the returned future is already complete; with file residency the
+        fetch runs on the executor (inline without one)."""
         with torch.no_grad():
-            return _Ready(self._select(x, normed=False))
+            if not self._file:
+                return _Ready(self._select(x, normed=False))
+            slots = self._cold_slots_host(x, normed=False)
+            if self.executor is not None:
+                return self.executor.submit(self._fetch_file, slots)
+            return _Ready(self._fetch_file(slots))
 
     def forward(self, x: torch.Tensor, prefetch_future=None) -> torch.Tensor:
         """engine.py:292-312: residual + FFN(RMSNorm(x)) for x (B, T, H)."""
         B, T, H = x.shape
-        cold = prefetch_future.result() if prefetch_future is not None else \
-            self._select(x, normed=False)
+        if prefetch_future is not None:
+            cold = prefetch_future.result()
+        elif self._file:
+            cold = self._fetch_file(self._cold_slots_host(x, normed=False))
+        else:
+            cold = self._select(x, normed=False)
         if isinstance(cold, Future):
             cold = cold.result()
+        stream = torch.cuda.current_stream(self.device)
+        ev = getattr(cold, "event", None)
+        if ev is not None:
+            stream.wait_event(ev)
         out = _ffn(x.reshape(B * T, H), self.norm_weight, self.eps, self.hot, cold,
                    self.activation, self.act_on_both, add_residual=True)
+        if ev is not None:
+            # the staged records are read on this stream; their pinned buffer
+            # is released once the copy has run
+            cold.section.records.record_stream(stream)
+            self._inflight = [(e, h) for e, h in self._inflight if not e.query()]
+            self._inflight.append((ev, cold.section.host_buffer))
         return out.reshape(B, T, H).to(x.dtype)

@@ -1,11 +1,12 @@
 """Cold INT4 neuron store: the split's ``cold_weights.bin`` / ``cold_index.npy``
 behind ColdWeightStore's interface (splitter.py:307-407), decoded on the GPU.
 
-The file is memory-mapped as the reference does (splitter.py:322-323).  A
-layer's section is uploaded to HBM once, on first access, as raw 6400-byte
-records (the device keeps the INT4 bytes, 16x smaller than the reference's
-fp32 tensors); 288 GB of HBM holds a 7B model's ~2.5 GB cold file many times
-over.  ``read_neurons`` keeps the reference's contract - request order,
+The file is memory-mapped as the reference does (splitter.py:322-323).  By
+default a layer's section is uploaded to HBM once, on first access, as raw
+6400-byte records (the device keeps the INT4 bytes, 16x smaller than the
+reference's fp32 tensors); 288 GB of HBM holds a 7B model's ~2.5 GB cold file
+many times over.  ``residency="file"`` keeps the reference's model instead:
+records are read from the file on every fetch.  ``read_neurons`` keeps the reference's contract - request order,
 duplicates kept, absent ids skipped, None when nothing is found or the section
 is empty, fp32 (N,H)/(N,H)/(H,N) - but returns device tensors produced by the
 dequant kernel.
@@ -62,14 +63,26 @@ class ColdSection:
 
 
 class ColdWeightStore:
-    """splitter.py:307-407 with a section cache: each section's records are
-    copied once out of the mapped file, into device memory, or with
-    ``pinned=True`` into pinned host memory (read by the GPU over PCIe; a
-    decode stack with staging copies the active ones into HBM one layer
-    ahead).  The nid -> slot LUT always lives on the device."""
+    """splitter.py:307-407.  Where the records live is a choice
+    (``residency``):
+
+      * ``"hbm"`` (default): each section's records are copied once out of the
+        mapped file into device memory; the FFN kernels gather the active
+        ones there (288 GB of HBM holds a 7B model's cold file many times);
+      * ``"pinned"`` (or ``pinned=True``): copied once into pinned host memory,
+        read by the GPU over PCIe (a decode stack with staging copies the
+        active ones into HBM one layer ahead);
+      * ``"file"``: the reference's memory model - nothing is copied ahead;
+        every fetch reads the requested records from the file (mapped, or
+        with ``direct_io=True`` by O_DIRECT page reads) into pinned memory
+        and on to the device (liboi2's native file store,
+        ``reader_threads`` threads).
+
+    The nid -> slot LUT always lives on the device."""
 
     def __init__(self, cold_bin: str, cold_index: str, config: dict, device="cuda",
-                 pinned: bool = False):
+                 pinned: bool = False, residency: str | None = None, direct_io: bool = False,
+                 reader_threads: int = 8):
         self.config = config
         self.index = np.load(cold_index)
         self._f = open(cold_bin, "rb")
@@ -81,7 +94,14 @@ class ColdWeightStore:
             raise ValueError(f"hidden_dim {self.H}: the cold-record layout is sized for "
                              f"{fmt.HIDDEN_DIM}")
         self.device = torch.device(device)
-        self.pinned = bool(pinned)
+        self.residency = residency or ("pinned" if pinned else "hbm")
+        if self.residency not in ("hbm", "pinned", "file"):
+            raise ValueError(f"residency {self.residency!r}: 'hbm', 'pinned' or 'file'")
+        self.pinned = self.residency == "pinned"
+        self.file = None
+        if self.residency == "file":
+            from .filestore import FileStore
+            self.file = FileStore(cold_bin, cold_index, direct=direct_io, threads=reader_threads)
         self._offset_cache: dict[tuple[int, int], dict[int, int]] = {}
         self._sections: dict[tuple[int, int], ColdSection | None] = {}
         self._lock = threading.Lock()
@@ -127,7 +147,9 @@ class ColdWeightStore:
             inter = max(int(self.I or 0), int(nids.max()) + 1)
             host = np.frombuffer(self._mm, dtype=np.uint8, count=n * fmt.NEURON_RECORD_BYTES,
                                  offset=base).reshape(n, fmt.NEURON_RECORD_BYTES)
-            if self.pinned:
+            if self.residency == "file":
+                records = None           # read per fetch (fetch_records)
+            elif self.pinned:
                 records = torch.empty((n, fmt.NEURON_RECORD_BYTES), dtype=torch.uint8,
                                       pin_memory=True)
                 records.numpy()[:] = host
@@ -139,8 +161,29 @@ class ColdWeightStore:
             lut[uniq] = (n - 1 - first_rev).astype(np.int32)
             sec = ColdSection(layer_idx, nids, records, torch.from_numpy(lut).to(self.device),
                               lut, inter)
+            sec.file_section = self.file.section_id(layer_idx, expert_idx) if self.file else None
             self._sections[key] = sec
             return sec
+
+    def fetch_records(self, sec: ColdSection, slots, stream) -> "ColdSection":
+        """File residency: the records ``slots`` of ``sec`` read from the file
+        and copied, in order, into a new device buffer on ``stream``; returns
+        a section over them (slot k = the k-th requested record) that carries
+        the copy's completion event and keeps its pinned buffer alive until
+        the copy has run."""
+        s = np.asarray(slots, dtype=np.int32).reshape(-1)
+        n = int(s.shape[0])
+        host = torch.empty(max(n, 1) * fmt.NEURON_RECORD_BYTES, dtype=torch.uint8, pin_memory=True)
+        dst = torch.empty((max(n, 1), fmt.NEURON_RECORD_BYTES), dtype=torch.uint8, device=self.device)
+        self.file.stage(sec.file_section, s, host, dst, stream)
+        ev = torch.cuda.Event()
+        ev.record(stream)
+        staged = ColdSection(sec.layer, sec.nids[s] if n else sec.nids[:0], dst, sec.lut, sec.lut_host,
+                             sec.inter)
+        staged.n_records = n
+        staged.event = ev
+        staged.host_buffer = host
+        return staged
 
     def read_neurons(self, layer_idx: int, expert_idx: int, neuron_ids):
         """(gate (N,H), up (N,H), down (H,N)) fp32 on the store's device, or
@@ -154,6 +197,10 @@ class ColdWeightStore:
             return None
         dev = self.device
         L = _lib.lib()
+        if self.residency == "file":
+            stream = torch.cuda.current_stream(dev)
+            sec = self.fetch_records(sec, slots, stream)
+            slots = np.arange(n, dtype=np.int32)
         gate = torch.empty((n, self.H), dtype=torch.float32, device=dev)
         up = torch.empty((n, self.H), dtype=torch.float32, device=dev)
         down = torch.empty((self.H, n), dtype=torch.float32, device=dev)
@@ -161,9 +208,13 @@ class ColdWeightStore:
         _lib.check(L.oi2_dequant_records(sec.records.data_ptr(), sec.n_records, s.data_ptr(), n,
                                          gate.data_ptr(), up.data_ptr(), down.data_ptr(),
                                          _lib.stream_handle(dev)))
+        if self.residency == "file":
+            sec.event.synchronize()      # the pinned buffer may be released now
         return gate, up, down
 
     def close(self):
+        if self.file is not None:
+            self.file.close()
         if self._mm is not None:
             self._mm.close()
         self._f.close()

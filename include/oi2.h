@@ -332,6 +332,14 @@ int oi2_file_store_open(const char* path, const uint64_t* index, int32_t n_secti
  * if a read fails.  One call at a time per handle. */
 int oi2_file_store_read(oi2_file_store* fs, int32_t section, const int32_t* slots, int32_t n,
                         uint8_t* dst);
+/* The cold fetch of SparseFFNLayer._fetch_cold (engine.py:266-272:
+ * read_neurons, then .to(device)) for a caller's worker thread: reads the
+ * records as oi2_file_store_read into host_buf (pinned, n x 6400 bytes), then
+ * enqueues one hipMemcpyAsync of them to dst (device, n x 6400 bytes) on
+ * `stream` and returns; host_buf must stay untouched until that copy has
+ * run (an event recorded on `stream` after the call marks it). */
+int oi2_file_store_stage(oi2_file_store* fs, int32_t section, const int32_t* slots, int32_t n,
+                         uint8_t* host_buf, uint8_t* dst, void* stream);
 /* ColdWeightStore.close (splitter.py:405-407). */
 int oi2_file_store_close(oi2_file_store* fs);
 

@@ -519,3 +519,80 @@ def test_sparse_ffn_layer_from_split_files(dev):
                          what="no predictor")
         # layers with an empty cold section compute the hot half only
         store.close()
+
+
+@pytest.mark.parametrize("direct_io", [False, True], ids=["mmap", "direct"])
+def test_sparse_ffn_layer_file_residency(dev, direct_io):
+    """The reference's memory model: ColdWeightStore(residency="file") keeps
+    the records in the split file, and SparseFFNLayer fetches each layer's
+    predicted records on the caller's executor (engine.py:266-290: read,
+    then copy to the device), from the mapping or with O_DIRECT page reads.
+    read_neurons equals the HBM-resident store's bit for bit; the layer's
+    output equals the HBM-resident layer's to rounding and the oracle's within
+    the FFN bar; a prefetched future and a direct forward agree exactly."""
+    from concurrent.futures import ThreadPoolExecutor
+    g = torch.Generator(device=dev).manual_seed(43)
+    inter = 14336
+    lay = SyntheticLayer(g, inter, 3584, device=dev, with_predictor=True, pred_dtype=torch.float32)
+    with tempfile.TemporaryDirectory(dir=os.path.dirname(os.path.abspath(__file__))) as tmp:
+        hot_dir = os.path.join(tmp, "hot")
+        os.makedirs(hot_dir)
+        lay.hot.save(os.path.join(hot_dir, "layer_000_expert_000.pt"))
+        w = oi2.format.ColdFileWriter(os.path.join(tmp, "cold_weights.bin"), 1)
+        w.add_section(0, lay.records.cpu().numpy())
+        w.close(os.path.join(tmp, "cold_index.npy"))
+        pdir = os.path.join(tmp, "pred")
+        os.makedirs(pdir)
+        lay.predictor.save(os.path.join(pdir, "layer_000_expert_000.pt"))
+        cfg = {"hidden_dim": H, "intermediate_dim": inter, "hidden_act": "silu",
+               "act_on_both": False, "rms_norm_eps": EPS, "num_experts": 1}
+        paths = (os.path.join(tmp, "cold_weights.bin"), os.path.join(tmp, "cold_index.npy"))
+        try:
+            fstore = oi2.ColdWeightStore(*paths, cfg, device=dev, residency="file", direct_io=direct_io)
+        except oi2.OI2Error as e:
+            if direct_io and "O_DIRECT" in str(e):
+                pytest.skip(f"this file system refuses O_DIRECT: {e}")
+            raise
+        hstore = oi2.ColdWeightStore(*paths, cfg, device=dev)
+        reg = oi2.PredictorRegistry(pdir, device=dev)
+        ex = ThreadPoolExecutor(max_workers=2)
+        try:
+            ids = [int(i) for i in lay.cold_ids[torch.randperm(lay.cold_ids.numel(), generator=g,
+                                                               device=dev)[:300]].tolist()]
+            ids += [ids[5], 10 ** 6]                      # a duplicate and an absent id
+            a = fstore.read_neurons(0, 0, ids)
+            b = hstore.read_neurons(0, 0, ids)
+            torch.cuda.synchronize()
+            assert all(torch.equal(u, v) for u, v in zip(a, b))
+            lf = oi2.SparseFFNLayer(0, hot_dir, fstore, reg, cfg, dev, ex, ffn_norm_weight=lay.norm_w.cpu())
+            lh = oi2.SparseFFNLayer(0, hot_dir, hstore, reg, cfg, dev, ex, ffn_norm_weight=lay.norm_w.cpu())
+            # one token: the single-token kernels sum in a fixed order, so a
+            # prefetched and a direct forward agree bit for bit
+            x1 = torch.randn((1, 1, H), generator=g, device=dev).half()
+            fut = lf.submit_cold_fetch(x1)
+            y1_pref = lf(x1, fut)
+            y1_dir = lf(x1)
+            torch.cuda.synchronize()
+            assert torch.equal(y1_pref, y1_dir)
+            # two tokens (the batch kernels, whose split sums round in any order)
+            x = torch.randn((2, 1, H), generator=g, device=dev).half()
+            fut = lf.submit_cold_fetch(x)
+            y_pref = lf(x, fut)
+            y_dir = lf(x)
+            y_hbm = lh(x)
+            torch.cuda.synchronize()
+            assert_ffn_close(y_pref.double().cpu().numpy().ravel(), y_dir.double().cpu().numpy().ravel(),
+                             tol=1e-3, cos_min=0.999999, what="prefetched vs direct")
+            assert_ffn_close(y_dir.double().cpu().numpy().ravel(), y_hbm.double().cpu().numpy().ravel(),
+                             tol=2e-3, cos_min=0.99999, what="file vs HBM residency")
+            # against the oracle: the layer's own selection, teacher-forced
+            slots = lf._cold_slots_host(x, normed=False)
+            xn = normed_f16(x[:, 0], lay.norm_w)
+            ref = O.sparse_ffn(xn, "silu", False, *hot_dense(lay.hot), *cold_dense(lay.records, slots))
+            res = y_dir[:, 0].double().cpu().numpy() - x[:, 0].double().cpu().numpy()
+            for r in range(2):
+                assert_ffn_close(res[r], ref[r], tol=1e-2, cos_min=0.9999, what=f"file residency row {r}")
+        finally:
+            ex.shutdown()
+            fstore.close()
+            hstore.close()
