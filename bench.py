@@ -406,6 +406,82 @@ def measure_multi_token(layers, dev, M, frac, reps, seed=1):
             "weight_gbs": weight_bytes / (us * 1e-6) / 1e9}
 
 
+def measure_attention(dev, contexts=(512, 4096), reps=20, seed=6):
+    """Decode attention (engine.py:63-125) at batch 1 through 32 layers of Mistral-7B geometry (32 query / 8 kv
+    heads of 128, fp8 projections): each layer's cache holds `ctx` positions
+    and the token attends to ctx + 1.  The 32 calls are captured in one graph
+    and replayed, so the time is GPU time.  Algorithmic bytes per layer: the
+    fp8 q/k/v/o weights (41.9 MB) plus the K and V rows read (4096 B per
+    position) plus the new rows and the token."""
+    import torch
+    import oi2
+    n_kv = 8
+    g = torch.Generator(device=dev).manual_seed(seed)
+    cfg = {"num_attention_heads": 32, "num_key_value_heads": n_kv, "hidden_dim": H,
+           "rms_norm_eps": EPS}
+    layers = []
+    for li in range(N_LAYERS):
+        p = f"layer_{li:03d}."
+
+        def w(r, c):
+            return (torch.randn((r, c), generator=g, device=dev) * 0.02).to(torch.float8_e4m3fn)
+        wd = {p + "q_proj": w(H, H), p + "k_proj": w(n_kv * 128, H), p + "v_proj": w(n_kv * 128, H),
+              p + "o_proj": w(H, H), p + "input_layernorm": torch.ones(H, dtype=torch.float16, device=dev)}
+        layers.append(oi2.GroupedQueryAttention(li, wd, cfg))
+    out = {"layers": N_LAYERS, "batch": 1, "n_q": 32, "n_kv": n_kv, "head_dim": 128,
+           "weight_bytes_per_layer": (H + 2 * n_kv * 128) * H + H * H}
+    stream = torch.cuda.Stream(device=dev)
+    for ctx in contexts:
+        cos, sin = oi2.rope_tables(ctx + 1, 128, 1e6, device=dev)
+        caches = []
+        for a in layers:
+            k = torch.randn((1, n_kv, ctx, 128), generator=g, device=dev).half()
+            caches.append((k, torch.randn_like(k)))
+        x0 = torch.randn((1, 1, H), generator=g, device=dev).half()
+        res = [torch.empty_like(x0) for _ in range(2)]
+        c1, s1 = cos[ctx:ctx + 1], sin[ctx:ctx + 1]
+        # the first call copies each cache into its layer's buffer; later
+        # calls pass back the views (in-place append at position ctx)
+        kvs = []
+        with torch.cuda.stream(stream):
+            for a, kv in zip(layers, caches):
+                _, kv2 = a(x0, c1, s1, kv)
+                kvs.append((kv2[0][:, :, :ctx], kv2[1][:, :, :ctx]))
+        stream.synchronize()
+
+        def chain():
+            x = x0
+            for i, (a, kv) in enumerate(zip(layers, kvs)):
+                a(x, c1, s1, kv, residual_out=res[i & 1])
+                x = res[i & 1]
+            return x
+        with torch.cuda.stream(stream):
+            chain()
+        stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            y = chain()
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        assert torch.isfinite(y.float()).all()
+        per_layer = out["weight_bytes_per_layer"] + (ctx + 1) * 2 * n_kv * 128 * 2 + 3 * H * 2
+        gbs = N_LAYERS * per_layer / (us * 1e-6) / 1e9
+        out[f"ctx{ctx}"] = {"us_per_32_layers": us, "us_per_layer": us / N_LAYERS,
+                            "bytes_per_layer": per_layer, "gbs": gbs, "frac_of_hbm_peak": gbs / HBM_PEAK_GBS,
+                            "tok_s_attention_only": 1e6 / us}
+        log(f"attention ctx {ctx}: {us / N_LAYERS:.2f} us/layer, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.3f} of HBM)")
+        del graph, caches, kvs
+    del layers
+    return out
+
+
 def measure_gemm_reference(dev, n=8192, reps=10):
     """The attainable fp16 matrix rate on this GPU: a vendor-library
     (hipBLASLt through torch.matmul) n x n x n fp16 GEMM, fp32 accumulate."""
@@ -487,6 +563,9 @@ def main():
     ap.add_argument("--no-batch8", dest="batch8", action="store_false",
                     help="skip the batch-8 Zipf decode with the records read from the file")
     ap.add_argument("--batch8-steps", type=int, default=8)
+    ap.add_argument("--no-attention", dest="attention", action="store_false",
+                    help="skip the decode-attention leg")
+    ap.add_argument("--attention-only", action="store_true")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 256 MiB device copy 8 times (the reference kernel "
@@ -512,6 +591,9 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         log(f"copied {src.numel() * 4} bytes 8 times")
+        return
+    if args.attention_only:
+        print(json.dumps({"attention": measure_attention(dev)}), flush=True)
         return
     t0 = time.time()
     layers, st, thr, g = build_stack(args.seed, dev)
@@ -635,6 +717,10 @@ def main():
     if args.batch8 and not args.hbm_only:
         batch8 = measure_batch8_file(dev, args.batch8_steps, 2)
 
+    attention = None
+    if args.attention and not args.hbm_only:
+        attention = measure_attention(dev)
+
     writer = None
     if args.split_writer and not args.hbm_only:
         writer = measure_split_writer(dev)
@@ -693,6 +779,7 @@ def main():
         "batch8_file": batch8,
         "multi_token": multi,
         "split_writer": writer,
+        "attention": attention,
     }
     if cpu is not None and cold is not None:
         out["cold_dequant"]["gpu_vs_cpu_cold_neurons"] = (

@@ -1,8 +1,10 @@
 """MI355X (gfx950) hot/cold sparse-FFN decode path behind OpenInfer2's
 interfaces: ColdWeightStore (splitter.py), SparseFFNLayer / sparse_ffn
-(engine.py) and PredictorRegistry / NeuronPredictor (predictor.py)."""
+(engine.py), PredictorRegistry / NeuronPredictor (predictor.py) and the
+decode attention GroupedQueryAttention (engine.py)."""
 from . import format
 from ._lib import OI2Error, load_library
+from .attention import GroupedQueryAttention, rope_tables
 from .format import (ALIGN_BYTES, HIDDEN_DIM, NEURON_RECORD_BYTES, PAGE_ALIGN, quantize_int4)
 from .hot import HotWeights
 from .layer import ColdNeurons, SparseFFNLayer, sparse_ffn
@@ -14,5 +16,5 @@ __all__ = [
     "format", "OI2Error", "load_library", "ALIGN_BYTES", "HIDDEN_DIM", "NEURON_RECORD_BYTES",
     "PAGE_ALIGN", "quantize_int4", "HotWeights", "ColdNeurons", "SparseFFNLayer", "sparse_ffn",
     "NeuronPredictor", "PredictorRegistry", "DecodeStack", "StackLayer", "ColdSection",
-    "ColdWeightStore",
+    "ColdWeightStore", "GroupedQueryAttention", "rope_tables",
 ]

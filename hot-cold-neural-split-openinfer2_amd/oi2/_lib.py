@@ -47,6 +47,11 @@ class Predictor(Structure):
                 ("up_w", c_void_p), ("up_b", c_void_p)]
 
 
+class Attn(Structure):
+    _fields_ = [("n_q", c_int32), ("n_kv", c_int32), ("wq", c_void_p), ("wk", c_void_p),
+                ("wv", c_void_p), ("wo", c_void_p), ("norm_w", c_void_p)]
+
+
 class Layer(Structure):
     _fields_ = [("hot", Hot), ("cold", Cold), ("lut", c_void_p), ("norm_w", c_void_p),
                 ("pred", Predictor)]
@@ -104,6 +109,10 @@ _SIGS = {
     "oi2_file_store_stage": (c_int32, [c_void_p, c_int32, c_void_p, c_int32, c_void_p, c_void_p,
                                        c_void_p]),
     "oi2_file_store_close": (c_int32, [c_void_p]),
+    "oi2_attn_workspace_bytes": (c_size_t, [c_int32, c_int32, c_int32, c_int32, c_int32]),
+    "oi2_attn_forward": (c_int32, [c_void_p, c_int32, c_int32, POINTER(Attn), c_float, c_void_p,
+                                   c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_void_p,
+                                   c_void_p, c_void_p, c_size_t, c_void_p]),
     "oi2_section_bytes": (c_size_t, [c_int32]),
     "oi2_quantize_section": (c_int32, [c_int32, c_int32, c_int32, c_void_p, c_void_p, c_void_p,
                                        c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_size_t,

@@ -343,6 +343,41 @@ int oi2_file_store_stage(oi2_file_store* fs, int32_t section, const int32_t* slo
 /* ColdWeightStore.close (splitter.py:405-407). */
 int oi2_file_store_close(oi2_file_store* fs);
 
+/* ---- grouped-query attention (decode) ----------------------------------- */
+/* One layer's attention weights as GroupedQueryAttention holds them
+ * (engine.py:66-88): q_proj, k_proj, v_proj, o_proj kept at fp8 e4m3fn,
+ * the reference's storage (splitter.py:175-177), unscaled; row-major
+ * (out_features, in_features).  head_dim = H / n_q must be 128. */
+typedef struct oi2_attn {
+  int32_t n_q;                /* query heads: H / 128 */
+  int32_t n_kv;               /* kv heads; n_q / n_kv in {1, 2, 4, 8} */
+  const uint8_t* wq;          /* (n_q * 128, H) */
+  const uint8_t* wk;          /* (n_kv * 128, H) */
+  const uint8_t* wv;          /* (n_kv * 128, H) */
+  const uint8_t* wo;          /* (H, n_q * 128) */
+  const uint16_t* norm_w;     /* (H) fp16 input_layernorm (ones for nn.RMSNorm's default) */
+} oi2_attn;
+
+/* Workspace of oi2_attn_forward for batch x seq query rows and a cache of
+ * cache_cap positions; 0 for invalid sizes. */
+size_t oi2_attn_workspace_bytes(int32_t batch, int32_t seq, int32_t n_q, int32_t n_kv, int32_t cache_cap);
+/* GroupedQueryAttention.forward (engine.py:90-125) for x (batch, seq, H)
+ * fp16: x_n = RMSNorm(x); q, k, v = x_n W^T; RoPE on q and k with cos / sin
+ * (seq, 64) fp32, the call's positions as the engine slices them
+ * (engine.py:414-416; rounded to fp16 as engine.py:153-154 does); k and v
+ * written into k_cache / v_cache (batch, n_kv, cache_cap, 128) fp16 at
+ * positions past .. past + seq - 1 (the reference's torch.cat,
+ * engine.py:105-109, done in place: positions below past are the cache);
+ * attention of each query over positions [0, past + seq), causal when
+ * `causal` (the reference: causal exactly when it has no cache,
+ * engine.py:121); out (batch * seq, H) fp16 = o_proj(attn), the tensor the
+ * reference returns.  x_out, if not NULL, receives fp16(x + out), the
+ * engine's residual add (engine.py:425).  Three kernels on `stream`. */
+int oi2_attn_forward(const uint16_t* x, int32_t batch, int32_t seq, const oi2_attn* w, float eps,
+                     const float* cos, const float* sin, uint16_t* k_cache, uint16_t* v_cache,
+                     int32_t cache_cap, int32_t past, int32_t causal, uint16_t* out, uint16_t* x_out,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- split writer ------------------------------------------------------- */
 /* Bytes of one cold_weights.bin section with n_cold records: the 16-byte
  * <HHIq header, n_cold x 6400, zero padding to a 4096 multiple

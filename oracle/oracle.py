@@ -21,6 +21,16 @@ Pins (see tests/test_oracle.py):
   predictor         predict_mask == sigmoid(logits) >= thr
                     (tests/test_predictor.py:78-85); logit-space threshold
                     equivalence; ascending order as nonzero()
+  rope_cache        closed form: cos^2 + sin^2 = 1, position 0 is (1, 0),
+                    angle t * theta^(-i/half) against torch's float32 table
+  apply_rope        position 0 is the identity, pair norms are kept, the dot
+                    of q at m and k at n depends on m - n only, rotating by p1
+                    then p2 equals rotating by p1 + p2
+  attention_core    torch's scaled_dot_product_attention (float64, with
+                    enable_gqa) on random and causal cases; one key returns
+                    its value; equal keys return the mean of the values
+  gqa_attention     the composition above with torch.nn.RMSNorm and
+                    F.linear in float64
 """
 from __future__ import annotations
 
@@ -343,3 +353,87 @@ def ambiguous(logits, threshold: float = 0.5, band: float = 1e-6):
     """Neurons whose logit is within ``band`` of the threshold: the parity
     contract exempts these from index-set equality."""
     return np.abs(np.asarray(logits, np.float64) - logit_threshold(threshold)) <= band
+
+
+# ── attention (engine.py:63-157) ────────────────────────────────────────────
+
+def rope_cache(max_seq_len: int, head_dim: int, theta: float):
+    """engine.py:128-137 in float64: angle[t, i] = t * theta^(-i / half) for
+    i < half = head_dim // 2; returns (cos, sin), each (max_seq_len, half)."""
+    half = head_dim // 2
+    inv = 1.0 / (float(theta) ** (np.arange(half, dtype=np.float64) / half))
+    ang = np.outer(np.arange(max_seq_len, dtype=np.float64), inv)
+    return np.cos(ang), np.sin(ang)
+
+
+def apply_rope(x, cos, sin):
+    """engine.py:140-157: x (..., T, D) split into halves x1 = x[..., :D/2],
+    x2 = x[..., D/2:]; returns cat(x1 cos - x2 sin, x1 sin + x2 cos) with the
+    tables (T, D/2) broadcast over the leading axes.  The reference casts the
+    tables to the activations' dtype first (engine.py:153-154); callers that
+    model that pass fp16-rounded tables."""
+    x = np.asarray(x, np.float64)
+    half = x.shape[-1] // 2
+    c = np.asarray(cos, np.float64)
+    s = np.asarray(sin, np.float64)
+    x1, x2 = x[..., :half], x[..., half:]
+    return np.concatenate([x1 * c - x2 * s, x1 * s + x2 * c], axis=-1)
+
+
+def attention_core(q, k, v, causal: bool):
+    """F.scaled_dot_product_attention as engine.py:118-121 calls it, after
+    repeat_interleave of the kv heads (engine.py:114-116): q (B, n_q, T, D),
+    k/v (B, n_kv, S, D); query head h reads kv head h // (n_q // n_kv);
+    scores scaled by 1/sqrt(D); with ``causal`` query t sees keys
+    s <= t (torch's top-left alignment, which the engine only uses with
+    T == S); float64."""
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    B, n_q, T, D = q.shape
+    n_kv, S = k.shape[1], k.shape[2]
+    grp = n_q // n_kv
+    kk = np.repeat(k, grp, axis=1)
+    vv = np.repeat(v, grp, axis=1)
+    sc = q @ np.swapaxes(kk, -1, -2) / math.sqrt(D)
+    if causal:
+        mask = np.arange(S)[None, :] > np.arange(T)[:, None]
+        sc = np.where(mask, -np.inf, sc)
+    sc = sc - sc.max(axis=-1, keepdims=True)
+    p = np.exp(sc)
+    p = p / p.sum(axis=-1, keepdims=True)
+    return p @ vv
+
+
+def f16(v):
+    """Round to fp16 and back to float64 (the reference's fp16 activations)."""
+    return np.asarray(v, np.float64).astype(np.float16).astype(np.float64)
+
+
+def gqa_attention(x, norm_w, eps, wq, wk, wv, wo, n_q, n_kv, cos, sin, kv_cache=None):
+    """GroupedQueryAttention.forward (engine.py:90-125) in float64 with the
+    reference's fp16 rounding points: x_n = fp16(RMSNorm(x)) (engine.py:93,
+    nn.RMSNorm on fp16); q, k, v = fp16(x_n W^T) (:94-96); RoPE with the
+    tables rounded to fp16 and its result rounded to fp16 (:102-103,
+    :153-157); k, v appended to the cache (:105-109); attention of every query
+    over the cache, causal only without a cache (:118-121), rounded to fp16;
+    out = fp16(attn W_o^T) (:122-123).
+    x (B, T, H); weights dense (out, in); cos/sin (T, D/2) for the call's
+    positions; kv_cache None or (k (B, n_kv, S, D), v).  Returns
+    (out (B, T, H), (k, v) with S + T positions)."""
+    x = np.asarray(x, np.float64)
+    B, T, H = x.shape
+    D = H // n_q
+    xn = f16(rmsnorm(x, norm_w, eps))
+    q = f16(xn @ np.asarray(wq, np.float64).T).reshape(B, T, n_q, D).transpose(0, 2, 1, 3)
+    k = f16(xn @ np.asarray(wk, np.float64).T).reshape(B, T, n_kv, D).transpose(0, 2, 1, 3)
+    v = f16(xn @ np.asarray(wv, np.float64).T).reshape(B, T, n_kv, D).transpose(0, 2, 1, 3)
+    c16, s16 = f16(cos)[:T], f16(sin)[:T]
+    q = f16(apply_rope(q, c16, s16))
+    k = f16(apply_rope(k, c16, s16))
+    if kv_cache is not None:
+        k = np.concatenate([np.asarray(kv_cache[0], np.float64), k], axis=2)
+        v = np.concatenate([np.asarray(kv_cache[1], np.float64), v], axis=2)
+    o = f16(attention_core(q, k, v, causal=kv_cache is None))
+    o = o.transpose(0, 2, 1, 3).reshape(B, T, n_q * D)
+    return f16(o @ np.asarray(wo, np.float64).T), (k, v)
