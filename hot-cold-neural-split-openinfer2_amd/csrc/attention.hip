@@ -32,9 +32,8 @@ constexpr int kHd = 128;                 // head_dim (engine.py:72: hidden / n_q
 constexpr int kHalf = kHd / 2;
 constexpr int kThreads = 256;
 constexpr int kMaxRows = 8;              // token rows per GEMV launch
-constexpr int kPosPerWave = 32;          // 8 steps of 4 positions
-constexpr int kPosPerWg = 4 * kPosPerWave;
-constexpr int kSteps = kPosPerWave / 4;
+constexpr int kMinPosPerWg = 32;         // 4 waves x 2 steps of 4 positions
+constexpr int kMaxTabBytes = 64 << 10;   // the merge's m / l table in LDS
 
 struct GemvArgs {
   const uint16_t* x;          // this launch's first input row (rows, H)
@@ -89,6 +88,19 @@ __device__ __forceinline__ void unpack16(const u32x4 (&x)[2], float v[16]) {
 
 __device__ __forceinline__ uint32_t pack_f16x2(float a, float b) {
   return (uint32_t)float_to_half_bits(a) | ((uint32_t)float_to_half_bits(b) << 16);
+}
+
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int kSc1 = 16;                 // cache-policy operand: agent-coherent access
+
+// A buffer descriptor over [p, p + bytes); p and bytes must be uniform over
+// the wave (lane 0's are taken).  Offsets past the range read zero.
+__device__ __forceinline__ rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint64_t u = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(v >> 32)) << 32) |
+                     (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)v);
+  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(u), (short)0,
+                                           __builtin_amdgcn_readfirstlane(bytes), 0x00020000);
 }
 
 template <typename T>
@@ -271,47 +283,54 @@ __global__ __launch_bounds__(kThreads) void k_attn_gemv(GemvArgs a) {
 // Attention of query row r (batch b, position past + t) against kv head g's
 // cache positions [0, n_r), n_r = past + t + 1 when causal, else past + seq
 // (engine.py:118-121: causal only without a cache).  Workgroup (split, g, r)
-// takes positions [128 split, 128 split + 128), 32 per wave.  Lane
+// takes 4 STEPS positions per wave, 16 STEPS per workgroup.  Lane
 // (k = lane >> 4, jj = lane & 15) holds dims [8 jj, 8 jj + 8) of position
 // 4 step + k, so one 16-byte load per lane reads 4 whole K (or V) rows, and
 // the 16-lane row sums give each of the G query heads its score.  Each wave
 // keeps its own max, exp-sum and weighted V sum; the workgroup merges its 4
 // waves and stores one partial; the workgroup that completes the set of
-// partials of (r, g) merges them into the fp16 output.
-template <int G>
+// partials of (r, g) merges them into the fp16 output, its loads all
+// independent of each other (the m / l table first, then 16-byte pieces of
+// the partial sums, several in flight per thread).
+template <int G, int STEPS>
 __global__ __launch_bounds__(kThreads) void k_attn_sdpa(SdpaArgs a) {
-  __shared__ float s_o[4][G][kHd];
+  extern __shared__ float s_tab[];                 // merge: m then l, (n_split, G) each
+  // the waves' partial sums; later the merge's per-group sums (1024 floats)
+  constexpr int kRedFloats = 4 * G * kHd > 1024 ? 4 * G * kHd : 1024;
+  __shared__ __align__(16) float s_red[kRedFloats];
+  float (*s_o)[G][kHd] = reinterpret_cast<float (*)[G][kHd]>(s_red);
   __shared__ float s_m[4][G], s_l[4][G];
   __shared__ uint32_t s_last;
+  constexpr int kPW = 4 * STEPS;
   const int split = blockIdx.x, g = blockIdx.y, r = blockIdx.z;
   const int tid = threadIdx.x, lane = lane_id(), wave = tid >> 6, k = lane >> 4, jj = lane & 15;
   const int b = r / a.seq, t = r - b * a.seq;
   const int n_r = a.causal ? a.past + t + 1 : a.past + a.seq;
   const int width = a.n_kv * G * kHd;
-  const int base = split * kPosPerWg + wave * kPosPerWave;
+  const int base = split * 4 * kPW + wave * kPW;
 
   u32x4 qv[G];
 #pragma unroll
   for (int h = 0; h < G; ++h)
     qv[h] = *reinterpret_cast<const u32x4*>(a.q + (size_t)r * width + (g * G + h) * kHd + 8 * jj);
   const size_t head = ((size_t)b * a.n_kv + g) * a.cap;
-  u32x4 kr[kSteps], vr[kSteps];
+  u32x4 kr[STEPS], vr[STEPS];
 #pragma unroll
-  for (int it = 0; it < kSteps; ++it) {
+  for (int it = 0; it < STEPS; ++it) {
     const int p = base + 4 * it + k;
     const int pc = p < n_r ? p : n_r - 1;
     kr[it] = *reinterpret_cast<const u32x4*>(a.k_cache + (head + pc) * kHd + 8 * jj);
   }
 #pragma unroll
-  for (int it = 0; it < kSteps; ++it) {
+  for (int it = 0; it < STEPS; ++it) {
     const int p = base + 4 * it + k;
     const int pc = p < n_r ? p : n_r - 1;
     vr[it] = *reinterpret_cast<const u32x4*>(a.v_cache + (head + pc) * kHd + 8 * jj);
   }
 
-  float s[kSteps * G];
+  float s[STEPS * G];
 #pragma unroll
-  for (int it = 0; it < kSteps; ++it)
+  for (int it = 0; it < STEPS; ++it)
 #pragma unroll
     for (int h = 0; h < G; ++h) {
       float d = 0.0f;
@@ -321,20 +340,20 @@ __global__ __launch_bounds__(kThreads) void k_attn_sdpa(SdpaArgs a) {
     }
   // sums over the 16 lanes of each row: every lane of the row gets the total
 #pragma unroll
-  for (int e = 0; e < kSteps * G; ++e) s[e] += dpp_f<0xB1>(s[e]);
+  for (int e = 0; e < STEPS * G; ++e) s[e] += dpp_f<0xB1>(s[e]);
 #pragma unroll
-  for (int e = 0; e < kSteps * G; ++e) s[e] += dpp_f<0x4E>(s[e]);
+  for (int e = 0; e < STEPS * G; ++e) s[e] += dpp_f<0x4E>(s[e]);
 #pragma unroll
-  for (int e = 0; e < kSteps * G; ++e) s[e] += dpp_f<0x141>(s[e]);
+  for (int e = 0; e < STEPS * G; ++e) s[e] += dpp_f<0x141>(s[e]);
 #pragma unroll
-  for (int e = 0; e < kSteps * G; ++e) s[e] += dpp_f<0x140>(s[e]);
+  for (int e = 0; e < STEPS * G; ++e) s[e] += dpp_f<0x140>(s[e]);
 
   const float ninf = -__builtin_inff();
   float mx[G];
 #pragma unroll
   for (int h = 0; h < G; ++h) mx[h] = ninf;
 #pragma unroll
-  for (int it = 0; it < kSteps; ++it) {
+  for (int it = 0; it < STEPS; ++it) {
     const bool ok = base + 4 * it + k < n_r;
 #pragma unroll
     for (int h = 0; h < G; ++h) {
@@ -355,7 +374,7 @@ __global__ __launch_bounds__(kThreads) void k_attn_sdpa(SdpaArgs a) {
     for (int e = 0; e < 8; ++e) o[h][e] = 0.0f;
   }
 #pragma unroll
-  for (int it = 0; it < kSteps; ++it) {
+  for (int it = 0; it < STEPS; ++it) {
     float vf[8];
 #pragma unroll
     for (int d = 0; d < 4; ++d) {
@@ -427,20 +446,72 @@ __global__ __launch_bounds__(kThreads) void k_attn_sdpa(SdpaArgs a) {
   }
   __syncthreads();
   if (!s_last) return;
-  for (int idx = tid; idx < G * kHd; idx += kThreads) {
-    const int h = idx / kHd, d = idx - h * kHd;
-    float M = ninf;
-    for (int sp = 0; sp < a.n_split; ++sp)
-      M = fmaxf(M, ld_coh(part_rg + (size_t)sp * a.part_stride + G * kHd + h));
-    float O = 0.0f, L = 0.0f;
-    for (int sp = 0; sp < a.n_split; ++sp) {
-      const float* P = part_rg + (size_t)sp * a.part_stride;
-      const float m = ld_coh(P + G * kHd + h);
-      const float sc = m == ninf ? 0.0f : __expf(m - M);
-      O = fmaf(sc, ld_coh(P + h * kHd + d), O);
-      L = fmaf(sc, ld_coh(P + G * kHd + G + h), L);
+
+  // thread (grp, h, q): 4 dims [4 q, 4 q + 4) of head h over splits
+  // grp, grp + kGrp, ...: its 16-byte agent-coherent loads of the partial
+  // sums (up to 8 at once) go out first, then the m / l table of every
+  // split (one agent-coherent load per entry), so both are in flight
+  // together
+  const int n_split = a.n_split;
+  float* s_pm = s_tab;
+  float* s_pl = s_tab + n_split * G;
+  constexpr int kGrp = kThreads / (32 * G);
+  constexpr int kBatch = 8;
+  const int q = tid & 31, h = (tid >> 5) % G, grp = tid / (32 * G);
+  const rsrc_t rs = make_rsrc(part_rg, (uint32_t)((size_t)n_split * a.part_stride * 4));
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  u32x4 pv[kBatch];
+  auto load_batch = [&](int sp0) {
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int sp = sp0 + u * kGrp;
+      // a split past the end reads zero through the descriptor's range
+      const uint32_t off = sp < n_split ? (uint32_t)(((size_t)sp * a.part_stride + h * kHd + 4 * q) * 4)
+                                        : 0xFFFFFFF0u;
+      pv[u] = __builtin_amdgcn_raw_buffer_load_b128(rs, off, 0, kSc1);
     }
-    a.out[(size_t)r * width + (g * G + h) * kHd + d] = float_to_half_bits(O / L);
+  };
+  load_batch(grp);
+  for (int i = tid; i < n_split * G; i += kThreads) {
+    const int sp = i / G, hh = i - sp * G;
+    const float* P = part_rg + (size_t)sp * a.part_stride + G * kHd;
+    s_pm[i] = ld_coh(P + hh);
+    s_pl[i] = ld_coh(P + G + hh);
+  }
+  __syncthreads();
+  float M = ninf;
+  for (int sp = 0; sp < n_split; ++sp) M = fmaxf(M, s_pm[sp * G + h]);
+  for (int sp0 = grp;;) {
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int sp = sp0 + u * kGrp;
+      const float m = sp < n_split ? s_pm[sp * G + h] : ninf;
+      const float w = m == ninf ? 0.0f : __expf(m - M);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[e] = fmaf(w, as_f32(pv[u][e]), acc[e]);
+    }
+    sp0 += kBatch * kGrp;
+    if (sp0 >= n_split) break;
+    load_batch(sp0);
+  }
+  __syncthreads();
+  float* red = s_red;                               // kGrp x G x 128 = 1024 floats
+#pragma unroll
+  for (int e = 0; e < 4; ++e) red[(grp * G + h) * kHd + 4 * q + e] = acc[e];
+  __syncthreads();
+  if (grp != 0) return;
+  float L = 0.0f;
+  for (int sp = 0; sp < n_split; ++sp) {
+    const float m = s_pm[sp * G + h];
+    L = fmaf(m == ninf ? 0.0f : __expf(m - M), s_pl[sp * G + h], L);
+  }
+  const float inv = 1.0f / L;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float O = 0.0f;
+#pragma unroll
+    for (int gg = 0; gg < kGrp; ++gg) O += red[(gg * G + h) * kHd + 4 * q + e];
+    a.out[(size_t)r * width + (g * G + h) * kHd + 4 * q + e] = float_to_half_bits(O * inv);
   }
 }
 
@@ -466,14 +537,34 @@ void launch_gemv(const GemvArgs& a, int rows, int blocks, hipStream_t st) {
   }
 }
 
-void launch_sdpa(const SdpaArgs& a, int G, int rows, hipStream_t st) {
+template <int G>
+void launch_sdpa_g(const SdpaArgs& a, int steps, int rows, size_t lds, hipStream_t st) {
   const dim3 grid(a.n_split, a.n_kv, rows);
-  switch (G) {
-    case 1: hipLaunchKernelGGL(k_attn_sdpa<1>, grid, dim3(kThreads), 0, st, a); break;
-    case 2: hipLaunchKernelGGL(k_attn_sdpa<2>, grid, dim3(kThreads), 0, st, a); break;
-    case 4: hipLaunchKernelGGL(k_attn_sdpa<4>, grid, dim3(kThreads), 0, st, a); break;
-    default: hipLaunchKernelGGL(k_attn_sdpa<8>, grid, dim3(kThreads), 0, st, a); break;
+  switch (steps) {
+    case 2: hipLaunchKernelGGL((k_attn_sdpa<G, 2>), grid, dim3(kThreads), lds, st, a); break;
+    case 4: hipLaunchKernelGGL((k_attn_sdpa<G, 4>), grid, dim3(kThreads), lds, st, a); break;
+    default: hipLaunchKernelGGL((k_attn_sdpa<G, 8>), grid, dim3(kThreads), lds, st, a); break;
   }
+}
+
+void launch_sdpa(const SdpaArgs& a, int G, int steps, int rows, size_t lds, hipStream_t st) {
+  switch (G) {
+    case 1: launch_sdpa_g<1>(a, steps, rows, lds, st); break;
+    case 2: launch_sdpa_g<2>(a, steps, rows, lds, st); break;
+    case 4: launch_sdpa_g<4>(a, steps, rows, lds, st); break;
+    default: launch_sdpa_g<8>(a, steps, rows, lds, st); break;
+  }
+}
+
+// Positions per wave step count: the longest span (8 steps, 128 positions
+// per workgroup) that still gives at least 256 workgroups, else shorter
+// spans for more of them (2 steps, 32 positions per workgroup at least).
+int choose_steps(int rows, int n_kv, int n_max) {
+  for (int steps = 8; steps > 2; steps /= 2) {
+    const int64_t wgs = (int64_t)rows * n_kv * ((n_max + 16 * steps - 1) / (16 * steps));
+    if (wgs >= 256) return steps;
+  }
+  return 2;
 }
 
 struct WsLayout {
@@ -482,7 +573,7 @@ struct WsLayout {
 
 WsLayout ws_layout(int rows, int n_q, int n_kv, int cap) {
   const int G = n_q / n_kv;
-  const size_t n_split = (size_t)(cap + kPosPerWg - 1) / kPosPerWg;
+  const size_t n_split = (size_t)(cap + kMinPosPerWg - 1) / kMinPosPerWg;
   WsLayout w;
   w.q = 0;
   w.attn = w.q + align256((size_t)rows * n_q * kHd * 2);
@@ -579,13 +670,20 @@ int oi2_attn_forward(const uint16_t* x, int32_t batch, int32_t seq, const oi2_at
   s.past = past;
   s.seq = seq;
   s.causal = causal ? 1 : 0;
-  s.n_split = (past + seq + kPosPerWg - 1) / kPosPerWg;
+  const int steps = choose_steps(rows, n_kv, past + seq);
+  s.n_split = (past + seq + 16 * steps - 1) / (16 * steps);
   s.part_stride = part_stride_floats(G);
+  const size_t tab = (size_t)2 * s.n_split * G * sizeof(float);
+  if (tab > (size_t)kMaxTabBytes) {
+    set_error("%d positions need %d sequence splits; the merge table holds %d", past + seq, s.n_split,
+              kMaxTabBytes / (int)(2 * G * sizeof(float)));
+    return OI2_EUNSUPPORTED;
+  }
   s.scale = 1.0f / sqrtf((float)kHd);
   s.part = part;
   s.counters = counters;
   s.out = attn;
-  launch_sdpa(s, G, rows, st);
+  launch_sdpa(s, G, steps, rows, tab, st);
   OI2_CHECK_LAUNCH();
 
   GemvArgs o{};

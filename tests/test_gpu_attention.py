@@ -89,7 +89,7 @@ def _rand_cache(dev, B, n_kv, past, seed):
     return k, v
 
 
-@pytest.mark.parametrize("B,past,n_kv", [(1, 37, 8), (3, 300, 8), (1, 4095, 8), (2, 100, 32),
+@pytest.mark.parametrize("B,past,n_kv", [(1, 5, 8), (1, 37, 8), (3, 300, 8), (1, 4095, 8), (3, 1000, 8), (2, 100, 32),
                                          (2, 129, 4), (1, 255, 16)])
 def test_decode_step_against_oracle(dev, B, past, n_kv):
     """One token per sequence over a cache from elsewhere (copied into the
