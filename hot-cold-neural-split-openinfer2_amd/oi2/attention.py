@@ -134,7 +134,7 @@ class GroupedQueryAttention(torch.nn.Module):
         positions (at least T rows of head_dim / 2); kv_cache None or (k, v).
         Returns (out, (k, v)) as engine.py:90-125.  With ``residual_out``
         (B, T, H) fp16 the kernel also writes x + out there, the engine's
-        residual add (engine.py:425)."""
+        residual add (engine.py:427)."""
         if x.dtype != torch.float16 or x.dim() != 3 or x.shape[2] != self.hidden:
             raise TypeError(f"x must be (B, T, {self.hidden}) fp16, got {tuple(x.shape)} {x.dtype}")
         B, T, H = x.shape

@@ -372,7 +372,7 @@ size_t oi2_attn_workspace_bytes(int32_t batch, int32_t seq, int32_t n_q, int32_t
  * `causal` (the reference: causal exactly when it has no cache,
  * engine.py:121); out (batch * seq, H) fp16 = o_proj(attn), the tensor the
  * reference returns.  x_out, if not NULL, receives fp16(x + out), the
- * engine's residual add (engine.py:425).  Three kernels on `stream`. */
+ * engine's residual add (engine.py:427).  Three kernels on `stream`. */
 int oi2_attn_forward(const uint16_t* x, int32_t batch, int32_t seq, const oi2_attn* w, float eps,
                      const float* cos, const float* sin, uint16_t* k_cache, uint16_t* v_cache,
                      int32_t cache_cap, int32_t past, int32_t causal, uint16_t* out, uint16_t* x_out,
