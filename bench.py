@@ -566,6 +566,8 @@ def main():
     ap.add_argument("--no-attention", dest="attention", action="store_false",
                     help="skip the decode-attention leg")
     ap.add_argument("--attention-only", action="store_true")
+    ap.add_argument("--multi-token-only", action="store_true",
+                    help="only the multi-token (batch decode / prefill) leg")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 256 MiB device copy 8 times (the reference kernel "
@@ -602,6 +604,13 @@ def main():
     if args.cold_only:
         cold = measure_cold_dequant(layers, dev)
         print(json.dumps({"cold_dequant": cold}), flush=True)
+        return
+    if args.multi_token_only:
+        multi = {}
+        for M, frac in ((8, 0.15), (64, 0.50), (512, 0.40), (1024, 0.40)):
+            multi[f"m{M}"] = measure_multi_token(layers, dev, M, frac, reps=5)
+            log(f"{M} tokens x 32 layers: {multi[f'm{M}']['us_per_32_layers']:.0f} us")
+        print(json.dumps({"multi_token": multi}), flush=True)
         return
     stream = torch.cuda.Stream(device=dev)
     x0 = torch.randn(H, generator=g, device=dev).half()
