@@ -68,7 +68,18 @@ __device__ float block_rnorm(const uint16_t* x, float eps, float* s_parts) {
 }
 
 // x_n = fp16((x * r) * w): the normalised hidden state as nn.RMSNorm's fp16
-// output (engine.py:247-249); the predictor query and oi2_rmsnorm use it.
-__device__ __forceinline__ float xn_exact(float x, float r, float w) { return round_f16(x * r * w); }
+// output (engine.py:247-249); the predictor query, oi2_rmsnorm and the
+// kernels that normalise their own input use it.  The fp32 product passes
+// through an empty asm before the fp16 rounding: otherwise instruction
+// selection fuses the last product with the rounding (v_fma_mixlo_f16, one
+// rounding instead of fp32 then fp16) in some kernels and not in others,
+// whatever the contraction setting, and the kernels' x_n then differ in rare
+// elements by one fp16 ulp - enough to move a predictor logit across the
+// threshold.
+__device__ __forceinline__ float xn_exact(float x, float r, float w) {
+  float u = x * r * w;
+  asm("" : "+v"(u));
+  return round_f16(u);
+}
 
 }  // namespace oi2

@@ -30,6 +30,7 @@
 #include <algorithm>
 
 #include "capi_util.h"
+#include "decode_util.h"
 #include "ffn_kernels.h"
 
 namespace oi2 {
@@ -991,6 +992,211 @@ __global__ __launch_bounds__(kThreads) void k_bup_s(BUpArgs a) {
     }
 }
 
+// ── gate/up for at most 16 tokens, RMSNorm fused ─────────────────────────────
+
+// Workgroup = 16 weight rows (hot rows, or items of the dense active list);
+// wave w takes K [1024 w, 1024 w + 1024).  The workgroup first normalises
+// the M <= MMAX token rows itself (x_n = fp16((x r) w), the rounding of
+// nn.RMSNorm's fp16 output) into LDS, every weight load of the first half of
+// its K range already in flight, so no operand of the MFMA loop is read from
+// global memory after the prologue.
+// Hot rows: lane (t, q) = (l & 15, l >> 4) loads 16 bytes of row r0 + t at
+// K 1024 w + 64 c + 16 q, the B operand of two 16x16x32 steps (K + 8 s,
+// s < 2); the A operand of the same steps is token t's x_n at the same K.
+// Cold items: the lane's 16 bytes are 32 nibbles of item t at K
+// 1024 w + 128 b + 32 q (four steps, decoded in int4x8_h8's order, the A
+// operand permuted to match); the group scale multiplies each 128-K block's
+// partial sums.
+template <int MMAX>
+__global__ __launch_bounds__(kThreads) void k_sbup(BUpArgs a, const uint16_t* x, const uint16_t* norm_w,
+                                                   float eps) {
+  constexpr int kLdX = kH + 8;          // halves per staged row: 8208 bytes, rows on distinct banks
+  constexpr int kScr = MMAX * kThreads > 3 * 2 * kWave * 4 ? MMAX * kThreads : 3 * 2 * kWave * 4;
+  __shared__ __attribute__((aligned(16))) uint16_t s_x[MMAX * kLdX];
+  __shared__ __attribute__((aligned(16))) float s_scr[kScr];   // norm partials, then the wave sums
+  const int tid = threadIdx.x, w = tid >> 6, l = lane_id();
+  const int t = l & 15, q = l >> 4;
+  const int M = a.M;
+  const bool hot = (int)blockIdx.x < a.hot_wg;
+  const int kq = 1024 * w;
+
+  int col, slot = -1;
+  bool cv;
+  u32x4 WG[16], WU[16];                 // hot: chunks c; cold: blocks 0..7 in WG/WU[0..7]
+  u32x4 SC[2] = {u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}};
+  if (hot) {
+    const int r0 = blockIdx.x * 16;
+    col = r0 + t;
+    cv = col < a.n_hot;
+    const rsrc_t rg = buf_rsrc(a.gate_q, (uint32_t)a.n_hot * kH);
+    const rsrc_t ru = buf_rsrc(a.up_q, (uint32_t)a.n_hot * kH);
+    const uint32_t voff = (uint32_t)col * kH + 16 * q;   // rows past n_hot read zero
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      WG[c] = bload16(rg, voff, kq + 64 * c);
+      WU[c] = bload16(ru, voff, kq + 64 * c);
+    }
+  } else {
+    const int i0 = ((int)blockIdx.x - a.hot_wg) * 16;
+    col = i0 + t;
+    const int raw_total = *a.total;
+    const int raw_slot = a.dslots[min(col, a.cap - 1)];
+    asm volatile("" ::"v"(raw_slot), "s"(raw_total));   // both loads in flight before either is used
+    const int total = min(raw_total, a.cap);
+    if (i0 >= total) return;   // the whole workgroup
+    slot = col < total ? raw_slot : -1;
+    cv = slot >= 0 && slot < a.n_records;
+    const rsrc_t rr = buf_rsrc(a.records, (uint32_t)a.n_records * kRecBytes);
+    const uint32_t ro = cv ? (uint32_t)slot * kRecBytes : kNoOffset;
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      WG[b] = bload16(rr, ro + kOffGate + 16 * q, 512 * w + 64 * b);
+      WU[b] = bload16(rr, ro + kOffUp + 16 * q, 512 * w + 64 * b);
+    }
+    // the quarter's 8 group scales of each vector (16 bytes at 2 mod 16)
+    SC[0] = bload16(rr, ro + kOffScales, 16 * w);
+    SC[1] = bload16(rr, ro + kOffScales + 2 * kGroups, 16 * w);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // prologue: the token rows into LDS (thread tid holds elements
+  // [16 tid, 16 tid + 16) of each row), their sum-of-squares partials, then
+  // x_n in place
+  u32x4 wn[2] = {u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}};
+  if (norm_w) {
+    wn[0] = reinterpret_cast<const u32x4*>(norm_w)[2 * tid];
+    wn[1] = reinterpret_cast<const u32x4*>(norm_w)[2 * tid + 1];
+  }
+#pragma unroll
+  for (int m = 0; m < MMAX; ++m) {
+    if (m >= M) break;
+    const u32x4* px = reinterpret_cast<const u32x4*>(x + (size_t)m * kH) + 2 * tid;
+    const u32x4 v0 = px[0], v1 = px[1];
+    u32x4* sx = reinterpret_cast<u32x4*>(s_x + m * kLdX + 16 * tid);
+    sx[0] = v0;
+    sx[1] = v1;
+    if (norm_w) {
+      float v[16];
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        v[2 * d] = half_bits_to_float((uint16_t)(v0[d] & 0xFFFFu));
+        v[2 * d + 1] = half_bits_to_float((uint16_t)(v0[d] >> 16));
+        v[8 + 2 * d] = half_bits_to_float((uint16_t)(v1[d] & 0xFFFFu));
+        v[8 + 2 * d + 1] = half_bits_to_float((uint16_t)(v1[d] >> 16));
+      }
+      float ss = 0.0f;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) ss = fmaf(v[e], v[e], ss);
+      s_scr[m * kThreads + tid] = ss;
+    }
+  }
+  if (norm_w) {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+    float wf[16];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      wf[2 * d] = half_bits_to_float((uint16_t)(wn[0][d] & 0xFFFFu));
+      wf[2 * d + 1] = half_bits_to_float((uint16_t)(wn[0][d] >> 16));
+      wf[8 + 2 * d] = half_bits_to_float((uint16_t)(wn[1][d] & 0xFFFFu));
+      wf[8 + 2 * d + 1] = half_bits_to_float((uint16_t)(wn[1][d] >> 16));
+    }
+#pragma unroll
+    for (int m = 0; m < MMAX; ++m) {
+      if (m >= M) break;
+      // the canonical factor: lane l sums partials 4 l .. 4 l + 3, then a DPP tree
+      const f32x4 pp = reinterpret_cast<const f32x4*>(s_scr + m * kThreads)[l];
+      const float rr = rsqrtf(wave_sum((pp.x + pp.y) + (pp.z + pp.w)) * (1.0f / kH) + eps);
+      u32x4* sx = reinterpret_cast<u32x4*>(s_x + m * kLdX + 16 * tid);
+      u32x4 v0 = sx[0], v1 = sx[1];
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const float e0 = xn_exact(half_bits_to_float((uint16_t)(v0[d] & 0xFFFFu)), rr, wf[2 * d]);
+        const float e1 = xn_exact(half_bits_to_float((uint16_t)(v0[d] >> 16)), rr, wf[2 * d + 1]);
+        const float e2 = xn_exact(half_bits_to_float((uint16_t)(v1[d] & 0xFFFFu)), rr, wf[8 + 2 * d]);
+        const float e3 = xn_exact(half_bits_to_float((uint16_t)(v1[d] >> 16)), rr, wf[8 + 2 * d + 1]);
+        v0[d] = (uint32_t)float_to_half_bits(e0) | ((uint32_t)float_to_half_bits(e1) << 16);
+        v1[d] = (uint32_t)float_to_half_bits(e2) | ((uint32_t)float_to_half_bits(e3) << 16);
+      }
+      sx[0] = v0;
+      sx[1] = v1;
+    }
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+  f32x4 accg = {0.f, 0.f, 0.f, 0.f}, accu = accg;
+  const bool ta = t < M;                 // this lane's A row is a token
+  const uint16_t* xa = s_x + t * kLdX + kq + 16 * q;   // hot: K kq + 64 c + 16 q + 8 s
+  const uint16_t* xc = s_x + t * kLdX + kq + 32 * q;   // cold: K kq + 128 b + 32 q + 8 s
+  if (hot) {
+    const rsrc_t rg = buf_rsrc(a.gate_q, (uint32_t)a.n_hot * kH);
+    const rsrc_t ru = buf_rsrc(a.up_q, (uint32_t)a.n_hot * kH);
+    const uint32_t voff = (uint32_t)col * kH + 16 * q;
+#pragma unroll
+    for (int c = 8; c < 16; ++c) {
+      WG[c] = bload16(rg, voff, kq + 64 * c);
+      WU[c] = bload16(ru, voff, kq + 64 * c);
+    }
+#pragma unroll
+    for (int c = 0; c < 16; ++c)
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        const h8 A = ta ? *reinterpret_cast<const h8*>(xa + 64 * c + 8 * st) : h8{};
+        accg = mfma16(A, fp8x8_h8(WG[c][2 * st], WG[c][2 * st + 1]), accg);
+        accu = mfma16(A, fp8x8_h8(WU[c][2 * st], WU[c][2 * st + 1]), accu);
+      }
+  } else {
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      f32x4 tg = {0.f, 0.f, 0.f, 0.f}, tu = tg;
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        h8 A = ta ? *reinterpret_cast<const h8*>(xc + 128 * b + 8 * st) : h8{};
+        A = __builtin_shufflevector(A, A, 0, 4, 1, 5, 2, 6, 3, 7);
+        tg = mfma16(A, int4x8_h8(WG[b][st]), tg);
+        tu = mfma16(A, int4x8_h8(WU[b][st]), tu);
+      }
+      const uint32_t sg2 = SC[0][b >> 1], su2 = SC[1][b >> 1];
+      const float sg = half_bits_to_float((uint16_t)((b & 1) ? sg2 >> 16 : sg2 & 0xFFFFu));
+      const float su = half_bits_to_float((uint16_t)((b & 1) ? su2 >> 16 : su2 & 0xFFFFu));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        accg[e] = fmaf(sg, tg[e], accg[e]);
+        accu[e] = fmaf(su, tu[e], accu[e]);
+      }
+    }
+  }
+  // the four waves' sums meet in LDS (the norm partials are no longer read)
+  f32x4* s_red = reinterpret_cast<f32x4*>(s_scr);   // [3][2][kWave]
+  __syncthreads();
+  if (w > 0) {
+    s_red[((w - 1) * 2) * kWave + l] = accg;
+    s_red[((w - 1) * 2 + 1) * kWave + l] = accu;
+  }
+  __syncthreads();
+  if (w != 0) return;
+#pragma unroll
+  for (int v = 0; v < 3; ++v) {
+    accg += s_red[(v * 2) * kWave + l];
+    accu += s_red[(v * 2 + 1) * kWave + l];
+  }
+  float sg = 1.f, su = 1.f, gb = 0.f;
+  if (hot) {
+    sg = cv ? a.gate_s[col] : 0.f;
+    su = cv ? a.up_s[col] : 0.f;
+    gb = (cv && a.hot_gbias) ? a.hot_gbias[col] : 0.f;
+  } else {
+    gb = (cv && a.cold_gbias) ? a.cold_gbias[slot] : 0.f;
+  }
+  uint16_t* dst = hot ? a.hh : a.hc;
+  const int ld = hot ? a.ldh : a.ldc;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int m = 4 * q + e;
+    const float h = cv ? gated_act(fmaf(accg[e], sg, gb), accu[e] * su, a.relu, a.both) : 0.f;
+    dst[(size_t)m * ld + col] = float_to_half_bits(h);
+  }
+}
+
 // ── down ────────────────────────────────────────────────────────────────────
 
 // Hot half for at most 64 tokens: workgroup = 16 output rows, the 4 waves
@@ -1207,9 +1413,12 @@ static BatchPlan batch_plan(int M, int n_hot, int cap) {
 
 size_t batch_ws_bytes(int M, int n_hot, int cap) { return batch_plan(M, n_hot, cap).bytes; }
 
-static void launch_skinny(const BUpArgs& ua, const BDownArgs& da, bool up, hipStream_t st) {
-  if (up)
-    hipLaunchKernelGGL(k_bup_s<1>, dim3(ua.hot_wg + ua.ldc / 16), dim3(kThreads), 0, st, ua);
+static void launch_skinny(const BUpArgs& ua, const BDownArgs& da, bool up, const uint16_t* x,
+                          const uint16_t* norm_w, float eps, hipStream_t st) {
+  if (up && ua.M <= 8)
+    hipLaunchKernelGGL(k_sbup<8>, dim3(ua.hot_wg + ua.ldc / 16), dim3(kThreads), 0, st, ua, x, norm_w, eps);
+  else if (up)
+    hipLaunchKernelGGL(k_sbup<16>, dim3(ua.hot_wg + ua.ldc / 16), dim3(kThreads), 0, st, ua, x, norm_w, eps);
   else
     hipLaunchKernelGGL(k_bdown_hot_s<1>, dim3(kH / 16), dim3(kThreads), 0, st, da);
 }
@@ -1234,7 +1443,7 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
   const bool skinny = M <= kSkinnyMax;
 
   const uint16_t* xa = x;
-  if (norm_w) {
+  if (norm_w && !skinny) {   // the skinny gate/up kernel normalises the rows itself
     hipLaunchKernelGGL(k_rmsnorm, dim3(M), dim3(kThreads), 0, st, x, norm_w, eps, xn);
     OI2_CHECK_LAUNCH();
     xa = xn;
@@ -1304,7 +1513,7 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
 
   if (p.ldh + p.ldc > 0) {
     if (skinny) {
-      launch_skinny(ua, da, true, st);
+      launch_skinny(ua, da, true, x, norm_w, eps, st);
     } else if (p.prefill) {
       const int hot_tiles = p.ldh / 128, n_tiles = hot_tiles + p.ldc / 128;
       const dim3 grid((n_tiles + 7) / 8 * 8 * p.pmt);
@@ -1334,7 +1543,7 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
   }
   if (n_hot) {
     if (skinny) {
-      launch_skinny(ua, da, false, st);
+      launch_skinny(ua, da, false, x, norm_w, eps, st);
     } else if (p.prefill) {
       const dim3 grid(32 * p.pmt * p.hot_splits);
       if (p.pms == 4)

@@ -323,6 +323,46 @@ def test_predictor_logits_mask_and_selection(dev, dtype, h_dtype):
         assert dslots[:n].cpu().tolist() == [3 * i for i in got]
 
 
+def test_batch_query_equals_mean_of_the_normalisation(dev):
+    """engine.py:277 at batch 8 on many batches: the device's query (the
+    fp16 batch mean of RMSNorm(x), cast to bf16, left in the predictor
+    workspace) equals the oracle's mean over oi2_rmsnorm's rows bit for bit,
+    so the selection equals the oracle's outside the 1e-6 band.  The norm
+    arithmetic must round every kernel's product the same way: a fused
+    multiply-and-round in one kernel and not in another gave one-ulp
+    differences in about one layer in seven."""
+    import ctypes
+    g = torch.Generator(device=dev).manual_seed(77)
+    inter = 14336
+    pred = random_predictor(g, inter, 64, torch.bfloat16, dev)
+    D, U, b = pred_weights(pred)
+    norm_w = (1 + 0.05 * torch.randn(H, generator=g, device=dev)).half()
+    lut = torch.arange(inter, dtype=torch.int32, device=dev)
+    nc = (inter + 255) // 256
+    slots = torch.empty(nc * 256, dtype=torch.int32, device=dev)
+    ids = torch.empty_like(slots)
+    counts = torch.empty(nc, dtype=torch.int32, device=dev)
+    p = pred.struct()
+    L = _lib.lib()
+    wsb = L.oi2_predict_workspace_bytes(ctypes.byref(p))
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    for k in range(24):
+        xq = (torch.randn((8, H), generator=g, device=dev) * (0.5 + k / 8)).half()
+        _lib.check(L.oi2_predict_select(xq.data_ptr(), 8, norm_w.data_ptr(), ctypes.c_float(EPS),
+                                        ctypes.byref(p), 0.0, lut.data_ptr(), slots.data_ptr(),
+                                        ids.data_ptr(), counts.data_ptr(), None, None, None,
+                                        ws.data_ptr(), wsb, None))
+        torch.cuda.synchronize()
+        q_dev = ws[:4 * H].view(torch.float32).double().cpu().numpy()
+        q = query_for(rmsnorm(xq, norm_w, EPS).double().cpu().numpy(), torch.bfloat16)
+        assert np.array_equal(q_dev, q), f"batch {k}: {int((q_dev != q).sum())} query elements differ"
+        ref = O.predictor_logits(q, D, U, b)
+        want = O.cold_ids_for(ref >= 0.0, [], inter)
+        got = chunked_ids(counts, ids)
+        amb = O.ambiguous(ref, 0.5)
+        assert all(amb[i] for i in set(got) ^ set(want)), f"batch {k}: ids differ outside the band"
+
+
 def test_predictor_registry_predict_from_files(dev):
     """PredictorRegistry.predict exactly as _cold_ids_for calls it
     (engine.py:277-278): an fp32 predictor file (as predictor.py saves it),
