@@ -994,8 +994,9 @@ __global__ __launch_bounds__(kThreads) void k_bup_s(BUpArgs a) {
 
 // ── gate/up for at most 16 tokens, RMSNorm fused ─────────────────────────────
 
-// Workgroup = 16 weight rows (hot rows, or items of the dense active list);
-// wave w takes K [1024 w, 1024 w + 1024).  The workgroup first normalises
+// Workgroup = 16 weight rows (items of the dense active list in the first
+// ldc / 16 workgroups, then hot rows); wave w takes K [1024 w, 1024 w + 1024).
+// The workgroup first normalises
 // the M <= MMAX token rows itself (x_n = fp16((x r) w), the rounding of
 // nn.RMSNorm's fp16 output) into LDS, every weight load of the first half of
 // its K range already in flight, so no operand of the MFMA loop is read from
@@ -1012,77 +1013,108 @@ __global__ __launch_bounds__(kThreads) void k_sbup(BUpArgs a, const uint16_t* x,
                                                    float eps) {
   constexpr int kLdX = kH + 8;          // halves per staged row: 8208 bytes, rows on distinct banks
   constexpr int kScr = MMAX * kThreads > 3 * 2 * kWave * 4 ? MMAX * kThreads : 3 * 2 * kWave * 4;
+  // with at most 8 token rows every weight load of the workgroup goes out
+  // before the prologue; with 16 the second half waits for it (registers)
+  constexpr bool kAllUpFront = MMAX <= 8;
   __shared__ __attribute__((aligned(16))) uint16_t s_x[MMAX * kLdX];
   __shared__ __attribute__((aligned(16))) float s_scr[kScr];   // norm partials, then the wave sums
   const int tid = threadIdx.x, w = tid >> 6, l = lane_id();
   const int t = l & 15, q = l >> 4;
   const int M = a.M;
-  const bool hot = (int)blockIdx.x < a.hot_wg;
+  // the cold workgroups come first in dispatch order: their loads depend on
+  // the list, and behind the hot rows' weight traffic they would start last
+  const int cold_wg = a.ldc / 16;
+  const bool hot = (int)blockIdx.x >= cold_wg;
   const int kq = 1024 * w;
+  // the down kernels that follow add into y: cleared here, a slice per
+  // workgroup, before any workgroup may leave early
+  for (int i = (int)blockIdx.x * kThreads + tid; i < a.yzero_n4; i += (int)gridDim.x * kThreads)
+    reinterpret_cast<f32x4*>(a.yzero)[i] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   int col, slot = -1;
-  bool cv;
-  u32x4 WG[16], WU[16];                 // hot: chunks c; cold: blocks 0..7 in WG/WU[0..7]
-  u32x4 SC[2] = {u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}};
+  bool cv = false;
+  const int i0 = (int)blockIdx.x * 16;
+  int raw_total = 0, raw_slot = -1;
   if (hot) {
-    const int r0 = blockIdx.x * 16;
-    col = r0 + t;
+    col = ((int)blockIdx.x - cold_wg) * 16 + t;
     cv = col < a.n_hot;
-    const rsrc_t rg = buf_rsrc(a.gate_q, (uint32_t)a.n_hot * kH);
-    const rsrc_t ru = buf_rsrc(a.up_q, (uint32_t)a.n_hot * kH);
-    const uint32_t voff = (uint32_t)col * kH + 16 * q;   // rows past n_hot read zero
-#pragma unroll
-    for (int c = 0; c < 8; ++c) {
-      WG[c] = bload16(rg, voff, kq + 64 * c);
-      WU[c] = bload16(ru, voff, kq + 64 * c);
-    }
   } else {
-    const int i0 = ((int)blockIdx.x - a.hot_wg) * 16;
     col = i0 + t;
-    const int raw_total = *a.total;
-    const int raw_slot = a.dslots[min(col, a.cap - 1)];
-    asm volatile("" ::"v"(raw_slot), "s"(raw_total));   // both loads in flight before either is used
-    const int total = min(raw_total, a.cap);
-    if (i0 >= total) return;   // the whole workgroup
-    slot = col < total ? raw_slot : -1;
-    cv = slot >= 0 && slot < a.n_records;
-    const rsrc_t rr = buf_rsrc(a.records, (uint32_t)a.n_records * kRecBytes);
-    const uint32_t ro = cv ? (uint32_t)slot * kRecBytes : kNoOffset;
-#pragma unroll
-    for (int b = 0; b < 8; ++b) {
-      WG[b] = bload16(rr, ro + kOffGate + 16 * q, 512 * w + 64 * b);
-      WU[b] = bload16(rr, ro + kOffUp + 16 * q, 512 * w + 64 * b);
-    }
-    // the quarter's 8 group scales of each vector (16 bytes at 2 mod 16)
-    SC[0] = bload16(rr, ro + kOffScales, 16 * w);
-    SC[1] = bload16(rr, ro + kOffScales + 2 * kGroups, 16 * w);
+    raw_total = *a.total;
+    raw_slot = a.dslots[min(col, a.cap - 1)];
   }
-  __builtin_amdgcn_sched_barrier(0);
-
-  // prologue: the token rows into LDS (thread tid holds elements
-  // [16 tid, 16 tid + 16) of each row), their sum-of-squares partials, then
-  // x_n in place
+  // the token rows next (L2-resident, needed by the prologue; a cold
+  // workgroup's go out with its list loads, before it waits on them), then
+  // the weights: a wave's loads complete in order
+  u32x4 xin[MMAX][2];
+#pragma unroll
+  for (int m = 0; m < MMAX; ++m) {
+    if (m < M) {
+      const u32x4* px = reinterpret_cast<const u32x4*>(x + (size_t)m * kH) + 2 * tid;
+      xin[m][0] = px[0];
+      xin[m][1] = px[1];
+    }
+  }
   u32x4 wn[2] = {u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}};
   if (norm_w) {
     wn[0] = reinterpret_cast<const u32x4*>(norm_w)[2 * tid];
     wn[1] = reinterpret_cast<const u32x4*>(norm_w)[2 * tid + 1];
   }
+  if (!hot) {
+    const int total = min(raw_total, a.cap);
+    if (i0 >= total) return;   // the whole workgroup
+    slot = col < total ? raw_slot : -1;
+    cv = slot >= 0 && slot < a.n_records;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  u32x4 WG[16], WU[16];                 // hot: chunks c; cold: blocks 0..7 in WG/WU[0..7]
+  u32x4 SC[2] = {u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}};
+  const rsrc_t rg = buf_rsrc(a.gate_q, (uint32_t)a.n_hot * kH);
+  const rsrc_t ru = buf_rsrc(a.up_q, (uint32_t)a.n_hot * kH);
+  const uint32_t voff = (uint32_t)col * kH + 16 * q;   // rows past n_hot read zero
+  const rsrc_t rr = buf_rsrc(a.records, (uint32_t)a.n_records * kRecBytes);
+  const uint32_t ro = cv ? (uint32_t)slot * kRecBytes : kNoOffset;
+  // the weight loads of this wave, in issue order: hot chunks c (gate and
+  // up), or cold blocks b and the scales; `issue(i0, i1)` sends loads
+  // [i0, i1) of that order, so the loads can be spread over the prologue's
+  // VALU work (a wave stalls at a load once the CU's memory queue is full)
+  const int n_loads = hot ? (kAllUpFront ? 16 : 8) : 9;
+  auto issue = [&](int i0, int i1) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (i < i0 || i >= i1 || i >= n_loads) continue;
+      if (hot) {
+        WG[i] = bload16(rg, voff, kq + 64 * i);
+        WU[i] = bload16(ru, voff, kq + 64 * i);
+      } else if (i < 8) {
+        WG[i] = bload16(rr, ro + kOffGate + 16 * q, 512 * w + 64 * i);
+        WU[i] = bload16(rr, ro + kOffUp + 16 * q, 512 * w + 64 * i);
+      } else {
+        // the quarter's 8 group scales of each vector (16 bytes at 2 mod 16)
+        SC[0] = bload16(rr, ro + kOffScales, 16 * w);
+        SC[1] = bload16(rr, ro + kOffScales + 2 * kGroups, 16 * w);
+      }
+    }
+  };
+  issue(0, 4);
+
+  // prologue: the token rows into LDS (thread tid holds elements
+  // [16 tid, 16 tid + 16) of each row) with their sum-of-squares partials,
+  // then x_n in place; the remaining weight loads go out between its rows
 #pragma unroll
   for (int m = 0; m < MMAX; ++m) {
     if (m >= M) break;
-    const u32x4* px = reinterpret_cast<const u32x4*>(x + (size_t)m * kH) + 2 * tid;
-    const u32x4 v0 = px[0], v1 = px[1];
     u32x4* sx = reinterpret_cast<u32x4*>(s_x + m * kLdX + 16 * tid);
-    sx[0] = v0;
-    sx[1] = v1;
+    sx[0] = xin[m][0];
+    sx[1] = xin[m][1];
     if (norm_w) {
       float v[16];
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
-        v[2 * d] = half_bits_to_float((uint16_t)(v0[d] & 0xFFFFu));
-        v[2 * d + 1] = half_bits_to_float((uint16_t)(v0[d] >> 16));
-        v[8 + 2 * d] = half_bits_to_float((uint16_t)(v1[d] & 0xFFFFu));
-        v[8 + 2 * d + 1] = half_bits_to_float((uint16_t)(v1[d] >> 16));
+        v[2 * d] = half_bits_to_float((uint16_t)(xin[m][0][d] & 0xFFFFu));
+        v[2 * d + 1] = half_bits_to_float((uint16_t)(xin[m][0][d] >> 16));
+        v[8 + 2 * d] = half_bits_to_float((uint16_t)(xin[m][1][d] & 0xFFFFu));
+        v[8 + 2 * d + 1] = half_bits_to_float((uint16_t)(xin[m][1][d] >> 16));
       }
       float ss = 0.0f;
 #pragma unroll
@@ -1103,11 +1135,11 @@ __global__ __launch_bounds__(kThreads) void k_sbup(BUpArgs a, const uint16_t* x,
 #pragma unroll
     for (int m = 0; m < MMAX; ++m) {
       if (m >= M) break;
+      issue(4 + 2 * m, 6 + 2 * m);
       // the canonical factor: lane l sums partials 4 l .. 4 l + 3, then a DPP tree
       const f32x4 pp = reinterpret_cast<const f32x4*>(s_scr + m * kThreads)[l];
       const float rr = rsqrtf(wave_sum((pp.x + pp.y) + (pp.z + pp.w)) * (1.0f / kH) + eps);
-      u32x4* sx = reinterpret_cast<u32x4*>(s_x + m * kLdX + 16 * tid);
-      u32x4 v0 = sx[0], v1 = sx[1];
+      u32x4 v0 = xin[m][0], v1 = xin[m][1];
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
         const float e0 = xn_exact(half_bits_to_float((uint16_t)(v0[d] & 0xFFFFu)), rr, wf[2 * d]);
@@ -1117,10 +1149,12 @@ __global__ __launch_bounds__(kThreads) void k_sbup(BUpArgs a, const uint16_t* x,
         v0[d] = (uint32_t)float_to_half_bits(e0) | ((uint32_t)float_to_half_bits(e1) << 16);
         v1[d] = (uint32_t)float_to_half_bits(e2) | ((uint32_t)float_to_half_bits(e3) << 16);
       }
+      u32x4* sx = reinterpret_cast<u32x4*>(s_x + m * kLdX + 16 * tid);
       sx[0] = v0;
       sx[1] = v1;
     }
   }
+  issue(norm_w ? 4 + 2 * M : 4, 16);
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
   f32x4 accg = {0.f, 0.f, 0.f, 0.f}, accu = accg;
@@ -1128,13 +1162,12 @@ __global__ __launch_bounds__(kThreads) void k_sbup(BUpArgs a, const uint16_t* x,
   const uint16_t* xa = s_x + t * kLdX + kq + 16 * q;   // hot: K kq + 64 c + 16 q + 8 s
   const uint16_t* xc = s_x + t * kLdX + kq + 32 * q;   // cold: K kq + 128 b + 32 q + 8 s
   if (hot) {
-    const rsrc_t rg = buf_rsrc(a.gate_q, (uint32_t)a.n_hot * kH);
-    const rsrc_t ru = buf_rsrc(a.up_q, (uint32_t)a.n_hot * kH);
-    const uint32_t voff = (uint32_t)col * kH + 16 * q;
+    if (!kAllUpFront) {
 #pragma unroll
-    for (int c = 8; c < 16; ++c) {
-      WG[c] = bload16(rg, voff, kq + 64 * c);
-      WU[c] = bload16(ru, voff, kq + 64 * c);
+      for (int c = 8; c < 16; ++c) {
+        WG[c] = bload16(rg, voff, kq + 64 * c);
+        WU[c] = bload16(ru, voff, kq + 64 * c);
+      }
     }
 #pragma unroll
     for (int c = 0; c < 16; ++c)
@@ -1199,16 +1232,30 @@ __global__ __launch_bounds__(kThreads) void k_sbup(BUpArgs a, const uint16_t* x,
 
 // ── down ────────────────────────────────────────────────────────────────────
 
-// Hot half for at most 64 tokens: workgroup = 16 output rows, the 4 waves
-// split the K blocks and meet in LDS; adds into y.
+// Hot half for at most 16 tokens, the last small-batch kernel: workgroup =
+// 16 output rows, the 4 waves split the K blocks and meet in LDS.  Each
+// wave's activation fragments (L2-resident, written by the gate/up kernel)
+// are loaded before its down rows, so no load waits behind another in the
+// loop.  The workgroup owns its rows outright: it adds the hot product to y
+// (the cold part, or zero) and writes out = fp16(res + y) and y32.
 template <int MS>
 __global__ __launch_bounds__(kThreads) void k_bdown_hot_s(BDownArgs a) {
+  static_assert(MS == 1, "at most 16 tokens");
   constexpr int NBmax = 8;   // ldh <= 4096: at most 32 blocks, 8 per wave
   __shared__ f32x4 s_red[3][MS][kWave];
   const int w = threadIdx.x >> 6, l = lane_id();
   const int h = blockIdx.x * 16 + (l & 15);
   const int nb = a.hot_blocks;
   const int b0 = w * nb / 4, b1 = (w + 1) * nb / 4;
+  const int m = l & 15;
+  const bool av = m < a.M;
+  const uint16_t* hr = a.hh + (size_t)(av ? m : 0) * a.ldh + 32 * (l >> 4);
+  h8 A[NBmax][4];
+#pragma unroll
+  for (int b = 0; b < NBmax; ++b)
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+      A[b][s] = (av && b0 + b < b1) ? *reinterpret_cast<const h8*>(hr + (b0 + b) * kBK + 8 * s) : h8{};
   const uint8_t* dr = a.down_q + (size_t)h * a.down_stride + 32 * (l >> 4);
   u32x4 D[NBmax][2];
 #pragma unroll
@@ -1219,47 +1266,31 @@ __global__ __launch_bounds__(kThreads) void k_bdown_hot_s(BDownArgs a) {
     D[b][0] = (in && k < a.down_stride) ? load16(dr + (b0 + b) * kBK) : z;
     D[b][1] = (in && k + 16 < a.down_stride) ? load16(dr + (b0 + b) * kBK + 16) : z;
   }
-  const uint16_t* hr[MS];
-  bool av[MS];
-#pragma unroll
-  for (int ms = 0; ms < MS; ++ms) {
-    const int m = 16 * ms + (l & 15);
-    av[ms] = m < a.M;
-    hr[ms] = a.hh + (size_t)(av[ms] ? m : 0) * a.ldh + 32 * (l >> 4);
-  }
-  f32x4 acc[MS];
-#pragma unroll
-  for (int ms = 0; ms < MS; ++ms) acc[ms] = f32x4{0.f, 0.f, 0.f, 0.f};
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int b = 0; b < NBmax; ++b) {
     if (b0 + b >= b1) break;
-    h8 A[MS][4];
-#pragma unroll
-    for (int ms = 0; ms < MS; ++ms)
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-        A[ms][s] = av[ms] ? *reinterpret_cast<const h8*>(hr[ms] + (b0 + b) * kBK + 8 * s) : h8{};
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const h8 bv = fp8x8_h8(dword_of(D[b][0], D[b][1], 2 * s), dword_of(D[b][0], D[b][1], 2 * s + 1));
-#pragma unroll
-      for (int ms = 0; ms < MS; ++ms) acc[ms] = mfma16(A[ms][s], bv, acc[ms]);
+      acc = mfma16(A[b][s], bv, acc);
     }
   }
-  if (w > 0) {
-#pragma unroll
-    for (int ms = 0; ms < MS; ++ms) s_red[w - 1][ms][l] = acc[ms];
-  }
+  if (w > 0) s_red[w - 1][0][l] = acc;
   __syncthreads();
   if (w != 0) return;
   const float sd = a.down_s[h];
+  const f32x4 v = acc + s_red[0][0][l] + s_red[1][0][l] + s_red[2][0][l];
 #pragma unroll
-  for (int ms = 0; ms < MS; ++ms) {
-    const f32x4 v = acc[ms] + s_red[0][ms][l] + s_red[1][ms][l] + s_red[2][ms][l];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int m = 16 * ms + 4 * (l >> 4) + e;
-      if (m < a.M) a.y[(size_t)m * kH + h] = v[e] * sd;   // the first and only hot writer
+  for (int e = 0; e < 4; ++e) {
+    const int t = 4 * (l >> 4) + e;
+    if (t >= a.M) continue;
+    const size_t i = (size_t)t * kH + h;
+    const float y = a.y[i] + v[e] * sd;
+    if (a.y32) a.y32[i] = y;
+    if (a.out) {
+      const float r = a.res ? half_bits_to_float(a.res[i]) : 0.f;
+      a.out[i] = float_to_half_bits(r + y);
     }
   }
 }
@@ -1381,7 +1412,6 @@ static BatchPlan batch_plan(int M, int n_hot, int cap) {
   if (p.prefill) {
     p.pms = prefill_ms(M);
     p.pmt = (M + 32 * p.pms - 1) / (32 * p.pms);
-    // hot down: 16 output tiles x token tiles x K splits, about 256 workgroups
     // hot down: 32 output tiles x token tiles x K splits, about 256 workgroups
     p.hot_splits = std::max(1, std::min(p.hot_blocks, 256 / (32 * p.pmt)));
   } else {
@@ -1412,6 +1442,15 @@ static BatchPlan batch_plan(int M, int n_hot, int cap) {
 }
 
 size_t batch_ws_bytes(int M, int n_hot, int cap) { return batch_plan(M, n_hot, cap).bytes; }
+
+// Cold down grid: 16 output tiles x 128-token tiles x item ranges, about 256
+// workgroups; a range holds at most kDcMaxItems items.
+static int cold_down_splits(int M, int cap) {
+  const int mtc = (M + 127) / 128;
+  const int n_blk = (cap + kDcItems - 1) / kDcItems;
+  const int min_splits = (n_blk + kDcMaxItems / kDcItems - 1) / (kDcMaxItems / kDcItems);
+  return std::max(min_splits, std::min(n_blk, std::max(1, 256 / (16 * mtc))));
+}
 
 static void launch_skinny(const BUpArgs& ua, const BDownArgs& da, bool up, const uint16_t* x,
                           const uint16_t* norm_w, float eps, hipStream_t st) {
@@ -1511,10 +1550,38 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
   }
   da.y = y;
 
-  if (p.ldh + p.ldc > 0) {
-    if (skinny) {
+  if (skinny) {
+    // gate/up (clearing y on the way), the cold down adding into y, then
+    // the hot down, which adds its product and writes the outputs
+    const int n4 = M * (kH / 4);
+    const int grid = std::min(2048, (n4 + kThreads - 1) / kThreads);
+    if (p.ldh + p.ldc > 0) {
+      ua.yzero = y;
+      ua.yzero_n4 = n4;
       launch_skinny(ua, da, true, x, norm_w, eps, st);
-    } else if (p.prefill) {
+    } else {
+      hipLaunchKernelGGL(k_bfill, dim3(grid), dim3(kThreads), 0, st, y, n4);
+    }
+    OI2_CHECK_LAUNCH();
+    if (has_cold) {
+      const int splits = cold_down_splits(M, cap);
+      hipLaunchKernelGGL(k_pgemm_down_cold, dim3(16 * splits), dim3(kThreads), 0, st, da, 1, splits);
+      OI2_CHECK_LAUNCH();
+    }
+    if (n_hot) {
+      da.res = add_residual ? x : nullptr;
+      da.out = out;
+      da.y32 = y32;
+      launch_skinny(ua, da, false, x, norm_w, eps, st);
+    } else {
+      hipLaunchKernelGGL(k_bfinal, dim3(grid), dim3(kThreads), 0, st, y, M, add_residual ? x : nullptr,
+                         out, y32);
+    }
+    OI2_CHECK_LAUNCH();
+    return OI2_OK;
+  }
+  if (p.ldh + p.ldc > 0) {
+    if (p.prefill) {
       const int hot_tiles = p.ldh / 128, n_tiles = hot_tiles + p.ldc / 128;
       const dim3 grid((n_tiles + 7) / 8 * 8 * p.pmt);
       if (p.pms == 4)
@@ -1537,14 +1604,12 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
   int grid = (n4 + kThreads - 1) / kThreads;
   grid = grid > 2048 ? 2048 : grid;
   // the hot product writes y outright when one workgroup owns each output
-  if (!n_hot || (!skinny && p.hot_splits > 1)) {
+  if (!n_hot || p.hot_splits > 1) {
     hipLaunchKernelGGL(k_bfill, dim3(grid), dim3(kThreads), 0, st, y, n4);
     OI2_CHECK_LAUNCH();
   }
   if (n_hot) {
-    if (skinny) {
-      launch_skinny(ua, da, false, x, norm_w, eps, st);
-    } else if (p.prefill) {
+    if (p.prefill) {
       const dim3 grid(32 * p.pmt * p.hot_splits);
       if (p.pms == 4)
         hipLaunchKernelGGL(k_pgemm_down_hot<4>, grid, dim3(kThreads), 0, st, da, p.pmt, p.hot_splits);
@@ -1557,12 +1622,8 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
     OI2_CHECK_LAUNCH();
   }
   if (has_cold) {
-    // 16 output tiles x 128-token tiles x item ranges, about 256 workgroups;
-    // a range holds at most kDcMaxItems items
     const int mtc = (M + 127) / 128;
-    const int n_blk = (cap + kDcItems - 1) / kDcItems;
-    const int min_splits = (n_blk + kDcMaxItems / kDcItems - 1) / (kDcMaxItems / kDcItems);
-    const int splits = std::max(min_splits, std::min(n_blk, std::max(1, 256 / (16 * mtc))));
+    const int splits = cold_down_splits(M, cap);
     hipLaunchKernelGGL(k_pgemm_down_cold, dim3(16 * mtc * splits), dim3(kThreads), 0, st, da, mtc, splits);
     OI2_CHECK_LAUNCH();
   }

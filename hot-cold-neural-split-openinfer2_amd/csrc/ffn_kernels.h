@@ -178,6 +178,8 @@ struct BUpArgs {
   float* pu;
   int ldp;                  // ldh + ldc
   int Mpad;
+  float* yzero;             // k_sbup: (M, H) fp32 cleared on the way (the down kernels add into it)
+  int yzero_n4;             // its length in float4
 };
 
 struct BDownArgs {
@@ -197,6 +199,12 @@ struct BDownArgs {
   const int32_t* total;
   int cap;
   float* y;                 // (M, H) fp32 output, accumulated with atomics
+  // k_bdown_hot_s, the last of the small-batch kernels: y (the cold part,
+  // or zero) plus the hot product -> out = fp16(res + y) (res may be null),
+  // and y32 = y when asked
+  const uint16_t* res;
+  uint16_t* out;
+  float* y32;
 };
 
 __global__ void k_bup(BUpArgs a);
