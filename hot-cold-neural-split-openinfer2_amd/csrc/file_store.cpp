@@ -13,7 +13,9 @@
 //          the page cache, and copied out from there.  Sections start on 4096
 //          (splitter.py:250-254) but records are 6400 bytes at 16 + 6400 k, so
 //          a record covers two or three pages; records whose page ranges meet
-//          (or lie within kGapPages of each other) are read with one pread.
+//          or lie within the read gap (16 KB unless set) of each other are read
+//          with one pread: on a device bound by its operation rate, reading a
+//          gap costs less than another operation.
 // A request is split over a fixed pool of threads by contiguous runs of the
 // records sorted by file position; each thread plans and issues its own
 // reads.  The call returns when every record is in place.
@@ -51,7 +53,7 @@ constexpr size_t kRec = 6400;          // NEURON_RECORD_BYTES (splitter.py:75-76
 constexpr size_t kHeader = 16;         // <HHIq section header (splitter.py:230)
 constexpr size_t kPage = 4096;
 constexpr size_t kBounce = 1 << 20;    // per-thread O_DIRECT bounce buffer
-constexpr size_t kGapPages = 1;        // pages of gap one read may span
+constexpr size_t kGapBytes = 16384;    // default gap one O_DIRECT read may span
 
 // A fixed pool: run(n, fn) calls fn(0..n-1) spread over the threads and
 // returns when all calls are done.
@@ -118,6 +120,7 @@ struct oi2_file_store {
   bool direct = false;
   std::vector<uint64_t> sec_off, sec_n;
   std::vector<void*> bounce;          // per part: kBounce bytes, 4096-aligned
+  size_t gap = kGapBytes;             // O_DIRECT: largest gap between records one read spans
   Pool* pool = nullptr;
   std::mutex call_mu;                 // one read at a time per handle
 };
@@ -141,7 +144,7 @@ int read_direct(oi2_file_store* fs, int part, uint64_t base, const int32_t* slot
   int k = b;
   while (k < e) {
     // one pread: records k .. k2-1 whose page ranges are contiguous (or
-    // within kGapPages) and fit the bounce buffer
+    // within fs->gap bytes of each other) and fit the bounce buffer
     const uint64_t first = base + kHeader + (uint64_t)slots[order[k]] * kRec;
     const uint64_t p0 = first / kPage * kPage;
     uint64_t p1 = (first + kRec + kPage - 1) / kPage * kPage;
@@ -149,7 +152,7 @@ int read_direct(oi2_file_store* fs, int part, uint64_t base, const int32_t* slot
     while (k2 < e) {
       const uint64_t s = base + kHeader + (uint64_t)slots[order[k2]] * kRec;
       const uint64_t q0 = s / kPage * kPage, q1 = (s + kRec + kPage - 1) / kPage * kPage;
-      if (q0 > p1 + kGapPages * kPage || q1 - p0 > kBounce) break;
+      if (q0 > p1 + fs->gap || q1 - p0 > kBounce) break;
       p1 = std::max(p1, q1);
       ++k2;
     }
@@ -315,6 +318,17 @@ int oi2_file_store_stage(oi2_file_store* fs, int32_t section, const int32_t* slo
     oi2::set_error("file store: hipMemcpyAsync of %d records failed: %s", n, hipGetErrorString(e));
     return OI2_EHIP;
   }
+  return OI2_OK;
+}
+
+int oi2_file_store_set_read_gap(oi2_file_store* fs, int64_t bytes) {
+  oi2::clear_error();
+  if (!fs || bytes < 0 || bytes > (int64_t)(kBounce / 2)) {
+    oi2::set_error("file store: null handle or read gap %lld outside 0 .. %zu", (long long)bytes,
+                   kBounce / 2);
+    return OI2_EINVAL;
+  }
+  fs->gap = (size_t)bytes;
   return OI2_OK;
 }
 

@@ -108,6 +108,7 @@ _SIGS = {
     "oi2_file_store_read": (c_int32, [c_void_p, c_int32, c_void_p, c_int32, c_void_p]),
     "oi2_file_store_stage": (c_int32, [c_void_p, c_int32, c_void_p, c_int32, c_void_p, c_void_p,
                                        c_void_p]),
+    "oi2_file_store_set_read_gap": (c_int32, [c_void_p, ctypes.c_int64]),
     "oi2_file_store_close": (c_int32, [c_void_p]),
     "oi2_attn_workspace_bytes": (c_size_t, [c_int32, c_int32, c_int32, c_int32, c_int32]),
     "oi2_attn_forward": (c_int32, [c_void_p, c_int32, c_int32, POINTER(Attn), c_float, c_void_p,

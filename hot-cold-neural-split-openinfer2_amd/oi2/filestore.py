@@ -20,7 +20,8 @@ from . import format as fmt
 
 
 class FileStore:
-    def __init__(self, cold_bin: str, cold_index: str, direct: bool = False, threads: int = 8):
+    def __init__(self, cold_bin: str, cold_index: str, direct: bool = False, threads: int = 8,
+                 read_gap: int | None = None):
         index = np.load(cold_index)
         self.n_experts = int(index.shape[1]) if index.ndim == 3 else 1
         flat = np.ascontiguousarray(index.reshape(-1, 2).astype(np.uint64))
@@ -35,6 +36,8 @@ class FileStore:
                                    int(self.direct), int(threads), ctypes.byref(h))
         _lib.check(rc)
         self._h = h
+        if read_gap is not None:
+            _lib.check(L.oi2_file_store_set_read_gap(h, int(read_gap)))
 
     def section_id(self, layer: int, expert: int = 0) -> int:
         return layer * self.n_experts + expert

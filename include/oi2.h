@@ -340,6 +340,12 @@ int oi2_file_store_read(oi2_file_store* fs, int32_t section, const int32_t* slot
  * run (an event recorded on `stream` after the call marks it). */
 int oi2_file_store_stage(oi2_file_store* fs, int32_t section, const int32_t* slots, int32_t n,
                          uint8_t* host_buf, uint8_t* dst, void* stream);
+/* O_DIRECT reads only: records whose page ranges lie within `bytes` of each
+ * other are read with one pread (the gap read and dropped); 0 merges only
+ * touching ranges.  Default 16384; at most 524288.  No reference
+ * counterpart: a tuning knob of the direct-I/O reads (splitter.py:322-323
+ * reads through a mapping). */
+int oi2_file_store_set_read_gap(oi2_file_store* fs, int64_t bytes);
 /* ColdWeightStore.close (splitter.py:405-407). */
 int oi2_file_store_close(oi2_file_store* fs);
 
