@@ -212,3 +212,31 @@ def test_file_store_reads_records_in_request_order(direct, threads):
                 fs.read(0, [0, 1], np.empty((1, 6400), np.uint8))
         finally:
             fs.close()
+
+
+@pytest.mark.parametrize("gap", [0, 4096, 16384, 131072, 524288])
+def test_file_store_direct_read_gap(gap):
+    """O_DIRECT reads that merge records across gaps of 0 to 512 KB (whole
+    sections in one read at the largest) return the same bytes as the
+    file; gaps outside 0 .. 512 KB are refused."""
+    from oi2 import _lib
+    with tempfile.TemporaryDirectory(dir=os.path.dirname(os.path.abspath(__file__))) as tmp:
+        cold_bin, cold_idx, config, layers = synthetic_cold_file(tmp, 2, 200, 5)
+        raw = np.frombuffer(open(cold_bin, "rb").read(), np.uint8)
+        index = np.load(cold_idx)
+        fs = _file_store_or_skip(cold_bin, cold_idx, True, 3)
+        try:
+            _lib.check(_lib.load_library().oi2_file_store_set_read_gap(fs._h, gap))
+            rng = np.random.default_rng(gap)
+            for li in range(2):
+                base = int(index[li, 0, 0]) + 16
+                for req in (rng.choice(200, 30, replace=False), rng.integers(0, 200, 120), np.arange(200)):
+                    out = np.empty((len(req), 6400), np.uint8)
+                    fs.read(li, req, out)
+                    want = np.stack([raw[base + 6400 * s: base + 6400 * (s + 1)] for s in req])
+                    assert np.array_equal(out, want)
+            for bad in (-1, 524289):
+                with pytest.raises(oi2.OI2Error, match="read gap"):
+                    _lib.check(_lib.load_library().oi2_file_store_set_read_gap(fs._h, bad))
+        finally:
+            fs.close()
