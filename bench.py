@@ -406,6 +406,90 @@ def measure_multi_token(layers, dev, M, frac, reps, seed=1):
             "weight_gbs": weight_bytes / (us * 1e-6) / 1e9}
 
 
+def attention_layers(dev, g, n_kv=8):
+    """32 GroupedQueryAttention layers of Mistral-7B geometry from seeded
+    N(0, 0.02) weights cast to fp8 e4m3fn, as splitter.py:175-177 stores them."""
+    import torch
+    import oi2
+    cfg = {"num_attention_heads": 32, "num_key_value_heads": n_kv, "hidden_dim": H,
+           "rms_norm_eps": EPS}
+    layers = []
+    for li in range(N_LAYERS):
+        p = f"layer_{li:03d}."
+
+        def w(r, c):
+            return (torch.randn((r, c), generator=g, device=dev) * 0.02).to(torch.float8_e4m3fn)
+        wd = {p + "q_proj": w(H, H), p + "k_proj": w(n_kv * 128, H), p + "v_proj": w(n_kv * 128, H),
+              p + "o_proj": w(H, H),
+              p + "input_layernorm": (1.0 + 0.05 * torch.randn(H, generator=g, device=dev)).half()}
+        layers.append(oi2.GroupedQueryAttention(li, wd, cfg))
+    return layers
+
+
+def measure_decode_step(ffn_layers_syn, thr, dev, ctx=512, reps=20, seed=7):
+    """A whole decode step of the 32 layers, attention and FFN, in
+    DesdemonaEngine.forward's order (engine.py:421-438) through the drop-in
+    layers (oi2.DecoderStep over GroupedQueryAttention and SparseFFNLayer):
+    batch 1, each layer's KV cache holding `ctx` positions, the cold records
+    in HBM, each layer's cold set predicted from the previous layer's
+    post-attention state.  The step is captured in one graph and replayed."""
+    import math
+    import torch
+    import oi2
+    from oi2.decode_step import DecoderStep
+    from oi2.store import ColdSection
+    g = torch.Generator(device=dev).manual_seed(seed)
+    attn = attention_layers(dev, g)
+
+    class _Sections:                  # the store interface SparseFFNLayer reads
+        residency = "hbm"
+
+        def __init__(self, lay):
+            self.sec = ColdSection(0, lay.cold_ids.cpu().numpy(), lay.records, lay.lut,
+                                   lay.lut.cpu().numpy(), INTER)
+
+        def section(self, layer_idx, expert_idx=0):
+            return self.sec
+
+    cfg = {"hidden_act": "silu", "intermediate_dim": INTER, "rms_norm_eps": EPS, "hidden_dim": H}
+    p_thr = 1.0 / (1.0 + math.exp(-thr))
+    ffn = [oi2.SparseFFNLayer(li, "", _Sections(l), l.predictor, cfg, dev, hot=l.hot,
+                              ffn_norm_weight=l.norm_w, threshold=p_thr)
+           for li, l in enumerate(ffn_layers_syn)]
+    step = DecoderStep(attn, ffn)
+    cos, sin = oi2.rope_tables(ctx + 1, 128, 1e6, device=dev)
+    c1, s1 = cos[ctx:ctx + 1], sin[ctx:ctx + 1]
+    x0 = torch.randn((1, 1, H), generator=g, device=dev).half()
+    caches = []
+    for _ in attn:
+        k = torch.randn((1, 8, ctx, 128), generator=g, device=dev).half()
+        caches.append((k, torch.randn_like(k)))
+    stream = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(stream):
+        _, kv = step(x0, c1, s1, caches)          # copies the caches into the layers' buffers
+        kvs = [(k[:, :, :ctx], v[:, :, :ctx]) for k, v in kv]
+        step(x0, c1, s1, kvs)
+    stream.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        y, _ = step(x0, c1, s1, kvs)
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    assert torch.isfinite(y.float()).all()
+    del graph
+    return {"layers": N_LAYERS, "batch": 1, "context": ctx, "us_per_token": us,
+            "us_per_layer": us / N_LAYERS, "tok_s": 1e6 / us,
+            "path": "DecoderStep: GroupedQueryAttention (3 kernels) + SparseFFNLayer (predictor, "
+                    "gate/up, down kernels) per layer, one graph per token"}
+
+
 def measure_attention(dev, contexts=(512, 4096), reps=20, seed=6):
     """Decode attention (engine.py:63-125) at batch 1 through 32 layers of Mistral-7B geometry (32 query / 8 kv
     heads of 128, fp8 projections): each layer's cache holds `ctx` positions
@@ -417,17 +501,7 @@ def measure_attention(dev, contexts=(512, 4096), reps=20, seed=6):
     import oi2
     n_kv = 8
     g = torch.Generator(device=dev).manual_seed(seed)
-    cfg = {"num_attention_heads": 32, "num_key_value_heads": n_kv, "hidden_dim": H,
-           "rms_norm_eps": EPS}
-    layers = []
-    for li in range(N_LAYERS):
-        p = f"layer_{li:03d}."
-
-        def w(r, c):
-            return (torch.randn((r, c), generator=g, device=dev) * 0.02).to(torch.float8_e4m3fn)
-        wd = {p + "q_proj": w(H, H), p + "k_proj": w(n_kv * 128, H), p + "v_proj": w(n_kv * 128, H),
-              p + "o_proj": w(H, H), p + "input_layernorm": torch.ones(H, dtype=torch.float16, device=dev)}
-        layers.append(oi2.GroupedQueryAttention(li, wd, cfg))
+    layers = attention_layers(dev, g, n_kv)
     out = {"layers": N_LAYERS, "batch": 1, "n_q": 32, "n_kv": n_kv, "head_dim": 128,
            "weight_bytes_per_layer": (H + 2 * n_kv * 128) * H + H * H}
     stream = torch.cuda.Stream(device=dev)
@@ -595,7 +669,11 @@ def main():
         log(f"copied {src.numel() * 4} bytes 8 times")
         return
     if args.attention_only:
-        print(json.dumps({"attention": measure_attention(dev)}), flush=True)
+        res = measure_attention(dev)
+        layers, st, thr, g = build_stack(args.seed, dev)
+        res["full_decode_step"] = measure_decode_step(layers, thr, dev)
+        log(f"full decode step: {res['full_decode_step']['us_per_token']:.0f} us/token")
+        print(json.dumps({"attention": res}), flush=True)
         return
     t0 = time.time()
     layers, st, thr, g = build_stack(args.seed, dev)
@@ -729,6 +807,10 @@ def main():
     attention = None
     if args.attention and not args.hbm_only:
         attention = measure_attention(dev)
+        attention["full_decode_step"] = measure_decode_step(layers, thr, dev)
+        f = attention["full_decode_step"]
+        log(f"full decode step (attention + FFN, ctx {f['context']}): {f['us_per_token']:.0f} us/token, "
+            f"{f['tok_s']:.0f} tok/s")
 
     writer = None
     if args.split_writer and not args.hbm_only:
