@@ -1018,7 +1018,10 @@ __global__ __launch_bounds__(kThreads) void k_sbup(BUpArgs a, const uint16_t* x,
   constexpr bool kAllUpFront = MMAX <= 8;
   __shared__ __attribute__((aligned(16))) uint16_t s_x[MMAX * kLdX];
   __shared__ __attribute__((aligned(16))) float s_scr[kScr];   // norm partials, then the wave sums
-  const int tid = threadIdx.x, w = tid >> 6, l = lane_id();
+  // the wave index as a scalar: the weight loads' K offsets then go in the
+  // buffer instructions' scalar offset operand (a per-lane value there would
+  // make the compiler wrap every load in a loop over distinct values)
+  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = lane_id();
   const int t = l & 15, q = l >> 4;
   const int M = a.M;
   // the cold workgroups come first in dispatch order: their loads depend on

@@ -797,8 +797,15 @@ __device__ void stage_copy_layer(const uint8_t* src_base, int n_records, const A
   total = total < cap ? total : cap;
   const int lane = lane_id();
   constexpr int kChunks = kRecBytes / 16;   // 400
-  const __amdgpu_buffer_rsrc_t rdst =
-      __builtin_amdgcn_make_buffer_rsrc(dst_base, (short)0, (int)((uint32_t)cap * kRecBytes), 0x00020000);
+  // the destination and its size as scalars (they come from a table in
+  // memory; a per-lane descriptor would make the compiler loop every store
+  // over the distinct values)
+  const uint64_t dv = reinterpret_cast<uint64_t>(dst_base);
+  uint8_t* dst_u = reinterpret_cast<uint8_t*>(
+      ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(dv >> 32)) << 32) |
+      (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)dv));
+  const __amdgpu_buffer_rsrc_t rdst = __builtin_amdgcn_make_buffer_rsrc(
+      dst_u, (short)0, __builtin_amdgcn_readfirstlane((int)((uint32_t)cap * kRecBytes)), 0x00020000);
   // two records per wave in flight, both loaded before either is stored
   // (measured: one leaves the PCIe link short of requests; three or four
   // gain nothing over two)
