@@ -9,14 +9,18 @@
 //            split K and meet in LDS, every weight load issued up front;
 //            k_bup + k_bact (M < 192): 64 tokens x 64 rows, split K;
 //            k_pgemm_up (M >= 192): 32x32x16 tiles, weights streamed in registers
-//   down     Y (M, H) fp32, accumulated with fp32 atomics after the first writer:
+//   down     Y (M, H) fp32
 //            hot  H_hot D_hot^T (fp8 rows, row scale): k_bdown_hot_s,
 //                 k_bdown_hot, k_pgemm_down_hot
 //            cold H_cold D_cold: k_pgemm_down_cold for every M, the records'
 //                 down nibbles transposed into a decoded LDS tile
 //   k_bfinal out = x + Y (fp16), y32 = Y
-// Summation order across workgroups follows the atomics, so repeated runs
-// can differ in the last bits (well inside the FFN tolerance).
+// Up to 16 tokens, the cold down stores one partial sum per item range and
+// the last kernel (k_bdown_hot_s, or k_bfinal without hot rows) adds them in
+// range order to the hot product: the result is the same on every run.  With
+// more tokens the down kernels accumulate Y with fp32 atomics after the
+// first writer, so the summation order follows the workgroups' timing and
+// repeated runs can differ in the last bits (well inside the FFN tolerance).
 // fp8 and INT4 weights convert to fp16 exactly.  The small-batch gate/up
 // kernels apply INT4 group scales (one per 128 K) to each block's fp32
 // partial sums, exact up to accumulation; the prefill gate/up and every cold
@@ -683,9 +687,14 @@ __device__ __forceinline__ void nibble_transpose8(uint32_t (&r)[8]) {
   }
 }
 
+// Workgroup = 256 outputs x 32 MS tokens x one range of K blocks (items).
+// PART (at most 16 tokens): the range's sum goes to a.part[split] as
+// (H, 16) fp32, an empty range storing zeros; otherwise it is added into y.
+template <int MS, bool PART>
 __global__ __launch_bounds__(kThreads) void k_pgemm_down_cold(BDownArgs a, int mt, int splits) {
-  constexpr int MS = 4, NB = 2;
-  constexpr int kT = 256 * kLdC, kA = 128 * kLdC;   // halves per buffer
+  constexpr int NB = 2;
+  constexpr int kT = 256 * kLdC, kA = 32 * MS * kLdC;   // halves per buffer
+  static_assert(!PART || MS == 1, "partial sums hold 16 tokens");
   __shared__ __attribute__((aligned(16))) uint16_t sT[2 * kT];
   __shared__ __attribute__((aligned(16))) uint16_t sH[2 * kA];
   __shared__ uint32_t s_rec[kDcMaxItems];
@@ -697,9 +706,16 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_down_cold(BDownArgs a, int m
   const int total = min(*a.total, a.cap);
   const int n_blk = (total + kDcItems - 1) / kDcItems;
   const int kb0 = split * n_blk / splits, kb1 = (split + 1) * n_blk / splits;
-  if (kb0 >= kb1) return;   // the whole workgroup
   const int t = threadIdx.x, w = t >> 6, l = lane_id();
-  const int m0 = mtile * 128, j0 = jt * 256;
+  const int m0 = mtile * 32 * MS, j0 = jt * 256;
+  if (kb0 >= kb1) {   // the whole workgroup
+    if (PART) {
+      f32x4* dst = reinterpret_cast<f32x4*>(a.part + ((size_t)split * kH + j0 + t) * 16);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dst[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    return;
+  }
   const int i_base = kb0 * kDcItems, n_items = (kb1 - kb0) * kDcItems;
 
   // record offsets of the range (items past the list or with invalid slots
@@ -717,13 +733,13 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_down_cold(BDownArgs a, int m
   const uint32_t dbyte = kOffDown + (j0 + 8 * jg) / 2;                        // this thread's dword
   const uint32_t sbyte = kOffScales + 2 * (2 * kGroups + (j0 + 8 * jg) / kGroup);  // its down scale
   // H tile: thread t loads chunk t & 7 (8 items) of token rows t / 8 + 32 r
-  uint32_t hoff[4];
+  uint32_t hoff[MS];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) hoff[r] = ((uint32_t)(m0 + (t >> 3) + 32 * r) * a.ldc + 8 * (t & 7)) * 2;
+  for (int r = 0; r < MS; ++r) hoff[r] = ((uint32_t)(m0 + (t >> 3) + 32 * r) * a.ldc + 8 * (t & 7)) * 2;
 
   uint32_t dq[8];
   uint16_t dsc[8];
-  u32x4 hv[4];
+  u32x4 hv[MS];
   int hkb = kb0;   // block held in dq / dsc / hv
   auto load_block = [&](int kb) {
     hkb = kb;
@@ -735,7 +751,7 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_down_cold(BDownArgs a, int m
       dsc[k] = bload2(rr, vr + sbyte, 0);
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) hv[r] = bload16(rh, hoff[r], kb * kDcItems * 2);
+    for (int r = 0; r < MS; ++r) hv[r] = bload16(rh, hoff[r], kb * kDcItems * 2);
   };
   // decode the loaded block into buffer `buf`
   auto store_block = [&](int buf) {
@@ -767,7 +783,7 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_down_cold(BDownArgs a, int m
     for (int d = 0; d < 4; ++d)
       km[d] = (2 * d < keep ? 0x0000FFFFu : 0u) | (2 * d + 1 < keep ? 0xFFFF0000u : 0u);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < MS; ++r) {
       const uint32_t d0 = hv[r].x & km[0], d1 = hv[r].y & km[1], d2 = hv[r].z & km[2], d3 = hv[r].w & km[3];
       u32x4 v;
       v.x = (d0 & 0xFFFFu) | (d2 << 16);
@@ -809,6 +825,18 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_down_cold(BDownArgs a, int m
     __builtin_amdgcn_sched_barrier(0);
     store_block(cur ^ 1);
     lds_barrier();
+  }
+  if (PART) {
+    // rows 0..15 of the 32x32 tile: elements 0..7, four consecutive rows each
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      float* dst = a.part + ((size_t)split * kH + j0 + 64 * w + 32 * nb + (l & 31)) * 16 + 4 * (l >> 5);
+#pragma unroll
+      for (int g = 0; g < 2; ++g)
+        *reinterpret_cast<f32x4*>(dst + 8 * g) =
+            f32x4{acc[0][nb][4 * g], acc[0][nb][4 * g + 1], acc[0][nb][4 * g + 2], acc[0][nb][4 * g + 3]};
+    }
+    return;
   }
 #pragma unroll
   for (int ms = 0; ms < MS; ++ms)
@@ -1246,8 +1274,32 @@ __global__ __launch_bounds__(kThreads) void k_bdown_hot_s(BDownArgs a) {
   static_assert(MS == 1, "at most 16 tokens");
   constexpr int NBmax = 8;   // ldh <= 4096: at most 32 blocks, 8 per wave
   __shared__ f32x4 s_red[3][MS][kWave];
-  const int w = threadIdx.x >> 6, l = lane_id();
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = lane_id();
   const int h = blockIdx.x * 16 + (l & 15);
+  // the epilogue's inputs (wave 0: output h, tokens 4 (l >> 4) + e): the cold
+  // ranges' partial sums added in range order, the row scale, the residual
+  f32x4 yc = {0.f, 0.f, 0.f, 0.f};
+  float sd = 0.f, rv[4] = {0.f, 0.f, 0.f, 0.f};
+  if (w == 0) {
+    // 16 ranges' loads in flight at a time, then their sums in range order
+    const f32x4* pp = reinterpret_cast<const f32x4*>(a.part + (size_t)h * 16 + 4 * (l >> 4));
+    for (int s0 = 0; s0 < a.n_part; s0 += 16) {
+      f32x4 pv[16];
+#pragma unroll
+      for (int u = 0; u < 16; ++u)
+        pv[u] = s0 + u < a.n_part ? pp[(size_t)(s0 + u) * kH * 4] : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int u = 0; u < 16; ++u) yc += pv[u];
+    }
+    sd = a.down_s[h];
+    if (a.res) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int t = 4 * (l >> 4) + e;
+        if (t < a.M) rv[e] = half_bits_to_float(a.res[(size_t)t * kH + h]);
+      }
+    }
+  }
   const int nb = a.hot_blocks;
   const int b0 = w * nb / 4, b1 = (w + 1) * nb / 4;
   const int m = l & 15;
@@ -1282,19 +1334,15 @@ __global__ __launch_bounds__(kThreads) void k_bdown_hot_s(BDownArgs a) {
   if (w > 0) s_red[w - 1][0][l] = acc;
   __syncthreads();
   if (w != 0) return;
-  const float sd = a.down_s[h];
   const f32x4 v = acc + s_red[0][0][l] + s_red[1][0][l] + s_red[2][0][l];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const int t = 4 * (l >> 4) + e;
     if (t >= a.M) continue;
     const size_t i = (size_t)t * kH + h;
-    const float y = a.y[i] + v[e] * sd;
+    const float y = yc[e] + v[e] * sd;
     if (a.y32) a.y32[i] = y;
-    if (a.out) {
-      const float r = a.res ? half_bits_to_float(a.res[i]) : 0.f;
-      a.out[i] = float_to_half_bits(r + y);
-    }
+    if (a.out) a.out[i] = float_to_half_bits(rv[e] + y);
   }
 }
 
@@ -1348,11 +1396,23 @@ __global__ __launch_bounds__(kThreads) void k_bfill(float* y, int n4) {
 }
 
 // out = res + y (fp16), y32 = y.
-__global__ __launch_bounds__(kThreads) void k_bfinal(const float* yacc, int M, const uint16_t* res,
-                                                    uint16_t* out, float* y32) {
+// Y from yacc (M, H), or, with n_part > 0, the sum in range order of the
+// cold ranges' partial sums part[s] (H, 16).
+__global__ __launch_bounds__(kThreads) void k_bfinal(const float* yacc, const float* part, int n_part, int M,
+                                                    const uint16_t* res, uint16_t* out, float* y32) {
   const int n4 = M * (kH / 4);
   for (int q = blockIdx.x * kThreads + threadIdx.x; q < n4; q += gridDim.x * kThreads) {
-    const f32x4 y = reinterpret_cast<const f32x4*>(yacc)[q];
+    f32x4 y = {0.f, 0.f, 0.f, 0.f};
+    if (n_part > 0) {
+      const int m = q / (kH / 4), j = 4 * (q % (kH / 4));
+      for (int sp = 0; sp < n_part; ++sp) {
+        const float* pp = part + ((size_t)sp * kH + j) * 16 + m;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) y[c] += pp[16 * c];
+      }
+    } else {
+      y = reinterpret_cast<const f32x4*>(yacc)[q];
+    }
     if (y32) reinterpret_cast<f32x4*>(y32)[q] = y;
     if (out) {
       float r[4] = {0.f, 0.f, 0.f, 0.f};
@@ -1392,7 +1452,8 @@ struct BatchPlan {
   int M, Mpad, mt, ldh, hot_blocks, cap, ldc, hot_splits, ksplit;
   bool prefill;
   int pms, pmt;   // prefill tiles: 32-token subtiles per tile, token tiles
-  size_t off_xn, off_hh, off_hc, off_dslots, off_total, off_y, off_pg, off_pu, bytes;
+  int cold_splits;   // at most 16 tokens: the cold down's item ranges
+  size_t off_xn, off_hh, off_hc, off_dslots, off_total, off_y, off_pg, off_pu, off_part, bytes;
 };
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -1401,6 +1462,16 @@ constexpr int kSkinnyMax = 16;    // token counts up to this use the one-tile sp
 constexpr int kPrefillMin = 192;  // token counts from this use the 128-row tile kernels
 
 static int prefill_ms(int M) { return M >= 384 ? 4 : 2; }   // 32-token subtiles per tile
+
+// Cold down grid: 16 output tiles x token tiles (32 tokens up to 16 tokens,
+// else 128) x item ranges, about 256 workgroups; a range holds at most
+// kDcMaxItems items.
+static int cold_down_splits(int M, int cap) {
+  const int mtc = M <= kSkinnyMax ? 1 : (M + 127) / 128;
+  const int n_blk = (cap + kDcItems - 1) / kDcItems;
+  const int min_splits = (n_blk + kDcMaxItems / kDcItems - 1) / (kDcMaxItems / kDcItems);
+  return std::max(min_splits, std::min(n_blk, std::max(1, 256 / (16 * mtc))));
+}
 
 static BatchPlan batch_plan(int M, int n_hot, int cap) {
   BatchPlan p{};
@@ -1440,20 +1511,14 @@ static BatchPlan batch_plan(int M, int n_hot, int cap) {
   o = align256(o + part);
   p.off_pu = o;
   o = align256(o + part);
+  p.cold_splits = (M <= kSkinnyMax && cap > 0) ? cold_down_splits(M, cap) : 0;
+  p.off_part = o;
+  o = align256(o + (size_t)p.cold_splits * kH * 16 * 4);
   p.bytes = o;
   return p;
 }
 
 size_t batch_ws_bytes(int M, int n_hot, int cap) { return batch_plan(M, n_hot, cap).bytes; }
-
-// Cold down grid: 16 output tiles x 128-token tiles x item ranges, about 256
-// workgroups; a range holds at most kDcMaxItems items.
-static int cold_down_splits(int M, int cap) {
-  const int mtc = (M + 127) / 128;
-  const int n_blk = (cap + kDcItems - 1) / kDcItems;
-  const int min_splits = (n_blk + kDcMaxItems / kDcItems - 1) / (kDcMaxItems / kDcItems);
-  return std::max(min_splits, std::min(n_blk, std::max(1, 256 / (16 * mtc))));
-}
 
 static void launch_skinny(const BUpArgs& ua, const BDownArgs& da, bool up, const uint16_t* x,
                           const uint16_t* norm_w, float eps, hipStream_t st) {
@@ -1554,21 +1619,22 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
   da.y = y;
 
   if (skinny) {
-    // gate/up (clearing y on the way), the cold down adding into y, then
-    // the hot down, which adds its product and writes the outputs
+    // gate/up, the cold down's partial sums per item range, then the hot
+    // down, which adds them to its product and writes the outputs
     const int n4 = M * (kH / 4);
     const int grid = std::min(2048, (n4 + kThreads - 1) / kThreads);
     if (p.ldh + p.ldc > 0) {
-      ua.yzero = y;
-      ua.yzero_n4 = n4;
       launch_skinny(ua, da, true, x, norm_w, eps, st);
     } else {
       hipLaunchKernelGGL(k_bfill, dim3(grid), dim3(kThreads), 0, st, y, n4);
     }
     OI2_CHECK_LAUNCH();
+    float* part = reinterpret_cast<float*>(ws + p.off_part);
     if (has_cold) {
-      const int splits = cold_down_splits(M, cap);
-      hipLaunchKernelGGL(k_pgemm_down_cold, dim3(16 * splits), dim3(kThreads), 0, st, da, 1, splits);
+      da.part = part;
+      da.n_part = p.cold_splits;
+      hipLaunchKernelGGL((k_pgemm_down_cold<1, true>), dim3(16 * p.cold_splits), dim3(kThreads), 0, st, da, 1,
+                         p.cold_splits);
       OI2_CHECK_LAUNCH();
     }
     if (n_hot) {
@@ -1577,8 +1643,8 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
       da.y32 = y32;
       launch_skinny(ua, da, false, x, norm_w, eps, st);
     } else {
-      hipLaunchKernelGGL(k_bfinal, dim3(grid), dim3(kThreads), 0, st, y, M, add_residual ? x : nullptr,
-                         out, y32);
+      hipLaunchKernelGGL(k_bfinal, dim3(grid), dim3(kThreads), 0, st, y, has_cold ? part : nullptr,
+                         has_cold ? p.cold_splits : 0, M, add_residual ? x : nullptr, out, y32);
     }
     OI2_CHECK_LAUNCH();
     return OI2_OK;
@@ -1627,10 +1693,11 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
   if (has_cold) {
     const int mtc = (M + 127) / 128;
     const int splits = cold_down_splits(M, cap);
-    hipLaunchKernelGGL(k_pgemm_down_cold, dim3(16 * mtc * splits), dim3(kThreads), 0, st, da, mtc, splits);
+    hipLaunchKernelGGL((k_pgemm_down_cold<4, false>), dim3(16 * mtc * splits), dim3(kThreads), 0, st, da, mtc,
+                       splits);
     OI2_CHECK_LAUNCH();
   }
-  hipLaunchKernelGGL(k_bfinal, dim3(grid), dim3(kThreads), 0, st, y, M, add_residual ? x : nullptr,
+  hipLaunchKernelGGL(k_bfinal, dim3(grid), dim3(kThreads), 0, st, y, nullptr, 0, M, add_residual ? x : nullptr,
                      out, y32);
   OI2_CHECK_LAUNCH();
   return OI2_OK;

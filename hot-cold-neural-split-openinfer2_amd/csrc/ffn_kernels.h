@@ -199,9 +199,12 @@ struct BDownArgs {
   const int32_t* total;
   int cap;
   float* y;                 // (M, H) fp32 output, accumulated with atomics
-  // k_bdown_hot_s, the last of the small-batch kernels: y (the cold part,
-  // or zero) plus the hot product -> out = fp16(res + y) (res may be null),
-  // and y32 = y when asked
+  // at most 16 tokens: the cold down's partial sums, n_part item ranges of
+  // (H, 16) fp32; k_bdown_hot_s, the last of the small-batch kernels, adds
+  // them in range order to the hot product -> out = fp16(res + y) (res may
+  // be null), and y32 = y when asked
+  float* part;
+  int n_part;
   const uint16_t* res;
   uint16_t* out;
   float* y32;

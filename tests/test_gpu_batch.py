@@ -201,3 +201,32 @@ def test_batch_ignores_workspace_contents(dev, layer25, B):
     assert np.isfinite(outs[0]).all()
     assert_ffn_close(outs[0].reshape(-1), outs[1].reshape(-1), tol=1e-5, cos_min=0.999999,
                      what=f"B={B} NaN-filled vs zeroed workspace")
+
+
+@pytest.mark.parametrize("B", [2, 8, 16])
+def test_small_batch_is_bit_reproducible(dev, layer25, B):
+    """Up to 16 tokens no kernel accumulates with atomics: the cold down's
+    item ranges are added in range order, so repeated calls (the workspace
+    NaN-filled in between, and only the hot half or only the cold half too)
+    give the same bits."""
+    from oi2.layer import workspace_bytes
+    lay, g = layer25
+    n_cold = lay.records.shape[0]
+    slots = torch.randperm(n_cold, generator=g, device=dev)[:1613].int()
+    cold = ColdNeurons.from_slots(_section(lay), slots)
+    x = torch.randn((B, H), generator=g, device=dev).half()
+    for hot, cd, what in ((lay.hot, cold, "hot + cold"), (None, cold, "cold only"), (lay.hot, None, "hot only")):
+        nbytes = workspace_bytes(B, hot, cd)
+        runs = []
+        for fill in (0xFF, 0x00, 0x5A):
+            ws = torch.full((nbytes,), fill, dtype=torch.uint8, device=dev)
+            out, y32 = _ffn(x, lay.norm_w, EPS, hot, cd, "silu", False, True, want_y32=True, workspace=ws)
+            runs.append((out.clone(), y32.clone()))
+        torch.cuda.synchronize()
+        print(f"[batch] B={B} {what}: {len(runs)} runs", flush=True)
+        for out, y32 in runs[1:]:
+            assert torch.equal(out, runs[0][0]) and torch.equal(y32, runs[0][1]), f"B={B} {what}"
+        if hot is None:
+            Gc, Uc, Dc = cold_dense(lay.records, slots)
+            ref = O.sparse_ffn(normed_f16(x, lay.norm_w), "silu", False, None, None, None, Gc, Uc, Dc)
+            assert_ffn_close(runs[0][1].cpu().numpy(), ref, what=f"B={B} cold only against the oracle")
