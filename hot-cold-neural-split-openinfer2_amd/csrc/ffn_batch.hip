@@ -1022,138 +1022,143 @@ __global__ __launch_bounds__(kThreads) void k_bup_s(BUpArgs a) {
 
 // ── gate/up for at most 16 tokens, RMSNorm fused ─────────────────────────────
 
-// Workgroup = 16 weight rows (items of the dense active list in the first
-// ldc / 16 workgroups, then hot rows); wave w takes K [1024 w, 1024 w + 1024).
-// The workgroup first normalises
-// the M <= MMAX token rows itself (x_n = fp16((x r) w), the rounding of
-// nn.RMSNorm's fp16 output) into LDS, every weight load of the first half of
-// its K range already in flight, so no operand of the MFMA loop is read from
-// global memory after the prologue.
-// Hot rows: lane (t, q) = (l & 15, l >> 4) loads 16 bytes of row r0 + t at
-// K 1024 w + 64 c + 16 q, the B operand of two 16x16x32 steps (K + 8 s,
-// s < 2); the A operand of the same steps is token t's x_n at the same K.
+constexpr int kSbGroups = 256;      // workgroups: one per CU
+constexpr int kSbThreads = 512;     // 8 waves; wave w takes K [512 w, 512 w + 512)
+
+// Workgroup g takes hot rows [g hr, g hr + hr) (hr = a.hot_per_wg, tiles of
+// 16 rows) and items g, g + 256, g + 512, ... of the dense active list
+// (tiles of 16), so every CU reads about the same number of weight lines.
+// It first normalises the M <= MMAX token rows itself (x_n = fp16((x r) w),
+// the rounding of nn.RMSNorm's fp16 output) into LDS: the two halves of the
+// workgroup take alternate rows, thread e of a half holds elements
+// [16 e, 16 e + 16) of them.  The first hot tile's weight loads and the first
+// cold tile's record loads are in flight by then.
+// Hot rows: lane (t, q) = (l & 15, l >> 4) loads 16 bytes of row t at K
+// 512 w + 64 c + 16 q, the B operand of two 16x16x32 steps (K + 8 s, s < 2);
+// the A operand of the same steps is token t's x_n at the same K.
 // Cold items: the lane's 16 bytes are 32 nibbles of item t at K
-// 1024 w + 128 b + 32 q (four steps, decoded in int4x8_h8's order, the A
+// 512 w + 128 b + 32 q (four steps, decoded in int4x8_h8's order, the A
 // operand permuted to match); the group scale multiplies each 128-K block's
-// partial sums.
+// partial sums.  The 8 waves' sums of a tile meet in LDS and are added in
+// wave order.
 template <int MMAX>
-__global__ __launch_bounds__(kThreads) void k_sbup(BUpArgs a, const uint16_t* x, const uint16_t* norm_w,
-                                                   float eps) {
-  constexpr int kLdX = kH + 8;          // halves per staged row: 8208 bytes, rows on distinct banks
-  constexpr int kScr = MMAX * kThreads > 3 * 2 * kWave * 4 ? MMAX * kThreads : 3 * 2 * kWave * 4;
-  // with at most 8 token rows every weight load of the workgroup goes out
-  // before the prologue; with 16 the second half waits for it (registers)
-  constexpr bool kAllUpFront = MMAX <= 8;
+__global__ __launch_bounds__(kSbThreads) void k_sbup(BUpArgs a, const uint16_t* x, const uint16_t* norm_w,
+                                                     float eps) {
+  constexpr int kLdX = kH + 8;          // halves per staged row: rows on distinct banks
+  constexpr int kRows = MMAX / 2;       // token rows per half of the workgroup
+  constexpr int kRed = 7 * 4 * kWave * 4;   // the first hot and cold tiles' wave sums
+  constexpr int kScr = MMAX * 256 > kRed ? MMAX * 256 : kRed;
   __shared__ __attribute__((aligned(16))) uint16_t s_x[MMAX * kLdX];
   __shared__ __attribute__((aligned(16))) float s_scr[kScr];   // norm partials, then the wave sums
-  // the wave index as a scalar: the weight loads' K offsets then go in the
-  // buffer instructions' scalar offset operand (a per-lane value there would
-  // make the compiler wrap every load in a loop over distinct values)
-  const int tid = threadIdx.x, w = __builtin_amdgcn_readfirstlane(tid >> 6), l = lane_id();
+  const int tid = threadIdx.x, l = lane_id();
+  // the wave index as a scalar, so that K offsets go in the buffer
+  // instructions' scalar offset operand
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int t = l & 15, q = l >> 4;
   const int M = a.M;
-  // the cold workgroups come first in dispatch order: their loads depend on
-  // the list, and behind the hot rows' weight traffic they would start last
-  const int cold_wg = a.ldc / 16;
-  const bool hot = (int)blockIdx.x >= cold_wg;
-  const int kq = 1024 * w;
-  // the down kernels that follow add into y: cleared here, a slice per
-  // workgroup, before any workgroup may leave early
-  for (int i = (int)blockIdx.x * kThreads + tid; i < a.yzero_n4; i += (int)gridDim.x * kThreads)
-    reinterpret_cast<f32x4*>(a.yzero)[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  int col, slot = -1;
-  bool cv = false;
-  const int i0 = (int)blockIdx.x * 16;
-  int raw_total = 0, raw_slot = -1;
-  if (hot) {
-    col = ((int)blockIdx.x - cold_wg) * 16 + t;
-    cv = col < a.n_hot;
-  } else {
-    col = i0 + t;
-    raw_total = *a.total;
-    raw_slot = a.dslots[min(col, a.cap - 1)];
-  }
-  // the token rows next (L2-resident, needed by the prologue; a cold
-  // workgroup's go out with its list loads, before it waits on them), then
-  // the weights: a wave's loads complete in order
-  u32x4 xin[MMAX][2];
+  const int g = blockIdx.x;
+  const int hr = a.hot_per_wg;
+  const int n_ht = (hr + 15) / 16;
+  const int hot0 = g * hr;
+  // Every load below is unconditional (absent data reads zero through a
+  // short or empty descriptor), so the compiler issues them back to back and
+  // waits for exactly the ones each step uses.  A wave's loads complete in
+  // order: the token rows first (the prologue waits on them), then the list
+  // (the first cold tile's loads wait on it), then the weights.
+  // This thread's token rows (half hf, rows 2 k + hf; rows past M read zero)
+  // and norm weights:
+  const int hf = tid >> 8, e16 = tid & 255;
+  const rsrc_t rx = buf_rsrc(x, (uint32_t)M * kH * 2);
+  const rsrc_t rw = buf_rsrc(norm_w, norm_w ? (uint32_t)kH * 2 : 0u);
+  u32x4 xin[kRows][2];
 #pragma unroll
-  for (int m = 0; m < MMAX; ++m) {
-    if (m < M) {
-      const u32x4* px = reinterpret_cast<const u32x4*>(x + (size_t)m * kH) + 2 * tid;
-      xin[m][0] = px[0];
-      xin[m][1] = px[1];
-    }
+  for (int k = 0; k < kRows; ++k) {
+    const uint32_t off = ((uint32_t)(2 * k + hf) * kH + 16 * e16) * 2;
+    xin[k][0] = bload16(rx, off, 0);
+    xin[k][1] = bload16(rx, off, 16);
   }
-  u32x4 wn[2] = {u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}};
-  if (norm_w) {
-    wn[0] = reinterpret_cast<const u32x4*>(norm_w)[2 * tid];
-    wn[1] = reinterpret_cast<const u32x4*>(norm_w)[2 * tid + 1];
-  }
-  if (!hot) {
-    const int total = min(raw_total, a.cap);
-    if (i0 >= total) return;   // the whole workgroup
-    slot = col < total ? raw_slot : -1;
-    cv = slot >= 0 && slot < a.n_records;
-  }
+  u32x4 wn[2];
+  wn[0] = bload16(rw, 32 * e16, 0);
+  wn[1] = bload16(rw, 32 * e16, 16);
+  // lane t's item of tile 0 is g + 256 t
+  const bool list = a.ldc > 0;
+  const rsrc_t rlt = buf_rsrc(a.total, list ? 4u : 0u);
+  const rsrc_t rls = buf_rsrc(a.dslots, list ? (uint32_t)a.cap * 4 : 0u);
+  int raw_total = (int)__builtin_amdgcn_raw_buffer_load_b32(rlt, 0, 0, 0);
+  int raw_slot = (int)__builtin_amdgcn_raw_buffer_load_b32(rls, 4 * (g + kSbGroups * t), 0, 0);
   __builtin_amdgcn_sched_barrier(0);
-  u32x4 WG[16], WU[16];                 // hot: chunks c; cold: blocks 0..7 in WG/WU[0..7]
-  u32x4 SC[2] = {u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}};
+  const int kq = 512 * w;
   const rsrc_t rg = buf_rsrc(a.gate_q, (uint32_t)a.n_hot * kH);
   const rsrc_t ru = buf_rsrc(a.up_q, (uint32_t)a.n_hot * kH);
-  const uint32_t voff = (uint32_t)col * kH + 16 * q;   // rows past n_hot read zero
   const rsrc_t rr = buf_rsrc(a.records, (uint32_t)a.n_records * kRecBytes);
-  const uint32_t ro = cv ? (uint32_t)slot * kRecBytes : kNoOffset;
-  // the weight loads of this wave, in issue order: hot chunks c (gate and
-  // up), or cold blocks b and the scales; `issue(i0, i1)` sends loads
-  // [i0, i1) of that order, so the loads can be spread over the prologue's
-  // VALU work (a wave stalls at a load once the CU's memory queue is full)
-  const int n_loads = hot ? (kAllUpFront ? 16 : 8) : 9;
-  auto issue = [&](int i0, int i1) {
+  const rsrc_t rgs = buf_rsrc(a.gate_s, (uint32_t)a.n_hot * 4);
+  const rsrc_t rus = buf_rsrc(a.up_s, (uint32_t)a.n_hot * 4);
+  const rsrc_t rhb = buf_rsrc(a.hot_gbias, a.hot_gbias ? (uint32_t)a.n_hot * 4 : 0u);
+  const rsrc_t rcb = buf_rsrc(a.cold_gbias, a.cold_gbias ? (uint32_t)a.n_records * 4 : 0u);
+  u32x4 WG[8], WU[8];                   // one hot tile's chunks
+  float hsg, hsu, hgb;                  // and its row scales and gate bias (zero past the rows)
+  auto hot_issue = [&](int ti) {
+    const int r = 16 * ti + t, col = hot0 + r;
+    // rows past this workgroup's share or past n_hot read zero
+    const bool in = r < hr && col < a.n_hot;
+    const uint32_t voff = in ? (uint32_t)col * kH + 16 * q : kNoOffset;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      if (i < i0 || i >= i1 || i >= n_loads) continue;
-      if (hot) {
-        WG[i] = bload16(rg, voff, kq + 64 * i);
-        WU[i] = bload16(ru, voff, kq + 64 * i);
-      } else if (i < 8) {
-        WG[i] = bload16(rr, ro + kOffGate + 16 * q, 512 * w + 64 * i);
-        WU[i] = bload16(rr, ro + kOffUp + 16 * q, 512 * w + 64 * i);
-      } else {
-        // the quarter's 8 group scales of each vector (16 bytes at 2 mod 16)
-        SC[0] = bload16(rr, ro + kOffScales, 16 * w);
-        SC[1] = bload16(rr, ro + kOffScales + 2 * kGroups, 16 * w);
-      }
+    for (int c = 0; c < 8; ++c) {
+      WG[c] = bload16(rg, voff, kq + 64 * c);
+      WU[c] = bload16(ru, voff, kq + 64 * c);
     }
+    const uint32_t soff = in ? (uint32_t)col * 4 : kNoOffset;
+    hsg = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rgs, soff, 0, 0));
+    hsu = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rus, soff, 0, 0));
+    hgb = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rhb, soff, 0, 0));
   };
-  issue(0, 4);
-
-  // prologue: the token rows into LDS (thread tid holds elements
-  // [16 tid, 16 tid + 16) of each row) with their sum-of-squares partials,
-  // then x_n in place; the remaining weight loads go out between its rows
+  u32x4 CG[4], CU[4], SC[2];            // one cold tile's blocks and group scales
+  float cgb;                            // and its items' gate bias
+  auto cold_issue = [&](int slot) {
+    const bool in = slot >= 0 && slot < a.n_records;
+    const uint32_t ro = in ? (uint32_t)slot * kRecBytes : kNoOffset;
 #pragma unroll
-  for (int m = 0; m < MMAX; ++m) {
-    if (m >= M) break;
-    u32x4* sx = reinterpret_cast<u32x4*>(s_x + m * kLdX + 16 * tid);
-    sx[0] = xin[m][0];
-    sx[1] = xin[m][1];
-    if (norm_w) {
+    for (int b = 0; b < 4; ++b) {
+      CG[b] = bload16(rr, ro + kOffGate + 16 * q, 256 * w + 64 * b);
+      CU[b] = bload16(rr, ro + kOffUp + 16 * q, 256 * w + 64 * b);
+    }
+    // the 8 group scales around the wave's 4 (16 bytes at 2 mod 16)
+    SC[0] = bload16(rr, ro + kOffScales, 16 * (w >> 1));
+    SC[1] = bload16(rr, ro + kOffScales + 2 * kGroups, 16 * (w >> 1));
+    cgb = __builtin_bit_cast(float,
+                             __builtin_amdgcn_raw_buffer_load_b32(rcb, in ? (uint32_t)slot * 4 : kNoOffset, 0, 0));
+  };
+  // the first tiles' loads go out unconditionally (a missing tile reads
+  // zero): with the same loads on every path the compiler can wait for the
+  // token rows alone in the prologue
+  hot_issue(0);
+  __builtin_amdgcn_sched_barrier(0);
+  // the list's values are first used here (not earlier: the hot loads would
+  // then wait for them)
+  asm volatile("" : "+v"(raw_total), "+v"(raw_slot));
+  const int total = list ? min(raw_total, a.cap) : 0;
+  const int n_items = total > g ? (total - g + kSbGroups - 1) / kSbGroups : 0;   // this workgroup's
+  const int n_ct = (n_items + 15) / 16;
+  int slot = list && g + kSbGroups * t < total ? raw_slot : -1;
+  cold_issue(slot);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // prologue: sum-of-squares partials of this thread's rows, then x_n (rows
+  // past M come out zero and are never read)
+  if (norm_w) {
+#pragma unroll
+    for (int k = 0; k < kRows; ++k) {
+      const int m = 2 * k + hf;
       float v[16];
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
-        v[2 * d] = half_bits_to_float((uint16_t)(xin[m][0][d] & 0xFFFFu));
-        v[2 * d + 1] = half_bits_to_float((uint16_t)(xin[m][0][d] >> 16));
-        v[8 + 2 * d] = half_bits_to_float((uint16_t)(xin[m][1][d] & 0xFFFFu));
-        v[8 + 2 * d + 1] = half_bits_to_float((uint16_t)(xin[m][1][d] >> 16));
+        v[2 * d] = half_bits_to_float((uint16_t)(xin[k][0][d] & 0xFFFFu));
+        v[2 * d + 1] = half_bits_to_float((uint16_t)(xin[k][0][d] >> 16));
+        v[8 + 2 * d] = half_bits_to_float((uint16_t)(xin[k][1][d] & 0xFFFFu));
+        v[8 + 2 * d + 1] = half_bits_to_float((uint16_t)(xin[k][1][d] >> 16));
       }
-      float ss = 0.0f;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) ss = fmaf(v[e], v[e], ss);
-      s_scr[m * kThreads + tid] = ss;
+      s_scr[m * 256 + e16] = ssq16(v);
     }
-  }
-  if (norm_w) {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
     float wf[16];
 #pragma unroll
@@ -1164,100 +1169,153 @@ __global__ __launch_bounds__(kThreads) void k_sbup(BUpArgs a, const uint16_t* x,
       wf[8 + 2 * d + 1] = half_bits_to_float((uint16_t)(wn[1][d] >> 16));
     }
 #pragma unroll
-    for (int m = 0; m < MMAX; ++m) {
-      if (m >= M) break;
-      issue(4 + 2 * m, 6 + 2 * m);
+    for (int k = 0; k < kRows; ++k) {
+      const int m = 2 * k + hf;
       // the canonical factor: lane l sums partials 4 l .. 4 l + 3, then a DPP tree
-      const f32x4 pp = reinterpret_cast<const f32x4*>(s_scr + m * kThreads)[l];
-      const float rr = rsqrtf(wave_sum((pp.x + pp.y) + (pp.z + pp.w)) * (1.0f / kH) + eps);
-      u32x4 v0 = xin[m][0], v1 = xin[m][1];
+      const f32x4 pp = reinterpret_cast<const f32x4*>(s_scr + m * 256)[l];
+      const float rn = rsqrtf(wave_sum((pp.x + pp.y) + (pp.z + pp.w)) * (1.0f / kH) + eps);
+      u32x4 v0 = xin[k][0], v1 = xin[k][1];
 #pragma unroll
       for (int d = 0; d < 4; ++d) {
-        const float e0 = xn_exact(half_bits_to_float((uint16_t)(v0[d] & 0xFFFFu)), rr, wf[2 * d]);
-        const float e1 = xn_exact(half_bits_to_float((uint16_t)(v0[d] >> 16)), rr, wf[2 * d + 1]);
-        const float e2 = xn_exact(half_bits_to_float((uint16_t)(v1[d] & 0xFFFFu)), rr, wf[8 + 2 * d]);
-        const float e3 = xn_exact(half_bits_to_float((uint16_t)(v1[d] >> 16)), rr, wf[8 + 2 * d + 1]);
+        const float e0 = xn_exact(half_bits_to_float((uint16_t)(v0[d] & 0xFFFFu)), rn, wf[2 * d]);
+        const float e1 = xn_exact(half_bits_to_float((uint16_t)(v0[d] >> 16)), rn, wf[2 * d + 1]);
+        const float e2 = xn_exact(half_bits_to_float((uint16_t)(v1[d] & 0xFFFFu)), rn, wf[8 + 2 * d]);
+        const float e3 = xn_exact(half_bits_to_float((uint16_t)(v1[d] >> 16)), rn, wf[8 + 2 * d + 1]);
         v0[d] = (uint32_t)float_to_half_bits(e0) | ((uint32_t)float_to_half_bits(e1) << 16);
         v1[d] = (uint32_t)float_to_half_bits(e2) | ((uint32_t)float_to_half_bits(e3) << 16);
       }
-      u32x4* sx = reinterpret_cast<u32x4*>(s_x + m * kLdX + 16 * tid);
+      u32x4* sx = reinterpret_cast<u32x4*>(s_x + m * kLdX + 16 * e16);
       sx[0] = v0;
       sx[1] = v1;
     }
+  } else {
+#pragma unroll
+    for (int k = 0; k < kRows; ++k) {
+      const int m = 2 * k + hf;
+      u32x4* sx = reinterpret_cast<u32x4*>(s_x + m * kLdX + 16 * e16);
+      sx[0] = xin[k][0];
+      sx[1] = xin[k][1];
+    }
   }
-  issue(norm_w ? 4 + 2 * M : 4, 16);
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 
-  f32x4 accg = {0.f, 0.f, 0.f, 0.f}, accu = accg;
   const bool ta = t < M;                 // this lane's A row is a token
   const uint16_t* xa = s_x + t * kLdX + kq + 16 * q;   // hot: K kq + 64 c + 16 q + 8 s
   const uint16_t* xc = s_x + t * kLdX + kq + 32 * q;   // cold: K kq + 128 b + 32 q + 8 s
-  if (hot) {
-    if (!kAllUpFront) {
+  f32x4* s_red = reinterpret_cast<f32x4*>(s_scr);      // [7][4][kWave], later [7][2][kWave]
+  // one hot tile (rows t) and one cold tile (items t) of products
+  auto hot_mfma = [&](f32x4& accg, f32x4& accu) {
+    accg = f32x4{0.f, 0.f, 0.f, 0.f};
+    accu = accg;
 #pragma unroll
-      for (int c = 8; c < 16; ++c) {
-        WG[c] = bload16(rg, voff, kq + 64 * c);
-        WU[c] = bload16(ru, voff, kq + 64 * c);
-      }
-    }
-#pragma unroll
-    for (int c = 0; c < 16; ++c)
+    for (int c = 0; c < 8; ++c)
 #pragma unroll
       for (int st = 0; st < 2; ++st) {
         const h8 A = ta ? *reinterpret_cast<const h8*>(xa + 64 * c + 8 * st) : h8{};
         accg = mfma16(A, fp8x8_h8(WG[c][2 * st], WG[c][2 * st + 1]), accg);
         accu = mfma16(A, fp8x8_h8(WU[c][2 * st], WU[c][2 * st + 1]), accu);
       }
-  } else {
+  };
+  auto cold_mfma = [&](f32x4& accg, f32x4& accu) {
+    accg = f32x4{0.f, 0.f, 0.f, 0.f};
+    accu = accg;
 #pragma unroll
-    for (int b = 0; b < 8; ++b) {
+    for (int b = 0; b < 4; ++b) {
       f32x4 tg = {0.f, 0.f, 0.f, 0.f}, tu = tg;
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
         h8 A = ta ? *reinterpret_cast<const h8*>(xc + 128 * b + 8 * st) : h8{};
         A = __builtin_shufflevector(A, A, 0, 4, 1, 5, 2, 6, 3, 7);
-        tg = mfma16(A, int4x8_h8(WG[b][st]), tg);
-        tu = mfma16(A, int4x8_h8(WU[b][st]), tu);
+        tg = mfma16(A, int4x8_h8(CG[b][st]), tg);
+        tu = mfma16(A, int4x8_h8(CU[b][st]), tu);
       }
-      const uint32_t sg2 = SC[0][b >> 1], su2 = SC[1][b >> 1];
-      const float sg = half_bits_to_float((uint16_t)((b & 1) ? sg2 >> 16 : sg2 & 0xFFFFu));
-      const float su = half_bits_to_float((uint16_t)((b & 1) ? su2 >> 16 : su2 & 0xFFFFu));
+      // group 4 w + b of each vector: half (w & 1) of the 16 loaded bytes
+      const int gi = 4 * (w & 1) + b;
+      const uint32_t sg2 = SC[0][gi >> 1], su2 = SC[1][gi >> 1];
+      const float sg = half_bits_to_float((uint16_t)((gi & 1) ? sg2 >> 16 : sg2 & 0xFFFFu));
+      const float su = half_bits_to_float((uint16_t)((gi & 1) ? su2 >> 16 : su2 & 0xFFFFu));
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         accg[e] = fmaf(sg, tg[e], accg[e]);
         accu[e] = fmaf(su, tu[e], accu[e]);
       }
     }
-  }
-  // the four waves' sums meet in LDS (the norm partials are no longer read)
-  f32x4* s_red = reinterpret_cast<f32x4*>(s_scr);   // [3][2][kWave]
-  __syncthreads();
-  if (w > 0) {
-    s_red[((w - 1) * 2) * kWave + l] = accg;
-    s_red[((w - 1) * 2 + 1) * kWave + l] = accu;
-  }
-  __syncthreads();
-  if (w != 0) return;
+  };
+  // wave 0's epilogue of one tile: lane column `col` of hh or hc, the value
+  // if `valid`, zero if only `write`
+  auto store_tile = [&](f32x4 accg, f32x4 accu, bool hot, int col, bool valid, bool write, float sg,
+                        float su, float gb) {
+    if (!write) return;
+    uint16_t* dst = hot ? a.hh : a.hc;
+    const int ld = hot ? a.ldh : a.ldc;
 #pragma unroll
-  for (int v = 0; v < 3; ++v) {
-    accg += s_red[(v * 2) * kWave + l];
-    accu += s_red[(v * 2 + 1) * kWave + l];
-  }
-  float sg = 1.f, su = 1.f, gb = 0.f;
-  if (hot) {
-    sg = cv ? a.gate_s[col] : 0.f;
-    su = cv ? a.up_s[col] : 0.f;
-    gb = (cv && a.hot_gbias) ? a.hot_gbias[col] : 0.f;
-  } else {
-    gb = (cv && a.cold_gbias) ? a.cold_gbias[slot] : 0.f;
-  }
-  uint16_t* dst = hot ? a.hh : a.hc;
-  const int ld = hot ? a.ldh : a.ldc;
+    for (int e = 0; e < 4; ++e) {
+      const int m = 4 * q + e;
+      const float h = valid ? gated_act(fmaf(accg[e], sg, gb), accu[e] * su, a.relu, a.both) : 0.f;
+      dst[(size_t)m * ld + col] = float_to_half_bits(h);
+    }
+  };
+
+  // the first hot tile and the first cold tile share one exchange of the 8
+  // waves' sums through LDS; wave 0 adds them in wave order
+  {
+    f32x4 hg, hu, cg, cu;
+    hot_mfma(hg, hu);
+    cold_mfma(cg, cu);
+    __syncthreads();
+    if (w > 0) {
+      s_red[((w - 1) * 4) * kWave + l] = hg;
+      s_red[((w - 1) * 4 + 1) * kWave + l] = hu;
+      s_red[((w - 1) * 4 + 2) * kWave + l] = cg;
+      s_red[((w - 1) * 4 + 3) * kWave + l] = cu;
+    }
+    __syncthreads();
+    if (w == 0) {
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const int m = 4 * q + e;
-    const float h = cv ? gated_act(fmaf(accg[e], sg, gb), accu[e] * su, a.relu, a.both) : 0.f;
-    dst[(size_t)m * ld + col] = float_to_half_bits(h);
+      for (int v = 0; v < 7; ++v) {
+        hg += s_red[(v * 4) * kWave + l];
+        hu += s_red[(v * 4 + 1) * kWave + l];
+        cg += s_red[(v * 4 + 2) * kWave + l];
+        cu += s_red[(v * 4 + 3) * kWave + l];
+      }
+      const int col = hot0 + t;
+      store_tile(hg, hu, true, col, t < hr && col < a.n_hot, t < hr && col < a.ldh, hsg, hsu, hgb);
+      const int it = g + kSbGroups * t;
+      store_tile(cg, cu, false, it, it < total && slot >= 0 && slot < a.n_records, it < total, 1.f, 1.f, cgb);
+    }
+  }
+  // further tiles (more than 16 rows or items per workgroup), one exchange each
+  auto finish = [&](f32x4 accg, f32x4 accu, bool hot, int col, bool valid, bool write, float sg, float su,
+                    float gb) {
+    __syncthreads();
+    if (w > 0) {
+      s_red[((w - 1) * 2) * kWave + l] = accg;
+      s_red[((w - 1) * 2 + 1) * kWave + l] = accu;
+    }
+    __syncthreads();
+    if (w == 0) {
+#pragma unroll
+      for (int v = 0; v < 7; ++v) {
+        accg += s_red[(v * 2) * kWave + l];
+        accu += s_red[(v * 2 + 1) * kWave + l];
+      }
+      store_tile(accg, accu, hot, col, valid, write, sg, su, gb);
+    }
+  };
+  for (int ti = 1; ti < n_ht; ++ti) {
+    hot_issue(ti);
+    f32x4 accg, accu;
+    hot_mfma(accg, accu);
+    const int r = 16 * ti + t, col = hot0 + r;
+    finish(accg, accu, true, col, r < hr && col < a.n_hot, r < hr && col < a.ldh, hsg, hsu, hgb);
+  }
+  for (int ti = 1; ti < n_ct; ++ti) {
+    const int it = g + kSbGroups * (16 * ti + t);
+    slot = it < total ? a.dslots[it] : -1;
+    cold_issue(slot);
+    f32x4 accg, accu;
+    cold_mfma(accg, accu);
+    finish(accg, accu, false, it, it < total && slot >= 0 && slot < a.n_records, it < total, 1.f, 1.f, cgb);
   }
 }
 
@@ -1523,9 +1581,9 @@ size_t batch_ws_bytes(int M, int n_hot, int cap) { return batch_plan(M, n_hot, c
 static void launch_skinny(const BUpArgs& ua, const BDownArgs& da, bool up, const uint16_t* x,
                           const uint16_t* norm_w, float eps, hipStream_t st) {
   if (up && ua.M <= 8)
-    hipLaunchKernelGGL(k_sbup<8>, dim3(ua.hot_wg + ua.ldc / 16), dim3(kThreads), 0, st, ua, x, norm_w, eps);
+    hipLaunchKernelGGL(k_sbup<8>, dim3(kSbGroups), dim3(kSbThreads), 0, st, ua, x, norm_w, eps);
   else if (up)
-    hipLaunchKernelGGL(k_sbup<16>, dim3(ua.hot_wg + ua.ldc / 16), dim3(kThreads), 0, st, ua, x, norm_w, eps);
+    hipLaunchKernelGGL(k_sbup<16>, dim3(kSbGroups), dim3(kSbThreads), 0, st, ua, x, norm_w, eps);
   else
     hipLaunchKernelGGL(k_bdown_hot_s<1>, dim3(kH / 16), dim3(kThreads), 0, st, da);
 }
@@ -1581,6 +1639,7 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
   ua.hh = hh;
   ua.ldh = p.ldh;
   ua.hot_wg = skinny ? p.ldh / 16 : p.ldh / kBN;
+  ua.hot_per_wg = (n_hot + kSbGroups - 1) / kSbGroups;
   if (has_cold) {
     ua.records = cold->records;
     ua.n_records = cold->n_records;

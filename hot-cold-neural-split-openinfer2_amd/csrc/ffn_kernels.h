@@ -178,8 +178,7 @@ struct BUpArgs {
   float* pu;
   int ldp;                  // ldh + ldc
   int Mpad;
-  float* yzero;             // k_sbup: (M, H) fp32 cleared on the way (the down kernels add into it)
-  int yzero_n4;             // its length in float4
+  int hot_per_wg;           // k_sbup: hot rows per workgroup (n_hot over 256 workgroups)
 };
 
 struct BDownArgs {
