@@ -428,15 +428,18 @@ def attention_layers(dev, g, n_kv=8):
 
 def measure_decode_step(ffn_layers_syn, thr, dev, ctx=512, reps=20, seed=7):
     """A whole decode step of the 32 layers, attention and FFN, in
-    DesdemonaEngine.forward's order (engine.py:421-438) through the drop-in
-    layers (oi2.DecoderStep over GroupedQueryAttention and SparseFFNLayer):
+    DesdemonaEngine.forward's order (engine.py:421-438) through oi2.DecoderStep:
     batch 1, each layer's KV cache holding `ctx` positions, the cold records
     in HBM, each layer's cold set predicted from the previous layer's
-    post-attention state.  The step is captured in one graph and replayed."""
+    post-attention state.  Two FFN sides over the same synthetic layers: the
+    drop-in SparseFFNLayers (predictor, then FFN, per layer) and a DecodeStack
+    (one layer per oi2_stack_layer call: FFN and the next layer's prediction
+    in two kernels).  Each step is captured in one graph and replayed."""
     import math
     import torch
     import oi2
     from oi2.decode_step import DecoderStep
+    from oi2.stack import DecodeStack, StackLayer
     from oi2.store import ColdSection
     g = torch.Generator(device=dev).manual_seed(seed)
     attn = attention_layers(dev, g)
@@ -456,7 +459,9 @@ def measure_decode_step(ffn_layers_syn, thr, dev, ctx=512, reps=20, seed=7):
     ffn = [oi2.SparseFFNLayer(li, "", _Sections(l), l.predictor, cfg, dev, hot=l.hot,
                               ffn_norm_weight=l.norm_w, threshold=p_thr)
            for li, l in enumerate(ffn_layers_syn)]
-    step = DecoderStep(attn, ffn)
+    stack = DecodeStack([StackLayer(l.hot, l.records, l.lut, l.norm_w, l.predictor) for l in ffn_layers_syn],
+                        INTER, EPS, "silu", False, thr)
+    stack.set_expected_active(int(1.3 * ACTIVE_FRAC * (INTER - N_HOT)))
     cos, sin = oi2.rope_tables(ctx + 1, 128, 1e6, device=dev)
     c1, s1 = cos[ctx:ctx + 1], sin[ctx:ctx + 1]
     x0 = torch.randn((1, 1, H), generator=g, device=dev).half()
@@ -464,30 +469,35 @@ def measure_decode_step(ffn_layers_syn, thr, dev, ctx=512, reps=20, seed=7):
     for _ in attn:
         k = torch.randn((1, 8, ctx, 128), generator=g, device=dev).half()
         caches.append((k, torch.randn_like(k)))
-    stream = torch.cuda.Stream(device=dev)
-    with torch.cuda.stream(stream):
-        _, kv = step(x0, c1, s1, caches)          # copies the caches into the layers' buffers
-        kvs = [(k[:, :, :ctx], v[:, :, :ctx]) for k, v in kv]
-        step(x0, c1, s1, kvs)
-    stream.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=stream):
-        y, _ = step(x0, c1, s1, kvs)
-    graph.replay()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
+    out = {"layers": N_LAYERS, "batch": 1, "context": ctx}
+    for name, ffn_side in (("drop_in_layers", ffn), ("stack_layers", stack)):
+        step = DecoderStep(attn, ffn_side)
+        stream = torch.cuda.Stream(device=dev)
+        with torch.cuda.stream(stream):
+            _, kv = step(x0, c1, s1, caches)          # copies the caches into the layers' buffers
+            kvs = [(k[:, :, :ctx], v[:, :, :ctx]) for k, v in kv]
+            step(x0, c1, s1, kvs)
+        stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            y, _ = step(x0, c1, s1, kvs)
         graph.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1e3 / reps
-    assert torch.isfinite(y.float()).all()
-    del graph
-    return {"layers": N_LAYERS, "batch": 1, "context": ctx, "us_per_token": us,
-            "us_per_layer": us / N_LAYERS, "tok_s": 1e6 / us,
-            "path": "DecoderStep: GroupedQueryAttention (3 kernels) + SparseFFNLayer (predictor, "
-                    "gate/up, down kernels) per layer, one graph per token"}
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / reps
+        assert torch.isfinite(y.float()).all()
+        del graph
+        out[name] = {"us_per_token": us, "us_per_layer": us / N_LAYERS, "tok_s": 1e6 / us}
+    stack.close()
+    out["path"] = ("DecoderStep: GroupedQueryAttention (3 kernels per layer) + FFN per layer as the "
+                   "drop-in SparseFFNLayer (predictor 3 kernels, FFN 3) or DecodeStack.layer "
+                   "(3 kernels with the next layer's prediction fused); one graph per token")
+    return out
 
 
 def measure_attention(dev, contexts=(512, 4096), reps=20, seed=6):
@@ -672,7 +682,8 @@ def main():
         res = measure_attention(dev)
         layers, st, thr, g = build_stack(args.seed, dev)
         res["full_decode_step"] = measure_decode_step(layers, thr, dev)
-        log(f"full decode step: {res['full_decode_step']['us_per_token']:.0f} us/token")
+        for side in ("drop_in_layers", "stack_layers"):
+            log(f"full decode step ({side}): {res['full_decode_step'][side]['us_per_token']:.0f} us/token")
         print(json.dumps({"attention": res}), flush=True)
         return
     t0 = time.time()
@@ -809,8 +820,9 @@ def main():
         attention = measure_attention(dev)
         attention["full_decode_step"] = measure_decode_step(layers, thr, dev)
         f = attention["full_decode_step"]
-        log(f"full decode step (attention + FFN, ctx {f['context']}): {f['us_per_token']:.0f} us/token, "
-            f"{f['tok_s']:.0f} tok/s")
+        for side in ("drop_in_layers", "stack_layers"):
+            log(f"full decode step (attention + FFN as {side}, ctx {f['context']}): "
+                f"{f[side]['us_per_token']:.0f} us/token, {f[side]['tok_s']:.0f} tok/s")
 
     writer = None
     if args.split_writer and not args.hbm_only:

@@ -746,6 +746,47 @@ int oi2_stack_decode(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, void* 
   return OI2_OK;
 }
 
+int oi2_stack_predict(oi2_stack* s, int32_t layer, const uint16_t* x, void* stream) {
+  clear_error();
+  OI2_CHECK_ARG(s && x, "null argument");
+  OI2_CHECK_ARG((uintptr_t)x % 16 == 0, "x must be 16-byte aligned");
+  OI2_CHECK_ARG(layer >= 0 && layer < s->n_layers, "layer %d of %d", layer, s->n_layers);
+  OI2_CHECK_ARG(!s->staged, "per-layer calls do not stage; turn staging off");
+  if (!s->layers[layer].has_pred) return OI2_OK;   // the layer takes every cold record
+  hipStream_t st = (hipStream_t)stream;
+  // the predictor normalises x from its sum-of-squares partials
+  hipLaunchKernelGGL(k_prep, dim3(1), dim3(kThreads), 0, st, x, s->layers[layer].l.norm_w, s->xw, s->ssq);
+  OI2_CHECK_LAUNCH();
+  return launch_predictor(s, layer, x, st);
+}
+
+int oi2_stack_layer(oi2_stack* s, int32_t layer, const uint16_t* x_in, uint16_t* x_out, void* stream) {
+  clear_error();
+  OI2_CHECK_ARG(s && x_in && x_out, "null argument");
+  OI2_CHECK_ARG(((uintptr_t)x_in | (uintptr_t)x_out) % 16 == 0, "x must be 16-byte aligned");
+  OI2_CHECK_ARG(x_in + kH <= x_out || x_out + kH <= x_in, "x_in and x_out overlap");
+  OI2_CHECK_ARG(layer >= 0 && layer < s->n_layers, "layer %d of %d", layer, s->n_layers);
+  OI2_CHECK_ARG(!s->staged, "per-layer calls do not stage; turn staging off");
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(k_prep, dim3(1), dim3(kThreads), 0, st, x_in, s->layers[layer].l.norm_w, s->xw, s->ssq);
+  OI2_CHECK_LAUNCH();
+  UpArgs ua;
+  DownArgs da;
+  layer_args(s, layer, x_in, x_out, ua, da);
+  // the caller's input and output; the next layer's input is not this
+  // output (attention comes between), so no norm partials are passed on
+  ua.tok = TokenIn{x_in, s->xw, s->ssq, s->eps, 1};
+  da.res = x_in;
+  da.out = x_out;
+  da.out2 = nullptr;
+  da.next_norm_w = nullptr;
+  da.xw_out = nullptr;
+  da.ssq_out = nullptr;
+  int rc = launch_up(ua, st);
+  if (rc == OI2_OK) rc = launch_down(da, st);
+  return rc;
+}
+
 int oi2_stack_set_expected_active(oi2_stack* s, int32_t expected) {
   clear_error();
   OI2_CHECK_ARG(s && expected >= 0, "bad argument");

@@ -87,6 +87,8 @@ _SIGS = {
     "oi2_stack_create": (c_int32, [POINTER(Layer), c_int32, c_int32, c_float, c_int32, c_int32,
                                    c_float, POINTER(c_void_p)]),
     "oi2_stack_decode": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p]),
+    "oi2_stack_predict": (c_int32, [c_void_p, c_int32, c_void_p, c_void_p]),
+    "oi2_stack_layer": (c_int32, [c_void_p, c_int32, c_void_p, c_void_p, c_void_p]),
     "oi2_stack_set_graph": (c_int32, [c_void_p, c_int32]),
     "oi2_stack_set_expected_active": (c_int32, [c_void_p, c_int32]),
     "oi2_stack_profile": (c_int32, [c_void_p, c_void_p, c_void_p, c_int32, POINTER(c_float),

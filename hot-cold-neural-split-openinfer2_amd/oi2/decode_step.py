@@ -8,6 +8,12 @@ Embedding, final norm and lm_head stay with the caller, as they are outside
 the decode path this library replaces.  With the cold records resident in
 HBM (or pinned memory) nothing in the loop waits on the host, so a caller may
 capture a whole step in a CUDA/HIP graph.
+
+The FFN side is either the drop-in layers (a list of SparseFFNLayer, any
+batch) or a DecodeStack holding the same layers (one token): the stack runs
+each layer as two kernels that also predict the next layer's cold set from
+the layer's post-attention input, where the drop-in layers run a separate
+predictor first.  Both give the same values.
 """
 from __future__ import annotations
 
@@ -15,12 +21,15 @@ import torch
 
 from .attention import GroupedQueryAttention
 from .layer import SparseFFNLayer
+from .stack import DecodeStack
 
 
 class DecoderStep:
-    def __init__(self, attention_layers: list[GroupedQueryAttention], ffn_layers: list[SparseFFNLayer]):
-        if len(attention_layers) != len(ffn_layers):
-            raise ValueError(f"{len(attention_layers)} attention layers but {len(ffn_layers)} FFN layers")
+    def __init__(self, attention_layers: list[GroupedQueryAttention],
+                 ffn_layers: "list[SparseFFNLayer] | DecodeStack"):
+        n_ffn = ffn_layers.n_layers if isinstance(ffn_layers, DecodeStack) else len(ffn_layers)
+        if len(attention_layers) != n_ffn:
+            raise ValueError(f"{len(attention_layers)} attention layers but {n_ffn} FFN layers")
         self.attention_layers = attention_layers
         self.ffn_layers = ffn_layers
 
@@ -29,6 +38,8 @@ class DecoderStep:
         the call's positions; kv_caches None or one (k, v) per layer.
         Returns (x after the last layer's FFN, the new caches), as the loop
         of engine.py:421-438 leaves them before the final norm."""
+        if isinstance(self.ffn_layers, DecodeStack):
+            return self._forward_stack(x, cos, sin, kv_caches)
         new_kv = []
         B, T, H = x.shape
         next_prefetch = self.ffn_layers[0].submit_cold_fetch(x)
@@ -42,6 +53,23 @@ class DecoderStep:
             next_prefetch = (self.ffn_layers[li + 1].submit_cold_fetch(x)
                              if li + 1 < len(self.ffn_layers) else None)
             x = ffn(x, this_prefetch)
+        return x, new_kv
+
+    def _forward_stack(self, x, cos, sin, kv_caches):
+        B, T, H = x.shape
+        if B * T != 1:
+            raise ValueError(f"a DecodeStack runs one token at a time, got batch {B} x {T}")
+        stack = self.ffn_layers
+        stack.predict(0, x.reshape(H))
+        new_kv = []
+        for li, attn in enumerate(self.attention_layers):
+            kv = kv_caches[li] if kv_caches else None
+            resid = torch.empty_like(x)
+            _, layer_kv = attn(x, cos, sin, kv, residual_out=resid)   # x + attention
+            new_kv.append(layer_kv)
+            out = torch.empty_like(x)
+            stack.layer(li, resid.reshape(H), out.reshape(H))         # FFN, and layer li + 1's set
+            x = out
         return x, new_kv
 
     __call__ = forward

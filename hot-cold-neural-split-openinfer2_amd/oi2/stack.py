@@ -105,6 +105,20 @@ class DecodeStack:
         s = stream.cuda_stream if stream is not None else _lib.stream_handle(x_in.device)
         _lib.check(_lib.lib().oi2_stack_decode(self._h, x_in.data_ptr(), x_out.data_ptr(), s or None))
 
+    def predict(self, layer: int, x: torch.Tensor, stream=None):
+        """Layer `layer`'s cold set predicted from x (H) fp16 (the engine
+        predicts layer 0's from the embedded token, engine.py:422)."""
+        s = stream.cuda_stream if stream is not None else _lib.stream_handle(x.device)
+        _lib.check(_lib.lib().oi2_stack_predict(self._h, int(layer), x.data_ptr(), s or None))
+
+    def layer(self, layer: int, x_in: torch.Tensor, x_out: torch.Tensor, stream=None):
+        """One layer on its own: x_out = x_in + FFN(RMSNorm(x_in)) over the
+        set held for `layer`, and the next layer's set predicted from x_in
+        (the engine's lookahead from the post-attention state,
+        engine.py:431-436).  For callers that run attention between layers."""
+        s = stream.cuda_stream if stream is not None else _lib.stream_handle(x_in.device)
+        _lib.check(_lib.lib().oi2_stack_layer(self._h, int(layer), x_in.data_ptr(), x_out.data_ptr(), s or None))
+
     def profile(self, x_in: torch.Tensor, x_out: torch.Tensor, stream=None, reps: int = 8):
         """Mean (ffn_up us, ffn_down us) per launch: every layer's kernel
         launched back to back `reps` times between two hipEvents on the launch

@@ -228,6 +228,20 @@ int oi2_stack_create(const oi2_layer* layers, int32_t n_layers, int32_t inter, f
                      oi2_stack** out);
 /* One token through all layers: x_out (H) fp16 from x_in (H) fp16. */
 int oi2_stack_decode(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, void* stream);
+/* The same layers one at a time, for a caller that runs other sublayers
+ * (attention) between them, as DesdemonaEngine.forward does
+ * (engine.py:421-438), batch 1:
+ *   oi2_stack_predict(s, L, x): layer L's cold set predicted from x (the
+ *     engine predicts layer 0's from the embedded token, engine.py:422);
+ *   oi2_stack_layer(s, L, x_in, x_out): x_out = x_in + FFN_L(RMSNorm_L(x_in))
+ *     over the set held for layer L (SparseFFNLayer.forward,
+ *     engine.py:292-312), and layer L+1's set predicted from x_in, the
+ *     engine's lookahead from layer L's post-attention state
+ *     (engine.py:431-436), inside the same two kernels.
+ * Both are launched directly on `stream` (a caller may capture them); not
+ * with staging.  x_in and x_out must not overlap. */
+int oi2_stack_predict(oi2_stack* s, int32_t layer, const uint16_t* x, void* stream);
+int oi2_stack_layer(oi2_stack* s, int32_t layer, const uint16_t* x_in, uint16_t* x_out, void* stream);
 /* Size the cold gather launch for about `expected` active cold records per
  * layer (any count up to the capacity is still processed; this only sets how
  * many workgroups the pass uses).  0 restores the capacity. */

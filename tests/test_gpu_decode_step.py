@@ -181,3 +181,72 @@ def test_graph_replays_equal_the_eager_step(dev, split):
         other = (other @ other).tanh()          # eager work between the replays
         torch.cuda.synchronize()
     del graph
+
+
+def _stack(split):
+    """The same layers held by a DecodeStack (its records and LUT from the
+    split file's store, the predictors from the registry, threshold 0.5 =
+    logit 0)."""
+    from oi2.stack import DecodeStack, StackLayer
+    layers = []
+    for li, lay in enumerate(split["syn"]):
+        sec = split["store"].section(li)
+        layers.append(StackLayer(lay.hot, sec.records, sec.lut, lay.norm_w, split["reg"].predictors[(li, 0)]))
+    return DecodeStack(layers, INTER, EPS, "silu", False, 0.0)
+
+
+def test_stack_layers_equal_drop_in_layers(dev, split):
+    """DecoderStep over a DecodeStack (each layer's FFN and the next layer's
+    prediction in two kernels, oi2_stack_layer) against DecoderStep over the
+    drop-in SparseFFNLayers: the same output and caches, bit for bit."""
+    past = 40
+    cos, sin = oi2.rope_tables(past + 1, D, 1e6, device=dev)
+    c1, s1 = cos[past:], sin[past:]
+    g = torch.Generator(device=dev).manual_seed(66)
+    x0 = torch.randn((1, 1, H), generator=g, device=dev).half()
+    caches = _caches(dev, split["n_layers"], 1, past, seed=67)
+    attn, ffn = _layers(split, dev)
+    print("[decode step] drop-in layers vs stack layers", flush=True)
+    y_ref, kv_ref = DecoderStep(attn, ffn)(x0, c1, s1, caches)
+    attn2, _ = _layers(split, dev)
+    stack = _stack(split)
+    y, kv = DecoderStep(attn2, stack)(x0, c1, s1, caches)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_ref), "stack path differs from the drop-in layers"
+    for (k, v), (kr, vr) in zip(kv, kv_ref):
+        assert torch.equal(k, kr) and torch.equal(v, vr)
+    with pytest.raises(ValueError):
+        DecoderStep(attn2, stack)(torch.zeros((2, 1, H), dtype=torch.float16, device=dev), c1, s1, caches)
+    stack.close()
+
+
+def test_stack_step_graph_replays(dev, split):
+    """The stack path captured in a graph: every replay equals the eager step."""
+    past = 200
+    cos, sin = oi2.rope_tables(past + 1, D, 1e6, device=dev)
+    c1, s1 = cos[past:], sin[past:]
+    g = torch.Generator(device=dev).manual_seed(68)
+    x0 = torch.randn((1, 1, H), generator=g, device=dev).half()
+    attn, _ = _layers(split, dev)
+    stack = _stack(split)
+    step = DecoderStep(attn, stack)
+    stream = torch.cuda.Stream(device=dev)
+    print("[decode step graph] stack layers", flush=True)
+    with torch.cuda.stream(stream):
+        _, kv = step(x0, c1, s1, _caches(dev, split["n_layers"], 1, past, seed=69))
+        views = [(k[:, :, :past], v[:, :, :past]) for k, v in kv]
+        y_eager, _ = step(x0, c1, s1, views)
+        y_eager = y_eager.clone()
+    stream.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        y, _ = step(x0, c1, s1, views)
+    other = torch.randn((512, 512), generator=g, device=dev)
+    for r in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, y_eager), f"replay {r} differs from the eager step"
+        other = (other @ other).tanh()
+        torch.cuda.synchronize()
+    del graph
+    stack.close()
