@@ -1024,6 +1024,7 @@ __global__ __launch_bounds__(kThreads) void k_bup_s(BUpArgs a) {
 
 constexpr int kSbGroups = 256;      // workgroups: one per CU
 constexpr int kSbThreads = 512;     // 8 waves; wave w takes K [512 w, 512 w + 512)
+constexpr int kHotEarly = 4;        // hot chunks each wave loads before the prologue
 
 // Workgroup g takes hot rows [g hr, g hr + hr) (hr = a.hot_per_wg, tiles of
 // 16 rows) and items g, g + 256, g + 512, ... of the dense active list
@@ -1031,8 +1032,10 @@ constexpr int kSbThreads = 512;     // 8 waves; wave w takes K [512 w, 512 w + 5
 // It first normalises the M <= MMAX token rows itself (x_n = fp16((x r) w),
 // the rounding of nn.RMSNorm's fp16 output) into LDS: the two halves of the
 // workgroup take alternate rows, thread e of a half holds elements
-// [16 e, 16 e + 16) of them.  The first hot tile's weight loads and the first
-// cold tile's record loads are in flight by then.
+// [16 e, 16 e + 16) of them.  Half of the first hot tile's weight loads are
+// in flight by then; the rest, and the first cold tile's record loads, go
+// out right after (with all of them first a wave would stall issuing at a
+// full memory queue, and the prologue's barriers wait for the slowest wave).
 // Hot rows: lane (t, q) = (l & 15, l >> 4) loads 16 bytes of row t at K
 // 512 w + 64 c + 16 q, the B operand of two 16x16x32 steps (K + 8 s, s < 2);
 // the A operand of the same steps is token t's x_n at the same K.
@@ -1097,16 +1100,19 @@ __global__ __launch_bounds__(kSbThreads) void k_sbup(BUpArgs a, const uint16_t* 
   const rsrc_t rcb = buf_rsrc(a.cold_gbias, a.cold_gbias ? (uint32_t)a.n_records * 4 : 0u);
   u32x4 WG[8], WU[8];                   // one hot tile's chunks
   float hsg, hsu, hgb;                  // and its row scales and gate bias (zero past the rows)
-  auto hot_issue = [&](int ti) {
+  // chunks [c0, c1) of hot tile ti
+  auto hot_issue = [&](int ti, int c0, int c1) {
     const int r = 16 * ti + t, col = hot0 + r;
     // rows past this workgroup's share or past n_hot read zero
     const bool in = r < hr && col < a.n_hot;
     const uint32_t voff = in ? (uint32_t)col * kH + 16 * q : kNoOffset;
 #pragma unroll
     for (int c = 0; c < 8; ++c) {
+      if (c < c0 || c >= c1) continue;
       WG[c] = bload16(rg, voff, kq + 64 * c);
       WU[c] = bload16(ru, voff, kq + 64 * c);
     }
+    if (c0 > 0) return;
     const uint32_t soff = in ? (uint32_t)col * 4 : kNoOffset;
     hsg = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rgs, soff, 0, 0));
     hsu = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rus, soff, 0, 0));
@@ -1128,19 +1134,10 @@ __global__ __launch_bounds__(kSbThreads) void k_sbup(BUpArgs a, const uint16_t* 
     cgb = __builtin_bit_cast(float,
                              __builtin_amdgcn_raw_buffer_load_b32(rcb, in ? (uint32_t)slot * 4 : kNoOffset, 0, 0));
   };
-  // the first tiles' loads go out unconditionally (a missing tile reads
+  // the first hot tile's loads go out unconditionally (a missing tile reads
   // zero): with the same loads on every path the compiler can wait for the
   // token rows alone in the prologue
-  hot_issue(0);
-  __builtin_amdgcn_sched_barrier(0);
-  // the list's values are first used here (not earlier: the hot loads would
-  // then wait for them)
-  asm volatile("" : "+v"(raw_total), "+v"(raw_slot));
-  const int total = list ? min(raw_total, a.cap) : 0;
-  const int n_items = total > g ? (total - g + kSbGroups - 1) / kSbGroups : 0;   // this workgroup's
-  const int n_ct = (n_items + 15) / 16;
-  int slot = list && g + kSbGroups * t < total ? raw_slot : -1;
-  cold_issue(slot);
+  hot_issue(0, 0, kHotEarly);
   __builtin_amdgcn_sched_barrier(0);
 
   // prologue: sum-of-squares partials of this thread's rows, then x_n (rows
@@ -1198,6 +1195,16 @@ __global__ __launch_bounds__(kSbThreads) void k_sbup(BUpArgs a, const uint16_t* 
     }
   }
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+
+  hot_issue(0, kHotEarly, 8);
+  // the list's values are first used here
+  asm volatile("" : "+v"(raw_total), "+v"(raw_slot));
+  const int total = list ? min(raw_total, a.cap) : 0;
+  const int n_items = total > g ? (total - g + kSbGroups - 1) / kSbGroups : 0;   // this workgroup's
+  const int n_ct = (n_items + 15) / 16;
+  int slot = list && g + kSbGroups * t < total ? raw_slot : -1;
+  cold_issue(slot);
+  __builtin_amdgcn_sched_barrier(0);
 
   const bool ta = t < M;                 // this lane's A row is a token
   const uint16_t* xa = s_x + t * kLdX + kq + 16 * q;   // hot: K kq + 64 c + 16 q + 8 s
@@ -1303,7 +1310,7 @@ __global__ __launch_bounds__(kSbThreads) void k_sbup(BUpArgs a, const uint16_t* 
     }
   };
   for (int ti = 1; ti < n_ht; ++ti) {
-    hot_issue(ti);
+    hot_issue(ti, 0, 8);
     f32x4 accg, accu;
     hot_mfma(accg, accu);
     const int r = 16 * ti + t, col = hot0 + r;
