@@ -161,9 +161,9 @@ __global__ __launch_bounds__(kThreads) void k_attn_gemv(GemvArgs a) {
   const uint8_t* row1 = row0 + (size_t)kHalf * kH;
   u32x4 w0[4], w1[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) w0[i] = load16(row0 + 1024 * i);
+  for (int i = 0; i < 4; ++i) w0[i] = load16_nt(row0 + 1024 * i);
 #pragma unroll
-  for (int i = 0; i < 4; ++i) w1[i] = load16(row1 + 1024 * i);
+  for (int i = 0; i < 4; ++i) w1[i] = load16_nt(row1 + 1024 * i);
   __builtin_amdgcn_sched_barrier(0);
 
   // x_n = fp16((x r) w) (nn.RMSNorm on fp16, engine.py:93), staged in LDS:

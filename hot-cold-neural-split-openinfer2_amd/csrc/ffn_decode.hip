@@ -224,7 +224,7 @@ __device__ void cold_role(const UpArgs& a, int wg, uint32_t* s_nat, uint32_t* s_
     if (!R.valid) return;
     const uint8_t* rec = a.records + (size_t)sl * kRecBytes;
 #pragma unroll
-    for (int it = 0; it < 6; ++it) R.q[it] = load16_a2(rec + kOffGate + 16 * (lane + 64 * it));
+    for (int it = 0; it < 6; ++it) R.q[it] = load16_a2_nt(rec + kOffGate + 16 * (lane + 64 * it));
     const uint16_t* sc = reinterpret_cast<const uint16_t*>(rec + kOffScales);
 #pragma unroll
     for (int v = 0; v < 3; ++v) {
@@ -344,7 +344,7 @@ __device__ void pred_d_role_t(const UpArgs& a, int row) {
   if constexpr (BF16) {
     const uint16_t* drow = reinterpret_cast<const uint16_t*>(a.pd_w) + (size_t)row * kH;
 #pragma unroll
-    for (int it = 0; it < 8; ++it) dw.v[it] = load16(reinterpret_cast<const uint8_t*>(drow + 8 * (lane + 64 * it)));
+    for (int it = 0; it < 8; ++it) dw.v[it] = load16_nt(reinterpret_cast<const uint8_t*>(drow + 8 * (lane + 64 * it)));
   }
   const bool norm = a.pd_norm_w && !a.pd_q;
   // every input of the row issued before the first use
@@ -424,10 +424,10 @@ __device__ void hot_up_role(const UpArgs& a, int wg, uint32_t* s_nat, uint32_t* 
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
     const size_t off = (size_t)k0 * kH + 1024 * it + 16 * lane;
-    qg[0][it] = one ? load16(a.gate_q + off) : u32x4{0, 0, 0, 0};
-    qu[0][it] = one ? load16(a.up_q + off) : u32x4{0, 0, 0, 0};
-    qg[1][it] = two ? load16(a.gate_q + off + kH) : u32x4{0, 0, 0, 0};
-    qu[1][it] = two ? load16(a.up_q + off + kH) : u32x4{0, 0, 0, 0};
+    qg[0][it] = one ? load16_nt(a.gate_q + off) : u32x4{0, 0, 0, 0};
+    qu[0][it] = one ? load16_nt(a.up_q + off) : u32x4{0, 0, 0, 0};
+    qg[1][it] = two ? load16_nt(a.gate_q + off + kH) : u32x4{0, 0, 0, 0};
+    qu[1][it] = two ? load16_nt(a.up_q + off + kH) : u32x4{0, 0, 0, 0};
   }
   // scales of neuron k0 + lane for lanes 0 and 1, and the norm partials
   const int kl = k0 + (lane & 1);
@@ -642,7 +642,7 @@ __device__ void down_role(const DownArgs& a, int b, DownShared& sh) {
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
       const int c = lane + 64 * it;
-      q[rr][it] = (a.n_hot > 0 && c < nch) ? load16(row + 16 * c) : u32x4{0, 0, 0, 0};
+      q[rr][it] = (a.n_hot > 0 && c < nch) ? load16_nt(row + 16 * c) : u32x4{0, 0, 0, 0};
     }
   }
   // h values for this lane's chunks (L2-resident, written by ffn_up)

@@ -48,6 +48,16 @@ __device__ __forceinline__ u32x4 load16(const uint8_t* p) {
   return *reinterpret_cast<const u32x4*>(p);
 }
 
+// The same loads with the non-temporal hint, for weights that one launch
+// reads once: a plain 2 GB read streams at ~6.0 TB/s on this GPU, a
+// non-temporal one at ~7.3 TB/s.
+__device__ __forceinline__ u32x4 load16_nt(const uint8_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+__device__ __forceinline__ u32x4 load16_a2_nt(const uint8_t* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4_a2*>(p));
+}
+
 __device__ __forceinline__ float half_bits_to_float(uint16_t b) {
   return (float)__builtin_bit_cast(_Float16, b);
 }
