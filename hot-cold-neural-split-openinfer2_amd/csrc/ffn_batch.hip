@@ -85,7 +85,6 @@ __device__ __forceinline__ h8 int4x8_h8_scaled(uint32_t d, _Float16 sc) {
 // single-token kernels' weight streams made the small-batch kernels slower:
 // 8 tokens x 32 layers 1112 -> 1145 us with it on both k_sbup and
 // k_bdown_hot_s, so these loads stay plain.)
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
 __device__ __forceinline__ rsrc_t buf_rsrc(const void* p, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
 }

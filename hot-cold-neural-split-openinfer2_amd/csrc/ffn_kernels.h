@@ -10,8 +10,12 @@ constexpr int kRowsPerDownWG = 16;
 constexpr int kDownWG = kH / kRowsPerDownWG;   // 256 output tiles
 constexpr int kSelChunk = 256;
 constexpr int kMaxChunks = 256;
-constexpr int kColdPerWG = 4;                  // one cold record per wave
-constexpr int kMaxColdWG = 1024;
+// Cold work of the single-token kernels: about kColdItemsPerWave active items
+// per wave, at most kMaxColdWaves waves plus one per chunk, four waves per
+// workgroup, each workgroup one fp32 partial row of y.
+constexpr int kColdItemsPerWave = 2;
+constexpr int kMaxColdWaves = 1024;
+constexpr int kMaxColdWG = (kMaxColdWaves + kMaxChunks + 3) / 4;   // 320
 
 // Active items in chunks: chunk c holds counts[c] items at slots[c * chunk ..].
 // slots == nullptr: item at position p uses record p.
@@ -50,8 +54,7 @@ struct UpArgs {
   const float* cold_gbias;
   ActiveList act;
   float* cold_part;         // (wg_cold, H) partial down sums, one row per workgroup
-  int32_t* cold_total;      // number of active items
-  int cold_cap;             // items beyond this are ignored
+  int cold_wpc;             // cold waves per chunk of the list
   // predictor down projection (lookahead layer): z = D q, q = cast(fp16(x r w'))
   const void* pd_w;
   int pd_rank;
@@ -78,8 +81,6 @@ struct DownArgs {
   const float* down_s;
   // cold down: partial rows from ffn_up's cold workgroups
   const float* cold_part;
-  const int32_t* cold_total;
-  int cold_cap;
   int cold_wg;              // ffn_up's cold workgroup count
   // outputs
   uint16_t* out;
@@ -219,7 +220,6 @@ size_t batch_ws_bytes(int M, int n_hot, int cap);
 struct FfnWs {
   float* h_hot;
   float* cold_part;
-  int32_t* cold_total;
   uint16_t* xw;
   float* ssq;
 };
@@ -229,7 +229,7 @@ __host__ __device__ constexpr size_t ffn_align256(size_t v) { return (v + 255) &
 // Bytes of that scratch for n_hot hot neurons and cold_wg cold workgroups.
 __host__ __device__ constexpr size_t ffn_ws_bytes(int n_hot, int cold_wg) {
   return ffn_align256((size_t)(n_hot > 0 ? n_hot : 0) * 4 + 64) +
-         ffn_align256((size_t)cold_wg * kH * 4) + ffn_align256(64) + ffn_align256(kH * 2) +
+         ffn_align256((size_t)cold_wg * kH * 4) + ffn_align256(kH * 2) +
          ffn_align256(kDownWG * 4);
 }
 
@@ -241,6 +241,7 @@ struct FfnCall {
   bool has_cold = false;
   int cap = 0;       // capacity of the active list
   int wg_cold = 0;   // cold workgroups of the launch (from the expected count)
+  int cold_wpc = 0;  // cold waves per chunk
 };
 
 int ffn_validate(const uint16_t* x, int batch, const uint16_t* norm_w, const oi2_hot* hot,
@@ -249,7 +250,21 @@ int ffn_decode_tokens(const uint16_t* x, int batch, const uint16_t* norm_w, floa
                       const oi2_hot* hot, const oi2_cold* cold, const oi2_active* active, int act,
                       int act_on_both, int add_residual, uint16_t* out, float* y32,
                       const FfnCall& c, const FfnWs& ws, hipStream_t st);
-int cold_wg_for(int expected);
+// The cold split of a list of n_chunks chunks with about `expected` items:
+// wpc waves per chunk, wg workgroups (never more than cold_rows_bound of any
+// expected count at least as large, nor than kMaxColdWG).
+struct ColdSplit {
+  int wpc;
+  int wg;
+};
+ColdSplit cold_split(int n_chunks, int expected);
+// Partial rows (cold workgroups) that any list of up to kMaxChunks chunks
+// with at most `capacity` expected items can need.
+constexpr int cold_rows_bound(int capacity) {
+  const int waves = (capacity + kColdItemsPerWave - 1) / kColdItemsPerWave;
+  const int wv = waves < 1 ? 1 : (waves > kMaxColdWaves ? kMaxColdWaves : waves);
+  return (wv + kMaxChunks - 1 + 3) / 4;
+}
 
 int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const oi2_hot* hot,
               const oi2_cold* cold, const oi2_active* active, int relu, int both, int add_residual,

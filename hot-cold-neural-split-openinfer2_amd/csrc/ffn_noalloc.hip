@@ -2,11 +2,11 @@
 // (the same k_prep / k_ffn_up / k_ffn_down launches, token by token) for
 // callers that cannot allocate device memory: code under HIP graph capture,
 // serving loops, harnesses that forbid hipMalloc.  Its scratch (h_hot, the
-// cold partial rows, the cold item total, x * w, the norm partials) is one
-// file-scope device array, `scratch`, of kNoAllocBytes: room for n_hot up to
-// 4096 and up to kNoAllocColdWG cold workgroups, i.e. an expected active
-// count up to 4 * kNoAllocColdWG records.  Each GPU holds its own copy until
-// the process ends.
+// cold partial rows, x * w, the norm partials) is one file-scope device
+// array, `scratch`, of kNoAllocBytes: room for n_hot up to 4096 and
+// kNoAllocColdWG cold partial rows, which covers any list with an expected
+// active count up to kNoAllocMaxExpected records.  Each GPU holds
+// its own copy until the process ends.
 //
 // In host code `scratch` names a host-side stand-in, not the device array:
 // the device address is looked up once per device with hipGetSymbolAddress
@@ -23,7 +23,10 @@
 namespace oi2 {
 
 constexpr int kNoAllocColdWG = 256;
-constexpr size_t kNoAllocBytes = ffn_ws_bytes(kH, kNoAllocColdWG);   // 4,220,416 bytes
+constexpr int kNoAllocMaxExpected = 1024;
+constexpr size_t kNoAllocBytes = ffn_ws_bytes(kH, kNoAllocColdWG);   // 4,220,160 bytes
+static_assert(cold_rows_bound(kNoAllocMaxExpected) <= kNoAllocColdWG,
+              "the scratch holds the partial rows of every list the limit admits");
 constexpr int kMaxDevices = 64;
 
 static __device__ __align__(256) uint8_t scratch[kNoAllocBytes];
@@ -60,7 +63,7 @@ extern "C" {
 
 size_t oi2_ffn_noalloc_scratch_bytes(void) { return kNoAllocBytes; }
 
-int32_t oi2_ffn_noalloc_max_expected(void) { return kNoAllocColdWG * kColdPerWG; }
+int32_t oi2_ffn_noalloc_max_expected(void) { return kNoAllocMaxExpected; }
 
 int oi2_ffn_forward_noalloc(const uint16_t* x, int32_t batch, const uint16_t* norm_w, float eps,
                             const oi2_hot* hot, const oi2_cold* cold, const oi2_active* active,
@@ -70,11 +73,11 @@ int oi2_ffn_forward_noalloc(const uint16_t* x, int32_t batch, const uint16_t* no
   FfnCall c;
   int rc = ffn_validate(x, batch, norm_w, hot, cold, active, act, &c);
   if (rc || batch == 0) return rc;
-  OI2_CHECK_ARG(c.wg_cold <= kNoAllocColdWG,
-                "expected active count %d needs %d cold workgroups; the static scratch of this "
-                "entry point holds %d (expected <= %d records; set oi2_active.expected)",
-                active->expected > 0 && active->expected < c.cap ? active->expected : c.cap,
-                c.wg_cold, kNoAllocColdWG, kNoAllocColdWG * kColdPerWG);
+  const int expected = active && active->expected > 0 && active->expected < c.cap ? active->expected : c.cap;
+  OI2_CHECK_ARG(!c.has_cold || expected <= kNoAllocMaxExpected,
+                "expected active count %d is beyond the %d records the static scratch of this "
+                "entry point covers (set oi2_active.expected)",
+                expected, kNoAllocMaxExpected);
   void* base = nullptr;
   rc = scratch_for_current_device(&base);
   if (rc) return rc;

@@ -38,13 +38,13 @@ struct oi2_stack {
   float* ssq = nullptr;          // 256 sum-of-squares partials of that x
   float* h_hot = nullptr;
   float* cold_part = nullptr;    // (kMaxColdWG, H) partial rows of the current layer
-  int32_t* cold_total = nullptr;
   int cold_cap = 0;
   double* z = nullptr;
   int32_t* sel_counts = nullptr; // (n_layers, n_chunks)
   int32_t* sel_slots = nullptr;  // (n_layers, n_chunks * 256)
   int32_t* sel_ids = nullptr;
   int cold_wg = 1;
+  int cold_wpc = 1;
   bool use_graph = true;
   // staging: each layer's active records are copied one layer ahead, on a
   // side stream, from their source (device or pinned host memory) into one
@@ -89,7 +89,6 @@ struct oi2_stack {
 
 namespace oi2 {
 
-int cold_wg_for(int expected);
 
 // Launch arguments of layer L's two kernels.  x_in is the token entering the
 // stack and x_out the buffer that receives the last layer's output.
@@ -140,10 +139,10 @@ static void layer_args(const oi2_stack* s, int L, const uint16_t* x_in, uint16_t
       ua.n_records = l.cold.n_records;
     }
     ua.cold_part = s->cold_part;
-    ua.cold_total = s->cold_total;
-    ua.cold_cap = s->cold_cap;
+    const ColdSplit cs = SL.has_pred ? ColdSplit{s->cold_wpc, s->cold_wg} : cold_split(1, SL.n_all);
+    ua.cold_wpc = cs.wpc;
+    ua.wg_cold = cs.wg;
   }
-  ua.wg_cold = has_cold ? (SL.has_pred ? s->cold_wg : cold_wg_for(SL.n_all)) : 0;
   ua.wg_hot = (l.hot.n_hot + 7) / 8;
   if (pred_next) {
     const oi2_layer& ln = s->layers[L + 1].l;
@@ -164,8 +163,6 @@ static void layer_args(const oi2_stack* s, int L, const uint16_t* x_in, uint16_t
   da.down_s = l.hot.down_scale;
   if (has_cold) {
     da.cold_part = s->cold_part;
-    da.cold_total = s->cold_total;
-    da.cold_cap = s->cold_cap;
     da.cold_wg = ua.wg_cold;
   }
   da.out = s->xbuf + (size_t)L * kH;
@@ -446,7 +443,7 @@ static void stack_free(oi2_stack* s) {
                   (void*)s->tok_sel_slots, (void*)s->tok_sel_ids, (void*)s->tok_hcs})
     if (p) (void)hipFree(p);
   for (void* p : {(void*)s->xbuf, (void*)s->xw, (void*)s->ssq, (void*)s->h_hot, (void*)s->cold_part,
-                  (void*)s->cold_total, (void*)s->z, (void*)s->sel_counts,
+                  (void*)s->z, (void*)s->sel_counts,
                   (void*)s->sel_slots, (void*)s->sel_ids})
     if (p) (void)hipFree(p);
 }
@@ -660,8 +657,12 @@ int oi2_stack_create(const oi2_layer* layers, int32_t n_layers, int32_t inter, f
     max_records = std::max(max_records, SL.l.cold.n_records);
     s->layers.push_back(SL);
   }
-  s->cold_wg = cold_wg_for(max_records);
   s->cold_cap = std::max(s->n_chunks * kSelChunk, max_records);
+  {
+    const ColdSplit cs = cold_split(s->n_chunks, s->cold_cap);
+    s->cold_wpc = cs.wpc;
+    s->cold_wg = cs.wg;
+  }
   const size_t sel = (size_t)n_layers * s->n_chunks * kSelChunk;
   hipError_t e = hipSuccess;
   auto alloc = [&](void** p, size_t bytes) {
@@ -672,7 +673,6 @@ int oi2_stack_create(const oi2_layer* layers, int32_t n_layers, int32_t inter, f
   alloc((void**)&s->ssq, (size_t)kDownWG * 4);
   alloc((void**)&s->h_hot, (size_t)(s->max_hot + 64) * 4);
   alloc((void**)&s->cold_part, (size_t)kMaxColdWG * kH * 4);
-  alloc((void**)&s->cold_total, 64);
   alloc((void**)&s->z, (size_t)(s->max_rank + 64) * sizeof(double));
   alloc((void**)&s->sel_counts, (size_t)n_layers * s->n_chunks * 4);
   alloc((void**)&s->sel_slots, sel * 4);
@@ -790,7 +790,9 @@ int oi2_stack_layer(oi2_stack* s, int32_t layer, const uint16_t* x_in, uint16_t*
 int oi2_stack_set_expected_active(oi2_stack* s, int32_t expected) {
   clear_error();
   OI2_CHECK_ARG(s && expected >= 0, "bad argument");
-  s->cold_wg = cold_wg_for(expected > 0 ? expected : s->cold_cap);
+  const ColdSplit cs = cold_split(s->n_chunks, expected > 0 ? expected : s->cold_cap);
+  s->cold_wpc = cs.wpc;
+  s->cold_wg = cs.wg;
   for (auto& g : s->graphs) (void)hipGraphExecDestroy(g.exec);
   s->graphs.clear();
   return OI2_OK;

@@ -75,11 +75,6 @@ static_assert(kWorkers == 7, "the row split and the epilogue's sum assume 7 work
 static_assert(kTokWorkers == kWorkers, "host and kernel agree on the worker count");
 static_assert(kTokBatch == kBatch, "host and kernel agree on the gather batch");
 
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
-typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
-typedef __attribute__((address_space(3))) void lds_void;
-constexpr uint32_t kNoOff = 0x80000000u;       // an offset past every range: reads zero
-
 // The layer table through the constant address space: its fields load with
 // scalar loads, which wait on their own counter, so reading them never makes
 // a wave wait for its vector loads (the weights in flight).
@@ -88,52 +83,6 @@ __device__ __forceinline__ CLayer* layer_table(const TokArgs& a) {
   return reinterpret_cast<CLayer*>(reinterpret_cast<uintptr_t>(a.layers));
 }
 
-// A buffer descriptor over [p, p + bytes).  p and bytes must be wave-uniform
-// (lane 0's are taken for the whole wave); lane-dependent parts go in the
-// access offset.  readfirstlane lets the compiler see the uniformity
-// (otherwise it wraps each access in a loop over the wave's descriptors).
-__device__ __forceinline__ rsrc_t rsrc(const void* p, uint32_t bytes) {
-  const uint64_t v = reinterpret_cast<uint64_t>(p);
-  // readfirstlane returns int: widen each half as uint32_t, or a low half
-  // >= 2^31 would sign-extend over the high half
-  const uint64_t u = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(v >> 32)) << 32) |
-                     (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)v);
-  return __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>(u), (short)0,
-                                           __builtin_amdgcn_readfirstlane(bytes), 0x00020000);
-}
-// Plain buffer loads: a lane whose offset is past the range reads zero, so
-// masked loads stay unconditional and the compiler never has to wait for one
-// before issuing the next.
-__device__ __forceinline__ u32x4 bld16(rsrc_t r, uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
-}
-__device__ __forceinline__ u32x2v bld8(rsrc_t r, uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
-}
-__device__ __forceinline__ uint32_t bld4(rsrc_t r, uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
-}
-__device__ __forceinline__ uint16_t bld2(rsrc_t r, uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
-}
-// 16 bytes per lane straight into LDS: lane l lands at dst + 16 l (a lane past
-// the range writes zero).  dst is the wave's 1 KB destination.
-__device__ __forceinline__ void bld16_lds(rsrc_t r, void* dst, uint32_t off) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)dst, 16, off, 0, 0, 0);
-}
-// The same loads with the non-temporal hint, for weights that one launch
-// reads once: a plain 2 GB read streams at ~6.0 TB/s on this GPU, a
-// non-temporal one at ~7.3 TB/s.
-constexpr int kNt = 2;
-__device__ __forceinline__ u32x4 wld16(rsrc_t r, uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kNt);
-}
-__device__ __forceinline__ u32x2v wld8(rsrc_t r, uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kNt);
-}
-__device__ __forceinline__ void wld16_lds(rsrc_t r, void* dst, uint32_t off) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)dst, 16, off, 0, 0, kNt);
-}
 // Agent-coherent (write-through) stores at a descriptor + lane offset: one
 // offset register per lane rather than a 64-bit address.
 __device__ __forceinline__ void cst2(rsrc_t r, uint32_t off, uint16_t v) {
