@@ -214,6 +214,53 @@ def build_staged(layers, thr):
     return sst, pinned
 
 
+def measure_token_phases(st, g, dev, tokens, warmup=16):
+    """The persistent token kernel's phase timeline: `tokens` tokens traced
+    after `warmup` plain ones (oi2_stack_trace_token: every group's control
+    wave stamps eight points of each layer on the 100 MHz counter).  Per
+    layer, over the groups: each step's median duration, the skew of the two
+    arrivals (last group minus the median group) and the time from the last
+    arrival to the median group seeing the signal; then the medians of those
+    over the layers 1..30 and the tokens."""
+    import numpy as np
+    import torch
+    stream = torch.cuda.Stream(device=dev)
+    x0 = torch.randn(H, generator=g, device=dev).half()
+    _, x = timed_decode(st, x0, stream, 0, warmup)
+    steps = ["U inputs (U start -> B1)", "U products (B1 -> B2)", "U stores + arrival (B2 -> U arrival)",
+             "U signal wait (U arrival -> U seen)", "D inputs (U seen -> D1a)", "D products + list (D1a -> D1b)",
+             "D epilogue + arrival (D1b -> D arrival)", "D signal wait (D arrival -> next U start)"]
+    per = {k: [] for k in steps}
+    extra = {"layer_us": [], "u_arrival_skew_us": [], "u_signal_after_last_us": [],
+             "d_arrival_skew_us": [], "d_signal_after_last_us": []}
+    y = torch.empty_like(x)
+    for _ in range(tokens):
+        with torch.cuda.stream(stream):
+            t = st.trace_token(x, y, stream)
+        stream.synchronize()
+        st.status(stream)
+        a = t.cpu().numpy().astype(np.int64) / 100.0        # us, (L, 256, 8)
+        x, y = y, x
+        for L in range(1, a.shape[0] - 1):
+            cur, nxt = a[L], a[L + 1]
+            d = [cur[:, k + 1] - cur[:, k] for k in range(7)] + [nxt[:, 0] - cur[:, 7]]
+            for k, name in enumerate(steps):
+                per[name].append(float(np.median(d[k])))
+            extra["layer_us"].append(float(np.median(nxt[:, 0] - cur[:, 0])))
+            extra["u_arrival_skew_us"].append(float(cur[:, 3].max() - np.median(cur[:, 3])))
+            extra["u_signal_after_last_us"].append(float(np.median(cur[:, 4]) - cur[:, 3].max()))
+            extra["d_arrival_skew_us"].append(float(cur[:, 7].max() - np.median(cur[:, 7])))
+            extra["d_signal_after_last_us"].append(float(np.median(nxt[:, 0]) - cur[:, 7].max()))
+    out = {"tokens": tokens, "layers_summarised": "1..30", "unit": "us",
+           "median_group_step": {k: float(np.median(v)) for k, v in per.items()}}
+    out.update({k: float(np.median(v)) for k, v in extra.items()})
+    for k, v in out["median_group_step"].items():
+        log(f"token phases: {k:42s} {v:6.2f} us")
+    for k in extra:
+        log(f"token phases: {k:42s} {out[k]:6.2f} us")
+    return out
+
+
 def measure_cold_dequant(layers, dev, reps=4):
     """The cold INT4 path alone, in GB/s of records against the HBM peak.
     fused: oi2_ffn_forward with no hot half over every cold record of a layer
@@ -660,6 +707,9 @@ def main():
                     help="only the HBM-resident token kernel leg (for profiling k_token)")
     ap.add_argument("--cold-only", action="store_true",
                     help="only the cold INT4 dequant measurement (for profiling the cold kernels)")
+    ap.add_argument("--token-phases", type=int, default=0, metavar="TOKENS",
+                    help="only trace the persistent token kernel's phases over TOKENS tokens "
+                         "(per-group s_memrealtime stamps) and print their summary")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path "
@@ -693,6 +743,9 @@ def main():
     if args.cold_only:
         cold = measure_cold_dequant(layers, dev)
         print(json.dumps({"cold_dequant": cold}), flush=True)
+        return
+    if args.token_phases:
+        print(json.dumps({"token_phases": measure_token_phases(st, g, dev, args.token_phases)}), flush=True)
         return
     if args.multi_token_only:
         multi = {}

@@ -352,9 +352,17 @@ struct TokArgs {
                             // row group, list positions < kTokBatch
   uint32_t* sync;           // kTokSyncWords, zero at allocation
   uint32_t spin;            // poll bound of every device-wide wait
+  uint64_t* trace;          // null, or (min(n_layers, kTokTraceLayers), kTokGroups, kTokTracePoints)
+                            // s_memrealtime stamps of each group's control wave
   float eps, thr;
   int relu, both;
 };
+
+// The control wave's trace points per layer: 0 the U phase starts (the
+// previous D signal seen), 1 B1, 2 B2, 3 the U arrival issued, 4 the U signal
+// seen, 5 D1a, 6 D1b, 7 the D arrival issued.
+constexpr int kTokTracePoints = 8;
+constexpr int kTokTraceLayers = 64;
 
 int tok_launch(const TokArgs& a, int npw, hipStream_t st);
 int tok_resident(int npw, int* resident);

@@ -1062,6 +1062,19 @@ int oi2_stack_profile_token(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out,
   return rc;
 }
 
+int oi2_stack_trace_token(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, uint64_t* trace,
+                          size_t trace_bytes, void* stream) {
+  clear_error();
+  OI2_CHECK_ARG(s && x_in && x_out && trace, "null argument");
+  OI2_CHECK_ARG(use_tok(s), "the persistent token kernel is not in use on this stack");
+  const size_t need = (size_t)std::min(s->n_layers, kTokTraceLayers) * kTokGroups * kTokTracePoints * 8;
+  OI2_CHECK_ARG(trace_bytes >= need, "trace buffer of %zu bytes is smaller than the %zu required",
+                trace_bytes, need);
+  TokArgs a = tok_args(s, x_in, x_out);
+  a.trace = trace;
+  return tok_launch(a, s->tok_npw, (hipStream_t)stream);
+}
+
 int oi2_stack_destroy(oi2_stack* s) {
   clear_error();
   if (!s) return OI2_OK;

@@ -182,6 +182,14 @@ __device__ __forceinline__ uint32_t tok_base(const uint32_t* sync, int g) {
   return cld(sync + kSyncGo + 64 * (8 + (g & 7)));
 }
 
+// A trace stamp of the control wave (kept in LDS, copied out at the end, so
+// tracing adds no memory traffic inside the launch).
+#define TOK_TRACE(L, k)                                                              \
+  do {                                                                               \
+    if (TR && (L) >= 0 && (L) < kTokTraceLayers && lane_id() == 0)                   \
+      sh.trace[(L)][(k)] = __builtin_amdgcn_s_memrealtime();                         \
+  } while (0)
+
 struct alignas(16) TokShared {
   uint32_t nat[kH / 2];       // x * w of the layer
   uint32_t xq[kH / 8];        // predictor group: a quarter of x_L,
@@ -202,6 +210,7 @@ struct alignas(16) TokShared {
   float cpart_ctl[kRows];     // the control wave's share of long gather lists
   float out[kRows];
   double z[kTokMaxRank];
+  uint64_t trace[kTokTraceLayers][kTokTracePoints];   // the control wave's stamps, when traced
   float r;
   int total, lst_cnt;
 };
@@ -239,7 +248,7 @@ __device__ __forceinline__ void list_pos(const TokShared& sh, const int (&i)[M],
 
 // ── the control wave ────────────────────────────────────────────────────────
 
-template <int NPW>
+template <int NPW, bool TR>
 __device__ void control(const TokArgs& a, int g, TokShared& sh) {
   const int l = lane_id();
   const int n = a.n_layers;
@@ -298,6 +307,7 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
       CD[i] = half_bits_to_float(bld2(rrec, ro + kOffScales + 2 * (2 * kGroups + (l & (kGroups - 1)))));
     }
     if (L >= 0) tok_wait(a.sync, 1, g, base + (uint32_t)(L + 1), base, a.spin);
+    TOK_TRACE(L, 0);
     // inputs the previous phase produced: x * w into LDS, the sum-of-squares
     // partials, the list's counts, and for a predictor group x_L
     if (T) {
@@ -366,6 +376,7 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
     }
     wait_vm();
     bar();   // B1: x * w, r and the list prefix are in LDS
+    TOK_TRACE(L, 1);
     // a quarter of the next layer's predictor row: z = D q, q =
     // bf16(fp16(x r w')) (pred_d_role's arithmetic and partial sums);
     // stored with the phase's other outputs
@@ -440,6 +451,7 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
       if (l < kGroups) sh.hcs_out[l][k] = hs;
     }
     bar();   // B2: the workers' activations are in LDS
+    TOK_TRACE(L, 2);
     if (pred && l == 0)
       cst8(rsrc(a.z + (size_t)(L + 1) * 4 * kTokMaxRank, 4 * kTokMaxRank * 8), 8 * (uint32_t)g, zrow);
     if (T) {
@@ -465,6 +477,7 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
     // B3 (inside): the stores are acknowledged and the arrival is issued,
     // ahead of the workers' next loads
     tok_arrive(a.sync, 0, g, base + (uint32_t)(L + 2), true);
+    TOK_TRACE(L, 3);
 
     // ================= D phase of layer L (L = -1: only layer 0's selection)
     const bool psel = N && N->pd_w;                      // the next layer's list is predicted
@@ -504,6 +517,7 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
                         l < ch_n ? 4 * (uint32_t)(g * ch_n + l) : kNoOff);
     }
     tok_wait(a.sync, 0, g, base + (uint32_t)(L + 2), base, a.spin);
+    TOK_TRACE(L, 4);
     // inputs the U phase produced: h, the batch's activations x the tile
     // group's down scale (list order), and the next layer's z
     if (T) {
@@ -528,6 +542,7 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
     // take the loaded values into plain registers now, before any store
     asm volatile("" : "+v"(res_v), "+v"(nwv));
     bar();   // D1a: h and the gather activations are in LDS (the workers start)
+    TOK_TRACE(L, 5);
     // the next layer's logits in the fma order of the two-launch path,
     // threshold, LUT hot filter and ascending compaction
     if (psel) {
@@ -562,6 +577,7 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
       sh.lst_cnt = 0;
     }
     bar();   // D1b: the next chunk's list is in LDS
+    TOK_TRACE(L, 6);
     // gather items past the first batch (long lists): this wave, a batch of
     // 64 at a time, while the workers run the first
     float ycc[kRows];
@@ -651,6 +667,14 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
     }
     bar();   // D2: the phase's stores are issued, ahead of the workers' next loads
     tok_arrive(a.sync, 1, g, base + (uint32_t)(L + 2));
+    TOK_TRACE(L, 7);
+  }
+  if (TR) {   // the stamps out, once every layer is done
+    const int nl = n < kTokTraceLayers ? n : kTokTraceLayers;
+    for (int i = l; i < nl * kTokTracePoints; i += kWave) {
+      const int L = i / kTokTracePoints, k = i % kTokTracePoints;
+      a.trace[((size_t)L * kTokGroups + g) * kTokTracePoints + k] = sh.trace[L][k];
+    }
   }
 }
 
@@ -937,13 +961,13 @@ __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
   }
 }
 
-template <int NPW>
+template <int NPW, bool TR = false>
 __global__ __launch_bounds__(kTokThreads) __attribute__((amdgpu_waves_per_eu(2))) void k_token(TokArgs a) {
   __shared__ TokShared sh;
   const int g = blockIdx.x;   // consecutive groups run on different XCDs (g & 7)
   const int w = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   if (w == 0)
-    control<NPW>(a, g, sh);
+    control<NPW, TR>(a, g, sh);
   else
     worker<NPW>(a, g, w - 1, sh);
 }
@@ -951,10 +975,18 @@ __global__ __launch_bounds__(kTokThreads) __attribute__((amdgpu_waves_per_eu(2))
 }  // namespace
 
 int tok_launch(const TokArgs& a, int npw, hipStream_t st) {
-  if (npw == 2)
+  // a traced launch runs its own instantiation: the untraced kernel carries
+  // no trace code at all
+  if (a.trace) {
+    if (npw == 2)
+      hipLaunchKernelGGL((k_token<2, true>), dim3(kTokGroups), dim3(kTokThreads), 0, st, a);
+    else
+      hipLaunchKernelGGL((k_token<3, true>), dim3(kTokGroups), dim3(kTokThreads), 0, st, a);
+  } else if (npw == 2) {
     hipLaunchKernelGGL(k_token<2>, dim3(kTokGroups), dim3(kTokThreads), 0, st, a);
-  else
+  } else {
     hipLaunchKernelGGL(k_token<3>, dim3(kTokGroups), dim3(kTokThreads), 0, st, a);
+  }
   OI2_CHECK_LAUNCH();
   return OI2_OK;
 }

@@ -104,6 +104,7 @@ _SIGS = {
     "oi2_stack_set_wait_bound": (c_int32, [c_void_p, c_int32]),
     "oi2_stack_profile_token": (c_int32, [c_void_p, c_void_p, c_void_p, c_int32, POINTER(c_float),
                                           c_void_p]),
+    "oi2_stack_trace_token": (c_int32, [c_void_p, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     "oi2_stack_destroy": (c_int32, [c_void_p]),
     "oi2_file_store_open": (c_int32, [ctypes.c_char_p, c_void_p, c_int32, c_int32, c_int32,
                                       POINTER(c_void_p)]),

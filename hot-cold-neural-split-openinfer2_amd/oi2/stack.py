@@ -90,6 +90,21 @@ class DecodeStack:
                                                       int(reps), ctypes.byref(us), s or None))
         return us.value
 
+    TRACE_POINTS = ("U start", "B1 U inputs in", "B2 U products in", "U arrival issued",
+                    "U signal seen", "D1a D inputs in", "D1b next list in", "D arrival issued")
+
+    def trace_token(self, x_in: torch.Tensor, x_out: torch.Tensor, stream=None) -> torch.Tensor:
+        """Decode x_in once on the persistent token kernel with its control
+        waves stamping eight points of every layer (TRACE_POINTS) on the
+        device's 100 MHz counter.  Returns an int64 device tensor (layers up
+        to 64, 256 groups, 8 points) of raw counter values."""
+        n = min(len(self.layers), 64)
+        t = torch.zeros((n, 256, len(self.TRACE_POINTS)), dtype=torch.int64, device=x_in.device)
+        s = stream.cuda_stream if stream is not None else _lib.stream_handle(x_in.device)
+        _lib.check(_lib.lib().oi2_stack_trace_token(self._h, x_in.data_ptr(), x_out.data_ptr(), t.data_ptr(),
+                                                    t.numel() * 8, s or None))
+        return t
+
     def selection_layout(self) -> tuple[int, int]:
         """(n_chunks, chunk) of the active sets trace() returns."""
         nc, ch = ctypes.c_int32(), ctypes.c_int32()

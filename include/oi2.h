@@ -320,6 +320,17 @@ int oi2_stack_set_wait_bound(oi2_stack* s, int32_t polls);
  * state of decoding x_in. */
 int oi2_stack_profile_token(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, int32_t reps,
                             float* token_us, void* stream);
+/* No counterpart in the reference (the reference's profiler times whole
+ * layers from the host): decodes x_in once on the persistent token kernel
+ * with its control waves stamping s_memrealtime (a 100 MHz counter) at eight
+ * points of every layer, and writes the stamps to `trace` (device memory),
+ * laid out (min(n_layers, 64), 256 groups, 8 points) as uint64: 0 the U phase
+ * starts, 1 its inputs are in LDS (B1), 2 the U products are in LDS (B2),
+ * 3 the U arrival is issued, 4 the U signal is seen, 5 the D inputs are in
+ * LDS (D1a), 6 the next list is in LDS (D1b), 7 the D arrival is issued.
+ * Leaves the state of decoding x_in; the stamps stay in LDS until the end. */
+int oi2_stack_trace_token(oi2_stack* s, const uint16_t* x_in, uint16_t* x_out, uint64_t* trace,
+                          size_t trace_bytes, void* stream);
 int oi2_stack_destroy(oi2_stack* s);
 
 /* ---- cold records read from the split file ------------------------------ */

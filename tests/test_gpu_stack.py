@@ -292,6 +292,30 @@ def test_token_kernel_matches_two_launches(stack4):
     assert torch.equal(res[True][0], res[True][1][-1])
 
 
+def test_token_trace_stamps_phases_in_order(stack4):
+    """The traced launch decodes the same bits as a plain one, and every
+    group's control-wave stamps of every layer run in phase order, each layer
+    after the previous one; no group sees a signal before the last arrival."""
+    dev, g, layers, st, thr = stack4
+    x_in = torch.randn(H, generator=g, device=dev).half()
+    ref, out = torch.empty_like(x_in), torch.empty_like(x_in)
+    st.decode(x_in, ref, None)
+    t = st.trace_token(x_in, out, None)
+    st.status()
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    a = t.cpu().numpy().astype(np.int64)
+    assert a.shape == (4, 256, 8) and (a > 0).all()
+    assert (np.diff(a, axis=2) >= 0).all()
+    assert (a[1:, :, 0] >= a[:-1, :, 7]).all()
+    # a signal is seen after every group's arrival; the slack (1 us of 10 ns
+    # ticks) covers the last arriver taking its stamp after issuing the flag
+    for L in range(4):
+        assert a[L, :, 4].min() >= a[L, :, 3].max() - 100
+        if L + 1 < 4:
+            assert a[L + 1, :, 0].min() >= a[L, :, 7].max() - 100
+
+
 @pytest.mark.parametrize("n_hot,activation,both,shift", [(4000, "silu", False, 0.0), (3584, "relu", True, -1.66)],
                          ids=["three_hot_rows_per_wave", "drelu_with_gate_bias"])
 def test_token_kernel_other_geometries(n_hot, activation, both, shift):
