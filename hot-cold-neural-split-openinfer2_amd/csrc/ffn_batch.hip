@@ -1340,66 +1340,75 @@ template <int MS>
 __global__ __launch_bounds__(kThreads) void k_bdown_hot_s(BDownArgs a) {
   static_assert(MS == 1, "at most 16 tokens");
   constexpr int NBmax = 8;   // ldh <= 4096: at most 32 blocks, 8 per wave
+  constexpr int kPre = 16;   // cold ranges whose partial sums are loaded up front
   __shared__ f32x4 s_red[3][MS][kWave];
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = lane_id();
   const int h = blockIdx.x * 16 + (l & 15);
-  // the epilogue's inputs (wave 0: output h, tokens 4 (l >> 4) + e): the cold
-  // ranges' partial sums added in range order, the row scale, the residual
-  f32x4 yc = {0.f, 0.f, 0.f, 0.f};
-  float sd = 0.f, rv[4] = {0.f, 0.f, 0.f, 0.f};
-  if (w == 0) {
-    // 16 ranges' loads in flight at a time, then their sums in range order
-    const f32x4* pp = reinterpret_cast<const f32x4*>(a.part + (size_t)h * 16 + 4 * (l >> 4));
-    for (int s0 = 0; s0 < a.n_part; s0 += 16) {
-      f32x4 pv[16];
+  // Every load is issued before any is used, all unconditional (past a range
+  // reads zero), so each step waits only for its own: first wave 0's epilogue
+  // inputs (output h, tokens 4 (l >> 4) + e: the first kPre cold ranges'
+  // partial sums, the row scale, the residual), then every wave's activation
+  // fragments and down rows.
+  const rsrc_t rp = buf_rsrc(a.part, (uint32_t)a.n_part * kH * 16 * 4);
+  const uint32_t pofs = ((uint32_t)h * 16 + 4 * (l >> 4)) * 4;
+  u32x4 pv[kPre];
 #pragma unroll
-      for (int u = 0; u < 16; ++u)
-        pv[u] = s0 + u < a.n_part ? pp[(size_t)(s0 + u) * kH * 4] : f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int u = 0; u < kPre; ++u)
+    pv[u] = bload16(rp, (w == 0 && u < a.n_part) ? pofs + (uint32_t)u * kH * 16 * 4 : kNoOffset, 0);
+  const float sd = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                 buf_rsrc(a.down_s, kH * 4), 4 * (uint32_t)h, 0, 0));
+  const rsrc_t rres = buf_rsrc(a.res, a.res ? (uint32_t)a.M * kH * 2 : 0u);
+  uint16_t rb[4];
 #pragma unroll
-      for (int u = 0; u < 16; ++u) yc += pv[u];
-    }
-    sd = a.down_s[h];
-    if (a.res) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int t = 4 * (l >> 4) + e;
-        if (t < a.M) rv[e] = half_bits_to_float(a.res[(size_t)t * kH + h]);
-      }
-    }
+  for (int e = 0; e < 4; ++e) {
+    const int t = 4 * (l >> 4) + e;
+    rb[e] = bload2(rres, w == 0 && t < a.M ? ((uint32_t)t * kH + h) * 2 : kNoOffset, 0);
   }
   const int nb = a.hot_blocks;
   const int b0 = w * nb / 4, b1 = (w + 1) * nb / 4;
   const int m = l & 15;
-  const bool av = m < a.M;
-  const uint16_t* hr = a.hh + (size_t)(av ? m : 0) * a.ldh + 32 * (l >> 4);
+  const rsrc_t rh = buf_rsrc(a.hh, (uint32_t)a.M * a.ldh * 2);
+  const uint32_t hro = m < a.M ? ((uint32_t)m * a.ldh + 32 * (l >> 4)) * 2 : kNoOffset;
   h8 A[NBmax][4];
 #pragma unroll
   for (int b = 0; b < NBmax; ++b)
 #pragma unroll
     for (int s = 0; s < 4; ++s)
-      A[b][s] = (av && b0 + b < b1) ? *reinterpret_cast<const h8*>(hr + (b0 + b) * kBK + 8 * s) : h8{};
-  const uint8_t* dr = a.down_q + (size_t)h * a.down_stride + 32 * (l >> 4);
+      A[b][s] = __builtin_bit_cast(
+          h8, bload16(rh, b0 + b < b1 ? hro + ((uint32_t)(b0 + b) * kBK + 8 * s) * 2 : kNoOffset, 0));
+  const rsrc_t rd = buf_rsrc(a.down_q, (uint32_t)kH * a.down_stride);
   u32x4 D[NBmax][2];
 #pragma unroll
   for (int b = 0; b < NBmax; ++b) {
     const int k = (b0 + b) * kBK + 32 * (l >> 4);
-    const u32x4 z = {0u, 0u, 0u, 0u};
+    const uint32_t ro = (uint32_t)h * a.down_stride + k;
     const bool in = b0 + b < b1;
-    D[b][0] = (in && k < a.down_stride) ? load16(dr + (b0 + b) * kBK) : z;
-    D[b][1] = (in && k + 16 < a.down_stride) ? load16(dr + (b0 + b) * kBK + 16) : z;
+    D[b][0] = bload16(rd, (in && k < a.down_stride) ? ro : kNoOffset, 0);
+    D[b][1] = bload16(rd, (in && k + 16 < a.down_stride) ? ro + 16 : kNoOffset, 0);
   }
+  __builtin_amdgcn_sched_barrier(0);
+  // wave 0: the cold ranges' partial sums in range order (past kPre, loaded now)
+  f32x4 yc = {0.f, 0.f, 0.f, 0.f};
+  if (w == 0) {
+#pragma unroll
+    for (int u = 0; u < kPre; ++u)
+      yc += f32x4{as_f32(pv[u].x), as_f32(pv[u].y), as_f32(pv[u].z), as_f32(pv[u].w)};
+    for (int u = kPre; u < a.n_part; ++u) {
+      const u32x4 v = bload16(rp, pofs + (uint32_t)u * kH * 16 * 4, 0);
+      yc += f32x4{as_f32(v.x), as_f32(v.y), as_f32(v.z), as_f32(v.w)};
+    }
+  }
+  // blocks past this wave's share hold zeros and add nothing
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int b = 0; b < NBmax; ++b) {
-    if (b0 + b >= b1) break;
+  for (int b = 0; b < NBmax; ++b)
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const h8 bv = fp8x8_h8(dword_of(D[b][0], D[b][1], 2 * s), dword_of(D[b][0], D[b][1], 2 * s + 1));
       acc = mfma16(A[b][s], bv, acc);
     }
-  }
   if (w > 0) s_red[w - 1][0][l] = acc;
-  __syncthreads();
+  lds_barrier();
   if (w != 0) return;
   const f32x4 v = acc + s_red[0][0][l] + s_red[1][0][l] + s_red[2][0][l];
 #pragma unroll
@@ -1409,7 +1418,7 @@ __global__ __launch_bounds__(kThreads) void k_bdown_hot_s(BDownArgs a) {
     const size_t i = (size_t)t * kH + h;
     const float y = yc[e] + v[e] * sd;
     if (a.y32) a.y32[i] = y;
-    if (a.out) a.out[i] = float_to_half_bits(rv[e] + y);
+    if (a.out) a.out[i] = float_to_half_bits(half_bits_to_float(rb[e]) + y);
   }
 }
 
