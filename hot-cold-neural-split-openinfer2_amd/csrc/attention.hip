@@ -515,6 +515,152 @@ __global__ __launch_bounds__(kThreads) void k_attn_sdpa(SdpaArgs a) {
   }
 }
 
+// Attention of query row r, query head hq, against its kv head's positions
+// [0, n_r) in one workgroup, for spans of at most kOneWgMax positions: no
+// partial sum leaves the workgroup, so there is no store to acknowledge, no
+// arrival and no second pass over partial sums.  Workgroup x takes kv head
+// g = x mod n_kv and query head hq = g G + x / n_kv, so that with 8 kv heads
+// the G workgroups reading one kv head's cache share an XCD (and its L2).
+// The 16 waves take chunks of 16 positions in turn (chunk c goes to wave
+// c mod 16); each wave keeps a running max, exp-sum and weighted V sum,
+// rescaled when a chunk raises the max, with its next chunk's K / V loads in
+// flight while it computes the current one.  The waves meet in LDS at the
+// end.  Lane (k = lane >> 4, jj = lane & 15) holds dims [8 jj, 8 jj + 8) of
+// position 16 c + 4 step + k, as in k_attn_sdpa; positions past n_r read zero
+// through the descriptors' range and score -inf.
+constexpr int kOneWgThreads = 1024;
+constexpr int kOneWgMax = 1024;
+
+__global__ __launch_bounds__(kOneWgThreads) void k_attn_sdpa1(SdpaArgs a, int G) {
+  constexpr int kW = kOneWgThreads / kWave;
+  constexpr int ST = 4;                           // steps of 4 positions per chunk
+  constexpr int kChunk = 4 * ST;
+  __shared__ __align__(16) float s_o[kW][kHd];
+  __shared__ float s_m[kW], s_l[kW];
+  const int g = blockIdx.x % a.n_kv, hq = g * G + blockIdx.x / a.n_kv, r = blockIdx.y;
+  const int tid = threadIdx.x, lane = lane_id(), k = lane >> 4, jj = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int b = r / a.seq, t = r - b * a.seq;
+  const int n_r = a.causal ? a.past + t + 1 : a.past + a.seq;
+  const int width = a.n_kv * G * kHd;
+  const float ninf = -__builtin_inff();
+
+  const u32x4 qv = *reinterpret_cast<const u32x4*>(a.q + (size_t)r * width + hq * kHd + 8 * jj);
+  const size_t head = ((size_t)b * a.n_kv + g) * a.cap * kHd;
+  const rsrc_t rk = make_rsrc(a.k_cache + head, (uint32_t)n_r * kHd * 2);
+  const rsrc_t rv = make_rsrc(a.v_cache + head, (uint32_t)n_r * kHd * 2);
+  const int n_ch = (n_r + kChunk - 1) / kChunk;
+
+  auto issue = [&](int c, u32x4 (&kr)[ST], u32x4 (&vr)[ST]) {
+#pragma unroll
+    for (int it = 0; it < ST; ++it)
+      kr[it] = __builtin_amdgcn_raw_buffer_load_b128(
+          rk, (uint32_t)(kChunk * c + 4 * it + k) * (kHd * 2) + 16 * jj, 0, 0);
+#pragma unroll
+    for (int it = 0; it < ST; ++it)
+      vr[it] = __builtin_amdgcn_raw_buffer_load_b128(
+          rv, (uint32_t)(kChunk * c + 4 * it + k) * (kHd * 2) + 16 * jj, 0, 0);
+  };
+
+  float m = ninf, l = 0.0f, o[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = 0.0f;
+  auto chunk = [&](int c, const u32x4 (&kr)[ST], const u32x4 (&vr)[ST]) {
+    float s[ST];
+#pragma unroll
+    for (int it = 0; it < ST; ++it) {
+      float d = 0.0f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) d = dot2(as_f16x2(kr[it][q]), as_f16x2(qv[q]), d);
+      s[it] = d;
+    }
+#pragma unroll
+    for (int e = 0; e < ST; ++e) s[e] += dpp_f<0xB1>(s[e]);
+#pragma unroll
+    for (int e = 0; e < ST; ++e) s[e] += dpp_f<0x4E>(s[e]);
+#pragma unroll
+    for (int e = 0; e < ST; ++e) s[e] += dpp_f<0x141>(s[e]);
+#pragma unroll
+    for (int e = 0; e < ST; ++e) s[e] += dpp_f<0x140>(s[e]);
+    float cm = ninf;
+#pragma unroll
+    for (int it = 0; it < ST; ++it) {
+      s[it] = kChunk * c + 4 * it + k < n_r ? s[it] * a.scale : ninf;
+      cm = fmaxf(cm, s[it]);
+    }
+    cm = fmaxf(cm, __shfl_xor(cm, 16));
+    cm = fmaxf(cm, __shfl_xor(cm, 32));
+    const float mn = fmaxf(m, cm);
+    // the running sums were taken against m; a chunk with a larger score
+    // rescales them (exp(-inf) = 0 before the first valid score)
+    const float alpha = mn == ninf ? 1.0f : __expf(m - mn);
+    l *= alpha;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] *= alpha;
+    m = mn;
+#pragma unroll
+    for (int it = 0; it < ST; ++it) {
+      const float p = s[it] == ninf ? 0.0f : __expf(s[it] - m);
+      l += p;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        o[2 * d] = fmaf(p, half_lo(vr[it][d]), o[2 * d]);
+        o[2 * d + 1] = fmaf(p, half_hi(vr[it][d]), o[2 * d + 1]);
+      }
+    }
+  };
+
+  // two register sets in turn: the next chunk's loads go out before the
+  // current chunk's arithmetic (past the last chunk they read zero and
+  // move no data)
+  if (wave < n_ch) {
+    u32x4 ka[ST], va[ST], kb[ST], vb[ST];
+    int c = wave;
+    issue(c, ka, va);
+    for (;;) {
+      issue(c + kW, kb, vb);
+      __builtin_amdgcn_sched_barrier(0);   // the loads stay ahead of the arithmetic
+      chunk(c, ka, va);
+      c += kW;
+      if (c >= n_ch) break;
+      issue(c + kW, ka, va);
+      __builtin_amdgcn_sched_barrier(0);
+      chunk(c, kb, vb);
+      c += kW;
+      if (c >= n_ch) break;
+    }
+  }
+  l += __shfl_xor(l, 16);
+  l += __shfl_xor(l, 32);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    o[e] += __shfl_xor(o[e], 16);
+    o[e] += __shfl_xor(o[e], 32);
+  }
+  if (k == 0) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) s_o[wave][8 * jj + e] = o[e];
+  }
+  if (lane == 0) {
+    s_m[wave] = m;
+    s_l[wave] = l;
+  }
+  __syncthreads();
+  if (tid < kHd) {
+    float M = ninf;
+#pragma unroll
+    for (int w = 0; w < kW; ++w) M = fmaxf(M, s_m[w]);
+    float O = 0.0f, L = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kW; ++w) {
+      const float sc = s_m[w] == ninf ? 0.0f : __expf(s_m[w] - M);
+      O = fmaf(sc, s_o[w][tid], O);
+      L = fmaf(sc, s_l[w], L);
+    }
+    a.out[(size_t)r * width + hq * kHd + tid] = float_to_half_bits(O * (1.0f / L));
+  }
+}
+
 inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 inline int part_stride_floats(int G) { return ((G * kHd + 2 * G) + 31) & ~31; }
@@ -545,6 +691,10 @@ void launch_sdpa_g(const SdpaArgs& a, int steps, int rows, size_t lds, hipStream
     case 4: hipLaunchKernelGGL((k_attn_sdpa<G, 4>), grid, dim3(kThreads), lds, st, a); break;
     default: hipLaunchKernelGGL((k_attn_sdpa<G, 8>), grid, dim3(kThreads), lds, st, a); break;
   }
+}
+
+void launch_sdpa1(const SdpaArgs& a, int G, int rows, hipStream_t st) {
+  hipLaunchKernelGGL(k_attn_sdpa1, dim3(a.n_kv * G, rows), dim3(kOneWgThreads), 0, st, a, G);
 }
 
 void launch_sdpa(const SdpaArgs& a, int G, int steps, int rows, size_t lds, hipStream_t st) {
@@ -670,21 +820,28 @@ int oi2_attn_forward(const uint16_t* x, int32_t batch, int32_t seq, const oi2_at
   s.past = past;
   s.seq = seq;
   s.causal = causal ? 1 : 0;
-  const int steps = choose_steps(rows, n_kv, past + seq);
-  s.n_split = (past + seq + 16 * steps - 1) / (16 * steps);
-  s.part_stride = part_stride_floats(G);
-  const size_t tab = (size_t)2 * s.n_split * G * sizeof(float);
-  if (tab > (size_t)kMaxTabBytes) {
-    set_error("%d positions need %d sequence splits; the merge table holds %d", past + seq, s.n_split,
-              kMaxTabBytes / (int)(2 * G * sizeof(float)));
-    return OI2_EUNSUPPORTED;
-  }
   s.scale = 1.0f / sqrtf((float)kHd);
-  s.part = part;
-  s.counters = counters;
   s.out = attn;
-  launch_sdpa(s, G, steps, rows, tab, st);
-  OI2_CHECK_LAUNCH();
+  if (past + seq <= kOneWgMax) {
+    // short spans: the whole span in one workgroup per (row, query head)
+    s.n_split = 1;
+    launch_sdpa1(s, G, rows, st);
+    OI2_CHECK_LAUNCH();
+  } else {
+    const int steps = choose_steps(rows, n_kv, past + seq);
+    s.n_split = (past + seq + 16 * steps - 1) / (16 * steps);
+    s.part_stride = part_stride_floats(G);
+    const size_t tab = (size_t)2 * s.n_split * G * sizeof(float);
+    if (tab > (size_t)kMaxTabBytes) {
+      set_error("%d positions need %d sequence splits; the merge table holds %d", past + seq, s.n_split,
+                kMaxTabBytes / (int)(2 * G * sizeof(float)));
+      return OI2_EUNSUPPORTED;
+    }
+    s.part = part;
+    s.counters = counters;
+    launch_sdpa(s, G, steps, rows, tab, st);
+    OI2_CHECK_LAUNCH();
+  }
 
   GemvArgs o{};
   o.norm_w = nullptr;
