@@ -90,10 +90,12 @@ def _rand_cache(dev, B, n_kv, past, seed):
 
 
 @pytest.mark.parametrize("B,past,n_kv", [(1, 5, 8), (1, 37, 8), (3, 300, 8), (1, 4095, 8), (3, 1000, 8), (2, 100, 32),
-                                         (2, 129, 4), (1, 255, 16)])
+                                         (2, 129, 4), (1, 255, 16), (1, 1023, 8), (2, 1024, 8)])
 def test_decode_step_against_oracle(dev, B, past, n_kv):
     """One token per sequence over a cache from elsewhere (copied into the
-    layer's buffer): 1 to 32 sequence splits, query groups of 1, 2, 4, 8."""
+    layer's buffer): query groups of 1, 2, 4, 8; spans up to 1024 positions
+    in one workgroup per query head (1024 itself included), longer ones split
+    over the sequence (1025 and 4096 positions)."""
     w = _weights(dev, n_kv, seed=past + n_kv)
     attn = oi2.GroupedQueryAttention(0, w, _cfg(n_kv))
     cos, sin = oi2.rope_tables(past + 8, D, 10000.0, device=dev)
