@@ -8,8 +8,11 @@
 //                      rest and widens to fp16, engine.py:80-83), RoPE on q
 //                      and k (engine.py:102-103, 140-157), q to a buffer and
 //                      k, v appended to the cache at past + t (engine.py:105-109)
-//   k_attn_sdpa        attention of every query row over its visible cache
-//                      positions (engine.py:114-121): split over the sequence,
+//   k_attn_sdpa1       attention of every query row over its visible cache
+//                      positions (engine.py:114-121) for spans of at most
+//                      1024 positions: one workgroup per (row, query head)
+//                      reads the whole span and writes the output
+//   k_attn_sdpa        the same for longer spans: split over the sequence,
 //                      every K / V row read once for the group's query heads;
 //                      the last workgroup of a (row, kv head) merges the splits
 //   k_attn_gemv (out)  out = fp16(attn W_o^T) (engine.py:122-123), and
