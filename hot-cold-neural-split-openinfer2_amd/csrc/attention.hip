@@ -524,19 +524,20 @@ __global__ __launch_bounds__(kThreads) void k_attn_sdpa(SdpaArgs a) {
 // arrival and no second pass over partial sums.  Workgroup x takes kv head
 // g = x mod n_kv and query head hq = g G + x / n_kv, so that with 8 kv heads
 // the G workgroups reading one kv head's cache share an XCD (and its L2).
-// The 16 waves take chunks of 16 positions in turn (chunk c goes to wave
-// c mod 16); each wave keeps a running max, exp-sum and weighted V sum,
-// rescaled when a chunk raises the max, with its next chunk's K / V loads in
-// flight while it computes the current one.  The waves meet in LDS at the
+// The 16 waves take chunks of 8 positions in turn (chunk c goes to wave
+// c mod 16: at 513 positions 65 chunks, 4 or 5 per wave, against 2 or 3 for
+// chunks of 16, 1.4 % slower); each wave keeps a running max, exp-sum and
+// weighted V sum, rescaled when a chunk raises the max, with its next
+// chunk's K / V loads in flight while it computes the current one.  The waves meet in LDS at the
 // end.  Lane (k = lane >> 4, jj = lane & 15) holds dims [8 jj, 8 jj + 8) of
-// position 16 c + 4 step + k, as in k_attn_sdpa; positions past n_r read zero
+// position 8 c + 4 step + k, as in k_attn_sdpa; positions past n_r read zero
 // through the descriptors' range and score -inf.
 constexpr int kOneWgThreads = 1024;
 constexpr int kOneWgMax = 1024;
 
 __global__ __launch_bounds__(kOneWgThreads) void k_attn_sdpa1(SdpaArgs a, int G) {
   constexpr int kW = kOneWgThreads / kWave;
-  constexpr int ST = 4;                           // steps of 4 positions per chunk
+  constexpr int ST = 2;                           // steps of 4 positions per chunk
   constexpr int kChunk = 4 * ST;
   __shared__ __align__(16) float s_o[kW][kHd];
   __shared__ float s_m[kW], s_l[kW];
