@@ -89,10 +89,12 @@ def cpu_baseline(layers, tokens, max_seconds):
     tokens, layer by layer, until max_seconds of timed CPU work.
 
     tokens: list of (xs_in (32 fp16 layer inputs), active cold ids per layer)."""
+    import numpy as np
     import torch
     from oracle import baseline_cpu as B
     secs = cold_secs = 0.0
     neurons = n_steps = 0
+    calls, fetches, call_neurons = [], [], []
     for L in range(N_LAYERS):
         if secs >= max_seconds:
             break
@@ -106,7 +108,10 @@ def cpu_baseline(layers, tokens, max_seconds):
             x = xs_in[L].float().cpu()[None]
             xn = x * torch.rsqrt((x * x).mean(-1, keepdim=True) + EPS) * w
             samples.append((xn, hot, buf, offs, active[L]))
-        dt, dc, nn = B.time_layers(samples, threads=1)
+        dt, dc, nn, cl, fe = B.time_layers(samples, threads=1)
+        calls += cl
+        fetches += fe
+        call_neurons += [len(a) for (_, _, _, _, a) in samples]
         secs += dt
         cold_secs += dc
         neurons += nn
@@ -131,6 +136,13 @@ def cpu_baseline(layers, tokens, max_seconds):
         "seconds": secs,
         "cold_seconds": cold_secs,
         "cold_neurons_per_s": neurons / cold_secs,
+        # per layer call (one layer of one token, the reference's FFN call),
+        # the median over every timed call
+        "layer_calls": len(calls),
+        "median_layer_call_ms": float(np.median(calls)) * 1e3,
+        "median_cold_fetch_ms": float(np.median(fetches)) * 1e3,
+        "median_cold_neurons_per_call": float(np.median(call_neurons)),
+        "median_call_cold_neurons_per_s": float(np.median(np.array(call_neurons) / np.array(fetches))),
     }
 
 
@@ -414,6 +426,180 @@ def measure_batch8_file(dev, steps, warmup, seed=4):
         f"{k['weight_gbs']:.0f} GB/s ({k['weight_gbs'] / HBM_PEAK_GBS:.3f} of HBM peak)")
     del layers
     tmp.cleanup()
+    return out
+
+
+def _graph_us(fn, dev, reps):
+    """Mean microseconds of one replay of a graph capturing fn() (GPU time,
+    events on the replay stream), after an eager warm-up call."""
+    import torch
+    stream = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(stream):
+        fn()
+    stream.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        out = fn()
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / reps
+    del graph
+    return us, out
+
+
+def measure_config1(dev, reps=20, seed=11, n_layers=32):
+    """Config 1: one SwiGLU layer, 2867 hot fp8 neurons with per-row fp32
+    scales, the other 11469 cold INT4 records, a fixed uniform-random 10 %
+    (1147) of them active, one fp16 token.  The per-layer call
+    (oi2_ffn_forward: RMSNorm, hot and cold gate/up, activation, down,
+    residual; engine.py:292-312) on n_layers distinct seeded layers chained
+    back to back (1.4 GB of weights: no layer's bytes come from a cache),
+    captured in one graph; and the same layers through the persistent token
+    kernel (a stack of layers without predictors whose records are the
+    active ones).  Reported per layer-token."""
+    import torch
+    from oi2.layer import ColdNeurons, _ffn
+    from oi2.stack import DecodeStack, StackLayer
+    from oi2.store import ColdSection
+    from oi2.synth import SyntheticLayer
+    n_hot, n_act = 2867, 1147
+    g = torch.Generator(device=dev).manual_seed(seed)
+    layers, colds, stack_layers = [], [], []
+    for _ in range(n_layers):
+        lay = SyntheticLayer(g, INTER, n_hot, std=0.02, device=dev, per_row_scale=True)
+        n_cold = lay.records.shape[0]
+        slots = torch.randperm(n_cold, generator=g, device=dev)[:n_act].sort().values.int()
+        sec = ColdSection(0, lay.cold_ids.cpu().numpy(), lay.records, lay.lut, lay.lut.cpu().numpy(), INTER)
+        colds.append(ColdNeurons.from_slots(sec, slots))
+        # the stack's layer holds only the active records (ascending id), so
+        # its fixed list (every record of the layer) is the same active set
+        act_ids = lay.cold_ids[slots.long()]
+        lut = torch.full((INTER,), -1, dtype=torch.int32, device=dev)
+        lut[act_ids] = torch.arange(n_act, dtype=torch.int32, device=dev)
+        stack_layers.append(StackLayer(lay.hot, lay.records[slots.long()].contiguous(), lut, lay.norm_w, None))
+        layers.append(lay)
+    x0 = torch.randn((1, H), generator=g, device=dev).half()
+
+    def chain():
+        x = x0
+        for l, c in zip(layers, colds):
+            x = _ffn(x, l.norm_w, EPS, l.hot, c, "silu", False, add_residual=True)
+        return x
+
+    us, y_call = _graph_us(chain, dev, reps)
+    st = DecodeStack(stack_layers, INTER, EPS, "silu", False, 0.0)
+    tok_us = None
+    y_tok = torch.empty_like(x0[0])
+    stream = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(stream):
+        st.decode(x0[0], y_tok, stream)
+    stream.synchronize()
+    st.status(stream)
+    same = None
+    if st.token_kernel:
+        xo = torch.empty_like(x0[0])
+        with torch.cuda.stream(stream):
+            tok_us = st.profile_token(x0[0], xo, stream, reps=8)
+        st.status(stream)
+        torch.cuda.synchronize()
+        same = bool(torch.equal(xo, y_tok))
+    # the two paths agree to the FFN bar (their sums run in other orders)
+    a, b = y_call[0].double(), y_tok.double()
+    rel = float((a - b).abs().max() / b.abs().max())
+    st.close()
+    layer_bytes = (n_hot * 3 * H + 2 * n_hot * 4 + H * 4 + n_act * 6400 + 3 * H * 2)
+    per = us / n_layers
+    out = {"workload": "config 1: one SwiGLU layer 4096x14336, 2867 hot fp8 (per-row scales), "
+                       "1147 of 11469 cold INT4 records active (uniform random 10 %), batch 1",
+           "layers_timed": n_layers, "bytes_per_layer_token": layer_bytes,
+           "per_layer_call": {"us_per_layer_token": per,
+                              "hbm_gbs": layer_bytes / (per * 1e-6) / 1e9,
+                              "frac_of_hbm_peak": layer_bytes / (per * 1e-6) / 1e9 / HBM_PEAK_GBS,
+                              "kernels": "k_ffn_up + k_ffn_down (oi2_ffn_forward), graph-replayed"},
+           "ideal_us_at_hbm_peak": layer_bytes / (HBM_PEAK_GBS * 1e9) * 1e6,
+           "target_us_at_60pct": layer_bytes / (0.6 * HBM_PEAK_GBS * 1e9) * 1e6,
+           "token_kernel_vs_per_layer_call_rel_err": rel}
+    if tok_us is not None:
+        pt = tok_us / n_layers
+        out["token_kernel"] = {"us_per_layer_token": pt, "hbm_gbs": layer_bytes / (pt * 1e-6) / 1e9,
+                               "frac_of_hbm_peak": layer_bytes / (pt * 1e-6) / 1e9 / HBM_PEAK_GBS,
+                               "kernel": "k_token, the 32 layers in one launch (profile_token)",
+                               "profiled_output_equals_decode": same}
+    del layers, colds, stack_layers
+    return out
+
+
+def measure_config2(dev, B=64, reps=10, seed=12, n_layers=16):
+    """Config 2: one dReLU (TurboSparse-style) layer at 4096x14336,
+    y = down(relu(gate x + b) * relu(up x)), gate pre-activations shifted by
+    b = -1.3 sigma (sigma = 0.02 sqrt(4096)), 25 % hot fp8, the rest cold
+    INT4; a batch of B independent fp16 tokens x ~ N(0, 1) sharing one cold
+    set, the union of the tokens' true firing sets (relu(g) relu(u) != 0 over
+    the served INT4 weights, profiler.py:130's definition).  n_layers
+    distinct seeded layers, each called on the same batch (1.8 GB of weights
+    in all), captured in one graph.  Reported per layer call."""
+    import math
+    import torch
+    from oi2 import _lib
+    from oi2.layer import ColdNeurons, _ffn, rmsnorm
+    from oi2.store import ColdSection
+    from oi2.synth import SyntheticLayer
+    n_hot = 3584
+    sigma = 0.02 * math.sqrt(H)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    x = torch.randn((B, H), generator=g, device=dev).half()
+    layers, colds, fire_tok, union_n = [], [], [], []
+    L = _lib.lib()
+    for _ in range(n_layers):
+        lay = SyntheticLayer(g, INTER, n_hot, std=0.02, device=dev, gate_bias_shift=-1.3 * sigma)
+        n = lay.records.shape[0]
+        gate = torch.empty((n, H), dtype=torch.float32, device=dev)
+        up = torch.empty((n, H), dtype=torch.float32, device=dev)
+        down = torch.empty((H, n), dtype=torch.float32, device=dev)
+        allslots = torch.arange(n, dtype=torch.int32, device=dev)
+        _lib.check(L.oi2_dequant_records(lay.records.data_ptr(), n, allslots.data_ptr(), n, gate.data_ptr(),
+                                         up.data_ptr(), down.data_ptr(), _lib.stream_handle(dev)))
+        xn = rmsnorm(x, lay.norm_w, EPS).float()
+        fire = (torch.relu(xn @ gate.t() + lay.cold_gate_bias) * torch.relu(xn @ up.t())) != 0
+        fire_tok.append(float(fire.float().sum(1).mean()) / n)
+        union = fire.any(0).nonzero().flatten().int()
+        union_n.append(int(union.numel()))
+        del gate, up, down, fire
+        sec = ColdSection(0, lay.cold_ids.cpu().numpy(), lay.records, lay.lut, lay.lut.cpu().numpy(), INTER)
+        colds.append(ColdNeurons.from_slots(sec, union, gate_bias=lay.cold_gate_bias))
+        layers.append(lay)
+    torch.cuda.empty_cache()
+
+    def calls():
+        return [_ffn(x, l.norm_w, EPS, l.hot, c, "relu", True, add_residual=True)
+                for l, c in zip(layers, colds)]
+
+    us, outs = _graph_us(calls, dev, reps)
+    assert all(torch.isfinite(o.float()).all() for o in outs)
+    per = us / n_layers
+    mean_union = sum(union_n) / n_layers
+    layer_bytes = (n_hot * 3 * H + 3 * n_hot * 4 + H * 4 + mean_union * (6400 + 4) + 2 * B * H * 2 + H * 2)
+    flop = 2 * B * H * (n_hot + mean_union) * 3
+    out = {"workload": f"config 2: one dReLU layer 4096x14336, gate bias -1.3 sigma, 3584 hot fp8, "
+                       f"batch {B} of independent tokens over the union of their true firing sets",
+           "layers_timed": n_layers, "batch": B,
+           "firing_per_token_frac_of_cold": sum(fire_tok) / n_layers,
+           "union_records_mean": mean_union,
+           "union_frac_of_cold": mean_union / (INTER - n_hot),
+           "us_per_layer": per, "bytes_per_layer": layer_bytes,
+           "hbm_gbs": layer_bytes / (per * 1e-6) / 1e9,
+           "frac_of_hbm_peak": layer_bytes / (per * 1e-6) / 1e9 / HBM_PEAK_GBS,
+           "ideal_us_at_hbm_peak": layer_bytes / (HBM_PEAK_GBS * 1e9) * 1e6,
+           "tflops": flop / (per * 1e-6) / 1e12,
+           "frac_of_fp16_dense_peak": flop / (per * 1e-6) / 1e12 / 2500.0,
+           "kernels": "oi2_ffn_forward at batch 64 (matrix-core batch kernels), graph-replayed"}
+    del layers, colds
     return out
 
 
@@ -713,6 +899,10 @@ def main():
     ap.add_argument("--attention-only", action="store_true")
     ap.add_argument("--multi-token-only", action="store_true",
                     help="only the multi-token (batch decode / prefill) leg")
+    ap.add_argument("--configs-only", action="store_true",
+                    help="only the single-layer legs: config 1 (bs1 SwiGLU) and config 2 (B=64 dReLU)")
+    ap.add_argument("--no-configs", dest="configs", action="store_false",
+                    help="skip the single-layer config 1 / config 2 legs")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 256 MiB device copy 8 times (the reference kernel "
@@ -749,6 +939,17 @@ def main():
         for side in ("drop_in_layers", "stack_layers"):
             log(f"full decode step ({side}): {res['full_decode_step'][side]['us_per_token']:.0f} us/token")
         print(json.dumps({"attention": res}), flush=True)
+        return
+    if args.configs_only:
+        c1 = measure_config1(dev)
+        log(f"config 1: {c1['per_layer_call']['us_per_layer_token']:.2f} us per layer-token per call "
+            f"({c1['per_layer_call']['frac_of_hbm_peak']:.3f} of HBM)"
+            + (f", token kernel {c1['token_kernel']['us_per_layer_token']:.2f} us "
+               f"({c1['token_kernel']['frac_of_hbm_peak']:.3f})" if "token_kernel" in c1 else ""))
+        c2 = measure_config2(dev)
+        log(f"config 2: {c2['us_per_layer']:.1f} us per layer, union {c2['union_frac_of_cold']:.3f} of cold, "
+            f"{c2['frac_of_hbm_peak']:.3f} of HBM")
+        print(json.dumps({"config1": c1, "config2": c2}), flush=True)
         return
     t0 = time.time()
     layers, st, thr, g = build_stack(args.seed, dev)
@@ -881,6 +1082,17 @@ def main():
             log(f"{M} tokens x 32 layers: {r['us_per_32_layers']:.0f} us, "
                 f"{r['tflops']:.1f} TFLOP/s, {r['weight_gbs']:.0f} GB/s")
 
+    config1 = config2 = None
+    if args.configs and not args.hbm_only:
+        config1 = measure_config1(dev)
+        log(f"config 1: {config1['per_layer_call']['us_per_layer_token']:.2f} us per layer-token per call "
+            f"({config1['per_layer_call']['frac_of_hbm_peak']:.3f} of HBM)"
+            + (f", token kernel {config1['token_kernel']['us_per_layer_token']:.2f} us "
+               f"({config1['token_kernel']['frac_of_hbm_peak']:.3f})" if "token_kernel" in config1 else ""))
+        config2 = measure_config2(dev)
+        log(f"config 2: {config2['us_per_layer']:.1f} us per layer, union {config2['union_frac_of_cold']:.3f} "
+            f"of cold, {config2['frac_of_hbm_peak']:.3f} of HBM")
+
     batch8 = None
     if args.batch8 and not args.hbm_only:
         batch8 = measure_batch8_file(dev, args.batch8_steps, 2)
@@ -942,13 +1154,17 @@ def main():
         "dtype": "fp8e4m3+int4 weights, fp16 activations, fp32 accumulate",
         "data": "synthetic (seeded N(0,0.02) weights, random-init bf16 predictors)",
         "config": {"workload": workload, "layers": N_LAYERS, "hidden": H, "intermediate": INTER,
-                   "n_hot": N_HOT, "batch": 1, "mean_active_cold": round(mean_active, 1),
+                   "n_hot": N_HOT, "batch": 1,
+                   "mean_active_cold": round(staged["mean_active_cold"] if staged is not None
+                                             else mean_active, 1),
                    "parallelism": "single GPU"},
         "roofline": roofline,
         "cpu_baseline": cpu,
         "staging": staged,
         "hbm_resident": hbm_resident,
         "cold_dequant": cold,
+        "config1": config1,
+        "config2": config2,
         "batch8_file": batch8,
         "multi_token": multi,
         "split_writer": writer,

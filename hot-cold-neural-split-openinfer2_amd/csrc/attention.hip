@@ -725,9 +725,13 @@ struct WsLayout {
   size_t q, attn, counters, part, total;
 };
 
-WsLayout ws_layout(int rows, int n_q, int n_kv, int cap) {
+// The split partial sums are sized for the launch the call makes: none when
+// the span (past + seq positions) fits one workgroup per query head, else
+// the splits choose_steps picks for that span.
+WsLayout ws_layout(int rows, int n_q, int n_kv, int span) {
   const int G = n_q / n_kv;
-  const size_t n_split = (size_t)(cap + kMinPosPerWg - 1) / kMinPosPerWg;
+  const int per_split = span <= kOneWgMax ? 0 : 16 * choose_steps(rows, n_kv, span);
+  const size_t n_split = per_split ? (size_t)(span + per_split - 1) / per_split : 0;
   WsLayout w;
   w.q = 0;
   w.attn = w.q + align256((size_t)rows * n_q * kHd * 2);
@@ -744,9 +748,11 @@ using namespace oi2;
 
 extern "C" {
 
-size_t oi2_attn_workspace_bytes(int32_t batch, int32_t seq, int32_t n_q, int32_t n_kv, int32_t cache_cap) {
-  if (batch <= 0 || seq <= 0 || n_q <= 0 || n_kv <= 0 || n_q % n_kv || cache_cap <= 0) return 0;
-  return ws_layout(batch * seq, n_q, n_kv, cache_cap).total;
+size_t oi2_attn_workspace_bytes(int32_t batch, int32_t seq, int32_t n_q, int32_t n_kv, int32_t past) {
+  if (batch <= 0 || seq <= 0 || n_q <= 0 || n_kv <= 0 || n_q % n_kv || past < 0 ||
+      (int64_t)past + seq > INT32_MAX)
+    return 0;
+  return ws_layout(batch * seq, n_q, n_kv, past + seq).total;
 }
 
 int oi2_attn_forward(const uint16_t* x, int32_t batch, int32_t seq, const oi2_attn* w, float eps,
@@ -776,7 +782,7 @@ int oi2_attn_forward(const uint16_t* x, int32_t batch, int32_t seq, const oi2_at
   OI2_CHECK_ARG(out, "null output");
   OI2_CHECK_ARG((size_t)batch * n_kv * cache_cap * kHd < ((size_t)1 << 40), "cache too large");
   const int rows = batch * seq;
-  const WsLayout L = ws_layout(rows, n_q, n_kv, cache_cap);
+  const WsLayout L = ws_layout(rows, n_q, n_kv, past + seq);
   OI2_CHECK_ARG(workspace && workspace_bytes >= L.total, "workspace of %zu bytes, %zu needed",
                 workspace_bytes, L.total);
   hipStream_t st = (hipStream_t)stream;

@@ -41,18 +41,30 @@ namespace oi2 {
 // published address is read at most once per launch after its signal, and
 // each launch starts with clean caches, so no stale line can be hit.  No L2
 // writeback or invalidate is issued (either stalls every in-flight load of
-// the XCD).  Past `spin` polls a wait sets the error word and goes on, so
-// every wait ends.
-__device__ __forceinline__ void stage_wait(const uint32_t* word, uint32_t target, uint32_t* err,
+// the XCD).  Past `spin` polls a wait sets the error word and gives up, so
+// every wait ends; once the error word is set (until the host reports and
+// clears it) every wait gives up at once, so a token whose streams did not
+// run side by side costs one bound, not one per layer.  Returns whether the
+// signal was seen (the same value in every lane).
+__device__ __forceinline__ bool stage_wait(const uint32_t* word, uint32_t target, uint32_t* err,
                                            uint32_t spin) {
+  if (__hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) return false;
   uint32_t n = 0;
-  while (__hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+  bool seen = true;
+  while ((uint32_t)__builtin_amdgcn_readfirstlane(
+             (int)__hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) < target) {
     __builtin_amdgcn_s_sleep(2);
     if (++n >= spin) {
       __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      seen = false;
+      break;
+    }
+    if ((n & 63) == 0 && __hip_atomic_load(err, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u) {
+      seen = false;
       break;
     }
   }
+  return __builtin_amdgcn_readfirstlane((int)seen) != 0;
 }
 
 __device__ __forceinline__ void stage_signal_wg(uint32_t* word) {
@@ -176,14 +188,25 @@ __device__ void cold_role(const UpArgs& a, int wg, uint32_t* s_pair, float* s_re
   const rsrc_t rp = rsrc(a.tok.ssq, a.tok.use_norm ? 256 * 4 : 0);
   const u32x4 pq = bld16(rp, 16 * lane);
   // staged records wait for the copy (records staged in list order: item j of
-  // chunk c is record c * chunk + j)
-  if (a.stage_ready) stage_wait(a.stage_ready, a.stage_target, a.stage_err, a.stage_spin);
+  // chunk c is record c * chunk + j); a wait that gives up reads the records
+  // from the copy's source through the slot list instead
+  const uint8_t* rec_base = a.records;
+  int n_rec = a.n_records;
+  const int32_t* slot_list = al.slots;
+  int lane_slot_v = lane_slot;
+  if (a.stage_ready && !stage_wait(a.stage_ready, a.stage_target, a.stage_err, a.stage_spin)) {
+    rec_base = a.stage_src;
+    n_rec = a.stage_src_n;
+    slot_list = a.stage_slots;
+    lane_slot_v = (int)bld4(rsrc(a.stage_slots, list_bytes), slot_off(lane));
+  }
+  const bool by_slot = slot_list != nullptr;
   const int n_items = cnt > j0 ? (cnt - j0 + wpc - 1) / wpc : 0;
 
   // 2. records through a descriptor over the record array: an absent item
   //    reads zero, so every load is unconditional
-  const rsrc_t rrec = rsrc(a.records, (uint32_t)a.n_records * kRecBytes);
-  const rsrc_t rgb = rsrc(a.cold_gbias, a.cold_gbias ? (uint32_t)a.n_records * 4 : 0);
+  const rsrc_t rrec = rsrc(rec_base, (uint32_t)n_rec * kRecBytes);
+  const rsrc_t rgb = rsrc(a.cold_gbias, a.cold_gbias ? (uint32_t)n_rec * 4 : 0);
   struct Rec {
     u32x4 q[6];
     uint32_t sdw;       // lane l < 48: halves 2l, 2l + 1 of the record's 96 group scales
@@ -192,7 +215,7 @@ __device__ void cold_role(const UpArgs& a, int wg, uint32_t* s_pair, float* s_re
   };
   const int g0 = lane >> 2;
   auto load_slot = [&](int sl, bool valid, Rec& R) {
-    R.valid = valid && sl >= 0 && sl < a.n_records;
+    R.valid = valid && sl >= 0 && sl < n_rec;
     const uint32_t ro = R.valid ? (uint32_t)sl * kRecBytes : kNoOff;
 #pragma unroll
     for (int it = 0; it < 6; ++it) R.q[it] = wld16(rrec, ro + kOffGate + 16 * (lane + 64 * it));
@@ -204,7 +227,7 @@ __device__ void cold_role(const UpArgs& a, int wg, uint32_t* s_pair, float* s_re
   // loads in flight on every pass and waits for exactly the record in use
   const int n_main = n_items < 64 ? n_items : 64;
   auto load_rec = [&](int k, Rec& R) {
-    const int sl = al.slots ? __builtin_amdgcn_readlane(lane_slot, k & 63) : cc * al.chunk + j0 + k * wpc;
+    const int sl = by_slot ? __builtin_amdgcn_readlane(lane_slot_v, k & 63) : cc * al.chunk + j0 + k * wpc;
     load_slot(sl, k < n_main, R);
   };
   Rec R[kColdRing];
@@ -288,7 +311,7 @@ __device__ void cold_role(const UpArgs& a, int wg, uint32_t* s_pair, float* s_re
   // items past 64 (a chunk longer than 64 of this wave's strides): one at a time
   for (int k = 64; k < n_items; ++k) {
     const int j = j0 + k * wpc;
-    load_slot(al.slots ? sload_i32(al.slots + cc * al.chunk + j) : cc * al.chunk + j, true, R[0]);
+    load_slot(by_slot ? sload_i32(slot_list + cc * al.chunk + j) : cc * al.chunk + j, true, R[0]);
     compute(R[0]);
   }
   // 4. sum the four waves in LDS (fixed order, padded against bank
@@ -864,17 +887,30 @@ __global__ __launch_bounds__(kThreads) void k_stage_gather(StageArgs a) {
 // go to was last read by the FFN two layers back, which the main stream
 // finishes before it signals this layer's selection.
 __global__ __launch_bounds__(kThreads) void k_stage_copy(StageCopyArgs a) {
-  __shared__ uint32_t s_reserve[kStageLdsWords];
+  __shared__ uint32_t s_reserve[kStageLdsWords - kThreads / kWave];
+  __shared__ bool s_ok[kThreads / kWave];
   if (a.cap < 0) reinterpret_cast<volatile uint32_t*>(s_reserve)[threadIdx.x] = 0;  // never runs
   uint32_t* err = a.sync + stage_err_word(a.n_layers);
   for (int L = 0; L < a.n_layers; ++L) {
     const StageLayer T = a.layers[L];
     if (T.n_records == 0) continue;
-    stage_wait(a.sync + stage_sel_word(L), T.sel_target, err, a.spin);
-    stage_copy_layer<true>(T.src, T.n_records, T.act, a.cap, T.dst,
-                           blockIdx.x * (kThreads / kWave) + (int)(threadIdx.x >> 6),
-                           gridDim.x * (kThreads / kWave));
-    stage_signal_wg(a.sync + stage_ready_word(L));
+    // a wave whose wait for the list gives up copies nothing, and its
+    // workgroup never signals the layer ready: the FFN's wait then gives up
+    // too and reads the records from the source
+    const bool listed = stage_wait(a.sync + stage_sel_word(L), T.sel_target, err, a.spin);
+    if (listed)
+      stage_copy_layer<true>(T.src, T.n_records, T.act, a.cap, T.dst,
+                             blockIdx.x * (kThreads / kWave) + (int)(threadIdx.x >> 6),
+                             gridDim.x * (kThreads / kWave));
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    s_ok[threadIdx.x >> 6] = listed;
+    __syncthreads();
+    bool all = true;
+#pragma unroll
+    for (int w = 0; w < kThreads / kWave; ++w) all = all && s_ok[w];
+    __syncthreads();
+    if (all && threadIdx.x == 0)
+      __hip_atomic_fetch_add(a.sync + stage_ready_word(L), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 

@@ -64,11 +64,17 @@ struct UpArgs {
   double* pd_z;
   int wg_cold, wg_pred, wg_hot;
   // staged records: the cold workgroups wait until *stage_ready reaches
-  // stage_target before reading them (null: no wait)
+  // stage_target before reading them (null: no wait).  A wait that gives up
+  // (or finds the error word set) reads the layer's records from where the
+  // copy takes them, stage_src (n records), through the chunked slot list
+  // stage_slots, so the output is the same either way.
   const uint32_t* stage_ready;
   uint32_t stage_target;
   uint32_t* stage_err;
   uint32_t stage_spin;
+  const uint8_t* stage_src;
+  int stage_src_n;
+  const int32_t* stage_slots;
 };
 
 struct DownArgs {

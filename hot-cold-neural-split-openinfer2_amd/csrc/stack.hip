@@ -134,6 +134,9 @@ static void layer_args(const oi2_stack* s, int L, const uint16_t* x_in, uint16_t
       ua.stage_target = (uint32_t)s->copy_wg;   // one arrival per copy workgroup
       ua.stage_err = s->stage_sync + stage_err_word(n);
       ua.stage_spin = s->stage_spin;
+      ua.stage_src = s->src[L];
+      ua.stage_src_n = l.cold.n_records;
+      ua.stage_slots = layer_list(s, L).slots;
     } else {
       ua.records = s->src[L];
       ua.n_records = l.cold.n_records;

@@ -11,10 +11,11 @@ engine's residual add; k, v are (B, n_kv, S, 128) fp16 with S = past + T.
 
 The reference grows its cache with torch.cat every step (engine.py:105-109).
 Here each layer owns one buffer with room for more positions and returns
-views of it; a call that passes back the views it returned appends in place.
-A cache from anywhere else is copied into the buffer first.  Passing an older
-(shorter) view of this layer's cache continues from that length: later
-positions of the buffer are overwritten.
+views of it; a call that passes back the latest views it returned appends in
+place, which leaves every earlier returned view as it was (they end before
+the positions written).  Any other cache (kv_cache=None, a cache from
+anywhere else, or an older, shorter view of this layer's cache) gets a new
+buffer, the older cache copied into it: earlier returned tensors never change.
 
 There is no CPU fallback: without liboi2.so or a GPU every call raises.
 """
@@ -100,14 +101,19 @@ class GroupedQueryAttention(torch.nn.Module):
         return cap
 
     def _own_view(self, k: torch.Tensor, B: int) -> bool:
+        """k is the latest view this layer returned: appending to it in place
+        leaves every earlier returned view as it was (they end at or before
+        the positions written)."""
         return (self._k is not None and k.is_cuda and k.data_ptr() == self._k.data_ptr()
                 and tuple(k.shape[:2]) == (B, self.n_kv) and k.shape[3] == HEAD_DIM
-                and k.stride() == self._k.stride() and k.shape[2] <= self._len)
+                and k.stride() == self._k.stride() and k.shape[2] == self._len)
 
     def _prepare_cache(self, B: int, T: int, kv_cache):
         if kv_cache is None:
-            if self._k is None or self._k.shape[0] != B or self.capacity < T:
-                self._k, self._v = self._alloc(B, self._room(T))
+            # a new sequence gets a new buffer, as the reference's torch.cat
+            # returns fresh tensors: views returned for an earlier sequence
+            # keep their contents
+            self._k, self._v = self._alloc(B, self._room(T))
             return 0
         k_in, v_in = kv_cache
         past = int(k_in.shape[2])
@@ -150,7 +156,7 @@ class GroupedQueryAttention(torch.nn.Module):
                                          or not residual_out.is_contiguous()):
             raise ValueError("residual_out must be a contiguous fp16 tensor shaped like x")
         cap = self.capacity
-        nbytes = L.oi2_attn_workspace_bytes(B, T, self.n_q, self.n_kv, cap)
+        nbytes = L.oi2_attn_workspace_bytes(B, T, self.n_q, self.n_kv, past)
         ws = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
         _lib.check(L.oi2_attn_forward(
             xc.data_ptr(), B, T, ctypes.byref(self._struct), self.eps, c.data_ptr(), s.data_ptr(),

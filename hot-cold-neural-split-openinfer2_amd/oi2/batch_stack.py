@@ -86,6 +86,7 @@ class BatchDecodeStack:
             if l.predictor is not None:
                 ws = max(ws, int(L.oi2_predict_workspace_bytes(ctypes.byref(l.predictor.struct()))))
         self._pws = torch.empty(max(ws, 256), dtype=torch.uint8, device=dev)
+        self._nid_cache: dict = {}     # section -> its record nids (this stack's store only)
         self.bytes_read = 0            # record bytes read from the file since construction
         self.trace = None              # set to a list to record (x_in, ids) per layer
 
@@ -119,8 +120,6 @@ class BatchDecodeStack:
             if self.trace is not None:
                 self._host_ids[par].copy_(S["dids"], non_blocking=True)
             self._sel_ev[par].record(stream)
-
-    _nid_cache: dict = {}
 
     def _section_nids(self, section: int) -> np.ndarray:
         if section not in self._nid_cache:

@@ -210,10 +210,12 @@ def sparse_ffn(x: torch.Tensor, activation: str, act_on_both: bool,
         up/down arguments None - computed by the fused fp8 / INT4 kernels.
     Either half may be None or empty; both empty gives zeros (:207-208).
     Accumulation is fp32 throughout; the halves are summed in fp32 and
-    rounded once to fp16."""
-    if x.dtype != torch.float16:
-        raise TypeError(f"x must be the engine's fp16 activations, got {x.dtype}")
-    x2d = x.reshape(-1, HIDDEN).contiguous()
+    rounded once to x.dtype.  The kernels read fp16 activations (the
+    engine's); a bf16 or fp32 x is rounded to fp16 first (exact for bf16
+    values in fp16's range)."""
+    if x.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        raise TypeError(f"x must be floating point (fp16, bf16 or fp32), got {x.dtype}")
+    x2d = x.reshape(-1, HIDDEN).to(torch.float16).contiguous()
     hot_handle = isinstance(gate_hot, HotWeights)
     cold_handle = isinstance(gate_cold, ColdNeurons)
     if hot_handle and (up_hot is not None or down_hot is not None):

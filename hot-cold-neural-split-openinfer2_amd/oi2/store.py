@@ -6,10 +6,12 @@ default a layer's section is uploaded to HBM once, on first access, as raw
 6400-byte records (the device keeps the INT4 bytes, 16x smaller than the
 reference's fp32 tensors); 288 GB of HBM holds a 7B model's ~2.5 GB cold file
 many times over.  ``residency="file"`` keeps the reference's model instead:
-records are read from the file on every fetch.  ``read_neurons`` keeps the reference's contract - request order,
-duplicates kept, absent ids skipped, None when nothing is found or the section
-is empty, fp32 (N,H)/(N,H)/(H,N) - but returns device tensors produced by the
-dequant kernel.
+records are read from the file on every fetch.  ``read_neurons`` keeps the
+reference's contract - request order, duplicates kept, absent ids skipped,
+None when nothing is found or the section is empty, fp32 (N,H)/(N,H)/(H,N) -
+with the dequantisation done by the GPU kernel.  Built with the reference's
+three arguments the store returns CPU tensors, as splitter.py:397-403 does;
+``device=`` (or ``out_device=``) keeps them on the GPU instead.
 """
 from __future__ import annotations
 
@@ -78,11 +80,15 @@ class ColdWeightStore:
         and on to the device (liboi2's native file store,
         ``reader_threads`` threads).
 
-    The nid -> slot LUT always lives on the device."""
+    The nid -> slot LUT always lives on the device.
 
-    def __init__(self, cold_bin: str, cold_index: str, config: dict, device="cuda",
+    ``read_neurons`` returns its tensors on ``out_device``: by default the
+    CPU when ``device`` is not given (the reference's three-argument form,
+    whose tensors are CPU tensors), else ``device``."""
+
+    def __init__(self, cold_bin: str, cold_index: str, config: dict, device=None,
                  pinned: bool = False, residency: str | None = None, direct_io: bool = False,
-                 reader_threads: int = 8):
+                 reader_threads: int = 8, out_device=None):
         self.config = config
         self.index = np.load(cold_index)
         self._f = open(cold_bin, "rb")
@@ -93,7 +99,9 @@ class ColdWeightStore:
         if self.H != fmt.HIDDEN_DIM:
             raise ValueError(f"hidden_dim {self.H}: the cold-record layout is sized for "
                              f"{fmt.HIDDEN_DIM}")
-        self.device = torch.device(device)
+        self.device = torch.device(device if device is not None else "cuda")
+        self.out_device = torch.device(out_device if out_device is not None
+                                       else (device if device is not None else "cpu"))
         self.residency = residency or ("pinned" if pinned else "hbm")
         if self.residency not in ("hbm", "pinned", "file"):
             raise ValueError(f"residency {self.residency!r}: 'hbm', 'pinned' or 'file'")
@@ -186,8 +194,9 @@ class ColdWeightStore:
         return staged
 
     def read_neurons(self, layer_idx: int, expert_idx: int, neuron_ids):
-        """(gate (N,H), up (N,H), down (H,N)) fp32 on the store's device, or
-        None if the section is empty or no requested id exists."""
+        """(gate (N,H), up (N,H), down (H,N)) fp32 on ``out_device``, or None
+        if the section is empty or no requested id exists
+        (splitter.py:354-403)."""
         sec = self.section(layer_idx, expert_idx)
         if sec is None:
             return None
@@ -210,6 +219,8 @@ class ColdWeightStore:
                                          _lib.stream_handle(dev)))
         if self.residency == "file":
             sec.event.synchronize()      # the pinned buffer may be released now
+        if self.out_device != dev:
+            return gate.to(self.out_device), up.to(self.out_device), down.to(self.out_device)
         return gate, up, down
 
     def close(self):

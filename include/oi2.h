@@ -389,9 +389,11 @@ typedef struct oi2_attn {
   const uint16_t* norm_w;     /* (H) fp16 input_layernorm (ones for nn.RMSNorm's default) */
 } oi2_attn;
 
-/* Workspace of oi2_attn_forward for batch x seq query rows and a cache of
- * cache_cap positions; 0 for invalid sizes. */
-size_t oi2_attn_workspace_bytes(int32_t batch, int32_t seq, int32_t n_q, int32_t n_kv, int32_t cache_cap);
+/* Workspace of oi2_attn_forward for batch x seq query rows attending to
+ * positions [0, past + seq): q, the attention output, and the sequence
+ * split's partial sums only when past + seq exceeds 1024 positions (the
+ * splits the launch picks for that span); 0 for invalid sizes. */
+size_t oi2_attn_workspace_bytes(int32_t batch, int32_t seq, int32_t n_q, int32_t n_kv, int32_t past);
 /* GroupedQueryAttention.forward (engine.py:90-125) for x (batch, seq, H)
  * fp16: x_n = RMSNorm(x); q, k, v = x_n W^T; RoPE on q and k with cos / sin
  * (seq, 64) fp32, the call's positions as the engine slices them

@@ -75,20 +75,25 @@ def ffn(x, hot, cold, activation="silu", act_on_both=False):
 def time_layers(samples, threads: int = 1):
     """Time the restated per-layer path over ``samples`` = list of
     (x_n (1,H) fp32, hot dense tuple, buf, id_to_offset, cold ids).  Returns
-    (seconds, seconds spent in the cold fetch + dequant, neurons fetched)."""
+    (seconds, seconds spent in the cold fetch + dequant, neurons fetched,
+    per-call seconds of each layer call, per-call seconds of its cold fetch)."""
     prev = torch.get_num_threads()
     torch.set_num_threads(threads)
     try:
         neurons = 0
         t_cold = 0.0
+        calls, fetches = [], []
         t0 = time.perf_counter()
         for xn, hot, buf, offs, ids in samples:
             t1 = time.perf_counter()
             cold = read_neurons(buf, offs, ids)
-            t_cold += time.perf_counter() - t1
+            t2 = time.perf_counter()
+            t_cold += t2 - t1
             neurons += 0 if cold is None else cold[0].shape[0]
             ffn(xn, hot, cold)
+            calls.append(time.perf_counter() - t1)
+            fetches.append(t2 - t1)
         dt = time.perf_counter() - t0
     finally:
         torch.set_num_threads(prev)
-    return dt, t_cold, neurons
+    return dt, t_cold, neurons, calls, fetches

@@ -161,3 +161,33 @@ def test_cache_growth_and_default_norm(dev):
         xt = torch.randn((B, 1, H), generator=g, device=dev).half()
         _, kv = _check_step(attn, w, n_kv, xt, cos[past:], sin[past:], kv, f"growth step {step}")
     assert attn.capacity == 512 and kv[0].shape[2] == 257
+
+
+def test_returned_caches_never_change(dev):
+    """Tensors a call returned keep their contents whatever later calls do:
+    a second sequence (kv_cache=None), a roll-back to an older, shorter view
+    of the cache, and the in-place append of the latest view (which writes
+    only past the earlier views' ends).  The reference returns fresh
+    torch.cat tensors every call (engine.py:105-109)."""
+    n_kv, B = 8, 1
+    w = _weights(dev, n_kv, seed=41)
+    attn = oi2.GroupedQueryAttention(0, w, _cfg(n_kv))
+    cos, sin = oi2.rope_tables(64, D, 10000.0, device=dev)
+    g = torch.Generator(device=dev).manual_seed(42)
+    x = torch.randn((B, 6, H), generator=g, device=dev).half()
+    _, kv_a = attn(x, cos, sin)
+    xt = torch.randn((B, 1, H), generator=g, device=dev).half()
+    _, kv_a1 = attn(xt, cos[6:], sin[6:], kv_a)          # in place: kv_a is unchanged
+    torch.cuda.synchronize()
+    snap = [t.clone() for t in (*kv_a, *kv_a1)]
+    x2 = torch.randn((B, 9, H), generator=g, device=dev).half()
+    _, kv_b = attn(x2, cos, sin)                          # a second sequence
+    x3 = torch.randn((B, 1, H), generator=g, device=dev).half()
+    _, kv_r = _check_step(attn, w, n_kv, x3, cos[6:], sin[6:], kv_a, "roll back to 6 positions")
+    torch.cuda.synchronize()
+    for t, s in zip((*kv_a, *kv_a1), snap):
+        assert torch.equal(t, s), "a returned cache changed"
+    assert kv_b[0].shape[2] == 9 and kv_r[0].shape[2] == 7
+    assert kv_b[0].data_ptr() != kv_a[0].data_ptr() and kv_r[0].data_ptr() != kv_a[0].data_ptr()
+    # the roll-back's new position differs from the first sequence's own 7th
+    assert not torch.equal(kv_r[0][:, :, 6], kv_a1[0][:, :, 6])

@@ -181,6 +181,57 @@ def test_prefill_chunk_512(dev):
     assert_ffn_close(y32.cpu().numpy(), ref_all, what="prefill all rows")
 
 
+def test_prefill_chain_32_layers(dev):
+    """Survey config 5 end to end: a 512-token chunk through 32 layers
+    (engine.py:424-438's chain: RMSNorm in front of every FFN, the residual
+    carried), each layer with its own 40 % cold union.  Teacher-forced on the
+    GPU's own layer inputs, layers 0 and 31 match the float64 oracle on rows
+    spread over the tiles and float32 torch on every row; every layer's
+    output is finite and its residual update within the FFN bar of a float32
+    reference over the same weights on the first, middle and last layers."""
+    g = torch.Generator(device=dev).manual_seed(61)
+    n_layers, M = 32, 512
+    layers, colds, slot_sets = [], [], []
+    for _ in range(n_layers):
+        lay = SyntheticLayer(g, 14336, 3584, device=dev)
+        n_cold = lay.records.shape[0]
+        slots = torch.randperm(n_cold, generator=g, device=dev)[: int(0.4 * n_cold)].int()
+        layers.append(lay)
+        slot_sets.append(slots)
+        colds.append(ColdNeurons.from_slots(_section(lay), slots))
+    x = torch.randn((M, H), generator=g, device=dev).to(torch.bfloat16).half()
+    ins, outs = [], []
+    for lay, cold in zip(layers, colds):
+        ins.append(x)
+        x = _ffn(x, lay.norm_w, EPS, lay.hot, cold, "silu", False, True)
+        outs.append(x)
+    torch.cuda.synchronize()
+    for o in outs:
+        assert torch.isfinite(o.float()).all()
+    f32 = lambda a: torch.as_tensor(a, dtype=torch.float32, device=dev)
+    rows = [0, 77, 190, 256, 383, 511]
+    for L in (0, 15, 31):
+        lay = layers[L]
+        Gh, Uh, Dh = hot_dense(lay.hot)
+        Gc, Uc, Dc = cold_dense(lay.records, slot_sets[L])
+        xn_all = torch.as_tensor(normed_f16(ins[L], lay.norm_w), dtype=torch.float32, device=dev)
+        hh = torch.nn.functional.silu(xn_all @ f32(Gh).T) * (xn_all @ f32(Uh).T)
+        hc = torch.nn.functional.silu(xn_all @ f32(Gc).T) * (xn_all @ f32(Uc).T)
+        ref_all = (hh @ f32(Dh).T + hc @ f32(Dc).T).double().cpu().numpy()
+        upd = outs[L].double().cpu().numpy() - ins[L].double().cpu().numpy()
+        # the output is fp16(x + y): the update carries one fp16 rounding of x + y
+        assert_ffn_close(upd, ref_all, tol=2e-2, cos_min=0.9999, what=f"layer {L} update, all rows")
+        if L in (0, 31):
+            _, y32 = _ffn(ins[L], lay.norm_w, EPS, lay.hot, colds[L], "silu", False, True, want_y32=True)
+            torch.cuda.synchronize()
+            xn = normed_f16(ins[L][rows], lay.norm_w)
+            ref = O.sparse_ffn(xn, "silu", False, Gh, Uh, Dh, Gc, Uc, Dc)
+            y = y32[rows].cpu().numpy()
+            for k, r in enumerate(rows):
+                assert_ffn_close(y[k], ref[k], what=f"layer {L} row {r} vs oracle")
+            assert_ffn_close(y32.cpu().numpy(), ref_all, what=f"layer {L} all rows")
+
+
 @pytest.mark.parametrize("B", [3, 17, 96, 300])
 def test_batch_ignores_workspace_contents(dev, layer25, B):
     """The workspace is scratch: filled with NaN before the call (every byte

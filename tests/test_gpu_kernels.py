@@ -463,7 +463,7 @@ def test_sparse_ffn_takes_the_reference_call(dev, config1_files, B, activation, 
 def test_sparse_ffn_reference_call_edges(dev, config1_files):
     """Either half missing or empty (engine.py:194, :199), both empty giving
     zeros (:207-208), cold records read out of request order with duplicates,
-    bf16 weights, and non-fp16 activations refused."""
+    bf16 weights, fp32 and bf16 activations, and integer activations refused."""
     lay, g, store, fp8 = config1_files
     gh, uh, dh = (fp8[k].to(torch.float16) for k in ("gate", "up", "down"))
     ids = [int(lay.cold_ids[k]) for k in (40, 3, 3, 700, 11000, 5)]
@@ -484,8 +484,17 @@ def test_sparse_ffn_reference_call_edges(dev, config1_files):
             assert_ffn_close(f64(y[r]), ref[r], what=f"{what} row {r}")
     z = oi2.sparse_ffn(x, "silu", False, None, None, None, None, None, None)
     assert z.dtype == torch.float16 and torch.count_nonzero(z) == 0
-    with pytest.raises(TypeError, match="fp16"):
-        oi2.sparse_ffn(x.float(), "silu", False, gh, uh, dh, None, None, None)
+    # activations of another float dtype, as engine.py:173-209 takes them:
+    # the result comes back in x's dtype, against the oracle over x itself
+    for xt in (x.float() * 1.0001, x.bfloat16()):
+        y = oi2.sparse_ffn(xt, "silu", False, gh, uh, dh, gc, uc, dc)
+        torch.cuda.synchronize()
+        assert y.dtype == xt.dtype and y.shape == xt.shape
+        ref = O.sparse_ffn(f64(xt), "silu", False, f64(gh), f64(uh), f64(dh), f64(gc), f64(uc), f64(dc))
+        for r in range(2):
+            assert_ffn_close(f64(y[r]), ref[r], what=f"{xt.dtype} activations row {r}")
+    with pytest.raises(TypeError, match="floating point"):
+        oi2.sparse_ffn(x.int(), "silu", False, gh, uh, dh, None, None, None)
     with pytest.raises(ValueError, match="gate/up must be"):
         oi2.sparse_ffn(x, "silu", False, gh, uh, dh.t(), None, None, None)
 

@@ -223,8 +223,10 @@ def test_staged_store_matches_resident(stack4):
 def test_staged_wait_past_bound_is_reported(stack4):
     """The staged path's device-side waits (the copy kernel for a layer's
     list, the FFN for its records) are bounded: forced to give up at once
-    (a bound of one poll), the token still completes, status() raises once,
-    and the next token with the default bound equals the resident result."""
+    (a bound of one poll), the token still completes with the resident
+    result (an FFN wait that gives up reads the records from their source
+    through the slot list), status() raises once, and the next tokens with
+    the default bound equal the resident result too."""
     dev, g, layers, st, thr = stack4
     stream = torch.cuda.Stream(device=dev)
     x_in = torch.randn(H, generator=g, device=dev).half()
@@ -246,6 +248,8 @@ def test_staged_wait_past_bound_is_reported(stack4):
         staged.set_wait_bound(1)
         with torch.cuda.stream(stream):
             staged.decode(x_in, out, stream)
+        stream.synchronize()
+        assert torch.equal(out, ref), "a wait that gave up changed the output"
         staged.set_wait_bound(1 << 20)
         with pytest.raises(oi2.OI2Error, match="past its bound"):
             staged.status(stream)
@@ -319,11 +323,14 @@ def test_token_trace_stamps_phases_in_order(stack4):
 @pytest.mark.parametrize("n_hot,activation,both,shift", [(4000, "silu", False, 0.0), (3584, "relu", True, -1.66)],
                          ids=["three_hot_rows_per_wave", "drelu_with_gate_bias"])
 def test_token_kernel_other_geometries(n_hot, activation, both, shift):
-    """The persistent kernel's other shapes against the two-launch sequence:
-    n_hot 4000 runs the variant with three hot neurons per worker wave, and
-    dReLU (relu on both halves, engine.py:163-170) with a gate bias runs the
-    bias and activation paths.  Layers 0 and 1 select from x_in, so their
-    active sets are identical; outputs agree to the summation order."""
+    """The persistent kernel's other shapes against the oracle and the
+    two-launch sequence: n_hot 4000 runs the variant with three hot neurons
+    per worker wave, and dReLU (relu on both halves, engine.py:163-170) with a
+    gate bias runs the bias and activation paths.  Teacher-forced on the
+    token kernel's own layer inputs, every layer's active set equals the
+    oracle's prediction outside the 1e-6 band and its FFN the float64 FFN
+    over that set.  Layers 0 and 1 select from x_in, so their active sets are
+    the two-launch path's too; outputs agree to the summation order."""
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(5)
     layers = [SyntheticLayer(g, 14336, n_hot, device=dev, with_predictor=True, gate_bias_shift=shift)
@@ -343,12 +350,37 @@ def test_token_kernel_other_geometries(n_hot, activation, both, shift):
             xs, counts, _, ids = st.trace()
             torch.cuda.synchronize()
             res[token] = (xs.clone(), [st.active_ids(L, counts, ids) for L in (0, 1)])
+            if token:
+                tok_ids = [st.active_ids(L, counts, ids) for L in range(3)]
         st.set_token_kernel(True)
         assert res[True][1] == res[False][1]
         assert all(len(s) > 0 for s in res[True][1])
         for L in range(3):
             assert_ffn_close(res[True][0][L].double().cpu().numpy(), res[False][0][L].double().cpu().numpy(),
                              tol=2e-3, cos_min=0.99999, what=f"layer {L} output")
+        # the token kernel against the oracle, layer by layer
+        xs = res[True][0]
+        inputs = [x_in] + [xs[i] for i in range(2)]
+        for L, lay in enumerate(layers):
+            src = inputs[L - 1] if L > 0 else x_in
+            q_rows = rmsnorm(src[None], lay.norm_w, EPS).double().cpu().numpy()
+            D, U, b = pred_weights(lay.predictor)
+            logits = O.predictor_logits(query_for(q_rows, lay.predictor.dtype), D, U, b)
+            want = O.cold_ids_for(logits >= thr, lay.hot_ids.cpu().tolist(), lay.inter)
+            got = tok_ids[L]
+            assert got == sorted(got)
+            amb = np.abs(logits - thr) <= 1e-6
+            assert all(amb[i] for i in set(got) ^ set(want)), f"layer {L}: index sets differ"
+            Gh, Uh, Dh = hot_dense(lay.hot)
+            Gc, Uc, Dc = cold_dense(lay.records, [int(lay.lut[i]) for i in got])
+            bh = bc = None
+            if shift:
+                bh = lay.hot.gate_bias.double().cpu().numpy()
+                bc = lay.cold_gate_bias.double().cpu().numpy()[[int(lay.lut[i]) for i in got]]
+            xn = normed_f16(inputs[L][None], lay.norm_w)
+            ref = O.sparse_ffn(xn, activation, both, Gh, Uh, Dh, Gc, Uc, Dc, bh, bc)[0]
+            y = xs[L].double().cpu().numpy() - inputs[L].double().cpu().numpy()
+            assert_ffn_close(y, ref, tol=1e-2, cos_min=0.9999, what=f"token kernel layer {L} vs oracle")
     finally:
         st.close()
 
@@ -414,4 +446,54 @@ def test_bench_stack_32_layers_consecutive_tokens():
         mean = sum(n_sel) / (3 * len(layers))
         assert 0.025 * 14336 < mean < 0.06 * 14336, mean
     finally:
+        st.close()
+
+
+def test_staged_32_layers_equal_resident():
+    """The benchmark's headline configuration end to end: 32 layers with the
+    records in pinned host memory, each layer's active records copied into
+    HBM one layer ahead by the side-stream copy kernel.  Three consecutive
+    tokens, each fed the previous output, equal the HBM-resident stack's
+    two-launch decode (the same kernels on the same records) bit for bit,
+    and the active sets of every layer are the same."""
+    from oi2.synth import build_decode_stack
+    dev = torch.device("cuda:0")
+    layers, st, thr, g = build_decode_stack(0, dev)
+    staged = None
+    try:
+        stream = torch.cuda.Stream(device=dev)
+        x0 = torch.randn(H, generator=g, device=dev).half()
+        st.set_token_kernel(False)
+        refs, ref_sets, x = [], [], x0
+        for t in range(3):
+            y = torch.empty_like(x0)
+            with torch.cuda.stream(stream):
+                st.decode(x, y, stream)
+            stream.synchronize()
+            st.status(stream)
+            _, c, _, i = st.trace()
+            torch.cuda.synchronize()
+            refs.append(y)
+            ref_sets.append([_ids_two_launch(c, i, L) for L in range(32)])
+            x = y
+        pinned = [l.records.cpu().pin_memory() for l in layers]
+        staged = DecodeStack([StackLayer(l.hot, p, l.lut, l.norm_w, l.predictor)
+                              for l, p in zip(layers, pinned)], 14336, EPS, "silu", False, thr, staging=8)
+        staged.set_expected_active(int(1.3 * 0.05 * (14336 - 3584)))
+        x = x0
+        for t in range(3):
+            y = torch.empty_like(x0)
+            with torch.cuda.stream(stream):
+                staged.decode(x, y, stream)
+            stream.synchronize()
+            staged.status(stream)
+            _, c, _, i = staged.trace()
+            torch.cuda.synchronize()
+            print(f"[staged32] token {t}: equal {torch.equal(y, refs[t])}", flush=True)
+            assert torch.equal(y, refs[t]), f"token {t}"
+            assert [_ids_two_launch(c, i, L) for L in range(32)] == ref_sets[t], f"token {t} active sets"
+            x = y
+    finally:
+        if staged is not None:
+            staged.close()
         st.close()

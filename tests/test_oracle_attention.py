@@ -155,3 +155,76 @@ def test_gqa_relative_positions_and_rope_only_on_q_k():
     b, _ = O.gqa_attention(x, nw, 1e-5, wq, wk, wv, wo, n_q, n_kv, cos[50:], sin[50:])
     # (a rotation applied to v as well would move the output with the shift)
     assert O.rel_err(b, a) < 1e-2 and O.cosine(b, a) > 0.9999
+
+
+def _torch_gqa(x, nw, eps, wq, wk, wv, wo, n_q, n_kv, cos, sin, kv_cache, head_split="reference"):
+    """GroupedQueryAttention.forward (engine.py:90-125) composed from torch's
+    own modules in float64, with the reference's fp16 rounding points as
+    casts: nn.RMSNorm, F.linear, view(B, T, n, D).transpose(1, 2), the
+    half-split rotation with fp16 tables, torch.cat onto the cache,
+    repeat_interleave over the kv heads, scaled_dot_product_attention
+    (causal only without a cache), transpose back and o_proj.
+    head_split="wrong" splits the heads as view(B, n, T, D) instead (a
+    plausible mistake the comparison must catch)."""
+    r = lambda t: t.half().double()
+    t64 = lambda a: torch.as_tensor(np.asarray(a, np.float64))
+    x = t64(x)
+    B, T, H = x.shape
+    D = H // n_q
+    norm = torch.nn.RMSNorm(H, eps=eps, dtype=torch.float64)
+    with torch.no_grad():
+        norm.weight.copy_(t64(nw))
+        xn = r(norm(x))
+
+    def heads(t, n):
+        if head_split == "wrong":
+            return t.reshape(B, n, T, D)
+        return t.view(B, T, n, D).transpose(1, 2)
+
+    q = heads(r(F.linear(xn, t64(wq))), n_q)
+    k = heads(r(F.linear(xn, t64(wk))), n_kv)
+    v = heads(r(F.linear(xn, t64(wv))), n_kv)
+
+    def rope(t):
+        half = D // 2
+        c = r(t64(cos)[:T])[None, None]
+        s = r(t64(sin)[:T])[None, None]
+        a, b = t[..., :half], t[..., half:]
+        return r(torch.cat([a * c - b * s, a * s + b * c], dim=-1))
+
+    q, k = rope(q), rope(k)
+    if kv_cache is not None:
+        k = torch.cat([t64(kv_cache[0]), k], dim=2)
+        v = torch.cat([t64(kv_cache[1]), v], dim=2)
+    g = n_q // n_kv
+    o = F.scaled_dot_product_attention(q, k.repeat_interleave(g, dim=1), v.repeat_interleave(g, dim=1),
+                                       is_causal=kv_cache is None)
+    o = r(o).transpose(1, 2).contiguous().view(B, T, H)
+    return r(F.linear(o, t64(wo))).numpy(), (k.numpy(), v.numpy())
+
+
+@pytest.mark.parametrize("n_q,n_kv,H,T,past", [(32, 8, 4096, 4, 0), (32, 8, 4096, 1, 23),
+                                               (8, 2, 1024, 5, 0), (8, 2, 1024, 2, 11)])
+def test_gqa_matches_torch_composition(n_q, n_kv, H, T, past):
+    """The oracle's attention against the torch composition of engine.py:90-125
+    with the same rounding points, with and without a cache; the head split,
+    the kv grouping, the rotation and the cache order all enter the result.
+    A wrong head split in the composition is far from the oracle, so the
+    comparison would catch that mistake on either side."""
+    rng = np.random.default_rng(100 + n_q + T + past)
+    wq, wk, wv, wo, nw = _layer(rng, n_q, n_kv, H)
+    D = H // n_q
+    x = rng.standard_normal((2, T, H))
+    cos, sin = O.rope_cache(past + T, D, 10000.0)
+    cache = None
+    if past:
+        cache = (O.f16(rng.standard_normal((2, n_kv, past, D))), O.f16(rng.standard_normal((2, n_kv, past, D))))
+    got, (gk, gv) = O.gqa_attention(x, nw, 1e-5, wq, wk, wv, wo, n_q, n_kv, cos[past:], sin[past:], cache)
+    want, (wk2, wv2) = _torch_gqa(x, nw, 1e-5, wq, wk, wv, wo, n_q, n_kv, cos[past:], sin[past:], cache)
+    assert got.shape == want.shape == (2, T, H)
+    # fp16 rounding points may flip by one ulp where float64 sums differ in order
+    assert O.rel_err(got, want) < 2e-3 and O.cosine(got, want) > 0.99999
+    assert O.rel_err(gk, wk2) < 2e-3 and O.rel_err(gv, wv2) < 2e-3
+    bad, _ = _torch_gqa(x, nw, 1e-5, wq, wk, wv, wo, n_q, n_kv, cos[past:], sin[past:], cache, head_split="wrong")
+    if T > 1:
+        assert O.rel_err(bad, want) > 0.05, "a wrong head split must be visible"
