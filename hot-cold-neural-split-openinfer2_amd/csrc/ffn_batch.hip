@@ -5,13 +5,13 @@
 // After the norm and a compaction of the active list:
 //   gate/up  H_hot  (M, n_hot) = act(s_g * X G^T + b, s_u * X U^T)   fp8 rows
 //            H_cold (M, n_act) = act(sum_g s_g,g (X Q_g^T)_g + b, ...)  INT4 records
-//            k_bup_s (M <= 16): 16 weight rows per workgroup, the 4 waves
-//            split K and meet in LDS, every weight load issued up front;
-//            k_bup + k_bact (M < 192): 64 tokens x 64 rows, split K;
-//            k_pgemm_up (M >= 192): 32x32x16 tiles, weights streamed in registers
+//            k_sbup (M <= 16): one workgroup per CU, RMSNorm fused;
+//            k_mup (M < 192): 64 tokens x 32 neurons, 32x32x16 tiles, the
+//            activation in the epilogue;
+//            k_pgemm_up (M >= 192): 32 pms tokens x 128 neurons
 //   down     Y (M, H) fp32
 //            hot  H_hot D_hot^T (fp8 rows, row scale): k_bdown_hot_s,
-//                 k_bdown_hot, k_pgemm_down_hot
+//                 k_pgemm_down_hot
 //            cold H_cold D_cold: k_pgemm_down_cold for every M, the records'
 //                 down nibbles transposed into a decoded LDS tile
 //   k_bfinal out = x + Y (fp16), y32 = Y
@@ -45,7 +45,6 @@ typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32_a2 __attribute__((aligned(2)));
 
 constexpr int kBM = 64;          // token rows per tile
-constexpr int kBN = 64;          // output columns per workgroup (4 waves x 16)
 constexpr int kBK = 128;         // K block = INT4 scale group
 constexpr int kLdA = kBK + 8;    // LDS row of the A tile, halves (272 B)
 
@@ -104,207 +103,6 @@ __device__ __forceinline__ uint32_t dword_of(const u32x4& a, const u32x4& b, int
   return i < 4 ? a[i] : b[i - 4];
 }
 
-// Rows m0..m0+63, columns k0..k0+127 of the fp16 matrix A (row stride ld
-// halves) into s[64][kLdA]; rows >= M and columns >= K read as zero.  PAIR
-// stores each group of 8 as (x0,x4,x1,x5,x2,x6,x3,x7), the order the INT4
-// decode produces.  Requires ld, K multiples of 8 and A 16-byte aligned.
-template <bool PAIR>
-__device__ __forceinline__ void stage_a(const uint16_t* A, int ld, int M, int K, int m0, int k0,
-                                        uint16_t* s) {
-  const int t = threadIdx.x;
-  const int c = t & 15;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int row = (t >> 4) + 16 * r;
-    const int m = m0 + row, k = k0 + 8 * c;
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if (m < M && k < K) v = *reinterpret_cast<const u32x4*>(A + (size_t)m * ld + k);
-    if (PAIR) {
-      const uint32_t d0 = v.x, d1 = v.y, d2 = v.z, d3 = v.w;
-      v.x = (d0 & 0xFFFFu) | (d2 << 16);
-      v.y = (d0 >> 16) | (d2 & 0xFFFF0000u);
-      v.z = (d1 & 0xFFFFu) | (d3 << 16);
-      v.w = (d1 >> 16) | (d3 & 0xFFFF0000u);
-    }
-    *reinterpret_cast<u32x4*>(s + row * kLdA + 8 * c) = v;
-  }
-}
-
-__device__ __forceinline__ h8 a_frag(const uint16_t* s, int ms, int step) {
-  const int l = lane_id();
-  return *reinterpret_cast<const h8*>(s + (16 * ms + (l & 15)) * kLdA + 32 * (l >> 4) + 8 * step);
-}
-
-// ── gate/up ─────────────────────────────────────────────────────────────────
-
-__global__ __launch_bounds__(kThreads) void k_bup(BUpArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t sA[kBM * kLdA];
-  const int w = threadIdx.x >> 6, l = lane_id();
-  const int m0 = blockIdx.y * kBM;
-  // K blocks of this workgroup (blockIdx.z of ksplit)
-  const int kbs = blockIdx.z * (kH / kBK) / a.ksplit, kbe = (blockIdx.z + 1) * (kH / kBK) / a.ksplit;
-  f32x4 accg[4], accu[4];
-#pragma unroll
-  for (int ms = 0; ms < 4; ++ms) accg[ms] = accu[ms] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  if ((int)blockIdx.x < a.hot_wg) {
-    // hot: this lane's weight row n, 32 fp8 per 128-wide K block
-    const int n = blockIdx.x * kBN + 16 * w + (l & 15);
-    const bool nv = n < a.n_hot;
-    const uint8_t* gr = a.gate_q + (size_t)(nv ? n : 0) * kH + 32 * (l >> 4);
-    const uint8_t* ur = a.up_q + (size_t)(nv ? n : 0) * kH + 32 * (l >> 4);
-    for (int kb = kbs; kb < kbe; ++kb) {
-      u32x4 g0 = {0u, 0u, 0u, 0u}, g1 = g0, u0 = g0, u1 = g0;
-      if (nv) {
-        g0 = load16(gr + kb * kBK);
-        g1 = load16(gr + kb * kBK + 16);
-        u0 = load16(ur + kb * kBK);
-        u1 = load16(ur + kb * kBK + 16);
-      }
-      __syncthreads();
-      stage_a<false>(a.xn, kH, a.M, kH, m0, kb * kBK, sA);
-      __syncthreads();
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const h8 bg = fp8x8_h8(dword_of(g0, g1, 2 * s), dword_of(g0, g1, 2 * s + 1));
-        const h8 bu = fp8x8_h8(dword_of(u0, u1, 2 * s), dword_of(u0, u1, 2 * s + 1));
-#pragma unroll
-        for (int ms = 0; ms < 4; ++ms) {
-          const h8 av = a_frag(sA, ms, s);
-          accg[ms] = mfma16(av, bg, accg[ms]);
-          accu[ms] = mfma16(av, bu, accu[ms]);
-        }
-      }
-    }
-    if (a.ksplit > 1) {   // partial sums; k_bact finishes
-      float* pg = a.pg + (size_t)blockIdx.z * a.Mpad * a.ldp;
-      float* pu = a.pu + (size_t)blockIdx.z * a.Mpad * a.ldp;
-#pragma unroll
-      for (int ms = 0; ms < 4; ++ms)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const size_t o = (size_t)(m0 + 16 * ms + 4 * (l >> 4) + i) * a.ldp + n;
-          pg[o] = accg[ms][i];
-          pu[o] = accu[ms][i];
-        }
-      return;
-    }
-    const float sg = nv ? a.gate_s[n] : 0.f, su = nv ? a.up_s[n] : 0.f;
-    const float gb = (nv && a.hot_gbias) ? a.hot_gbias[n] : 0.f;
-#pragma unroll
-    for (int ms = 0; ms < 4; ++ms)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int m = m0 + 16 * ms + 4 * (l >> 4) + i;
-        const float h = nv ? gated_act(fmaf(accg[ms][i], sg, gb), accu[ms][i] * su, a.relu, a.both)
-                           : 0.f;
-        a.hh[(size_t)m * a.ldh + n] = float_to_half_bits(h);
-      }
-    return;
-  }
-
-  // cold: this lane's item i of the dense active list
-  const int total = min(*a.total, a.cap);
-  const int i0 = ((int)blockIdx.x - a.hot_wg) * kBN;
-  if (i0 >= total) return;
-  const int i = i0 + 16 * w + (l & 15);
-  int slot = i < total ? a.dslots[i] : -1;
-  const bool iv = slot >= 0 && slot < a.n_records;
-  const uint8_t* rec = a.records + (size_t)(iv ? slot : 0) * kRecBytes;
-  const uint16_t* sc = reinterpret_cast<const uint16_t*>(rec + kOffScales);
-  for (int kb = kbs; kb < kbe; ++kb) {
-    u32x4 qg = {0u, 0u, 0u, 0u}, qu = qg;
-    float sg = 0.f, su = 0.f;
-    if (iv) {
-      qg = load16_a2(rec + kOffGate + 64 * kb + 16 * (l >> 4));
-      qu = load16_a2(rec + kOffUp + 64 * kb + 16 * (l >> 4));
-      sg = half_bits_to_float(sc[kb]);
-      su = half_bits_to_float(sc[kGroups + kb]);
-    }
-    __syncthreads();
-    stage_a<true>(a.xn, kH, a.M, kH, m0, kb * kBK, sA);
-    __syncthreads();
-    f32x4 tg[4], tu[4];
-#pragma unroll
-    for (int ms = 0; ms < 4; ++ms) tg[ms] = tu[ms] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const h8 bg = int4x8_h8(qg[s]);
-      const h8 bu = int4x8_h8(qu[s]);
-#pragma unroll
-      for (int ms = 0; ms < 4; ++ms) {
-        const h8 av = a_frag(sA, ms, s);
-        tg[ms] = mfma16(av, bg, tg[ms]);
-        tu[ms] = mfma16(av, bu, tu[ms]);
-      }
-    }
-#pragma unroll
-    for (int ms = 0; ms < 4; ++ms)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        accg[ms][e] = fmaf(sg, tg[ms][e], accg[ms][e]);
-        accu[ms][e] = fmaf(su, tu[ms][e], accu[ms][e]);
-      }
-  }
-  if (a.ksplit > 1) {
-    float* pg = a.pg + (size_t)blockIdx.z * a.Mpad * a.ldp;
-    float* pu = a.pu + (size_t)blockIdx.z * a.Mpad * a.ldp;
-#pragma unroll
-    for (int ms = 0; ms < 4; ++ms)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const size_t o = (size_t)(m0 + 16 * ms + 4 * (l >> 4) + e) * a.ldp + a.ldh + i;
-        pg[o] = accg[ms][e];
-        pu[o] = accu[ms][e];
-      }
-    return;
-  }
-  const float gb = (iv && a.cold_gbias) ? a.cold_gbias[slot] : 0.f;
-#pragma unroll
-  for (int ms = 0; ms < 4; ++ms)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int m = m0 + 16 * ms + 4 * (l >> 4) + e;
-      const float h = iv ? gated_act(accg[ms][e] + gb, accu[ms][e], a.relu, a.both) : 0.f;
-      a.hc[(size_t)m * a.ldc + i] = float_to_half_bits(h);
-    }
-}
-
-// Sum of k_bup's ksplit partial gate/up sums, then scales, bias and the
-// activation: H_hot and H_cold for rows < M.
-__global__ __launch_bounds__(kThreads) void k_bact(BUpArgs a) {
-  const int total = a.total ? min(*a.total, a.cap) : 0;
-  const int n = a.M * a.ldp;
-  for (int q = blockIdx.x * kThreads + threadIdx.x; q < n; q += gridDim.x * kThreads) {
-    const int m = q / a.ldp, c = q - m * a.ldp;
-    float g = 0.f, u = 0.f;
-    for (int z = 0; z < a.ksplit; ++z) {
-      const size_t o = (size_t)z * a.Mpad * a.ldp + (size_t)m * a.ldp + c;
-      g += a.pg[o];
-      u += a.pu[o];
-    }
-    if (c < a.ldh) {
-      const bool nv = c < a.n_hot;
-      float h = 0.f;
-      if (nv) {
-        const float gb = a.hot_gbias ? a.hot_gbias[c] : 0.f;
-        h = gated_act(fmaf(g, a.gate_s[c], gb), u * a.up_s[c], a.relu, a.both);
-      }
-      a.hh[(size_t)m * a.ldh + c] = float_to_half_bits(h);
-    } else {
-      const int i = c - a.ldh;
-      if (i >= total) continue;   // never read
-      const int slot = a.dslots[i];
-      float h = 0.f;
-      if (slot >= 0 && slot < a.n_records) {
-        const float gb = a.cold_gbias ? a.cold_gbias[slot] : 0.f;
-        h = gated_act(g + gb, u, a.relu, a.both);
-      }
-      a.hc[(size_t)m * a.ldc + i] = float_to_half_bits(h);
-    }
-  }
-}
-
 // ── gate/up and hot down for prefill-sized token counts ─────────────────────
 //
 // v_mfma_f32_32x32x16_f16 (lane l, element i): A[l%32][8(l/32)+i],
@@ -351,7 +149,8 @@ struct ARows {
   }
 };
 
-// The loaded chunks into s[32 MS][kLdA]; PAIR as in stage_a.
+// The loaded chunks into s[32 MS][kLdA].  PAIR stores each group of 8 halves
+// as (x0,x4,x1,x5,x2,x6,x3,x7), the order the INT4 decode produces.
 template <int NR, bool PAIR>
 __device__ __forceinline__ void store_a_rows(const u32x4 (&r)[NR], uint16_t* s) {
   const int t = threadIdx.x;
@@ -569,6 +368,204 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_up(BUpArgs a, int hot_tiles,
   const int i0 = (nt - hot_tiles) * 128;
   if (i0 >= total) return;   // the whole workgroup
   pgemm_up_tile<MS, false>(a, nt, m0, total, i0, sA, sB, sSc);
+}
+
+// ── gate/up for 17 .. 191 tokens ────────────────────────────────────────────
+//
+// Workgroup tile: 64 tokens x 32 neurons (hot fp8 rows, or cold items of the
+// dense active list).  The whole K range stays in one workgroup, so the
+// activation is applied in the epilogue (no partial sums leave it); at 3584
+// hot + 10752 cold there are ~440 workgroups.  Operands go through two LDS
+// buffers, loaded kMupPD blocks ahead, with the 32x32x16 MFMA as in
+// pgemm_up_tile: the 32 columns are the tile's neurons, B tile 0 the gate
+// rows and tile 1 the up rows.  Wave w takes token subtile w & 1 and K steps
+// 4 (w >> 1) .. +4 of every block; the two K halves meet in LDS at the end.
+// A cold tile's group scales (32 gate + 32 up per item) go to LDS once, up
+// front.  (64-item cold tiles, measured first, ran twice as long as the hot
+// tiles and set the kernel's end.)
+constexpr int kMupN = 32;   // neurons per tile
+constexpr int kMupPD = 2;   // K blocks of weights and tokens in flight per workgroup
+constexpr int kMupBbuf = 64 * kLdB8;                 // bytes per B buffer (32 x 2 rows)
+constexpr int kMupAbuf = 64 * kLdA * 2;              // bytes per A buffer
+constexpr int kMupLds = 2 * kMupAbuf + 2 * kMupBbuf + kMupN * 2 * kGroups * 2;
+static_assert(2 * kMupAbuf + 2 * kMupBbuf >= 2 * 2 * 16 * 64 * 4, "the K-half reduction fits the operand buffers");
+
+template <bool HOT>
+__device__ __forceinline__ void mup_tile(const BUpArgs& a, int nt, int m0, int total, int i0, uint8_t* smem) {
+  constexpr int MS = 2;
+  uint16_t* sA = reinterpret_cast<uint16_t*>(smem);
+  uint8_t* sB = smem + 2 * kMupAbuf;
+  uint16_t* sSc = reinterpret_cast<uint16_t*>(smem + 2 * kMupAbuf + 2 * kMupBbuf);
+  const int t = threadIdx.x, w = t >> 6, l = lane_id(), h = l >> 5;
+  const int ms = w & 1, kh = w >> 1, col = l & 31;
+  const ARows<MS> arows(a.xn, kH, a.M, m0);
+  f32x16 acc[2] = {f32x16{}, f32x16{}};   // gate, up
+  u32x4 ra[kMupPD][2 * MS], rb[kMupPD][2];
+  // staging: hot, chunk t & 7 of neuron row t >> 3 (gate, up); cold, chunk
+  // t & 3 of item t >> 3, gate for (t >> 2) & 1 == 0 else up.  Absent rows
+  // read as zero.
+  const rsrc_t rw = HOT ? buf_rsrc(a.gate_q, (uint32_t)a.n_hot * kH)
+                        : buf_rsrc(a.records, (uint32_t)a.n_records * kRecBytes);
+  const rsrc_t ru = buf_rsrc(a.up_q, HOT ? (uint32_t)a.n_hot * kH : 0u);
+  auto item_rec = [&](int it) {
+    const int slot = it < total ? a.dslots[it] : -1;
+    return (slot >= 0 && slot < a.n_records) ? (uint32_t)slot * kRecBytes : kNoOffset;
+  };
+  uint32_t voff[2];
+  if constexpr (HOT) {
+    voff[0] = voff[1] = (uint32_t)(nt * kMupN + (t >> 3)) * kH + 16 * (t & 7);
+  } else {
+    const uint32_t v = item_rec(i0 + (t >> 3));
+    voff[0] = v + (((t >> 2) & 1) ? kOffUp : kOffGate) + 16 * (t & 3);
+    // scales: item t >> 3, 16-byte piece t & 7 of its gate (64 B) and up
+    // (64 B) scale arrays, stored as sSc[item][gate 0..31, up 0..31]
+    const u32x4 sv = bload16(rw, v + kOffScales + 16 * (t & 7), 0);
+    reinterpret_cast<u32x4*>(sSc)[t] = sv;
+  }
+  auto load_b = [&](int kb, int sl) {
+    if constexpr (HOT) {
+      rb[sl][0] = bload16(rw, voff[0], kb * kBK);
+      rb[sl][1] = bload16(ru, voff[1], kb * kBK);
+    } else {
+      rb[sl][0] = bload16(rw, voff[0], 64 * kb);
+    }
+  };
+  auto store_b = [&](int buf, int sl) {
+    uint8_t* B = sB + buf * kMupBbuf;
+    if constexpr (HOT) {
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        uint8_t* d = B + ((t >> 3) + 32 * i) * kLdB8 + 16 * (t & 7);
+        reinterpret_cast<u32x2*>(d)[0] = u32x2{rb[sl][i].x, rb[sl][i].y};
+        reinterpret_cast<u32x2*>(d)[1] = u32x2{rb[sl][i].z, rb[sl][i].w};
+      }
+    } else {   // rows: gate items 0..31, then up items 0..31
+      uint8_t* d = B + ((t >> 3) + 32 * ((t >> 2) & 1)) * kLdB4 + 16 * (t & 3);
+      reinterpret_cast<u32x2*>(d)[0] = u32x2{rb[sl][0].x, rb[sl][0].y};
+      reinterpret_cast<u32x2*>(d)[1] = u32x2{rb[sl][0].z, rb[sl][0].w};
+    }
+  };
+  // this wave's K steps of one block, its token subtile
+  auto mma_block = [&](const uint16_t* A, const uint8_t* B, int kb) {
+    if constexpr (HOT) {
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const int st = 4 * kh + s4;
+        const u32x2 vg = *reinterpret_cast<const u32x2*>(B + col * kLdB8 + 64 * h + 8 * st);
+        const u32x2 vu = *reinterpret_cast<const u32x2*>(B + (32 + col) * kLdB8 + 64 * h + 8 * st);
+        const h8 av = a_frag32(A, ms, st);
+        acc[0] = mfma32(av, fp8x8_h8(vg[0], vg[1]), acc[0]);
+        acc[1] = mfma32(av, fp8x8_h8(vu[0], vu[1]), acc[1]);
+      }
+    } else {
+      const _Float16 sg = __builtin_bit_cast(_Float16, sSc[col * 2 * kGroups + kb]);
+      const _Float16 su = __builtin_bit_cast(_Float16, sSc[col * 2 * kGroups + kGroups + kb]);
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const int st = 4 * kh + s4;
+        const uint32_t dg = *reinterpret_cast<const uint32_t*>(B + col * kLdB4 + 32 * h + 4 * st);
+        const uint32_t du = *reinterpret_cast<const uint32_t*>(B + (32 + col) * kLdB4 + 32 * h + 4 * st);
+        const h8 av = a_frag32(A, ms, st);
+        acc[0] = mfma32(av, int4x8_h8_scaled(dg, sg), acc[0]);
+        acc[1] = mfma32(av, int4x8_h8_scaled(du, su), acc[1]);
+      }
+    }
+  };
+
+  constexpr int kNB = kH / kBK;
+  static_assert(kNB % kMupPD == 0, "the block loop is unrolled by the prefetch distance");
+  // blocks 0 .. kMupPD - 1 in flight, block 0 to LDS, block kMupPD into its slot
+#pragma unroll
+  for (int b = 0; b < kMupPD; ++b) {
+    arows.load(b, ra[b]);
+    load_b(b, b);
+  }
+  store_a_rows<2 * MS, !HOT>(ra[0], sA);
+  store_b(0, 0);
+  arows.load(kMupPD, ra[0]);
+  load_b(kMupPD, 0);
+  lds_barrier();
+#pragma unroll 1
+  for (int k0 = 0; k0 < kNB; k0 += kMupPD) {
+#pragma unroll
+    for (int u = 0; u < kMupPD; ++u) {
+      const int kb = k0 + u, cur = kb & 1, sl = (u + 1) % kMupPD;   // block kb + 1 is in slot sl
+      __builtin_amdgcn_sched_barrier(0);
+      mma_block(sA + cur * (kMupAbuf / 2), sB + cur * kMupBbuf, kb);
+      __builtin_amdgcn_sched_barrier(0);
+      if (kb + 1 < kNB) {
+        store_a_rows<2 * MS, !HOT>(ra[sl], sA + (cur ^ 1) * (kMupAbuf / 2));
+        store_b(cur ^ 1, sl);
+        if (kb + 1 + kMupPD < kNB) {
+          arows.load(kb + 1 + kMupPD, ra[sl]);
+          load_b(kb + 1 + kMupPD, sl);
+        }
+      }
+      lds_barrier();
+    }
+  }
+
+  // the K halves meet in LDS (the operand buffers are free now), upper onto
+  // lower, in a fixed order: red[subtile][gate, up][element][lane]
+  float* red = reinterpret_cast<float*>(smem);
+  if (kh == 1) {
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) red[((ms * 2 + g) * 16 + j) * 64 + l] = acc[g][j];
+  }
+  __syncthreads();
+  if (kh == 1) return;
+#pragma unroll
+  for (int g = 0; g < 2; ++g)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[g][j] += red[((ms * 2 + g) * 16 + j) * 64 + l];
+  // epilogue: lane l holds column l & 31, tokens m0 + 32 ms + 8 (j / 4) + 4 h + j % 4
+  if constexpr (HOT) {
+    const int row = nt * kMupN + col;
+    const bool ok = row < a.n_hot;
+    const float sg = ok ? a.gate_s[row] : 0.f, su = ok ? a.up_s[row] : 0.f;
+    const float gb = (ok && a.hot_gbias) ? a.hot_gbias[row] : 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int m = m0 + 32 * ms + 8 * (j >> 2) + 4 * h + (j & 3);
+      if (m >= a.M) continue;
+      const float hv = ok ? gated_act(fmaf(acc[0][j], sg, gb), acc[1][j] * su, a.relu, a.both) : 0.f;
+      a.hh[(size_t)m * a.ldh + row] = float_to_half_bits(hv);
+    }
+  } else {
+    const int item = i0 + col;
+    const int slot = item < total ? a.dslots[item] : -1;
+    const bool ok = slot >= 0 && slot < a.n_records;
+    const float gb = (ok && a.cold_gbias) ? a.cold_gbias[slot] : 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int m = m0 + 32 * ms + 8 * (j >> 2) + 4 * h + (j & 3);
+      if (m >= a.M) continue;
+      const float hv = ok ? gated_act(acc[0][j] + gb, acc[1][j], a.relu, a.both) : 0.f;
+      a.hc[(size_t)m * a.ldc + item] = float_to_half_bits(hv);
+    }
+  }
+}
+
+// Grid: (hot tiles + cold tiles, rounded up to 8) x token tiles, the token
+// tiles of one weight tile on one XCD (workgroups go round-robin over the 8
+// XCDs), sharing its L2 for the weights.
+__global__ __launch_bounds__(kThreads) void k_mup(BUpArgs a, int hot_tiles, int n_tiles, int mt) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kMupLds];
+  const int b = blockIdx.x;
+  const int q = b >> 3;
+  const int nt = (q / mt) * 8 + (b & 7), mtile = q % mt;
+  if (nt >= n_tiles) return;   // the whole workgroup
+  const int m0 = mtile * 64;
+  if (nt < hot_tiles) {
+    mup_tile<true>(a, nt, m0, 0, 0, smem);
+    return;
+  }
+  const int total = min(*a.total, a.cap);
+  const int i0 = (nt - hot_tiles) * kMupN;
+  if (i0 >= total) return;   // the whole workgroup
+  mup_tile<false>(a, nt - hot_tiles, m0, total, i0, smem);
 }
 
 // Hot down for 32 MS tokens x 128 outputs (4 waves x 32) over the K blocks of
@@ -849,177 +846,6 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_down_cold(BDownArgs a, int m
         const int m = m0 + 32 * ms + 8 * (e >> 2) + 4 * (l >> 5) + (e & 3);
         if (m < a.M) unsafeAtomicAdd(a.y + (size_t)m * kH + j0 + 64 * w + 32 * nb + (l & 31), acc[ms][nb][e]);
       }
-}
-
-// ── gate/up for at most 64 tokens ───────────────────────────────────────────
-
-// Workgroup = 16 weight rows (hot rows, or items of the dense active list);
-// wave w takes K blocks [8w, 8w+8).  MS = token subtiles of 16 (M <= 16 MS).
-// Hot rows are loaded as whole cache lines (8 lanes per 128-byte segment of
-// a row, every block's loads issued up front) and re-laid through a
-// wave-private LDS area into the MFMA operand layout; a cold record's block
-// (64 bytes per vector) is read by the 4 lanes that use it.
-template <int MS>
-__global__ __launch_bounds__(kThreads) void k_bup_s(BUpArgs a) {
-  constexpr int NB = kH / kBK / 4;
-  constexpr int PF = MS >= 4 ? 4 : 8;   // K blocks whose weight loads are in flight together
-  __shared__ f32x4 s_red[3][2 * MS][kWave];
-  __shared__ __attribute__((aligned(16))) uint8_t s_w[4][32 * kLdB8];   // per wave: 16 gate + 16 up rows
-  const int w = threadIdx.x >> 6, l = lane_id();
-  const int kb0 = w * NB;
-  const uint16_t* xr[MS];
-  bool av[MS];
-#pragma unroll
-  for (int ms = 0; ms < MS; ++ms) {
-    const int m = 16 * ms + (l & 15);
-    av[ms] = m < a.M;
-    xr[ms] = a.xn + (size_t)(av[ms] ? m : 0) * kH + 32 * (l >> 4);
-  }
-  f32x4 accg[MS], accu[MS];
-#pragma unroll
-  for (int ms = 0; ms < MS; ++ms) accg[ms] = accu[ms] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const bool hot = (int)blockIdx.x < a.hot_wg;
-  int col;
-  bool cv;
-  int slot = -1;
-  if (hot) {
-    const int r0 = blockIdx.x * 16;
-    col = r0 + (l & 15);
-    cv = col < a.n_hot;
-    // load j (0..3) of a block: matrix j / 2 (gate, up), rows 8 (j & 1) + l / 8,
-    // 16-byte chunk l & 7; rows past n_hot read as zero
-    const rsrc_t rg = buf_rsrc(a.gate_q, (uint32_t)a.n_hot * kH);
-    const rsrc_t ru = buf_rsrc(a.up_q, (uint32_t)a.n_hot * kH);
-    uint32_t voff[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) voff[h] = (uint32_t)(r0 + 8 * h + (l >> 3)) * kH + 16 * (l & 7);
-    uint8_t* sw = s_w[w];
-    for (int ph = 0; ph < NB; ph += PF) {
-      u32x4 W[PF][4];
-#pragma unroll
-      for (int b = 0; b < PF; ++b)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) W[b][j] = bload16(j < 2 ? rg : ru, voff[j & 1], (kb0 + ph + b) * kBK);
-#pragma unroll
-      for (int b = 0; b < PF; ++b) {
-        // block b into the wave's rows: gate rows 0..15, up rows 16..31
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          uint8_t* d = sw + (16 * (j >> 1) + 8 * (j & 1) + (l >> 3)) * kLdB8 + 16 * (l & 7);
-          reinterpret_cast<u32x2*>(d)[0] = u32x2{W[b][j].x, W[b][j].y};
-          reinterpret_cast<u32x2*>(d)[1] = u32x2{W[b][j].z, W[b][j].w};
-        }
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          h8 A[MS];
-#pragma unroll
-          for (int ms = 0; ms < MS; ++ms)
-            A[ms] = av[ms] ? *reinterpret_cast<const h8*>(xr[ms] + (kb0 + ph + b) * kBK + 8 * s) : h8{};
-          const u32x2 g2 = *reinterpret_cast<const u32x2*>(sw + (l & 15) * kLdB8 + 32 * (l >> 4) + 8 * s);
-          const u32x2 u2 = *reinterpret_cast<const u32x2*>(sw + (16 + (l & 15)) * kLdB8 + 32 * (l >> 4) + 8 * s);
-          const h8 bg = fp8x8_h8(g2[0], g2[1]);
-          const h8 bu = fp8x8_h8(u2[0], u2[1]);
-#pragma unroll
-          for (int ms = 0; ms < MS; ++ms) {
-            accg[ms] = mfma16(A[ms], bg, accg[ms]);
-            accu[ms] = mfma16(A[ms], bu, accu[ms]);
-          }
-        }
-      }
-    }
-  } else {
-    // the list length and this lane's slot are loaded together (the list has
-    // cap entries, those past the length are ignored): one dependent hop
-    // fewer before the record loads
-    const int i0 = ((int)blockIdx.x - a.hot_wg) * 16;
-    col = i0 + (l & 15);
-    const int raw_total = *a.total;
-    const int raw_slot = a.dslots[min(col, a.cap - 1)];
-    asm volatile("" ::"v"(raw_slot), "s"(raw_total));   // both loads in flight before either is used
-    const int total = min(raw_total, a.cap);
-    if (i0 >= total) return;   // the whole workgroup
-    slot = col < total ? raw_slot : -1;
-    cv = slot >= 0 && slot < a.n_records;
-    const uint8_t* rec = a.records + (size_t)(cv ? slot : 0) * kRecBytes;
-    const uint16_t* sc = reinterpret_cast<const uint16_t*>(rec + kOffScales);
-    for (int ph = 0; ph < NB; ph += PF) {
-      u32x4 QG[PF], QU[PF];
-      float SG[PF], SU[PF];
-#pragma unroll
-      for (int b = 0; b < PF; ++b) {
-        const int kb = kb0 + ph + b;
-        const u32x4 z = {0u, 0u, 0u, 0u};
-        QG[b] = cv ? load16_a2(rec + kOffGate + 64 * kb + 16 * (l >> 4)) : z;
-        QU[b] = cv ? load16_a2(rec + kOffUp + 64 * kb + 16 * (l >> 4)) : z;
-        SG[b] = cv ? half_bits_to_float(sc[kb]) : 0.f;
-        SU[b] = cv ? half_bits_to_float(sc[kGroups + kb]) : 0.f;
-      }
-#pragma unroll
-      for (int b = 0; b < PF; ++b) {
-        f32x4 tg[MS], tu[MS];
-#pragma unroll
-        for (int ms = 0; ms < MS; ++ms) tg[ms] = tu[ms] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          h8 A[MS];
-#pragma unroll
-          for (int ms = 0; ms < MS; ++ms) {
-            const h8 v = av[ms] ? *reinterpret_cast<const h8*>(xr[ms] + (kb0 + ph + b) * kBK + 8 * s)
-                                : h8{};
-            A[ms] = __builtin_shufflevector(v, v, 0, 4, 1, 5, 2, 6, 3, 7);
-          }
-          const h8 bg = int4x8_h8(QG[b][s]);
-          const h8 bu = int4x8_h8(QU[b][s]);
-#pragma unroll
-          for (int ms = 0; ms < MS; ++ms) {
-            tg[ms] = mfma16(A[ms], bg, tg[ms]);
-            tu[ms] = mfma16(A[ms], bu, tu[ms]);
-          }
-        }
-#pragma unroll
-        for (int ms = 0; ms < MS; ++ms)
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            accg[ms][e] = fmaf(SG[b], tg[ms][e], accg[ms][e]);
-            accu[ms][e] = fmaf(SU[b], tu[ms][e], accu[ms][e]);
-          }
-      }
-    }
-  }
-  if (w > 0) {
-#pragma unroll
-    for (int ms = 0; ms < MS; ++ms) {
-      s_red[w - 1][2 * ms][l] = accg[ms];
-      s_red[w - 1][2 * ms + 1][l] = accu[ms];
-    }
-  }
-  __syncthreads();
-  if (w != 0) return;
-#pragma unroll
-  for (int v = 0; v < 3; ++v)
-#pragma unroll
-    for (int ms = 0; ms < MS; ++ms) {
-      accg[ms] += s_red[v][2 * ms][l];
-      accu[ms] += s_red[v][2 * ms + 1][l];
-    }
-  float sg = 1.f, su = 1.f, gb = 0.f;
-  if (hot) {
-    sg = cv ? a.gate_s[col] : 0.f;
-    su = cv ? a.up_s[col] : 0.f;
-    gb = (cv && a.hot_gbias) ? a.hot_gbias[col] : 0.f;
-  } else {
-    gb = (cv && a.cold_gbias) ? a.cold_gbias[slot] : 0.f;
-  }
-  uint16_t* dst = hot ? a.hh : a.hc;
-  const int ld = hot ? a.ldh : a.ldc;
-#pragma unroll
-  for (int ms = 0; ms < MS; ++ms)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int m = 16 * ms + 4 * (l >> 4) + e;
-      const float h = cv ? gated_act(fmaf(accg[ms][e], sg, gb), accu[ms][e] * su, a.relu, a.both) : 0.f;
-      dst[(size_t)m * ld + col] = float_to_half_bits(h);
-    }
 }
 
 // ── gate/up for at most 16 tokens, RMSNorm fused ─────────────────────────────
@@ -1422,49 +1248,6 @@ __global__ __launch_bounds__(kThreads) void k_bdown_hot_s(BDownArgs a) {
   }
 }
 
-// Hot half for more than 64 tokens: 64 tokens x 64 outputs per workgroup, A
-// tiles through LDS, K blocks split over hot_splits workgroups; adds into y.
-__global__ __launch_bounds__(kThreads) void k_bdown_hot(BDownArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t sA[kBM * kLdA];
-  const int w = threadIdx.x >> 6, l = lane_id();
-  const int m0 = blockIdx.y * kBM;
-  const int tile = blockIdx.x % (kH / kBN), split = blockIdx.x / (kH / kBN);
-  const int hcol = tile * kBN + 16 * w + (l & 15);
-  f32x4 acc[4];
-#pragma unroll
-  for (int ms = 0; ms < 4; ++ms) acc[ms] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const int kb0 = split * a.hot_blocks / a.hot_splits;
-  const int kb1 = (split + 1) * a.hot_blocks / a.hot_splits;
-  const uint8_t* dr = a.down_q + (size_t)hcol * a.down_stride;
-  for (int kb = kb0; kb < kb1; ++kb) {
-    const int k = kb * kBK + 32 * (l >> 4);
-    u32x4 q0 = {0u, 0u, 0u, 0u}, q1 = q0;
-    if (k < a.down_stride) q0 = load16(dr + k);
-    if (k + 16 < a.down_stride) q1 = load16(dr + k + 16);
-    __syncthreads();
-    stage_a<false>(a.hh, a.ldh, a.M, a.ldh, m0, kb * kBK, sA);
-    __syncthreads();
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const h8 b = fp8x8_h8(dword_of(q0, q1, 2 * s), dword_of(q0, q1, 2 * s + 1));
-#pragma unroll
-      for (int ms = 0; ms < 4; ++ms) acc[ms] = mfma16(a_frag(sA, ms, s), b, acc[ms]);
-    }
-  }
-  const float sd = a.down_s[hcol];
-#pragma unroll
-  for (int ms = 0; ms < 4; ++ms)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int m = m0 + 16 * ms + 4 * (l >> 4) + e;
-      if (m >= a.M) continue;
-      if (a.hot_splits == 1)
-        a.y[(size_t)m * kH + hcol] = acc[ms][e] * sd;   // the first and only hot writer
-      else
-        unsafeAtomicAdd(a.y + (size_t)m * kH + hcol, acc[ms][e] * sd);
-    }
-}
-
 // y = 0 over M rows.
 __global__ __launch_bounds__(kThreads) void k_bfill(float* y, int n4) {
   for (int q = blockIdx.x * kThreads + threadIdx.x; q < n4; q += gridDim.x * kThreads)
@@ -1525,11 +1308,11 @@ __global__ __launch_bounds__(kThreads) void k_bcompact(ActiveList al, int cap, i
 // ── host ────────────────────────────────────────────────────────────────────
 
 struct BatchPlan {
-  int M, Mpad, mt, ldh, hot_blocks, cap, ldc, hot_splits, ksplit;
+  int M, Mpad, mt, ldh, hot_blocks, cap, ldc, hot_splits;
   bool prefill;
   int pms, pmt;   // prefill tiles: 32-token subtiles per tile, token tiles
   int cold_splits;   // at most 16 tokens: the cold down's item ranges
-  size_t off_xn, off_hh, off_hc, off_dslots, off_total, off_y, off_pg, off_pu, off_part, bytes;
+  size_t off_xn, off_hh, off_hc, off_dslots, off_total, off_y, off_part, bytes;
 };
 
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -1543,7 +1326,7 @@ static int prefill_ms(int M) { return M >= 384 ? 4 : 2; }   // 32-token subtiles
 // else 128) x item ranges, about 256 workgroups; a range holds at most
 // kDcMaxItems items.
 static int cold_down_splits(int M, int cap) {
-  const int mtc = M <= kSkinnyMax ? 1 : (M + 127) / 128;
+  const int mtc = M <= kSkinnyMax ? 1 : M < kPrefillMin ? (M + 63) / 64 : (M + 127) / 128;
   const int n_blk = (cap + kDcItems - 1) / kDcItems;
   const int min_splits = (n_blk + kDcMaxItems / kDcItems - 1) / (kDcMaxItems / kDcItems);
   return std::max(min_splits, std::min(n_blk, std::max(1, 256 / (16 * mtc))));
@@ -1559,16 +1342,16 @@ static BatchPlan batch_plan(int M, int n_hot, int cap) {
   p.cap = cap;
   p.ldc = cap > 0 ? (cap + 127) / 128 * 128 : 0;
   p.prefill = M >= kPrefillMin;
-  if (p.prefill) {
-    p.pms = prefill_ms(M);
+  if (M > kSkinnyMax) {
+    // 64-token tiles (k_mup and the down kernels at two 32-token subtiles)
+    // below the prefill sizes, 32 pms-token tiles from them on
+    p.pms = p.prefill ? prefill_ms(M) : 2;
     p.pmt = (M + 32 * p.pms - 1) / (32 * p.pms);
     // hot down: 32 output tiles x token tiles x K splits, about 256 workgroups
     p.hot_splits = std::max(1, std::min(p.hot_blocks, 256 / (32 * p.pmt)));
   } else {
     p.hot_splits = p.mt >= 4 ? 1 : 4 / p.mt;
   }
-  // tiled gate/up with few token tiles: split K over workgroups
-  p.ksplit = (M > kSkinnyMax && !p.prefill && p.mt < 4) ? 4 / p.mt : 1;
   size_t o = 0;
   p.off_xn = o;
   o = align256(o + (size_t)M * kH * 2);
@@ -1582,11 +1365,6 @@ static BatchPlan batch_plan(int M, int n_hot, int cap) {
   o = align256(o + 16);
   p.off_y = o;
   o = align256(o + (size_t)M * kH * 4);
-  const size_t part = p.ksplit > 1 ? (size_t)p.ksplit * p.Mpad * (p.ldh + p.ldc) * 4 : 0;
-  p.off_pg = o;
-  o = align256(o + part);
-  p.off_pu = o;
-  o = align256(o + part);
   p.cold_splits = (M <= kSkinnyMax && cap > 0) ? cold_down_splits(M, cap) : 0;
   p.off_part = o;
   o = align256(o + (size_t)p.cold_splits * kH * 16 * 4);
@@ -1656,7 +1434,6 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
   }
   ua.hh = hh;
   ua.ldh = p.ldh;
-  ua.hot_wg = skinny ? p.ldh / 16 : p.ldh / kBN;
   ua.hot_per_wg = (n_hot + kSbGroups - 1) / kSbGroups;
   if (has_cold) {
     ua.records = cold->records;
@@ -1668,10 +1445,6 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
   }
   ua.hc = hc;
   ua.ldc = p.ldc;
-  ua.ksplit = skinny ? 1 : p.ksplit;
-  ua.pg = reinterpret_cast<float*>(ws + p.off_pg);
-  ua.pu = reinterpret_cast<float*>(ws + p.off_pu);
-  ua.ldp = p.ldh + p.ldc;
   ua.Mpad = p.Mpad;
   BDownArgs da{};
   da.M = M;
@@ -1735,16 +1508,11 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
       else
         hipLaunchKernelGGL(k_pgemm_up<2>, grid, dim3(kThreads), 0, st, ua, hot_tiles, n_tiles, p.pmt);
     } else {
-      hipLaunchKernelGGL(k_bup, dim3(p.ldh / kBN + p.ldc / kBN, p.mt, ua.ksplit), dim3(kThreads), 0,
-                         st, ua);
+      const int hot_tiles = p.ldh / kMupN, n_tiles = hot_tiles + p.ldc / kMupN;
+      hipLaunchKernelGGL(k_mup, dim3((n_tiles + 7) / 8 * 8 * p.pmt), dim3(kThreads), 0, st, ua, hot_tiles,
+                         n_tiles, p.pmt);
     }
     OI2_CHECK_LAUNCH();
-    if (ua.ksplit > 1) {
-      const int n = M * ua.ldp;
-      int g = (n + kThreads - 1) / kThreads;
-      hipLaunchKernelGGL(k_bact, dim3(g > 4096 ? 4096 : g), dim3(kThreads), 0, st, ua);
-      OI2_CHECK_LAUNCH();
-    }
   }
   const int n4 = M * (kH / 4);
   int grid = (n4 + kThreads - 1) / kThreads;
@@ -1755,23 +1523,24 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
     OI2_CHECK_LAUNCH();
   }
   if (n_hot) {
-    if (p.prefill) {
-      const dim3 grid(32 * p.pmt * p.hot_splits);
-      if (p.pms == 4)
-        hipLaunchKernelGGL(k_pgemm_down_hot<4>, grid, dim3(kThreads), 0, st, da, p.pmt, p.hot_splits);
-      else
-        hipLaunchKernelGGL(k_pgemm_down_hot<2>, grid, dim3(kThreads), 0, st, da, p.pmt, p.hot_splits);
-    } else {
-      hipLaunchKernelGGL(k_bdown_hot, dim3((kH / kBN) * p.hot_splits, p.mt), dim3(kThreads), 0, st,
-                         da);
-    }
+    const dim3 grid(32 * p.pmt * p.hot_splits);
+    if (p.pms == 4)
+      hipLaunchKernelGGL(k_pgemm_down_hot<4>, grid, dim3(kThreads), 0, st, da, p.pmt, p.hot_splits);
+    else
+      hipLaunchKernelGGL(k_pgemm_down_hot<2>, grid, dim3(kThreads), 0, st, da, p.pmt, p.hot_splits);
     OI2_CHECK_LAUNCH();
   }
   if (has_cold) {
-    const int mtc = (M + 127) / 128;
     const int splits = cold_down_splits(M, cap);
-    hipLaunchKernelGGL((k_pgemm_down_cold<4, false>), dim3(16 * mtc * splits), dim3(kThreads), 0, st, da, mtc,
-                       splits);
+    if (p.prefill) {
+      const int mtc = (M + 127) / 128;
+      hipLaunchKernelGGL((k_pgemm_down_cold<4, false>), dim3(16 * mtc * splits), dim3(kThreads), 0, st, da,
+                         mtc, splits);
+    } else {
+      const int mtc = (M + 63) / 64;
+      hipLaunchKernelGGL((k_pgemm_down_cold<2, false>), dim3(16 * mtc * splits), dim3(kThreads), 0, st, da,
+                         mtc, splits);
+    }
     OI2_CHECK_LAUNCH();
   }
   hipLaunchKernelGGL(k_bfinal, dim3(grid), dim3(kThreads), 0, st, y, nullptr, 0, M, add_residual ? x : nullptr,

@@ -171,7 +171,6 @@ struct BUpArgs {
   const float* hot_gbias;
   uint16_t* hh;             // (Mpad, ldh) fp16 hot activations, zero past n_hot
   int ldh;
-  int hot_wg;               // workgroups of hot columns (ldh / 64, or ldh / 16 for M <= 64)
   const uint8_t* records;
   int n_records;
   const float* cold_gbias;
@@ -180,10 +179,6 @@ struct BUpArgs {
   int cap;
   uint16_t* hc;             // (Mpad, ldc) fp16 cold activations
   int ldc;
-  int ksplit;               // K splits of the tiled kernel (1: it applies the activation)
-  float* pg;                // (ksplit, Mpad, ldp) partial gate sums, hot columns then cold
-  float* pu;
-  int ldp;                  // ldh + ldc
   int Mpad;
   int hot_per_wg;           // k_sbup: hot rows per workgroup (n_hot over 256 workgroups)
 };
