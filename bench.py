@@ -49,6 +49,7 @@ TOKEN_TRAFFIC_BYTES = (802809.9 * 2.0 + 14279.4) * 1024     # k_token
 TOKEN_TRAFFIC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE of k_token on this workload, "
                         "profiles/k_token_traffic_decode32_bs1.md")
 COPY_WORKGROUPS = 8          # the staging copy kernel's workgroups (swept: 6 / 8 / 10 / 12 / 16)
+READER_THREADS = 8           # file store reader threads for batch 8 (8 and 16 measured alike)
 
 
 def log(msg):
@@ -389,9 +390,11 @@ def measure_batch8_file(dev, steps, warmup, seed=4):
     x0 = torch.randn((8, H), generator=g, device=dev).half()
     out = {"tokens_per_step": 8, "layers": N_LAYERS, "n_hot": layers[0].hot.n_hot,
            "file_gb": file_gb, "popularity": "Zipf(1.1) over the intermediate dimension"}
+    link = pcie_link_gbs(dev)
+    out["h2d_link_gbs_pinned_memcpy"] = link
     for mode, direct in (("page_cache", False), ("direct_io", True)):
         try:
-            store = FileStore(cold_bin, cold_idx, direct=direct, threads=8)
+            store = FileStore(cold_bin, cold_idx, direct=direct, threads=READER_THREADS)
         except oi2.OI2Error as e:
             out[mode] = {"error": str(e)}
             continue
@@ -409,13 +412,27 @@ def measure_batch8_file(dev, steps, warmup, seed=4):
         secs = time.perf_counter() - t1
         rec_bytes = st.bytes_read - b0
         assert torch.isfinite(x.float()).all()
+        bound_tok_s = 8 * link * 1e9 / (rec_bytes / steps)
+        serial = None
+        if not direct:
+            serial = host_path_bound(store, layers, rec_bytes / steps / 6400 / N_LAYERS, dev)
         out[mode] = {"tok_s": 8 * steps / secs, "ms_per_step": secs * 1e3 / steps, "steps": steps,
                      "record_bytes_per_step": rec_bytes / steps,
                      "mean_active_cold": rec_bytes / steps / 6400 / N_LAYERS,
-                     "file_read_and_h2d_gbs": rec_bytes / secs / 1e9}
+                     "file_read_and_h2d_gbs": rec_bytes / secs / 1e9,
+                     "reader_threads": READER_THREADS,
+                     "pcie_bound_tok_s": bound_tok_s,
+                     "frac_of_pcie_bound": 8 * steps / secs / bound_tok_s}
+        if serial is not None:
+            out[mode]["host_path"] = serial
+            out[mode]["frac_of_host_path_bound"] = out[mode]["tok_s"] / serial["bound_tok_s"]
         log(f"batch 8 ({mode}): {out[mode]['tok_s']:.1f} tok/s, {out[mode]['ms_per_step']:.2f} ms/step, "
             f"{out[mode]['mean_active_cold']:.0f} active cold per layer, "
-            f"{out[mode]['file_read_and_h2d_gbs']:.2f} GB/s of records from the file")
+            f"{out[mode]['file_read_and_h2d_gbs']:.2f} GB/s of records from the file, "
+            f"{out[mode]['frac_of_pcie_bound']:.3f} of the {bound_tok_s:.0f} tok/s PCIe bound ({link:.1f} GB/s)"
+            + (f"; host path: read {serial['read_us_per_layer']:.0f} + copy {serial['h2d_copy_us_per_layer']:.0f} "
+               f"us/layer, {out[mode]['frac_of_host_path_bound']:.3f} of its {serial['bound_tok_s']:.0f} tok/s"
+               if serial is not None else ""))
         st.close()
         store.close()
     frac = out["page_cache"]["mean_active_cold"] / (INTER - layers[0].hot.n_hot) \
@@ -601,6 +618,38 @@ def measure_config2(dev, B=64, reps=10, seed=12, n_layers=16):
            "kernels": "oi2_ffn_forward at batch 64 (matrix-core batch kernels), graph-replayed"}
     del layers, colds
     return out
+
+
+def host_path_bound(store, layers, n_act, dev, reps=3):
+    """The host side of config 4 alone, per layer: the file store's read of
+    n_act ascending records (page cache -> pinned buffer) and, separately,
+    one pinned -> device copy of those bytes.  On this host the two share
+    the host's memory bandwidth (run side by side they took longer than one
+    after the other), so their sum per layer bounds the step."""
+    import numpy as np
+    import torch
+    n = int(round(n_act))
+    rng = np.random.default_rng(0)
+    host = torch.empty(n * 6400, dtype=torch.uint8).pin_memory()
+    dst = torch.empty(n * 6400, dtype=torch.uint8, device=dev)
+    n_rec = int(layers[0].records.shape[0])
+    sets = [np.sort(rng.choice(n_rec, n, replace=False)).astype(np.int32) for _ in range(N_LAYERS)]
+    best_r = best_c = float("inf")
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        for L in range(N_LAYERS):
+            store.read(L, sets[L], host)
+        best_r = min(best_r, (time.perf_counter() - t0) / N_LAYERS)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for L in range(N_LAYERS):
+            dst.copy_(host, non_blocking=True)
+        torch.cuda.synchronize()
+        best_c = min(best_c, (time.perf_counter() - t0) / N_LAYERS)
+    per_layer = best_r + best_c
+    return {"records_per_layer": n, "read_us_per_layer": best_r * 1e6, "read_gbs": n * 6400 / best_r / 1e9,
+            "h2d_copy_us_per_layer": best_c * 1e6, "h2d_copy_gbs": n * 6400 / best_c / 1e9,
+            "bound_tok_s": 8 / (N_LAYERS * per_layer)}
 
 
 def measure_multi_token(layers, dev, M, frac, reps, seed=1):
@@ -899,6 +948,8 @@ def main():
     ap.add_argument("--attention-only", action="store_true")
     ap.add_argument("--multi-token-only", action="store_true",
                     help="only the multi-token (batch decode / prefill) leg")
+    ap.add_argument("--batch8-only", action="store_true",
+                    help="only the batch-8 Zipf decode with the records read from the file (config 4)")
     ap.add_argument("--configs-only", action="store_true",
                     help="only the single-layer legs: config 1 (bs1 SwiGLU) and config 2 (B=64 dReLU)")
     ap.add_argument("--no-configs", dest="configs", action="store_false",
@@ -939,6 +990,9 @@ def main():
         for side in ("drop_in_layers", "stack_layers"):
             log(f"full decode step ({side}): {res['full_decode_step'][side]['us_per_token']:.0f} us/token")
         print(json.dumps({"attention": res}), flush=True)
+        return
+    if args.batch8_only:
+        print(json.dumps({"batch8_file": measure_batch8_file(dev, args.batch8_steps, 2)}), flush=True)
         return
     if args.configs_only:
         c1 = measure_config1(dev)

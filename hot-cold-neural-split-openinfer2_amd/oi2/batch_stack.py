@@ -9,10 +9,12 @@ compaction; engine.py:432-436) ahead of FFN(L).  The host takes the list
 back, and a worker thread reads those records from the file (liboi2's native
 file store: a mapping of the file, or O_DIRECT page reads) into one of two
 pinned buffers, in list order, while the device computes FFN(L) - the
-reference's executor-backed prefetch (engine.py:266-272, 285-290).  One
-contiguous hipMemcpyAsync on a copy stream then moves them into one of two
-device buffers, and FFN(L+1) (the matrix-core batch kernels, B tokens at
-once) reads them there through a slot-less list.
+reference's executor-backed prefetch (engine.py:266-272, 285-290).  The same
+worker then enqueues one hipMemcpyAsync of them into one of two device
+buffers on a copy stream, and FFN(L+1) (the matrix-core batch kernels, B
+tokens at once) waits for that copy on the device and reads the records
+there through a slot-less list.  A pinned buffer is refilled only after the
+copy that last read it has run.
 """
 from __future__ import annotations
 
@@ -134,9 +136,17 @@ class BatchDecodeStack:
         return n, self._host_slots[par][:n].numpy()
 
     def _read(self, L: int, slots: np.ndarray):
+        """Worker thread: layer L's records from the file into pinned buffer
+        L & 1, their copy to device buffer L & 1 enqueued on the copy
+        stream, then the parity's copy event."""
         n = int(slots.shape[0])
+        par = L & 1
+        # the pinned buffer was last copied out for layer L - 2
+        self._copy_ev[par].synchronize()
         if n:
-            self.store.read(self.layers[L].section, slots, self._ring[L & 1])
+            self.store.stage(self.layers[L].section, slots, self._ring[par], self._stage[par].view(-1),
+                             self.copy_stream)
+        self._copy_ev[par].record(self.copy_stream)
         return n
 
     # ── one step: B tokens through every layer ──
@@ -150,6 +160,9 @@ class BatchDecodeStack:
         if self.trace is not None:
             self.trace.clear()
             self.trace.append([x.clone(), self._host_ids[0][:n0].numpy().copy()])
+        # the device buffer of a parity was last read by FFN(L - 2): the copy
+        # stream waits for it before the worker enqueues the next copies
+        self.copy_stream.wait_event(self._ffn_ev[0])
         fut = self._pool.submit(self._read, 0, sl0)
         for L in range(n_layers):
             lay = self.layers[L]
@@ -160,11 +173,6 @@ class BatchDecodeStack:
             par = L & 1
             cold = None
             if n:
-                # the device buffer of this parity was last read by FFN(L-2)
-                self.copy_stream.wait_event(self._ffn_ev[par])
-                with torch.cuda.stream(self.copy_stream):
-                    self._stage[par].view(-1)[:n * REC].copy_(self._ring[par][:n * REC], non_blocking=True)
-                    self._copy_ev[par].record(self.copy_stream)
                 stream.wait_event(self._copy_ev[par])
                 sec = ColdSection(L, np.zeros(0, np.int64), self._stage[par], lay.lut, None, self.inter)
                 sec.n_records = n
@@ -178,6 +186,7 @@ class BatchDecodeStack:
                 n1, sl1 = self._list(L + 1)
                 if self.trace is not None:
                     self.trace.append([x, self._host_ids[(L + 1) & 1][:n1].numpy().copy()])
+                self.copy_stream.wait_event(self._ffn_ev[(L + 1) & 1])
                 fut = self._pool.submit(self._read, L + 1, sl1)
         return x
 
