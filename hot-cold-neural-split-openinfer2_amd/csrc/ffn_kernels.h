@@ -299,7 +299,6 @@ constexpr int kTokChunks = 256;            // active-list chunks: one per group
 constexpr int kTokMaxChunk = 64;           // ids per chunk (one lane each)
 constexpr int kTokMaxRank = 64;
 constexpr int kTokMaxHot = 4096;           // h staged in LDS; also the per-layer h slice
-constexpr int kTokBatch = 896;             // gather items the worker waves take per layer (list order)
 constexpr int kTokSyncWords = 2048 + 192;
 constexpr int kTokSyncErr = 2048 + 128;       // epoch base + 1 of a launch whose wait ran past its bound
 constexpr int kTokSyncGoD = 64 * 8;           // XCD 0's flag of the D phase
@@ -346,11 +345,9 @@ struct TokArgs {
   uint16_t* xw;             // (n_layers, H) x_L * norm weight of layer L
   float* ssq;               // (n_layers, 256) sum-of-squares partials of x_L
   float* h;                 // (n_layers, kTokMaxHot) hot activations, zero past n_hot
-  float* hc;                // (n_layers, kTokChunks * kTokMaxChunk) cold activations, list order
   double* z;                // (n_layers, 4 * kTokMaxRank) predictor down projection of layer L:
                             // quarter q of row r at 4 r + q
-  float* hcs;               // (n_layers, kGroups, kTokBatch) cold activation x down scale of each
-                            // row group, list positions < kTokBatch
+  float* cpart;             // (n_layers, kTokGroups, H) cold down partial of each chunk with items
   uint32_t* sync;           // kTokSyncWords, zero at allocation
   uint32_t spin;            // poll bound of every device-wide wait
   uint64_t* trace;          // null, or (min(n_layers, kTokTraceLayers), kTokGroups, kTokTracePoints)

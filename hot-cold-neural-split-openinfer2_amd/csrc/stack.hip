@@ -78,9 +78,8 @@ struct oi2_stack {
   uint16_t* tok_xw = nullptr;    // one slice per layer of everything the launch writes
   float* tok_ssq = nullptr;
   float* tok_h = nullptr;
-  float* tok_hc = nullptr;
   double* tok_z = nullptr;
-  float* tok_hcs = nullptr;
+  float* tok_cpart = nullptr;
   int32_t* tok_sel_counts = nullptr;
   int32_t* tok_sel_slots = nullptr;
   int32_t* tok_sel_ids = nullptr;
@@ -344,9 +343,8 @@ static TokArgs tok_args(const oi2_stack* s, const uint16_t* x_in, uint16_t* x_ou
   a.xw = s->tok_xw;
   a.ssq = s->tok_ssq;
   a.h = s->tok_h;
-  a.hc = s->tok_hc;
   a.z = s->tok_z;
-  a.hcs = s->tok_hcs;
+  a.cpart = s->tok_cpart;
   a.sync = s->tok_sync;
   a.spin = s->tok_spin;
   a.eps = s->eps;
@@ -442,8 +440,8 @@ static void stack_free(oi2_stack* s) {
     if (p) (void)hipFree(p);
   s->tok_static.clear();
   for (void* p : {(void*)s->tok_layers, (void*)s->tok_sync, (void*)s->tok_xw, (void*)s->tok_ssq,
-                  (void*)s->tok_h, (void*)s->tok_hc, (void*)s->tok_z, (void*)s->tok_sel_counts,
-                  (void*)s->tok_sel_slots, (void*)s->tok_sel_ids, (void*)s->tok_hcs})
+                  (void*)s->tok_h, (void*)s->tok_z, (void*)s->tok_sel_counts,
+                  (void*)s->tok_sel_slots, (void*)s->tok_sel_ids, (void*)s->tok_cpart})
     if (p) (void)hipFree(p);
   for (void* p : {(void*)s->xbuf, (void*)s->xw, (void*)s->ssq, (void*)s->h_hot, (void*)s->cold_part,
                   (void*)s->z, (void*)s->sel_counts,
@@ -501,9 +499,8 @@ static int tok_setup(oi2_stack* s) {
   alloc((void**)&s->tok_xw, (size_t)n * kH * 2);
   alloc((void**)&s->tok_ssq, (size_t)n * kTokGroups * 4);
   alloc((void**)&s->tok_h, (size_t)n * kTokMaxHot * 4);
-  alloc((void**)&s->tok_hc, (size_t)n * kTokChunks * kTokMaxChunk * 4);
   alloc((void**)&s->tok_z, (size_t)n * 4 * kTokMaxRank * sizeof(double));
-  alloc((void**)&s->tok_hcs, (size_t)n * kGroups * kTokBatch * 4);
+  alloc((void**)&s->tok_cpart, (size_t)n * kTokGroups * kH * 4);
   alloc((void**)&s->tok_sel_counts, (size_t)n * kTokChunks * 4);
   alloc((void**)&s->tok_sel_slots, sel * 4);
   alloc((void**)&s->tok_sel_ids, sel * 4);

@@ -5,10 +5,12 @@
 // 256 workgroups of 512 threads, one per CU, all resident together.  Group g
 // owns, in every layer:
 //   hot      neurons [14 g, 14 g + 14) of the gate/up half (fp8 rows)
-//   cold     chunk g of the layer's active list (INT4 gate/up -> h_cold)
-//   down     output tile g: 16 rows (fp8 down rows x h_hot, plus the 16 down
-//            nibbles of every active cold record x h_cold), the residual and
-//            the next layer's x * w and sum-of-squares partial
+//   cold     chunk g of the layer's active list: the INT4 gate/up of its
+//            records -> h_cold, and their down columns x h_cold summed over
+//            the chunk's items into a partial of all 4096 outputs
+//   down     output tile g: 16 rows (fp8 down rows x h_hot, plus the tile's
+//            rows of every chunk's cold partial), the residual and the next
+//            layer's x * w and sum-of-squares partial
 //   predictor row g of the next layer's z = D q (g < rank), and chunk g of the
 //            next layer's logits, threshold and ascending compaction
 // Each layer is a U phase (gate/up) and a D phase (down), and each phase ends
@@ -21,20 +23,28 @@
 // LDS.  The split matters because a wave's loads complete in order: the
 // control wave never has weight loads in flight ahead of the loads the
 // phase waits on, and the workers never wait on a cross-group input.
-// Worker loads, in issue order per layer: gather nibbles and half the next
-// gate/up rows (end of U, after the control wave's stores are acknowledged
-// and its arrival is issued: B3), the other half (D1a, once the phase's
-// inputs are in), then at the end of D (D2, once the control wave has
-// computed the next list, which overlaps the workers' down products, and
-// issued the phase's stores) the next chunk's records and the next layer's
-// first down rows; the gather items' slots at B1 (a few loads, found by an
-// LDS search that the SIMD's other wave overlaps with its products), and the
-// other down rows after the U products (issued earlier they would stall
-// those products while the CU's memory queue is full).  Each
-// phase's compute needs only loads older than the ones still streaming, and
-// the halves issued at B1 / D1 go out after the phase's cross-group inputs:
-// a CU's memory pipeline is in order, and a backlog of weight loads ahead of
-// those inputs would delay the whole phase.
+// Worker loads, in issue order per layer: half the next gate/up rows (end of
+// U, after the control wave's stores are acknowledged and its arrival is
+// issued: B3), the other half (D1a, once the phase's inputs are in), then at
+// the end of D (D2, once the control wave has computed the next list, which
+// overlaps the workers' down products, and issued the phase's stores) the
+// next chunk's records and the next layer's first down rows, and the other
+// down rows after the U products (issued earlier they would stall those
+// products while the CU's memory queue is full).  Each phase's compute needs
+// only loads older than the ones still streaming, and the halves issued at
+// B1 / D1 go out after the phase's cross-group inputs: a CU's memory pipeline
+// is in order, and a backlog of weight loads ahead of those inputs would
+// delay the whole phase.
+//
+// The cold down projection is done where the records are: after the U
+// products every wave of a group with items takes 512 output rows and sums
+// its chunk's items' down nibbles x activation x scale over them, in list
+// order; the control wave stores the 16 KB partial, and in the D phase each
+// output tile adds its 16 rows of every chunk's partial (chunks without items
+// are skipped), in chunk order.  (The alternative, each tile gathering the 8
+// bytes of its rows from every active record, costs ~540 scattered loads per
+// group per layer; they queue ahead of the U signal's polls, and the groups
+// whose rows share a cache line across XCDs see the signal ~2.5 us late.)
 //
 // Signals: per-XCD arrival counters (32 groups each); the last arrival of an
 // XCD writes that XCD's flag for the phase, and a waiting group polls all 8
@@ -67,13 +77,11 @@ constexpr int kSc1 = 16;                       // cache-policy operand: agent-co
 constexpr int kWorkers = kTokThreads / kWave - 1;
 constexpr int kColdR = 1;                      // cold records per worker (items wi + 7 i)
 constexpr int kCtlCold = 2;                    // the control wave's items, right after the workers'
-constexpr int kGat = 2;                        // gather items per worker lane per batch
-constexpr int kBatch = kWorkers * kWave * kGat;
-constexpr int kCtlItems = kBatch / kWave;      // gather items per control lane per batch
 constexpr int kRows = kH / kTokGroups;         // 16 output rows per group
+constexpr int kSlice = kH / (kWorkers + 1);    // cold partial rows per wave: 512, 8 per lane
+constexpr int kPre = 16;                       // items whose slice nibbles are in LDS before the U phase
 static_assert(kWorkers == 7, "the row split and the epilogue's sum assume 7 workers");
 static_assert(kTokWorkers == kWorkers, "host and kernel agree on the worker count");
-static_assert(kTokBatch == kBatch, "host and kernel agree on the gather batch");
 
 // The layer table through the constant address space: its fields load with
 // scalar loads, which wait on their own counter, so reading them never makes
@@ -90,6 +98,9 @@ __device__ __forceinline__ void cst2(rsrc_t r, uint32_t off, uint16_t v) {
 }
 __device__ __forceinline__ void cst4(rsrc_t r, uint32_t off, uint32_t v) {
   __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, kSc1);
+}
+__device__ __forceinline__ void cst16(rsrc_t r, uint32_t off, u32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, kSc1);
 }
 __device__ __forceinline__ void cst8(rsrc_t r, uint32_t off, double v) {
   const uint64_t u = __builtin_bit_cast(uint64_t, v);
@@ -197,53 +208,96 @@ struct alignas(16) TokShared {
   uint32_t pd[kH / 8];        //   and of its predictor down row (bf16)
   float h[kTokMaxHot];        // the layer's hot activations
   uint32_t pu[8 * kWave * 4]; // predictor up rows of chunk g: 16-byte piece m of neuron l at 64 m + l
-  float it_hcs[1024];         // gather items of the current batch: cold activation x down scale
-                              // of the tile's row group (list order; 4 KB, one copy's reach),
-  float hcs_out[kGroups][kTokMaxChunk];   // this group's items: activation x down scale, per row group
+  float ycp[kH];              // this group's cold down partial (its chunk's items), all rows
+  uint32_t snib[kWorkers + 1][kPre][kWave];   // the first items' down nibbles: wave w's slice, lane l
+  uint16_t sdsc[kPre][kGroups];               // and their down scales
+  float cpin[kTokGroups * kRows];   // every chunk's cold partial, the tile's 16 rows (chunk-major)
   float dsc[kRows];           // the tile's down row scales
-  int pfx[kTokChunks + 1];    // exclusive prefix of the list's chunk counts
+  int cnt[kTokChunks];        // the layer's chunk counts
   int lst_slot[kTokMaxChunk]; // chunk g of the next layer's list
   int lst_id[kTokMaxChunk];
   float h_out[kWorkers * 3];  // this group's hot activations
   float hc_out[kTokMaxChunk]; // this group's cold activations (chunk order)
   float cpart[kWorkers][kRows];
-  float cpart_ctl[kRows];     // the control wave's share of long gather lists
   float out[kRows];
   double z[kTokMaxRank];
   uint64_t trace[kTokTraceLayers][kTokTracePoints];   // the control wave's stamps, when traced
   float r;
-  int total, lst_cnt;
+  int lst_cnt;
 };
 static_assert(offsetof(TokShared, nat) % 16 == 0 && offsetof(TokShared, xq) % 16 == 0 &&
               offsetof(TokShared, wq) % 16 == 0 && offsetof(TokShared, pd) % 16 == 0 &&
               offsetof(TokShared, h) % 16 == 0 && offsetof(TokShared, pu) % 16 == 0 &&
-              offsetof(TokShared, it_hcs) % 16 == 0 && offsetof(TokShared, dsc) % 16 == 0,
+              offsetof(TokShared, ycp) % 16 == 0 && offsetof(TokShared, cpin) % 16 == 0 &&
+              offsetof(TokShared, dsc) % 16 == 0,
               "LDS DMA targets and 16-byte reads are 16-byte aligned");
 
-// List positions of items i[m] (0 <= i[m] < total): item i - pfx[c] of the
-// chunk c with pfx[c] <= i < pfx[c + 1], that is the last c < kTokChunks
-// with pfx[c] <= i (empty chunks before it have smaller c, those after it a
-// larger prefix).  A four-way search over the 256 chunks, 4 steps of 3 LDS
-// reads each, the M searches interleaved so that their reads overlap.
-template <int M>
-__device__ __forceinline__ void list_pos(const TokShared& sh, const int (&i)[M], int chunk, int (&pos)[M]) {
-  static_assert(kTokChunks == 256, "four steps of a four-way search");
-  int lo[M];
+// The cold down partial of this group's chunk for rows 512 w + 8 l .. + 8
+// (wave w, lane l): every item of the chunk in list order, its down nibbles
+// times its activation times the rows' group scale (the two-launch path's
+// arithmetic: activation x scale in fp32, then the fma with the nibble).
+// Items k < kPre come from LDS (loaded by the control wave before the phase);
+// the rest are loaded here, four at a time.  Result to ycp.
+__device__ __forceinline__ void cold_slice(const TokShared& sh, float* ycp, int w, int cnt, rsrc_t rrec,
+                                           int n_records) {
+  const int l = lane_id();
+  const uint32_t nb_off = kOffDown + (uint32_t)(kSlice / 2 * w + 4 * l);
+  const uint32_t sc_off = kOffScales + 2 * (uint32_t)(2 * kGroups + kSlice / kGroup * w + (8 * l) / kGroup);
+  float y8[8];
 #pragma unroll
-  for (int m = 0; m < M; ++m) lo[m] = 0;
+  for (int e = 0; e < 8; ++e) y8[e] = 0.0f;
+  auto add = [&](uint32_t nib, float sc, float hv) {
+    const float hs = hv * sc;
+    f16x2 tq[4];
+    int4x8_to_f16x2x4(nib, tq);
 #pragma unroll
-  for (int st = 64; st >= 1; st >>= 2) {
-    int p[M][3];
+    for (int k = 0; k < 4; ++k) {
+      y8[k] = fmaf(hs, (float)tq[k].x, y8[k]);
+      y8[k + 4] = fmaf(hs, (float)tq[k].y, y8[k + 4]);
+    }
+  };
+  const int kp = cnt < kPre ? cnt : kPre;
+  for (int k = 0; k < kp; ++k)
+    add(sh.snib[w][k][l], half_bits_to_float(sh.sdsc[k][kSlice / kGroup * w + (8 * l) / kGroup]), sh.hc_out[k]);
+  for (int k0 = kPre; k0 < cnt; k0 += 4) {
+    uint32_t nb[4];
+    float sc[4];
 #pragma unroll
-    for (int m = 0; m < M; ++m)
+    for (int q = 0; q < 4; ++q) {
+      const int k = k0 + q;
+      const int sl = k < cnt ? sh.lst_slot[k] : -1;
+      const uint32_t ro = (sl >= 0 && sl < n_records) ? (uint32_t)sl * kRecBytes : kNoOff;
+      nb[q] = bld4(rrec, ro == kNoOff ? kNoOff : ro + nb_off);
+      sc[q] = half_bits_to_float(bld2(rrec, ro == kNoOff ? kNoOff : ro + sc_off));
+    }
 #pragma unroll
-      for (int q = 0; q < 3; ++q) p[m][q] = sh.pfx[lo[m] + st * (q + 1)];
-#pragma unroll
-    for (int m = 0; m < M; ++m)
-      lo[m] += st * ((int)(p[m][0] <= i[m]) + (int)(p[m][1] <= i[m]) + (int)(p[m][2] <= i[m]));
+    for (int q = 0; q < 4; ++q)
+      if (k0 + q < cnt) add(nb[q], sc[q], sh.hc_out[k0 + q]);
   }
+  reinterpret_cast<f32x4*>(ycp)[2 * l] = f32x4{y8[0], y8[1], y8[2], y8[3]};
+  reinterpret_cast<f32x4*>(ycp)[2 * l + 1] = f32x4{y8[4], y8[5], y8[6], y8[7]};
+}
+
+// Control wave, before the U phase's wait: the down nibbles of every wave's
+// slice and the down scales of the chunk's first kPre items into LDS (their
+// completion is covered by the wave's vmcnt(0) before B1).
+__device__ __forceinline__ void slice_preload(TokShared& sh, int cnt, rsrc_t rrec, int n_records) {
+  const int l = lane_id();
+  const int kp = cnt < kPre ? cnt : kPre;
+  for (int k = 0; k < kp; ++k) {
+    const int sl = sh.lst_slot[k];
+    const bool ok = sl >= 0 && sl < n_records;
+    const uint32_t ro = (uint32_t)sl * kRecBytes;
 #pragma unroll
-  for (int m = 0; m < M; ++m) pos[m] = lo[m] * chunk + (i[m] - sh.pfx[lo[m]]);
+    for (int w = 0; w <= kWorkers; ++w)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rrec, (lds_void*)sh.snib[w][k], 4, ok ? ro + kOffDown + (uint32_t)(kSlice / 2 * w + 4 * l) : kNoOff, 0, 0, 0);
+  }
+  // scales: lane l takes 16 bytes l & 3 of item l >> 2's 64-byte down scale array
+  const int k = l >> 2;
+  const int sl = k < kp ? sh.lst_slot[k] : -1;
+  const bool ok = sl >= 0 && sl < n_records;
+  bld16_lds(rrec, sh.sdsc, ok ? (uint32_t)sl * kRecBytes + kOffScales + 4 * kGroups + 16 * (uint32_t)(l & 3) : kNoOff);
 }
 
 // ── the control wave ────────────────────────────────────────────────────────
@@ -284,7 +338,7 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
     const rsrc_t rcgb = rsrc(has_cold ? T->cold_gbias : nullptr,
                              (has_cold && T->cold_gbias) ? (uint32_t)T->n_records * 4 : 0u);
     u32x4 CQ[kCtlCold][4];
-    float CS[kCtlCold][4], CG[kCtlCold], CD[kCtlCold];   // CD: down scale of row group l
+    float CS[kCtlCold][4], CG[kCtlCold];
     int CSL[kCtlCold];
 #pragma unroll
     for (int i = 0; i < kCtlCold; ++i) {
@@ -304,8 +358,11 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
         CS[i][2 * q + 1] = half_bits_to_float(bld2(rrec, ro + kOffScales + 2 * (32 * q + 16 + g0)));
       }
       CG[i] = as_f32(bld4(rcgb, vv ? 4 * (uint32_t)sl : kNoOff));
-      CD[i] = half_bits_to_float(bld2(rrec, ro + kOffScales + 2 * (2 * kGroups + (l & (kGroups - 1)))));
     }
+    // the slices of the chunk's cold down partial: the first items' nibbles
+    // and scales
+    const int nrec = has_cold ? T->n_records : 0;
+    if (has_cold) slice_preload(sh, ccnt, rrec, nrec);
     if (L >= 0) tok_wait(a.sync, 1, g, base + (uint32_t)(L + 1), base, a.spin);
     TOK_TRACE(L, 0);
     // inputs the previous phase produced: x * w into LDS, the sum-of-squares
@@ -349,33 +406,13 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
         bld16_lds(rx, sh.xq + 256 * it, 16 * (uint32_t)(l + 64 * (2 * (g & 3) + it)));
     }
     const float r = r_from_part(f32x4{as_f32(pp.x), as_f32(pp.y), as_f32(pp.z), as_f32(pp.w)}, a.eps);
-    // exclusive prefix of the chunk counts (lane l: chunks 4 l .. 4 l + 3)
-    int tot4 = 0;
+    // the chunk counts (lane l: chunks 4 l .. 4 l + 3): which chunks' cold
+    // partials the D phase reads
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      cnt4[q] = min(max(cnt4[q], 0), chunk);
-      tot4 += cnt4[q];
-    }
-    int v = tot4;
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-      const int u = __shfl_up(v, off, kWave);
-      if (l >= off) v += u;
-    }
-    const int total = __shfl(v, kWave - 1, kWave);
-    int run = v - tot4;
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      sh.pfx[4 * l + q] = run;
-      run += cnt4[q];
-    }
-    if (l == 0) {
-      sh.pfx[kTokChunks] = total;
-      sh.total = total;
-      sh.r = r;
-    }
+    for (int q = 0; q < 4; ++q) sh.cnt[4 * l + q] = min(max(cnt4[q], 0), chunk);
+    if (l == 0) sh.r = r;
     wait_vm();
-    bar();   // B1: x * w, r and the list prefix are in LDS
+    bar();   // B1: x * w, r and the chunk counts are in LDS
     TOK_TRACE(L, 1);
     // a quarter of the next layer's predictor row: z = D q, q =
     // bf16(fp16(x r w')) (pred_d_role's arithmetic and partial sums);
@@ -418,10 +455,9 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
           CS[0][2 * q + 1] = half_bits_to_float(bld2(rrec, ro + kOffScales + 2 * (32 * q + 16 + g0)));
         }
         CG[0] = as_f32(bld4(rcgb, vv ? 4 * (uint32_t)sl : kNoOff));
-        CD[0] = half_bits_to_float(bld2(rrec, ro + kOffScales + 2 * (2 * kGroups + (l & (kGroups - 1)))));
       }
       const int c = i >= kCtlCold ? 0 : i;
-      float hv = 0.0f, hs = 0.0f;
+      float hv = 0.0f;
 #pragma unroll
       for (int cc = 0; cc < kCtlCold; ++cc) {
         if (cc != c) continue;
@@ -445,33 +481,27 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
         const float gv = r * wave_sum(pg[0] * CS[cc][0] + pg[1] * CS[cc][1]) + CG[cc];
         const float uv = r * wave_sum(pu[0] * CS[cc][2] + pu[1] * CS[cc][3]);
         hv = gated_act(gv, uv, a.relu, a.both);
-        hs = hv * CD[cc];
       }
       if (l == 0) sh.hc_out[k] = hv;
-      if (l < kGroups) sh.hcs_out[l][k] = hs;
     }
     bar();   // B2: the workers' activations are in LDS
     TOK_TRACE(L, 2);
+    // this wave's rows of the cold down partial, then every wave's in LDS
+    if (has_cold && ccnt > 0) cold_slice(sh, sh.ycp, 0, ccnt, rrec, nrec);
+    bar();
     if (pred && l == 0)
       cst8(rsrc(a.z + (size_t)(L + 1) * 4 * kTokMaxRank, 4 * kTokMaxRank * 8), 8 * (uint32_t)g, zrow);
     if (T) {
       const int k = g * kWorkers * NPW + l;
       if (l < kWorkers * NPW && k < T->n_hot)
         cst4(rsrc(a.h + (size_t)L * kTokMaxHot, kTokMaxHot * 4), 4 * (uint32_t)k, as_u32(sh.h_out[l]));
-      if (has_cold && l < sh.lst_cnt)
-        cst4(rsrc(a.hc + (size_t)L * kTokChunks * kTokMaxChunk, kTokChunks * kTokMaxChunk * 4),
-             4 * (uint32_t)(g * chunk + l), as_u32(sh.hc_out[l]));
-      // activation x down scale of every row group, at the items' list
-      // positions (those the workers gather): lane l takes group l & 31 of
-      // item k0 + (l >> 5)
-      if (has_cold) {
-        const int p0 = sh.pfx[g], cnt = sh.lst_cnt;
-        const rsrc_t rs = rsrc(a.hcs + (size_t)L * kGroups * kBatch, kGroups * kBatch * 4);
-        for (int k0 = 0; k0 < cnt && p0 + k0 < kBatch; k0 += 2) {
-          const int k = k0 + (l >> 5), gi = l & (kGroups - 1);
-          if (k < cnt && p0 + k < kBatch)
-            cst4(rs, 4 * (uint32_t)(gi * kBatch + p0 + k), as_u32(sh.hcs_out[gi][k]));
-        }
+      // the chunk's cold down partial (chunks without items store none;
+      // the D phase skips them by their count)
+      if (has_cold && ccnt > 0) {
+        const rsrc_t rc = rsrc(a.cpart + ((size_t)L * kTokGroups + g) * kH, kH * 4);
+#pragma unroll
+        for (int i = 0; i < kH / 4 / kWave; ++i)
+          cst16(rc, 16 * (uint32_t)(l + kWave * i), reinterpret_cast<const u32x4*>(sh.ycp)[l + kWave * i]);
       }
     }
     // B3 (inside): the stores are acknowledged and the arrival is issued,
@@ -524,10 +554,16 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
       const rsrc_t rh = rsrc(a.h + (size_t)L * kTokMaxHot, kTokMaxHot * 4);
 #pragma unroll
       for (int it = 0; it < kTokMaxHot * 4 / 1024; ++it) bld16_lds(rh, sh.h + 256 * it, 16 * (l + 64 * it));
+      // the tile's 16 rows of every chunk's cold partial (chunk-major; a
+      // chunk without items reads zero)
       if (has_cold) {
-        const rsrc_t rg = rsrc(a.hcs + ((size_t)L * kGroups + j0 / kGroup) * kBatch, kBatch * 4);
+        const rsrc_t rc = rsrc(a.cpart + (size_t)L * kTokGroups * kH, kTokGroups * kH * 4);
 #pragma unroll
-        for (int it = 0; it < 4; ++it) bld16_lds(rg, sh.it_hcs + 256 * it, 16 * (l + 64 * it));
+        for (int m = 0; m < kTokGroups * kRows / 4 / kWave; ++m) {
+          const int cg = 16 * m + (l >> 2);
+          const uint32_t off = sh.cnt[cg] > 0 ? 4 * (uint32_t)(cg * kH + j0) + 16 * (uint32_t)(l & 3) : kNoOff;
+          bld16_lds(rc, sh.cpin + 256 * m, off);
+        }
       }
     }
     double zl = 0.0;
@@ -578,56 +614,6 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
     }
     bar();   // D1b: the next chunk's list is in LDS
     TOK_TRACE(L, 6);
-    // gather items past the first batch (long lists): this wave, a batch of
-    // 64 at a time, while the workers run the first
-    float ycc[kRows];
-#pragma unroll
-    for (int e = 0; e < kRows; ++e) ycc[e] = 0.0f;
-    if (T && has_cold && total > kBatch) {
-      const rsrc_t rsl = rsrc(T->act_slots, (uint32_t)kTokChunks * chunk * 4);
-      const rsrc_t rhc = rsrc(a.hc + (size_t)L * kTokChunks * kTokMaxChunk, kTokChunks * kTokMaxChunk * 4);
-      for (int i0 = kBatch; i0 < total; i0 += kWave) {
-        const int i = i0 + l;
-        int pos = -1;
-        if (i < total) {
-          int lo = 0, hi = kTokChunks;        // pfx[lo] <= i < pfx[hi]
-          while (hi - lo > 1) {
-            const int mid = (lo + hi) >> 1;
-            if (sh.pfx[mid] <= i) lo = mid;
-            else hi = mid;
-          }
-          pos = lo * chunk + (i - sh.pfx[lo]);
-        }
-        const int sl = (int)bld4(rsl, pos >= 0 ? 4 * (uint32_t)pos : kNoOff);
-        const bool vv = pos >= 0 && sl >= 0 && sl < T->n_records;
-        const uint32_t ro = vv ? (uint32_t)sl * kRecBytes : kNoOff;
-        const u32x2v nib = bld8(rrec, ro + kOffDown + j0 / 2);
-        const float sc = half_bits_to_float(bld2(rrec, ro + kOffScales + 2 * (64 + j0 / kGroup)));
-        const float hs = as_f32(bld4(rhc, vv ? 4 * (uint32_t)pos : kNoOff)) * sc;
-        f16x2 tq[4];
-        int4x8_to_f16x2x4(nib.x, tq);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          ycc[k] = fmaf(hs, (float)tq[k].x, ycc[k]);
-          ycc[k + 4] = fmaf(hs, (float)tq[k].y, ycc[k + 4]);
-        }
-        int4x8_to_f16x2x4(nib.y, tq);
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          ycc[8 + k] = fmaf(hs, (float)tq[k].x, ycc[8 + k]);
-          ycc[12 + k] = fmaf(hs, (float)tq[k].y, ycc[12 + k]);
-        }
-      }
-    }
-    if (T && has_cold && total > kBatch) {
-#pragma unroll
-      for (int e = 0; e < kRows; ++e) {
-        const float sv = wave_sum(ycc[e]);
-        if (l == 0) sh.cpart_ctl[e] = sv;
-      }
-    } else if (l < kRows) {
-      sh.cpart_ctl[l] = 0.0f;
-    }
     // the next layer's list, after every use of a loaded value: the compiler
     // makes a wave wait for its outstanding stores before it uses a load
     // issued ahead of them
@@ -642,8 +628,8 @@ __device__ void control(const TokArgs& a, int g, TokShared& sh) {
     // the epilogue: the workers' row sums were in LDS at D1b
     if (T) {
       if (l < kRows) {
-        const float y = (((sh.cpart[0][l] + sh.cpart[1][l]) + (sh.cpart[2][l] + sh.cpart[3][l])) +
-                         ((sh.cpart[4][l] + sh.cpart[5][l]) + sh.cpart[6][l])) + sh.cpart_ctl[l];
+        const float y = ((sh.cpart[0][l] + sh.cpart[1][l]) + (sh.cpart[2][l] + sh.cpart[3][l])) +
+                        ((sh.cpart[4][l] + sh.cpart[5][l]) + sh.cpart[6][l]);
         const uint16_t ob = float_to_half_bits(res_v + y);
         cst2(rsrc(a.xbuf + (size_t)L * kH, kH * 2), 2 * (uint32_t)(j0 + l), ob);
         if (L == n - 1) __builtin_amdgcn_raw_buffer_store_b16(ob, rsrc(a.x_out, kH * 2), 2 * (uint32_t)(j0 + l), 0, 0);
@@ -693,7 +679,8 @@ __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
   const int j0 = tile * kRows;
   // down rows: every worker lane takes kpl columns of all 16 rows of the tile
   // (columns k0 .. k0 + kpl), so the h reads and the products are split
-  // evenly; its per-row sums join the cold terms' before one reduction
+  // evenly; its per-row sums take one chunk's cold partial (lane slot
+  // wi 64 + l < 256) before one reduction
   constexpr int kpl = NPW == 2 ? 8 : 16;
   static_assert(kWorkers * kWave * kpl >= (NPW == 2 ? NPW * kWorkers * kTokGroups : kTokMaxHot),
                 "the worker columns cover every hot neuron");
@@ -709,10 +696,7 @@ __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
   u32x4 RQ[kColdR][4];        // cold records of the chunk: gate and up halves,
   float RS[kColdR][4];        //   their group scales,
   float RG[kColdR];           //   gate bias
-  int RSL[kColdR];            //   slots,
-  float RD[kColdR];           //   and the down scale of row group l (lanes < kGroups)
-  int NPOS[kGat], NSL[kGat];  // gather items (list positions wi 64 + l + 448 m): position and slot,
-  u32x2v NB[kGat];            //   down nibbles of the tile's rows
+  int RSL[kColdR];            //   and slots
   // neurons [j0h, j1h) of the gate/up rows (and, with the first, the scales)
   auto load_hot = [&](int L, int j0h, int j1h) {          // L may be n: reads zero
     const bool v = L < n;
@@ -778,47 +762,13 @@ __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
         RS[i][2 * q + 1] = half_bits_to_float(bld2(rr, ro + kOffScales + 2 * (32 * q + 16 + g0)));
       }
       RG[i] = as_f32(bld4(rb, ok ? 4 * (uint32_t)sl : kNoOff));
-      RD[i] = half_bits_to_float(bld2(rr, ro + kOffScales + 2 * (2 * kGroups + (l & (kGroups - 1)))));
     }
   };
-  // record slots of this lane's gather items of layer L: list positions from
-  // the prefix in LDS, slots loaded here and checked when used
-  auto load_slots = [&](int L) {
-    const bool v = L >= 0 && LT[L].n_records > 0 && LT[L].act_counts;
-    CLayer& T = LT[L >= 0 ? L : 0];
-    const int chunk = v ? T.act_chunk : 0;
-    const int total = v ? sh.total : 0;
-    const rsrc_t rs = rsrc(T.act_slots, v ? (uint32_t)kTokChunks * chunk * 4 : 0u);
-    int it[kGat];
-#pragma unroll
-    for (int m = 0; m < kGat; ++m) it[m] = wi * kWave + l + kWorkers * kWave * m;
-    list_pos(sh, it, chunk, NPOS);
-#pragma unroll
-    for (int m = 0; m < kGat; ++m) {
-      if (it[m] >= total) NPOS[m] = -1;
-      NSL[m] = (int)bld4(rs, NPOS[m] >= 0 ? 4 * (uint32_t)NPOS[m] : kNoOff);
-    }
-  };
-  // down nibbles of those items
-  auto load_nibbles = [&](int L) {
-    const bool v = L >= 0 && LT[L].n_records > 0 && LT[L].act_counts;
-    CLayer& T = LT[L >= 0 ? L : 0];
-    const int nr = v ? T.n_records : 0;
-    const rsrc_t rr = rsrc(T.records, v ? (uint32_t)T.n_records * kRecBytes : 0u);
-#pragma unroll
-    for (int m = 0; m < kGat; ++m) {
-      NSL[m] = (NPOS[m] >= 0 && NSL[m] >= 0 && NSL[m] < nr) ? NSL[m] : -1;
-      const uint32_t ro = NSL[m] >= 0 ? (uint32_t)NSL[m] * kRecBytes : kNoOff;
-      NB[m] = bld8(rr, ro + kOffDown + j0 / 2);
-    }
-  };
-
   for (int L = -1; L < n; ++L) {
     CLayer* T = L >= 0 ? LT + L : nullptr;
     const bool has_cold = T && T->n_records > 0 && T->act_counts;
     // ================= U phase
     bar();   // B1: the control's inputs have landed
-    load_slots(L);               // the slots of this lane's gather items (the prefix is in LDS)
     if (T) {
       const float r = sh.r;
       // hot neurons (the accumulation order of the two-launch path)
@@ -864,7 +814,10 @@ __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
       if (has_cold) {
 #pragma unroll
         for (int i = 0; i < kColdR; ++i) {
-          if (RSL[i] < 0) continue;
+          if (RSL[i] < 0) {   // an invalid slot contributes zero to the partial
+            if (l == 0 && wi + kWorkers * i < sh.lst_cnt) sh.hc_out[wi + kWorkers * i] = 0.0f;
+            continue;
+          }
           float pg[2] = {0.0f, 0.0f}, pu[2] = {0.0f, 0.0f};
 #pragma unroll
           for (int it = 0; it < 2; ++it) {
@@ -887,14 +840,17 @@ __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
           const float uv = r * readlane_f(su[1], kWave - 1);
           const float hv = gated_act(gv, uv, a.relu, a.both);
           if (l == 0) sh.hc_out[wi + kWorkers * i] = hv;
-          if (l < kGroups) sh.hcs_out[l][wi + kWorkers * i] = hv * RD[i];
         }
       }
     }
     load_down(L, 6, kRows);      // the rest of this layer's down rows
-    bar();   // B2
+    bar();   // B2: every item's activation is in LDS
+    // this wave's rows of the chunk's cold down partial
+    if (has_cold && sh.lst_cnt > 0)
+      cold_slice(sh, sh.ycp + kSlice * (wi + 1), wi + 1, sh.lst_cnt, rsrc(T->records, (uint32_t)T->n_records * kRecBytes),
+                 T->n_records);
+    bar();   // every wave's slice is in LDS
     bar();   // B3
-    load_nibbles(L);
     load_hot(L + 1, 0, 1);       // half the next gate/up rows now ...
     // ================= D phase
     bar();   // D1a: the control's inputs have landed
@@ -928,27 +884,15 @@ __device__ void worker(const TokArgs& a, int g, int wi, TokShared& sh) {
         }
         yc[r] = p * sh.dsc[r];
       }
-      // cold: this lane's items of the first gather batch x their 16 down nibbles
-      if (has_cold) {
+      // cold: chunk wi 64 + l's partial of the tile's 16 rows (zero for a
+      // chunk without items)
+      if (has_cold && wi * kWave + l < kTokGroups) {
+        const f32x4* cp = reinterpret_cast<const f32x4*>(sh.cpin + (wi * kWave + l) * kRows);
 #pragma unroll
-        for (int m = 0; m < kGat; ++m) {
-          const int i = wi * kWave + l + kWorkers * kWave * m;
-          if (NSL[m] >= 0) {
-            const float hs = sh.it_hcs[i];
-            f16x2 tq[4];
-            int4x8_to_f16x2x4(NB[m].x, tq);
+        for (int q = 0; q < kRows / 4; ++q) {
+          const f32x4 v = cp[q];
 #pragma unroll
-            for (int k = 0; k < 4; ++k) {
-              yc[k] = fmaf(hs, (float)tq[k].x, yc[k]);
-              yc[k + 4] = fmaf(hs, (float)tq[k].y, yc[k + 4]);
-            }
-            int4x8_to_f16x2x4(NB[m].y, tq);
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-              yc[8 + k] = fmaf(hs, (float)tq[k].x, yc[8 + k]);
-              yc[12 + k] = fmaf(hs, (float)tq[k].y, yc[12 + k]);
-            }
-          }
+          for (int e = 0; e < 4; ++e) yc[4 * q + e] += v[e];
         }
       }
       const float yt = wave_sums16_transposed(yc);   // lane l: row l & 15
