@@ -16,9 +16,12 @@
 //          or lie within the read gap (16 KB unless set) of each other are read
 //          with one pread: on a device bound by its operation rate, reading a
 //          gap costs less than another operation.
-// A request is split over a fixed pool of threads by contiguous runs of the
+// A read is split over a fixed pool of threads by contiguous runs of the
 // records sorted by file position; each thread plans and issues its own
-// reads.  The call returns when every record is in place.
+// reads.  The call returns when every record is in place.  A staged read
+// (read, then copy to the device) overlaps the two: the threads take chunks
+// of the request in order and the caller enqueues the copy of each finished
+// run from the front while the rest are still being read.
 #include <errno.h>
 #include <fcntl.h>
 #include <stdarg.h>
@@ -29,8 +32,11 @@
 #include <sys/mman.h>
 #include <sys/stat.h>
 #include <unistd.h>
+#include <emmintrin.h>
 
 #include <algorithm>
+#include <atomic>
+#include <chrono>
 #include <condition_variable>
 #include <functional>
 #include <mutex>
@@ -72,13 +78,22 @@ class Pool {
   }
   int size() const { return (int)workers_.size(); }
   void run(int n, const std::function<void(int)>& fn) {
-    std::unique_lock<std::mutex> l(mu_);
+    start(n, fn);
+    wait();
+  }
+  // start(n, fn) hands out fn(0..n-1) and returns at once; wait() returns
+  // when every call is done.  fn must stay alive until wait() returns.
+  void start(int n, const std::function<void(int)>& fn) {
+    std::lock_guard<std::mutex> l(mu_);
     fn_ = &fn;
     next_ = 0;
     total_ = n;
     done_ = 0;
     ++gen_;
     cv_.notify_all();
+  }
+  void wait() {
+    std::unique_lock<std::mutex> l(mu_);
     done_cv_.wait(l, [&] { return done_ == total_; });
     fn_ = nullptr;
   }
@@ -127,14 +142,40 @@ struct oi2_file_store {
 
 namespace {
 
+// One record into a 16-byte aligned destination with non-temporal stores:
+// a cached store first reads the destination line (for ownership), so a plain
+// copy moves each byte over the memory bus three times; streaming stores
+// write it once.  On a host where the read and the device copy share the
+// memory bandwidth that is a quarter less traffic per staged record.
+inline void copy_record_nt(uint8_t* dst, const uint8_t* src) {
+  static_assert(kRec % 64 == 0, "whole 64-byte lines");
+  __m128i* d = reinterpret_cast<__m128i*>(dst);
+  const __m128i* s = reinterpret_cast<const __m128i*>(src);
+  for (size_t k = 0; k < kRec / 16; k += 4) {
+    const __m128i a = _mm_loadu_si128(s + k), b = _mm_loadu_si128(s + k + 1);
+    const __m128i c = _mm_loadu_si128(s + k + 2), e = _mm_loadu_si128(s + k + 3);
+    _mm_stream_si128(d + k, a);
+    _mm_stream_si128(d + k + 1, b);
+    _mm_stream_si128(d + k + 2, c);
+    _mm_stream_si128(d + k + 3, e);
+  }
+}
+
 // Copy out records [b, e) of `order` (indices into slots, sorted by file
-// position) with buffered memcpy from the mapping.
+// position) from the mapping: streaming stores into a 16-byte aligned
+// destination (the whole run fenced at its end), else memcpy.
 void read_mapped(oi2_file_store* fs, uint64_t base, const int32_t* slots, const int32_t* order, int b,
                  int e, uint8_t* dst) {
+  const bool nt = (reinterpret_cast<uintptr_t>(dst) & 15) == 0;
   for (int k = b; k < e; ++k) {
     const int i = order[k];
-    memcpy(dst + (size_t)i * kRec, fs->map + base + kHeader + (uint64_t)slots[i] * kRec, kRec);
+    const uint8_t* src = fs->map + base + kHeader + (uint64_t)slots[i] * kRec;
+    if (nt)
+      copy_record_nt(dst + (size_t)i * kRec, src);
+    else
+      memcpy(dst + (size_t)i * kRec, src, kRec);
   }
+  if (nt) _mm_sfence();
 }
 
 // The same with O_DIRECT page reads through this part's bounce buffer.
@@ -259,8 +300,12 @@ int oi2_file_store_open(const char* path, const uint64_t* index, int32_t n_secti
   return OI2_OK;
 }
 
-int oi2_file_store_read(oi2_file_store* fs, int32_t section, const int32_t* slots, int32_t n, uint8_t* dst) {
-  oi2::clear_error();
+}  // extern "C"
+
+namespace {
+
+// Checks a request; OI2_OK, or an error code with the message set.
+int check_request(oi2_file_store* fs, int32_t section, const int32_t* slots, int32_t n, const void* dst) {
   if (!fs) {
     oi2::set_error("file store: null handle");
     return OI2_EINVAL;
@@ -273,7 +318,6 @@ int oi2_file_store_read(oi2_file_store* fs, int32_t section, const int32_t* slot
     oi2::set_error("file store: null slots or destination, or negative count");
     return OI2_EINVAL;
   }
-  if (n == 0) return OI2_OK;
   const uint64_t n_rec = fs->sec_n[section];
   for (int i = 0; i < n; ++i)
     if (slots[i] < 0 || (uint64_t)slots[i] >= n_rec) {
@@ -281,6 +325,23 @@ int oi2_file_store_read(oi2_file_store* fs, int32_t section, const int32_t* slot
                      section, (unsigned long long)n_rec);
       return OI2_EINVAL;
     }
+  return OI2_OK;
+}
+
+// Records per chunk of a staged request, and the least a copy moves unless
+// it is the request's last.
+constexpr int kStageChunkMapped = 32;
+constexpr int kStageChunkDirect = 128;   // O_DIRECT: fewer, longer page runs
+constexpr size_t kCopyMin = 1 << 20;
+
+}  // namespace
+
+extern "C" {
+
+int oi2_file_store_read(oi2_file_store* fs, int32_t section, const int32_t* slots, int32_t n, uint8_t* dst) {
+  oi2::clear_error();
+  int rc = check_request(fs, section, slots, n, dst);
+  if (rc != OI2_OK || n == 0) return rc;
   std::lock_guard<std::mutex> lock(fs->call_mu);
   // plan: items in file order, split into one contiguous run per thread
   std::vector<int32_t> order(n);
@@ -304,18 +365,76 @@ int oi2_file_store_read(oi2_file_store* fs, int32_t section, const int32_t* slot
   return OI2_OK;
 }
 
+// Read and copy overlap: the request is cut into chunks of consecutive items
+// (request order), which the pool's threads take in order and read (each
+// chunk in file order); this thread enqueues one hipMemcpyAsync for every
+// run of finished chunks from the front of the request once the run holds at
+// least kCopyMin bytes (or ends the request), so the link carries the first
+// records while the later ones are still being read.
 int oi2_file_store_stage(oi2_file_store* fs, int32_t section, const int32_t* slots, int32_t n,
                          uint8_t* host_buf, uint8_t* dst, void* stream) {
-  int rc = oi2_file_store_read(fs, section, slots, n, host_buf);
+  oi2::clear_error();
+  int rc = check_request(fs, section, slots, n, host_buf);
   if (rc != OI2_OK || n == 0) return rc;
   if (!dst) {
     oi2::set_error("file store: null device destination");
     return OI2_EINVAL;
   }
-  const hipError_t e = hipMemcpyAsync(dst, host_buf, (size_t)n * kRec, hipMemcpyHostToDevice,
-                                      (hipStream_t)stream);
-  if (e != hipSuccess) {
-    oi2::set_error("file store: hipMemcpyAsync of %d records failed: %s", n, hipGetErrorString(e));
+  std::lock_guard<std::mutex> lock(fs->call_mu);
+  const int K = fs->direct ? kStageChunkDirect : kStageChunkMapped;
+  const int n_chunks = (n + K - 1) / K;
+  std::vector<int32_t> order(n);
+  for (int i = 0; i < n; ++i) order[i] = i;
+  for (int c = 0; c < n_chunks; ++c)
+    std::stable_sort(order.begin() + (size_t)c * K, order.begin() + std::min(n, (c + 1) * K),
+                     [&](int a, int b) { return slots[a] < slots[b]; });
+  const uint64_t base = fs->sec_off[section];
+  const int parts = std::min(fs->pool->size(), n_chunks);
+  std::vector<int> err(parts, 0);
+  std::vector<uint8_t> done(n_chunks, 0);   // guarded by mu
+  std::atomic<int> next{0};
+  std::mutex mu;
+  std::condition_variable cv;
+  const std::function<void(int)> fn = [&](int p) {
+    for (int c; (c = next.fetch_add(1)) < n_chunks;) {
+      const int b = c * K, e = std::min(n, b + K);
+      int r = 0;
+      if (fs->direct)
+        r = read_direct(fs, p, base, slots, order.data(), b, e, host_buf);
+      else
+        read_mapped(fs, base, slots, order.data(), b, e, host_buf);
+      if (r && !err[p]) err[p] = r;
+      {
+        std::lock_guard<std::mutex> l(mu);
+        done[c] = 1;
+      }
+      cv.notify_one();
+    }
+  };
+  fs->pool->start(parts, fn);
+  hipError_t he = hipSuccess;
+  for (int copied = 0; copied < n_chunks;) {
+    int e = copied;
+    {
+      std::unique_lock<std::mutex> l(mu);
+      cv.wait(l, [&] {
+        while (e < n_chunks && done[e]) ++e;
+        return e == n_chunks || (size_t)(e - copied) * K * kRec >= kCopyMin;
+      });
+    }
+    const size_t b0 = (size_t)copied * K * kRec, b1 = (size_t)std::min(n, e * K) * kRec;
+    if (he == hipSuccess)
+      he = hipMemcpyAsync(dst + b0, host_buf + b0, b1 - b0, hipMemcpyHostToDevice, (hipStream_t)stream);
+    copied = e;
+  }
+  fs->pool->wait();
+  for (int p = 0; p < parts; ++p)
+    if (err[p]) {
+      oi2::set_error("file store: read of section %d failed: %s", section, strerror(err[p]));
+      return OI2_EIO;
+    }
+  if (he != hipSuccess) {
+    oi2::set_error("file store: hipMemcpyAsync of %d records failed: %s", n, hipGetErrorString(he));
     return OI2_EHIP;
   }
   return OI2_OK;

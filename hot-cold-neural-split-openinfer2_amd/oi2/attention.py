@@ -100,6 +100,17 @@ class GroupedQueryAttention(torch.nn.Module):
             cap *= 2
         return cap
 
+    def rewind(self, n: int) -> None:
+        """Roll this layer's cache back to its first n positions, so that a
+        call passing views of length n appends in place at position n (a
+        rolled-back draft, or one position decoded again).  Unlike every other
+        path, this rewrites positions >= n of the buffer: views returned
+        earlier that reach past n see those positions change."""
+        n = int(n)
+        if self._k is None or not 0 <= n <= self._len:
+            raise ValueError(f"rewind to {n} positions of a cache holding {self._len}")
+        self._len = n
+
     def _own_view(self, k: torch.Tensor, B: int) -> bool:
         """k is the latest view this layer returned: appending to it in place
         leaves every earlier returned view as it was (they end at or before

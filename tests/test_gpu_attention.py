@@ -191,3 +191,32 @@ def test_returned_caches_never_change(dev):
     assert kv_b[0].data_ptr() != kv_a[0].data_ptr() and kv_r[0].data_ptr() != kv_a[0].data_ptr()
     # the roll-back's new position differs from the first sequence's own 7th
     assert not torch.equal(kv_r[0][:, :, 6], kv_a1[0][:, :, 6])
+
+
+def test_rewind_decodes_a_position_again_in_place(dev):
+    """rewind(n) is the one opt-in roll-back that reuses the buffer: a view
+    of length n then appends in place at position n, the first n positions
+    stay bit for bit, and decoding the same token at the same position twice
+    gives the same output and cache row (the oracle checks the step)."""
+    n_kv, B = 8, 1
+    w = _weights(dev, n_kv, seed=43)
+    attn = oi2.GroupedQueryAttention(0, w, _cfg(n_kv))
+    cos, sin = oi2.rope_tables(64, D, 10000.0, device=dev)
+    g = torch.Generator(device=dev).manual_seed(44)
+    x = torch.randn((B, 10, H), generator=g, device=dev).half()
+    _, kv = attn(x, cos, sin)
+    view = (kv[0][:, :, :10], kv[1][:, :, :10])
+    head = [t.clone() for t in view]
+    xt = torch.randn((B, 1, H), generator=g, device=dev).half()
+    out1, kv1 = _check_step(attn, w, n_kv, xt, cos[10:], sin[10:], view, "decode at 10")
+    row1 = (kv1[0][:, :, 10].clone(), kv1[1][:, :, 10].clone())
+    attn.rewind(10)
+    out2, kv2 = attn(xt, cos[10:], sin[10:], view)
+    torch.cuda.synchronize()
+    assert kv2[0].data_ptr() == kv[0].data_ptr(), "rewind must reuse the layer's buffer"
+    assert torch.equal(out1, out2)
+    assert torch.equal(kv2[0][:, :, 10], row1[0]) and torch.equal(kv2[1][:, :, 10], row1[1])
+    for t, s in zip(view, head):
+        assert torch.equal(t, s)
+    with pytest.raises(ValueError):
+        attn.rewind(12)
