@@ -141,6 +141,63 @@ __device__ __forceinline__ float token_r(const TokenIn& tk, u32x4 pq) {
                      : 1.0f;
 }
 
+// The token as the up roles read it, thread t of 256 taking elements
+// [16 t, 16 t + 16): its xw halves (xa, xb) and the lane's four partials
+// (pq).  With tk.norm_w the thread forms them from x and the weight with
+// k_prep's arithmetic (xw = fp16(x w), partial t = ssq16 of x) and puts its
+// partial in s_ssq[t]: finish_partials() then reads the lane's four after
+// the role's first LDS barrier.  Otherwise xw and the partials are loaded.
+struct TokenLoads {
+  u32x4 xa, xb, pq, wa, wb;
+};
+
+// Issued first in a role (every load unconditional: absent data reads zero).
+__device__ __forceinline__ TokenLoads token_loads(const TokenIn& tk, int t) {
+  TokenLoads r;
+  const bool fold = tk.norm_w != nullptr;
+  const rsrc_t rx = rsrc(fold ? tk.x : tk.xw, kH * 2);
+  r.xa = bld16(rx, 32 * t);
+  r.xb = bld16(rx, 32 * t + 16);
+  r.pq = bld16(rsrc(tk.ssq, (tk.use_norm && !fold) ? 256 * 4 : 0u), 16 * lane_id());
+  const rsrc_t rw = rsrc(tk.norm_w, fold ? kH * 2 : 0u);
+  r.wa = bld16(rw, 32 * t);
+  r.wb = bld16(rw, 32 * t + 16);
+  return r;
+}
+
+__device__ __forceinline__ void token_fold(const TokenIn& tk, int t, TokenLoads& r, float* s_ssq) {
+  if (!tk.norm_w) return;
+  const u32x4 wa = r.wa, wb = r.wb;
+  float v[16], w[16];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    v[2 * d] = half_lo(r.xa[d]);
+    v[2 * d + 1] = half_hi(r.xa[d]);
+    v[8 + 2 * d] = half_lo(r.xb[d]);
+    v[8 + 2 * d + 1] = half_hi(r.xb[d]);
+    w[2 * d] = half_lo(wa[d]);
+    w[2 * d + 1] = half_hi(wa[d]);
+    w[8 + 2 * d] = half_lo(wb[d]);
+    w[8 + 2 * d + 1] = half_hi(wb[d]);
+  }
+  s_ssq[t] = ssq16(v);
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    r.xa[d] = (uint32_t)float_to_half_bits(v[2 * d] * w[2 * d]) |
+              ((uint32_t)float_to_half_bits(v[2 * d + 1] * w[2 * d + 1]) << 16);
+    r.xb[d] = (uint32_t)float_to_half_bits(v[8 + 2 * d] * w[8 + 2 * d]) |
+              ((uint32_t)float_to_half_bits(v[8 + 2 * d + 1] * w[8 + 2 * d + 1]) << 16);
+  }
+}
+
+// After the first LDS barrier: the lane's four partials from s_ssq when the
+// role formed them.
+__device__ __forceinline__ void finish_partials(const TokenIn& tk, TokenLoads& r, const float* s_ssq) {
+  if (!tk.norm_w) return;
+  const f32x4 p = reinterpret_cast<const f32x4*>(s_ssq)[lane_id()];
+  r.pq = u32x4{as_u32(p.x), as_u32(p.y), as_u32(p.z), as_u32(p.w)};
+}
+
 // ── ffn_up roles ────────────────────────────────────────────────────────────
 
 // ── cold gate/up/act/down ───────────────────────────────────────────────────
@@ -165,7 +222,7 @@ __device__ __forceinline__ int32_t sload_i32(const int32_t* p) {
   return *reinterpret_cast<ci32*>(reinterpret_cast<uintptr_t>(p));
 }
 
-__device__ void cold_role(const UpArgs& a, int wg, uint32_t* s_pair, float* s_red) {
+__device__ void cold_role(const UpArgs& a, int wg, uint32_t* s_pair, float* s_red, float* s_ssq) {
   const int t = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(t >> 6), lane = lane_id();
   const ActiveList& al = a.act;
@@ -183,10 +240,7 @@ __device__ void cold_role(const UpArgs& a, int wg, uint32_t* s_pair, float* s_re
     return j < al.chunk ? 4 * (uint32_t)(cc * al.chunk + j) : kNoOff;
   };
   const int lane_slot = (int)bld4(rsl, slot_off(lane));
-  const rsrc_t rx = rsrc(a.tok.xw, kH * 2);
-  const u32x4 xa = bld16(rx, 32 * t), xb = bld16(rx, 32 * t + 16);
-  const rsrc_t rp = rsrc(a.tok.ssq, a.tok.use_norm ? 256 * 4 : 0);
-  const u32x4 pq = bld16(rp, 16 * lane);
+  TokenLoads tl = token_loads(a.tok, t);
   // staged records wait for the copy (records staged in list order: item j of
   // chunk c is record c * chunk + j); a wait that gives up reads the records
   // from the copy's source through the slot list instead
@@ -236,7 +290,9 @@ __device__ void cold_role(const UpArgs& a, int wg, uint32_t* s_pair, float* s_re
 
   // 3. the token's (e0,e4) (e1,e5) (e2,e6) (e3,e7) pairs, the order the INT4
   //    unpack produces, into LDS
+  token_fold(a.tok, t, tl, s_ssq);
   {
+    const u32x4 xa = tl.xa, xb = tl.xb;
     u32x4 pa, pb;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
@@ -250,7 +306,8 @@ __device__ void cold_role(const UpArgs& a, int wg, uint32_t* s_pair, float* s_re
     reinterpret_cast<u32x4*>(s_pair)[2 * t + 1] = pb;
   }
   lds_barrier();
-  const float r = token_r(a.tok, pq);
+  finish_partials(a.tok, tl, s_ssq);
+  const float r = token_r(a.tok, tl.pq);
   float acc[64];
 #pragma unroll
   for (int k = 0; k < 64; ++k) acc[k] = 0.0f;
@@ -431,14 +488,11 @@ __device__ void pred_d_role(const UpArgs& a, int wg) {
 // token, the barrier waits for no global load, and each step of the dot
 // products waits only for the weight chunk it uses: the products run while
 // the later chunks are still arriving.
-__device__ void hot_up_role(const UpArgs& a, int wg, uint32_t* s_nat) {
+__device__ void hot_up_role(const UpArgs& a, int wg, uint32_t* s_nat, float* s_ssq) {
   const int t = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(t >> 6), lane = lane_id();
   const int k0 = (wg * 4 + w) * 2;
-  const rsrc_t rx = rsrc(a.tok.xw, kH * 2);
-  const u32x4 xa = bld16(rx, 32 * t), xb = bld16(rx, 32 * t + 16);
-  const rsrc_t rp = rsrc(a.tok.ssq, a.tok.use_norm ? 256 * 4 : 0);
-  const u32x4 pq = bld16(rp, 16 * lane);
+  TokenLoads tl = token_loads(a.tok, t);
   const uint32_t hot_bytes = (uint32_t)a.n_hot * kH;
   const rsrc_t rg = rsrc(a.gate_q, hot_bytes), ru = rsrc(a.up_q, hot_bytes);
   u32x4 qg[2][4], qu[2][4];
@@ -457,11 +511,13 @@ __device__ void hot_up_role(const UpArgs& a, int wg, uint32_t* s_nat) {
   const float gsc = as_f32(bld4(rsrc(a.gate_s, sb), so));
   const float usc = as_f32(bld4(rsrc(a.up_s, sb), so));
   const float gbi = as_f32(bld4(rsrc(a.hot_gbias, a.hot_gbias ? sb : 0), so));
-  reinterpret_cast<u32x4*>(s_nat)[2 * t] = xa;
-  reinterpret_cast<u32x4*>(s_nat)[2 * t + 1] = xb;
+  token_fold(a.tok, t, tl, s_ssq);
+  reinterpret_cast<u32x4*>(s_nat)[2 * t] = tl.xa;
+  reinterpret_cast<u32x4*>(s_nat)[2 * t + 1] = tl.xb;
   lds_barrier();
   if (k0 >= a.n_hot) return;
-  const float r = token_r(a.tok, pq);
+  finish_partials(a.tok, tl, s_ssq);
+  const float r = token_r(a.tok, tl.pq);
   float g[2] = {0.0f, 0.0f}, u[2] = {0.0f, 0.0f};
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
@@ -495,10 +551,11 @@ __global__ __launch_bounds__(kThreads, 3) void k_ffn_up(UpArgs a) {
   // hot: natural xw (8 KB); cold: paired xw (8 KB) + padded reduction (16.5 KB)
   __shared__ u32x4 s_xw4[kH / 8];
   __shared__ float s_red[kH + kH / 32];
+  __shared__ __attribute__((aligned(16))) float s_ssq[256];   // the partials a role formed itself
   uint32_t* s_xw = reinterpret_cast<uint32_t*>(s_xw4);
   int b = blockIdx.x;
   if (b < a.wg_cold) {
-    cold_role(a, b, s_xw, s_red);
+    cold_role(a, b, s_xw, s_red, s_ssq);
     return;
   }
   b -= a.wg_cold;
@@ -507,7 +564,7 @@ __global__ __launch_bounds__(kThreads, 3) void k_ffn_up(UpArgs a) {
     return;
   }
   b -= a.wg_pred;
-  hot_up_role(a, b, s_xw);
+  hot_up_role(a, b, s_xw, s_ssq);
 }
 
 // Predictor-only launches (layer 0's lookahead, the standalone predictor
@@ -1260,12 +1317,10 @@ int ffn_decode_tokens(const uint16_t* x, int batch, const uint16_t* norm_w, floa
   const int wg_cold = c.wg_cold;
   for (int b = 0; b < batch; ++b) {
     const uint16_t* xb = x + (size_t)b * kH;
-    if (norm_w) {
-      hipLaunchKernelGGL(k_prep, dim3(1), dim3(kThreads), 0, st, xb, norm_w, ws.xw, ws.ssq);
-      OI2_CHECK_LAUNCH();
-    }
+    // with a norm, every up workgroup forms x * w and the norm's partials
+    // itself (no separate prep launch)
     UpArgs ua{};
-    ua.tok = TokenIn{xb, norm_w ? ws.xw : xb, ws.ssq, eps, norm_w ? 1 : 0};
+    ua.tok = TokenIn{xb, xb, nullptr, eps, norm_w ? 1 : 0, norm_w};
     ua.relu = act == OI2_ACT_RELU;
     ua.both = act_on_both != 0;
     ua.n_hot = n_hot;

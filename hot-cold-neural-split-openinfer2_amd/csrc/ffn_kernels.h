@@ -35,6 +35,9 @@ struct TokenIn {
   const float* ssq;         // 256 partial sums of x^2
   float eps;
   int use_norm;
+  // non-null: the norm weight, and the kernel forms xw and the partials from
+  // x itself (k_prep's arithmetic) instead of reading xw and ssq
+  const uint16_t* norm_w;
 };
 
 struct UpArgs {
