@@ -350,11 +350,23 @@ __device__ __forceinline__ void pgemm_up_tile(const BUpArgs& a, int nt, int m0, 
   }
 }
 
+// The down kernels' fp32 accumulator cleared by the gate/up launch that
+// precedes them (its workgroups take consecutive float4s, before any of them
+// returns), instead of a fill launch of its own.
+__device__ __forceinline__ void zero_y_share(const BUpArgs& a) {
+  if (!a.yzero) return;
+  const int per = (a.yzero_n4 + (int)gridDim.x - 1) / (int)gridDim.x;
+  const int q0 = blockIdx.x * per, q1 = min(q0 + per, a.yzero_n4);
+  for (int q = q0 + (int)threadIdx.x; q < q1; q += (int)blockDim.x)
+    reinterpret_cast<f32x4*>(a.yzero)[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+}
+
 template <int MS>
 __global__ __launch_bounds__(kThreads) void k_pgemm_up(BUpArgs a, int hot_tiles, int n_tiles, int mt) {
   __shared__ __attribute__((aligned(16))) uint16_t sA[2 * 32 * MS * kLdA];
   __shared__ __attribute__((aligned(16))) uint8_t sB[2 * 256 * kLdB8];
   __shared__ uint16_t sSc[2 * 256];
+  zero_y_share(a);
   const int b = blockIdx.x;
   const int q = b >> 3;
   const int nt = (q / mt) * 8 + (b & 7), mtile = q % mt;
@@ -553,6 +565,7 @@ __device__ __forceinline__ void mup_tile(const BUpArgs& a, int nt, int m0, int t
 // XCDs), sharing its L2 for the weights.
 __global__ __launch_bounds__(kThreads) void k_mup(BUpArgs a, int hot_tiles, int n_tiles, int mt) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[kMupLds];
+  zero_y_share(a);
   const int b = blockIdx.x;
   const int q = b >> 3;
   const int nt = (q / mt) * 8 + (b & 7), mtile = q % mt;
@@ -1499,7 +1512,17 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
     OI2_CHECK_LAUNCH();
     return OI2_OK;
   }
+  const int n4 = M * (kH / 4);
+  int grid = (n4 + kThreads - 1) / kThreads;
+  grid = grid > 2048 ? 2048 : grid;
+  // the hot product writes y outright when one workgroup owns each output;
+  // otherwise y is cleared, by the gate/up launch when there is one
+  const bool clear_y = !n_hot || p.hot_splits > 1;
   if (p.ldh + p.ldc > 0) {
+    if (clear_y) {
+      ua.yzero = y;
+      ua.yzero_n4 = n4;
+    }
     if (p.prefill) {
       const int hot_tiles = p.ldh / 128, n_tiles = hot_tiles + p.ldc / 128;
       const dim3 grid((n_tiles + 7) / 8 * 8 * p.pmt);
@@ -1514,11 +1537,7 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
     }
     OI2_CHECK_LAUNCH();
   }
-  const int n4 = M * (kH / 4);
-  int grid = (n4 + kThreads - 1) / kThreads;
-  grid = grid > 2048 ? 2048 : grid;
-  // the hot product writes y outright when one workgroup owns each output
-  if (!n_hot || p.hot_splits > 1) {
+  if (clear_y && p.ldh + p.ldc == 0) {
     hipLaunchKernelGGL(k_bfill, dim3(grid), dim3(kThreads), 0, st, y, n4);
     OI2_CHECK_LAUNCH();
   }

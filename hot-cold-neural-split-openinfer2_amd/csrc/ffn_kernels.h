@@ -184,6 +184,8 @@ struct BUpArgs {
   int ldc;
   int Mpad;
   int hot_per_wg;           // k_sbup: hot rows per workgroup (n_hot over 256 workgroups)
+  float* yzero;             // k_mup / k_pgemm_up: non-null, zero these yzero_n4 float4s first
+  int yzero_n4;             //   (the down kernels' accumulator; the launch spreads them over its workgroups)
 };
 
 struct BDownArgs {
