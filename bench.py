@@ -45,7 +45,7 @@ HBM_PEAK_GBS = 8000.0
 # HBM bytes per launch on this workload, from rocprofv3 --pmc runs
 # (FETCH_SIZE x 2.000 + WRITE_SIZE x 1.000 KiB, the factors being what each
 # counter reads for a plain 256 MiB copy, --copy-calibration)
-TOKEN_TRAFFIC_BYTES = (802809.9 * 2.0 + 14279.4) * 1024     # k_token
+TOKEN_TRAFFIC_BYTES = (848467.9 * 2.0 + 115692.4) * 1024    # k_token
 TOKEN_TRAFFIC_SOURCE = ("rocprofv3 --pmc FETCH_SIZE and WRITE_SIZE of k_token on this workload, "
                         "profiles/k_token_traffic_decode32_bs1.md")
 COPY_WORKGROUPS = 8          # the staging copy kernel's workgroups (swept: 6 / 8 / 10 / 12 / 16)
