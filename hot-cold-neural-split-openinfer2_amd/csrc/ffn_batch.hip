@@ -385,176 +385,211 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_up(BUpArgs a, int hot_tiles,
 // ── gate/up for 17 .. 191 tokens ────────────────────────────────────────────
 //
 // Workgroup tile: 64 tokens x 32 neurons (hot fp8 rows, or cold items of the
-// dense active list).  The whole K range stays in one workgroup, so the
-// activation is applied in the epilogue (no partial sums leave it); at 3584
-// hot + 10752 cold there are ~440 workgroups.  Operands go through two LDS
-// buffers, loaded kMupPD blocks ahead, with the 32x32x16 MFMA as in
-// pgemm_up_tile: the 32 columns are the tile's neurons, B tile 0 the gate
-// rows and tile 1 the up rows.  Wave w takes token subtile w & 1 and K steps
-// 4 (w >> 1) .. +4 of every block; the two K halves meet in LDS at the end.
+// dense active list), 512 threads.  The whole K range stays in one
+// workgroup, so the activation is applied in the epilogue (no partial sums
+// leave it).  Wave w takes K step w (16 of every 128-wide block) for both
+// 32-token subtiles and both the gate and the up rows: four independent
+// 32x32x16 MFMAs per block, each weight fragment decoded once for two of
+// them, and two waves per SIMD (two workgroups per CU) to hide each one's
+// LDS and decode latency.  (With four waves, each on one subtile and half of
+// every block, a tile took ~34 us whatever it held: one wave per SIMD ran a
+// chain of LDS reads, decodes and MFMAs with nothing to overlap it.)
+// Operands go through two LDS buffers; each block's token rows and weight
+// rows are loaded two blocks ahead into registers.  At the end the eight
+// waves' sums meet in LDS in a fixed order (w and w + 4, then the four pairs
+// in wave order), and each wave applies the activation to an eighth of the
+// tile.
 // A cold tile's group scales (32 gate + 32 up per item) go to LDS once, up
-// front.  (64-item cold tiles, measured first, ran twice as long as the hot
-// tiles and set the kernel's end.)
-constexpr int kMupN = 32;   // neurons per tile
-constexpr int kMupPD = 2;   // K blocks of weights and tokens in flight per workgroup
+// front.
+constexpr int kMupN = 32;                            // neurons per tile
+constexpr int kMupThreads = 512;
 constexpr int kMupBbuf = 64 * kLdB8;                 // bytes per B buffer (32 x 2 rows)
 constexpr int kMupAbuf = 64 * kLdA * 2;              // bytes per A buffer
-constexpr int kMupLds = 2 * kMupAbuf + 2 * kMupBbuf + kMupN * 2 * kGroups * 2;
-static_assert(2 * kMupAbuf + 2 * kMupBbuf >= 2 * 2 * 16 * 64 * 4, "the K-half reduction fits the operand buffers");
+constexpr int kMupSc = 2 * kMupAbuf + 2 * kMupBbuf;  // the scales' byte offset
+constexpr int kMupRedBuf = 2 * 2 * 16 * 64 * 4;      // one wave's sums: [ms][g][j][lane] fp32
+constexpr int kMupLds = std::max(kMupSc + kMupN * 2 * kGroups * 2, 4 * kMupRedBuf);
 
 template <bool HOT>
 __device__ __forceinline__ void mup_tile(const BUpArgs& a, int nt, int m0, int total, int i0, uint8_t* smem) {
-  constexpr int MS = 2;
   uint16_t* sA = reinterpret_cast<uint16_t*>(smem);
   uint8_t* sB = smem + 2 * kMupAbuf;
-  uint16_t* sSc = reinterpret_cast<uint16_t*>(smem + 2 * kMupAbuf + 2 * kMupBbuf);
-  const int t = threadIdx.x, w = t >> 6, l = lane_id(), h = l >> 5;
-  const int ms = w & 1, kh = w >> 1, col = l & 31;
-  const ARows<MS> arows(a.xn, kH, a.M, m0);
-  f32x16 acc[2] = {f32x16{}, f32x16{}};   // gate, up
-  u32x4 ra[kMupPD][2 * MS], rb[kMupPD][2];
-  // staging: hot, chunk t & 7 of neuron row t >> 3 (gate, up); cold, chunk
-  // t & 3 of item t >> 3, gate for (t >> 2) & 1 == 0 else up.  Absent rows
-  // read as zero.
-  const rsrc_t rw = HOT ? buf_rsrc(a.gate_q, (uint32_t)a.n_hot * kH)
-                        : buf_rsrc(a.records, (uint32_t)a.n_records * kRecBytes);
-  const rsrc_t ru = buf_rsrc(a.up_q, HOT ? (uint32_t)a.n_hot * kH : 0u);
+  uint16_t* sSc = reinterpret_cast<uint16_t*>(smem + kMupSc);
+  const int t = threadIdx.x, w = __builtin_amdgcn_readfirstlane(t >> 6), l = lane_id(), h = l >> 5, col = l & 31;
+  // cold: waves 0-3 stage the 4 KB weight block, waves 4-7 issue the same
+  // load over an empty range (every wave runs the same loads, so the
+  // compiler's wait counts stay exact)
+  const bool bstore = HOT || w < 4;
+  // A staging: chunk t & 15 (8 halves) of token rows m0 + (t >> 4) + 32 i;
+  // rows past M read zero
+  const rsrc_t rx = buf_rsrc(a.xn, (uint32_t)a.M * kH * 2);
+  uint32_t aoff[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) aoff[i] = ((uint32_t)(m0 + (t >> 4) + 32 * i) * kH + 8 * (t & 15)) * 2;
+  // B staging: hot, chunk t & 7 of row t >> 3 (rows 0..31 the gate rows of
+  // the tile's neurons, 32..63 their up rows); cold (t < 256), chunk t & 3 of
+  // item t >> 3, gate for (t >> 2) & 1 == 0 else up.  Absent rows read zero.
+  const rsrc_t rw = HOT ? buf_rsrc(w < 4 ? a.gate_q : a.up_q, (uint32_t)a.n_hot * kH)
+                        : buf_rsrc(a.records, w < 4 ? (uint32_t)a.n_records * kRecBytes : 0u);
   auto item_rec = [&](int it) {
     const int slot = it < total ? a.dslots[it] : -1;
     return (slot >= 0 && slot < a.n_records) ? (uint32_t)slot * kRecBytes : kNoOffset;
   };
-  uint32_t voff[2];
+  uint32_t boff;
   if constexpr (HOT) {
-    voff[0] = voff[1] = (uint32_t)(nt * kMupN + (t >> 3)) * kH + 16 * (t & 7);
+    boff = (uint32_t)(nt * kMupN + ((t >> 3) & 31)) * kH + 16 * (t & 7);
   } else {
-    const uint32_t v = item_rec(i0 + (t >> 3));
-    voff[0] = v + (((t >> 2) & 1) ? kOffUp : kOffGate) + 16 * (t & 3);
+    const uint32_t v = item_rec(i0 + ((t >> 3) & 31));
+    boff = v + (((t >> 2) & 1) ? kOffUp : kOffGate) + 16 * (t & 3);
     // scales: item t >> 3, 16-byte piece t & 7 of its gate (64 B) and up
-    // (64 B) scale arrays, stored as sSc[item][gate 0..31, up 0..31]
-    const u32x4 sv = bload16(rw, v + kOffScales + 16 * (t & 7), 0);
-    reinterpret_cast<u32x4*>(sSc)[t] = sv;
+    // (64 B) scale arrays, stored as sSc[gate, up][group][item] (a block's
+    // 32 items side by side: lanes read consecutive halves)
+    if (w < 4) {
+      const u32x4 sv = bload16(rw, v + kOffScales + 16 * (t & 7), 0);
+      const int it = t >> 3, g0 = 8 * (t & 3), gu = (t >> 2) & 1;
+#pragma unroll
+      for (int k = 0; k < 8; ++k)
+        sSc[(gu * kGroups + g0 + k) * kMupN + it] = (uint16_t)(sv[k >> 1] >> (16 * (k & 1)));
+    }
   }
-  auto load_b = [&](int kb, int sl) {
-    if constexpr (HOT) {
-      rb[sl][0] = bload16(rw, voff[0], kb * kBK);
-      rb[sl][1] = bload16(ru, voff[1], kb * kBK);
-    } else {
-      rb[sl][0] = bload16(rw, voff[0], 64 * kb);
+  u32x4 ra[2][2], rb[2];
+  auto load = [&](int kb, int sl) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) ra[sl][i] = bload16(rx, aoff[i], kb * kBK * 2);
+    rb[sl] = bload16(rw, boff, HOT ? kb * kBK : 64 * kb);
+  };
+  auto store = [&](int buf, int sl) {
+    uint16_t* A = sA + buf * (kMupAbuf / 2);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      u32x4 v = ra[sl][i];
+      if constexpr (!HOT) {   // (x0,x4,x1,x5,x2,x6,x3,x7): the INT4 decode's pair order
+        const uint32_t d0 = v.x, d1 = v.y, d2 = v.z, d3 = v.w;
+        v.x = (d0 & 0xFFFFu) | (d2 << 16);
+        v.y = (d0 >> 16) | (d2 & 0xFFFF0000u);
+        v.z = (d1 & 0xFFFFu) | (d3 << 16);
+        v.w = (d1 >> 16) | (d3 & 0xFFFF0000u);
+      }
+      *reinterpret_cast<u32x4*>(A + ((t >> 4) + 32 * i) * kLdA + 8 * (t & 15)) = v;
+    }
+    if (bstore) {
+      uint8_t* d = sB + buf * kMupBbuf +
+                   (HOT ? (t >> 3) * kLdB8 + 16 * (t & 7) : ((t >> 3) + 32 * ((t >> 2) & 1)) * kLdB4 + 16 * (t & 3));
+      reinterpret_cast<u32x2*>(d)[0] = u32x2{rb[sl].x, rb[sl].y};
+      reinterpret_cast<u32x2*>(d)[1] = u32x2{rb[sl].z, rb[sl].w};
     }
   };
-  auto store_b = [&](int buf, int sl) {
-    uint8_t* B = sB + buf * kMupBbuf;
-    if constexpr (HOT) {
+  f32x16 acc[2][2];   // [token subtile][gate, up]
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        uint8_t* d = B + ((t >> 3) + 32 * i) * kLdB8 + 16 * (t & 7);
-        reinterpret_cast<u32x2*>(d)[0] = u32x2{rb[sl][i].x, rb[sl][i].y};
-        reinterpret_cast<u32x2*>(d)[1] = u32x2{rb[sl][i].z, rb[sl][i].w};
-      }
-    } else {   // rows: gate items 0..31, then up items 0..31
-      uint8_t* d = B + ((t >> 3) + 32 * ((t >> 2) & 1)) * kLdB4 + 16 * (t & 3);
-      reinterpret_cast<u32x2*>(d)[0] = u32x2{rb[sl][0].x, rb[sl][0].y};
-      reinterpret_cast<u32x2*>(d)[1] = u32x2{rb[sl][0].z, rb[sl][0].w};
-    }
-  };
-  // this wave's K steps of one block, its token subtile
-  auto mma_block = [&](const uint16_t* A, const uint8_t* B, int kb) {
+  for (int ms = 0; ms < 2; ++ms) acc[ms][0] = acc[ms][1] = f32x16{};
+  // K step w of block kb: rows col (gate) and 32 + col (up), this lane's 8 K
+  auto mma_block = [&](int buf, int kb) {
+    const uint16_t* A = sA + buf * (kMupAbuf / 2);
+    const uint8_t* B = sB + buf * kMupBbuf;
+    h8 bg, bu;
     if constexpr (HOT) {
-#pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4) {
-        const int st = 4 * kh + s4;
-        const u32x2 vg = *reinterpret_cast<const u32x2*>(B + col * kLdB8 + 64 * h + 8 * st);
-        const u32x2 vu = *reinterpret_cast<const u32x2*>(B + (32 + col) * kLdB8 + 64 * h + 8 * st);
-        const h8 av = a_frag32(A, ms, st);
-        acc[0] = mfma32(av, fp8x8_h8(vg[0], vg[1]), acc[0]);
-        acc[1] = mfma32(av, fp8x8_h8(vu[0], vu[1]), acc[1]);
-      }
+      const u32x2 vg = *reinterpret_cast<const u32x2*>(B + col * kLdB8 + 64 * h + 8 * w);
+      const u32x2 vu = *reinterpret_cast<const u32x2*>(B + (32 + col) * kLdB8 + 64 * h + 8 * w);
+      bg = fp8x8_h8(vg[0], vg[1]);
+      bu = fp8x8_h8(vu[0], vu[1]);
     } else {
-      const _Float16 sg = __builtin_bit_cast(_Float16, sSc[col * 2 * kGroups + kb]);
-      const _Float16 su = __builtin_bit_cast(_Float16, sSc[col * 2 * kGroups + kGroups + kb]);
+      const _Float16 sg = __builtin_bit_cast(_Float16, sSc[kb * kMupN + col]);
+      const _Float16 su = __builtin_bit_cast(_Float16, sSc[(kGroups + kb) * kMupN + col]);
+      const uint32_t dg = *reinterpret_cast<const uint32_t*>(B + col * kLdB4 + 32 * h + 4 * w);
+      const uint32_t du = *reinterpret_cast<const uint32_t*>(B + (32 + col) * kLdB4 + 32 * h + 4 * w);
+      bg = int4x8_h8_scaled(dg, sg);
+      bu = int4x8_h8_scaled(du, su);
+    }
 #pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4) {
-        const int st = 4 * kh + s4;
-        const uint32_t dg = *reinterpret_cast<const uint32_t*>(B + col * kLdB4 + 32 * h + 4 * st);
-        const uint32_t du = *reinterpret_cast<const uint32_t*>(B + (32 + col) * kLdB4 + 32 * h + 4 * st);
-        const h8 av = a_frag32(A, ms, st);
-        acc[0] = mfma32(av, int4x8_h8_scaled(dg, sg), acc[0]);
-        acc[1] = mfma32(av, int4x8_h8_scaled(du, su), acc[1]);
-      }
+    for (int ms = 0; ms < 2; ++ms) {
+      const h8 av = a_frag32(A, ms, w);
+      acc[ms][0] = mfma32(av, bg, acc[ms][0]);
+      acc[ms][1] = mfma32(av, bu, acc[ms][1]);
     }
   };
 
   constexpr int kNB = kH / kBK;
-  static_assert(kNB % kMupPD == 0, "the block loop is unrolled by the prefetch distance");
-  // blocks 0 .. kMupPD - 1 in flight, block 0 to LDS, block kMupPD into its slot
-#pragma unroll
-  for (int b = 0; b < kMupPD; ++b) {
-    arows.load(b, ra[b]);
-    load_b(b, b);
-  }
-  store_a_rows<2 * MS, !HOT>(ra[0], sA);
-  store_b(0, 0);
-  arows.load(kMupPD, ra[0]);
-  load_b(kMupPD, 0);
+  static_assert(kNB % 2 == 0, "the block loop is unrolled by two");
+  load(0, 0);
+  load(1, 1);
+  store(0, 0);
   lds_barrier();
 #pragma unroll 1
-  for (int k0 = 0; k0 < kNB; k0 += kMupPD) {
+  for (int k0 = 0; k0 < kNB; k0 += 2) {
 #pragma unroll
-    for (int u = 0; u < kMupPD; ++u) {
-      const int kb = k0 + u, cur = kb & 1, sl = (u + 1) % kMupPD;   // block kb + 1 is in slot sl
+    for (int u = 0; u < 2; ++u) {
+      const int kb = k0 + u;
+      // slot u held block kb, already in LDS buffer u: refill it with kb + 2
+      // (the last two passes load the last block again, unused)
+      load(min(kb + 2, kNB - 1), u);
       __builtin_amdgcn_sched_barrier(0);
-      mma_block(sA + cur * (kMupAbuf / 2), sB + cur * kMupBbuf, kb);
+      mma_block(u, kb);
       __builtin_amdgcn_sched_barrier(0);
-      if (kb + 1 < kNB) {
-        store_a_rows<2 * MS, !HOT>(ra[sl], sA + (cur ^ 1) * (kMupAbuf / 2));
-        store_b(cur ^ 1, sl);
-        if (kb + 1 + kMupPD < kNB) {
-          arows.load(kb + 1 + kMupPD, ra[sl]);
-          load_b(kb + 1 + kMupPD, sl);
-        }
-      }
+      if (kb + 1 < kNB) store(u ^ 1, u ^ 1);
       lds_barrier();
     }
   }
 
-  // the K halves meet in LDS (the operand buffers are free now), upper onto
-  // lower, in a fixed order: red[subtile][gate, up][element][lane]
-  float* red = reinterpret_cast<float*>(smem);
-  if (kh == 1) {
-#pragma unroll
-    for (int g = 0; g < 2; ++g)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) red[((ms * 2 + g) * 16 + j) * 64 + l] = acc[g][j];
-  }
-  __syncthreads();
-  if (kh == 1) return;
-#pragma unroll
-  for (int g = 0; g < 2; ++g)
-#pragma unroll
-    for (int j = 0; j < 16; ++j) acc[g][j] += red[((ms * 2 + g) * 16 + j) * 64 + l];
-  // epilogue: lane l holds column l & 31, tokens m0 + 32 ms + 8 (j / 4) + 4 h + j % 4
+  // the epilogue's operands of this lane's column, loaded while the sums meet
+  float sg = 0.f, su = 0.f, gb = 0.f;
+  bool ok;
+  int item = 0;
   if constexpr (HOT) {
     const int row = nt * kMupN + col;
-    const bool ok = row < a.n_hot;
-    const float sg = ok ? a.gate_s[row] : 0.f, su = ok ? a.up_s[row] : 0.f;
-    const float gb = (ok && a.hot_gbias) ? a.hot_gbias[row] : 0.f;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int m = m0 + 32 * ms + 8 * (j >> 2) + 4 * h + (j & 3);
-      if (m >= a.M) continue;
-      const float hv = ok ? gated_act(fmaf(acc[0][j], sg, gb), acc[1][j] * su, a.relu, a.both) : 0.f;
-      a.hh[(size_t)m * a.ldh + row] = float_to_half_bits(hv);
+    ok = row < a.n_hot;
+    if (ok) {
+      sg = a.gate_s[row];
+      su = a.up_s[row];
+      gb = a.hot_gbias ? a.hot_gbias[row] : 0.f;
     }
   } else {
-    const int item = i0 + col;
+    item = i0 + col;
     const int slot = item < total ? a.dslots[item] : -1;
-    const bool ok = slot >= 0 && slot < a.n_records;
-    const float gb = (ok && a.cold_gbias) ? a.cold_gbias[slot] : 0.f;
+    ok = slot >= 0 && slot < a.n_records;
+    gb = (ok && a.cold_gbias) ? a.cold_gbias[slot] : 0.f;
+  }
+  // the eight waves' sums meet in LDS (the operand buffers are free now):
+  // waves 4-7 store theirs, waves 0-3 add them to their own and store the
+  // pair; then wave w adds the four pairs (in wave order) for its four
+  // (subtile, row group) pairs of the tile and writes those outputs
+  float* red = reinterpret_cast<float*>(smem);
+  auto red_at = [&](int buf, int ms, int g, int j) { return red + buf * (kMupRedBuf / 4) + ((ms * 2 + g) * 16 + j) * 64 + l; };
+  if (w >= 4) {
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int m = m0 + 32 * ms + 8 * (j >> 2) + 4 * h + (j & 3);
-      if (m >= a.M) continue;
-      const float hv = ok ? gated_act(acc[0][j] + gb, acc[1][j], a.relu, a.both) : 0.f;
+    for (int ms = 0; ms < 2; ++ms)
+#pragma unroll
+      for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) *red_at(w - 4, ms, g, j) = acc[ms][g][j];
+  }
+  __syncthreads();
+  if (w < 4) {
+#pragma unroll
+    for (int ms = 0; ms < 2; ++ms)
+#pragma unroll
+      for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) *red_at(w, ms, g, j) = acc[ms][g][j] + *red_at(w, ms, g, j);
+  }
+  __syncthreads();
+  // wave w: subtile ms = w >> 2, output rows j = 4 (w & 3) .. + 3, i.e. tokens
+  // m0 + 32 ms + 8 (w & 3) + 4 h + i, i < 4
+  const int ms = w >> 2;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int j = 4 * (w & 3) + i;
+    float gs = 0.f, us = 0.f;
+#pragma unroll
+    for (int bq = 0; bq < 4; ++bq) {
+      gs += *red_at(bq, ms, 0, j);
+      us += *red_at(bq, ms, 1, j);
+    }
+    const int m = m0 + 32 * ms + 8 * (j >> 2) + 4 * h + (j & 3);
+    if (m >= a.M) continue;
+    if constexpr (HOT) {
+      const float hv = ok ? gated_act(fmaf(gs, sg, gb), us * su, a.relu, a.both) : 0.f;
+      a.hh[(size_t)m * a.ldh + nt * kMupN + col] = float_to_half_bits(hv);
+    } else {
+      const float hv = ok ? gated_act(gs + gb, us, a.relu, a.both) : 0.f;
       a.hc[(size_t)m * a.ldc + item] = float_to_half_bits(hv);
     }
   }
@@ -563,7 +598,7 @@ __device__ __forceinline__ void mup_tile(const BUpArgs& a, int nt, int m0, int t
 // Grid: (hot tiles + cold tiles, rounded up to 8) x token tiles, the token
 // tiles of one weight tile on one XCD (workgroups go round-robin over the 8
 // XCDs), sharing its L2 for the weights.
-__global__ __launch_bounds__(kThreads) void k_mup(BUpArgs a, int hot_tiles, int n_tiles, int mt) {
+__global__ __launch_bounds__(kMupThreads) void k_mup(BUpArgs a, int hot_tiles, int n_tiles, int mt) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[kMupLds];
   zero_y_share(a);
   const int b = blockIdx.x;
@@ -1532,7 +1567,7 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
         hipLaunchKernelGGL(k_pgemm_up<2>, grid, dim3(kThreads), 0, st, ua, hot_tiles, n_tiles, p.pmt);
     } else {
       const int hot_tiles = p.ldh / kMupN, n_tiles = hot_tiles + p.ldc / kMupN;
-      hipLaunchKernelGGL(k_mup, dim3((n_tiles + 7) / 8 * 8 * p.pmt), dim3(kThreads), 0, st, ua, hot_tiles,
+      hipLaunchKernelGGL(k_mup, dim3((n_tiles + 7) / 8 * 8 * p.pmt), dim3(kMupThreads), 0, st, ua, hot_tiles,
                          n_tiles, p.pmt);
     }
     OI2_CHECK_LAUNCH();

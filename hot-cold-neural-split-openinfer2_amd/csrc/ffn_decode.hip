@@ -754,9 +754,14 @@ __device__ void down_role(const DownArgs& a, int b, DownShared& sh) {
   f32x4 cp = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
   for (int k = 0; k < kPre; ++k) cp += f32x4{as_f32(pv[k].x), as_f32(pv[k].y), as_f32(pv[k].z), as_f32(pv[k].w)};
-  for (int p = (t >> 2) + 64 * kPre; p < n_part; p += kThreads / 4) {
-    const u32x4 v = bld16(rcp, part_off(p));
-    cp += f32x4{as_f32(v.x), as_f32(v.y), as_f32(v.z), as_f32(v.w)};
+  // (four loads in flight per pass, rows past n_part reading zero; the sum
+  // keeps the row order)
+  for (int p0 = (t >> 2) + 64 * kPre; p0 < n_part; p0 += 4 * (kThreads / 4)) {
+    u32x4 v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = bld16(rcp, part_off(p0 + k * (kThreads / 4)));
+#pragma unroll
+    for (int k = 0; k < 4; ++k) cp += f32x4{as_f32(v[k].x), as_f32(v[k].y), as_f32(v[k].z), as_f32(v[k].w)};
   }
   // h values of this lane's chunks
   float hv[4][16];
