@@ -239,6 +239,48 @@ __device__ __forceinline__ void mma_block_lds(const uint16_t* sA, const uint8_t*
   }
 }
 
+// gated_act with the activation chosen at compile time (the same operations,
+// so the same bits).
+template <bool RELU, bool BOTH>
+__device__ __forceinline__ float gated_act_t(float g, float u) {
+  const float ag = RELU ? fmaxf(g, 0.0f) : silu(g);
+  const float au = BOTH ? (RELU ? fmaxf(u, 0.0f) : silu(u)) : u;
+  return ag * au;
+}
+
+// The gate/up epilogue of one lane's column: for each of the MS x 16
+// accumulator elements, h = act(g sg + gb, u su) (zero when !ok), stored as
+// fp16 at dst[m * ld + c] through a descriptor that drops rows m >= M.  The
+// activation is chosen once, outside the element loop, and no element takes
+// a branch, so the elements' exp / divide chains overlap.  (Taken per
+// element, the choice and the row test made a prefill tile's epilogue a
+// chain of 64 basic blocks: ~14 us of a 98 us tile.)
+template <int MS, bool RELU, bool BOTH>
+__device__ __forceinline__ void up_epilogue_t(const f32x16 (&acc)[MS][2], float sg, float su, float gb, bool ok,
+                                              uint16_t* dst, int M, int ld, int c, int m0) {
+  const rsrc_t rd = buf_rsrc(dst, (uint32_t)M * ld * 2);
+  const int h = lane_id() >> 5;
+#pragma unroll
+  for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int m = m0 + 32 * ms + 8 * (j >> 2) + 4 * h + (j & 3);
+      const float hv = gated_act_t<RELU, BOTH>(fmaf(acc[ms][0][j], sg, gb), acc[ms][1][j] * su);
+      __builtin_amdgcn_raw_buffer_store_b16(float_to_half_bits(ok ? hv : 0.f), rd, ((uint32_t)m * ld + c) * 2, 0, 0);
+    }
+}
+template <int MS>
+__device__ __forceinline__ void up_epilogue(const BUpArgs& a, const f32x16 (&acc)[MS][2], float sg, float su,
+                                            float gb, bool ok, uint16_t* dst, int ld, int c, int m0) {
+  if (a.relu) {
+    if (a.both) up_epilogue_t<MS, true, true>(acc, sg, su, gb, ok, dst, a.M, ld, c, m0);
+    else up_epilogue_t<MS, true, false>(acc, sg, su, gb, ok, dst, a.M, ld, c, m0);
+  } else {
+    if (a.both) up_epilogue_t<MS, false, true>(acc, sg, su, gb, ok, dst, a.M, ld, c, m0);
+    else up_epilogue_t<MS, false, false>(acc, sg, su, gb, ok, dst, a.M, ld, c, m0);
+  }
+}
+
 template <int MS, bool HOT>
 __device__ __forceinline__ void pgemm_up_tile(const BUpArgs& a, int nt, int m0, int total, int i0,
                                               uint16_t* sA, uint8_t* sB, uint16_t* sSc) {
@@ -324,29 +366,13 @@ __device__ __forceinline__ void pgemm_up_tile(const BUpArgs& a, int nt, int m0, 
     const bool ok = row < a.n_hot;
     const float sg = ok ? a.gate_s[row] : 0.f, su = ok ? a.up_s[row] : 0.f;
     const float gb = (ok && a.hot_gbias) ? a.hot_gbias[row] : 0.f;
-#pragma unroll
-    for (int ms = 0; ms < MS; ++ms)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int m = m0 + 32 * ms + 8 * (j >> 2) + 4 * (l >> 5) + (j & 3);
-        if (m >= a.M) continue;
-        const float hv = ok ? gated_act(fmaf(acc[ms][0][j], sg, gb), acc[ms][1][j] * su, a.relu, a.both) : 0.f;
-        a.hh[(size_t)m * a.ldh + row] = float_to_half_bits(hv);
-      }
+    up_epilogue<MS>(a, acc, sg, su, gb, ok, a.hh, a.ldh, row, m0);
   } else {
     const int item = i0 + col;
     const int slot = item < total ? a.dslots[item] : -1;
     const bool ok = slot >= 0 && slot < a.n_records;
     const float gb = (ok && a.cold_gbias) ? a.cold_gbias[slot] : 0.f;
-#pragma unroll
-    for (int ms = 0; ms < MS; ++ms)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int m = m0 + 32 * ms + 8 * (j >> 2) + 4 * (l >> 5) + (j & 3);
-        if (m >= a.M) continue;
-        const float hv = ok ? gated_act(acc[ms][0][j] + gb, acc[ms][1][j], a.relu, a.both) : 0.f;
-        a.hc[(size_t)m * a.ldc + item] = float_to_half_bits(hv);
-      }
+    up_epilogue<MS>(a, acc, 1.0f, 1.0f, gb, ok, a.hc, a.ldc, item, m0);
   }
 }
 
@@ -682,17 +708,26 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_down_hot(BDownArgs a, int mt
   }
   const int row = nt * 128 + 32 * w + (l & 31);
   const float sd = a.down_s[row];
+  // no element takes a branch (rows past M: dropped by the store's range, or
+  // a zero added to the last row)
+  if (splits == 1) {   // the first and only hot writer
+    const rsrc_t ry = buf_rsrc(a.y, (uint32_t)a.M * kH * 4);
+#pragma unroll
+    for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int m = m0 + 32 * ms + 8 * (j >> 2) + 4 * (l >> 5) + (j & 3);
+        __builtin_amdgcn_raw_buffer_store_b32(acc[ms][0][j] * sd, ry, ((uint32_t)m * kH + row) * 4, 0, 0);
+      }
+    return;
+  }
 #pragma unroll
   for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const int m = m0 + 32 * ms + 8 * (j >> 2) + 4 * (l >> 5) + (j & 3);
-      if (m >= a.M) continue;
-      float* p = a.y + (size_t)m * kH + row;
-      if (splits == 1)
-        *p = acc[ms][0][j] * sd;   // the first and only hot writer
-      else
-        unsafeAtomicAdd(p, acc[ms][0][j] * sd);
+      const bool in = m < a.M;
+      unsafeAtomicAdd(a.y + (size_t)(in ? m : a.M - 1) * kH + row, in ? acc[ms][0][j] * sd : 0.f);
     }
 }
 
@@ -890,9 +925,11 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_down_cold(BDownArgs a, int m
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
+      for (int e = 0; e < 16; ++e) {   // rows past M: a zero added to the last row, no branch
         const int m = m0 + 32 * ms + 8 * (e >> 2) + 4 * (l >> 5) + (e & 3);
-        if (m < a.M) unsafeAtomicAdd(a.y + (size_t)m * kH + j0 + 64 * w + 32 * nb + (l & 31), acc[ms][nb][e]);
+        const bool in = m < a.M;
+        unsafeAtomicAdd(a.y + (size_t)(in ? m : a.M - 1) * kH + j0 + 64 * w + 32 * nb + (l & 31),
+                        in ? acc[ms][nb][e] : 0.f);
       }
 }
 
