@@ -17,10 +17,11 @@
 //   k_bfinal out = x + Y (fp16), y32 = Y
 // Up to 16 tokens, the cold down stores one partial sum per item range and
 // the last kernel (k_bdown_hot_s, or k_bfinal without hot rows) adds them in
-// range order to the hot product: the result is the same on every run.  With
-// more tokens the down kernels accumulate Y with fp32 atomics after the
-// first writer, so the summation order follows the workgroups' timing and
-// repeated runs can differ in the last bits (well inside the FFN tolerance).
+// range order to the hot product.  With more tokens every down workgroup
+// stores its K range's partial sum of its output tile (hot ranges, then
+// cold), and k_bfinal adds them in range order.  No path uses atomics, so the
+// result is the same on every run.  (fp32 atomics into one Y cost the 512-
+// token cold down 65 against 44 us, the 64-token one 28 against 18 us.)
 // fp8 and INT4 weights convert to fp16 exactly.  The small-batch gate/up
 // kernels apply INT4 group scales (one per 128 K) to each block's fp32
 // partial sums, exact up to accumulation; the prefill gate/up and every cold
@@ -376,23 +377,11 @@ __device__ __forceinline__ void pgemm_up_tile(const BUpArgs& a, int nt, int m0, 
   }
 }
 
-// The down kernels' fp32 accumulator cleared by the gate/up launch that
-// precedes them (its workgroups take consecutive float4s, before any of them
-// returns), instead of a fill launch of its own.
-__device__ __forceinline__ void zero_y_share(const BUpArgs& a) {
-  if (!a.yzero) return;
-  const int per = (a.yzero_n4 + (int)gridDim.x - 1) / (int)gridDim.x;
-  const int q0 = blockIdx.x * per, q1 = min(q0 + per, a.yzero_n4);
-  for (int q = q0 + (int)threadIdx.x; q < q1; q += (int)blockDim.x)
-    reinterpret_cast<f32x4*>(a.yzero)[q] = f32x4{0.f, 0.f, 0.f, 0.f};
-}
-
 template <int MS>
 __global__ __launch_bounds__(kThreads) void k_pgemm_up(BUpArgs a, int hot_tiles, int n_tiles, int mt) {
   __shared__ __attribute__((aligned(16))) uint16_t sA[2 * 32 * MS * kLdA];
   __shared__ __attribute__((aligned(16))) uint8_t sB[2 * 256 * kLdB8];
   __shared__ uint16_t sSc[2 * 256];
-  zero_y_share(a);
   const int b = blockIdx.x;
   const int q = b >> 3;
   const int nt = (q / mt) * 8 + (b & 7), mtile = q % mt;
@@ -626,7 +615,6 @@ __device__ __forceinline__ void mup_tile(const BUpArgs& a, int nt, int m0, int t
 // XCDs), sharing its L2 for the weights.
 __global__ __launch_bounds__(kMupThreads) void k_mup(BUpArgs a, int hot_tiles, int n_tiles, int mt) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[kMupLds];
-  zero_y_share(a);
   const int b = blockIdx.x;
   const int q = b >> 3;
   const int nt = (q / mt) * 8 + (b & 7), mtile = q % mt;
@@ -708,26 +696,15 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_down_hot(BDownArgs a, int mt
   }
   const int row = nt * 128 + 32 * w + (l & 31);
   const float sd = a.down_s[row];
-  // no element takes a branch (rows past M: dropped by the store's range, or
-  // a zero added to the last row)
-  if (splits == 1) {   // the first and only hot writer
-    const rsrc_t ry = buf_rsrc(a.y, (uint32_t)a.M * kH * 4);
-#pragma unroll
-    for (int ms = 0; ms < MS; ++ms)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int m = m0 + 32 * ms + 8 * (j >> 2) + 4 * (l >> 5) + (j & 3);
-        __builtin_amdgcn_raw_buffer_store_b32(acc[ms][0][j] * sd, ry, ((uint32_t)m * kH + row) * 4, 0, 0);
-      }
-    return;
-  }
+  // this range's partial sum of y (rows past M dropped by the store's range;
+  // no element takes a branch)
+  const rsrc_t ry = buf_rsrc(a.y + (size_t)split * a.M * kH, (uint32_t)a.M * kH * 4);
 #pragma unroll
   for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const int m = m0 + 32 * ms + 8 * (j >> 2) + 4 * (l >> 5) + (j & 3);
-      const bool in = m < a.M;
-      unsafeAtomicAdd(a.y + (size_t)(in ? m : a.M - 1) * kH + row, in ? acc[ms][0][j] * sd : 0.f);
+      __builtin_amdgcn_raw_buffer_store_b32(as_u32(acc[ms][0][j] * sd), ry, ((uint32_t)m * kH + row) * 4, 0, 0);
     }
 }
 
@@ -790,11 +767,18 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_down_cold(BDownArgs a, int m
   const int kb0 = split * n_blk / splits, kb1 = (split + 1) * n_blk / splits;
   const int t = threadIdx.x, w = t >> 6, l = lane_id();
   const int m0 = mtile * 32 * MS, j0 = jt * 256;
-  if (kb0 >= kb1) {   // the whole workgroup
+  // (from 17 tokens) this range's partial sum of y, rows past M dropped
+  const rsrc_t ry = buf_rsrc(PART ? nullptr : a.y + (size_t)(a.cold_split0 + split) * a.M * kH,
+                             PART ? 0u : (uint32_t)a.M * kH * 4);
+  if (kb0 >= kb1) {   // the whole workgroup: an empty range sums to zero
     if (PART) {
       f32x4* dst = reinterpret_cast<f32x4*>(a.part + ((size_t)split * kH + j0 + t) * 16);
 #pragma unroll
       for (int i = 0; i < 4; ++i) dst[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    } else {
+      for (int i = t; i < 32 * MS * 64; i += kThreads)
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, ry,
+                                                ((uint32_t)(m0 + (i >> 6)) * kH + j0 + 4 * (i & 63)) * 4, 0, 0);
     }
     return;
   }
@@ -925,11 +909,10 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_down_cold(BDownArgs a, int m
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {   // rows past M: a zero added to the last row, no branch
+      for (int e = 0; e < 16; ++e) {
         const int m = m0 + 32 * ms + 8 * (e >> 2) + 4 * (l >> 5) + (e & 3);
-        const bool in = m < a.M;
-        unsafeAtomicAdd(a.y + (size_t)(in ? m : a.M - 1) * kH + j0 + 64 * w + 32 * nb + (l & 31),
-                        in ? acc[ms][nb][e] : 0.f);
+        __builtin_amdgcn_raw_buffer_store_b32(as_u32(acc[ms][nb][e]), ry,
+                                              ((uint32_t)m * kH + j0 + 64 * w + 32 * nb + (l & 31)) * 4, 0, 0);
       }
 }
 
@@ -1340,10 +1323,11 @@ __global__ __launch_bounds__(kThreads) void k_bfill(float* y, int n4) {
 }
 
 // out = res + y (fp16), y32 = y.
-// Y from yacc (M, H), or, with n_part > 0, the sum in range order of the
-// cold ranges' partial sums part[s] (H, 16).
-__global__ __launch_bounds__(kThreads) void k_bfinal(const float* yacc, const float* part, int n_part, int M,
-                                                    const uint16_t* res, uint16_t* out, float* y32) {
+// Y the sum in order of the n_ys partial sums ys[s] (M, H), or, with
+// n_part > 0, the sum in range order of the cold ranges' partial sums
+// part[s] (H, 16).  Either way the result is the same on every run.
+__global__ __launch_bounds__(kThreads) void k_bfinal(const float* ys, int n_ys, const float* part, int n_part,
+                                                    int M, const uint16_t* res, uint16_t* out, float* y32) {
   const int n4 = M * (kH / 4);
   for (int q = blockIdx.x * kThreads + threadIdx.x; q < n4; q += gridDim.x * kThreads) {
     f32x4 y = {0.f, 0.f, 0.f, 0.f};
@@ -1355,7 +1339,17 @@ __global__ __launch_bounds__(kThreads) void k_bfinal(const float* yacc, const fl
         for (int c = 0; c < 4; ++c) y[c] += pp[16 * c];
       }
     } else {
-      y = reinterpret_cast<const f32x4*>(yacc)[q];
+      // four partial sums in flight per pass, added in range order
+      const f32x4* yp = reinterpret_cast<const f32x4*>(ys) + q;
+      int sp = 0;
+      for (; sp + 4 <= n_ys; sp += 4) {
+        f32x4 v[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[k] = yp[(size_t)(sp + k) * n4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) y += v[k];
+      }
+      for (; sp < n_ys; ++sp) y += yp[(size_t)sp * n4];
     }
     if (y32) reinterpret_cast<f32x4*>(y32)[q] = y;
     if (out) {
@@ -1449,7 +1443,10 @@ static BatchPlan batch_plan(int M, int n_hot, int cap) {
   p.off_total = o;
   o = align256(o + 16);
   p.off_y = o;
-  o = align256(o + (size_t)M * kH * 4);
+  // up to 16 tokens: y (M, H); from 17: one (M, H) partial sum per down range
+  const int y_parts = M <= kSkinnyMax ? 1
+                                      : (n_hot > 0 ? p.hot_splits : 0) + (cap > 0 ? cold_down_splits(M, cap) : 0);
+  o = align256(o + (size_t)std::max(1, y_parts) * M * kH * 4);
   p.cold_splits = (M <= kSkinnyMax && cap > 0) ? cold_down_splits(M, cap) : 0;
   p.off_part = o;
   o = align256(o + (size_t)p.cold_splits * kH * 16 * 4);
@@ -1578,7 +1575,7 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
       da.y32 = y32;
       launch_skinny(ua, da, false, x, norm_w, eps, st);
     } else {
-      hipLaunchKernelGGL(k_bfinal, dim3(grid), dim3(kThreads), 0, st, y, has_cold ? part : nullptr,
+      hipLaunchKernelGGL(k_bfinal, dim3(grid), dim3(kThreads), 0, st, y, 1, has_cold ? part : nullptr,
                          has_cold ? p.cold_splits : 0, M, add_residual ? x : nullptr, out, y32);
     }
     OI2_CHECK_LAUNCH();
@@ -1587,14 +1584,12 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
   const int n4 = M * (kH / 4);
   int grid = (n4 + kThreads - 1) / kThreads;
   grid = grid > 2048 ? 2048 : grid;
-  // the hot product writes y outright when one workgroup owns each output;
-  // otherwise y is cleared, by the gate/up launch when there is one
-  const bool clear_y = !n_hot || p.hot_splits > 1;
+  // each down range stores its own partial sum of y (hot ranges, then cold);
+  // k_bfinal adds them in that order
+  const int hot_splits = n_hot ? p.hot_splits : 0;
+  const int cold_splits = has_cold ? cold_down_splits(M, cap) : 0;
+  da.cold_split0 = hot_splits;
   if (p.ldh + p.ldc > 0) {
-    if (clear_y) {
-      ua.yzero = y;
-      ua.yzero_n4 = n4;
-    }
     if (p.prefill) {
       const int hot_tiles = p.ldh / 128, n_tiles = hot_tiles + p.ldc / 128;
       const dim3 grid((n_tiles + 7) / 8 * 8 * p.pmt);
@@ -1609,10 +1604,6 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
     }
     OI2_CHECK_LAUNCH();
   }
-  if (clear_y && p.ldh + p.ldc == 0) {
-    hipLaunchKernelGGL(k_bfill, dim3(grid), dim3(kThreads), 0, st, y, n4);
-    OI2_CHECK_LAUNCH();
-  }
   if (n_hot) {
     const dim3 grid(32 * p.pmt * p.hot_splits);
     if (p.pms == 4)
@@ -1622,20 +1613,19 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
     OI2_CHECK_LAUNCH();
   }
   if (has_cold) {
-    const int splits = cold_down_splits(M, cap);
     if (p.prefill) {
       const int mtc = (M + 127) / 128;
-      hipLaunchKernelGGL((k_pgemm_down_cold<4, false>), dim3(16 * mtc * splits), dim3(kThreads), 0, st, da,
-                         mtc, splits);
+      hipLaunchKernelGGL((k_pgemm_down_cold<4, false>), dim3(16 * mtc * cold_splits), dim3(kThreads), 0, st, da,
+                         mtc, cold_splits);
     } else {
       const int mtc = (M + 63) / 64;
-      hipLaunchKernelGGL((k_pgemm_down_cold<2, false>), dim3(16 * mtc * splits), dim3(kThreads), 0, st, da,
-                         mtc, splits);
+      hipLaunchKernelGGL((k_pgemm_down_cold<2, false>), dim3(16 * mtc * cold_splits), dim3(kThreads), 0, st, da,
+                         mtc, cold_splits);
     }
     OI2_CHECK_LAUNCH();
   }
-  hipLaunchKernelGGL(k_bfinal, dim3(grid), dim3(kThreads), 0, st, y, nullptr, 0, M, add_residual ? x : nullptr,
-                     out, y32);
+  hipLaunchKernelGGL(k_bfinal, dim3(grid), dim3(kThreads), 0, st, y, hot_splits + cold_splits, nullptr, 0, M,
+                     add_residual ? x : nullptr, out, y32);
   OI2_CHECK_LAUNCH();
   return OI2_OK;
 }

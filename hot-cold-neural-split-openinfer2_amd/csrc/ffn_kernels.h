@@ -184,8 +184,6 @@ struct BUpArgs {
   int ldc;
   int Mpad;
   int hot_per_wg;           // k_sbup: hot rows per workgroup (n_hot over 256 workgroups)
-  float* yzero;             // k_mup / k_pgemm_up: non-null, zero these yzero_n4 float4s first
-  int yzero_n4;             //   (the down kernels' accumulator; the launch spreads them over its workgroups)
 };
 
 struct BDownArgs {
@@ -204,7 +202,11 @@ struct BDownArgs {
   const int32_t* dslots;
   const int32_t* total;
   int cap;
-  float* y;                 // (M, H) fp32 output, accumulated with atomics
+  // from 17 tokens: (splits, M, H) fp32, one partial sum of y per down range
+  // (the hot ranges, then the cold ranges from cold_split0), which k_bfinal
+  // adds in that order
+  float* y;
+  int cold_split0;
   // at most 16 tokens: the cold down's partial sums, n_part item ranges of
   // (H, 16) fp32; k_bdown_hot_s, the last of the small-batch kernels, adds
   // them in range order to the hot product -> out = fp16(res + y) (res may
