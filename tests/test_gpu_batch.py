@@ -254,12 +254,13 @@ def test_batch_ignores_workspace_contents(dev, layer25, B):
                      what=f"B={B} NaN-filled vs zeroed workspace")
 
 
-@pytest.mark.parametrize("B", [2, 8, 16])
-def test_small_batch_is_bit_reproducible(dev, layer25, B):
-    """Up to 16 tokens no kernel accumulates with atomics: the cold down's
-    item ranges are added in range order, so repeated calls (the workspace
-    NaN-filled in between, and only the hot half or only the cold half too)
-    give the same bits."""
+@pytest.mark.parametrize("B", [2, 8, 16, 17, 64, 200, 512])
+def test_batch_is_bit_reproducible(dev, layer25, B):
+    """No batch kernel accumulates with atomics: up to 16 tokens the cold
+    down's item ranges are added in range order, from 17 tokens every down
+    workgroup's partial sum is added in range order by the final launch, so
+    repeated calls (the workspace NaN-filled in between, and only the hot
+    half or only the cold half too) give the same bits."""
     from oi2.layer import workspace_bytes
     lay, g = layer25
     n_cold = lay.records.shape[0]
