@@ -634,18 +634,19 @@ __global__ __launch_bounds__(kMupThreads) void k_mup(BUpArgs a, int hot_tiles, i
   mup_tile<false>(a, nt - hot_tiles, m0, total, i0, smem);
 }
 
-// Hot down for 32 MS tokens x 128 outputs (4 waves x 32) over the K blocks of
-// one of `splits` ranges; y gets the scaled sums (stored when splits == 1,
-// else added atomically into a zeroed y).  The down rows of each K block are
-// staged through padded LDS like the gate/up weights (thread t: chunk t & 7
-// of rows t / 8 + 32 i); chunks past the row stride read as zero (the stride
-// is a multiple of 64, so a chunk never straddles it).  Same XCD-aware
-// index mapping.
-template <int MS>
+// Hot down for 32 MS tokens x 128 NB outputs (4 waves x 32 NB) over the K
+// blocks of one of `splits` ranges, whose partial sum of y it stores.  The
+// down rows of each K block are staged through padded LDS like the gate/up
+// weights (thread t: chunk t & 7 of rows t / 8 + 32 i); chunks past the row
+// stride read as zero (the stride is a multiple of 64, so a chunk never
+// straddles it).  Same XCD-aware index mapping.  At 128 tokens a wave's 32
+// output rows took 4 A fragments per B fragment from LDS; NB = 2 halves the
+// LDS reads per MFMA.
+template <int MS, int NB>
 __global__ __launch_bounds__(kThreads) void k_pgemm_down_hot(BDownArgs a, int mt, int splits) {
   constexpr int kAbuf = 32 * MS * kLdA;
-  constexpr int kBbuf = 128 * kLdB8;
-  constexpr int kTiles = kH / 128;
+  constexpr int kBbuf = 128 * NB * kLdB8;
+  constexpr int kTiles = kH / (128 * NB);
   __shared__ __attribute__((aligned(16))) uint16_t sA[2 * kAbuf];
   __shared__ __attribute__((aligned(16))) uint8_t sB[2 * kBbuf];
   const int b = blockIdx.x;
@@ -659,24 +660,27 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_down_hot(BDownArgs a, int mt
   const int t = threadIdx.x, w = t >> 6, l = lane_id();
   const ARows<MS> arows(a.hh, a.ldh, a.M, m0);
   const rsrc_t rd = buf_rsrc(a.down_q, (uint32_t)kH * a.down_stride);
-  uint32_t voff[4];
+  uint32_t voff[4 * NB];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) voff[i] = (uint32_t)(nt * 128 + (t >> 3) + 32 * i) * a.down_stride + 16 * (t & 7);
-  f32x16 acc[MS][1];
+  for (int i = 0; i < 4 * NB; ++i)
+    voff[i] = (uint32_t)(nt * 128 * NB + (t >> 3) + 32 * i) * a.down_stride + 16 * (t & 7);
+  f32x16 acc[MS][NB];
 #pragma unroll
-  for (int ms = 0; ms < MS; ++ms) acc[ms][0] = f32x16{};
-  u32x4 ra[2 * MS], rb[4];
+  for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[ms][nb] = f32x16{};
+  u32x4 ra[2 * MS], rb[4 * NB];
   auto load_b = [&](int kb) {
     const bool in = kb * kBK + 16 * (t & 7) < a.down_stride;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 4 * NB; ++i) {
       const u32x4 v = bload16(rd, voff[i], kb * kBK);
       rb[i] = in ? v : u32x4{0u, 0u, 0u, 0u};
     }
   };
   auto store_b = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 4 * NB; ++i) {
       uint8_t* d = sB + buf * kBbuf + ((t >> 3) + 32 * i) * kLdB8 + 16 * (t & 7);
       reinterpret_cast<u32x2*>(d)[0] = u32x2{rb[i].x, rb[i].y};
       reinterpret_cast<u32x2*>(d)[1] = u32x2{rb[i].z, rb[i].w};
@@ -692,24 +696,27 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_down_hot(BDownArgs a, int mt
     arows.load(kn, ra);
     load_b(kn);
     __builtin_amdgcn_sched_barrier(0);
-    mma_block_lds<MS, 1, false>(sA + cur * kAbuf, sB + cur * kBbuf, nullptr, acc);
+    mma_block_lds<MS, NB, false>(sA + cur * kAbuf, sB + cur * kBbuf, nullptr, acc);
     __builtin_amdgcn_sched_barrier(0);
     store_a_rows<2 * MS, false>(ra, sA + (cur ^ 1) * kAbuf);
     store_b(cur ^ 1);
     lds_barrier();
   }
-  const int row = nt * 128 + 32 * w + (l & 31);
-  const float sd = a.down_s[row];
   // this range's partial sum of y (rows past M dropped by the store's range;
   // no element takes a branch)
   const rsrc_t ry = buf_rsrc(a.y + (size_t)split * a.M * kH, (uint32_t)a.M * kH * 4);
 #pragma unroll
-  for (int ms = 0; ms < MS; ++ms)
+  for (int nb = 0; nb < NB; ++nb) {
+    const int row = nt * 128 * NB + 128 * nb + 32 * w + (l & 31);
+    const float sd = a.down_s[row];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int m = m0 + 32 * ms + 8 * (j >> 2) + 4 * (l >> 5) + (j & 3);
-      __builtin_amdgcn_raw_buffer_store_b32(as_u32(acc[ms][0][j] * sd), ry, ((uint32_t)m * kH + row) * 4, 0, 0);
-    }
+    for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int m = m0 + 32 * ms + 8 * (j >> 2) + 4 * (l >> 5) + (j & 3);
+        __builtin_amdgcn_raw_buffer_store_b32(as_u32(acc[ms][nb][j] * sd), ry, ((uint32_t)m * kH + row) * 4, 0, 0);
+      }
+  }
 }
 
 // Cold down for 128 tokens x 256 outputs (4 waves x 64) over a range of the
@@ -1404,6 +1411,8 @@ constexpr int kSkinnyMax = 16;    // token counts up to this use the one-tile sp
 constexpr int kPrefillMin = 192;  // token counts from this use the 128-row tile kernels
 
 static int prefill_ms(int M) { return M >= 384 ? 4 : 2; }   // 32-token subtiles per tile
+// hot down output tiles: 256 outputs each on the 128-token tiles, else 128
+static int hot_down_tiles(int pms) { return pms == 4 ? kH / 256 : kH / 128; }
 
 // Cold down grid: 16 output tiles x token tiles (32 tokens up to 16 tokens,
 // else 128) x item ranges, about 256 workgroups; a range holds at most
@@ -1430,8 +1439,9 @@ static BatchPlan batch_plan(int M, int n_hot, int cap) {
     // below the prefill sizes, 32 pms-token tiles from them on
     p.pms = p.prefill ? prefill_ms(M) : 2;
     p.pmt = (M + 32 * p.pms - 1) / (32 * p.pms);
-    // hot down: 32 output tiles x token tiles x K splits, about 256 workgroups
-    p.hot_splits = std::max(1, std::min(p.hot_blocks, 256 / (32 * p.pmt)));
+    // hot down: output tiles (128 outputs, 256 on the 128-token tiles) x token
+    // tiles x K splits, about 256 workgroups
+    p.hot_splits = std::max(1, std::min(p.hot_blocks, 256 / (hot_down_tiles(p.pms) * p.pmt)));
   } else {
     p.hot_splits = p.mt >= 4 ? 1 : 4 / p.mt;
   }
@@ -1609,11 +1619,11 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
     OI2_CHECK_LAUNCH();
   }
   if (n_hot) {
-    const dim3 grid(32 * p.pmt * p.hot_splits);
+    const dim3 grid(hot_down_tiles(p.pms) * p.pmt * p.hot_splits);
     if (p.pms == 4)
-      hipLaunchKernelGGL(k_pgemm_down_hot<4>, grid, dim3(kThreads), 0, st, da, p.pmt, p.hot_splits);
+      hipLaunchKernelGGL((k_pgemm_down_hot<4, 2>), grid, dim3(kThreads), 0, st, da, p.pmt, p.hot_splits);
     else
-      hipLaunchKernelGGL(k_pgemm_down_hot<2>, grid, dim3(kThreads), 0, st, da, p.pmt, p.hot_splits);
+      hipLaunchKernelGGL((k_pgemm_down_hot<2, 1>), grid, dim3(kThreads), 0, st, da, p.pmt, p.hot_splits);
     OI2_CHECK_LAUNCH();
   }
   if (has_cold) {
