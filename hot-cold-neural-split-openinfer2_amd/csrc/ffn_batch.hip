@@ -808,25 +808,28 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_down_cold(BDownArgs a, int m
   const rsrc_t rh = buf_rsrc(a.hc, (uint32_t)a.M * a.ldc * 2);
   const int ig = t & 7, jg = t >> 3;
   const uint32_t dbyte = kOffDown + (j0 + 8 * jg) / 2;                        // this thread's dword
-  const uint32_t sbyte = kOffScales + 2 * (2 * kGroups + (j0 + 8 * jg) / kGroup);  // its down scale
+  // the wave's down scale group: its threads' outputs j0 + 8 jg, jg in
+  // [8 w, 8 w + 8), all lie in group (j0 + 64 w) / kGroup
+  const uint32_t sbyte = kOffScales + 2 * (2 * kGroups + (j0 + 64 * w) / kGroup);
   // H tile: thread t loads chunk t & 7 (8 items) of token rows t / 8 + 32 r
   uint32_t hoff[MS];
 #pragma unroll
   for (int r = 0; r < MS; ++r) hoff[r] = ((uint32_t)(m0 + (t >> 3) + 32 * r) * a.ldc + 8 * (t & 7)) * 2;
 
   uint32_t dq[8];
-  uint16_t dsc[8];
+  uint32_t sc_l;   // lane l: the wave's down scale of item l of the block
   u32x4 hv[MS];
-  int hkb = kb0;   // block held in dq / dsc / hv
+  int hkb = kb0;   // block held in dq / sc_l / hv
   auto load_block = [&](int kb) {
     hkb = kb;
     const int ib = (kb - kb0) * kDcItems + 8 * ig;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const uint32_t vr = s_rec[ib + k];
-      dq[k] = __builtin_amdgcn_raw_buffer_load_b32(rr, (int)(vr + dbyte), 0, 0);
-      dsc[k] = bload2(rr, vr + sbyte, 0);
-    }
+    for (int k = 0; k < 8; ++k)
+      dq[k] = __builtin_amdgcn_raw_buffer_load_b32(rr, (int)(s_rec[ib + k] + dbyte), 0, 0);
+    // one scale per item per wave (the wave's outputs share a group): one
+    // 2-byte load per lane instead of eight per thread, handed to the
+    // threads that decode the item by a lane shuffle
+    sc_l = bload2(rr, s_rec[(kb - kb0) * kDcItems + l] + sbyte, 0);
 #pragma unroll
     for (int r = 0; r < MS; ++r) hv[r] = bload16(rh, hoff[r], kb * kDcItems * 2);
   };
@@ -839,8 +842,8 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_down_cold(BDownArgs a, int m
     h8 sv;   // the items' scales in pair order (i0, i4, i1, i5, ...)
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      sv[2 * k] = __builtin_bit_cast(_Float16, dsc[k]);
-      sv[2 * k + 1] = __builtin_bit_cast(_Float16, dsc[k + 4]);
+      sv[2 * k] = __builtin_bit_cast(_Float16, (uint16_t)__shfl(sc_l, 8 * ig + k, kWave));
+      sv[2 * k + 1] = __builtin_bit_cast(_Float16, (uint16_t)__shfl(sc_l, 8 * ig + k + 4, kWave));
     }
     uint16_t* T = sT + buf * kT;
 #pragma unroll
