@@ -768,6 +768,7 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_down_cold(BDownArgs a, int m
   __shared__ __attribute__((aligned(16))) uint16_t sT[2 * kT];
   __shared__ __attribute__((aligned(16))) uint16_t sH[2 * kA];
   __shared__ uint32_t s_rec[kDcMaxItems];
+  __shared__ __attribute__((aligned(16))) uint16_t s_sc[4 * kDcItems];   // per wave: the block's item scales
   const int b = blockIdx.x;
   const int q = b >> 3, per = mt * splits;
   const int jt = (q / per) * 8 + (b & 7), rem = q % per;
@@ -816,35 +817,45 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_down_cold(BDownArgs a, int m
 #pragma unroll
   for (int r = 0; r < MS; ++r) hoff[r] = ((uint32_t)(m0 + (t >> 3) + 32 * r) * a.ldc + 8 * (t & 7)) * 2;
 
-  uint32_t dq[8];
-  uint32_t sc_l;   // lane l: the wave's down scale of item l of the block
-  u32x4 hv[MS];
-  int hkb = kb0;   // block held in dq / sc_l / hv
-  auto load_block = [&](int kb) {
-    hkb = kb;
+  // a K block's loads, held in registers until it is decoded into LDS
+  struct Blk {
+    uint32_t dq[8];   // this thread's record dword of items 8 ig .. 8 ig + 7
+    uint32_t sc;      // lane l: the wave's down scale of item l of the block
+    u32x4 hv[MS];     // the H tile
+    int kb;
+  };
+  auto load_block = [&](int kb, Blk& B) {
+    B.kb = kb;
     const int ib = (kb - kb0) * kDcItems + 8 * ig;
 #pragma unroll
     for (int k = 0; k < 8; ++k)
-      dq[k] = __builtin_amdgcn_raw_buffer_load_b32(rr, (int)(s_rec[ib + k] + dbyte), 0, 0);
+      B.dq[k] = __builtin_amdgcn_raw_buffer_load_b32(rr, (int)(s_rec[ib + k] + dbyte), 0, 0);
     // one scale per item per wave (the wave's outputs share a group): one
     // 2-byte load per lane instead of eight per thread, handed to the
-    // threads that decode the item by a lane shuffle
-    sc_l = bload2(rr, s_rec[(kb - kb0) * kDcItems + l] + sbyte, 0);
+    // threads that decode the item through the wave's own LDS row
+    B.sc = bload2(rr, s_rec[(kb - kb0) * kDcItems + l] + sbyte, 0);
 #pragma unroll
-    for (int r = 0; r < MS; ++r) hv[r] = bload16(rh, hoff[r], kb * kDcItems * 2);
+    for (int r = 0; r < MS; ++r) B.hv[r] = bload16(rh, hoff[r], kb * kDcItems * 2);
   };
   // decode the loaded block into buffer `buf`
-  auto store_block = [&](int buf) {
+  auto store_block = [&](int buf, const Blk& B) {
+    const int hkb = B.kb;
     uint32_t c[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) c[k] = dq[k];
+    for (int k = 0; k < 8; ++k) c[k] = B.dq[k];
     nibble_transpose8(c);
-    h8 sv;   // the items' scales in pair order (i0, i4, i1, i5, ...)
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      sv[2 * k] = __builtin_bit_cast(_Float16, (uint16_t)__shfl(sc_l, 8 * ig + k, kWave));
-      sv[2 * k + 1] = __builtin_bit_cast(_Float16, (uint16_t)__shfl(sc_l, 8 * ig + k + 4, kWave));
-    }
+    // the wave's LDS row: written by lane l, read back 8 items per thread
+    // by the same wave (its LDS operations complete in order)
+    s_sc[w * kDcItems + l] = (uint16_t)B.sc;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const u32x4 s8 = *reinterpret_cast<const u32x4*>(s_sc + w * kDcItems + 8 * ig);   // items 0..7, 2 a dword
+    // the items' scales in pair order (i0, i4, i1, i5, ...)
+    const h8 sv = __builtin_bit_cast(h8, u32x4{__builtin_amdgcn_perm(s8.z, s8.x, 0x05040100u),
+                                               __builtin_amdgcn_perm(s8.z, s8.x, 0x07060302u),
+                                               __builtin_amdgcn_perm(s8.w, s8.y, 0x05040100u),
+                                               __builtin_amdgcn_perm(s8.w, s8.y, 0x07060302u)});
     uint16_t* T = sT + buf * kT;
 #pragma unroll
     for (int n = 0; n < 8; ++n) {
@@ -864,7 +875,7 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_down_cold(BDownArgs a, int m
       km[d] = (2 * d < keep ? 0x0000FFFFu : 0u) | (2 * d + 1 < keep ? 0xFFFF0000u : 0u);
 #pragma unroll
     for (int r = 0; r < MS; ++r) {
-      const uint32_t d0 = hv[r].x & km[0], d1 = hv[r].y & km[1], d2 = hv[r].z & km[2], d3 = hv[r].w & km[3];
+      const uint32_t d0 = B.hv[r].x & km[0], d1 = B.hv[r].y & km[1], d2 = B.hv[r].z & km[2], d3 = B.hv[r].w & km[3];
       u32x4 v;
       v.x = (d0 & 0xFFFFu) | (d2 << 16);
       v.y = (d0 >> 16) | (d2 & 0xFFFF0000u);
@@ -879,13 +890,9 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_down_cold(BDownArgs a, int m
   for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) acc[ms][nb] = f32x16{};
-  load_block(kb0);
-  store_block(0);
-  lds_barrier();
-  for (int kb = kb0; kb < kb1; ++kb) {
-    const int cur = (kb - kb0) & 1;
-    load_block(min(kb + 1, kb1 - 1));
-    __builtin_amdgcn_sched_barrier(0);
+  // blocks are loaded two ahead: block kb + 2's loads go out while block kb
+  // is multiplied and block kb + 1 (loaded an iteration earlier) is decoded
+  auto mma_block = [&](int cur) {
     const uint16_t* T = sT + cur * kT;
     const uint16_t* Hs = sH + cur * kA;
 #pragma unroll
@@ -902,8 +909,27 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_down_cold(BDownArgs a, int m
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) acc[ms][nb] = mfma32(av[ms], bf[nb], acc[ms][nb]);
     }
+  };
+  Blk B0, B1;
+  load_block(kb0, B0);
+  load_block(min(kb0 + 1, kb1 - 1), B1);
+  store_block(0, B0);
+  lds_barrier();
+  for (int kb = kb0; kb < kb1; kb += 2) {
+    // block kb in LDS buffer 0, block kb + 1 in B1
+    load_block(min(kb + 2, kb1 - 1), B0);
     __builtin_amdgcn_sched_barrier(0);
-    store_block(cur ^ 1);
+    mma_block(0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (kb + 1 >= kb1) break;   // workgroup-uniform
+    store_block(1, B1);
+    lds_barrier();
+    // block kb + 1 in LDS buffer 1, block kb + 2 in B0
+    load_block(min(kb + 3, kb1 - 1), B1);
+    __builtin_amdgcn_sched_barrier(0);
+    mma_block(1);
+    __builtin_amdgcn_sched_barrier(0);
+    store_block(0, B0);
     lds_barrier();
   }
   if (PART) {
