@@ -641,8 +641,10 @@ __global__ __launch_bounds__(kMupThreads) void k_mup(BUpArgs a, int hot_tiles, i
 // stride read as zero (the stride is a multiple of 64, so a chunk never
 // straddles it).  Same XCD-aware index mapping.  At 128 tokens a wave's 32
 // output rows took 4 A fragments per B fragment from LDS; NB = 2 halves the
-// LDS reads per MFMA.
-template <int MS, int NB>
+// LDS reads per MFMA.  The K blocks are loaded D ahead into D register sets
+// (a range of a few blocks at 17-191 tokens is otherwise one load latency
+// per block).
+template <int MS, int NB, int D>
 __global__ __launch_bounds__(kThreads) void k_pgemm_down_hot(BDownArgs a, int mt, int splits) {
   constexpr int kAbuf = 32 * MS * kLdA;
   constexpr int kBbuf = 128 * NB * kLdB8;
@@ -669,38 +671,46 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_down_hot(BDownArgs a, int mt
   for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) acc[ms][nb] = f32x16{};
-  u32x4 ra[2 * MS], rb[4 * NB];
-  auto load_b = [&](int kb) {
-    const bool in = kb * kBK + 16 * (t & 7) < a.down_stride;
-#pragma unroll
-    for (int i = 0; i < 4 * NB; ++i) {
-      const u32x4 v = bload16(rd, voff[i], kb * kBK);
-      rb[i] = in ? v : u32x4{0u, 0u, 0u, 0u};
-    }
+  struct Stage {
+    u32x4 ra[2 * MS], rb[4 * NB];
+    bool in;   // the block's chunk lies inside the row stride
   };
-  auto store_b = [&](int buf) {
+  auto load = [&](int kb, Stage& S) {
+    arows.load(kb, S.ra);
+    S.in = kb * kBK + 16 * (t & 7) < a.down_stride;
+#pragma unroll
+    for (int i = 0; i < 4 * NB; ++i) S.rb[i] = bload16(rd, voff[i], kb * kBK);
+  };
+  auto store = [&](int buf, const Stage& S) {
+    store_a_rows<2 * MS, false>(S.ra, sA + buf * kAbuf);
 #pragma unroll
     for (int i = 0; i < 4 * NB; ++i) {
+      const u32x4 v = S.in ? S.rb[i] : u32x4{0u, 0u, 0u, 0u};
       uint8_t* d = sB + buf * kBbuf + ((t >> 3) + 32 * i) * kLdB8 + 16 * (t & 7);
-      reinterpret_cast<u32x2*>(d)[0] = u32x2{rb[i].x, rb[i].y};
-      reinterpret_cast<u32x2*>(d)[1] = u32x2{rb[i].z, rb[i].w};
+      reinterpret_cast<u32x2*>(d)[0] = u32x2{v.x, v.y};
+      reinterpret_cast<u32x2*>(d)[1] = u32x2{v.z, v.w};
     }
   };
-  arows.load(kb0, ra);
-  load_b(kb0);
-  store_a_rows<2 * MS, false>(ra, sA);
-  store_b(0);
+  // set i holds block kb + i of each D-block round; block b + 1 is staged
+  // while block b is multiplied, and set b % D reloads block b + D
+  Stage S[D];
+#pragma unroll
+  for (int i = 0; i < D; ++i) load(min(kb0 + i, kb1 - 1), S[i]);
+  store(0, S[0]);
   lds_barrier();
-  for (int kb = kb0; kb < kb1; ++kb) {
-    const int kn = min(kb + 1, kb1 - 1), cur = (kb - kb0) & 1;
-    arows.load(kn, ra);
-    load_b(kn);
-    __builtin_amdgcn_sched_barrier(0);
-    mma_block_lds<MS, NB, false>(sA + cur * kAbuf, sB + cur * kBbuf, nullptr, acc);
-    __builtin_amdgcn_sched_barrier(0);
-    store_a_rows<2 * MS, false>(ra, sA + (cur ^ 1) * kAbuf);
-    store_b(cur ^ 1);
-    lds_barrier();
+  for (int kb = kb0; kb < kb1; kb += D) {
+#pragma unroll
+    for (int i = 0; i < D; ++i) {
+      const int bk = kb + i, cur = (bk - kb0) & 1;
+      if (bk >= kb1) break;   // workgroup-uniform
+      load(min(bk + D, kb1 - 1), S[i]);
+      __builtin_amdgcn_sched_barrier(0);
+      mma_block_lds<MS, NB, false>(sA + cur * kAbuf, sB + cur * kBbuf, nullptr, acc);
+      __builtin_amdgcn_sched_barrier(0);
+      if (bk + 1 >= kb1) break;
+      store(cur ^ 1, S[(i + 1) % D]);
+      lds_barrier();
+    }
   }
   // this range's partial sum of y (rows past M dropped by the store's range;
   // no element takes a branch)
@@ -1650,9 +1660,9 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
   if (n_hot) {
     const dim3 grid(hot_down_tiles(p.pms) * p.pmt * p.hot_splits);
     if (p.pms == 4)
-      hipLaunchKernelGGL((k_pgemm_down_hot<4, 2>), grid, dim3(kThreads), 0, st, da, p.pmt, p.hot_splits);
+      hipLaunchKernelGGL((k_pgemm_down_hot<4, 2, 1>), grid, dim3(kThreads), 0, st, da, p.pmt, p.hot_splits);
     else
-      hipLaunchKernelGGL((k_pgemm_down_hot<2, 1>), grid, dim3(kThreads), 0, st, da, p.pmt, p.hot_splits);
+      hipLaunchKernelGGL((k_pgemm_down_hot<2, 1, 4>), grid, dim3(kThreads), 0, st, da, p.pmt, p.hot_splits);
     OI2_CHECK_LAUNCH();
   }
   if (has_cold) {
