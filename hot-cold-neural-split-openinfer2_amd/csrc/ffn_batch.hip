@@ -420,61 +420,73 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_up(BUpArgs a, int hot_tiles,
 // tile.
 // A cold tile's group scales (32 gate + 32 up per item) go to LDS once, up
 // front.
-constexpr int kMupN = 32;                            // neurons per tile
+// Wide tiles (NW = 2: 64 neurons, eight MFMAs per block and wave) make up
+// the difference when a batch of at most 64 tokens has more 32-neuron units
+// than the GPU has CUs: every tile then runs in one round, one per CU, where
+// narrow tiles alone would put a second tile on some CUs (a CU with two
+// takes ~1.5x as long as one with one).
+constexpr int kMupN = 32;                            // neurons per subtile
 constexpr int kMupThreads = 512;
-constexpr int kMupBbuf = 64 * kLdB8;                 // bytes per B buffer (32 x 2 rows)
+constexpr int kMupBbuf = 128 * kLdB8;                // bytes per B buffer (2 subtiles x 32 x 2 rows)
 constexpr int kMupAbuf = 64 * kLdA * 2;              // bytes per A buffer
 constexpr int kMupSc = 2 * kMupAbuf + 2 * kMupBbuf;  // the scales' byte offset
-constexpr int kMupRedBuf = 2 * 2 * 16 * 64 * 4;      // one wave's sums: [ms][g][j][lane] fp32
-constexpr int kMupLds = std::max(kMupSc + kMupN * 2 * kGroups * 2, 4 * kMupRedBuf);
+constexpr int kMupRedBuf = 2 * 2 * 16 * 64 * 4;      // one wave's sums of a subtile: [ms][g][j][lane] fp32
+constexpr int kMupLds = std::max(kMupSc + 2 * kMupN * 2 * kGroups * 2, 4 * kMupRedBuf);
 
-template <bool HOT>
-__device__ __forceinline__ void mup_tile(const BUpArgs& a, int nt, int m0, int total, int i0, uint8_t* smem) {
+// n0: the tile's first hot row (HOT) or dense list item (cold).
+template <bool HOT, int NW>
+__device__ __forceinline__ void mup_tile(const BUpArgs& a, int n0, int m0, int total, uint8_t* smem) {
+  constexpr int TW = kMupN * NW;   // neurons of the tile
   uint16_t* sA = reinterpret_cast<uint16_t*>(smem);
   uint8_t* sB = smem + 2 * kMupAbuf;
   uint16_t* sSc = reinterpret_cast<uint16_t*>(smem + kMupSc);
   const int t = threadIdx.x, w = __builtin_amdgcn_readfirstlane(t >> 6), l = lane_id(), h = l >> 5, col = l & 31;
-  // cold: waves 0-3 stage the 4 KB weight block, waves 4-7 issue the same
-  // load over an empty range (every wave runs the same loads, so the
-  // compiler's wait counts stay exact)
-  const bool bstore = HOT || w < 4;
+  // cold, narrow: waves 0-3 stage the 4 KB weight block, waves 4-7 issue the
+  // same load over an empty range (every wave runs the same loads, so the
+  // compiler's wait counts stay exact); wide: all eight stage the 8 KB
+  const bool bstore = HOT || NW == 2 || w < 4;
   // A staging: chunk t & 15 (8 halves) of token rows m0 + (t >> 4) + 32 i;
   // rows past M read zero
   const rsrc_t rx = buf_rsrc(a.xn, (uint32_t)a.M * kH * 2);
   uint32_t aoff[2];
 #pragma unroll
   for (int i = 0; i < 2; ++i) aoff[i] = ((uint32_t)(m0 + (t >> 4) + 32 * i) * kH + 8 * (t & 15)) * 2;
-  // B staging: hot, chunk t & 7 of row t >> 3 (rows 0..31 the gate rows of
-  // the tile's neurons, 32..63 their up rows); cold (t < 256), chunk t & 3 of
-  // item t >> 3, gate for (t >> 2) & 1 == 0 else up.  Absent rows read zero.
+  // B staging (LDS row 64 s + 32 gu + n: neuron n of subtile s, gate for
+  // gu = 0, up for 1): hot, chunk t & 7 of rows 64 s + (t >> 3), s < NW;
+  // cold, chunk t & 3 of item t >> 3 (t < 256 when narrow), gate for
+  // (t >> 2) & 1 == 0 else up.  Absent rows read zero.
   const rsrc_t rw = HOT ? buf_rsrc(w < 4 ? a.gate_q : a.up_q, (uint32_t)a.n_hot * kH)
-                        : buf_rsrc(a.records, w < 4 ? (uint32_t)a.n_records * kRecBytes : 0u);
+                        : buf_rsrc(a.records, (NW == 2 || w < 4) ? (uint32_t)a.n_records * kRecBytes : 0u);
   auto item_rec = [&](int it) {
     const int slot = it < total ? a.dslots[it] : -1;
     return (slot >= 0 && slot < a.n_records) ? (uint32_t)slot * kRecBytes : kNoOffset;
   };
-  uint32_t boff;
+  constexpr int NBL = HOT ? NW : 1;   // B loads per thread and block
+  uint32_t boff[NBL];
   if constexpr (HOT) {
-    boff = (uint32_t)(nt * kMupN + ((t >> 3) & 31)) * kH + 16 * (t & 7);
+#pragma unroll
+    for (int sb = 0; sb < NW; ++sb) boff[sb] = (uint32_t)(n0 + 32 * sb + ((t >> 3) & 31)) * kH + 16 * (t & 7);
   } else {
-    const uint32_t v = item_rec(i0 + ((t >> 3) & 31));
-    boff = v + (((t >> 2) & 1) ? kOffUp : kOffGate) + 16 * (t & 3);
+    const int it = NW == 2 ? t >> 3 : (t >> 3) & 31;
+    const uint32_t v = item_rec(n0 + it);
+    boff[0] = v + (((t >> 2) & 1) ? kOffUp : kOffGate) + 16 * (t & 3);
     // scales: item t >> 3, 16-byte piece t & 7 of its gate (64 B) and up
     // (64 B) scale arrays, stored as sSc[gate, up][group][item] (a block's
-    // 32 items side by side: lanes read consecutive halves)
-    if (w < 4) {
+    // items side by side: lanes read consecutive halves)
+    if (NW == 2 || w < 4) {
       const u32x4 sv = bload16(rw, v + kOffScales + 16 * (t & 7), 0);
-      const int it = t >> 3, g0 = 8 * (t & 3), gu = (t >> 2) & 1;
+      const int g0 = 8 * (t & 3), gu = (t >> 2) & 1;
 #pragma unroll
       for (int k = 0; k < 8; ++k)
-        sSc[(gu * kGroups + g0 + k) * kMupN + it] = (uint16_t)(sv[k >> 1] >> (16 * (k & 1)));
+        sSc[(gu * kGroups + g0 + k) * TW + it] = (uint16_t)(sv[k >> 1] >> (16 * (k & 1)));
     }
   }
-  u32x4 ra[2][2], rb[2];
+  u32x4 ra[2][2], rb[2][NBL];
   auto load = [&](int kb, int sl) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) ra[sl][i] = bload16(rx, aoff[i], kb * kBK * 2);
-    rb[sl] = bload16(rw, boff, HOT ? kb * kBK : 64 * kb);
+#pragma unroll
+    for (int sb = 0; sb < NBL; ++sb) rb[sl][sb] = bload16(rw, boff[sb], HOT ? kb * kBK : 64 * kb);
   };
   auto store = [&](int buf, int sl) {
     uint16_t* A = sA + buf * (kMupAbuf / 2);
@@ -491,38 +503,55 @@ __device__ __forceinline__ void mup_tile(const BUpArgs& a, int nt, int m0, int t
       *reinterpret_cast<u32x4*>(A + ((t >> 4) + 32 * i) * kLdA + 8 * (t & 15)) = v;
     }
     if (bstore) {
-      uint8_t* d = sB + buf * kMupBbuf +
-                   (HOT ? (t >> 3) * kLdB8 + 16 * (t & 7) : ((t >> 3) + 32 * ((t >> 2) & 1)) * kLdB4 + 16 * (t & 3));
-      reinterpret_cast<u32x2*>(d)[0] = u32x2{rb[sl].x, rb[sl].y};
-      reinterpret_cast<u32x2*>(d)[1] = u32x2{rb[sl].z, rb[sl].w};
+#pragma unroll
+      for (int sb = 0; sb < NBL; ++sb) {
+        uint8_t* d;
+        if constexpr (HOT) {
+          d = sB + buf * kMupBbuf + (64 * sb + (t >> 3)) * kLdB8 + 16 * (t & 7);
+        } else {
+          const int it = t >> 3;   // < 32 when narrow
+          d = sB + buf * kMupBbuf + (64 * (it >> 5) + 32 * ((t >> 2) & 1) + (it & 31)) * kLdB4 + 16 * (t & 3);
+        }
+        reinterpret_cast<u32x2*>(d)[0] = u32x2{rb[sl][sb].x, rb[sl][sb].y};
+        reinterpret_cast<u32x2*>(d)[1] = u32x2{rb[sl][sb].z, rb[sl][sb].w};
+      }
     }
   };
-  f32x16 acc[2][2];   // [token subtile][gate, up]
+  f32x16 acc[2][2][NW];   // [token subtile][gate, up][neuron subtile]
 #pragma unroll
-  for (int ms = 0; ms < 2; ++ms) acc[ms][0] = acc[ms][1] = f32x16{};
-  // K step w of block kb: rows col (gate) and 32 + col (up), this lane's 8 K
+  for (int ms = 0; ms < 2; ++ms)
+#pragma unroll
+    for (int sb = 0; sb < NW; ++sb) acc[ms][0][sb] = acc[ms][1][sb] = f32x16{};
+  // K step w of block kb: rows 64 s + col (gate) and 64 s + 32 + col (up),
+  // this lane's 8 K
   auto mma_block = [&](int buf, int kb) {
     const uint16_t* A = sA + buf * (kMupAbuf / 2);
     const uint8_t* B = sB + buf * kMupBbuf;
-    h8 bg, bu;
-    if constexpr (HOT) {
-      const u32x2 vg = *reinterpret_cast<const u32x2*>(B + col * kLdB8 + 64 * h + 8 * w);
-      const u32x2 vu = *reinterpret_cast<const u32x2*>(B + (32 + col) * kLdB8 + 64 * h + 8 * w);
-      bg = fp8x8_h8(vg[0], vg[1]);
-      bu = fp8x8_h8(vu[0], vu[1]);
-    } else {
-      const _Float16 sg = __builtin_bit_cast(_Float16, sSc[kb * kMupN + col]);
-      const _Float16 su = __builtin_bit_cast(_Float16, sSc[(kGroups + kb) * kMupN + col]);
-      const uint32_t dg = *reinterpret_cast<const uint32_t*>(B + col * kLdB4 + 32 * h + 4 * w);
-      const uint32_t du = *reinterpret_cast<const uint32_t*>(B + (32 + col) * kLdB4 + 32 * h + 4 * w);
-      bg = int4x8_h8_scaled(dg, sg);
-      bu = int4x8_h8_scaled(du, su);
+    h8 bg[NW], bu[NW];
+#pragma unroll
+    for (int sb = 0; sb < NW; ++sb) {
+      if constexpr (HOT) {
+        const u32x2 vg = *reinterpret_cast<const u32x2*>(B + (64 * sb + col) * kLdB8 + 64 * h + 8 * w);
+        const u32x2 vu = *reinterpret_cast<const u32x2*>(B + (64 * sb + 32 + col) * kLdB8 + 64 * h + 8 * w);
+        bg[sb] = fp8x8_h8(vg[0], vg[1]);
+        bu[sb] = fp8x8_h8(vu[0], vu[1]);
+      } else {
+        const _Float16 sg = __builtin_bit_cast(_Float16, sSc[kb * TW + 32 * sb + col]);
+        const _Float16 su = __builtin_bit_cast(_Float16, sSc[(kGroups + kb) * TW + 32 * sb + col]);
+        const uint32_t dg = *reinterpret_cast<const uint32_t*>(B + (64 * sb + col) * kLdB4 + 32 * h + 4 * w);
+        const uint32_t du = *reinterpret_cast<const uint32_t*>(B + (64 * sb + 32 + col) * kLdB4 + 32 * h + 4 * w);
+        bg[sb] = int4x8_h8_scaled(dg, sg);
+        bu[sb] = int4x8_h8_scaled(du, su);
+      }
     }
 #pragma unroll
     for (int ms = 0; ms < 2; ++ms) {
       const h8 av = a_frag32(A, ms, w);
-      acc[ms][0] = mfma32(av, bg, acc[ms][0]);
-      acc[ms][1] = mfma32(av, bu, acc[ms][1]);
+#pragma unroll
+      for (int sb = 0; sb < NW; ++sb) {
+        acc[ms][0][sb] = mfma32(av, bg[sb], acc[ms][0][sb]);
+        acc[ms][1][sb] = mfma32(av, bu[sb], acc[ms][1][sb]);
+      }
     }
   };
 
@@ -548,90 +577,113 @@ __device__ __forceinline__ void mup_tile(const BUpArgs& a, int nt, int m0, int t
     }
   }
 
-  // the epilogue's operands of this lane's column, loaded while the sums meet
-  float sg = 0.f, su = 0.f, gb = 0.f;
-  bool ok;
-  int item = 0;
-  if constexpr (HOT) {
-    const int row = nt * kMupN + col;
-    ok = row < a.n_hot;
-    if (ok) {
-      sg = a.gate_s[row];
-      su = a.up_s[row];
-      gb = a.hot_gbias ? a.hot_gbias[row] : 0.f;
+  // the epilogue's operands of this lane's columns, loaded while the sums meet
+  float sg[NW], su[NW], gb[NW];
+  bool ok[NW];
+#pragma unroll
+  for (int sb = 0; sb < NW; ++sb) {
+    sg[sb] = su[sb] = gb[sb] = 0.f;
+    if constexpr (HOT) {
+      const int row = n0 + 32 * sb + col;
+      ok[sb] = row < a.n_hot;
+      if (ok[sb]) {
+        sg[sb] = a.gate_s[row];
+        su[sb] = a.up_s[row];
+        gb[sb] = a.hot_gbias ? a.hot_gbias[row] : 0.f;
+      }
+    } else {
+      const int item = n0 + 32 * sb + col;
+      const int slot = item < total ? a.dslots[item] : -1;
+      ok[sb] = slot >= 0 && slot < a.n_records;
+      gb[sb] = (ok[sb] && a.cold_gbias) ? a.cold_gbias[slot] : 0.f;
     }
-  } else {
-    item = i0 + col;
-    const int slot = item < total ? a.dslots[item] : -1;
-    ok = slot >= 0 && slot < a.n_records;
-    gb = (ok && a.cold_gbias) ? a.cold_gbias[slot] : 0.f;
   }
-  // the eight waves' sums meet in LDS (the operand buffers are free now):
-  // waves 4-7 store theirs, waves 0-3 add them to their own and store the
-  // pair; then wave w adds the four pairs (in wave order) for its four
-  // (subtile, row group) pairs of the tile and writes those outputs
+  // the eight waves' sums of each neuron subtile meet in LDS (the operand
+  // buffers are free now): waves 4-7 store theirs, waves 0-3 add them to
+  // their own and store the pair; then wave w adds the four pairs (in wave
+  // order) for its four (token subtile, row group) pairs and writes those
+  // outputs
   float* red = reinterpret_cast<float*>(smem);
   auto red_at = [&](int buf, int ms, int g, int j) { return red + buf * (kMupRedBuf / 4) + ((ms * 2 + g) * 16 + j) * 64 + l; };
-  if (w >= 4) {
-#pragma unroll
-    for (int ms = 0; ms < 2; ++ms)
-#pragma unroll
-      for (int g = 0; g < 2; ++g)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) *red_at(w - 4, ms, g, j) = acc[ms][g][j];
-  }
-  __syncthreads();
-  if (w < 4) {
-#pragma unroll
-    for (int ms = 0; ms < 2; ++ms)
-#pragma unroll
-      for (int g = 0; g < 2; ++g)
-#pragma unroll
-        for (int j = 0; j < 16; ++j) *red_at(w, ms, g, j) = acc[ms][g][j] + *red_at(w, ms, g, j);
-  }
-  __syncthreads();
-  // wave w: subtile ms = w >> 2, output rows j = 4 (w & 3) .. + 3, i.e. tokens
-  // m0 + 32 ms + 8 (w & 3) + 4 h + i, i < 4
   const int ms = w >> 2;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int j = 4 * (w & 3) + i;
-    float gs = 0.f, us = 0.f;
+  for (int sb = 0; sb < NW; ++sb) {
+    if (sb > 0) __syncthreads();   // the previous subtile's sums are read
+    if (w >= 4) {
 #pragma unroll
-    for (int bq = 0; bq < 4; ++bq) {
-      gs += *red_at(bq, ms, 0, j);
-      us += *red_at(bq, ms, 1, j);
+      for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int g = 0; g < 2; ++g)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) *red_at(w - 4, q, g, j) = acc[q][g][sb][j];
     }
-    const int m = m0 + 32 * ms + 8 * (j >> 2) + 4 * h + (j & 3);
-    if (m >= a.M) continue;
-    if constexpr (HOT) {
-      const float hv = ok ? gated_act(fmaf(gs, sg, gb), us * su, a.relu, a.both) : 0.f;
-      a.hh[(size_t)m * a.ldh + nt * kMupN + col] = float_to_half_bits(hv);
-    } else {
-      const float hv = ok ? gated_act(gs + gb, us, a.relu, a.both) : 0.f;
-      a.hc[(size_t)m * a.ldc + item] = float_to_half_bits(hv);
+    __syncthreads();
+    if (w < 4) {
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int g = 0; g < 2; ++g)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) *red_at(w, q, g, j) = acc[q][g][sb][j] + *red_at(w, q, g, j);
+    }
+    __syncthreads();
+    // wave w: token subtile ms = w >> 2, output rows j = 4 (w & 3) .. + 3,
+    // i.e. tokens m0 + 32 ms + 8 (w & 3) + 4 h + i, i < 4
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = 4 * (w & 3) + i;
+      float gs = 0.f, us = 0.f;
+#pragma unroll
+      for (int bq = 0; bq < 4; ++bq) {
+        gs += *red_at(bq, ms, 0, j);
+        us += *red_at(bq, ms, 1, j);
+      }
+      const int m = m0 + 32 * ms + 8 * (j >> 2) + 4 * h + (j & 3);
+      if (m >= a.M) continue;
+      if constexpr (HOT) {
+        const float hv = ok[sb] ? gated_act(fmaf(gs, sg[sb], gb[sb]), us * su[sb], a.relu, a.both) : 0.f;
+        a.hh[(size_t)m * a.ldh + n0 + 32 * sb + col] = float_to_half_bits(hv);
+      } else {
+        const float hv = ok[sb] ? gated_act(gs + gb[sb], us, a.relu, a.both) : 0.f;
+        a.hc[(size_t)m * a.ldc + n0 + 32 * sb + col] = float_to_half_bits(hv);
+      }
     }
   }
 }
 
-// Grid: (hot tiles + cold tiles, rounded up to 8) x token tiles, the token
-// tiles of one weight tile on one XCD (workgroups go round-robin over the 8
-// XCDs), sharing its L2 for the weights.
-__global__ __launch_bounds__(kMupThreads) void k_mup(BUpArgs a, int hot_tiles, int n_tiles, int mt) {
+// Tiles: the hot rows' 32-neuron units, then the dense list's, each side's
+// first `wide_*` tiles two units wide.  Grid: tiles rounded up to 8, x token
+// tiles, the token tiles of one weight tile on one XCD (workgroups go
+// round-robin over the 8 XCDs), sharing its L2 for the weights.
+// (WIDE = false: no wide tile, and the narrow tile's registers allow two
+// workgroups per CU.)
+struct MupTiles {
+  int hot_units, wide_hot, wide_cold, n_tiles;
+};
+template <bool WIDE>
+__global__ __launch_bounds__(kMupThreads) void k_mup(BUpArgs a, MupTiles mtl, int mt) {
   __shared__ __attribute__((aligned(16))) uint8_t smem[kMupLds];
   const int b = blockIdx.x;
   const int q = b >> 3;
   const int nt = (q / mt) * 8 + (b & 7), mtile = q % mt;
-  if (nt >= n_tiles) return;   // the whole workgroup
+  if (nt >= mtl.n_tiles) return;   // the whole workgroup
   const int m0 = mtile * 64;
+  const int hot_tiles = mtl.hot_units - mtl.wide_hot;
   if (nt < hot_tiles) {
-    mup_tile<true>(a, nt, m0, 0, 0, smem);
+    if (WIDE && nt < mtl.wide_hot)
+      mup_tile<true, WIDE ? 2 : 1>(a, 64 * nt, m0, 0, smem);
+    else
+      mup_tile<true, 1>(a, kMupN * (nt + mtl.wide_hot), m0, 0, smem);
     return;
   }
   const int total = min(*a.total, a.cap);
-  const int i0 = (nt - hot_tiles) * kMupN;
+  const int c = nt - hot_tiles;
+  const int i0 = c < mtl.wide_cold ? 64 * c : kMupN * (c + mtl.wide_cold);
   if (i0 >= total) return;   // the whole workgroup
-  mup_tile<false>(a, nt - hot_tiles, m0, total, i0, smem);
+  if (WIDE && c < mtl.wide_cold)
+    mup_tile<false, WIDE ? 2 : 1>(a, i0, m0, total, smem);
+  else
+    mup_tile<false, 1>(a, i0, m0, total, smem);
 }
 
 // Hot down for 32 MS tokens x 128 NB outputs (4 waves x 32 NB) over the K
@@ -1507,6 +1559,33 @@ static BatchPlan batch_plan(int M, int n_hot, int cap) {
   return p;
 }
 
+// The current device's CU count (cached per device).
+static int device_cus() {
+  static int cache[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int c = 0;
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+    cache[dev] = c;
+  }
+  return cache[dev];
+}
+
+// k_mup's tiles: one token tile with more 32-neuron units than CUs makes just
+// enough tiles two units wide (list items first) to run them all in one
+// round; up to twice the CU count.
+static MupTiles mup_tiles(const BatchPlan& p) {
+  MupTiles m{};
+  m.hot_units = p.ldh / kMupN;
+  const int cold_units = p.ldc / kMupN, units = m.hot_units + cold_units;
+  const int wide = p.pmt == 1 ? std::min(std::max(0, units - device_cus()), units / 2) : 0;
+  m.wide_cold = std::min(wide, cold_units / 2);
+  m.wide_hot = std::min(wide - m.wide_cold, m.hot_units / 2);
+  m.n_tiles = units - m.wide_hot - m.wide_cold;
+  return m;
+}
+
 size_t batch_ws_bytes(int M, int n_hot, int cap) { return batch_plan(M, n_hot, cap).bytes; }
 
 static void launch_skinny(const BUpArgs& ua, const BDownArgs& da, bool up, const uint16_t* x,
@@ -1651,9 +1730,12 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
       else
         hipLaunchKernelGGL(k_pgemm_up<2>, grid, dim3(kThreads), 0, st, ua, hot_tiles, n_tiles, p.pmt);
     } else {
-      const int hot_tiles = p.ldh / kMupN, n_tiles = hot_tiles + p.ldc / kMupN;
-      hipLaunchKernelGGL(k_mup, dim3((n_tiles + 7) / 8 * 8 * p.pmt), dim3(kMupThreads), 0, st, ua, hot_tiles,
-                         n_tiles, p.pmt);
+      const MupTiles mtl = mup_tiles(p);
+      const dim3 grid((mtl.n_tiles + 7) / 8 * 8 * p.pmt);
+      if (mtl.wide_hot + mtl.wide_cold > 0)
+        hipLaunchKernelGGL(k_mup<true>, grid, dim3(kMupThreads), 0, st, ua, mtl, p.pmt);
+      else
+        hipLaunchKernelGGL(k_mup<false>, grid, dim3(kMupThreads), 0, st, ua, mtl, p.pmt);
     }
     OI2_CHECK_LAUNCH();
   }

@@ -63,6 +63,37 @@ def test_batch_decode_shared_active_set(dev, layer25, B):
                      what="batch row vs single token")
 
 
+@pytest.mark.parametrize("B,frac", [(64, 0.5), (40, 1.0), (33, 0.47)])
+def test_batch_wide_tiles(dev, layer25, B, frac):
+    """At most 64 tokens with more 32-neuron units than the GPU has CUs: part
+    of the gate/up tiles are two units wide (list items at 0.5 and 0.47, the
+    last tile part full at 0.47; every item and some hot rows at 1.0).  Rows
+    against the float64 oracle, every row against float32 torch over the same
+    dequantised weights."""
+    lay, g = layer25
+    n_cold = lay.records.shape[0]
+    slots = torch.randperm(n_cold, generator=g, device=dev)[: int(frac * n_cold)].int()
+    cold = ColdNeurons.from_slots(_section(lay), slots)
+    x = torch.randn((B, H), generator=g, device=dev).half()
+    _, y32 = _ffn(x, lay.norm_w, EPS, lay.hot, cold, "silu", False, False, want_y32=True)
+    torch.cuda.synchronize()
+    xn = normed_f16(x, lay.norm_w)
+    Gh, Uh, Dh = hot_dense(lay.hot)
+    Gc, Uc, Dc = cold_dense(lay.records, slots)
+    rows = sorted({0, 1, 31, 32, B // 2, B - 1})
+    ref = O.sparse_ffn(xn[rows], "silu", False, Gh, Uh, Dh, Gc, Uc, Dc)
+    y = y32.cpu().numpy()
+    for k, r in enumerate(rows):
+        assert_ffn_close(y[r], ref[k], what=f"B={B} frac={frac} row {r}")
+    f32 = lambda a: torch.as_tensor(a, dtype=torch.float32, device=dev)
+    xa = f32(xn)
+    silu = torch.nn.functional.silu
+    hh = silu(xa @ f32(Gh).T) * (xa @ f32(Uh).T)
+    hc = silu(xa @ f32(Gc).T) * (xa @ f32(Uc).T)
+    ref_all = (hh @ f32(Dh).T + hc @ f32(Dc).T).double().cpu().numpy()
+    assert_ffn_close(y, ref_all, what=f"B={B} frac={frac} all rows")
+
+
 @pytest.fixture(scope="module")
 def drelu_layer(dev):
     """Config 2's layer: dReLU at 4096 x 14336, 25 % hot, gate pre-activation
