@@ -1057,17 +1057,27 @@ __global__ __launch_bounds__(kThreads) void k_dequant(const uint8_t* records, in
   }
 }
 
+// One row per workgroup; thread t holds elements 16 t .. 16 t + 15 of the row
+// and of the weight (both loaded up front), and writes its 16 outputs as two
+// 16-byte stores.
 __global__ __launch_bounds__(kThreads) void k_rmsnorm(const uint16_t* x, const uint16_t* w,
                                                       float eps, uint16_t* out) {
   __shared__ float s_parts[kThreads];
   const uint16_t* xr = x + (size_t)blockIdx.x * kH;
-  const float r = block_rnorm(xr, eps, s_parts);
   float v[16], wv[16];
   load_h16(xr, 16 * threadIdx.x, v);
   load_h16(w, 16 * threadIdx.x, wv);
-  uint16_t* o = out + (size_t)blockIdx.x * kH + 16 * threadIdx.x;
+  s_parts[threadIdx.x] = ssq16(v);
+  __syncthreads();
+  const float r = r_from_parts(s_parts, eps);
+  u32x4 o[2];
 #pragma unroll
-  for (int e = 0; e < 16; ++e) o[e] = float_to_half_bits(xn_exact(v[e], r, wv[e]));
+  for (int e = 0; e < 16; e += 2)
+    o[e >> 3][(e & 7) >> 1] = (uint32_t)float_to_half_bits(xn_exact(v[e], r, wv[e])) |
+                              ((uint32_t)float_to_half_bits(xn_exact(v[e + 1], r, wv[e + 1])) << 16);
+  u32x4* dst = reinterpret_cast<u32x4*>(out + (size_t)blockIdx.x * kH + 16 * threadIdx.x);
+  dst[0] = o[0];
+  dst[1] = o[1];
 }
 
 // Query for batch > 1 (engine.py:277): mean over rows of RMSNorm(x), fp16
