@@ -696,21 +696,13 @@ __global__ __launch_bounds__(kMupThreads) void k_mup(BUpArgs a, MupTiles mtl, in
 // LDS reads per MFMA.  The K blocks are loaded D ahead into D register sets
 // (a range of a few blocks at 17-191 tokens is otherwise one load latency
 // per block).
+// Hot down main loop: acc += the token rows m0 .. of H_hot over K blocks
+// [kb0, kb1) times the down rows of output tile nt (unscaled).
 template <int MS, int NB, int D>
-__global__ __launch_bounds__(kThreads) void k_pgemm_down_hot(BDownArgs a, int mt, int splits) {
+__device__ __forceinline__ void hot_down_blocks(const BDownArgs& a, int nt, int m0, int kb0, int kb1,
+                                                f32x16 (&acc)[MS][NB], uint16_t* sA, uint8_t* sB) {
   constexpr int kAbuf = 32 * MS * kLdA;
   constexpr int kBbuf = 128 * NB * kLdB8;
-  constexpr int kTiles = kH / (128 * NB);
-  __shared__ __attribute__((aligned(16))) uint16_t sA[2 * kAbuf];
-  __shared__ __attribute__((aligned(16))) uint8_t sB[2 * kBbuf];
-  const int b = blockIdx.x;
-  const int q = b >> 3, per = mt * splits;
-  const int nt = (q / per) * 8 + (b & 7), rem = q % per;
-  if (nt >= kTiles) return;   // the whole workgroup
-  const int mtile = rem % mt, split = rem / mt;
-  const int kb0 = split * a.hot_blocks / splits, kb1 = (split + 1) * a.hot_blocks / splits;
-  if (kb0 >= kb1) return;
-  const int m0 = mtile * 32 * MS;
   const int t = threadIdx.x, w = t >> 6, l = lane_id();
   const ARows<MS> arows(a.hh, a.ldh, a.M, m0);
   const rsrc_t rd = buf_rsrc(a.down_q, (uint32_t)kH * a.down_stride);
@@ -718,11 +710,6 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_down_hot(BDownArgs a, int mt
 #pragma unroll
   for (int i = 0; i < 4 * NB; ++i)
     voff[i] = (uint32_t)(nt * 128 * NB + (t >> 3) + 32 * i) * a.down_stride + 16 * (t & 7);
-  f32x16 acc[MS][NB];
-#pragma unroll
-  for (int ms = 0; ms < MS; ++ms)
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) acc[ms][nb] = f32x16{};
   struct Stage {
     u32x4 ra[2 * MS], rb[4 * NB];
     bool in;   // the block's chunk lies inside the row stride
@@ -764,6 +751,30 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_down_hot(BDownArgs a, int mt
       lds_barrier();
     }
   }
+}
+
+template <int MS, int NB, int D>
+__global__ __launch_bounds__(kThreads) void k_pgemm_down_hot(BDownArgs a, int mt, int splits) {
+  constexpr int kAbuf = 32 * MS * kLdA;
+  constexpr int kBbuf = 128 * NB * kLdB8;
+  constexpr int kTiles = kH / (128 * NB);
+  __shared__ __attribute__((aligned(16))) uint16_t sA[2 * kAbuf];
+  __shared__ __attribute__((aligned(16))) uint8_t sB[2 * kBbuf];
+  const int b = blockIdx.x;
+  const int q = b >> 3, per = mt * splits;
+  const int nt = (q / per) * 8 + (b & 7), rem = q % per;
+  if (nt >= kTiles) return;   // the whole workgroup
+  const int mtile = rem % mt, split = rem / mt;
+  const int kb0 = split * a.hot_blocks / splits, kb1 = (split + 1) * a.hot_blocks / splits;
+  if (kb0 >= kb1) return;
+  const int m0 = mtile * 32 * MS;
+  const int w = threadIdx.x >> 6, l = lane_id();
+  f32x16 acc[MS][NB];
+#pragma unroll
+  for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[ms][nb] = f32x16{};
+  hot_down_blocks<MS, NB, D>(a, nt, m0, kb0, kb1, acc, sA, sB);
   // this range's partial sum of y (rows past M dropped by the store's range;
   // no element takes a branch)
   const rsrc_t ry = buf_rsrc(a.y + (size_t)split * a.M * kH, (uint32_t)a.M * kH * 4);
@@ -822,40 +833,17 @@ __device__ __forceinline__ void nibble_transpose8(uint32_t (&r)[8]) {
 // Workgroup = 256 outputs x 32 MS tokens x one range of K blocks (items).
 // PART (at most 16 tokens): the range's sum goes to a.part[split] as
 // (H, 16) fp32, an empty range storing zeros; otherwise it is added into y.
-template <int MS, bool PART>
-__global__ __launch_bounds__(kThreads) void k_pgemm_down_cold(BDownArgs a, int mt, int splits) {
+// Cold down main loop: acc += the token rows m0 .. of H_cold over the dense
+// list's K blocks [kb0, kb1) (64 items each) times the items' down columns
+// for outputs j0 .. j0 + 255.  Wave w multiplies outputs j0 + 64 w + 32 nb
+// (+ lane), or with HOTMAP j0 + 128 nb + 32 w, the hot down's layout.
+template <int MS, bool HOTMAP>
+__device__ __forceinline__ void cold_down_blocks(const BDownArgs& a, int j0, int m0, int total, int kb0, int kb1,
+                                                 f32x16 (&acc)[MS][2], uint16_t* sT, uint16_t* sH,
+                                                 uint32_t* s_rec, uint16_t* s_sc) {
   constexpr int NB = 2;
   constexpr int kT = 256 * kLdC, kA = 32 * MS * kLdC;   // halves per buffer
-  static_assert(!PART || MS == 1, "partial sums hold 16 tokens");
-  __shared__ __attribute__((aligned(16))) uint16_t sT[2 * kT];
-  __shared__ __attribute__((aligned(16))) uint16_t sH[2 * kA];
-  __shared__ uint32_t s_rec[kDcMaxItems];
-  __shared__ __attribute__((aligned(16))) uint16_t s_sc[4 * kDcItems];   // per wave: the block's item scales
-  const int b = blockIdx.x;
-  const int q = b >> 3, per = mt * splits;
-  const int jt = (q / per) * 8 + (b & 7), rem = q % per;
-  if (jt >= kH / 256) return;   // the whole workgroup
-  const int mtile = rem % mt, split = rem / mt;
-  const int total = min(*a.total, a.cap);
-  const int n_blk = (total + kDcItems - 1) / kDcItems;
-  const int kb0 = split * n_blk / splits, kb1 = (split + 1) * n_blk / splits;
   const int t = threadIdx.x, w = t >> 6, l = lane_id();
-  const int m0 = mtile * 32 * MS, j0 = jt * 256;
-  // (from 17 tokens) this range's partial sum of y, rows past M dropped
-  const rsrc_t ry = buf_rsrc(PART ? nullptr : a.y + (size_t)(a.cold_split0 + split) * a.M * kH,
-                             PART ? 0u : (uint32_t)a.M * kH * 4);
-  if (kb0 >= kb1) {   // the whole workgroup: an empty range sums to zero
-    if (PART) {
-      f32x4* dst = reinterpret_cast<f32x4*>(a.part + ((size_t)split * kH + j0 + t) * 16);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) dst[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-    } else {
-      for (int i = t; i < 32 * MS * 64; i += kThreads)
-        __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, ry,
-                                                ((uint32_t)(m0 + (i >> 6)) * kH + j0 + 4 * (i & 63)) * 4, 0, 0);
-    }
-    return;
-  }
   const int i_base = kb0 * kDcItems, n_items = (kb1 - kb0) * kDcItems;
 
   // record offsets of the range (items past the list or with invalid slots
@@ -947,11 +935,6 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_down_cold(BDownArgs a, int m
     }
   };
 
-  f32x16 acc[MS][NB];
-#pragma unroll
-  for (int ms = 0; ms < MS; ++ms)
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) acc[ms][nb] = f32x16{};
   // blocks are loaded two ahead: block kb + 2's loads go out while block kb
   // is multiplied and block kb + 1 (loaded an iteration earlier) is decoded
   auto mma_block = [&](int cur) {
@@ -963,7 +946,7 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_down_cold(BDownArgs a, int m
       h8 bf[NB], av[MS];
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb)
-        bf[nb] = *reinterpret_cast<const h8*>(T + (64 * w + 32 * nb + (l & 31)) * kLdC + col);
+        bf[nb] = *reinterpret_cast<const h8*>(T + ((HOTMAP ? 128 * nb + 32 * w : 64 * w + 32 * nb) + (l & 31)) * kLdC + col);
 #pragma unroll
       for (int ms = 0; ms < MS; ++ms) av[ms] = *reinterpret_cast<const h8*>(Hs + (32 * ms + (l & 31)) * kLdC + col);
 #pragma unroll
@@ -994,6 +977,48 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_down_cold(BDownArgs a, int m
     store_block(0, B0);
     lds_barrier();
   }
+}
+
+template <int MS, bool PART>
+__global__ __launch_bounds__(kThreads) void k_pgemm_down_cold(BDownArgs a, int mt, int splits) {
+  constexpr int NB = 2;
+  constexpr int kT = 256 * kLdC, kA = 32 * MS * kLdC;   // halves per buffer
+  static_assert(!PART || MS == 1, "partial sums hold 16 tokens");
+  __shared__ __attribute__((aligned(16))) uint16_t sT[2 * kT];
+  __shared__ __attribute__((aligned(16))) uint16_t sH[2 * kA];
+  __shared__ uint32_t s_rec[kDcMaxItems];
+  __shared__ __attribute__((aligned(16))) uint16_t s_sc[4 * kDcItems];   // per wave: the block's item scales
+  const int b = blockIdx.x;
+  const int q = b >> 3, per = mt * splits;
+  const int jt = (q / per) * 8 + (b & 7), rem = q % per;
+  if (jt >= kH / 256) return;   // the whole workgroup
+  const int mtile = rem % mt, split = rem / mt;
+  const int total = min(*a.total, a.cap);
+  const int n_blk = (total + kDcItems - 1) / kDcItems;
+  const int kb0 = split * n_blk / splits, kb1 = (split + 1) * n_blk / splits;
+  const int t = threadIdx.x, w = t >> 6, l = lane_id();
+  const int m0 = mtile * 32 * MS, j0 = jt * 256;
+  // (from 17 tokens) this range's partial sum of y, rows past M dropped
+  const rsrc_t ry = buf_rsrc(PART ? nullptr : a.y + (size_t)(a.cold_split0 + split) * a.M * kH,
+                             PART ? 0u : (uint32_t)a.M * kH * 4);
+  if (kb0 >= kb1) {   // the whole workgroup: an empty range sums to zero
+    if (PART) {
+      f32x4* dst = reinterpret_cast<f32x4*>(a.part + ((size_t)split * kH + j0 + t) * 16);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dst[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    } else {
+      for (int i = t; i < 32 * MS * 64; i += kThreads)
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, ry,
+                                                ((uint32_t)(m0 + (i >> 6)) * kH + j0 + 4 * (i & 63)) * 4, 0, 0);
+    }
+    return;
+  }
+  f32x16 acc[MS][NB];
+#pragma unroll
+  for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[ms][nb] = f32x16{};
+  cold_down_blocks<MS, false>(a, j0, m0, total, kb0, kb1, acc, sT, sH, s_rec, s_sc);
   if (PART) {
     // rows 0..15 of the 32x32 tile: elements 0..7, four consecutive rows each
 #pragma unroll
@@ -1016,6 +1041,65 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_down_cold(BDownArgs a, int m
         __builtin_amdgcn_raw_buffer_store_b32(as_u32(acc[ms][nb][e]), ry,
                                               ((uint32_t)m * kH + j0 + 64 * w + 32 * nb + (l & 31)) * 4, 0, 0);
       }
+}
+
+// Prefill on 128-token tiles: the hot and the cold down of one 256-output
+// tile in one workgroup, over range `split` of the hot K blocks and range
+// `split` of the list's K blocks, so each range stores one partial sum (the
+// final add reads half as many).  The hot sums take their row scales before
+// the cold sums join them; the two loops share the LDS.
+__global__ __launch_bounds__(kThreads) void k_pgemm_down_both(BDownArgs a, int mt, int splits) {
+  constexpr int MS = 4, NB = 2;
+  constexpr int kHotA = 2 * 32 * MS * kLdA * 2, kHotLds = kHotA + 2 * 128 * NB * kLdB8;   // bytes
+  constexpr int kColdT = 2 * 256 * kLdC * 2, kColdH = 2 * 32 * MS * kLdC * 2;
+  constexpr int kColdLds = kColdT + kColdH + kDcMaxItems * 4 + 4 * kDcItems * 2;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kHotLds > kColdLds ? kHotLds : kColdLds];
+  const int b = blockIdx.x;
+  const int q = b >> 3, per = mt * splits;
+  const int jt = (q / per) * 8 + (b & 7), rem = q % per;
+  if (jt >= kH / 256) return;   // the whole workgroup
+  const int mtile = rem % mt, split = rem / mt;
+  const int m0 = mtile * 32 * MS, j0 = jt * 256;
+  const int w = threadIdx.x >> 6, l = lane_id();
+  const int hb0 = split * a.hot_blocks / splits, hb1 = (split + 1) * a.hot_blocks / splits;
+  const int total = min(*a.total, a.cap);
+  const int n_blk = (total + kDcItems - 1) / kDcItems;
+  const int cb0 = split * n_blk / splits, cb1 = (split + 1) * n_blk / splits;
+  f32x16 acc[MS][NB];
+#pragma unroll
+  for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[ms][nb] = f32x16{};
+  if (hb0 < hb1) {   // workgroup-uniform
+    hot_down_blocks<MS, NB, 1>(a, jt, m0, hb0, hb1, acc, reinterpret_cast<uint16_t*>(smem), smem + kHotA);
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const float sd = a.down_s[j0 + 128 * nb + 32 * w + (l & 31)];
+#pragma unroll
+      for (int ms = 0; ms < MS; ++ms) acc[ms][nb] *= sd;
+    }
+    __syncthreads();   // every wave is done with the hot blocks' LDS
+  }
+  if (cb0 < cb1) {
+    uint16_t* sT = reinterpret_cast<uint16_t*>(smem);
+    uint16_t* sH = reinterpret_cast<uint16_t*>(smem + kColdT);
+    uint32_t* s_rec = reinterpret_cast<uint32_t*>(smem + kColdT + kColdH);
+    uint16_t* s_sc = reinterpret_cast<uint16_t*>(smem + kColdT + kColdH + kDcMaxItems * 4);
+    cold_down_blocks<MS, true>(a, j0, m0, total, cb0, cb1, acc, sT, sH, s_rec, s_sc);
+  }
+  // this range's partial sum of y (rows past M dropped by the store's range)
+  const rsrc_t ry = buf_rsrc(a.y + (size_t)split * a.M * kH, (uint32_t)a.M * kH * 4);
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int row = j0 + 128 * nb + 32 * w + (l & 31);
+#pragma unroll
+    for (int ms = 0; ms < MS; ++ms)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int m = m0 + 32 * ms + 8 * (e >> 2) + 4 * (l >> 5) + (e & 3);
+        __builtin_amdgcn_raw_buffer_store_b32(as_u32(acc[ms][nb][e]), ry, ((uint32_t)m * kH + row) * 4, 0, 0);
+      }
+  }
 }
 
 // ── gate/up for at most 16 tokens, RMSNorm fused ─────────────────────────────
@@ -1738,6 +1822,16 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
         hipLaunchKernelGGL(k_mup<false>, grid, dim3(kMupThreads), 0, st, ua, mtl, p.pmt);
     }
     OI2_CHECK_LAUNCH();
+  }
+  if (p.prefill && p.pms == 4 && n_hot && has_cold) {
+    // one launch for both downs: one partial sum per range
+    const int splits = std::max(p.hot_splits, cold_splits);
+    hipLaunchKernelGGL(k_pgemm_down_both, dim3(16 * p.pmt * splits), dim3(kThreads), 0, st, da, p.pmt, splits);
+    OI2_CHECK_LAUNCH();
+    hipLaunchKernelGGL(k_bfinal, dim3(grid), dim3(kThreads), 0, st, y, splits, nullptr, 0, M,
+                       add_residual ? x : nullptr, out, y32);
+    OI2_CHECK_LAUNCH();
+    return OI2_OK;
   }
   if (n_hot) {
     const dim3 grid(hot_down_tiles(p.pms) * p.pmt * p.hot_splits);
