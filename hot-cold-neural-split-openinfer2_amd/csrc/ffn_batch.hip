@@ -1043,13 +1043,14 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_down_cold(BDownArgs a, int m
       }
 }
 
-// Prefill on 128-token tiles: the hot and the cold down of one 256-output
-// tile in one workgroup, over range `split` of the hot K blocks and range
-// `split` of the list's K blocks, so each range stores one partial sum (the
-// final add reads half as many).  The hot sums take their row scales before
-// the cold sums join them; the two loops share the LDS.
+// The hot and the cold down of one 32 MS-token x 256-output tile in one
+// workgroup, over range `split` of the hot K blocks and range `split` of the
+// list's K blocks, so each range stores one partial sum (the final add reads
+// fewer).  The hot sums take their row scales before the cold sums join
+// them; the two loops share the LDS.  D: the hot blocks loaded ahead.
+template <int MS, int D>
 __global__ __launch_bounds__(kThreads) void k_pgemm_down_both(BDownArgs a, int mt, int splits) {
-  constexpr int MS = 4, NB = 2;
+  constexpr int NB = 2;
   constexpr int kHotA = 2 * 32 * MS * kLdA * 2, kHotLds = kHotA + 2 * 128 * NB * kLdB8;   // bytes
   constexpr int kColdT = 2 * 256 * kLdC * 2, kColdH = 2 * 32 * MS * kLdC * 2;
   constexpr int kColdLds = kColdT + kColdH + kDcMaxItems * 4 + 4 * kDcItems * 2;
@@ -1071,7 +1072,7 @@ __global__ __launch_bounds__(kThreads) void k_pgemm_down_both(BDownArgs a, int m
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) acc[ms][nb] = f32x16{};
   if (hb0 < hb1) {   // workgroup-uniform
-    hot_down_blocks<MS, NB, 1>(a, jt, m0, hb0, hb1, acc, reinterpret_cast<uint16_t*>(smem), smem + kHotA);
+    hot_down_blocks<MS, NB, D>(a, jt, m0, hb0, hb1, acc, reinterpret_cast<uint16_t*>(smem), smem + kHotA);
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
       const float sd = a.down_s[j0 + 128 * nb + 32 * w + (l & 31)];
@@ -1577,6 +1578,7 @@ struct BatchPlan {
   bool prefill;
   int pms, pmt;   // prefill tiles: 32-token subtiles per tile, token tiles
   int cold_splits;   // at most 16 tokens: the cold down's item ranges
+  int both_splits;   // from 17 tokens with both halves: the joint down's ranges (0: separate downs)
   size_t off_xn, off_hh, off_hc, off_dslots, off_total, off_y, off_part, bytes;
 };
 
@@ -1633,8 +1635,17 @@ static BatchPlan batch_plan(int M, int n_hot, int cap) {
   o = align256(o + 16);
   p.off_y = o;
   // up to 16 tokens: y (M, H); from 17: one (M, H) partial sum per down range
+  // (separate hot and cold downs, or the ranges of the joint one)
+  p.both_splits = 0;
+  if (M > kSkinnyMax && n_hot > 0 && cap > 0) {
+    if (p.pms == 4)
+      p.both_splits = std::max(p.hot_splits, cold_down_splits(M, cap));
+    else if (!p.prefill)
+      p.both_splits = std::max(cold_down_splits(M, cap), std::min(p.hot_blocks, 256 / (16 * p.pmt)));
+  }
   const int y_parts = M <= kSkinnyMax ? 1
-                                      : (n_hot > 0 ? p.hot_splits : 0) + (cap > 0 ? cold_down_splits(M, cap) : 0);
+                                      : std::max(p.both_splits, (n_hot > 0 ? p.hot_splits : 0) +
+                                                                    (cap > 0 ? cold_down_splits(M, cap) : 0));
   o = align256(o + (size_t)std::max(1, y_parts) * M * kH * 4);
   p.cold_splits = (M <= kSkinnyMax && cap > 0) ? cold_down_splits(M, cap) : 0;
   p.off_part = o;
@@ -1823,10 +1834,22 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
     }
     OI2_CHECK_LAUNCH();
   }
-  if (p.prefill && p.pms == 4 && n_hot && has_cold) {
-    // one launch for both downs: one partial sum per range
-    const int splits = std::max(p.hot_splits, cold_splits);
-    hipLaunchKernelGGL(k_pgemm_down_both, dim3(16 * p.pmt * splits), dim3(kThreads), 0, st, da, p.pmt, splits);
+  if (p.pms == 4 && n_hot && has_cold && p.both_splits > 0) {
+    // one launch for both downs (128-token tiles): one partial sum per range
+    const int splits = p.both_splits;
+    hipLaunchKernelGGL((k_pgemm_down_both<4, 1>), dim3(16 * p.pmt * splits), dim3(kThreads), 0, st, da, p.pmt,
+                       splits);
+    OI2_CHECK_LAUNCH();
+    hipLaunchKernelGGL(k_bfinal, dim3(grid), dim3(kThreads), 0, st, y, splits, nullptr, 0, M,
+                       add_residual ? x : nullptr, out, y32);
+    OI2_CHECK_LAUNCH();
+    return OI2_OK;
+  }
+  if (!p.prefill && n_hot && has_cold && p.both_splits > 0) {
+    // the same on 64-token tiles
+    const int splits = p.both_splits;
+    hipLaunchKernelGGL((k_pgemm_down_both<2, 2>), dim3(16 * p.pmt * splits), dim3(kThreads), 0, st, da, p.pmt,
+                       splits);
     OI2_CHECK_LAUNCH();
     hipLaunchKernelGGL(k_bfinal, dim3(grid), dim3(kThreads), 0, st, y, splits, nullptr, 0, M,
                        add_residual ? x : nullptr, out, y32);
