@@ -12,14 +12,17 @@
 //   down     Y (M, H) fp32
 //            hot  H_hot D_hot^T (fp8 rows, row scale): k_bdown_hot_s,
 //                 k_pgemm_down_hot
-//            cold H_cold D_cold: k_pgemm_down_cold for every M, the records'
-//                 down nibbles transposed into a decoded LDS tile
+//            cold H_cold D_cold: k_pgemm_down_cold, the records' down
+//                 nibbles transposed into a decoded LDS tile
+//            both halves from 17 tokens (17-191 and from 384):
+//                 k_pgemm_down_both, one workgroup per output tile and K
+//                 range of each half
 //   k_bfinal out = x + Y (fp16), y32 = Y
 // Up to 16 tokens, the cold down stores one partial sum per item range and
-// the last kernel (k_bdown_hot_s, or k_bfinal without hot rows) adds them in
-// range order to the hot product.  With more tokens every down workgroup
-// stores its K range's partial sum of its output tile (hot ranges, then
-// cold), and k_bfinal adds them in range order.  No path uses atomics, so the
+// the last kernel (k_bdown_hot_s, or k_bfinal16 without hot rows) adds them
+// in range order to the hot product.  With more tokens every down workgroup
+// stores its K range's partial sum of its output tile, and k_bfinal adds
+// them in range order.  No path uses atomics, so the
 // result is the same on every run.  (fp32 atomics into one Y cost the 512-
 // token cold down 65 against 44 us, the 64-token one 28 against 18 us.)
 // fp8 and INT4 weights convert to fp16 exactly.  The small-batch gate/up
@@ -1509,23 +1512,14 @@ __global__ __launch_bounds__(kThreads) void k_bfill(float* y, int n4) {
     reinterpret_cast<f32x4*>(y)[q] = f32x4{0.f, 0.f, 0.f, 0.f};
 }
 
-// out = res + y (fp16), y32 = y.
-// Y the sum in order of the n_ys partial sums ys[s] (M, H), or, with
-// n_part > 0, the sum in range order of the cold ranges' partial sums
-// part[s] (H, 16).  Either way the result is the same on every run.
-__global__ __launch_bounds__(kThreads) void k_bfinal(const float* ys, int n_ys, const float* part, int n_part,
-                                                    int M, const uint16_t* res, uint16_t* out, float* y32) {
+// out = res + y (fp16), y32 = y; y the sum in order of the n_ys partial sums
+// ys[s] (M, H), the same on every run.
+__global__ __launch_bounds__(kThreads) void k_bfinal(const float* ys, int n_ys, int M, const uint16_t* res,
+                                                    uint16_t* out, float* y32) {
   const int n4 = M * (kH / 4);
   for (int q = blockIdx.x * kThreads + threadIdx.x; q < n4; q += gridDim.x * kThreads) {
     f32x4 y = {0.f, 0.f, 0.f, 0.f};
-    if (n_part > 0) {
-      const int m = q / (kH / 4), j = 4 * (q % (kH / 4));
-      for (int sp = 0; sp < n_part; ++sp) {
-        const float* pp = part + ((size_t)sp * kH + j) * 16 + m;
-#pragma unroll
-        for (int c = 0; c < 4; ++c) y[c] += pp[16 * c];
-      }
-    } else {
+    {
       // four partial sums in flight per pass, added in range order
       const f32x4* yp = reinterpret_cast<const f32x4*>(ys) + q;
       int sp = 0;
@@ -1553,6 +1547,38 @@ __global__ __launch_bounds__(kThreads) void k_bfinal(const float* ys, int n_ys, 
       const uint32_t hi = (uint32_t)float_to_half_bits(r[2] + y.z) |
                           ((uint32_t)float_to_half_bits(r[3] + y.w) << 16);
       reinterpret_cast<uint2*>(out)[q] = make_uint2(lo, hi);
+    }
+  }
+}
+
+// Up to 16 tokens without hot rows: out = res + y (fp16), y32 = y, y the sum
+// in range order of the cold ranges' partial sums part[s] (H, 16).  Thread t takes output column
+// t / 4 and rows 4 (t & 3) .. + 3: the four threads of a column read its 64
+// bytes of each partial together.
+__global__ __launch_bounds__(kThreads) void k_bfinal16(const float* part, int n_part, int M, const uint16_t* res,
+                                                      uint16_t* out, float* y32) {
+  const int q = blockIdx.x * kThreads + threadIdx.x;
+  const int j = q >> 2, m0 = 4 * (q & 3);
+  if (j >= kH) return;
+  f32x4 y = {0.f, 0.f, 0.f, 0.f};
+  const f32x4* pp = reinterpret_cast<const f32x4*>(part + (size_t)j * 16 + m0);
+  int sp = 0;
+  for (; sp + 4 <= n_part; sp += 4) {
+    f32x4 v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) v[k] = pp[(size_t)(sp + k) * kH * 4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) y += v[k];
+  }
+  for (; sp < n_part; ++sp) y += pp[(size_t)sp * kH * 4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = m0 + i;
+    if (m >= M) break;
+    if (y32) y32[(size_t)m * kH + j] = y[i];
+    if (out) {
+      const float r = res ? half_bits_to_float(res[(size_t)m * kH + j]) : 0.f;
+      out[(size_t)m * kH + j] = float_to_half_bits(r + y[i]);
     }
   }
 }
@@ -1801,9 +1827,11 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
       da.out = out;
       da.y32 = y32;
       launch_skinny(ua, da, false, x, norm_w, eps, st);
+    } else if (has_cold) {   // cold only: the final add of the ranges' partial sums
+      hipLaunchKernelGGL(k_bfinal16, dim3(kH * 4 / kThreads), dim3(kThreads), 0, st, part, p.cold_splits, M,
+                         add_residual ? x : nullptr, out, y32);
     } else {
-      hipLaunchKernelGGL(k_bfinal, dim3(grid), dim3(kThreads), 0, st, y, 1, has_cold ? part : nullptr,
-                         has_cold ? p.cold_splits : 0, M, add_residual ? x : nullptr, out, y32);
+      hipLaunchKernelGGL(k_bfinal, dim3(grid), dim3(kThreads), 0, st, y, 1, M, add_residual ? x : nullptr, out, y32);
     }
     OI2_CHECK_LAUNCH();
     return OI2_OK;
@@ -1840,7 +1868,7 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
     hipLaunchKernelGGL((k_pgemm_down_both<4, 1>), dim3(16 * p.pmt * splits), dim3(kThreads), 0, st, da, p.pmt,
                        splits);
     OI2_CHECK_LAUNCH();
-    hipLaunchKernelGGL(k_bfinal, dim3(grid), dim3(kThreads), 0, st, y, splits, nullptr, 0, M,
+    hipLaunchKernelGGL(k_bfinal, dim3(grid), dim3(kThreads), 0, st, y, splits, M,
                        add_residual ? x : nullptr, out, y32);
     OI2_CHECK_LAUNCH();
     return OI2_OK;
@@ -1851,7 +1879,7 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
     hipLaunchKernelGGL((k_pgemm_down_both<2, 2>), dim3(16 * p.pmt * splits), dim3(kThreads), 0, st, da, p.pmt,
                        splits);
     OI2_CHECK_LAUNCH();
-    hipLaunchKernelGGL(k_bfinal, dim3(grid), dim3(kThreads), 0, st, y, splits, nullptr, 0, M,
+    hipLaunchKernelGGL(k_bfinal, dim3(grid), dim3(kThreads), 0, st, y, splits, M,
                        add_residual ? x : nullptr, out, y32);
     OI2_CHECK_LAUNCH();
     return OI2_OK;
@@ -1876,7 +1904,7 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
     }
     OI2_CHECK_LAUNCH();
   }
-  hipLaunchKernelGGL(k_bfinal, dim3(grid), dim3(kThreads), 0, st, y, hot_splits + cold_splits, nullptr, 0, M,
+  hipLaunchKernelGGL(k_bfinal, dim3(grid), dim3(kThreads), 0, st, y, hot_splits + cold_splits, M,
                      add_residual ? x : nullptr, out, y32);
   OI2_CHECK_LAUNCH();
   return OI2_OK;

@@ -63,6 +63,27 @@ def test_batch_decode_shared_active_set(dev, layer25, B):
                      what="batch row vs single token")
 
 
+@pytest.mark.parametrize("B", [3, 8, 16])
+def test_batch_cold_only_small(dev, layer25, B):
+    """Up to 16 tokens with no hot half: the cold down's ranges are added by
+    the final launch, with the residual."""
+    lay, g = layer25
+    n_cold = lay.records.shape[0]
+    slots = torch.randperm(n_cold, generator=g, device=dev)[: int(0.15 * n_cold)].int()
+    cold = ColdNeurons.from_slots(_section(lay), slots)
+    x = torch.randn((B, H), generator=g, device=dev).half()
+    out, y32 = _ffn(x, lay.norm_w, EPS, None, cold, "silu", False, add_residual=True, want_y32=True)
+    torch.cuda.synchronize()
+    xn = normed_f16(x, lay.norm_w)
+    Gc, Uc, Dc = cold_dense(lay.records, slots)
+    ref = O.sparse_ffn(xn, "silu", False, None, None, None, Gc, Uc, Dc)
+    y = y32.cpu().numpy()
+    for r in range(B):
+        assert_ffn_close(y[r], ref[r], what=f"cold only B={B} row {r}")
+    assert_ffn_close(out.float().cpu().numpy(), x.float().cpu().numpy() + ref, tol=2e-3, cos_min=0.99999,
+                     what="cold only residual out")
+
+
 @pytest.mark.parametrize("B,frac", [(64, 0.5), (40, 1.0), (33, 0.47)])
 def test_batch_wide_tiles(dev, layer25, B, frac):
     """At most 64 tokens with more 32-neuron units than the GPU has CUs: part
