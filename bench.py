@@ -678,33 +678,50 @@ def measure_multi_token(layers, dev, M, frac, reps, seed=1):
     x0 = torch.randn((M, H), generator=g, device=dev).half()
     stream = torch.cuda.Stream(device=dev)
 
-    def chain(x):
+    def separate(x):
         for l, c in zip(layers, colds):
             x = _ffn(x, l.norm_w, EPS, l.hot, c, "silu", False, add_residual=True)
         return x
 
-    with torch.cuda.stream(stream):
-        chain(x0)                                   # warm (workspaces, library)
-    stream.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph, stream=stream):
-        y = chain(x0)
-    graph.replay()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(reps):
+    def chained(x):
+        # from 17 tokens each call's final add writes the next layer's
+        # normalised rows (oi2_ffn_forward_chain): one launch fewer per layer
+        xn = None
+        for i, (l, c) in enumerate(zip(layers, colds)):
+            nxt = layers[i + 1].norm_w if i + 1 < len(layers) else None
+            r = _ffn(x, l.norm_w, EPS, l.hot, c, "silu", False, add_residual=True, xn_in=xn, next_norm_w=nxt)
+            x, xn = r if nxt is not None else (r, None)
+        return x
+
+    def timed(chain):
+        with torch.cuda.stream(stream):
+            chain(x0)                                   # warm (workspaces, library)
+        stream.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            y = chain(x0)
         graph.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    us = e0.elapsed_time(e1) * 1e3 / reps
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us_ = e0.elapsed_time(e1) * 1e3 / reps
+        del graph
+        return us_, y
+
+    us_sep, y_sep = timed(separate)
+    us, y = timed(chained) if M > 16 else (us_sep, y_sep)
+    assert torch.equal(y, y_sep), "the chained calls must give the separate calls' bits"
     n_hot = layers[0].hot.n_hot
     n_act = int(frac * (INTER - n_hot))
     flop = N_LAYERS * 2 * M * H * (n_hot + n_act) * 3
     weight_bytes = N_LAYERS * (3 * n_hot * H + n_act * 6400)
     assert torch.isfinite(y.float()).all()
-    del graph
     return {"tokens": M, "active_cold_frac": frac, "us_per_32_layers": us,
+            "separate_calls_us_per_32_layers": us_sep,
             "tok_s": M / (us * 1e-6), "tflops": flop / (us * 1e-6) / 1e12,
             "mfma_frac_fp16_dense": flop / (us * 1e-6) / 2.5e15,
             "weight_gbs": weight_bytes / (us * 1e-6) / 1e9}
@@ -1038,7 +1055,8 @@ def main():
         multi = {}
         for M, frac in ((8, 0.15), (64, 0.50), (512, 0.40), (1024, 0.40)):
             multi[f"m{M}"] = measure_multi_token(layers, dev, M, frac, reps=5)
-            log(f"{M} tokens x 32 layers: {multi[f'm{M}']['us_per_32_layers']:.0f} us")
+            log(f"{M} tokens x 32 layers: {multi[f'm{M}']['us_per_32_layers']:.0f} us "
+                f"(separate calls {multi[f'm{M}']['separate_calls_us_per_32_layers']:.0f} us)")
         print(json.dumps({"multi_token": multi}), flush=True)
         return
     stream = torch.cuda.Stream(device=dev)
@@ -1152,7 +1170,9 @@ def main():
             r["frac_of_fp16_gemm_ref"] = r["tflops"] / multi["fp16_gemm_ref_tflops"]
             multi[f"m{M}"] = r
             log(f"{M} tokens x 32 layers: {r['us_per_32_layers']:.0f} us, "
-                f"{r['tflops']:.1f} TFLOP/s, {r['weight_gbs']:.0f} GB/s")
+                f"{r['tflops']:.1f} TFLOP/s, {r['weight_gbs']:.0f} GB/s"
+                + (f" (chained calls; separate calls {r['separate_calls_us_per_32_layers']:.0f} us)"
+                   if M > 16 else ""))
 
     config1 = config2 = None
     if args.configs and not args.hbm_only:

@@ -1551,6 +1551,66 @@ __global__ __launch_bounds__(kThreads) void k_bfinal(const float* ys, int n_ys, 
   }
 }
 
+// k_bfinal for one row per workgroup that also writes the next layer's
+// normalised rows: xn = RMSNorm(out) with weight w (k_rmsnorm's arithmetic on
+// the fp16 out, so the same bits as a norm launch after the call).  Thread t
+// takes elements 16 t .. 16 t + 15 of row blockIdx.x.
+__global__ __launch_bounds__(kThreads) void k_bfinal_norm(const float* ys, int n_ys, int M, const uint16_t* res,
+                                                         uint16_t* out, float* y32, const uint16_t* w, float eps,
+                                                         uint16_t* xn) {
+  __shared__ float s_parts[kThreads];
+  const int t = threadIdx.x;
+  const size_t e0 = (size_t)blockIdx.x * kH + 16 * t;
+  const size_t stride4 = (size_t)M * kH / 4;
+  const f32x4* yp = reinterpret_cast<const f32x4*>(ys + e0);
+  f32x4 y[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) y[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  u32x4 rv[2] = {u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}};
+  if (res) {
+    rv[0] = reinterpret_cast<const u32x4*>(res + e0)[0];
+    rv[1] = reinterpret_cast<const u32x4*>(res + e0)[1];
+  }
+  float wv[16];
+  load_h16(w, 16 * t, wv);
+  for (int sp = 0; sp < n_ys; ++sp) {   // the partial sums in order, as k_bfinal adds them
+    f32x4 v[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) v[c] = yp[(size_t)sp * stride4 + c];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) y[c] += v[c];
+  }
+  if (y32) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) reinterpret_cast<f32x4*>(y32 + e0)[c] = y[c];
+  }
+  float o[16];
+  u32x4 ob[2];
+#pragma unroll
+  for (int e = 0; e < 16; e += 2) {
+    const uint32_t rr = rv[e >> 3][(e & 7) >> 1];
+    const uint16_t b0 = float_to_half_bits(half_bits_to_float((uint16_t)(rr & 0xFFFFu)) + y[e >> 2][e & 3]);
+    const uint16_t b1 = float_to_half_bits(half_bits_to_float((uint16_t)(rr >> 16)) + y[(e + 1) >> 2][(e + 1) & 3]);
+    ob[e >> 3][(e & 7) >> 1] = (uint32_t)b0 | ((uint32_t)b1 << 16);
+    o[e] = half_bits_to_float(b0);
+    o[e + 1] = half_bits_to_float(b1);
+  }
+  if (out) {
+    reinterpret_cast<u32x4*>(out + e0)[0] = ob[0];
+    reinterpret_cast<u32x4*>(out + e0)[1] = ob[1];
+  }
+  s_parts[t] = ssq16(o);
+  __syncthreads();
+  const float r = r_from_parts(s_parts, eps);
+  u32x4 xv[2];
+#pragma unroll
+  for (int e = 0; e < 16; e += 2)
+    xv[e >> 3][(e & 7) >> 1] = (uint32_t)float_to_half_bits(xn_exact(o[e], r, wv[e])) |
+                               ((uint32_t)float_to_half_bits(xn_exact(o[e + 1], r, wv[e + 1])) << 16);
+  reinterpret_cast<u32x4*>(xn + e0)[0] = xv[0];
+  reinterpret_cast<u32x4*>(xn + e0)[1] = xv[1];
+}
+
 // Up to 16 tokens without hot rows: out = res + y (fp16), y32 = y, y the sum
 // in range order of the cold ranges' partial sums part[s] (H, 16).  Thread t takes output column
 // t / 4 and rows 4 (t & 3) .. + 3: the four threads of a column read its 64
@@ -1721,7 +1781,8 @@ static void launch_skinny(const BUpArgs& ua, const BDownArgs& da, bool up, const
 
 int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const oi2_hot* hot,
               const oi2_cold* cold, const oi2_active* active, int relu, int both, int add_residual,
-              uint16_t* out, float* y32, void* workspace, size_t workspace_bytes, hipStream_t st) {
+              uint16_t* out, float* y32, void* workspace, size_t workspace_bytes, hipStream_t st,
+              const uint16_t* xn_in, const uint16_t* next_w, float next_eps, uint16_t* xn_next) {
   const int n_hot = hot ? hot->n_hot : 0;
   const bool has_cold = cold && active && cold->n_records > 0 && active->n_chunks > 0;
   const int cap = has_cold ? active->n_chunks * active->chunk : 0;
@@ -1738,8 +1799,8 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
   float* y = reinterpret_cast<float*>(ws + p.off_y);
   const bool skinny = M <= kSkinnyMax;
 
-  const uint16_t* xa = x;
-  if (norm_w && !skinny) {   // the skinny gate/up kernel normalises the rows itself
+  const uint16_t* xa = xn_in ? xn_in : x;
+  if (norm_w && !skinny && !xn_in) {   // the skinny gate/up kernel normalises the rows itself
     hipLaunchKernelGGL(k_rmsnorm, dim3(M), dim3(kThreads), 0, st, x, norm_w, eps, xn);
     OI2_CHECK_LAUNCH();
     xa = xn;
@@ -1809,7 +1870,7 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
     const int n4 = M * (kH / 4);
     const int grid = std::min(2048, (n4 + kThreads - 1) / kThreads);
     if (p.ldh + p.ldc > 0) {
-      launch_skinny(ua, da, true, x, norm_w, eps, st);
+      launch_skinny(ua, da, true, xa, xn_in ? nullptr : norm_w, eps, st);
     } else {
       hipLaunchKernelGGL(k_bfill, dim3(grid), dim3(kThreads), 0, st, y, n4);
     }
@@ -1834,11 +1895,24 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
       hipLaunchKernelGGL(k_bfinal, dim3(grid), dim3(kThreads), 0, st, y, 1, M, add_residual ? x : nullptr, out, y32);
     }
     OI2_CHECK_LAUNCH();
+    if (next_w) {   // the next layer's rows (no final launch of its own here to fold them into)
+      hipLaunchKernelGGL(k_rmsnorm, dim3(M), dim3(kThreads), 0, st, out, next_w, next_eps, xn_next);
+      OI2_CHECK_LAUNCH();
+    }
     return OI2_OK;
   }
   const int n4 = M * (kH / 4);
   int grid = (n4 + kThreads - 1) / kThreads;
   grid = grid > 2048 ? 2048 : grid;
+  // the final add of the n_ys partial sums, with the next layer's rows when asked
+  auto final_add = [&](int n_ys) {
+    if (next_w)
+      hipLaunchKernelGGL(k_bfinal_norm, dim3(M), dim3(kThreads), 0, st, y, n_ys, M, add_residual ? x : nullptr,
+                         out, y32, next_w, next_eps, xn_next);
+    else
+      hipLaunchKernelGGL(k_bfinal, dim3(grid), dim3(kThreads), 0, st, y, n_ys, M, add_residual ? x : nullptr, out,
+                         y32);
+  };
   // each down range stores its own partial sum of y (hot ranges, then cold);
   // k_bfinal adds them in that order
   const int hot_splits = n_hot ? p.hot_splits : 0;
@@ -1868,8 +1942,7 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
     hipLaunchKernelGGL((k_pgemm_down_both<4, 1>), dim3(16 * p.pmt * splits), dim3(kThreads), 0, st, da, p.pmt,
                        splits);
     OI2_CHECK_LAUNCH();
-    hipLaunchKernelGGL(k_bfinal, dim3(grid), dim3(kThreads), 0, st, y, splits, M,
-                       add_residual ? x : nullptr, out, y32);
+    final_add(splits);
     OI2_CHECK_LAUNCH();
     return OI2_OK;
   }
@@ -1879,8 +1952,7 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
     hipLaunchKernelGGL((k_pgemm_down_both<2, 2>), dim3(16 * p.pmt * splits), dim3(kThreads), 0, st, da, p.pmt,
                        splits);
     OI2_CHECK_LAUNCH();
-    hipLaunchKernelGGL(k_bfinal, dim3(grid), dim3(kThreads), 0, st, y, splits, M,
-                       add_residual ? x : nullptr, out, y32);
+    final_add(splits);
     OI2_CHECK_LAUNCH();
     return OI2_OK;
   }
@@ -1904,8 +1976,7 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
     }
     OI2_CHECK_LAUNCH();
   }
-  hipLaunchKernelGGL(k_bfinal, dim3(grid), dim3(kThreads), 0, st, y, hot_splits + cold_splits, M,
-                     add_residual ? x : nullptr, out, y32);
+  final_add(hot_splits + cold_splits);
   OI2_CHECK_LAUNCH();
   return OI2_OK;
 }

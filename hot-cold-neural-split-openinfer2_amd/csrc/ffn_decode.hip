@@ -1285,6 +1285,25 @@ int oi2_ffn_forward(const uint16_t* x, int32_t batch, const uint16_t* norm_w, fl
                            out, y32, c, ffn_ws(workspace, c.n_hot, ws_wg), st);
 }
 
+int oi2_ffn_forward_chain(const uint16_t* x, int32_t batch, const uint16_t* norm_w, float eps,
+                          const uint16_t* xn_in, const oi2_hot* hot, const oi2_cold* cold,
+                          const oi2_active* active, int32_t act, int32_t act_on_both, int32_t add_residual,
+                          uint16_t* out, float* y32, const uint16_t* next_norm_w, float next_eps,
+                          uint16_t* xn_next, void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  OI2_CHECK_ARG(batch >= 2, "batch %d: the chained call runs batches of 2 and more", batch);
+  FfnCall c;
+  int rc = ffn_validate(x, batch, norm_w, hot, cold, active, act, &c);
+  if (rc) return rc;
+  OI2_CHECK_ARG((uintptr_t)xn_in % 16 == 0 && (uintptr_t)next_norm_w % 16 == 0 && (uintptr_t)xn_next % 16 == 0 &&
+                    (uintptr_t)out % 16 == 0,
+                "xn_in, next_norm_w, xn_next and out must be 16-byte aligned");
+  OI2_CHECK_ARG(!next_norm_w || (xn_next && out), "next_norm_w needs xn_next and out");
+  return batch_ffn(x, batch, norm_w, eps, hot, c.has_cold ? cold : nullptr, c.has_cold ? active : nullptr,
+                   act == OI2_ACT_RELU, act_on_both != 0, add_residual, out, y32, workspace, workspace_bytes,
+                   (hipStream_t)stream, xn_in, next_norm_w, next_eps, next_norm_w ? xn_next : nullptr);
+}
+
 }  // extern "C"
 
 namespace oi2 {

@@ -274,9 +274,13 @@ constexpr int cold_rows_bound(int capacity) {
   return (wv + kMaxChunks - 1 + 3) / 4;
 }
 
+// With xn_in the rows are taken as already normalised (no norm launch);
+// with next_w the call also writes xn_next = RMSNorm(out) with that weight.
 int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const oi2_hot* hot,
               const oi2_cold* cold, const oi2_active* active, int relu, int both, int add_residual,
-              uint16_t* out, float* y32, void* workspace, size_t workspace_bytes, hipStream_t st);
+              uint16_t* out, float* y32, void* workspace, size_t workspace_bytes, hipStream_t st,
+              const uint16_t* xn_in = nullptr, const uint16_t* next_w = nullptr, float next_eps = 0.f,
+              uint16_t* xn_next = nullptr);
 
 // Exclusive prefix of the (clamped) chunk counts into s_prefix[0..n_chunks];
 // all threads of a 256-thread workgroup call it (it contains barriers).

@@ -68,6 +68,10 @@ _SIGS = {
     "oi2_ffn_forward": (c_int32, [c_void_p, c_int32, c_void_p, c_float, POINTER(Hot), POINTER(Cold),
                                   POINTER(Active), c_int32, c_int32, c_int32, c_void_p, c_void_p,
                                   c_void_p, c_size_t, c_void_p]),
+    "oi2_ffn_forward_chain": (c_int32, [c_void_p, c_int32, c_void_p, c_float, c_void_p, POINTER(Hot),
+                                        POINTER(Cold), POINTER(Active), c_int32, c_int32, c_int32,
+                                        c_void_p, c_void_p, c_void_p, c_float, c_void_p, c_void_p,
+                                        c_size_t, c_void_p]),
     "oi2_sparse_ffn_dense_workspace_bytes": (c_size_t, [c_int32, c_int32, c_int32]),
     "oi2_sparse_ffn_dense": (c_int32, [c_void_p, c_int32, c_int32, c_int32, c_int32, c_int32,
                                        c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_void_p,

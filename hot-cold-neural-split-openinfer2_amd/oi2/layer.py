@@ -121,10 +121,16 @@ def workspace_bytes(batch: int, hot: HotWeights | None, cold: ColdNeurons | None
 
 
 def _ffn(x2d, norm_w, eps, hot: HotWeights | None, cold: ColdNeurons | None, activation,
-         act_on_both, add_residual, out_dtype=torch.float16, want_y32=False, workspace=None):
+         act_on_both, add_residual, out_dtype=torch.float16, want_y32=False, workspace=None,
+         xn_in=None, next_norm_w=None, next_eps=None):
     """One oi2_ffn_forward call.  ``workspace`` (uint8 device tensor of at least
     workspace_bytes(...)) is used instead of a fresh allocation when given; its
-    contents on entry do not matter."""
+    contents on entry do not matter.
+
+    With ``xn_in`` or ``next_norm_w`` (batch >= 2) it is one oi2_ffn_forward_chain
+    call: ``xn_in`` is RMSNorm(x) as the previous layer's call wrote it (no norm
+    launch), and with ``next_norm_w`` the call also returns the next layer's
+    normalised rows, (out, xn_next) or (out, y32, xn_next)."""
     dev = x2d.device
     x2d = x2d.to(torch.float16).contiguous()
     B = x2d.shape[0]
@@ -142,14 +148,26 @@ def _ffn(x2d, norm_w, eps, hot: HotWeights | None, cold: ColdNeurons | None, act
     out = torch.empty_like(x2d)
     y32 = torch.empty((B, HIDDEN), dtype=torch.float32, device=dev) if want_y32 else None
     act = _lib.ACT_RELU if activation == "relu" else _lib.ACT_SILU
-    _lib.check(L.oi2_ffn_forward(
-        x2d.data_ptr(), B, _lib.ptr(norm_w), ctypes.c_float(eps),
-        ctypes.byref(hot_s) if hot_s is not None else None,
-        ctypes.byref(cold_s) if cold_s is not None else None,
-        ctypes.byref(act_s) if act_s is not None else None,
+    hot_p = ctypes.byref(hot_s) if hot_s is not None else None
+    cold_p = ctypes.byref(cold_s) if cold_s is not None else None
+    act_p = ctypes.byref(act_s) if act_s is not None else None
+    if xn_in is None and next_norm_w is None:
+        _lib.check(L.oi2_ffn_forward(
+            x2d.data_ptr(), B, _lib.ptr(norm_w), ctypes.c_float(eps), hot_p, cold_p, act_p,
+            act, int(bool(act_on_both)), int(bool(add_residual)), out.data_ptr(), _lib.ptr(y32),
+            ws.data_ptr(), ws_bytes, _lib.stream_handle(dev)))
+        return (out, y32) if want_y32 else out
+    if xn_in is not None and (xn_in.dtype != torch.float16 or tuple(xn_in.shape) != tuple(x2d.shape)
+                              or not xn_in.is_contiguous()):
+        raise ValueError(f"xn_in must be a contiguous fp16 tensor of shape {tuple(x2d.shape)}")
+    xn_next = torch.empty_like(x2d) if next_norm_w is not None else None
+    _lib.check(L.oi2_ffn_forward_chain(
+        x2d.data_ptr(), B, _lib.ptr(norm_w), ctypes.c_float(eps), _lib.ptr(xn_in), hot_p, cold_p, act_p,
         act, int(bool(act_on_both)), int(bool(add_residual)), out.data_ptr(), _lib.ptr(y32),
+        _lib.ptr(next_norm_w), ctypes.c_float(eps if next_eps is None else next_eps), _lib.ptr(xn_next),
         ws.data_ptr(), ws_bytes, _lib.stream_handle(dev)))
-    return (out, y32) if want_y32 else out
+    res = (out, y32) if want_y32 else (out,)
+    return res + (xn_next,) if next_norm_w is not None else (res if want_y32 else out)
 
 
 _DENSE_DTYPES = (torch.float16, torch.float32, torch.bfloat16)

@@ -133,6 +133,26 @@ int oi2_ffn_forward(const uint16_t* x, int32_t batch, const uint16_t* norm_w, fl
                     int32_t act, int32_t act_on_both, int32_t add_residual, uint16_t* out,
                     float* y32, void* workspace, size_t workspace_bytes, void* stream);
 
+/* No counterpart in the reference (its layers each run their own
+ * input_layernorm, engine.py:295).  oi2_ffn_forward for one layer of a chain
+ * of layers run back to back (engine.py:424-438) at batch >= 2, with the
+ * RMSNorm moved across the layer boundary, for callers that run several
+ * layers on one batch (batched decode, prefill chunks):
+ *   xn_in       (may be NULL) RMSNorm(x) as the previous call of the chain
+ *               wrote it: the call takes it as x_n and launches no norm
+ *               (x is still the residual; norm_w is then not read)
+ *   next_norm_w (may be NULL) the next layer's norm weight: the call also
+ *               writes xn_next = RMSNorm(out) with it and next_eps, (batch, H)
+ *               fp16; needs out.  From 17 tokens the final add of the call
+ *               writes it, so the next call has one launch fewer.
+ * The outputs are the same bits as oi2_ffn_forward calls with their own
+ * norms.  Pointers 16-byte aligned; the workspace as oi2_ffn_forward's. */
+int oi2_ffn_forward_chain(const uint16_t* x, int32_t batch, const uint16_t* norm_w, float eps,
+                          const uint16_t* xn_in, const oi2_hot* hot, const oi2_cold* cold,
+                          const oi2_active* active, int32_t act, int32_t act_on_both, int32_t add_residual,
+                          uint16_t* out, float* y32, const uint16_t* next_norm_w, float next_eps,
+                          uint16_t* xn_next, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Workspace bytes for oi2_sparse_ffn_dense. */
 size_t oi2_sparse_ffn_dense_workspace_bytes(int32_t rows, int32_t n_hot, int32_t n_cold);
 

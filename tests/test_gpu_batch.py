@@ -63,6 +63,45 @@ def test_batch_decode_shared_active_set(dev, layer25, B):
                      what="batch row vs single token")
 
 
+@pytest.fixture(scope="module")
+def chain3(dev):
+    """Three layers of 4096 x 14336 (3584 hot), each with 30 % of its cold
+    records active."""
+    g = torch.Generator(device=dev).manual_seed(77)
+    lays, colds = [], []
+    for _ in range(3):
+        lay = SyntheticLayer(g, 14336, 3584, device=dev)
+        n = lay.records.shape[0]
+        slots = torch.randperm(n, generator=g, device=dev)[: int(0.3 * n)].int()
+        lays.append(lay)
+        colds.append(ColdNeurons.from_slots(_section(lay), slots))
+    return lays, colds, g
+
+
+@pytest.mark.parametrize("B", [8, 40, 64, 512])
+def test_batch_chain_equals_separate_calls(dev, chain3, B):
+    """Three layers through oi2_ffn_forward_chain (each call takes the
+    previous call's normalised rows and writes the next layer's) give the
+    same bits as three oi2_ffn_forward calls with their own norms, and every
+    xn_next equals oi2_rmsnorm of that call's output bit for bit."""
+    from oi2.layer import rmsnorm
+    lays, colds, g = chain3
+    x0 = torch.randn((B, H), generator=g, device=dev).half()
+    ref, x = [], x0
+    for lay, c in zip(lays, colds):
+        x = _ffn(x, lay.norm_w, EPS, lay.hot, c, "silu", False, True)
+        ref.append(x)
+    x, xn = x0, None
+    for i, (lay, c) in enumerate(zip(lays, colds)):
+        nxt = lays[i + 1].norm_w if i + 1 < len(lays) else None
+        r = _ffn(x, lay.norm_w, EPS, lay.hot, c, "silu", False, True, xn_in=xn, next_norm_w=nxt)
+        x, xn = r if nxt is not None else (r, None)
+        torch.cuda.synchronize()
+        assert torch.equal(x, ref[i]), f"B={B} layer {i}"
+        if nxt is not None:
+            assert torch.equal(xn, rmsnorm(x, nxt, EPS)), f"B={B} layer {i} xn_next"
+
+
 @pytest.mark.parametrize("B", [3, 8, 16])
 def test_batch_cold_only_small(dev, layer25, B):
     """Up to 16 tokens with no hot half: the cold down's ranges are added by
