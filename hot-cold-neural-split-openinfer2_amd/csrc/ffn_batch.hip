@@ -1573,12 +1573,22 @@ __global__ __launch_bounds__(kThreads) void k_bfinal_norm(const float* ys, int n
   }
   float wv[16];
   load_h16(w, 16 * t, wv);
-  for (int sp = 0; sp < n_ys; ++sp) {   // the partial sums in order, as k_bfinal adds them
-    f32x4 v[4];
+  // the partial sums in order, as k_bfinal adds them, four in flight
+  int sp = 0;
+  for (; sp + 4 <= n_ys; sp += 4) {
+    f32x4 v[4][4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) v[c] = yp[(size_t)sp * stride4 + c];
+    for (int k = 0; k < 4; ++k)
 #pragma unroll
-    for (int c = 0; c < 4; ++c) y[c] += v[c];
+      for (int c = 0; c < 4; ++c) v[k][c] = yp[(size_t)(sp + k) * stride4 + c];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) y[c] += v[k][c];
+  }
+  for (; sp < n_ys; ++sp) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) y[c] += yp[(size_t)sp * stride4 + c];
   }
   if (y32) {
 #pragma unroll
