@@ -6,15 +6,15 @@
 //   gate/up  H_hot  (M, n_hot) = act(s_g * X G^T + b, s_u * X U^T)   fp8 rows
 //            H_cold (M, n_act) = act(sum_g s_g,g (X Q_g^T)_g + b, ...)  INT4 records
 //            k_sbup (M <= 16): one workgroup per CU, RMSNorm fused;
-//            k_mup (M < 192): 64 tokens x 32 neurons, 32x32x16 tiles, the
+//            k_mup (M < 160): 64 tokens x 32 neurons, 32x32x16 tiles, the
 //            activation in the epilogue;
-//            k_pgemm_up (M >= 192): 32 pms tokens x 128 neurons
+//            k_pgemm_up (M >= 160): 128 tokens x 128 neurons
 //   down     Y (M, H) fp32
 //            hot  H_hot D_hot^T (fp8 rows, row scale): k_bdown_hot_s,
 //                 k_pgemm_down_hot
 //            cold H_cold D_cold: k_pgemm_down_cold, the records' down
 //                 nibbles transposed into a decoded LDS tile
-//            both halves from 17 tokens (17-191 and from 384):
+//            both halves from 17 tokens:
 //                 k_pgemm_down_both, one workgroup per output tile and K
 //                 range of each half
 //   k_bfinal out = x + Y (fp16), y32 = Y
@@ -180,10 +180,9 @@ __device__ __forceinline__ h8 a_frag32(const uint16_t* s, int ms, int step) {
 
 // Gate/up for 32 MS tokens x 128 weight rows (hot rows first, then items of
 // the dense active list).  Both operands go through two LDS buffers: each K
-// block's token rows and weight rows are loaded a block ahead as whole
-// 16-byte chunks (eight lanes per 128-byte weight row, so every load
-// instruction reads full cache lines) and written to LDS after the block's
-// MFMAs.  Weight rows are padded to 136 bytes (fp8) or 72 bytes (INT4): the
+// block's token rows and weight rows are loaded as whole 16-byte chunks
+// (eight lanes per 128-byte weight row, so every load instruction reads full
+// cache lines) by the staging waves.  Weight rows are padded to 136 bytes (fp8) or 72 bytes (INT4): the
 // 32 rows a wave reads at one column then fall on distinct banks.  Wave w
 // owns rows 32 w + (l & 31); B tile 0 is the gate row, tile 1 the up row.
 // The linear workgroup index is mapped so that the token tiles of one row
@@ -289,84 +288,125 @@ __device__ __forceinline__ void up_epilogue(const BUpArgs& a, const f32x16 (&acc
   }
 }
 
+// 8 waves: waves 0-3 only multiply (mma_block_lds, then the epilogue of
+// their 32 rows), waves 4-7 only stage, each K block two blocks ahead of its
+// use: their loads, waits and LDS stores stay out of the multiplying waves'
+// instruction streams, and every SIMD holds one wave of each kind (with all
+// eight waves doing both, one wave per SIMD, a 512-token tile took 80 us
+// against 70).  One barrier per block: the multiplying waves are done with
+// buffer kb & 1's previous block, and the staging waves have written block
+// kb + 1.
 template <int MS, bool HOT>
 __device__ __forceinline__ void pgemm_up_tile(const BUpArgs& a, int nt, int m0, int total, int i0,
-                                              uint16_t* sA, uint8_t* sB, uint16_t* sSc) {
+                                                 uint16_t* sA, uint8_t* sB, uint16_t* sSc) {
   constexpr int kAbuf = 32 * MS * kLdA;   // halves per A buffer
   constexpr int kBbuf = 256 * kLdB8;      // bytes per B buffer (INT4 rows use kLdB4 of it)
   constexpr int NR = HOT ? 8 : 4;         // 16-byte weight chunks staged per thread
-  const int t = threadIdx.x, w = t >> 6, l = lane_id();
-  const ARows<MS> arows(a.xn, kH, a.M, m0);
-  f32x16 acc[MS][2];
-#pragma unroll
-  for (int ms = 0; ms < MS; ++ms) acc[ms][0] = acc[ms][1] = f32x16{};
-  u32x4 ra[2 * MS], rb[NR];
-  uint16_t rsc = 0;
-
-  // this thread's staging rows: hot, chunk t & 7 of tile rows (t >> 3) + 32 i
-  // (i < 4 gate, else up); cold, chunk t & 3 of items (t >> 2) + 64 (i & 1),
-  // gate for i < 2, up for i >= 2, and the scale of item t & 127 (gate, up
-  // by t >> 7).  Rows past n_hot and invalid items read as zero.
-  const rsrc_t rw = HOT ? buf_rsrc(a.gate_q, (uint32_t)a.n_hot * kH)
-                        : buf_rsrc(a.records, (uint32_t)a.n_records * kRecBytes);
-  const rsrc_t ru = buf_rsrc(a.up_q, HOT ? (uint32_t)a.n_hot * kH : 0u);
-  uint32_t voff[4], vsc = 0;
+  constexpr int kNB = kH / kBK;
+  static_assert(kNB % 2 == 0, "the block loop is unrolled by two");
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), l = lane_id();
   auto item_rec = [&](int it) {
     const int slot = it < total ? a.dslots[it] : -1;
     return (slot >= 0 && slot < a.n_records) ? (uint32_t)slot * kRecBytes : kNoOffset;
   };
-  if constexpr (HOT) {
+  if (w >= 4) {
+    // staging thread t: token rows (t >> 4) + 16 i, chunk t & 15; hot, chunk
+    // t & 7 of tile rows (t >> 3) + 32 i (i < 4 gate, else up); cold, chunk
+    // t & 3 of items (t >> 2) + 64 (i & 1), gate for i < 2, up for i >= 2,
+    // and the scale of item t & 127 (gate, up by t >> 7).  Rows past M or
+    // n_hot and invalid items read as zero.
+    const int t = threadIdx.x - 256;
+    const rsrc_t rx = buf_rsrc(a.xn, (uint32_t)a.M * kH * 2);
+    uint32_t aoff[2 * MS];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) voff[i] = (uint32_t)(nt * 128 + (t >> 3) + 32 * i) * kH + 16 * (t & 7);
-  } else {
-    const uint32_t v0 = item_rec(i0 + (t >> 2)), v1 = item_rec(i0 + (t >> 2) + 64);
-    voff[0] = v0 + kOffGate + 16 * (t & 3);
-    voff[1] = v1 + kOffGate + 16 * (t & 3);
-    voff[2] = v0 + kOffUp + 16 * (t & 3);
-    voff[3] = v1 + kOffUp + 16 * (t & 3);
-    vsc = item_rec(i0 + (t & 127)) + (t >> 7) * 2 * kGroups;
-  }
-  auto load_b = [&](int kb) {
+    for (int i = 0; i < 2 * MS; ++i) aoff[i] = ((uint32_t)(m0 + (t >> 4) + 16 * i) * kH + 8 * (t & 15)) * 2;
+    const rsrc_t rw = HOT ? buf_rsrc(a.gate_q, (uint32_t)a.n_hot * kH)
+                          : buf_rsrc(a.records, (uint32_t)a.n_records * kRecBytes);
+    const rsrc_t ru = buf_rsrc(a.up_q, HOT ? (uint32_t)a.n_hot * kH : 0u);
+    uint32_t voff[4], vsc = 0;
     if constexpr (HOT) {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) rb[i] = bload16(i < 4 ? rw : ru, voff[i & 3], kb * kBK);
+      for (int i = 0; i < 4; ++i) voff[i] = (uint32_t)(nt * 128 + (t >> 3) + 32 * i) * kH + 16 * (t & 7);
     } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) rb[i] = bload16(rw, voff[i], 64 * kb);
-      rsc = bload2(rw, vsc, kOffScales + 2 * kb);
+      const uint32_t v0 = item_rec(i0 + (t >> 2)), v1 = item_rec(i0 + (t >> 2) + 64);
+      voff[0] = v0 + kOffGate + 16 * (t & 3);
+      voff[1] = v1 + kOffGate + 16 * (t & 3);
+      voff[2] = v0 + kOffUp + 16 * (t & 3);
+      voff[3] = v1 + kOffUp + 16 * (t & 3);
+      vsc = item_rec(i0 + (t & 127)) + (t >> 7) * 2 * kGroups;
     }
-  };
-  auto store_b = [&](int buf) {
-    uint8_t* B = sB + buf * kBbuf;
+    u32x4 ra[2][2 * MS], rb[2][NR];
+    uint16_t rsc[2] = {0, 0};
+    auto load = [&](int kb, int sl) {
 #pragma unroll
-    for (int i = 0; i < NR; ++i) {
-      uint8_t* d = HOT ? B + ((t >> 3) + 32 * i) * kLdB8 + 16 * (t & 7)
-                       : B + ((t >> 2) + 64 * i) * kLdB4 + 16 * (t & 3);
-      reinterpret_cast<u32x2*>(d)[0] = u32x2{rb[i].x, rb[i].y};
-      reinterpret_cast<u32x2*>(d)[1] = u32x2{rb[i].z, rb[i].w};
+      for (int i = 0; i < 2 * MS; ++i) ra[sl][i] = bload16(rx, aoff[i], kb * kBK * 2);
+      if constexpr (HOT) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) rb[sl][i] = bload16(i < 4 ? rw : ru, voff[i & 3], kb * kBK);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) rb[sl][i] = bload16(rw, voff[i], 64 * kb);
+        rsc[sl] = bload2(rw, vsc, kOffScales + 2 * kb);
+      }
+    };
+    auto store = [&](int buf, int sl) {
+      uint16_t* A = sA + buf * kAbuf;
+#pragma unroll
+      for (int i = 0; i < 2 * MS; ++i) {
+        u32x4 v = ra[sl][i];
+        if constexpr (!HOT) {   // (x0,x4,x1,x5,x2,x6,x3,x7): the INT4 decode's pair order
+          const uint32_t d0 = v.x, d1 = v.y, d2 = v.z, d3 = v.w;
+          v.x = (d0 & 0xFFFFu) | (d2 << 16);
+          v.y = (d0 >> 16) | (d2 & 0xFFFF0000u);
+          v.z = (d1 & 0xFFFFu) | (d3 << 16);
+          v.w = (d1 >> 16) | (d3 & 0xFFFF0000u);
+        }
+        *reinterpret_cast<u32x4*>(A + ((t >> 4) + 16 * i) * kLdA + 8 * (t & 15)) = v;
+      }
+      uint8_t* B = sB + buf * kBbuf;
+#pragma unroll
+      for (int i = 0; i < NR; ++i) {
+        uint8_t* d = HOT ? B + ((t >> 3) + 32 * i) * kLdB8 + 16 * (t & 7)
+                         : B + ((t >> 2) + 64 * i) * kLdB4 + 16 * (t & 3);
+        reinterpret_cast<u32x2*>(d)[0] = u32x2{rb[sl][i].x, rb[sl][i].y};
+        reinterpret_cast<u32x2*>(d)[1] = u32x2{rb[sl][i].z, rb[sl][i].w};
+      }
+      if constexpr (!HOT) sSc[buf * 256 + t] = rsc[sl];
+    };
+    // block b sits in register slot and LDS buffer b & 1
+    load(0, 0);
+    load(1, 1);
+    store(0, 0);
+    load(2, 0);
+    lds_barrier();   // block 0 in buffer 0
+#pragma unroll 1
+    for (int k0 = 0; k0 < kNB; k0 += 2) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int kb = k0 + u;
+        // block kb + 1 into the buffer block kb - 1 left, then its slot
+        // loads block kb + 3 (the last passes load the last block again)
+        if (kb + 1 < kNB) {
+          store(u ^ 1, u ^ 1);
+          load(min(kb + 3, kNB - 1), u ^ 1);
+        }
+        lds_barrier();
+      }
     }
-    if constexpr (!HOT) sSc[buf * 256 + t] = rsc;
-  };
-
-  arows.load(0, ra);
-  load_b(0);
-  store_a_rows<2 * MS, !HOT>(ra, sA);
-  store_b(0);
-  lds_barrier();
-  for (int kb = 0; kb < kH / kBK; ++kb) {
-    const int kn = min(kb + 1, kH / kBK - 1), cur = kb & 1;
-    arows.load(kn, ra);
-    load_b(kn);
-    // sched_barrier(0) keeps these loads issued before the MFMAs (the
-    // scheduler would otherwise sink them to shorten register lifetimes)
-    __builtin_amdgcn_sched_barrier(0);
-    mma_block_lds<MS, 2, !HOT>(sA + cur * kAbuf, sB + cur * kBbuf, sSc + cur * 256, acc);
-    __builtin_amdgcn_sched_barrier(0);
-    store_a_rows<2 * MS, !HOT>(ra, sA + (cur ^ 1) * kAbuf);
-    store_b(cur ^ 1);
-    lds_barrier();
+    return;
   }
-
+  f32x16 acc[MS][2];
+#pragma unroll
+  for (int ms = 0; ms < MS; ++ms) acc[ms][0] = acc[ms][1] = f32x16{};
+  lds_barrier();   // block 0 in buffer 0
+#pragma unroll 1
+  for (int k0 = 0; k0 < kNB; k0 += 2) {
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      mma_block_lds<MS, 2, !HOT>(sA + u * kAbuf, sB + u * kBbuf, sSc + u * 256, acc);
+      lds_barrier();
+    }
+  }
   // epilogue: this lane's column, rows m0 + 32 ms + 8 (j / 4) + 4 (l / 32) + j % 4
   const int col = 32 * w + (l & 31);
   if constexpr (HOT) {
@@ -385,7 +425,7 @@ __device__ __forceinline__ void pgemm_up_tile(const BUpArgs& a, int nt, int m0, 
 }
 
 template <int MS>
-__global__ __launch_bounds__(kThreads) void k_pgemm_up(BUpArgs a, int hot_tiles, int n_tiles, int mt) {
+__global__ __launch_bounds__(2 * kThreads) void k_pgemm_up(BUpArgs a, int hot_tiles, int n_tiles, int mt) {
   __shared__ __attribute__((aligned(16))) uint16_t sA[2 * 32 * MS * kLdA];
   __shared__ __attribute__((aligned(16))) uint8_t sB[2 * 256 * kLdB8];
   __shared__ uint16_t sSc[2 * 256];
@@ -1681,9 +1721,10 @@ struct BatchPlan {
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 constexpr int kSkinnyMax = 16;    // token counts up to this use the one-tile split-K kernels
-constexpr int kPrefillMin = 192;  // token counts from this use the 128-row tile kernels
+// token counts from this use the 128-token tile kernels (160 tokens: 3072
+// against 3099 us per 32 layers on 64-token tiles; 128 tokens: 2888 against 2578)
+constexpr int kPrefillMin = 160;
 
-static int prefill_ms(int M) { return M >= 384 ? 4 : 2; }   // 32-token subtiles per tile
 // hot down output tiles: 256 outputs each on the 128-token tiles, else 128
 static int hot_down_tiles(int pms) { return pms == 4 ? kH / 256 : kH / 128; }
 
@@ -1709,8 +1750,11 @@ static BatchPlan batch_plan(int M, int n_hot, int cap) {
   p.prefill = M >= kPrefillMin;
   if (M > kSkinnyMax) {
     // 64-token tiles (k_mup and the down kernels at two 32-token subtiles)
-    // below the prefill sizes, 32 pms-token tiles from them on
-    p.pms = p.prefill ? prefill_ms(M) : 2;
+    // below the prefill sizes, 128-token tiles from them on (measured from
+    // 192 to 448 tokens, 128-token tiles are as fast or faster than 64-token
+    // ones even where they leave tokens of the last tile empty: 192 tokens
+    // 3011 against 3142 us per 32 layers, 320 tokens 3587 against 4822)
+    p.pms = p.prefill ? 4 : 2;
     p.pmt = (M + 32 * p.pms - 1) / (32 * p.pms);
     // hot down: output tiles (128 outputs, 256 on the 128-token tiles) x token
     // tiles x K splits, about 256 workgroups
@@ -1736,7 +1780,7 @@ static BatchPlan batch_plan(int M, int n_hot, int cap) {
   if (M > kSkinnyMax && n_hot > 0 && cap > 0) {
     if (p.pms == 4)
       p.both_splits = std::max(p.hot_splits, cold_down_splits(M, cap));
-    else if (!p.prefill)
+    else
       p.both_splits = std::max(cold_down_splits(M, cap), std::min(p.hot_blocks, 256 / (16 * p.pmt)));
   }
   const int y_parts = M <= kSkinnyMax ? 1
@@ -1932,10 +1976,7 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
     if (p.prefill) {
       const int hot_tiles = p.ldh / 128, n_tiles = hot_tiles + p.ldc / 128;
       const dim3 grid((n_tiles + 7) / 8 * 8 * p.pmt);
-      if (p.pms == 4)
-        hipLaunchKernelGGL(k_pgemm_up<4>, grid, dim3(kThreads), 0, st, ua, hot_tiles, n_tiles, p.pmt);
-      else
-        hipLaunchKernelGGL(k_pgemm_up<2>, grid, dim3(kThreads), 0, st, ua, hot_tiles, n_tiles, p.pmt);
+      hipLaunchKernelGGL(k_pgemm_up<4>, grid, dim3(2 * kThreads), 0, st, ua, hot_tiles, n_tiles, p.pmt);
     } else {
       const MupTiles mtl = mup_tiles(p);
       const dim3 grid((mtl.n_tiles + 7) / 8 * 8 * p.pmt);
@@ -1956,7 +1997,7 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
     OI2_CHECK_LAUNCH();
     return OI2_OK;
   }
-  if (!p.prefill && n_hot && has_cold && p.both_splits > 0) {
+  if (p.pms == 2 && n_hot && has_cold && p.both_splits > 0) {
     // the same on 64-token tiles
     const int splits = p.both_splits;
     hipLaunchKernelGGL((k_pgemm_down_both<2, 2>), dim3(16 * p.pmt * splits), dim3(kThreads), 0, st, da, p.pmt,

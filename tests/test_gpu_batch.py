@@ -205,10 +205,10 @@ def test_batch_drelu_union_of_firing_sets_equals_dense(dev, drelu_layer, B):
         assert_ffn_close(y, ref_all, what=f"dReLU B={B} all rows")
 
 
-@pytest.mark.parametrize("B", [70, 200, 400])
+@pytest.mark.parametrize("B", [70, 159, 160, 200, 400])
 def test_batch_edge_shapes(dev, B):
-    """Token count not a multiple of the 64- or 128-row tile (70 on the
-    64-token tiles, 200 and 400 on the prefill tiles), n_hot not a multiple
+    """Token count not a multiple of the 64- or 128-row tile (70 and 159 on
+    the 64-token tiles, 160, 200 and 400 on the prefill tiles), n_hot not a multiple
     of the 128 K block, a chunked active list with an empty chunk, duplicates
     and invalid slots, one half missing."""
     g = torch.Generator(device=dev).manual_seed(6)
