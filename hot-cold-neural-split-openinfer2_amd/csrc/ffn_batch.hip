@@ -1259,12 +1259,14 @@ __global__ __launch_bounds__(2 * kThreads) void k_pgemm_down_both(BDownArgs a, i
   for (int ms = 0; ms < MS; ++ms)
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) acc[ms][nb] = f32x16{};
+  float sd_pre[NB];   // the row scales, loaded up front (loaded between the loops they cost spills)
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) sd_pre[nb] = a.down_s[j0 + 128 * nb + 32 * w + (l & 31)];
   auto scale_hot = [&]() {   // the hot sums take their row scales before the cold ones join
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
-      const float sd = a.down_s[j0 + 128 * nb + 32 * w + (l & 31)];
 #pragma unroll
-      for (int ms = 0; ms < MS; ++ms) acc[ms][nb] *= sd;
+      for (int ms = 0; ms < MS; ++ms) acc[ms][nb] *= sd_pre[nb];
     }
   };
   auto cold_mma = [&](const uint8_t* base) {
