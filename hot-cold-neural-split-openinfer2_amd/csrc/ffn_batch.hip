@@ -1769,72 +1769,64 @@ __global__ __launch_bounds__(kThreads) void k_bfinal(const float* ys, int n_ys, 
 
 // k_bfinal for one row per workgroup that also writes the next layer's
 // normalised rows: xn = RMSNorm(out) with weight w (k_rmsnorm's arithmetic on
-// the fp16 out, so the same bits as a norm launch after the call).  Thread t
-// takes elements 16 t .. 16 t + 15 of row blockIdx.x.
-__global__ __launch_bounds__(kThreads) void k_bfinal_norm(const float* ys, int n_ys, int M, const uint16_t* res,
-                                                         uint16_t* out, float* y32, const uint16_t* w, float eps,
-                                                         uint16_t* xn) {
-  __shared__ float s_parts[kThreads];
+// the fp16 out, so the same bits as a norm launch after the call).  1024
+// threads, thread t adding elements 4 t .. 4 t + 3 of row blockIdx.x over
+// every partial sum, eight loads in flight: with 256 threads of 16 elements,
+// four in flight, 64 rows (64 workgroups) took 7.0 us.  The sum of squares
+// is taken as k_rmsnorm takes it (16 consecutive elements per partial, in
+// order) from the fp16 outputs staged in LDS.
+constexpr int kFnThreads = 1024;
+__global__ __launch_bounds__(kFnThreads) void k_bfinal_norm(const float* ys, int n_ys, int M, const uint16_t* res,
+                                                            uint16_t* out, float* y32, const uint16_t* w, float eps,
+                                                            uint16_t* xn) {
+  static_assert(kH == 4 * kFnThreads, "four elements per thread");
+  __shared__ __attribute__((aligned(16))) float s_o[kH];
+  __shared__ __attribute__((aligned(16))) float s_parts[kThreads];
   const int t = threadIdx.x;
-  const size_t e0 = (size_t)blockIdx.x * kH + 16 * t;
+  const size_t e0 = (size_t)blockIdx.x * kH + 4 * t;
   const size_t stride4 = (size_t)M * kH / 4;
   const f32x4* yp = reinterpret_cast<const f32x4*>(ys + e0);
-  f32x4 y[4];
-#pragma unroll
-  for (int c = 0; c < 4; ++c) y[c] = f32x4{0.f, 0.f, 0.f, 0.f};
-  u32x4 rv[2] = {u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}};
-  if (res) {
-    rv[0] = reinterpret_cast<const u32x4*>(res + e0)[0];
-    rv[1] = reinterpret_cast<const u32x4*>(res + e0)[1];
-  }
-  float wv[16];
-  load_h16(w, 16 * t, wv);
-  // the partial sums in order, as k_bfinal adds them, four in flight
+  f32x4 y = f32x4{0.f, 0.f, 0.f, 0.f};
+  const u32x2 rv = res ? *reinterpret_cast<const u32x2*>(res + e0) : u32x2{0u, 0u};
+  const u32x2 wb = *reinterpret_cast<const u32x2*>(w + 4 * t);
+  // the partial sums in order, as k_bfinal adds them, eight in flight
   int sp = 0;
-  for (; sp + 4 <= n_ys; sp += 4) {
-    f32x4 v[4][4];
+  for (; sp + 8 <= n_ys; sp += 8) {
+    f32x4 v[8];
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
+    for (int k = 0; k < 8; ++k) v[k] = yp[(size_t)(sp + k) * stride4];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) v[k][c] = yp[(size_t)(sp + k) * stride4 + c];
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) y[c] += v[k][c];
+    for (int k = 0; k < 8; ++k) y += v[k];
   }
-  for (; sp < n_ys; ++sp) {
+  for (; sp < n_ys; ++sp) y += yp[(size_t)sp * stride4];
+  if (y32) *reinterpret_cast<f32x4*>(y32 + e0) = y;
+  float o[4];
+  uint16_t ob[4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) y[c] += yp[(size_t)sp * stride4 + c];
+  for (int e = 0; e < 4; ++e) {
+    const uint16_t rb = (uint16_t)(rv[e >> 1] >> (16 * (e & 1)));
+    ob[e] = float_to_half_bits(half_bits_to_float(rb) + y[e]);
+    o[e] = half_bits_to_float(ob[e]);
   }
-  if (y32) {
+  if (out)
+    *reinterpret_cast<u32x2*>(out + e0) =
+        u32x2{(uint32_t)ob[0] | ((uint32_t)ob[1] << 16), (uint32_t)ob[2] | ((uint32_t)ob[3] << 16)};
+  *reinterpret_cast<f32x4*>(s_o + 4 * t) = f32x4{o[0], o[1], o[2], o[3]};
+  __syncthreads();
+  if (t < kThreads) {
+    float v16[16];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) reinterpret_cast<f32x4*>(y32 + e0)[c] = y[c];
+    for (int e = 0; e < 16; ++e) v16[e] = s_o[16 * t + e];
+    s_parts[t] = ssq16(v16);
   }
-  float o[16];
-  u32x4 ob[2];
-#pragma unroll
-  for (int e = 0; e < 16; e += 2) {
-    const uint32_t rr = rv[e >> 3][(e & 7) >> 1];
-    const uint16_t b0 = float_to_half_bits(half_bits_to_float((uint16_t)(rr & 0xFFFFu)) + y[e >> 2][e & 3]);
-    const uint16_t b1 = float_to_half_bits(half_bits_to_float((uint16_t)(rr >> 16)) + y[(e + 1) >> 2][(e + 1) & 3]);
-    ob[e >> 3][(e & 7) >> 1] = (uint32_t)b0 | ((uint32_t)b1 << 16);
-    o[e] = half_bits_to_float(b0);
-    o[e + 1] = half_bits_to_float(b1);
-  }
-  if (out) {
-    reinterpret_cast<u32x4*>(out + e0)[0] = ob[0];
-    reinterpret_cast<u32x4*>(out + e0)[1] = ob[1];
-  }
-  s_parts[t] = ssq16(o);
   __syncthreads();
   const float r = r_from_parts(s_parts, eps);
-  u32x4 xv[2];
+  uint16_t xb[4];
 #pragma unroll
-  for (int e = 0; e < 16; e += 2)
-    xv[e >> 3][(e & 7) >> 1] = (uint32_t)float_to_half_bits(xn_exact(o[e], r, wv[e])) |
-                               ((uint32_t)float_to_half_bits(xn_exact(o[e + 1], r, wv[e + 1])) << 16);
-  reinterpret_cast<u32x4*>(xn + e0)[0] = xv[0];
-  reinterpret_cast<u32x4*>(xn + e0)[1] = xv[1];
+  for (int e = 0; e < 4; ++e)
+    xb[e] = float_to_half_bits(xn_exact(o[e], r, half_bits_to_float((uint16_t)(wb[e >> 1] >> (16 * (e & 1))))));
+  *reinterpret_cast<u32x2*>(xn + e0) =
+      u32x2{(uint32_t)xb[0] | ((uint32_t)xb[1] << 16), (uint32_t)xb[2] | ((uint32_t)xb[3] << 16)};
 }
 
 // Up to 16 tokens without hot rows: out = res + y (fp16), y32 = y, y the sum
@@ -2137,7 +2129,7 @@ int batch_ffn(const uint16_t* x, int M, const uint16_t* norm_w, float eps, const
   // the final add of the n_ys partial sums, with the next layer's rows when asked
   auto final_add = [&](int n_ys) {
     if (next_w)
-      hipLaunchKernelGGL(k_bfinal_norm, dim3(M), dim3(kThreads), 0, st, y, n_ys, M, add_residual ? x : nullptr,
+      hipLaunchKernelGGL(k_bfinal_norm, dim3(M), dim3(kFnThreads), 0, st, y, n_ys, M, add_residual ? x : nullptr,
                          out, y32, next_w, next_eps, xn_next);
     else
       hipLaunchKernelGGL(k_bfinal, dim3(grid), dim3(kThreads), 0, st, y, n_ys, M, add_residual ? x : nullptr, out,
